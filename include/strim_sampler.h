@@ -1,0 +1,180 @@
+/*
+ * strim_sampler.h — C ABI of the MI355X (gfx950) token-selection path.
+ *
+ * This library replaces strim's per-step token selection: logit penalties, grammar
+ * bitmask, temperature, min-p, top-k / top-p, categorical draw, and the MTP
+ * speculative accept/reject verifier. Every entry point is plain C: device pointers,
+ * sizes and a HIP stream passed as void*. No torch or C++ types cross the boundary.
+ *
+ * Reference interfaces replaced (paths relative to the strim-engine repository):
+ *   strim_sample  <- Sampler.sample / Sampler.sampleFirst
+ *                      (Sources/StrimEngine/Sampler.swift:29-54),
+ *                    SpecSampling.sample (Sources/StrimCore/SpecSampling.swift:109-116),
+ *                    the per-row pick loop of EngineCore.decodeBatch
+ *                      (Sources/StrimEngine/EngineCore.swift:968-974,998-1002),
+ *                    greedy argMax (EngineCore.swift:933,973).
+ *   strim_verify  <- SpecSampling.verify / rowOutcome
+ *                      (Sources/StrimCore/SpecSampling.swift:74-106) and the greedy
+ *                    prefix-compare verify (Sources/StrimCore/SpecStream.swift:256-273).
+ *   strim_mask_logits <- maskLogits (Sources/StrimCore/TokenMask.swift:15-17).
+ *   strim_draft_argmax <- MTP.nextTokenIndex / nextToken draft map
+ *                      (Sources/StrimCore/MTP.swift:104-111,120-125).
+ *   strim_sampling_params <- GenParams (Sources/StrimEngine/EngineAPI.swift:47-67) and
+ *                    SamplingConfig (Sources/StrimCore/SpecSampling.swift:7-15).
+ *   strim_check_params <- request validation (Sources/StrimServer/ChatRequest.swift:148-161).
+ *
+ * Conventions
+ *   - All array arguments are DEVICE pointers unless stated, owned by the caller.
+ *   - Calls are stream-ordered and asynchronous. A context (strim_ctx) owns scratch
+ *     memory; calls that share one context must not overlap in time (use one context
+ *     per stream), mirroring the reference's single engine thread
+ *     (Sources/StrimEngine/Inbox.swift:42-46).
+ *   - The synchronous return value reports host-checkable errors (sizes, pointers,
+ *     dtype). Data-dependent errors are reported per row in out_status (device) and
+ *     the row's output id is -1.
+ *   - Token order used for every ordered decision: logit descending, then token id
+ *     ascending.
+ */
+#ifndef STRIM_SAMPLER_H
+#define STRIM_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------------- */
+#define STRIM_OK 0
+#define STRIM_EINVAL (-1)     /* bad params / sizes / pointers / draft id not in table */
+#define STRIM_EEMPTY (-2)     /* the row allows no token (all-zero mask or all -inf)    */
+#define STRIM_ENONFINITE (-3) /* NaN or +inf logit in an allowed position              */
+#define STRIM_ECAPACITY (-4)  /* candidate set larger than the context capacity        */
+#define STRIM_EHIP (-5)       /* HIP runtime error                                      */
+#define STRIM_ENOMEM (-6)     /* device allocation failed                              */
+
+/* ---- logits dtype --------------------------------------------------------------- */
+#define STRIM_DTYPE_F32 0
+#define STRIM_DTYPE_BF16 1
+
+/* ---- noise modes -----------------------------------------------------------------
+ * ICDF   : one draw uniform and one accept uniform per row. Injected layout [R][2]
+ *          (draw, accept). Draw = first kept token (in token order) whose inclusive
+ *          cumulative mass exceeds u * (kept mass).
+ * GUMBEL : the reference scheme (SpecSampling.swift:24-27,78-85): uniforms [R][V+1];
+ *          element i < V is Gumbel noise for token i (or for sorted rank i with
+ *          STRIM_FLAG_NOISE_BY_RANK), element V is the accept uniform.
+ * noise == NULL: uniforms come from Philox4x32-10 keyed by
+ *          SplitMix64(seed, position) (SpecSampling.mix, SpecSampling.swift:29-34), counter
+ *          = element index / 4. ICDF uses elements 0 (draw) and 1 (accept).          */
+#define STRIM_NOISE_ICDF 0
+#define STRIM_NOISE_GUMBEL 1
+
+/* ---- per-row flags ------------------------------------------------------------- */
+#define STRIM_FLAG_TOPK_KEEP_TIES 1u /* keep every token tied with the k-th value
+                                        (Sampler.swift:39-43); default keeps exactly k
+                                        (SpecSampling.swift:49-54)                      */
+#define STRIM_FLAG_NOISE_BY_RANK 2u  /* Gumbel noise indexed by sorted rank when top-p
+                                        is active (Sampler.swift:44-51)                 */
+#define STRIM_FLAG_SCORE_NO_LSE 4u   /* Gumbel score = logit + g (categorical, Sampler)
+                                        instead of log-prob + g (SpecSampling)          */
+#define STRIM_FLAG_SAMPLER_COMPAT 7u /* all three: the non-MTP Sampler.sample          */
+
+/* One per row. Defaults (strim_default_params) reproduce the reference exactly:
+ * extensions are no-ops. Chain order: penalties -> mask -> /T -> min-p -> top-k -> top-p
+ * -> draw. 48 bytes, naturally aligned. */
+typedef struct strim_sampling_params {
+  float temperature;        /* <= 0: greedy argmax (GenParams.isGreedy, EngineAPI.swift:66) */
+  int32_t top_k;            /* 0 = off; >= V = off                                          */
+  float top_p;              /* (0,1]; drop a token iff the mass strictly before it > top_p  */
+  float min_p;              /* [0,1]; 0 = off. Drop p < min_p * p_max (extension)           */
+  float repetition_penalty; /* > 0; 1 = off. In-history logit l: l>0 ? l/r : l*r (ext.)     */
+  float presence_penalty;   /* 0 = off. In-history: l -= presence (extension)               */
+  float frequency_penalty;  /* 0 = off. In-history: l -= frequency * count (extension)      */
+  uint32_t flags;           /* STRIM_FLAG_*                                                 */
+  uint64_t seed;            /* Philox key base (Sampler.seed)                               */
+  uint64_t position;        /* output position (SpecStream.sampleIndex)                      */
+} strim_sampling_params;
+
+typedef struct strim_ctx strim_ctx;
+
+/* Fill *p with the reference defaults: T=1, top_k=0, top_p=1, extensions off. Host. */
+void strim_default_params(strim_sampling_params* p);
+
+/* Validate n HOST param structs the way ChatRequest.parse does (temperature >= 0,
+ * top_p in (0,1], top_k >= 0) plus the extensions (min_p in [0,1], repetition > 0,
+ * finite penalties). Returns STRIM_OK or STRIM_EINVAL. */
+int strim_check_params(const strim_sampling_params* host_params, int32_t n);
+
+/* Create a context on `device` for up to max_rows rows of up to max_vocab tokens per
+ * call. Allocates scratch once (hipMalloc); no call below allocates. */
+int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t max_vocab);
+int strim_ctx_destroy(strim_ctx* ctx);
+
+/* Sample one token per row from logits [B][V] (row r at logits + r*row_stride elements).
+ *   params      device [B]
+ *   mask_words  device [B][mask_stride] uint32 or NULL. Token i allowed iff bit (i & 31)
+ *               of word (i >> 5) is set — the byte layout of the reference's UInt64
+ *               bitset (GrammarVocab.swift:77-86) on little-endian hosts.
+ *   history     device [B][H] int32 token ids or NULL; history_len device [B] (<= H) or
+ *               NULL (= H). Ids outside [0,V) are ignored. Feeds the penalties.
+ *   noise       see STRIM_NOISE_*.
+ *   out_ids     device [B]; -1 on a row error.
+ *   out_status  device [B] or NULL; STRIM_OK or a negative STRIM_E* per row.
+ *   out_probs   device [B][V] float or NULL: the processed distribution (validation).
+ * Replaces Sampler.sample / SpecSampling.sample (Sampler.swift:34-54,
+ * SpecSampling.swift:109-116) and the batched pick loop (EngineCore.swift:998-1002). */
+int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype, int32_t B,
+                 int32_t V, int64_t row_stride, const strim_sampling_params* params,
+                 const uint32_t* mask_words, int64_t mask_stride, const int32_t* history,
+                 const int32_t* history_len, int32_t H, int32_t noise_mode, const float* noise,
+                 int32_t* out_ids, int32_t* out_status, float* out_probs);
+
+/* Speculative verification of k drafts for B independent sequences.
+ *   target_logits [B][k+1][V] (row j = target distribution after the pending token and
+ *                 drafts[0..j)), dtype as strim_sample.
+ *   draft_logits  [B][k][Vd] (same dtype) or NULL. NULL: the draft is one-hot (the
+ *                 reference's argmax drafter, SpecSampling.swift:17-22). Otherwise the
+ *                 draft distribution q = softmax(draft_logits / T) over the draft vocab,
+ *                 mapped to full-vocab ids by draft_to_full.
+ *   draft_to_full [Vd] strictly ascending ids < V (Weights.swift:196-209); used only
+ *                 with draft_logits.
+ *   draft_tokens  [B][k] full-vocab ids.
+ *   mask_words    [B][k+1][mask_stride] or NULL (VerifyConstraint, TokenMask.swift:7-12).
+ *   history       as strim_sample; row j additionally counts drafts[0..j).
+ *   noise         ICDF [B][k+1][2]; GUMBEL [B][k+1][V+1]; NULL = Philox at positions
+ *                 params[b].position + j (SpecSampling.swift:98).
+ *   out_accepted  [B] leading accepted drafts n; out_token [B] the token decided at row n
+ *                 (residual at the first rejection, bonus sample after k accepts).
+ *   out_row_accept [B][k] / out_row_token [B][k+1] or NULL: per-row outcomes
+ *                 (SpecSampling.rowOutcome). out_status [B] or NULL.
+ * T <= 0 rows use the greedy rule: accept while argmax == draft (SpecStream.swift:269-273). */
+int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_t dtype,
+                 int32_t B, int32_t k, int32_t V, const void* draft_logits, int32_t Vd,
+                 const int32_t* draft_to_full, const int32_t* draft_tokens,
+                 const strim_sampling_params* params, const uint32_t* mask_words,
+                 int64_t mask_stride, const int32_t* history, const int32_t* history_len,
+                 int32_t H, int32_t noise_mode, const float* noise, int32_t* out_accepted,
+                 int32_t* out_token, int32_t* out_row_accept, int32_t* out_row_token,
+                 int32_t* out_status);
+
+/* out[r][i] = allowed(r,i) ? float(logits[r][i]) : -inf, float32 [R][V] (maskLogits,
+ * TokenMask.swift:15-17). mask_words as strim_sample (NULL = all allowed). */
+int strim_mask_logits(void* stream, const void* logits, int32_t dtype, int32_t R, int32_t V,
+                      int64_t row_stride, const uint32_t* mask_words, int64_t mask_stride,
+                      float* out);
+
+/* Draft-side map: out[r] = draft_to_full[argmax_j draft_logits[r][j]] (first max), or
+ * argmax itself when draft_to_full is NULL (MTP.swift:104-111,120-125). */
+int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, int32_t R,
+                       int32_t Vd, int64_t row_stride, const int32_t* draft_to_full,
+                       int32_t* out);
+
+/* Library version string (static storage). */
+const char* strim_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRIM_SAMPLER_H */

@@ -1,0 +1,188 @@
+"""Device-tensor front end of the C ABI.
+
+Torch is used only to hold device memory and the current HIP stream; every
+computation runs in libstrim_sampler.so. Inputs must already live on the GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _native as N
+
+
+def _ptr(t) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None) -> ctypes.c_void_p:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return N.DTYPE_BF16
+    if t.dtype == torch.float32:
+        return N.DTYPE_F32
+    raise TypeError(f"logits must be bfloat16 or float32, got {t.dtype}")
+
+
+def params_to_device(params: np.ndarray, device) -> torch.Tensor:
+    """Host strim_sampling_params rows -> a device byte tensor of the same layout."""
+    p = np.ascontiguousarray(params, dtype=N.PARAMS_DTYPE)
+    return torch.from_numpy(p.view(np.uint8).copy()).to(device)
+
+
+def _as_params(params, device) -> torch.Tensor:
+    if isinstance(params, torch.Tensor):
+        if params.dtype != torch.uint8 or not params.is_cuda:
+            raise TypeError("device params must be a cuda uint8 tensor of 48-byte rows")
+        return params
+    return params_to_device(params, device)
+
+
+def _check_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("every tensor argument must be on the GPU")
+        if t is not None and not t.is_contiguous():
+            raise ValueError("tensor arguments must be contiguous")
+
+
+class Context:
+    """strim_ctx: scratch for up to max_rows rows of up to max_vocab tokens."""
+
+    def __init__(self, device: int = 0, max_rows: int = 64, max_vocab: int = 262144):
+        self.device = device
+        self.max_rows = max_rows
+        self.max_vocab = max_vocab
+        h = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            N.check(N.lib().strim_ctx_create(ctypes.byref(h), device, max_rows, max_vocab),
+                    "strim_ctx_create")
+        self._h = h
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            torch.cuda.synchronize(self.device)
+            N.check(N.lib().strim_ctx_destroy(self._h), "strim_ctx_destroy")
+            self._h = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -------------------------------------------------------------------------
+    def sample(self, logits: torch.Tensor, params, mask: torch.Tensor | None = None,
+               history: torch.Tensor | None = None, history_len: torch.Tensor | None = None,
+               noise_mode: int = N.NOISE_ICDF, noise: torch.Tensor | None = None,
+               want_probs: bool = False, out_ids: torch.Tensor | None = None,
+               out_status: torch.Tensor | None = None, stream=None):
+        """strim_sample over logits [B,V]. Returns (ids int32[B], status int32[B],
+        probs float32[B,V] or None), all on the device."""
+        if logits.dim() == 1:
+            logits = logits.unsqueeze(0)
+        B, V = logits.shape
+        dev = logits.device
+        p = _as_params(params, dev)
+        _check_cuda(logits, mask, history, history_len, noise)
+        if out_ids is None:
+            out_ids = torch.empty(B, dtype=torch.int32, device=dev)
+        if out_status is None:
+            out_status = torch.empty(B, dtype=torch.int32, device=dev)
+        probs = torch.empty(B, V, dtype=torch.float32, device=dev) if want_probs else None
+        H = 0 if history is None else history.shape[-1]
+        mstride = 0 if mask is None else mask.shape[-1]
+        rc = N.lib().strim_sample(self._h, _stream(stream), _ptr(logits), _dtype_code(logits),
+                                  B, V, logits.stride(0), _ptr(p), _ptr(mask), mstride,
+                                  _ptr(history), _ptr(history_len), H, noise_mode, _ptr(noise),
+                                  _ptr(out_ids), _ptr(out_status), _ptr(probs))
+        N.check(rc, "strim_sample")
+        return out_ids, out_status, probs
+
+    def verify(self, target_logits: torch.Tensor, draft_tokens: torch.Tensor | None, params,
+               draft_logits: torch.Tensor | None = None,
+               draft_to_full: torch.Tensor | None = None, mask: torch.Tensor | None = None,
+               history: torch.Tensor | None = None, history_len: torch.Tensor | None = None,
+               noise_mode: int = N.NOISE_ICDF, noise: torch.Tensor | None = None,
+               row_outputs: bool = True, stream=None):
+        """strim_verify over target [B,k+1,V]. Returns a dict of device tensors:
+        accepted [B], token [B], status [B], row_accept [B,k], row_token [B,k+1]."""
+        B, k1, V = target_logits.shape
+        k = k1 - 1
+        dev = target_logits.device
+        p = _as_params(params, dev)
+        _check_cuda(target_logits, draft_tokens, draft_logits, draft_to_full, mask, history,
+                    history_len, noise)
+        acc = torch.empty(B, dtype=torch.int32, device=dev)
+        tok = torch.empty(B, dtype=torch.int32, device=dev)
+        st = torch.empty(B, dtype=torch.int32, device=dev)
+        racc = torch.empty(B, max(k, 1), dtype=torch.int32, device=dev) if row_outputs else None
+        rtok = torch.empty(B, k + 1, dtype=torch.int32, device=dev) if row_outputs else None
+        H = 0 if history is None else history.shape[-1]
+        mstride = 0 if mask is None else mask.shape[-1]
+        Vd = 0 if draft_logits is None else draft_logits.shape[-1]
+        rc = N.lib().strim_verify(self._h, _stream(stream), _ptr(target_logits),
+                                  _dtype_code(target_logits), B, k, V, _ptr(draft_logits), Vd,
+                                  _ptr(draft_to_full), _ptr(draft_tokens), _ptr(p), _ptr(mask),
+                                  mstride, _ptr(history), _ptr(history_len), H, noise_mode,
+                                  _ptr(noise), _ptr(acc), _ptr(tok), _ptr(racc), _ptr(rtok),
+                                  _ptr(st))
+        N.check(rc, "strim_verify")
+        return {"accepted": acc, "token": tok, "status": st,
+                "row_accept": None if racc is None else racc[:, :k], "row_token": rtok}
+
+
+def mask_logits(logits: torch.Tensor, mask_words: torch.Tensor | None, stream=None):
+    """maskLogits (TokenMask.swift:15-17): float32 logits with disallowed tokens at -inf."""
+    if logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    R, V = logits.shape
+    _check_cuda(logits, mask_words)
+    out = torch.empty(R, V, dtype=torch.float32, device=logits.device)
+    mstride = 0 if mask_words is None else mask_words.shape[-1]
+    N.check(N.lib().strim_mask_logits(_stream(stream), _ptr(logits), _dtype_code(logits), R, V,
+                                      logits.stride(0), _ptr(mask_words), mstride, _ptr(out)),
+            "strim_mask_logits")
+    return out
+
+
+def draft_argmax(draft_logits: torch.Tensor, draft_to_full: torch.Tensor | None = None,
+                 stream=None):
+    """MTP.nextTokenIndex (MTP.swift:104-111): table[argmax(draft logits)] per row."""
+    if draft_logits.dim() == 1:
+        draft_logits = draft_logits.unsqueeze(0)
+    R, Vd = draft_logits.shape
+    _check_cuda(draft_logits, draft_to_full)
+    out = torch.empty(R, dtype=torch.int32, device=draft_logits.device)
+    N.check(N.lib().strim_draft_argmax(_stream(stream), _ptr(draft_logits),
+                                       _dtype_code(draft_logits), R, Vd, draft_logits.stride(0),
+                                       _ptr(draft_to_full), _ptr(out)), "strim_draft_argmax")
+    return out
+
+
+def pack_mask(allowed: torch.Tensor) -> torch.Tensor:
+    """bool [..., V] -> int32 words [..., ceil(V/32)], bit (i & 31) of word (i >> 5)
+    (the byte layout of the reference's UInt64 bitset, GrammarVocab.swift:77-86)."""
+    V = allowed.shape[-1]
+    W = (V + 31) // 32
+    pad = torch.zeros(allowed.shape[:-1] + (W * 32,), dtype=torch.int64, device=allowed.device)
+    pad[..., :V] = allowed.to(torch.int64)
+    bits = pad.reshape(allowed.shape[:-1] + (W, 32))
+    words = (bits << torch.arange(32, device=allowed.device, dtype=torch.int64)).sum(-1)
+    return _to_i32(words)
+
+
+def _to_i32(words: torch.Tensor) -> torch.Tensor:
+    w = words & 0xFFFFFFFF
+    w = torch.where(w >= (1 << 31), w - (1 << 32), w)
+    return w.to(torch.int32)

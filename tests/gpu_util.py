@@ -1,0 +1,105 @@
+"""Helpers shared by the GPU parity tests: move seeded host inputs to the device, run
+the HIP path and the oracle on the same inputs, and compare to the parity bar:
+  - statuses equal;
+  - token ids bit-exact unless the oracle's fp64 decision margin is below TIE_EPS;
+  - processed probabilities within 1e-6 relative (plus 1e-12 absolute)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle as O
+from strim_amd import ops
+from strim_amd import workloads as W
+
+PROB_RTOL = 1e-6
+
+
+def dev_logits(x: np.ndarray, dtype: str) -> torch.Tensor:
+    if dtype == "bf16":
+        bits = W.bf16_bits(W.bf16_round(x)).view(np.int16)
+        return torch.from_numpy(bits.copy()).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def host_logits(x: np.ndarray, dtype: str) -> np.ndarray:
+    return W.bf16_round(x) if dtype == "bf16" else np.ascontiguousarray(x, np.float32)
+
+
+def dev(a, dt=None):
+    if a is None:
+        return None
+    a = np.ascontiguousarray(a if dt is None else np.asarray(a, dt))
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a.copy()).cuda()
+
+
+def run_sample(ctx, x, params, dtype="bf16", mask=None, history=None, history_len=None,
+               noise_mode=O.NOISE_ICDF, noise=None, probs=True):
+    out_ids, out_st, out_p = ctx.sample(dev_logits(x, dtype), params, mask=dev(mask),
+                                        history=dev(history, np.int32),
+                                        history_len=dev(history_len, np.int32),
+                                        noise_mode=noise_mode, noise=dev(noise, np.float32),
+                                        want_probs=probs)
+    torch.cuda.synchronize()
+    return (out_ids.cpu().numpy(), out_st.cpu().numpy(),
+            None if out_p is None else out_p.cpu().numpy())
+
+
+def check_sample(ctx, x, params, dtype="bf16", mask=None, history=None, history_len=None,
+                 noise_mode=O.NOISE_ICDF, noise=None, probs=True, label=""):
+    xh = host_logits(x, dtype)
+    ids, st, pr = run_sample(ctx, xh, params, dtype, mask, history, history_len, noise_mode,
+                             noise, probs)
+    ref = O.sample(xh, params, mask=mask, history=history, history_len=history_len,
+                   noise_mode=noise_mode, noise=noise, want_probs=probs)
+    np.testing.assert_array_equal(st, ref["status"], err_msg=f"{label} status")
+    for r in range(len(ids)):
+        if ids[r] != ref["token"][r]:
+            assert ref["margin"][r] < O.TIE_EPS, (
+                f"{label} row {r}: gpu {ids[r]} oracle {ref['token'][r]} "
+                f"margin {ref['margin'][r]:.3g} status {st[r]}")
+    if probs:
+        for r in range(len(ids)):
+            if ref["status"][r] != 0 or ref["margin"][r] < O.TIE_EPS:
+                continue
+            a, b = pr[r].astype(np.float64), ref["probs"][r].astype(np.float64)
+            np.testing.assert_array_equal(a > 0, b > 0, err_msg=f"{label} row {r} support")
+            np.testing.assert_allclose(a, b, rtol=PROB_RTOL, atol=1e-12,
+                                       err_msg=f"{label} row {r} probs")
+    return ids, st, ref
+
+
+def run_verify(ctx, target, k, drafts, params, dtype="bf16", mask=None, history=None,
+               history_len=None, noise_mode=O.NOISE_ICDF, noise=None, draft_logits=None,
+               table=None):
+    B = target.shape[0]
+    out = ctx.verify(dev_logits(target.reshape(B, k + 1, -1), dtype),
+                     dev(np.asarray(drafts, np.int32).reshape(B, k)), params,
+                     draft_logits=None if draft_logits is None else dev_logits(draft_logits, dtype),
+                     draft_to_full=dev(table, np.int32), mask=dev(mask),
+                     history=dev(history, np.int32), history_len=dev(history_len, np.int32),
+                     noise_mode=noise_mode, noise=dev(noise, np.float32))
+    torch.cuda.synchronize()
+    return {k_: (None if v is None else v.cpu().numpy()) for k_, v in out.items()}
+
+
+def check_verify(ctx, target, k, drafts, params, dtype="bf16", mask=None, history=None,
+                 history_len=None, noise_mode=O.NOISE_ICDF, noise=None, draft_logits=None,
+                 table=None, label=""):
+    th = host_logits(target, dtype)
+    dlh = None if draft_logits is None else host_logits(draft_logits, dtype)
+    g = run_verify(ctx, th, k, drafts, params, dtype, mask, history, history_len, noise_mode,
+                   noise, dlh, table)
+    ref = O.verify(th, k, np.asarray(drafts, np.int32).reshape(th.shape[0], k), params,
+                   draft_logits=dlh, draft_to_full=table, mask=mask, history=history,
+                   history_len=history_len, noise_mode=noise_mode, noise=noise)
+    np.testing.assert_array_equal(g["status"], ref["status"], err_msg=f"{label} status")
+    for b in range(th.shape[0]):
+        same = (g["accepted"][b] == ref["accepted"][b] and g["token"][b] == ref["token"][b])
+        if not same:
+            assert ref["margin"][b] < O.TIE_EPS, (
+                f"{label} seq {b}: gpu ({g['accepted'][b]},{g['token'][b]}) oracle "
+                f"({ref['accepted'][b]},{ref['token'][b]}) margin {ref['margin'][b]:.3g}")
+    return g, ref

@@ -1,0 +1,330 @@
+"""Pins of the CPU oracle (CPU only).
+
+Each check is chosen so a plausible mistake in the oracle fails it:
+  - published RNG vectors (SplitMix64, Random123 Philox4x32-10);
+  - the reference's own known-answer tests (SpecSamplingTests.swift:58-68,70-88,181-197);
+  - an independent pure-Python restatement on tiny rows (tests/pyref.py);
+  - exact icdf quantile grids (the draw reproduces the filtered distribution);
+  - chi-square marginals of the verifier (the lossless property, SpecSamplingTests.swift:104-156);
+  - closed-form penalty steps.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import pyref
+
+
+# ---------------------------------------------------------------- RNG ----
+def test_splitmix64_published_outputs(oracle_mod):
+    # SpecSampling.mix(0, j) is the j-th output of SplitMix64 seeded with 0 (Vigna's
+    # splitmix64.c: e220a8397b1dcdaf, 6e789e6aa1b965f4, 06c45d188009454f, f88bb8a8724c81ec)
+    want = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+    assert [oracle_mod.mix(0, j) for j in range(4)] == want
+
+
+@pytest.mark.parametrize("ctr,key,want", [
+    ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+    ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+    ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+     [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+])
+def test_philox_random123_kat(oracle_mod, ctr, key, want):
+    assert oracle_mod.philox4x32_10(ctr, key).tolist() == want
+
+
+def test_uniforms_layout(oracle_mod):
+    u = oracle_mod.uniforms(5, 9, 11)
+    k = oracle_mod.mix(5, 9)
+    key = [k & 0xFFFFFFFF, k >> 32]
+    for i in range(11):
+        w = oracle_mod.philox4x32_10([i // 4, 0, 0, 0], key)[i % 4]
+        assert u[i] == np.float32((int(w) >> 8) * 2.0 ** -24)
+        assert 0.0 <= u[i] < 1.0
+    assert u[0] == oracle_mod.lib().so_uniform(5, 9, 0)
+
+
+def test_gumbel_transform(oracle_mod):
+    for u in [1e-40, 1e-30, 0.1, 0.5, 0.999]:
+        uu = max(np.float32(u), np.float32(1e-30))
+        assert oracle_mod.gumbel(u) == pytest.approx(-math.log(-math.log(float(uu))), rel=1e-15)
+
+
+# ------------------------------------------------ reference known-answer tests ----
+def _probs(oracle_mod, row, **kw):
+    r = oracle_mod.sample(np.asarray(row, np.float32)[None], oracle_mod.make_params(1, **kw),
+                          want_probs=True)
+    return r["probs"][0].astype(np.float64)
+
+
+def test_filtered_matches_reference(oracle_mod):
+    # SpecSamplingTests.filteredMatchesReference (SpecSampling tests :58-68)
+    row = np.log(np.array([8, 4, 2, 1, 1], np.float32)).astype(np.float32)
+    full = _probs(oracle_mod, row)
+    assert abs(full[0] - 0.5) < 1e-5 and abs(full[4] - 0.0625) < 1e-5
+    k2 = _probs(oracle_mod, row, top_k=2)
+    assert abs(k2[0] - 2 / 3) < 1e-5 and abs(k2[1] - 1 / 3) < 1e-5 and k2[2] == 0
+    p7 = _probs(oracle_mod, row, top_p=0.7)
+    assert abs(p7[0] - 2 / 3) < 1e-5 and abs(p7[1] - 1 / 3) < 1e-5 and p7[2] == 0
+
+
+def test_temperature_zero_path_equals_argmax(oracle_mod):
+    # SpecSamplingTests.temperatureZeroPathEqualsArgmax (:70-88), rows as k=1 verifies
+    rng = np.random.default_rng(7)
+    n, V = 1000, 64
+    x = (rng.normal(size=(n, V)) * 3).astype(np.float32)
+    best = x.argmax(-1).astype(np.int32)
+    nz = rng.random((n, 2, V + 1), dtype=np.float32)
+    p = oracle_mod.make_params(n, temperature=1e-4)
+    tgt = np.repeat(x[:, None, :], 2, axis=1)
+    plain = oracle_mod.sample(x, p, noise_mode=oracle_mod.NOISE_GUMBEL, noise=nz[:, 0])
+    assert (plain["token"] == best).all()
+    hit = oracle_mod.verify(tgt, 1, best[:, None], p, noise_mode=oracle_mod.NOISE_GUMBEL, noise=nz)
+    assert hit["row_accept"].all()
+    other = ((best + 1) % V).astype(np.int32)
+    miss = oracle_mod.verify(tgt, 1, other[:, None], p, noise_mode=oracle_mod.NOISE_GUMBEL,
+                             noise=nz)
+    assert not miss["row_accept"].any()
+    assert (miss["row_token"][:, 0] == best).all()
+
+
+def test_verify_accept_count_semantics(oracle_mod):
+    # SpecSamplingTests.verifyAcceptCountSemantics (:181-197)
+    V = 8
+    r0 = np.full(V, -50, np.float32); r0[1] = 0
+    r1 = r0.copy(); r1[1] = -50; r1[2] = 0
+    r2 = np.full(V, -50, np.float32); r2[5] = 0
+    logits = np.stack([r0, r1, r2, r2])
+    for first in range(20):
+        p = oracle_mod.make_params(1, temperature=1.0, seed=1, position=first)
+        for mode in (oracle_mod.NOISE_GUMBEL, oracle_mod.NOISE_ICDF):
+            out = oracle_mod.verify(logits[None], 3, [[1, 2, 3]], p, noise_mode=mode)
+            assert out["accepted"][0] == 2 and out["token"][0] == 5
+    out = oracle_mod.verify(logits[2:3][None], 0, np.zeros((1, 0), np.int32),
+                            oracle_mod.make_params(1, seed=1))
+    assert out["accepted"][0] == 0 and out["token"][0] == 5
+
+
+def test_verify_reproducible_and_seed_sensitive(oracle_mod):
+    # SpecSamplingTests.verifyIsReproducibleAndSeedSensitive (:158-179)
+    # a flat row: the drawn MLX row of the reference test is not reproducible here, and
+    # a peaked row would leave too few distinct outcomes for the sensitivity check
+    rng = np.random.default_rng(3)
+    V, k = 32, 3
+    logits = (rng.normal(size=(k + 1, V)) * 0.5).astype(np.float32)
+
+    def run(seed, first=5):
+        p = oracle_mod.make_params(1, temperature=1, top_k=20, top_p=0.95, seed=seed,
+                                   position=first)
+        o = oracle_mod.verify(logits[None], k, [[1, 2, 3]], p, noise_mode=oracle_mod.NOISE_GUMBEL)
+        return (int(o["accepted"][0]), int(o["token"][0]))
+
+    assert run(9) == run(9)
+    assert len({run(s) for s in range(40)}) > 3
+    assert len({run(9, f) for f in range(40)}) > 3
+
+
+# ------------------------------------------------------------- brute force ----
+def _rand_params(rng, n):
+    return dict(
+        temperature=rng.choice([0.3, 0.7, 1.0, 1.7]),
+        top_k=int(rng.choice([0, 1, 2, 3, n - 1, n, n + 5])),
+        top_p=float(rng.choice([1.0, 0.99, 0.9, 0.5, 0.2, 1e-3])),
+        min_p=float(rng.choice([0.0, 0.0, 0.05, 0.3, 1.0])),
+        repetition_penalty=float(rng.choice([1.0, 1.3, 0.8])),
+        presence_penalty=float(rng.choice([0.0, 0.5, -0.25])),
+        frequency_penalty=float(rng.choice([0.0, 0.3])),
+        flags=int(rng.choice([0, 1])),
+    )
+
+
+def test_oracle_matches_independent_python_restatement(oracle_mod):
+    rng = np.random.default_rng(11)
+    for trial in range(400):
+        V = int(rng.integers(1, 9))
+        # small integer-ish logits create exact ties on purpose
+        x = (rng.integers(-3, 4, size=V) * rng.choice([0.5, 1.0])).astype(np.float32)
+        if trial % 3 == 0:
+            x = rng.normal(size=V).astype(np.float32)
+        mask = rng.random(V) < 0.8
+        if not mask.any():
+            mask[rng.integers(0, V)] = True
+        hist = rng.integers(-1, V + 1, size=int(rng.integers(0, 6))).astype(np.int32)
+        kw = _rand_params(rng, V)
+        p = oracle_mod.make_params(1, **kw)[0]
+        l_py = pyref.process(x, p, mask, hist.tolist())
+        st, l_c = oracle_mod.process_row(x, p, mask=oracle_mod.pack_mask(mask), history=hist)
+        assert st == 0
+        np.testing.assert_array_equal(np.asarray(l_py, np.float32), l_c)
+        kept = pyref.filtered(l_py, p)
+        res = oracle_mod.sample(x[None], p.reshape(1), mask=oracle_mod.pack_mask(mask)[None],
+                                history=hist[None] if hist.size else None,
+                                history_len=np.array([hist.size], np.int32) if hist.size else None,
+                                want_probs=True, noise=np.array([[0.37, 0.5]], np.float32))
+        probs = np.zeros(V)
+        for i, pr in kept:
+            probs[i] = pr
+        np.testing.assert_allclose(res["probs"][0], probs, rtol=1e-6, atol=1e-7)
+        assert res["n_kept"][0] == len(kept)
+        assert res["token"][0] == pyref.icdf_draw(kept, np.float32(0.37))
+
+
+def test_icdf_quantile_grid_reproduces_distribution(oracle_mod):
+    # u on an exact grid: the share of u mapped to token i must equal P(i) to 1/N
+    rng = np.random.default_rng(5)
+    V, N = 12, 4096
+    x = rng.normal(size=V).astype(np.float32) * 2
+    for kw in [dict(), dict(top_k=4), dict(top_p=0.8), dict(min_p=0.1, temperature=0.6),
+               dict(top_k=6, top_p=0.7, flags=1)]:
+        p = oracle_mod.make_params(N, **kw)
+        u = ((np.arange(N) + 0.5) / N).astype(np.float32)
+        nz = np.stack([u, np.zeros(N, np.float32)], 1)
+        r = oracle_mod.sample(np.repeat(x[None], N, 0), p, noise=nz, want_probs=True)
+        freq = np.bincount(r["token"], minlength=V) / N
+        np.testing.assert_allclose(freq, r["probs"][0], atol=1.5 / N)
+
+
+def _chi2_crit01(df):
+    # Wilson-Hilferty approximation of the p=0.01 critical value
+    z = 2.3263478740408408
+    return df * (1 - 2 / (9 * df) + z * math.sqrt(2 / (9 * df))) ** 3
+
+
+def _chi2(counts, probs):
+    n = counts.sum()
+    e = n * probs
+    big = e >= 5
+    stat = (((counts[big] - e[big]) ** 2) / e[big]).sum()
+    cells = int(big.sum())
+    pe, po = e[~big].sum(), counts[~big].sum()
+    if pe >= 5:
+        stat += (po - pe) ** 2 / pe
+        cells += 1
+    else:
+        assert po <= 20 + 10 * pe
+    return stat, _chi2_crit01(max(cells - 1, 1))
+
+
+@pytest.mark.parametrize("t,k,pp", [(1.0, 0, 1.0), (0.8, 5, 1.0), (1.0, 0, 0.8), (1.0, 6, 0.9)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_verify_marginal_matches_target(oracle_mod, t, k, pp, mode):
+    # SpecSamplingTests.marginalMatchesTarget (:104-118): accept-or-residual ~ P
+    rng = np.random.default_rng(11)
+    V, n = 16, 200_000
+    row = (rng.normal(size=V) * 2).astype(np.float32)
+    P = _probs(oracle_mod, row, temperature=t, top_k=k, top_p=pp)
+    order = np.argsort(-P, kind="stable")
+    drafts = [int(order[0]), int(order[2])]
+    zero = np.nonzero(P == 0)[0]
+    if zero.size:
+        drafts.append(int(zero[0]))
+    tgt = np.repeat(np.repeat(row[None, None], 2, 1), n, 0)
+    for jd, d in enumerate(drafts):
+        p = oracle_mod.make_params(n, temperature=t, top_k=k, top_p=pp, seed=2000 + jd)
+        p["position"] = np.arange(n, dtype=np.uint64) * 2
+        out = oracle_mod.verify(tgt, 1, np.full((n, 1), d, np.int32), p, noise_mode=mode)
+        acc = out["row_accept"][:, 0].astype(bool)
+        emitted = np.where(acc, d, out["row_token"][:, 0])
+        stat, crit = _chi2(np.bincount(emitted, minlength=V).astype(np.float64), P)
+        assert stat < crit, (t, k, pp, d, stat, crit)
+        assert abs(acc.mean() - P[d]) < 0.01
+
+
+def test_sampler_gumbel_marginal(oracle_mod):
+    # plain draws (both noise modes, Sampler and SpecSampling scoring) follow P
+    rng = np.random.default_rng(21)
+    V, n = 16, 100_000
+    row = (rng.normal(size=V) * 2).astype(np.float32)
+    for kw in [dict(top_k=5), dict(top_p=0.8), dict(top_k=6, top_p=0.9, flags=7)]:
+        P = _probs(oracle_mod, row, **kw)
+        for mode in (0, 1):
+            p = oracle_mod.make_params(n, seed=77, **kw)
+            p["position"] = np.arange(n, dtype=np.uint64)
+            r = oracle_mod.sample(np.repeat(row[None], n, 0), p, noise_mode=mode)
+            stat, crit = _chi2(np.bincount(r["token"], minlength=V).astype(np.float64), P)
+            assert stat < crit, (kw, mode, stat, crit)
+
+
+# --------------------------------------------------------------- penalties ----
+def test_penalty_closed_form(oracle_mod):
+    x = np.array([2.0, -2.0, 0.0, 3.0, 1.0], np.float32)
+    p = oracle_mod.make_params(1, repetition_penalty=2.0, presence_penalty=0.5,
+                               frequency_penalty=0.25, temperature=0.5)[0]
+    st, l = oracle_mod.process_row(x, p, history=np.array([0, 1, 2, 0, 7, -1], np.int32))
+    assert st == 0
+    # token 0: count 2 -> 2/2 - 0.25*2 - 0.5 = 0 ; token 1: count 1 -> -2*2 - .25 - .5
+    want = np.array([0.0, -4.75, -0.75, 3.0, 1.0], np.float32) / np.float32(0.5)
+    np.testing.assert_array_equal(l, want)
+    # defaults are exact no-ops
+    st, l0 = oracle_mod.process_row(x, oracle_mod.make_params(1)[0],
+                                    history=np.array([0, 1, 2], np.int32))
+    np.testing.assert_array_equal(l0, x)
+
+
+def test_row_errors(oracle_mod):
+    V = 10
+    x = np.zeros((4, V), np.float32)
+    x[1, 3] = np.nan
+    p = oracle_mod.make_params(4)
+    p["top_p"][2] = 0.0  # invalid
+    allowed = np.ones((4, V), bool)
+    allowed[3] = False
+    r = oracle_mod.sample(x, p, mask=oracle_mod.pack_mask(allowed))
+    assert r["status"].tolist() == [0, oracle_mod.STRIM_ENONFINITE, oracle_mod.STRIM_EINVAL,
+                                    oracle_mod.STRIM_EEMPTY]
+    assert (r["token"][1:] == -1).all()
+    # a NaN in a masked position is ignored
+    allowed2 = np.ones((1, V), bool)
+    allowed2[0, 3] = False
+    r = oracle_mod.sample(x[1:2], p[:1], mask=oracle_mod.pack_mask(allowed2))
+    assert r["status"][0] == 0
+
+
+def test_masked_greedy_and_forbidden_draft(oracle_mod):
+    # ConstraintRowTests.verifyRows (GrammarTests.swift:325-371): a peak on a forbidden
+    # token must not win; a forbidden draft is rejected with probability 1
+    V = 40
+    peak = np.zeros(V, np.float32); peak[7] = 10; peak[3] = 1
+    allowed = np.ones(V, bool); allowed[7] = False
+    m = oracle_mod.pack_mask(allowed)
+    g = oracle_mod.sample(peak[None], oracle_mod.make_params(1, temperature=0), mask=m[None])
+    assert g["token"][0] == 3
+    for seed in range(50):
+        p = oracle_mod.make_params(1, temperature=1.0, seed=seed, position=1)
+        out = oracle_mod.verify(np.stack([peak, peak])[None], 1, [[7]], p,
+                                mask=np.stack([m, m])[None], noise_mode=oracle_mod.NOISE_GUMBEL)
+        assert out["accepted"][0] == 0 and out["token"][0] != 7
+
+
+def test_general_q_reduces_to_one_hot(oracle_mod):
+    # with a draft distribution concentrated on the draft (q(d) = 1), the general
+    # residual max(0, p - q) and accept rule give exactly the reference's one-hot result
+    rng = np.random.default_rng(9)
+    B, k, V = 6, 2, 50
+    tgt = rng.normal(size=(B, k + 1, V)).astype(np.float32) * 2
+    table = np.arange(0, V, 2, dtype=np.int32)
+    Vd = table.size
+    drafts = rng.choice(table, size=(B, k)).astype(np.int32)
+    dl = np.full((B, k, Vd), -1e4, np.float32)
+    for b in range(B):
+        for j in range(k):
+            dl[b, j, np.searchsorted(table, drafts[b, j])] = 0.0
+    p = oracle_mod.make_params(B, temperature=0.9, seed=np.arange(B, dtype=np.uint64) + 4)
+    for mode in (0, 1):
+        one = oracle_mod.verify(tgt, k, drafts, p, noise_mode=mode)
+        gen = oracle_mod.verify(tgt, k, drafts, p, draft_logits=dl, draft_to_full=table,
+                                noise_mode=mode)
+        for key in ("accepted", "token", "row_accept", "row_token", "status"):
+            np.testing.assert_array_equal(one[key], gen[key])
+
+
+def test_bf16_round_matches_torch():
+    import torch
+
+    from strim_amd import workloads
+
+    x = np.random.default_rng(0).normal(size=10000).astype(np.float32) * 7
+    ours = workloads.bf16_round(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(ours, theirs)

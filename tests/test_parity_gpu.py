@@ -1,0 +1,319 @@
+"""GPU parity: the HIP path against the CPU oracle on identical seeded inputs.
+
+Full-size cases use the benchmark configurations; the sweep covers small and ragged
+shapes, ties, masks, penalties, both noise modes, the Sampler flags and error rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import check_sample, check_verify, dev, dev_logits, run_sample
+from strim_amd import ops
+from strim_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+# ------------------------------------------------------------ small sweep ----
+def _sweep_case(rng, V, B):
+    x = rng.normal(0, rng.choice([0.5, 2.0, 4.0]), size=(B, V)).astype(np.float32)
+    if rng.random() < 0.3:  # heavy exact ties
+        x = (rng.integers(-4, 4, size=(B, V)) * 0.5).astype(np.float32)
+    allowed = None
+    if rng.random() < 0.5:
+        allowed = rng.random((B, V)) < rng.choice([0.01, 0.3, 0.9])
+        for r in range(B):
+            if not allowed[r].any():
+                allowed[r, rng.integers(0, V)] = True
+    H = int(rng.choice([0, 0, 8, 64]))
+    hist = rng.integers(-2, V + 2, size=(B, H)).astype(np.int32) if H else None
+    hl = rng.integers(0, H + 1, size=B).astype(np.int32) if H else None
+    p = O.make_params(
+        B, temperature=rng.choice([0.0, 0.5, 0.8, 1.0, 1.5], size=B),
+        top_k=rng.choice([0, 0, 1, 5, 40, V, V + 3], size=B),
+        top_p=rng.choice([1.0, 0.95, 0.8, 0.3], size=B),
+        min_p=rng.choice([0.0, 0.0, 0.02, 0.2], size=B),
+        repetition_penalty=rng.choice([1.0, 1.2], size=B),
+        presence_penalty=rng.choice([0.0, 0.4], size=B),
+        frequency_penalty=rng.choice([0.0, 0.2], size=B),
+        flags=rng.choice([0, 0, 1, 7], size=B),
+        seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+        position=rng.integers(0, 1000, size=B).astype(np.uint64))
+    mask = None if allowed is None else W.pack_mask(allowed)
+    return x, p, mask, hist, hl
+
+
+@pytest.mark.parametrize("V", [1, 7, 64, 1000, 4096, 4097, 9001, 40000])
+def test_sweep_small(ctx, V):
+    rng = np.random.default_rng(1000 + V)
+    for it in range(6):
+        B = int(rng.choice([1, 3, 8, 16]))
+        x, p, mask, hist, hl = _sweep_case(rng, V, B)
+        for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+            for injected in (False, True):
+                noise = None
+                if injected:
+                    n = (V + 1) if mode == O.NOISE_GUMBEL else 2
+                    noise = rng.random((B, n), dtype=np.float32)
+                say(f"sweep V={V} it={it} B={B} mode={mode} injected={injected}")
+                dt = "bf16" if it % 2 == 0 else "f32"
+                check_sample(ctx, x, p, dt, mask, hist, hl, mode, noise,
+                             label=f"V={V} it={it} mode={mode}")
+
+
+# ------------------------------------------------------------- configs ----
+def test_cfg1_fp32_chain_and_greedy(ctx):
+    w = W.cfg1()
+    say("cfg1 icdf")
+    check_sample(ctx, w["x"], w["params"], "f32", None, w["history"], w["history_len"],
+                 O.NOISE_ICDF, w["noise"], label="cfg1")
+    say("cfg1 gumbel philox")
+    check_sample(ctx, w["x"], w["params"], "f32", None, w["history"], w["history_len"],
+                 O.NOISE_GUMBEL, None, label="cfg1 gumbel")
+    say("cfg1 greedy")
+    ids, st, ref = check_sample(ctx, w["x"], w["greedy_params"], "f32", None, w["history"],
+                                w["history_len"], label="cfg1 greedy")
+    assert ids[0] in set(w["spikes"].tolist())
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_ICDF, O.NOISE_GUMBEL])
+@pytest.mark.parametrize("injected", [False, True])
+def test_cfg2_heterogeneous(ctx, mode, injected):
+    w = W.cfg2()
+    B, V = w["x"].shape
+    noise = w["noise"] if mode == O.NOISE_ICDF else np.random.default_rng(9).random(
+        (B, V + 1), dtype=np.float32)
+    say(f"cfg2 mode={mode} injected={injected}")
+    check_sample(ctx, w["x"], w["params"], "bf16", None, w["history"], w["history_len"], mode,
+                 noise if injected else None, label="cfg2")
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_ICDF, O.NOISE_GUMBEL])
+def test_cfg3_masks(ctx, mode):
+    w = W.cfg3()
+    say(f"cfg3 mode={mode}")
+    ids, st, ref = check_sample(ctx, w["x"], w["params"], "bf16", w["mask"], None, None, mode,
+                                w["noise"] if mode == O.NOISE_ICDF else None, label="cfg3")
+    assert (st == 0).all()
+    for r in range(len(ids)):
+        assert w["allowed"][r, ids[r]]
+    assert ids[6] == int(np.nonzero(w["allowed"][6])[0][0])
+
+
+def test_cfg5_stress_batch(ctx):
+    w = W.cfg5()
+    say("cfg5")
+    check_sample(ctx, w["x"], w["params"], "bf16", w["mask"], w["history"], w["history_len"],
+                 O.NOISE_ICDF, None, label="cfg5")
+
+
+# ------------------------------------------------------------ large kept sets ----
+@pytest.mark.parametrize("mode", [O.NOISE_ICDF, O.NOISE_GUMBEL])
+def test_unfiltered_full_vocab(ctx, mode):
+    # no top-k / top-p / min-p: the kept set is the whole row (histogram-summary path)
+    rng = np.random.default_rng(31)
+    B, V = 8, W.V_DEFAULT
+    x = rng.normal(0, 1.5, size=(B, V)).astype(np.float32)
+    p = O.make_params(B, temperature=np.float32(0.9), seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                      position=np.arange(B, dtype=np.uint64))
+    say(f"unfiltered mode={mode}")
+    check_sample(ctx, x, p, "bf16", None, None, None, mode, None, label="unfiltered")
+
+
+def test_large_nucleus_top_p(ctx):
+    rng = np.random.default_rng(32)
+    B, V = 8, W.V_DEFAULT
+    x = rng.normal(0, 1.0, size=(B, V)).astype(np.float32)
+    p = O.make_params(B, top_p=np.linspace(0.3, 0.99, B).astype(np.float32),
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64))
+    for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+        say(f"large nucleus mode={mode}")
+        check_sample(ctx, x, p, "bf16", None, None, None, mode, None, label="nucleus")
+
+
+def test_flat_row_ties(ctx):
+    # every logit equal: order is by id; top-k keeps the K smallest ids
+    V, B = 10000, 4
+    x = np.zeros((B, V), np.float32)
+    p = O.make_params(B, top_k=[100, 0, 3000, 7], top_p=[1.0, 0.5, 0.9, 1.0], flags=[0, 0, 1, 1],
+                      seed=5, position=np.arange(B, dtype=np.uint64))
+    say("flat ties")
+    ids, st, ref = check_sample(ctx, x, p, "bf16", label="flat")
+
+
+# ------------------------------------------------------------ errors / layout ----
+def test_row_errors(ctx):
+    V, B = 5000, 5
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(B, V)).astype(np.float32)
+    x[1, 17] = np.nan
+    x[4, 9] = np.inf
+    allowed = np.ones((B, V), bool)
+    allowed[3] = False
+    p = O.make_params(B)
+    p["top_p"][2] = 0.0
+    say("row errors")
+    ids, st, ref = check_sample(ctx, x, p, "f32", W.pack_mask(allowed), label="errors")
+    assert st.tolist() == [0, O.STRIM_ENONFINITE, O.STRIM_EINVAL, O.STRIM_EEMPTY,
+                           O.STRIM_ENONFINITE]
+    assert (ids[1:] == -1).all()
+
+
+def test_strided_and_unaligned_rows(ctx):
+    rng = np.random.default_rng(4)
+    B, V = 4, 3001
+    x = rng.normal(size=(B, V + 13)).astype(np.float32)
+    p = O.make_params(B, top_k=10, seed=3)
+    for dt in ("f32", "bf16"):
+        full = dev_logits(x, dt)
+        view = full[:, 1:V + 1]  # row stride V+13, base not 16-byte aligned
+        say(f"strided dtype={dt}")
+        ids, st, _ = ctx.sample(view, p, noise=dev(np.full((B, 2), 0.3, np.float32)))
+        torch.cuda.synchronize()
+        xh = W.bf16_round(x[:, 1:V + 1]) if dt == "bf16" else x[:, 1:V + 1]
+        ref = O.sample(np.ascontiguousarray(xh), p, noise=np.full((B, 2), 0.3, np.float32))
+        np.testing.assert_array_equal(ids.cpu().numpy(), ref["token"])
+
+
+def test_reproducible(ctx):
+    w = W.cfg2()
+    say("reproducible")
+    a = run_sample(ctx, w["x"], w["params"], "bf16", None, w["history"], w["history_len"],
+                   O.NOISE_GUMBEL, None, probs=False)[0]
+    b = run_sample(ctx, w["x"], w["params"], "bf16", None, w["history"], w["history_len"],
+                   O.NOISE_GUMBEL, None, probs=False)[0]
+    np.testing.assert_array_equal(a, b)
+    p2 = w["params"].copy()
+    p2["position"] += 1
+    c = run_sample(ctx, w["x"], p2, "bf16", None, w["history"], w["history_len"],
+                   O.NOISE_GUMBEL, None, probs=False)[0]
+    assert (a != c).any()
+
+
+# ------------------------------------------------------------------ verify ----
+def test_verify_accept_count_semantics(ctx):
+    # SpecSamplingTests.verifyAcceptCountSemantics (SpecSamplingTests.swift:181-197)
+    V = 8
+    r0 = np.full(V, -50, np.float32); r0[1] = 0
+    r1 = r0.copy(); r1[1] = -50; r1[2] = 0
+    r2 = np.full(V, -50, np.float32); r2[5] = 0
+    logits = np.stack([r0, r1, r2, r2])[None]
+    say("verify KAT")
+    for first in range(20):
+        p = O.make_params(1, temperature=1.0, seed=1, position=first)
+        for mode in (O.NOISE_GUMBEL, O.NOISE_ICDF):
+            g, _ = check_verify(ctx, logits, 3, [[1, 2, 3]], p, "f32", noise_mode=mode)
+            assert g["accepted"][0] == 2 and g["token"][0] == 5
+
+
+@pytest.mark.parametrize("k", [0, 1, 3])
+def test_verify_random(ctx, k):
+    rng = np.random.default_rng(50 + k)
+    for it in range(6):
+        B = int(rng.choice([1, 4, 8]))
+        V = int(rng.choice([50, 4096, 20000, W.V_DEFAULT]))
+        tgt = rng.normal(0, rng.choice([1.0, 3.0]), size=(B, k + 1, V)).astype(np.float32)
+        drafts = rng.integers(0, V, size=(B, k)).astype(np.int32)
+        # sometimes draft the argmax so accepts happen
+        am = tgt[:, :k, :].argmax(-1)
+        pick = rng.random((B, k)) < 0.5
+        drafts[pick] = am[pick]
+        p = O.make_params(B, temperature=rng.choice([0.0, 0.7, 1.0], size=B),
+                          top_k=rng.choice([0, 20], size=B), top_p=rng.choice([1.0, 0.9], size=B),
+                          min_p=rng.choice([0.0, 0.05], size=B),
+                          seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                          position=rng.integers(0, 100, size=B).astype(np.uint64))
+        mask = None
+        if it % 2 == 1:
+            allowed = rng.random((B, k + 1, V)) < 0.5
+            mask = W.pack_mask(allowed)
+        H = 16 if it % 3 == 0 else 0
+        hist = rng.integers(0, V, size=(B, H)).astype(np.int32) if H else None
+        if H:
+            p["repetition_penalty"] = 1.3
+        for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+            say(f"verify k={k} it={it} B={B} V={V} mode={mode}")
+            check_verify(ctx, tgt, k, drafts, p, "bf16", mask, hist, None, mode,
+                         label=f"verify k={k} it={it}")
+
+
+# ------------------------------------------------------------------ aux ops ----
+def test_mask_logits(ctx):
+    rng = np.random.default_rng(6)
+    R, V = 3, 1003
+    x = rng.normal(size=(R, V)).astype(np.float32)
+    allowed = rng.random((R, V)) < 0.4
+    for dt in ("f32", "bf16"):
+        say(f"mask_logits {dt}")
+        out = ops.mask_logits(dev_logits(x, dt), dev(W.pack_mask(allowed))).cpu().numpy()
+        xh = W.bf16_round(x) if dt == "bf16" else x
+        np.testing.assert_array_equal(out, np.where(allowed, xh, -np.inf).astype(np.float32))
+
+
+def test_draft_argmax(ctx):
+    rng = np.random.default_rng(7)
+    R, Vd = 5, 32768
+    dl = rng.normal(size=(R, Vd)).astype(np.float32)
+    table = np.sort(rng.choice(W.V_DEFAULT, size=Vd, replace=False)).astype(np.int32)
+    say("draft_argmax")
+    got = ops.draft_argmax(dev_logits(dl, "bf16"), dev(table)).cpu().numpy()
+    xh = W.bf16_round(dl)
+    np.testing.assert_array_equal(got, table[xh.argmax(-1)])
+
+
+# ------------------------------------------------------------ mirror API ----
+def test_sampler_mirror_matches_oracle(ctx):
+    from strim_amd.sampler import GenParams, Sampler, SamplingConfig, SpecSampling
+
+    rng = np.random.default_rng(8)
+    V = 4000
+    x = rng.normal(size=V).astype(np.float32)
+    xd = dev_logits(x, "f32")[0]
+    s = Sampler(GenParams(temperature=0.9, top_k=20, top_p=0.9, seed=123), ctx=ctx)
+    say("mirror Sampler.sample")
+    for i in range(5):
+        got = s.sample(xd)
+        p = O.make_params(1, temperature=0.9, top_k=20, top_p=0.9, seed=123, position=i,
+                          flags=O.FLAG_SAMPLER_COMPAT)
+        ref = O.sample(x[None], p, noise_mode=O.NOISE_GUMBEL)
+        assert got == ref["token"][0] or ref["margin"][0] < O.TIE_EPS
+    cfg = SamplingConfig(temperature=1.0, top_k=0, top_p=1.0, seed=77)
+    say("mirror SpecSampling.sample")
+    a = [SpecSampling.sample(xd, cfg, i, ctx=ctx) for i in range(20)]
+    b = [SpecSampling.sample(xd, cfg, i, ctx=ctx) for i in range(20)]
+    assert a == b and len(set(a)) > 5
+
+
+# ------------------------------------------------------------ statistics ----
+@pytest.mark.parametrize("t,k,pp", [(1.0, 0, 1.0), (1.0, 6, 0.9)])
+def test_gpu_verify_marginal(ctx, t, k, pp):
+    # marginalMatchesTarget on the GPU verifier: accepted-or-residual ~ P
+    from test_oracle import _chi2
+
+    rng = np.random.default_rng(11)
+    V, n, chunk = 16, 32768, 4096
+    row = (rng.normal(size=V) * 2).astype(np.float32)
+    P = O.sample(row[None], O.make_params(1, temperature=t, top_k=k, top_p=pp),
+                 want_probs=True)["probs"][0].astype(np.float64)
+    d = int(np.argsort(-P, kind="stable")[2])
+    tgt = np.repeat(np.repeat(row[None, None], 2, 1), chunk, 0)
+    for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+        emitted, accs = [], []
+        for c0 in range(0, n, chunk):
+            p = O.make_params(chunk, temperature=t, top_k=k, top_p=pp, seed=99)
+            p["position"] = (np.arange(chunk, dtype=np.uint64) + c0) * 2
+            say(f"marginal mode={mode} chunk={c0}")
+            g = ctx.verify(dev_logits(tgt, "f32"), dev(np.full((chunk, 1), d, np.int32)), p,
+                           noise_mode=mode)
+            acc = g["row_accept"][:, 0].cpu().numpy().astype(bool)
+            emitted.append(np.where(acc, d, g["row_token"][:, 0].cpu().numpy()))
+            accs.append(acc)
+        e = np.concatenate(emitted)
+        stat, crit = _chi2(np.bincount(e, minlength=V).astype(np.float64), P)
+        assert stat < crit
+        assert abs(np.concatenate(accs).mean() - P[d]) < 0.015
