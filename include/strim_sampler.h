@@ -24,7 +24,9 @@
  *   strim_check_params <- request validation (Sources/StrimServer/ChatRequest.swift:148-161).
  *
  * Conventions
- *   - All array arguments are DEVICE pointers unless stated, owned by the caller.
+ *   - All array arguments are DEVICE pointers unless stated, owned by the caller. The
+ *     per-row sampling params are HOST structs (the reference's GenParams are host
+ *     values); they travel inside the kernel arguments, so a call copies nothing.
  *   - Calls are stream-ordered and asynchronous. A context (strim_ctx) owns scratch
  *     memory; calls that share one context must not overlap in time (use one context
  *     per stream), mirroring the reference's single engine thread
@@ -107,12 +109,14 @@ void strim_default_params(strim_sampling_params* p);
 int strim_check_params(const strim_sampling_params* host_params, int32_t n);
 
 /* Create a context on `device` for up to max_rows rows of up to max_vocab tokens per
- * call. Allocates scratch once (hipMalloc); no call below allocates. */
+ * call (max_vocab <= 2^20). Allocates scratch once (hipMalloc); no call below allocates.
+ * Calls with more rows than max_rows are processed in groups. */
 int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t max_vocab);
 int strim_ctx_destroy(strim_ctx* ctx);
 
 /* Sample one token per row from logits [B][V] (row r at logits + r*row_stride elements).
- *   params      device [B]
+ *   params      HOST [B], read during the call (validated like strim_check_params; an
+ *               invalid row fails the call with STRIM_EINVAL before any launch)
  *   mask_words  device [B][mask_stride] uint32 or NULL. Token i allowed iff bit (i & 31)
  *               of word (i >> 5) is set — the byte layout of the reference's UInt64
  *               bitset (GrammarVocab.swift:77-86) on little-endian hosts.
@@ -120,7 +124,8 @@ int strim_ctx_destroy(strim_ctx* ctx);
  *               NULL (= H). Ids outside [0,V) are ignored. Feeds the penalties.
  *   noise       see STRIM_NOISE_*.
  *   out_ids     device [B]; -1 on a row error.
- *   out_status  device [B] or NULL; STRIM_OK or a negative STRIM_E* per row.
+ *   out_status  device [B] or NULL; STRIM_OK or a negative STRIM_E* per row
+ *               (EEMPTY, ENONFINITE, ECAPACITY).
  *   out_probs   device [B][V] float or NULL: the processed distribution (validation).
  * Replaces Sampler.sample / SpecSampling.sample (Sampler.swift:34-54,
  * SpecSampling.swift:109-116) and the batched pick loop (EngineCore.swift:998-1002). */
@@ -140,6 +145,7 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
  *   draft_to_full [Vd] strictly ascending ids < V (Weights.swift:196-209); used only
  *                 with draft_logits.
  *   draft_tokens  [B][k] full-vocab ids.
+ *   params        HOST [B], as strim_sample.
  *   mask_words    [B][k+1][mask_stride] or NULL (VerifyConstraint, TokenMask.swift:7-12).
  *   history       as strim_sample; row j additionally counts drafts[0..j).
  *   noise         ICDF [B][k+1][2]; GUMBEL [B][k+1][V+1]; NULL = Philox at positions
@@ -169,6 +175,18 @@ int strim_mask_logits(void* stream, const void* logits, int32_t dtype, int32_t R
 int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, int32_t R,
                        int32_t Vd, int64_t row_stride, const int32_t* draft_to_full,
                        int32_t* out);
+
+/* ---- per-kernel timing -------------------------------------------------------------
+ * Counterpart of the reference's fenced per-region GPU timer OpTimer
+ * (Sources/StrimCore/OpTimer.swift:1-60). While profiling is on, every kernel a call
+ * launches is bracketed by HIP events recorded on the call's stream; strim_profile_end
+ * synchronises, sums the elapsed time per kernel and turns profiling off. Profiling
+ * allocates its events in strim_profile_begin, never in the calls it times. */
+#define STRIM_KERNEL_COUNT 5 /* scan, collect, final, probs, verify_combine */
+int strim_profile_begin(strim_ctx* ctx, int32_t max_launches);
+int strim_profile_end(strim_ctx* ctx, double* total_ms /* [STRIM_KERNEL_COUNT] */,
+                      int64_t* launches /* [STRIM_KERNEL_COUNT] */);
+const char* strim_kernel_name(int32_t kernel);
 
 /* Library version string (static storage). */
 const char* strim_version(void);

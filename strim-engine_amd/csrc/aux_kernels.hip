@@ -38,12 +38,7 @@ __global__ __launch_bounds__(256) void k_draft_argmax(const void* logits, int dt
     // NaN never wins; -inf rows fall back to index 0 like argMax over all -inf
     if (!isnan(x)) argmax_merge(bv, bi, x, i);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float v2 = __shfl_xor(bv, o, WAVE);
-    int i2 = __shfl_xor(bi, o, WAVE);
-    argmax_merge(bv, bi, v2, i2);
-  }
+  wave_argmax(bv, bi);
   if ((threadIdx.x & (WAVE - 1)) == 0) {
     s_v[threadIdx.x / WAVE] = bv;
     s_i[threadIdx.x / WAVE] = bi;

@@ -10,8 +10,7 @@
 #include "kernels.hpp"
 
 namespace strim {
-__global__ void k_stats(Args a);
-__global__ void k_hist(Args a);
+__global__ void k_scan(Args a);
 __global__ void k_collect(Args a);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
@@ -31,6 +30,12 @@ struct strim_ctx {
   void* base;
   size_t bytes;
   Scratch s;
+  // per-kernel event profiling (off unless strim_profile_begin)
+  int32_t prof_on = 0;
+  int32_t prof_cap = 0;
+  int32_t prof_n = 0;
+  hipEvent_t* prof_ev = nullptr;  // [cap][2]
+  int32_t* prof_kind = nullptr;   // [cap]
 };
 
 namespace {
@@ -54,23 +59,64 @@ int on_device(int32_t device, F fn) {
 }
 
 bool dtype_ok(int32_t d) { return d == STRIM_DTYPE_F32 || d == STRIM_DTYPE_BF16; }
+size_t dtype_size(int32_t d) { return d == STRIM_DTYPE_BF16 ? 2 : 4; }
 
 int32_t vec_ok(const void* p, int64_t row_stride, int32_t dtype) {
   const int64_t per16 = dtype == STRIM_DTYPE_BF16 ? 8 : 4;
   return ((uintptr_t)p % 16 == 0) && (row_stride % per16 == 0) ? 1 : 0;
 }
 
-// The launch sequence shared by strim_sample and strim_verify.
-int run_chain(strim_ctx* ctx, hipStream_t st, Args& a, bool probs) {
-  const int R = a.R, W = a.W;
-  const dim3 grid_rc((unsigned)(R * W));
-  hipLaunchKernelGGL(k_stats, grid_rc, dim3(TPB), 0, st, a);
-  hipLaunchKernelGGL(k_hist, grid_rc, dim3(TPB), 0, st, a);
-  hipLaunchKernelGGL(k_collect, grid_rc, dim3(TPB), 0, st, a);
-  hipLaunchKernelGGL(k_final, dim3((unsigned)R), dim3(FIN_T), 0, st, a);
-  if (probs) hipLaunchKernelGGL(k_probs, grid_rc, dim3(TPB), 0, st, a);
-  (void)ctx;
+enum KernelId { KID_SCAN = 0, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE };
+const char* const kKernelNames[STRIM_KERNEL_COUNT] = {"k_scan", "k_collect", "k_final",
+                                                      "k_probs", "k_verify_combine"};
+
+// Launches `launch()` on stream st, bracketed by profiling events when enabled.
+template <typename F>
+void timed(strim_ctx* ctx, hipStream_t st, int kind, F launch) {
+  if (ctx && ctx->prof_on && ctx->prof_n < ctx->prof_cap) {
+    const int i = ctx->prof_n++;
+    ctx->prof_kind[i] = kind;
+    (void)hipEventRecord(ctx->prof_ev[2 * i], st);
+    launch();
+    (void)hipEventRecord(ctx->prof_ev[2 * i + 1], st);
+  } else {
+    launch();
+  }
+}
+
+bool nofilter(const strim_sampling_params& p, int32_t V) {
+  return !(p.top_k > 0 && p.top_k < V) && !(p.min_p > 0.0f) && !(p.top_p < 1.0f);
+}
+
+// The launch sequence of one row group. k_collect runs only when a row of the group
+// needs the general path's second pass.
+int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
+  bool need_collect = false;
+  for (int i = 0; i < nb; ++i)
+    if (row_class(a.p[i], a.V) == CLS_GENERAL &&
+        !(a.noise_mode == STRIM_NOISE_GUMBEL && nofilter(a.p[i], a.V)))
+      need_collect = true;
+  const dim3 grid_rc((unsigned)(a.R * a.W));
+  timed(ctx, st, KID_SCAN, [&] { hipLaunchKernelGGL(k_scan, grid_rc, dim3(TPB), 0, st, a); });
+  if (need_collect)
+    timed(ctx, st, KID_COLLECT,
+          [&] { hipLaunchKernelGGL(k_collect, grid_rc, dim3(TPB), 0, st, a); });
+  timed(ctx, st, KID_FINAL,
+        [&] { hipLaunchKernelGGL(k_final, dim3((unsigned)a.R), dim3(FIN_T), 0, st, a); });
+  if (probs)
+    timed(ctx, st, KID_PROBS, [&] { hipLaunchKernelGGL(k_probs, grid_rc, dim3(TPB), 0, st, a); });
   return launch_status();
+}
+
+void profile_free(strim_ctx* ctx) {
+  if (ctx->prof_ev) {
+    for (int i = 0; i < 2 * ctx->prof_cap; ++i) (void)hipEventDestroy(ctx->prof_ev[i]);
+    delete[] ctx->prof_ev;
+    delete[] ctx->prof_kind;
+  }
+  ctx->prof_ev = nullptr;
+  ctx->prof_kind = nullptr;
+  ctx->prof_cap = ctx->prof_n = ctx->prof_on = 0;
 }
 
 }  // namespace
@@ -112,9 +158,10 @@ int strim_check_params(const strim_sampling_params* hp, int32_t n) {
 }
 
 int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t max_vocab) {
-  // the fixed-point histogram (2^40 per token) must fit in 64 bits: V < 2^24
+  // V <= 2^20 keeps a row within 256 chunks, the bound of the finalize's per-chunk
+  // LDS tables (and the 2^40 fixed-point masses far from 64-bit overflow)
   if (!out || max_rows <= 0 || max_vocab <= 0 || max_rows > (1 << 20) ||
-      max_vocab >= (1 << 24))
+      max_vocab > (1 << 20))
     return STRIM_EINVAL;
   *out = nullptr;
   strim_ctx* ctx = new (std::nothrow) strim_ctx();
@@ -131,14 +178,13 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
     return o;
   };
   const size_t o_cstat = carve(R * wmax * sizeof(ChunkStat));
+  const size_t o_slot = carve(R * wmax * SLOT * sizeof(Cand));
+  const size_t o_chc = carve(R * wmax * NCB * sizeof(uint32_t));
+  const size_t o_chm = carve(R * wmax * NCB * sizeof(unsigned long long));
+  const size_t o_part = carve(R * wmax * sizeof(ChunkPart));
   const size_t o_rs = carve(R * sizeof(RowState));
-  const size_t o_cs = carve(R * sizeof(uint32_t));
-  const size_t o_ch = carve(R * sizeof(uint32_t));
-  const size_t o_hc = carve(R * NBINS * sizeof(uint32_t));
-  const size_t o_hm = carve(R * NBINS * sizeof(unsigned long long));
   const size_t o_cand = carve(R * CAP * sizeof(Cand));
   const size_t o_nc = carve(R * sizeof(uint32_t));
-  const size_t o_ct = carve(R * wmax * sizeof(ChunkTop));
   ctx->bytes = off;
   int rc = on_device(device, [&]() -> int {
     if (hipMalloc(&ctx->base, ctx->bytes) != hipSuccess) return STRIM_ENOMEM;
@@ -153,14 +199,13 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   }
   char* b = (char*)ctx->base;
   ctx->s.cstat = (ChunkStat*)(b + o_cstat);
+  ctx->s.slot = (Cand*)(b + o_slot);
+  ctx->s.chc = (uint32_t*)(b + o_chc);
+  ctx->s.chm = (unsigned long long*)(b + o_chm);
+  ctx->s.part = (ChunkPart*)(b + o_part);
   ctx->s.rs = (RowState*)(b + o_rs);
-  ctx->s.cnt_stats = (uint32_t*)(b + o_cs);
-  ctx->s.cnt_hist = (uint32_t*)(b + o_ch);
-  ctx->s.hcnt = (uint32_t*)(b + o_hc);
-  ctx->s.hmass = (unsigned long long*)(b + o_hm);
   ctx->s.cand = (Cand*)(b + o_cand);
   ctx->s.ncand = (uint32_t*)(b + o_nc);
-  ctx->s.ctop = (ChunkTop*)(b + o_ct);
   ctx->s.wmax = wmax;
   *out = ctx;
   return STRIM_OK;
@@ -169,6 +214,7 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
 int strim_ctx_destroy(strim_ctx* ctx) {
   if (!ctx) return STRIM_EINVAL;
   int rc = on_device(ctx->device, [&]() -> int {
+    profile_free(ctx);
     if (ctx->base && hipFree(ctx->base) != hipSuccess) return STRIM_EHIP;
     return STRIM_OK;
   });
@@ -182,38 +228,47 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
                  const int32_t* history_len, int32_t H, int32_t noise_mode, const float* noise,
                  int32_t* out_ids, int32_t* out_status, float* out_probs) {
   if (!ctx || !logits || !params || !out_ids || !dtype_ok(dtype)) return STRIM_EINVAL;
-  if (B <= 0 || B > ctx->max_rows || V <= 0 || V > ctx->max_vocab || row_stride < V)
-    return STRIM_EINVAL;
+  if (B <= 0 || V <= 0 || V > ctx->max_vocab || row_stride < V) return STRIM_EINVAL;
   if (mask_words && mask_stride < ((int64_t)V + 31) / 32) return STRIM_EINVAL;
   if (H < 0 || (H > 0 && !history) || (history && H == 0)) return STRIM_EINVAL;
   if (noise_mode != STRIM_NOISE_ICDF && noise_mode != STRIM_NOISE_GUMBEL) return STRIM_EINVAL;
-  Args a;
-  memset(&a, 0, sizeof(a));
-  a.logits = logits;
-  a.row_stride = row_stride;
-  a.dtype = dtype;
-  a.vec_ok = vec_ok(logits, row_stride, dtype);
-  a.R = B;
-  a.V = V;
-  a.W = (V + CHUNK - 1) / CHUNK;
-  a.B = B;
-  a.k = 0;
-  a.verify = 0;
-  a.xcd_map = (B % 8 == 0) ? 1 : 0;
-  a.params = params;
-  a.mask = mask_words;
-  a.mask_stride = mask_stride;
-  a.hist = history;
-  a.hist_len = history ? history_len : nullptr;
-  a.H = H;
-  a.noise_mode = noise_mode;
-  a.noise = noise;
-  a.noise_stride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
-  a.s = ctx->s;
-  a.out_ids = out_ids;
-  a.out_status = out_status;
-  a.out_probs = out_probs;
-  return on_device(ctx->device, [&]() { return run_chain(ctx, (hipStream_t)stream, a, out_probs != nullptr); });
+  if (strim_check_params(params, B) != STRIM_OK) return STRIM_EINVAL;
+  const int64_t nstride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
+  const int gmax = ctx->max_rows < MAXP ? ctx->max_rows : MAXP;
+  return on_device(ctx->device, [&]() -> int {
+    for (int32_t g0 = 0; g0 < B; g0 += gmax) {
+      const int nb = (B - g0) < gmax ? (B - g0) : gmax;
+      Args a;
+      memset(&a, 0, sizeof(a));
+      a.logits = (const char*)logits + (size_t)g0 * row_stride * dtype_size(dtype);
+      a.row_stride = row_stride;
+      a.dtype = dtype;
+      a.vec_ok = vec_ok(a.logits, row_stride, dtype);
+      a.R = nb;
+      a.V = V;
+      a.W = (V + CHUNK - 1) / CHUNK;
+      a.B = nb;
+      a.k = 0;
+      a.verify = 0;
+      a.xcd_map = (nb % 8 == 0) ? 1 : 0;
+      a.mask = mask_words ? mask_words + (size_t)g0 * mask_stride : nullptr;
+      a.mask_stride = mask_stride;
+      a.hist = history ? history + (size_t)g0 * H : nullptr;
+      a.hist_len = (history && history_len) ? history_len + g0 : nullptr;
+      a.H = H;
+      a.noise_mode = noise_mode;
+      a.noise = noise ? noise + (size_t)g0 * nstride : nullptr;
+      a.noise_stride = nstride;
+      a.s = ctx->s;
+      a.out_ids = out_ids + g0;
+      a.out_status = out_status ? out_status + g0 : nullptr;
+      a.out_probs = out_probs ? out_probs + (size_t)g0 * V : nullptr;
+      for (int i = 0; i < nb; ++i) a.p[i] = params[g0 + i];
+      const int rc = run_group(ctx, (hipStream_t)stream, a, nb, out_probs != nullptr);
+      if (rc != STRIM_OK) return rc;
+    }
+    return STRIM_OK;
+  });
 }
 
 int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_t dtype,
@@ -227,7 +282,7 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
   if (!ctx || !target_logits || !params || !out_accepted || !out_token || !dtype_ok(dtype))
     return STRIM_EINVAL;
   if (B <= 0 || k < 0 || k > 64 || V <= 0 || V > ctx->max_vocab) return STRIM_EINVAL;
-  if ((int64_t)B * (k + 1) > ctx->max_rows) return STRIM_EINVAL;
+  if (k + 1 > ctx->max_rows) return STRIM_EINVAL;
   if (k > 0 && !draft_tokens) return STRIM_EINVAL;
   if (draft_logits) return STRIM_EINVAL;  // general-q drafts: not supported yet
   (void)Vd;
@@ -235,41 +290,110 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
   if (mask_words && mask_stride < ((int64_t)V + 31) / 32) return STRIM_EINVAL;
   if (H < 0 || (H > 0 && !history) || (history && H == 0)) return STRIM_EINVAL;
   if (noise_mode != STRIM_NOISE_ICDF && noise_mode != STRIM_NOISE_GUMBEL) return STRIM_EINVAL;
-  Args a;
-  memset(&a, 0, sizeof(a));
-  a.logits = target_logits;
-  a.row_stride = V;
-  a.dtype = dtype;
-  a.vec_ok = vec_ok(target_logits, V, dtype);
-  a.R = B * (k + 1);
-  a.V = V;
-  a.W = (V + CHUNK - 1) / CHUNK;
-  a.B = B;
-  a.k = k;
-  a.verify = 1;
-  a.xcd_map = (a.R % 8 == 0) ? 1 : 0;
-  a.params = params;
-  a.mask = mask_words;
-  a.mask_stride = mask_stride;
-  a.hist = history;
-  a.hist_len = history ? history_len : nullptr;
-  a.H = H;
-  a.drafts = draft_tokens;
-  a.noise_mode = noise_mode;
-  a.noise = noise;
-  a.noise_stride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
-  a.s = ctx->s;
-  a.out_accepted = out_accepted;
-  a.out_token = out_token;
-  a.out_row_accept = out_row_accept;
-  a.out_row_token = out_row_token;
-  a.out_status = out_status;
+  if (strim_check_params(params, B) != STRIM_OK) return STRIM_EINVAL;
+  const int64_t nstride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
+  int gmax = ctx->max_rows / (k + 1);
+  if (gmax > MAXP) gmax = MAXP;
   return on_device(ctx->device, [&]() -> int {
     hipStream_t st = (hipStream_t)stream;
-    int rc = run_chain(ctx, st, a, false);
-    if (rc != STRIM_OK) return rc;
-    hipLaunchKernelGGL(k_verify_combine, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, st, a);
-    return launch_status();
+    for (int32_t g0 = 0; g0 < B; g0 += gmax) {
+      const int nb = (B - g0) < gmax ? (B - g0) : gmax;
+      const int rows = nb * (k + 1);
+      Args a;
+      memset(&a, 0, sizeof(a));
+      a.logits = (const char*)target_logits + (size_t)g0 * (k + 1) * V * dtype_size(dtype);
+      a.row_stride = V;
+      a.dtype = dtype;
+      a.vec_ok = vec_ok(a.logits, V, dtype);
+      a.R = rows;
+      a.V = V;
+      a.W = (V + CHUNK - 1) / CHUNK;
+      a.B = nb;
+      a.k = k;
+      a.verify = 1;
+      a.xcd_map = (rows % 8 == 0) ? 1 : 0;
+      a.mask = mask_words ? mask_words + (size_t)g0 * (k + 1) * mask_stride : nullptr;
+      a.mask_stride = mask_stride;
+      a.hist = history ? history + (size_t)g0 * H : nullptr;
+      a.hist_len = (history && history_len) ? history_len + g0 : nullptr;
+      a.H = H;
+      a.drafts = draft_tokens ? draft_tokens + (size_t)g0 * k : nullptr;
+      a.noise_mode = noise_mode;
+      a.noise = noise ? noise + (size_t)g0 * (k + 1) * nstride : nullptr;
+      a.noise_stride = nstride;
+      a.s = ctx->s;
+      a.out_accepted = out_accepted + g0;
+      a.out_token = out_token + g0;
+      a.out_row_accept = out_row_accept ? out_row_accept + (size_t)g0 * k : nullptr;
+      a.out_row_token = out_row_token ? out_row_token + (size_t)g0 * (k + 1) : nullptr;
+      a.out_status = out_status ? out_status + g0 : nullptr;
+      for (int i = 0; i < nb; ++i) a.p[i] = params[g0 + i];
+      int rc = run_group(ctx, st, a, nb, false);
+      if (rc != STRIM_OK) return rc;
+      timed(ctx, st, KID_COMBINE, [&] {
+        hipLaunchKernelGGL(k_verify_combine, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, st, a);
+      });
+      rc = launch_status();
+      if (rc != STRIM_OK) return rc;
+    }
+    return STRIM_OK;
+  });
+}
+
+const char* strim_kernel_name(int32_t kernel) {
+  return (kernel >= 0 && kernel < STRIM_KERNEL_COUNT) ? kKernelNames[kernel] : "";
+}
+
+int strim_profile_begin(strim_ctx* ctx, int32_t max_launches) {
+  if (!ctx || max_launches <= 0 || max_launches > (1 << 22)) return STRIM_EINVAL;
+  return on_device(ctx->device, [&]() -> int {
+    profile_free(ctx);
+    ctx->prof_ev = new (std::nothrow) hipEvent_t[2 * (size_t)max_launches];
+    ctx->prof_kind = new (std::nothrow) int32_t[max_launches];
+    if (!ctx->prof_ev || !ctx->prof_kind) {
+      delete[] ctx->prof_ev;
+      delete[] ctx->prof_kind;
+      ctx->prof_ev = nullptr;
+      ctx->prof_kind = nullptr;
+      return STRIM_ENOMEM;
+    }
+    for (int i = 0; i < 2 * max_launches; ++i) {
+      if (hipEventCreate(&ctx->prof_ev[i]) != hipSuccess) {
+        for (int q = 0; q < i; ++q) (void)hipEventDestroy(ctx->prof_ev[q]);
+        delete[] ctx->prof_ev;
+        delete[] ctx->prof_kind;
+        ctx->prof_ev = nullptr;
+        ctx->prof_kind = nullptr;
+        return STRIM_EHIP;
+      }
+    }
+    ctx->prof_cap = max_launches;
+    ctx->prof_n = 0;
+    ctx->prof_on = 1;
+    return STRIM_OK;
+  });
+}
+
+int strim_profile_end(strim_ctx* ctx, double* total_ms, int64_t* launches) {
+  if (!ctx || !total_ms || !launches || !ctx->prof_on) return STRIM_EINVAL;
+  return on_device(ctx->device, [&]() -> int {
+    for (int k = 0; k < STRIM_KERNEL_COUNT; ++k) {
+      total_ms[k] = 0.0;
+      launches[k] = 0;
+    }
+    int rc = STRIM_OK;
+    for (int i = 0; i < ctx->prof_n; ++i) {
+      float ms = 0.0f;
+      if (hipEventSynchronize(ctx->prof_ev[2 * i + 1]) != hipSuccess ||
+          hipEventElapsedTime(&ms, ctx->prof_ev[2 * i], ctx->prof_ev[2 * i + 1]) != hipSuccess) {
+        rc = STRIM_EHIP;
+        break;
+      }
+      total_ms[ctx->prof_kind[i]] += (double)ms;
+      launches[ctx->prof_kind[i]] += 1;
+    }
+    profile_free(ctx);
+    return rc;
   });
 }
 

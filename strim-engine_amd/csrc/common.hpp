@@ -18,9 +18,7 @@ namespace strim {
 constexpr int CHUNK = 4096;    // tokens per workgroup
 constexpr int TPB = 512;       // threads per streaming workgroup (8 waves of 64)
 constexpr int EPT = 8;         // tokens per thread
-constexpr int NBINS = 2048;    // bins over d = m - l: width 1/32 on [0, 64), last = tail
-constexpr float BIN_SCALE = 32.0f;
-constexpr int CAP = 4096;      // candidates per row held by the finalize workgroup
+constexpr int CAP = 8192;      // candidates per row held by the finalize workgroup
 constexpr int FIN_T = 1024;    // finalize workgroup size
 constexpr int FIN_Q = CAP / FIN_T;
 constexpr double FIX_SCALE = 1099511627776.0;  // 2^40 fixed-point mass scale
@@ -28,52 +26,6 @@ constexpr float FIX_SCALE_F = 1099511627776.0f;
 constexpr int WAVE = 64;
 
 static_assert(CHUNK == TPB * EPT, "chunk geometry");
-
-// ---- row status / mode ---------------------------------------------------------
-enum RowMode : int32_t { MODE_NONE = 0, MODE_A = 1, MODE_B = 2 };
-
-// Per (row, chunk) statistics written by k_stats.
-struct ChunkStat {
-  float m;        // max processed logit of the chunk (-inf if none allowed)
-  int32_t arg;    // first id reaching m (greedy rows: over the untempered logits)
-  int32_t n;      // allowed tokens
-  int32_t flags;  // bit0: non-finite logit seen
-};
-
-// Per-chunk best two surely-kept tokens by the fp32 Gumbel proxy l + g.
-struct ChunkTop {
-  float l0;
-  int32_t id0;
-  float l1;
-  int32_t id1;
-};
-
-struct Cand {
-  float l;
-  int32_t id;
-};
-
-// Per-row state shared by the kernels of one call.
-struct RowState {
-  float m;            // max processed logit
-  int32_t status;     // STRIM_OK or STRIM_E*
-  int32_t n_allowed;
-  int32_t argmax;     // greedy result
-  int32_t greedy;
-  int32_t mode;       // RowMode
-  int32_t s;          // bins < s (and not collected) are surely kept
-  int32_t e;          // bins > e (and not collected) are surely dropped
-  int32_t s1;         // bins < s1 surely pass min-p and top-k
-  int32_t rng[3][2];  // collected bin ranges [lo, hi] (lo > hi = empty)
-  int32_t draft;      // verify: draft token of this row or -1
-  float l_draft;      // verify: processed logit of the draft (-inf if not allowed)
-  int32_t pad0;
-  double q_draft;     // verify: q(draft)
-  double sum_kept;    // finalize: kept mass (relative to exp(m))
-  uint64_t last_key;  // finalize: ckey of the last kept collected token in [s, e] (0 = none)
-  int32_t token;      // finalize: row outcome token
-  int32_t accept;     // verify: accept flag
-};
 
 // ---- scalar helpers --------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
@@ -95,11 +47,6 @@ __device__ __forceinline__ float fkey_desc_inv(uint32_t k) {
 // Ascending order = (l descending, id ascending): the token order of every decision.
 __device__ __forceinline__ uint64_t ckey(float l, int32_t id) {
   return ((uint64_t)fkey_desc(l) << 32) | (uint32_t)id;
-}
-
-// Bin of d = m - l (d >= 0). Monotone in l, equal l share a bin.
-__device__ __forceinline__ int dbin(float d) {
-  return d < 64.0f ? (int)(d * BIN_SCALE) : (NBINS - 1);
 }
 
 // ---- random numbers ----------------------------------------------------------------
@@ -146,70 +93,133 @@ __device__ __forceinline__ float gumbel32(float u) {
   return -logf(-logf(uu));
 }
 
-// ---- wave / block reductions (wave64) ---------------------------------------------
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-  return v;
+// ---- wave64 primitives on DPP ---------------------------------------------------------
+// Cross-lane steps use DPP (quad_perm / row_half_mirror / row_mirror / row_shr) and
+// v_readlane, never ds_bpermute: a DPP move costs a VALU slot, not an LDS round trip.
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7 - i within 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15 - i within 16
+constexpr int DPP_SHR1 = 0x111, DPP_SHR2 = 0x112, DPP_SHR4 = 0x114, DPP_SHR8 = 0x118;
+
+template <int C>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, C, 0xF, 0xF, false);
 }
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
-    v += ((uint64_t)hi << 32) | lo;
-  }
-  return v;
+template <int C>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<C>(__float_as_int(v)));
 }
-__device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, WAVE));
-  return v;
+template <int C>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)dpp_i<C>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)dpp_i<C>((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, WAVE));
-  return v;
+template <int C>
+__device__ __forceinline__ double dpp_d(double v) {
+  return __longlong_as_double((long long)dpp_u64<C>((uint64_t)__double_as_longlong(v)));
 }
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
-    uint64_t w = ((uint64_t)hi << 32) | lo;
-    v = w > v ? w : v;
-  }
-  return v;
+__device__ __forceinline__ int rl_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+__device__ __forceinline__ float rl_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
-// Inclusive scan over the wave (Hillis-Steele, fixed order => deterministic).
-template <typename T>
-__device__ __forceinline__ T wave_incl_scan(T v) {
-  const int lane = threadIdx.x & (WAVE - 1);
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    T w = __shfl_up(v, o, WAVE);
-    if (lane >= o) v += w;
-  }
-  return v;
+__device__ __forceinline__ uint64_t rl_u64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
-  const int lane = threadIdx.x & (WAVE - 1);
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    uint32_t lo = __shfl_up((uint32_t)v, o, WAVE);
-    uint32_t hi = __shfl_up((uint32_t)(v >> 32), o, WAVE);
-    if (lane >= o) v += ((uint64_t)hi << 32) | lo;
-  }
-  return v;
+__device__ __forceinline__ double rl_d(double v, int lane) {
+  return __longlong_as_double((long long)rl_u64((uint64_t)__double_as_longlong(v), lane));
 }
 
-// (value, id) argmax: larger value wins, equal values -> smaller id.
+// Reduce within each 16-lane row (every lane ends with its row's value), then combine
+// the four rows through readlane: the result is wave-uniform. `op` is associative and
+// commutative; the fixed pattern keeps floating-point sums deterministic.
+#define STRIM_WAVE_REDUCE(T, v, DPP, RL, OP)              \
+  do {                                                    \
+    v = OP(v, DPP<DPP_XOR1>(v));                          \
+    v = OP(v, DPP<DPP_XOR2>(v));                          \
+    v = OP(v, DPP<DPP_HALF_MIRROR>(v));                   \
+    v = OP(v, DPP<DPP_MIRROR>(v));                        \
+    const T r0 = RL(v, 0), r1 = RL(v, 16), r2 = RL(v, 32), r3 = RL(v, 48); \
+    v = OP(OP(r0, r1), OP(r2, r3));                       \
+  } while (0)
+
+__device__ __forceinline__ int op_add_i(int a, int b) { return a + b; }
+__device__ __forceinline__ int op_min_i(int a, int b) { return a < b ? a : b; }
+__device__ __forceinline__ int op_max_i(int a, int b) { return a > b ? a : b; }
+__device__ __forceinline__ int op_or_i(int a, int b) { return a | b; }
+__device__ __forceinline__ double op_add_d(double a, double b) { return a + b; }
+__device__ __forceinline__ uint64_t op_add_u64(uint64_t a, uint64_t b) { return a + b; }
+
+__device__ __forceinline__ int wave_sum(int v) { STRIM_WAVE_REDUCE(int, v, dpp_i, rl_i, op_add_i); return v; }
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) { return (uint32_t)wave_sum((int)v); }
+__device__ __forceinline__ int wave_min_i(int v) { STRIM_WAVE_REDUCE(int, v, dpp_i, rl_i, op_min_i); return v; }
+__device__ __forceinline__ int wave_max_i(int v) { STRIM_WAVE_REDUCE(int, v, dpp_i, rl_i, op_max_i); return v; }
+__device__ __forceinline__ int wave_or_i(int v) { STRIM_WAVE_REDUCE(int, v, dpp_i, rl_i, op_or_i); return v; }
+__device__ __forceinline__ double wave_sum(double v) { STRIM_WAVE_REDUCE(double, v, dpp_d, rl_d, op_add_d); return v; }
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) { STRIM_WAVE_REDUCE(uint64_t, v, dpp_u64, rl_u64, op_add_u64); return v; }
+
+// (value, id) argmax: larger value wins, equal values -> smaller id; id < 0 is empty.
 __device__ __forceinline__ void argmax_merge(float& v, int& id, float v2, int id2) {
   if (id2 >= 0 && (id < 0 || v2 > v || (v2 == v && id2 < id))) {
     v = v2;
     id = id2;
   }
+}
+template <int C>
+__device__ __forceinline__ void argmax_dpp_step(float& v, int& id) {
+  const float v2 = dpp_f<C>(v);
+  const int i2 = dpp_i<C>(id);
+  argmax_merge(v, id, v2, i2);
+}
+// Wave-uniform argmax of (v, id).
+__device__ __forceinline__ void wave_argmax(float& v, int& id) {
+  argmax_dpp_step<DPP_XOR1>(v, id);
+  argmax_dpp_step<DPP_XOR2>(v, id);
+  argmax_dpp_step<DPP_HALF_MIRROR>(v, id);
+  argmax_dpp_step<DPP_MIRROR>(v, id);
+  float bv = rl_f(v, 0);
+  int bi = rl_i(id, 0);
+  argmax_merge(bv, bi, rl_f(v, 16), rl_i(id, 16));
+  argmax_merge(bv, bi, rl_f(v, 32), rl_i(id, 32));
+  argmax_merge(bv, bi, rl_f(v, 48), rl_i(id, 48));
+  v = bv;
+  id = bi;
+}
+
+// Lanes below this one whose bit is set in `mask`.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+// Exclusive prefix and wave total of small per-lane counts (0..15) via ballots.
+__device__ __forceinline__ int wave_excl_count(int c, int* total) {
+  int ex = 0, tot = 0;
+#pragma unroll
+  for (int bit = 0; bit < 4; ++bit) {
+    const uint64_t m = __ballot((c >> bit) & 1);
+    ex += lanes_below(m) << bit;
+    tot += __popcll(m) << bit;
+  }
+  *total = tot;
+  return ex;
+}
+
+// Inclusive scan of doubles over the wave in a fixed order (deterministic): row_shr
+// steps within 16-lane rows, then the row totals through readlane.
+__device__ __forceinline__ double wave_incl_scan(double v) {
+  v += dpp_d<DPP_SHR1>(v);
+  v += dpp_d<DPP_SHR2>(v);
+  v += dpp_d<DPP_SHR4>(v);
+  v += dpp_d<DPP_SHR8>(v);
+  const double t0 = rl_d(v, 15), t1 = rl_d(v, 31), t2 = rl_d(v, 47);
+  const int row = (threadIdx.x & (WAVE - 1)) >> 4;
+  if (row >= 1) v += t0;
+  if (row >= 2) v += t1;
+  if (row >= 3) v += t2;
+  return v;
 }
 
 // Block-wide exclusive scan of one double per thread, fixed order (deterministic).
@@ -217,13 +227,13 @@ __device__ __forceinline__ void argmax_merge(float& v, int& id, float v2, int id
 template <int NT>
 __device__ __forceinline__ double block_excl_scan_f64(double v, double* scratch, double* total) {
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-  double inc = wave_incl_scan(v);
+  const double inc = wave_incl_scan(v);
   if (lane == WAVE - 1) scratch[w] = inc;
   __syncthreads();
   double base = 0.0, tot = 0.0;
 #pragma unroll
   for (int i = 0; i < NT / WAVE; ++i) {
-    double s = scratch[i];
+    const double s = scratch[i];
     if (i < w) base += s;
     tot += s;
   }
@@ -231,23 +241,18 @@ __device__ __forceinline__ double block_excl_scan_f64(double v, double* scratch,
   *total = tot;
   return base + inc - v;
 }
+
+// Block-wide min of one int per thread; every thread gets the result.
 template <int NT>
-__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t* scratch,
-                                                        uint64_t* total) {
-  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-  uint64_t inc = wave_incl_scan_u64(v);
-  if (lane == WAVE - 1) scratch[w] = inc;
+__device__ __forceinline__ int block_min(int v, int* scratch) {
+  v = wave_min_i(v);
+  if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x / WAVE] = v;
   __syncthreads();
-  uint64_t base = 0, tot = 0;
+  int b = scratch[0];
 #pragma unroll
-  for (int i = 0; i < NT / WAVE; ++i) {
-    uint64_t s = scratch[i];
-    if (i < w) base += s;
-    tot += s;
-  }
+  for (int q = 1; q < NT / WAVE; ++q) b = min(b, scratch[q]);
   __syncthreads();
-  *total = tot;
-  return base + inc - v;
+  return b;
 }
 
 }  // namespace strim

@@ -1,21 +1,91 @@
-// kernels.hpp — argument block and per-row processing shared by the gfx950 kernels.
+// kernels.hpp — argument block, scratch layout and per-row processing shared by the
+// gfx950 kernels.
+//
+// One call runs up to three kernels over R rows of V logits:
+//   k_scan    (rows x chunks)  single streaming pass: processed logits, chunk statistics,
+//                              and either the chunk's local candidates (fast rows) or a
+//                              64-bin coarse mass histogram (general rows);
+//   k_collect (rows x chunks)  general rows only: second pass that collects the tokens the
+//                              coarse bounds cannot resolve and sums the rest exactly;
+//   k_final   (one workgroup per row) exact decisions in fp64 over the sorted candidates.
+// Workgroups never wait for or fence against each other: every partial result is a
+// plain store into a per-(row, chunk) slot that the next kernel reads.
 #pragma once
 
 #include "common.hpp"
 
 namespace strim {
 
+constexpr int MAXP = 64;         // parameter rows carried inline per launch group
+constexpr int SLOT = 128;        // fast-path candidates per chunk
+constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
+constexpr float CB_SCALE = 2.0f;
+constexpr int NGB = 129;         // global coarse bins: width 1/2 over [0, 64) + tail
+constexpr int KLOC = 256;        // largest top-k served by local candidates
+constexpr float MINP_FAST = 3.3546262e-4f;  // e^-8: min-p at or above bounds candidates
+constexpr int NSEG = 8;          // non-collected intervals summarised per chunk
+
+enum RowClass : int32_t { CLS_GREEDY = 0, CLS_FAST = 1, CLS_GENERAL = 2, CLS_INVALID = 3 };
+
+// How a row's candidates are resolved (set by k_collect for general rows).
+enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
+
+struct ChunkStat {
+  float m;         // chunk max of processed logits (-inf if none allowed)
+  int32_t arg;     // first id reaching m
+  int32_t n;       // allowed tokens
+  int32_t flags;   // bit0: non-finite logit
+  double S;        // sum exp(l - m) over the chunk (general rows)
+  uint32_t nslot;  // fast rows: local candidates written (SLOT + 1 = overflow)
+  int32_t pad;
+};
+
+// General-path per-chunk summary of the tokens k_collect did not collect: fixed-point
+// mass and count per non-collected interval, and the two best surely-kept tokens by the
+// fp32 Gumbel proxy.
+struct ChunkPart {
+  unsigned long long mass[NSEG];
+  uint32_t cnt[NSEG];
+  float l0, l1;
+  int32_t id0, id1;
+};
+
+struct Cand {
+  float l;
+  int32_t id;
+};
+
+// Bounds of a general row, in global coarse bins gd = floor(2 * (m - l)) (tail = 128).
+struct Bounds {
+  int32_t mode;
+  int32_t s, e;      // gd < s surely kept; gd > e (and not collected) surely dropped
+  int32_t s1, e1;    // gd < s1 surely pre-kept (min-p, top-k); gd > e1 surely not
+  int32_t rng[3][2]; // collected ranges
+  int32_t seg_lo[NSEG], seg_hi[NSEG];  // non-collected intervals (lo > hi = empty)
+};
+
+struct RowState {
+  float l_draft;   // verify: processed logit of the row's draft (-inf if masked)
+  int32_t status;
+  int32_t token;
+  int32_t accept;
+  double sum_kept;
+  float m;
+  int32_t pad;
+  uint64_t last_key;  // last kept token's order key (0 = none kept beyond bin rules)
+  Bounds bd;          // general rows (k_collect)
+};
+
 // Device scratch owned by a context (allocated once in strim_ctx_create).
 struct Scratch {
-  ChunkStat* cstat;     // [rows][wmax]
-  RowState* rs;         // [rows]
-  uint32_t* cnt_stats;  // [rows] last-block counters, kept at zero between calls
-  uint32_t* cnt_hist;   // [rows]
-  uint32_t* hcnt;       // [rows][NBINS]
-  unsigned long long* hmass;  // [rows][NBINS] fixed-point 2^40
-  Cand* cand;           // [rows][CAP]
-  uint32_t* ncand;      // [rows]
-  ChunkTop* ctop;       // [rows][wmax]
+  ChunkStat* cstat;               // [rows][wmax]
+  Cand* slot;                     // [rows][wmax][SLOT]
+  uint32_t* chc;                  // [rows][wmax][NCB] coarse counts
+  unsigned long long* chm;        // [rows][wmax][NCB] coarse fixed-point masses
+  ChunkPart* part;                // [rows][wmax]
+  RowState* rs;                   // [rows]
+  Cand* cand;                     // [rows][CAP]
+  uint32_t* ncand;                // [rows]
   int32_t wmax;
 };
 
@@ -24,18 +94,17 @@ struct Args {
   const void* logits;
   int64_t row_stride;
   int32_t dtype;
-  int32_t vec_ok;  // 16-byte vector loads are aligned for every row
-  int32_t R, V, W; // rows, vocab, chunks per row
-  int32_t B, k;    // batch and draft length (k = 0 for strim_sample)
+  int32_t vec_ok;
+  int32_t R, V, W;   // rows in this group, vocab, chunks per row
+  int32_t B, k;      // batch rows in this group and draft length (k = 0: sample)
   int32_t verify;
   int32_t xcd_map;
-  const strim_sampling_params* params;
   const uint32_t* mask;
   int64_t mask_stride;
   const int32_t* hist;
   const int32_t* hist_len;
   int32_t H;
-  const int32_t* drafts;  // [B][k]
+  const int32_t* drafts;  // [B][k] (group-relative)
   int32_t noise_mode;
   const float* noise;
   int64_t noise_stride;
@@ -43,21 +112,30 @@ struct Args {
   int32_t* out_ids;
   int32_t* out_status;
   float* out_probs;
-  // verify outputs
   int32_t* out_accepted;
   int32_t* out_token;
   int32_t* out_row_accept;
   int32_t* out_row_token;
+  strim_sampling_params p[MAXP];  // per batch row of the group
 };
 
-// Row parameters in registers.
 struct RowParams {
   float T, rep, pres, freq, min_p, top_p;
   int32_t top_k;
   uint32_t flags;
   uint64_t seed, position;
-  bool greedy, pen, valid;
+  bool greedy, pen;
+  int32_t cls;
 };
+
+// Classification shared by host and device: which path resolves the row.
+__host__ __device__ inline int32_t row_class(const strim_sampling_params& p, int32_t V) {
+  if (!(p.temperature > 0.0f)) return CLS_GREEDY;
+  const bool topk = p.top_k > 0 && p.top_k < V;
+  if (topk && p.top_k <= KLOC) return CLS_FAST;
+  if (p.min_p >= MINP_FAST) return CLS_FAST;
+  return CLS_GENERAL;
+}
 
 __device__ __forceinline__ void row_bj(const Args& a, int r, int& b, int& j) {
   if (a.verify) {
@@ -70,7 +148,7 @@ __device__ __forceinline__ void row_bj(const Args& a, int r, int& b, int& j) {
 }
 
 // Workgroup -> (row, chunk). With rows a multiple of 8, row r's chunks all run on
-// XCD r % 8 (hardware dispatches workgroup i to XCD i % 8).
+// XCD r % 8 (workgroup i is dispatched to XCD i % 8), so re-reads stay in one L2.
 __device__ __forceinline__ void map_block(const Args& a, int bid, int& r, int& c) {
   if (a.xcd_map) {
     int x = bid & 7, slot = bid >> 3;
@@ -82,18 +160,8 @@ __device__ __forceinline__ void map_block(const Args& a, int bid, int& r, int& c
   }
 }
 
-__device__ __forceinline__ bool params_valid(const strim_sampling_params& p) {
-  if (!isfinite(p.temperature)) return false;
-  if (!(p.top_p > 0.0f && p.top_p <= 1.0f)) return false;
-  if (p.top_k < 0) return false;
-  if (!(p.min_p >= 0.0f && p.min_p <= 1.0f)) return false;
-  if (!(p.repetition_penalty > 0.0f) || isinf(p.repetition_penalty)) return false;
-  if (!isfinite(p.presence_penalty) || !isfinite(p.frequency_penalty)) return false;
-  return true;
-}
-
 __device__ __forceinline__ RowParams load_params(const Args& a, int b, int j) {
-  const strim_sampling_params& sp = a.params[b];
+  const strim_sampling_params& sp = a.p[b];
   RowParams p;
   p.T = sp.temperature;
   p.rep = sp.repetition_penalty;
@@ -102,15 +170,45 @@ __device__ __forceinline__ RowParams load_params(const Args& a, int b, int j) {
   p.min_p = sp.min_p;
   p.top_p = sp.top_p;
   p.top_k = sp.top_k;
-  p.flags = sp.flags;
-  if (a.verify) p.flags &= STRIM_FLAG_TOPK_KEEP_TIES;  // verify is the SpecSampling path
+  p.flags = a.verify ? (sp.flags & STRIM_FLAG_TOPK_KEEP_TIES) : sp.flags;
   p.seed = sp.seed;
   p.position = sp.position + (uint64_t)j;
-  p.valid = params_valid(sp);
   p.greedy = !(p.T > 0.0f);
   const bool active = p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f;
   p.pen = active && (a.hist != nullptr || (a.verify && j > 0));
+  p.cls = row_class(sp, a.V);
   return p;
+}
+
+// Raw logits of this thread's EPT tokens (issued before anything waits on memory).
+__device__ __forceinline__ void load_tokens(const Args& a, int r, int i0, float (&x)[EPT]) {
+  const int64_t base = (int64_t)r * a.row_stride;
+  if (a.dtype == STRIM_DTYPE_BF16) {
+    const uint16_t* xb = (const uint16_t*)a.logits + base;
+    if (a.vec_ok && i0 + EPT <= a.V) {
+      const uint4 v = *(const uint4*)(xb + i0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = __uint_as_float(w[e] << 16);
+        x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? bf16_to_f32(xb[i0 + e]) : 0.0f;
+    }
+  } else {
+    const float* xf = (const float*)a.logits + base;
+    if (a.vec_ok && i0 + EPT <= a.V) {
+      const float4 v0 = *(const float4*)(xf + i0);
+      const float4 v1 = *(const float4*)(xf + i0 + 4);
+      x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+      x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? xf[i0 + e] : 0.0f;
+    }
+  }
 }
 
 // History counts of the chunk [c0, c0 + CHUNK) in LDS (plus the verify draft prefix).
@@ -124,64 +222,35 @@ __device__ __forceinline__ void build_counts(const Args& a, int b, int j, int c0
     hl = hl < 0 ? 0 : (hl > a.H ? a.H : hl);
     const int32_t* h = a.hist + (int64_t)b * a.H;
     for (int i = threadIdx.x; i < hl; i += TPB) {
-      int id = h[i];
-      unsigned o = (unsigned)(id - c0);
+      const int id = h[i];
+      const unsigned o = (unsigned)(id - c0);
       if (o < (unsigned)CHUNK && id < a.V) atomicAdd(&s_cnt[o], 1u);
     }
   }
   if (a.verify && (int)threadIdx.x < j) {
-    int id = a.drafts[(int64_t)b * a.k + threadIdx.x];
-    unsigned o = (unsigned)(id - c0);
+    const int id = a.drafts[(int64_t)b * a.k + threadIdx.x];
+    const unsigned o = (unsigned)(id - c0);
     if (o < (unsigned)CHUNK && id < a.V) atomicAdd(&s_cnt[o], 1u);
   }
   __syncthreads();
 }
 
-// Processed logits of this thread's EPT tokens: penalties -> mask -> temperature.
-// Masked and out-of-range tokens get -inf. Greedy rows skip the temperature.
-// Each step is one IEEE float32 operation (the file is built with -ffp-contract=off).
-__device__ __forceinline__ void process_tokens(const Args& a, int r, int c0, const RowParams& p,
-                                               const uint32_t* s_cnt, float (&l)[EPT],
-                                               bool& nonfinite) {
-  const int i0 = c0 + (int)threadIdx.x * EPT;
-  float x[EPT];
-  const int64_t base = (int64_t)r * a.row_stride;
-  if (a.dtype == STRIM_DTYPE_BF16) {
-    const uint16_t* xb = (const uint16_t*)a.logits + base;
-    if (a.vec_ok && i0 + EPT <= a.V) {
-      uint4 v = *(const uint4*)(xb + i0);
-      uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[2 * e] = __uint_as_float(w[e] << 16);
-        x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? bf16_to_f32(xb[i0 + e]) : 0.0f;
-    }
-  } else {
-    const float* xf = (const float*)a.logits + base;
-    if (a.vec_ok && i0 + EPT <= a.V) {
-      float4 v0 = *(const float4*)(xf + i0);
-      float4 v1 = *(const float4*)(xf + i0 + 4);
-      x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
-      x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? xf[i0 + e] : 0.0f;
-    }
-  }
+// Penalties -> mask -> temperature on raw values x. Masked / out-of-range tokens get
+// -inf. Greedy rows skip the temperature. Each step is one IEEE float32 operation (the
+// library is built with -ffp-contract=off).
+__device__ __forceinline__ void process_tokens(const Args& a, int r, int i0, const RowParams& p,
+                                               const uint32_t* s_cnt, const float (&x)[EPT],
+                                               float (&l)[EPT], bool& nonfinite) {
   uint32_t bits = 0xFFu;
   if (a.mask && i0 < a.V) {
-    uint32_t wd = a.mask[(int64_t)r * a.mask_stride + (i0 >> 5)];
+    const uint32_t wd = a.mask[(int64_t)r * a.mask_stride + (i0 >> 5)];
     bits = (wd >> (i0 & 31)) & 0xFFu;
   }
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     float v = x[e];
     if (p.pen) {
-      uint32_t cnt = s_cnt[threadIdx.x * EPT + e];
+      const uint32_t cnt = s_cnt[(i0 & (CHUNK - 1)) + e];
       if (cnt > 0u) {
         v = v > 0.0f ? v / p.rep : v * p.rep;
         v = v - p.freq * (float)cnt;
@@ -194,10 +263,32 @@ __device__ __forceinline__ void process_tokens(const Args& a, int r, int c0, con
       continue;
     }
     if (isnan(v) || v == INFINITY) nonfinite = true;
-    float lv = p.greedy ? v : v / p.T;
+    const float lv = p.greedy ? v : v / p.T;
     if (lv == INFINITY) nonfinite = true;
     l[e] = lv;
   }
+}
+
+// Global coarse bin of d = m - l (monotone in l; equal l share a bin).
+__device__ __forceinline__ int gbin(float d) { return d < 64.0f ? (int)(d * CB_SCALE) : NGB - 1; }
+
+__device__ __forceinline__ bool in_rng(const Bounds& bd, int g) {
+  return (g >= bd.rng[0][0] && g <= bd.rng[0][1]) || (g >= bd.rng[1][0] && g <= bd.rng[1][1]) ||
+         (g >= bd.rng[2][0] && g <= bd.rng[2][1]);
+}
+__device__ __forceinline__ int seg_of(const Bounds& bd, int g) {
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+    if (g >= bd.seg_lo[q] && g <= bd.seg_hi[q]) return q;
+  return -1;
+}
+
+// Uniform element `idx` of row r's noise vector: injected, or Philox at the row's
+// (seed, position) key.
+__device__ __forceinline__ float row_uniform(const Args& a, int r, const RowParams& p,
+                                             int64_t idx) {
+  if (a.noise) return a.noise[(int64_t)r * a.noise_stride + idx];
+  return philox_uniform(mix64(p.seed, p.position), (uint64_t)idx);
 }
 
 }  // namespace strim

@@ -1,58 +1,124 @@
-// sample_kernels.hip — the four passes of one token-selection call on gfx950.
+// sample_kernels.hip — the gfx950 token-selection kernels.
 //
-//   k_stats   (rows x chunks) processed logits -> chunk max / argmax / allowed count;
-//             the row's last workgroup merges them (row max m, greedy result, status).
-//   k_hist    (rows x chunks) histogram of d = m - l over NBINS bins: counts and
-//             fixed-point masses exp(-d) * 2^40, merged with integer atomics (exact,
-//             order-independent). The last workgroup turns the histogram into bin-level
-//             bounds for min-p / top-k / top-p / the icdf draw, and picks the bins whose
-//             tokens must be resolved exactly.
-//   k_collect (rows x chunks) appends the tokens of those bins to the row's candidate
-//             buffer and keeps, per chunk, the two best surely-kept tokens by the fp32
-//             Gumbel proxy (used when the kept set is too large to collect).
-//   k_final   (one 1024-thread workgroup per row) sorts the candidates in LDS by
-//             (l desc, id asc) and resolves every decision in fp64, then draws.
-// No pass waits on another workgroup: the merges use the last-arriving workgroup.
+// Fast rows (greedy, min-p >= e^-8, or 0 < top-k <= 256) are resolved by one streaming
+// pass (k_scan) and one finalize (k_final): each chunk keeps its local candidates —
+// every token that could survive min-p/top-k given only the chunk's own maximum — and
+// the finalize resolves them exactly. General rows (top-p alone, no filter, very small
+// min-p, large top-k) add k_collect: from k_scan's 64-bin coarse histograms it derives
+// conservative bin bounds, collects the tokens of the undecided bins and sums the rest
+// exactly. k_final sorts the candidates in LDS by (l desc, id asc) and takes every
+// decision in fp64.
 #include "kernels.hpp"
 
 namespace strim {
 
 // ---------------------------------------------------------------------------------
-// k_stats
+// shared helpers
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(TPB) void k_stats(Args a) {
+// Ladder rung of d >= 0: 0 for d == 0, else ceil(2 log2 d) + 13 clamped to [1, 31].
+// Monotone in d (equal d -> equal rung); used only to bound a chunk's top-k.
+__device__ __forceinline__ int ladder_rung(float d) {
+  if (!(d > 0.0f)) return 0;
+  if (!(d < 1e30f)) return 31;
+  const int r = (int)ceilf(2.0f * __log2f(d)) + 13;
+  return r < 1 ? 1 : (r > 31 ? 31 : r);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Merge (t0, t1) into the pair (s0 >= s1) of fp32 proxy scores; ids break ties.
+__device__ __forceinline__ void top2_merge(float& s0, float& l0, int& i0, float& s1, float& l1,
+                                           int& i1, float t0, float tl0, int ti0, float t1,
+                                           float tl1, int ti1) {
+  auto better = [](float a, int ia, float b, int ib) {
+    return ia >= 0 && (ib < 0 || a > b || (a == b && ia < ib));
+  };
+  float cs[4] = {s0, s1, t0, t1}, cl[4] = {l0, l1, tl0, tl1};
+  int ci[4] = {i0, i1, ti0, ti1};
+  int bi = 0;
+#pragma unroll
+  for (int q = 1; q < 4; ++q)
+    if (better(cs[q], ci[q], cs[bi], ci[bi])) bi = q;
+  int si = bi == 0 ? 1 : 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (q != bi && better(cs[q], ci[q], cs[si], ci[si])) si = q;
+  float ns0 = -INFINITY, nl0 = 0.f, ns1 = -INFINITY, nl1 = 0.f;
+  int ni0 = -1, ni1 = -1;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (q == bi) { ns0 = cs[q]; nl0 = cl[q]; ni0 = ci[q]; }
+    if (q == si) { ns1 = cs[q]; nl1 = cl[q]; ni1 = ci[q]; }
+  }
+  s0 = ns0; l0 = nl0; i0 = ni0;
+  s1 = ns1; l1 = nl1; i1 = ni1;
+}
+
+// Wave-then-block reduction of the two best (score, l, id); result in thread 0.
+template <int NT>
+__device__ __forceinline__ void block_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
+                                           int& i1, float* sf, int* si) {
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ts0 = __shfl_xor(s0, o, WAVE), tl0 = __shfl_xor(l0, o, WAVE);
+    const float ts1 = __shfl_xor(s1, o, WAVE), tl1 = __shfl_xor(l1, o, WAVE);
+    const int ti0 = __shfl_xor(i0, o, WAVE), ti1 = __shfl_xor(i1, o, WAVE);
+    top2_merge(s0, l0, i0, s1, l1, i1, ts0, tl0, ti0, ts1, tl1, ti1);
+  }
+  if (lane == 0) {
+    sf[4 * w + 0] = s0; sf[4 * w + 1] = l0; sf[4 * w + 2] = s1; sf[4 * w + 3] = l1;
+    si[2 * w + 0] = i0; si[2 * w + 1] = i1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int q = 1; q < NT / WAVE; ++q)
+      top2_merge(s0, l0, i0, s1, l1, i1, sf[4 * q], sf[4 * q + 1], si[2 * q], sf[4 * q + 2],
+                 sf[4 * q + 3], si[2 * q + 1]);
+}
+
+__device__ __forceinline__ bool row_nofilter(const RowParams& p, int V) {
+  return !(p.top_k > 0 && p.top_k < V) && !(p.min_p > 0.0f) && !(p.top_p < 1.0f);
+}
+
+// ---------------------------------------------------------------------------------
+// k_scan: the single streaming pass
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(TPB) void k_scan(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
+  __shared__ uint32_t s_hc[NCB];
+  __shared__ unsigned long long s_hm[NCB];
+  __shared__ uint32_t s_lad[32];
   __shared__ float s_v[TPB / WAVE];
-  __shared__ int s_i[TPB / WAVE];
-  __shared__ int s_n[TPB / WAVE];
-  __shared__ int s_f[TPB / WAVE];
-  __shared__ int s_last;
+  __shared__ int s_i[TPB / WAVE], s_n[TPB / WAVE], s_f[TPB / WAVE];
+  __shared__ double s_d[TPB / WAVE];
+  __shared__ int s_off[TPB / WAVE];
+  __shared__ float s_tf[4 * TPB / WAVE];
+  __shared__ int s_ti[2 * TPB / WAVE];
 
   int r, c;
   map_block(a, blockIdx.x, r, c);
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);
-  const int c0 = c * CHUNK;
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int c0 = c * CHUNK, i0 = c0 + t * EPT;
+  const bool topk_lad = p.cls == CLS_FAST && p.top_k > 0 && p.top_k < a.V;
 
-  if (p.valid && p.pen) build_counts(a, b, j, c0, s_cnt);
+  float x[EPT];
+  load_tokens(a, r, i0, x);
+  if (p.pen) build_counts(a, b, j, c0, s_cnt);
   float l[EPT];
   bool nf = false;
-  process_tokens(a, r, c0, p, s_cnt, l, nf);
+  process_tokens(a, r, i0, p, s_cnt, x, l, nf);
 
-  float mv = -INFINITY;
-  int mi = -1, n = 0;
-#pragma unroll
-  for (int e = 0; e < EPT; ++e)
-    if (l[e] > -INFINITY) {
-      ++n;
-      argmax_merge(mv, mi, l[e], c0 + t * EPT + e);
-    }
-  // verify: the draft token's processed logit
   if (a.verify && j < a.k) {
     const int d = a.drafts[(int64_t)b * a.k + j];
-    const int o = d - (c0 + t * EPT);
+    const int o = d - i0;
     if (o >= 0 && o < EPT) {
       float ld = -INFINITY;
 #pragma unroll
@@ -61,474 +127,464 @@ __global__ __launch_bounds__(TPB) void k_stats(Args a) {
       a.s.rs[r].l_draft = ld;
     }
   }
+  if (c == 0 && t == 0) a.s.ncand[r] = 0u;
+
+  // chunk max (first id on ties), allowed count, non-finite flag
+  float mv = -INFINITY;
+  int mi = -1, n = 0;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float v2 = __shfl_xor(mv, o, WAVE);
-    int i2 = __shfl_xor(mi, o, WAVE);
-    argmax_merge(mv, mi, v2, i2);
-  }
+  for (int e = 0; e < EPT; ++e)
+    if (l[e] > -INFINITY) {
+      ++n;
+      argmax_merge(mv, mi, l[e], i0 + e);
+    }
+  wave_argmax(mv, mi);
   n = wave_sum(n);
-  int f = __any(nf) ? 1 : 0;
+  const int f = __any(nf) ? 1 : 0;
+  if (topk_lad) s_lad[t & 31] = 0u;  // cleared before the barrier below
   if (lane == 0) {
     s_v[w] = mv;
     s_i[w] = mi;
     s_n[w] = n;
     s_f[w] = f;
   }
-  // zero this chunk's slice of the row histogram for k_hist
-  {
-    const int slice = (NBINS + a.W - 1) / a.W;
-    const int lo = c * slice, hi = min(NBINS, lo + slice);
-    for (int i = lo + t; i < hi; i += TPB) {
-      a.s.hcnt[(int64_t)r * NBINS + i] = 0u;
-      a.s.hmass[(int64_t)r * NBINS + i] = 0ull;
-    }
-  }
   __syncthreads();
-  if (t == 0) {
-    float bv = s_v[0];
-    int bi = s_i[0], bn = s_n[0], bf = s_f[0];
-    for (int i = 1; i < TPB / WAVE; ++i) {
-      argmax_merge(bv, bi, s_v[i], s_i[i]);
-      bn += s_n[i];
-      bf |= s_f[i];
-    }
-    a.s.cstat[(int64_t)r * a.s.wmax + c] = ChunkStat{bv, bi, bn, bf};
-    __threadfence();
-    unsigned prev = atomicAdd(&a.s.cnt_stats[r], 1u);
-    s_last = (prev == (unsigned)(a.W - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // ---- last workgroup of row r: merge the chunk statistics -----------------------
-  float bv = -INFINITY;
-  int bi = -1, bn = 0, bf = 0;
-  for (int cc = t; cc < a.W; cc += TPB) {
-    ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + cc];
-    argmax_merge(bv, bi, cs.m, cs.arg);
-    bn += cs.n;
-    bf |= cs.flags;
-  }
+  float m_w = s_v[0];
+  int a_w = s_i[0], n_w = s_n[0], f_w = s_f[0];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float v2 = __shfl_xor(bv, o, WAVE);
-    int i2 = __shfl_xor(bi, o, WAVE);
-    argmax_merge(bv, bi, v2, i2);
-    bn += __shfl_xor(bn, o, WAVE);
-    bf |= __shfl_xor(bf, o, WAVE);
+  for (int q = 1; q < TPB / WAVE; ++q) {
+    argmax_merge(m_w, a_w, s_v[q], s_i[q]);
+    n_w += s_n[q];
+    f_w |= s_f[q];
   }
-  __syncthreads();
-  if (lane == 0) {
-    s_v[w] = bv;
-    s_i[w] = bi;
-    s_n[w] = bn;
-    s_f[w] = bf;
-  }
-  __syncthreads();
-  if (t == 0) {
-    for (int i = 1; i < TPB / WAVE; ++i) {
-      argmax_merge(s_v[0], s_i[0], s_v[i], s_i[i]);
-      s_n[0] += s_n[i];
-      s_f[0] |= s_f[i];
-    }
-    int status = STRIM_OK;
-    int draft = -1;
-    if (a.verify && j < a.k) {
-      draft = a.drafts[(int64_t)b * a.k + j];
-      if (draft < 0 || draft >= a.V) status = STRIM_EINVAL;
-    }
-    if (!p.valid) status = STRIM_EINVAL;
-    else if (s_f[0]) status = STRIM_ENONFINITE;
-    else if (s_n[0] == 0) status = STRIM_EEMPTY;
-    RowState& rs = a.s.rs[r];
-    rs.m = s_v[0];
-    rs.status = status;
-    rs.n_allowed = s_n[0];
-    rs.argmax = s_i[0];
-    rs.greedy = p.greedy ? 1 : 0;
-    rs.mode = MODE_NONE;
-    rs.draft = draft;
-    rs.token = -1;
-    rs.accept = 0;
-    rs.sum_kept = 0.0;
-    rs.last_key = 0ull;
-    if (!a.verify) {
-      if (status != STRIM_OK) {
-        a.out_ids[r] = -1;
-        if (a.out_status) a.out_status[r] = status;
-      } else if (p.greedy) {
-        a.out_ids[r] = s_i[0];
-        if (a.out_status) a.out_status[r] = STRIM_OK;
+  ChunkStat cs{m_w, a_w, n_w, f_w, 0.0, 0u, 0};
+  const bool live = n_w > 0 && !f_w;
+
+  if (p.cls == CLS_FAST && live) {
+    // Local candidates: every token that can pass min-p and top-k given m >= m_w.
+    const bool topk = p.top_k > 0 && p.top_k < a.V;
+    const bool minp = p.min_p > 0.0f;
+    const float dmp = minp ? (float)(-log((double)p.min_p)) * 1.000002f : INFINITY;
+    int rstar = 31;
+    if (topk) {
+      // counts per ladder rung (s_lad was cleared before the previous barrier)
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float d = m_w - l[e];
+        if (l[e] > -INFINITY && d <= dmp) atomicAdd(&s_lad[ladder_rung(d)], 1u);
+      }
+      __syncthreads();
+      uint32_t cum = 0;
+#pragma unroll
+      for (int q = 0; q < 32; ++q) {
+        cum += s_lad[q];
+        if (cum >= (uint32_t)p.top_k && rstar == 31) rstar = q;
       }
     }
-    if (p.greedy) rs.token = s_i[0];
-    a.s.cnt_stats[r] = 0u;
+    uint32_t sel = 0u;
+    int mycnt = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      if (!(l[e] > -INFINITY)) continue;
+      const float d = m_w - l[e];
+      if (d <= dmp && (!topk || ladder_rung(d) <= rstar)) {
+        sel |= 1u << e;
+        ++mycnt;
+      }
+    }
+    int wtot;
+    const int wex = wave_excl_count(mycnt, &wtot);
+    if (lane == 0) s_off[w] = wtot;
+    __syncthreads();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int q = 0; q < TPB / WAVE; ++q) {
+      if (q < w) base += s_off[q];
+      total += s_off[q];
+    }
+    if (total <= SLOT) {
+      int pos = base + wex;
+      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        if ((sel >> e) & 1u) dst[pos++] = Cand{l[e], i0 + e};
+    }
+    cs.nslot = total <= SLOT ? (uint32_t)total : (uint32_t)(SLOT + 1);
+  } else if (p.cls == CLS_GENERAL && live) {
+    // chunk sum exp(l - m_w) and a 64-bin coarse histogram of d_w = m_w - l
+    if (t < NCB) {
+      s_hc[t] = 0u;
+      s_hm[t] = 0ull;
+    }
+    __syncthreads();
+    double ssum = 0.0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      if (!(l[e] > -INFINITY)) continue;
+      const float d = m_w - l[e];
+      const float wgt = expf(-d);
+      ssum += (double)wgt;
+      const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
+      atomicAdd(&s_hc[bb], 1u);
+      const unsigned long long fx = __float2ull_rn(wgt * FIX_SCALE_F);
+      if (fx) atomicAdd(&s_hm[bb], fx);
+    }
+    ssum = wave_sum(ssum);
+    if (lane == 0) s_d[w] = ssum;
+    __syncthreads();
+    double S = 0.0;
+#pragma unroll
+    for (int q = 0; q < TPB / WAVE; ++q) S += s_d[q];
+    cs.S = S;
+    if (t < NCB) {
+      const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
+      a.s.chc[o] = s_hc[t];
+      a.s.chm[o] = s_hm[t];
+    }
+    // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
+    if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) {
+      const uint64_t key = mix64(p.seed, p.position);
+      float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
+      int id0 = -1, id1 = -1;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        if (!(l[e] > -INFINITY)) continue;
+        const int id = i0 + e;
+        const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
+                                : philox_uniform(key, (uint64_t)id);
+        top2_merge(s0, l0, id0, s1, l1, id1, l[e] + gumbel32(u), l[e], id, -INFINITY, 0.f, -1);
+      }
+      block_top2<TPB>(s0, l0, id0, s1, l1, id1, s_tf, s_ti);
+      if (t == 0) {
+        ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
+        pt.l0 = l0; pt.id0 = id0; pt.l1 = l1; pt.id1 = id1;
+      }
+    }
   }
+  if (t == 0) a.s.cstat[(int64_t)r * a.s.wmax + c] = cs;
 }
 
 // ---------------------------------------------------------------------------------
-// k_hist
+// k_collect: general rows
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ bool in_ranges(const RowState& rs, int bin) {
-  return (bin >= rs.rng[0][0] && bin <= rs.rng[0][1]) ||
-         (bin >= rs.rng[1][0] && bin <= rs.rng[1][1]) ||
-         (bin >= rs.rng[2][0] && bin <= rs.rng[2][1]);
-}
-
-// First bin b in [lo, hi] with pred(b) true, for a monotone predicate; hi + 1 if none.
 template <typename F>
 __device__ __forceinline__ int first_true(int lo, int hi, F pred) {
   int L = lo, H = hi + 1;
   while (L < H) {
-    int mid = (L + H) >> 1;
+    const int mid = (L + H) >> 1;
     if (pred(mid)) H = mid;
     else L = mid + 1;
   }
   return L;
 }
 
-__device__ __forceinline__ float row_uniform(const Args& a, int r, const RowParams& p,
-                                             int64_t idx) {
-  if (a.noise) return a.noise[(int64_t)r * a.noise_stride + idx];
-  return philox_uniform(mix64(p.seed, p.position), (uint64_t)idx);
+// Row statistics merged from the chunk statistics, identically in every workgroup.
+struct RowStats {
+  float m;
+  int32_t arg;
+  int32_t n;
+  int32_t flags;
+};
+
+template <int NT>
+__device__ __forceinline__ RowStats merge_chunks(const Args& a, int r, float* sv, int* si,
+                                                 int* sn, int* sf) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  float bv = -INFINITY;
+  int bi = -1, bn = 0, bf = 0;
+  for (int cc = t; cc < a.W; cc += NT) {
+    const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + cc];
+    argmax_merge(bv, bi, cs.m, cs.arg);
+    bn += cs.n;
+    bf |= cs.flags;
+  }
+  wave_argmax(bv, bi);
+  bn = wave_sum(bn);
+  bf = wave_or_i(bf);
+  if (lane == 0) {
+    sv[w] = bv;
+    si[w] = bi;
+    sn[w] = bn;
+    sf[w] = bf;
+  }
+  __syncthreads();
+  RowStats rs{sv[0], si[0], sn[0], sf[0]};
+  for (int q = 1; q < NT / WAVE; ++q) {
+    argmax_merge(rs.m, rs.arg, sv[q], si[q]);
+    rs.n += sn[q];
+    rs.flags |= sf[q];
+  }
+  __syncthreads();
+  return rs;
 }
 
-__global__ __launch_bounds__(TPB) void k_hist(Args a) {
-  __shared__ uint32_t s_cnt[CHUNK];
-  __shared__ uint32_t s_hc[NBINS];
-  __shared__ unsigned long long s_hm[NBINS];
-  __shared__ uint64_t s_red[TPB / WAVE];
-  __shared__ int s_last;
-
-  int r, c;
-  map_block(a, blockIdx.x, r, c);
-  const RowState* rsp = &a.s.rs[r];
-  if (rsp->status != STRIM_OK || rsp->greedy) return;  // uniform over the row
-  int b, j;
-  row_bj(a, r, b, j);
-  const RowParams p = load_params(a, b, j);
-  const int c0 = c * CHUNK;
-  const int t = threadIdx.x;
-  const float m = rsp->m;
-
-  for (int i = t; i < NBINS; i += TPB) {
-    s_hc[i] = 0u;
-    s_hm[i] = 0ull;
-  }
-  if (p.pen) build_counts(a, b, j, c0, s_cnt);
-  else __syncthreads();
-  float l[EPT];
-  bool nf = false;
-  process_tokens(a, r, c0, p, s_cnt, l, nf);
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    if (!(l[e] > -INFINITY)) continue;
-    const float d = m - l[e];
-    const int bin = dbin(d);
-    const unsigned long long fix = __float2ull_rn(expf(-d) * FIX_SCALE_F);
-    atomicAdd(&s_hc[bin], 1u);
-    if (fix) atomicAdd(&s_hm[bin], fix);
-  }
-  __syncthreads();
-  for (int i = t; i < NBINS; i += TPB) {
-    const uint32_t cn = s_hc[i];
-    if (cn) {
-      atomicAdd(&a.s.hcnt[(int64_t)r * NBINS + i], cn);
-      const unsigned long long ms = s_hm[i];
-      if (ms) atomicAdd(&a.s.hmass[(int64_t)r * NBINS + i], ms);
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    unsigned prev = atomicAdd(&a.s.cnt_hist[r], 1u);
-    s_last = (prev == (unsigned)(a.W - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // ---- last workgroup: inclusive cumulative counts C[b] and masses M[b] -----------
-  constexpr int BPT = NBINS / TPB;  // bins per thread
-  uint32_t lc[BPT];
-  unsigned long long lm[BPT];
-  uint32_t sc = 0;
-  unsigned long long sm = 0;
-#pragma unroll
-  for (int q = 0; q < BPT; ++q) {
-    const int bi = t * BPT + q;
-    lc[q] = __hip_atomic_load(&a.s.hcnt[(int64_t)r * NBINS + bi], __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-    lm[q] = __hip_atomic_load(&a.s.hmass[(int64_t)r * NBINS + bi], __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-    sc += lc[q];
-    sm += lm[q];
-  }
-  uint64_t tot_m;
-  const uint64_t base_m = block_excl_scan_u64<TPB>((uint64_t)sm, s_red, &tot_m);
-  uint64_t tot_c64;
-  const uint64_t base_c64 = block_excl_scan_u64<TPB>((uint64_t)sc, s_red, &tot_c64);
-  {
-    uint32_t cc = (uint32_t)base_c64;
-    unsigned long long mm = base_m;
-#pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      cc += lc[q];
-      mm += lm[q];
-      s_hc[t * BPT + q] = cc;  // inclusive cumulative count
-      s_hm[t * BPT + q] = mm;  // inclusive cumulative mass
-    }
-  }
-  __syncthreads();
-  if (t != 0) return;
-
-  RowState& rs = a.s.rs[r];
-  const int V = a.V;
-  const uint32_t N = s_hc[NBINS - 1];
-  const double inv = 1.0 / FIX_SCALE;
-  const double EPS = 1e-5;
-  const double SLACK = ((double)N + 2.0) * 2.0 * inv;
-  auto Mb = [&](int bb) -> double { return bb < 0 ? 0.0 : (double)s_hm[bb] * inv; };
-  auto Cb = [&](int bb) -> uint32_t { return bb < 0 ? 0u : s_hc[bb]; };
-
-  // pre-kept bounds (min-p and top-k): bins < s1 surely pass, bins > e1 surely fail
-  int s1 = NBINS, e1 = NBINS - 1;
+// Conservative bin bounds of a general row from the coarse chunk histograms
+// (thread 0; the same arithmetic in every workgroup of the row gives the same result).
+// cU/cL: cumulative fixed-point mass with each chunk bin placed at its earliest /
+// latest possible global bin; kU/kL: the same for counts.
+__device__ void compute_bounds(const Args& a, int r, const RowParams& p, float m, uint32_t N,
+                               const unsigned long long* cU, const unsigned long long* cL,
+                               const uint32_t* kU, const uint32_t* kL, Bounds& bd) {
+  const double inv = 1.0 / FIX_SCALE, EPS = 1e-5;
+  const double SLACK = (double)(a.W * NCB + 16) * 4.0 * inv;
+  auto MU = [&](int g) { return g < 0 ? 0.0 : (double)cU[g] * inv * (1.0 + EPS) + SLACK; };
+  auto ML = [&](int g) { return g < 0 ? 0.0 : (double)cL[g] * inv * (1.0 - EPS) - SLACK; };
+  int s1 = NGB, e1 = NGB - 1;
   if (p.min_p > 0.0f) {
     const double thr = -log((double)p.min_p);
-    const int bt = thr < 63.0 ? (int)(thr * (double)BIN_SCALE) : NBINS - 1;
-    s1 = min(s1, max(0, bt - 1));
-    e1 = min(e1, min(NBINS - 1, bt + 1));
+    const int gt = thr < 63.0 ? (int)(thr * (double)CB_SCALE) : NGB - 1;
+    s1 = min(s1, max(0, gt - 1));
+    e1 = min(e1, min(NGB - 1, gt + 1));
   }
-  const bool topk = p.top_k > 0 && p.top_k < V;
+  const bool topk = p.top_k > 0 && p.top_k < a.V;
   if (topk && N > (uint32_t)p.top_k) {
     const uint32_t K = (uint32_t)p.top_k;
-    const int bk = first_true(0, NBINS - 1, [&](int bb) { return s_hc[bb] >= K; });
-    s1 = min(s1, bk);
-    e1 = min(e1, bk);
+    const int glo = first_true(0, NGB - 1, [&](int g) { return kU[g] >= K; });
+    const int ghi = first_true(0, NGB - 1, [&](int g) { return kL[g] >= K; });
+    s1 = min(s1, glo);
+    e1 = min(e1, ghi);
   }
-  // top-p bounds
   int s = s1, e = e1;
   const bool topp = p.top_p < 1.0f;
   if (topp) {
     const double P = (double)p.top_p;
-    const double sig_hi = Mb(e1) * (1.0 + EPS) + SLACK;
-    const double sig_lo = Mb(s1 - 1) * (1.0 - EPS) - SLACK;
+    const double hi = MU(e1), lo = ML(s1 - 1);
     const int lim = min(e1, s1 - 1);
     int ep = e1;
     if (lim >= 0) {
-      const int f = first_true(0, lim, [&](int bb) { return Mb(bb) * (1.0 - EPS) - SLACK > P * sig_hi; });
+      const int f = first_true(0, lim, [&](int g) { return ML(g) > P * hi; });
       if (f <= lim) ep = f;
     }
-    // bins < sp surely kept: M[b](1+eps)+slack <= P * sig_lo
-    const int sp = first_true(0, NBINS - 1, [&](int bb) { return Mb(bb) * (1.0 + EPS) + SLACK > P * sig_lo; });
+    const int sp = first_true(0, NGB - 1, [&](int g) { return MU(g) > P * lo; });
     e = min(e1, ep);
     s = min(s1, sp);
   }
   if (s > e + 1) s = e + 1;
   const bool icdf = a.noise_mode == STRIM_NOISE_ICDF;
   const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
+  for (int q = 0; q < 3; ++q) { bd.rng[q][0] = 1; bd.rng[q][1] = 0; }
   int mode;
-  int rng[3][2] = {{1, 0}, {1, 0}, {1, 0}};
-  if (Cb(e1) <= (uint32_t)CAP) {
-    mode = MODE_A;  // every possibly pre-kept token is collected: all decisions exact
-    rng[0][0] = 0;
-    rng[0][1] = e1;
+  if (kU[e1] <= (uint32_t)CAP) {
+    mode = MODE_A;  // everything possibly pre-kept is collected
+    bd.rng[0][0] = 0;
+    bd.rng[0][1] = e1;
     s = 0;
   } else if (by_rank) {
-    mode = MODE_NONE;  // rank-indexed noise needs the whole kept set in order
+    mode = MODE_NONE;
   } else {
     mode = MODE_B;
-    rng[0][0] = s;
-    rng[0][1] = e;
-    if (s1 <= e1) {
-      rng[1][0] = s1;
-      rng[1][1] = e1;
-    }
+    bd.rng[0][0] = s;
+    bd.rng[0][1] = e;
+    if (s1 <= e1) { bd.rng[1][0] = s1; bd.rng[1][1] = e1; }
     if (icdf) {
       const double u = (double)row_uniform(a, r, p, 0);
       double wd = 0.0;
-      if (a.verify && rs.draft >= 0 && rs.l_draft > -INFINITY)
-        wd = exp((double)rs.l_draft - (double)m);
-      const double klo = Mb(s - 1) * (1.0 - EPS) - SLACK;
-      const double khi = Mb(e) * (1.0 + EPS) + SLACK;
-      const double tlo = u * (klo - wd) - SLACK;
-      const double thi = u * khi + wd + SLACK;
-      const int dlo = first_true(0, NBINS - 1, [&](int bb) { return Mb(bb) * (1.0 + EPS) + SLACK > tlo; });
-      int dhi = first_true(0, NBINS - 1, [&](int bb) { return Mb(bb) * (1.0 - EPS) - SLACK > thi; });
-      dhi = min(dhi, e);
-      rng[2][0] = dlo;
-      rng[2][1] = dhi;
-    }
-    uint32_t total = 0;
-    // union size of the (possibly overlapping) ranges, bin by bin (<= NBINS steps)
-    int lo = NBINS, hi = -1;
-    for (int q = 0; q < 3; ++q)
-      if (rng[q][0] <= rng[q][1]) {
-        lo = min(lo, rng[q][0]);
-        hi = max(hi, rng[q][1]);
+      if (a.verify) {
+        int bb, jj;
+        row_bj(a, r, bb, jj);
+        const float ld = a.s.rs[r].l_draft;
+        if (jj < a.k && ld > -INFINITY) wd = exp((double)ld - (double)m);
       }
-    for (int bb = lo; bb <= hi; ++bb) {
-      bool in = false;
-      for (int q = 0; q < 3; ++q) in |= (bb >= rng[q][0] && bb <= rng[q][1]);
-      if (in) total += Cb(bb) - Cb(bb - 1);
+      const double tlo = u * (ML(s - 1) - wd) - SLACK;
+      const double thi = u * MU(e) + wd + SLACK;
+      const int dlo = first_true(0, NGB - 1, [&](int g) { return MU(g) > tlo; });
+      int dhi = first_true(0, NGB - 1, [&](int g) { return ML(g) > thi; });
+      dhi = min(dhi, e);
+      bd.rng[2][0] = dlo;
+      bd.rng[2][1] = dhi;
+    }
+    // upper bound of the tokens in the collected bins: per contiguous run [lo, hi],
+    // kU[hi] - kL[lo - 1]
+    uint32_t total = 0;
+    int g = 0;
+    while (g < NGB) {
+      if (!in_rng(bd, g)) { ++g; continue; }
+      const int lo = g;
+      while (g + 1 < NGB && in_rng(bd, g + 1)) ++g;
+      const uint32_t below = lo > 0 ? kL[lo - 1] : 0u;
+      total += kU[g] > below ? kU[g] - below : 0u;
+      ++g;
     }
     if (total > (uint32_t)CAP) mode = MODE_NONE;
   }
-  if (mode == MODE_NONE) {
-    rs.status = STRIM_ECAPACITY;
-    if (!a.verify) {
-      a.out_ids[r] = -1;
-      if (a.out_status) a.out_status[r] = STRIM_ECAPACITY;
-    }
+  // non-collected intervals, split where the kept / pre-kept classification changes
+  int ns = 0;
+  for (int q = 0; q < NSEG; ++q) { bd.seg_lo[q] = 1; bd.seg_hi[q] = 0; }
+  int g = 0;
+  while (g < NGB && mode != MODE_NONE) {
+    if (in_rng(bd, g)) { ++g; continue; }
+    const int lo = g;
+    while (g + 1 < NGB && !in_rng(bd, g + 1) && g + 1 != s && g + 1 != s1) ++g;
+    if (ns == NSEG) { mode = MODE_NONE; break; }
+    bd.seg_lo[ns] = lo;
+    bd.seg_hi[ns] = g;
+    ++ns;
+    ++g;
   }
-  rs.mode = mode;
-  rs.s = s;
-  rs.e = e;
-  rs.s1 = s1;
-  for (int q = 0; q < 3; ++q) {
-    rs.rng[q][0] = rng[q][0];
-    rs.rng[q][1] = rng[q][1];
-  }
-  a.s.ncand[r] = 0u;
-  a.s.cnt_hist[r] = 0u;
-}
-
-// ---------------------------------------------------------------------------------
-// k_collect
-// ---------------------------------------------------------------------------------
-__device__ __forceinline__ void top2_merge(float& s0, float& l0, int& i0, float& s1, float& l1,
-                                           int& i1, float t0, float tl0, int ti0, float t1,
-                                           float tl1, int ti1) {
-  // merge (t0, t1) into the sorted pair (s0 >= s1); ids break ties (smaller first)
-  auto better = [](float a, int ia, float b, int ib) {
-    return ib < 0 || (ia >= 0 && (a > b || (a == b && ia < ib)));
-  };
-  float cs[4] = {s0, s1, t0, t1}, cl[4] = {l0, l1, tl0, tl1};
-  int ci[4] = {i0, i1, ti0, ti1};
-  int bi = 0;
-  for (int q = 1; q < 4; ++q)
-    if (better(cs[q], ci[q], cs[bi], ci[bi])) bi = q;
-  int si = -1;
-  for (int q = 0; q < 4; ++q)
-    if (q != bi && (si < 0 || better(cs[q], ci[q], cs[si], ci[si]))) si = q;
-  s0 = cs[bi]; l0 = cl[bi]; i0 = ci[bi];
-  s1 = cs[si]; l1 = cl[si]; i1 = ci[si];
+  bd.mode = mode;
+  bd.s = s;
+  bd.e = e;
+  bd.s1 = s1;
+  bd.e1 = e1;
 }
 
 __global__ __launch_bounds__(TPB) void k_collect(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
-  __shared__ float s_s0[TPB / WAVE], s_l0[TPB / WAVE], s_s1[TPB / WAVE], s_l1[TPB / WAVE];
-  __shared__ int s_i0[TPB / WAVE], s_i1[TPB / WAVE];
+  __shared__ unsigned long long s_U[NGB], s_L[NGB];
+  __shared__ uint32_t s_kU[NGB], s_kL[NGB];
+  __shared__ Bounds s_bd;
+  __shared__ float s_v[TPB / WAVE];
+  __shared__ int s_i[TPB / WAVE], s_n[TPB / WAVE], s_f[TPB / WAVE];
+  __shared__ unsigned long long s_sm[TPB / WAVE][NSEG];
+  __shared__ uint32_t s_sc[TPB / WAVE][NSEG];
+  __shared__ float s_tf[4 * TPB / WAVE];
+  __shared__ int s_ti[2 * TPB / WAVE];
 
   int r, c;
   map_block(a, blockIdx.x, r, c);
-  const RowState rs = a.s.rs[r];
-  if (rs.status != STRIM_OK || rs.greedy || rs.mode == MODE_NONE) return;
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);
-  const int c0 = c * CHUNK;
+  if (p.cls != CLS_GENERAL) return;
+  if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) return;
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int c0 = c * CHUNK, i0 = c0 + t * EPT;
 
+  float x[EPT];
+  load_tokens(a, r, i0, x);
+  const RowStats st = merge_chunks<TPB>(a, r, s_v, s_i, s_n, s_f);
+  if (st.n == 0 || st.flags) return;  // k_final reports the row status
+  const float m = st.m;
+
+  // global coarse bounds: each chunk bin lands in [g_lo, g_hi] of the global bins
+  for (int g = t; g < NGB; g += TPB) {
+    s_U[g] = 0ull; s_L[g] = 0ull; s_kU[g] = 0u; s_kL[g] = 0u;
+  }
+  __syncthreads();
+  for (int e = t; e < a.W * NCB; e += TPB) {
+    const int cc = e / NCB, bb = e - cc * NCB;
+    const int64_t o = ((int64_t)r * a.s.wmax + cc) * NCB + bb;
+    const uint32_t cn = a.s.chc[o];
+    if (!cn) continue;
+    const float mw = a.s.cstat[(int64_t)r * a.s.wmax + cc].m;
+    const double dlt = (double)m - (double)mw;
+    const double lo = (dlt + 0.5 * bb) * (1.0 - 2e-6) * CB_SCALE;
+    const double hi = bb == NCB - 1 ? 1e300 : (dlt + 0.5 * (bb + 1)) * (1.0 + 2e-6) * CB_SCALE;
+    const int glo = lo < (double)(NGB - 1) ? max(0, (int)floor(lo)) : NGB - 1;
+    const int ghi = hi < (double)(NGB - 1) ? max(0, (int)floor(hi)) : NGB - 1;
+    const double ms = (double)a.s.chm[o] * exp(-dlt);
+    atomicAdd(&s_U[glo], (unsigned long long)(ms + 1.0));
+    atomicAdd(&s_L[ghi], (unsigned long long)ms);
+    atomicAdd(&s_kU[glo], cn);
+    atomicAdd(&s_kL[ghi], cn);
+  }
   if (p.pen) build_counts(a, b, j, c0, s_cnt);
+  else __syncthreads();
+  if (t == 0) {
+    for (int g = 1; g < NGB; ++g) {
+      s_U[g] += s_U[g - 1]; s_L[g] += s_L[g - 1];
+      s_kU[g] += s_kU[g - 1]; s_kL[g] += s_kL[g - 1];
+    }
+    compute_bounds(a, r, p, m, (uint32_t)st.n, s_U, s_L, s_kU, s_kL, s_bd);
+    if (c == 0) a.s.rs[r].bd = s_bd;
+  }
+  __syncthreads();
+  const Bounds bd = s_bd;
+  if (bd.mode == MODE_NONE) return;
+
   float l[EPT];
   bool nf = false;
-  process_tokens(a, r, c0, p, s_cnt, l, nf);
-
-  const bool want_top = rs.mode == MODE_B && a.noise_mode == STRIM_NOISE_GUMBEL;
+  process_tokens(a, r, i0, p, s_cnt, x, l, nf);
+  const bool want_top = bd.mode == MODE_B && a.noise_mode == STRIM_NOISE_GUMBEL;
   const uint64_t key = mix64(p.seed, p.position);
-  int mycnt = 0;
+  unsigned long long sm[NSEG];
+  uint32_t sc[NSEG];
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q) { sm[q] = 0ull; sc[q] = 0u; }
   uint32_t sel = 0u;
+  int mycnt = 0;
   float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-  int i0 = -1, i1 = -1;
+  int id0 = -1, id1 = -1;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     if (!(l[e] > -INFINITY)) continue;
-    const int bin = dbin(rs.m - l[e]);
-    if (in_ranges(rs, bin)) {
+    const float d = m - l[e];
+    const int g = gbin(d);
+    if (in_rng(bd, g)) {
       sel |= 1u << e;
       ++mycnt;
-    } else if (want_top && bin < rs.s) {
-      const int id = c0 + t * EPT + e;
+      continue;
+    }
+    const int q = seg_of(bd, g);
+    const unsigned long long fx = __float2ull_rn(expf(-d) * FIX_SCALE_F);
+#pragma unroll
+    for (int qq = 0; qq < NSEG; ++qq)
+      if (qq == q) { sm[qq] += fx; sc[qq] += 1u; }
+    if (want_top && g < bd.s) {
+      const int id = i0 + e;
       const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
                               : philox_uniform(key, (uint64_t)id);
-      const float sc = l[e] + gumbel32(u);
-      top2_merge(s0, l0, i0, s1, l1, i1, sc, l[e], id, -INFINITY, 0.f, -1);
+      top2_merge(s0, l0, id0, s1, l1, id1, l[e] + gumbel32(u), l[e], id, -INFINITY, 0.f, -1);
     }
   }
-  // wave-aggregated append to the row's candidate buffer
-  const int incl = wave_incl_scan(mycnt);
-  const int tot = __shfl(incl, WAVE - 1, WAVE);
+  // append the collected tokens (one atomic per wave)
+  int tot;
+  const int wex = wave_excl_count(mycnt, &tot);
   if (tot > 0) {
     unsigned base = 0;
-    if (lane == WAVE - 1) base = atomicAdd(&a.s.ncand[r], (unsigned)tot);
-    base = __shfl(base, WAVE - 1, WAVE);
-    unsigned pos = base + (unsigned)(incl - mycnt);
+    if (lane == 0) base = atomicAdd(&a.s.ncand[r], (unsigned)tot);
+    base = (unsigned)__builtin_amdgcn_readlane((int)base, 0);
+    unsigned pos = base + (unsigned)wex;
 #pragma unroll
     for (int e = 0; e < EPT; ++e)
       if ((sel >> e) & 1u) {
-        if (pos < (unsigned)CAP)
-          a.s.cand[(int64_t)r * CAP + pos] = Cand{l[e], c0 + t * EPT + e};
+        if (pos < (unsigned)CAP) a.s.cand[(int64_t)r * CAP + pos] = Cand{l[e], i0 + e};
         ++pos;
       }
   }
-  if (want_top) {
+  // per-interval sums of the tokens not collected
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      float ts0 = __shfl_xor(s0, o, WAVE), tl0 = __shfl_xor(l0, o, WAVE);
-      float ts1 = __shfl_xor(s1, o, WAVE), tl1 = __shfl_xor(l1, o, WAVE);
-      int ti0 = __shfl_xor(i0, o, WAVE), ti1 = __shfl_xor(i1, o, WAVE);
-      top2_merge(s0, l0, i0, s1, l1, i1, ts0, tl0, ti0, ts1, tl1, ti1);
+  for (int q = 0; q < NSEG; ++q) {
+    sm[q] = wave_sum_u64(sm[q]);
+    sc[q] = wave_sum(sc[q]);
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int q = 0; q < NSEG; ++q) { s_sm[w][q] = sm[q]; s_sc[w][q] = sc[q]; }
+  if (want_top) block_top2<TPB>(s0, l0, id0, s1, l1, id1, s_tf, s_ti);
+  else __syncthreads();
+  if (t == 0) {
+    ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
+    for (int q = 0; q < NSEG; ++q) {
+      unsigned long long tm = 0ull;
+      uint32_t tc = 0u;
+      for (int ww = 0; ww < TPB / WAVE; ++ww) { tm += s_sm[ww][q]; tc += s_sc[ww][q]; }
+      pt.mass[q] = tm;
+      pt.cnt[q] = tc;
     }
-    if (lane == 0) {
-      s_s0[w] = s0; s_l0[w] = l0; s_i0[w] = i0;
-      s_s1[w] = s1; s_l1[w] = l1; s_i1[w] = i1;
-    }
-    __syncthreads();
-    if (t == 0) {
-      for (int q = 1; q < TPB / WAVE; ++q)
-        top2_merge(s0, l0, i0, s1, l1, i1, s_s0[q], s_l0[q], s_i0[q], s_s1[q], s_l1[q], s_i1[q]);
-      a.s.ctop[(int64_t)r * a.s.wmax + c] = ChunkTop{l0, i0, l1, i1};
-    }
+    pt.l0 = l0; pt.id0 = want_top ? id0 : -1;
+    pt.l1 = l1; pt.id1 = want_top ? id1 : -1;
   }
 }
 
 // ---------------------------------------------------------------------------------
 // k_final
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-  uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
-  uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Bitonic sort of FIN_Q * FIN_T keys held striped in registers (element e = q*FIN_T + t).
-// Only the first n2 (a power of two >= 64) elements take part; the rest are padding.
+// Bitonic sort of the first n2 (power of two, >= 64) keys. Keys live in registers,
+// striped (element e = q * FIN_T + t); strides >= 64 exchange through LDS, smaller ones
+// through wave shuffles. Register arrays are only indexed by unrolled constants.
 __device__ void bitonic_sort(uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key) {
   const int t = threadIdx.x;
   for (int size = 2; size <= n2; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= FIN_T) {
-        const int qs = stride / FIN_T;
+      if (stride >= WAVE) {
 #pragma unroll
-        for (int q = 0; q < FIN_Q; ++q) {
-          const int e = q * FIN_T + t;
-          const int pq = q ^ qs;
-          if (pq > q) {
-            const bool asc = (e & size) == 0;
-            uint64_t x = k[q], y = k[pq];
-            bool sw = asc ? (x > y) : (x < y);
-            if (sw) { k[q] = y; k[pq] = x; }
-          }
-        }
-      } else if (stride >= WAVE) {
-#pragma unroll
-        for (int q = 0; q < FIN_Q; ++q) s_key[q * FIN_T + t] = k[q];
+        for (int q = 0; q < FIN_Q; ++q)
+          if (q * FIN_T < n2) s_key[q * FIN_T + t] = k[q];
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < FIN_Q; ++q) {
+          if (q * FIN_T >= n2) continue;
           const int e = q * FIN_T + t;
           const int pe = e ^ stride;
           const uint64_t o = s_key[pe];
@@ -540,6 +596,7 @@ __device__ void bitonic_sort(uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key) {
       } else {
 #pragma unroll
         for (int q = 0; q < FIN_Q; ++q) {
+          if (q * FIN_T >= n2) continue;
           const int e = q * FIN_T + t;
           const uint64_t o = shfl_xor_u64(k[q], stride);
           const bool asc = (e & size) == 0;
@@ -550,317 +607,466 @@ __device__ void bitonic_sort(uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key) {
     }
   }
 #pragma unroll
-  for (int q = 0; q < FIN_Q; ++q) s_key[q * FIN_T + t] = k[q];
+  for (int q = 0; q < FIN_Q; ++q)
+    if (q * FIN_T < n2) s_key[q * FIN_T + t] = k[q];
   __syncthreads();
 }
 
-// Block argmax over (score desc, tie key asc). Returns the winner's id in *out_id.
+// Block argmax over (score desc, tie key asc); the winner's id lands in *out_id.
 __device__ void block_argmax_score(double sc, uint64_t tk, int id, double* s_sc, uint64_t* s_tk,
-                                   int* s_id, int* out_id, double* out_sc, double* out_second) {
+                                   int* s_id, int* out_id) {
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
-  // track best and second best score values for the margin
-  double sec = -INFINITY;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    double sc2 = __shfl_xor(sc, o, WAVE);
-    uint64_t tk2 = shfl_xor_u64(tk, o);
-    int id2 = __shfl_xor(id, o, WAVE);
-    double sec2 = __shfl_xor(sec, o, WAVE);
-    bool take = id2 >= 0 && (id < 0 || sc2 > sc || (sc2 == sc && tk2 < tk));
-    double lose = take ? sc : sc2;
-    sec = fmax(fmax(sec, sec2), (id >= 0 && id2 >= 0) ? lose : -INFINITY);
-    if (take) { sc = sc2; tk = tk2; id = id2; }
+  auto take = [](double& a, uint64_t& ak, int& ai, double b, uint64_t bk, int bi) {
+    if (bi >= 0 && (ai < 0 || b > a || (b == a && bk < ak))) { a = b; ak = bk; ai = bi; }
+  };
+#define STRIM_ARG_STEP(C) take(sc, tk, id, dpp_d<C>(sc), dpp_u64<C>(tk), dpp_i<C>(id))
+  STRIM_ARG_STEP(DPP_XOR1);
+  STRIM_ARG_STEP(DPP_XOR2);
+  STRIM_ARG_STEP(DPP_HALF_MIRROR);
+  STRIM_ARG_STEP(DPP_MIRROR);
+#undef STRIM_ARG_STEP
+  {
+    double bs = rl_d(sc, 0);
+    uint64_t bk = rl_u64(tk, 0);
+    int bi = rl_i(id, 0);
+    take(bs, bk, bi, rl_d(sc, 16), rl_u64(tk, 16), rl_i(id, 16));
+    take(bs, bk, bi, rl_d(sc, 32), rl_u64(tk, 32), rl_i(id, 32));
+    take(bs, bk, bi, rl_d(sc, 48), rl_u64(tk, 48), rl_i(id, 48));
+    sc = bs; tk = bk; id = bi;
   }
-  if (lane == 0) { s_sc[w] = sc; s_tk[w] = tk; s_id[w] = id; s_sc[FIN_T / WAVE + w] = sec; }
+  __syncthreads();
+  if (lane == 0) { s_sc[w] = sc; s_tk[w] = tk; s_id[w] = id; }
   __syncthreads();
   if (t == 0) {
-    double bs = s_sc[0], bsec = s_sc[FIN_T / WAVE];
+    double bs = s_sc[0];
     uint64_t btk = s_tk[0];
     int bid = s_id[0];
     for (int q = 1; q < FIN_T / WAVE; ++q) {
-      bsec = fmax(bsec, s_sc[FIN_T / WAVE + q]);
       if (s_id[q] < 0) continue;
-      bool take = bid < 0 || s_sc[q] > bs || (s_sc[q] == bs && s_tk[q] < btk);
-      if (bid >= 0) bsec = fmax(bsec, take ? bs : s_sc[q]);
-      if (take) { bs = s_sc[q]; btk = s_tk[q]; bid = s_id[q]; }
+      if (bid < 0 || s_sc[q] > bs || (s_sc[q] == bs && s_tk[q] < btk)) {
+        bs = s_sc[q]; btk = s_tk[q]; bid = s_id[q];
+      }
     }
     *out_id = bid;
-    *out_sc = bs;
-    *out_second = bsec;
   }
   __syncthreads();
 }
 
 __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   __shared__ uint64_t s_key[CAP];
-  __shared__ double s_P1[NBINS + 1];
-  __shared__ double s_P2[NBINS + 1];
-  __shared__ uint32_t s_PC[NBINS + 1];
-  __shared__ double s_dred[2 * FIN_T / WAVE];
+  __shared__ double s_w[CAP];
+  __shared__ double s_dred[FIN_T / WAVE];
   __shared__ uint64_t s_ured[FIN_T / WAVE];
   __shared__ int s_ired[FIN_T / WAVE];
-  __shared__ int s_int[4];
+  __shared__ float s_v[FIN_T / WAVE];
+  __shared__ int s_i[FIN_T / WAVE], s_n[FIN_T / WAVE], s_f[FIN_T / WAVE];
+  __shared__ int s_int[8];
   __shared__ float s_kth;
+  __shared__ uint32_t s_pre[256];
+  __shared__ uint32_t s_ns[256];
+  __shared__ double s_segm[NSEG];
+  __shared__ uint32_t s_segc[NSEG];
+  __shared__ int s_segk[NSEG];  // 2 = kept, 1 = pre-kept only, 0 = neither
+  __shared__ Bounds s_bd;
 
   const int r = blockIdx.x;
-  const RowState rs = a.s.rs[r];
-  if (rs.status != STRIM_OK || rs.greedy) return;
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);
   const int t = threadIdx.x;
-  const uint32_t nc = a.s.ncand[r];
   const int V = a.V;
   const bool verify_draft_row = a.verify && j < a.k;
+  RowState* rsp = &a.s.rs[r];
 
-  auto fail = [&](int st) {
+  const RowStats st = merge_chunks<FIN_T>(a, r, s_v, s_i, s_n, s_f);
+  int status = STRIM_OK;
+  int draft = -1;
+  if (verify_draft_row) {
+    draft = a.drafts[(int64_t)b * a.k + j];
+    if (draft < 0 || draft >= V) status = STRIM_EINVAL;
+  }
+  if (status == STRIM_OK && st.flags) status = STRIM_ENONFINITE;
+  if (status == STRIM_OK && st.n == 0) status = STRIM_EEMPTY;
+  const bool tops = p.cls == CLS_GENERAL && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, V);
+  if (status == STRIM_OK && !p.greedy && p.cls == CLS_GENERAL && !tops) {
+    if (t == 0) s_bd = rsp->bd;
+    __syncthreads();
+    if (s_bd.mode == MODE_NONE) status = STRIM_ECAPACITY;
+  }
+  auto finish = [&](int stt, int token, int accept, double sig, uint64_t lk) {
     if (t == 0) {
-      a.s.rs[r].status = st;
+      rsp->status = stt;
+      rsp->token = token;
+      rsp->accept = accept;
+      rsp->sum_kept = sig;
+      rsp->m = st.m;
+      rsp->last_key = lk;
       if (!a.verify) {
-        a.out_ids[r] = -1;
-        if (a.out_status) a.out_status[r] = st;
+        a.out_ids[r] = stt == STRIM_OK ? token : -1;
+        if (a.out_status) a.out_status[r] = stt;
       }
     }
   };
-  if (nc > (uint32_t)CAP) {
-    fail(STRIM_ECAPACITY);
+  if (status != STRIM_OK) {
+    finish(status, -1, 0, 0.0, 0ull);
     return;
   }
-  const int n = (int)nc;
+  if (p.greedy) {
+    finish(STRIM_OK, st.arg, verify_draft_row && st.arg == draft, 1.0, 0ull);
+    return;
+  }
+  const float m = st.m;
+  const int W = a.W;
+  const bool topk = p.top_k > 0 && p.top_k < V;
+  const bool topp = p.top_p < 1.0f;
+  const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
+  const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
+  const bool cand_sorted = no_lse ? topp : (topk || topp);
+  const uint64_t pkey = mix64(p.seed, p.position);
+  const int excl_id = verify_draft_row ? draft : -1;
 
-  // 1. candidates -> sorted keys (l desc, id asc)
-  uint64_t kk[FIN_Q];
-#pragma unroll
-  for (int q = 0; q < FIN_Q; ++q) {
-    const int idx = q * FIN_T + t;
-    if (idx < n) {
-      const Cand cd = a.s.cand[(int64_t)r * CAP + idx];
-      kk[q] = ckey(cd.l, cd.id);
-    } else {
-      kk[q] = ~0ull;
+  // ---- unfiltered Gumbel rows: the chunks' two best tokens -------------------------
+  if (tops) {
+    // row mass: each chunk's contribution loaded in parallel, summed in chunk order
+    for (int cc = t; cc < W; cc += FIN_T) {
+      const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + cc];
+      s_w[cc] = cs.n > 0 ? cs.S * exp((double)cs.m - (double)m) : 0.0;
     }
+    __syncthreads();
+    if (t == 0) {
+      double sig = 0.0;
+      for (int cc = 0; cc < W; ++cc) sig += s_w[cc];
+      s_dred[0] = sig;
+    }
+    __syncthreads();
+    const double sig = s_dred[0];
+    const double lse = log(sig);
+    double bsc = -INFINITY;
+    uint64_t btk = ~0ull;
+    int bid = -1;
+    for (int cc = t; cc < W; cc += FIN_T) {
+      const ChunkPart pt = a.s.part[(int64_t)r * a.s.wmax + cc];
+      for (int h = 0; h < 2; ++h) {
+        const int id = h == 0 ? pt.id0 : pt.id1;
+        const float l = h == 0 ? pt.l0 : pt.l1;
+        if (id < 0 || id == excl_id) continue;
+        const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
+                                : philox_uniform(pkey, (uint64_t)id);
+        const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
+        const double sc = base + gumbel64(u);
+        if (bid < 0 || sc > bsc || (sc == bsc && (uint64_t)id < btk)) {
+          bsc = sc; btk = (uint64_t)id; bid = id;
+        }
+      }
+    }
+    __syncthreads();
+    block_argmax_score(bsc, btk, bid, s_dred, s_ured, s_ired, &s_int[3]);
+    int token = s_int[3];
+    int acc = 0;
+    if (verify_draft_row) {
+      double w_d = 0.0;
+      if (rsp->l_draft > -INFINITY) w_d = exp((double)rsp->l_draft - (double)m);
+      const float ua = row_uniform(a, r, p, (int64_t)V);
+      acc = ((double)ua < w_d / sig) ? 1 : 0;
+      if (token < 0) token = st.arg;  // the draft is the only allowed token
+    }
+    finish(STRIM_OK, token, acc, sig, ~0ull);
+    return;
+  }
+
+  // ---- gather candidates --------------------------------------------------------
+  int n = 0;
+  const bool fast = p.cls == CLS_FAST;
+  if (fast) {
+    // chunk-order prefix of the local candidate counts (ids ascending overall)
+    for (int cc = t; cc < W && cc < 256; cc += FIN_T)
+      s_ns[cc] = a.s.cstat[(int64_t)r * a.s.wmax + cc].nslot;
+    __syncthreads();
+    if (t == 0) {
+      uint32_t acc = 0;
+      int over = W > 256 ? 1 : 0;
+      for (int cc = 0; cc < W && !over; ++cc) {
+        const uint32_t ns = s_ns[cc];
+        if (ns > (uint32_t)SLOT) over = 1;
+        s_pre[cc] = acc;
+        acc += ns;
+      }
+      s_int[0] = (over || acc > (uint32_t)CAP) ? -1 : (int)acc;
+    }
+    __syncthreads();
+    n = s_int[0];
+    if (n < 0) {
+      finish(STRIM_ECAPACITY, -1, 0, 0.0, 0ull);
+      return;
+    }
+  } else {
+    n = (int)a.s.ncand[r];
+    if (n > CAP) {
+      finish(STRIM_ECAPACITY, -1, 0, 0.0, 0ull);
+      return;
+    }
+    // per-chunk interval sums staged in LDS (s_w is free until the masses are computed),
+    // then summed in chunk order by one thread per interval
+    unsigned long long* st_m = (unsigned long long*)s_w;   // [NSEG][W]
+    uint32_t* st_c = (uint32_t*)(st_m + NSEG * W);          // [NSEG][W]
+    for (int e = t; e < W * NSEG; e += FIN_T) {
+      const int cc = e / NSEG, q = e - cc * NSEG;
+      const ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + cc];
+      st_m[q * W + cc] = pt.mass[q];
+      st_c[q * W + cc] = pt.cnt[q];
+    }
+    __syncthreads();
+    if (t < NSEG) {
+      unsigned long long tm = 0ull;
+      uint32_t tc = 0u;
+      for (int cc = 0; cc < W; ++cc) {
+        tm += st_m[t * W + cc];
+        tc += st_c[t * W + cc];
+      }
+      s_segm[t] = (double)tm * (1.0 / FIX_SCALE);
+      s_segc[t] = tc;
+      const bool valid = s_bd.seg_lo[t] <= s_bd.seg_hi[t];
+      s_segk[t] = !valid ? 0 : (s_bd.seg_hi[t] < s_bd.s ? 2 : (s_bd.seg_hi[t] < s_bd.s1 ? 1 : 0));
+    }
+    __syncthreads();
   }
   int n2 = 64;
   while (n2 < n) n2 <<= 1;
-  bitonic_sort(kk, n2, s_key);
-
-  // 2. per-bin prefixes over NON-collected bins (histogram masses)
-  {
-    constexpr int BPT = NBINS / FIN_T;
-    double m1[BPT], m2[BPT];
-    uint32_t cn[BPT];
-    double t1 = 0.0, t2 = 0.0;
-    uint64_t tc = 0;
-#pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      const int bb = t * BPT + q;
-      const bool col = in_ranges(rs, bb);
-      const uint32_t hc = a.s.hcnt[(int64_t)r * NBINS + bb];
-      const double hm = (double)a.s.hmass[(int64_t)r * NBINS + bb] * (1.0 / FIX_SCALE);
-      cn[q] = col ? 0u : hc;
-      m1[q] = (!col && bb < rs.s1) ? hm : 0.0;
-      m2[q] = (!col && bb < rs.s) ? hm : 0.0;
-      t1 += m1[q];
-      t2 += m2[q];
-      tc += cn[q];
+  uint64_t kk[FIN_Q];
+  if (fast) {
+    // slot entries of chunk cc land at s_pre[cc] + i; scatter into LDS, then load
+    for (int e = t; e < W * SLOT; e += FIN_T) {
+      const int cc = e / SLOT, i = e - cc * SLOT;
+      if ((uint32_t)i < s_ns[cc]) {
+        const Cand cd = a.s.slot[((int64_t)r * a.s.wmax + cc) * SLOT + i];
+        s_key[s_pre[cc] + i] = ckey(cd.l, cd.id);
+      }
     }
-    double tot1, tot2;
-    uint64_t totc;
-    double b1 = block_excl_scan_f64<FIN_T>(t1, s_dred, &tot1);
-    double b2 = block_excl_scan_f64<FIN_T>(t2, s_dred, &tot2);
-    uint64_t bc = block_excl_scan_u64<FIN_T>(tc, s_ured, &totc);
+    __syncthreads();
 #pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      const int bb = t * BPT + q;
-      s_P1[bb] = b1;
-      s_P2[bb] = b2;
-      s_PC[bb] = (uint32_t)bc;
-      b1 += m1[q];
-      b2 += m2[q];
-      bc += cn[q];
+    for (int q = 0; q < FIN_Q; ++q) {
+      const int idx = q * FIN_T + t;
+      kk[q] = idx < n ? s_key[idx] : ~0ull;
     }
-    if (t == 0) {
-      s_P1[NBINS] = tot1;
-      s_P2[NBINS] = tot2;
-      s_PC[NBINS] = (uint32_t)totc;
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int q = 0; q < FIN_Q; ++q) {
+      const int idx = q * FIN_T + t;
+      kk[q] = ~0ull;
+      if (idx < n) {
+        const Cand cd = a.s.cand[(int64_t)r * CAP + idx];
+        kk[q] = ckey(cd.l, cd.id);
+      }
     }
   }
   if (t == 0) s_kth = -INFINITY;
-  __syncthreads();
+  if (n <= FIN_T) {
+    // rank by counting: one key per thread, broadcast reads of every key (keys are
+    // unique, so the ranks are a permutation of 0..n-1)
+    if (t < n) s_key[t] = kk[0];
+    __syncthreads();
+    const uint64_t k0 = kk[0];
+    uint32_t rank = 0;
+    int jj = 0;
+    for (; jj + 4 <= n; jj += 4)
+      rank += (uint32_t)(s_key[jj] < k0) + (uint32_t)(s_key[jj + 1] < k0) +
+              (uint32_t)(s_key[jj + 2] < k0) + (uint32_t)(s_key[jj + 3] < k0);
+    for (; jj < n; ++jj) rank += (uint32_t)(s_key[jj] < k0);
+    __syncthreads();
+    if (t < n) s_key[rank] = k0;
+    __syncthreads();
+  } else {
+    bitonic_sort(kk, n2, s_key);
+  }
 
-  // 3. decode this thread's blocked positions [t*Q, t*Q+Q)
-  const float m = rs.m;
-  float lv[FIN_Q];
-  int idv[FIN_Q], binv[FIN_Q];
-  double wv[FIN_Q];
-  uint64_t keyv[FIN_Q];
-  bool pre[FIN_Q];
+  // ---- per-position data lives in LDS: keys in s_key, fp64 masses in s_w ----------
   const bool minp = p.min_p > 0.0f;
   const double lmp = minp ? log((double)p.min_p) : 0.0;
-  const bool topk = p.top_k > 0 && p.top_k < V;
   const bool keep_ties = (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) != 0;
+  // non-collected tokens before global coarse bin g: count, pre-kept mass, kept mass
+  auto seg_before = [&](int g, uint32_t& cb, double& pb, double& kb) {
+    cb = 0u;
+    pb = 0.0;
+    kb = 0.0;
+    if (fast) return;
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s)
+      if (s_bd.seg_lo[s] <= s_bd.seg_hi[s] && s_bd.seg_hi[s] < g) {
+        cb += s_segc[s];
+        if (s_segk[s] >= 1) pb += s_segm[s];
+        if (s_segk[s] == 2) kb += s_segm[s];
+      }
+  };
 #pragma unroll
   for (int q = 0; q < FIN_Q; ++q) {
     const int pos = t * FIN_Q + q;
+    if (pos >= n) break;
     const uint64_t key = s_key[pos];
-    keyv[q] = key;
-    lv[q] = fkey_desc_inv((uint32_t)(key >> 32));
-    idv[q] = (int)(uint32_t)key;
-    binv[q] = pos < n ? dbin(m - lv[q]) : NBINS - 1;
-    wv[q] = pos < n ? exp((double)lv[q] - (double)m) : 0.0;
-    if (pos < n && topk && keep_ties && s_PC[binv[q]] + (uint32_t)pos == (uint32_t)(p.top_k - 1))
-      s_kth = lv[q];
+    const float l = fkey_desc_inv((uint32_t)(key >> 32));
+    s_w[pos] = exp((double)l - (double)m);
+    if (topk && keep_ties) {
+      uint32_t cb;
+      double pb, kb;
+      seg_before(gbin(m - l), cb, pb, kb);
+      if (cb + (uint32_t)pos == (uint32_t)(p.top_k - 1)) s_kth = l;
+    }
   }
   __syncthreads();
   const float kth = s_kth;
+  double seg_pre = 0.0, seg_kept = 0.0;
+  if (!fast)
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+      if (s_segk[s] >= 1) seg_pre += s_segm[s];
+      if (s_segk[s] == 2) seg_kept += s_segm[s];
+    }
+
+  // ---- pre-filters (min-p, top-k): a prefix of the order ---------------------------
   int first_bad = n;
 #pragma unroll
   for (int q = 0; q < FIN_Q; ++q) {
     const int pos = t * FIN_Q + q;
-    bool ok = pos < n;
-    if (ok && minp) ok = ((double)lv[q] - (double)m) >= lmp;
+    if (pos >= n) break;
+    const uint64_t key = s_key[pos];
+    const float l = fkey_desc_inv((uint32_t)(key >> 32));
+    bool ok = true;
+    if (minp) ok = ((double)l - (double)m) >= lmp;
     if (ok && topk) {
-      const uint32_t rank = s_PC[binv[q]] + (uint32_t)pos;
-      ok = keep_ties ? (lv[q] >= kth) : (rank < (uint32_t)p.top_k);
+      if (keep_ties) {
+        ok = l >= kth;
+      } else {
+        uint32_t cb;
+        double pb, kb;
+        seg_before(gbin(m - l), cb, pb, kb);
+        ok = cb + (uint32_t)pos < (uint32_t)p.top_k;
+      }
     }
-    pre[q] = ok;
     if (!ok && pos < first_bad) first_bad = pos;
   }
-  // n_pre = first position failing the pre-filters (prefix property)
-  first_bad = wave_min_i(first_bad);
-  if ((t & (WAVE - 1)) == 0) s_ired[t / WAVE] = first_bad;
-  __syncthreads();
-  if (t == 0) {
-    int v = n;
-    for (int q = 0; q < FIN_T / WAVE; ++q) v = min(v, s_ired[q]);
-    s_int[0] = v;
-  }
-  __syncthreads();
-  const int n_pre = s_int[0];
+  const int n_pre = block_min<FIN_T>(first_bad, s_ired);
 
-  // 4. top-p over the pre-kept set
+  // ---- top-p over the pre-kept set ---------------------------------------------------
   double loc = 0.0;
 #pragma unroll
-  for (int q = 0; q < FIN_Q; ++q) loc += (t * FIN_Q + q < n_pre) ? wv[q] : 0.0;
+  for (int q = 0; q < FIN_Q; ++q) {
+    const int pos = t * FIN_Q + q;
+    if (pos < n_pre) loc += s_w[pos];
+  }
   double tot_pre;
-  double ex = block_excl_scan_f64<FIN_T>(loc, s_dred, &tot_pre);
-  const double sig_pre = s_P1[NBINS] + tot_pre;
+  const double ex = block_excl_scan_f64<FIN_T>(loc, s_dred, &tot_pre);
+  const double sig_pre = seg_pre + tot_pre;
   int n_keep = n_pre;
-  if (p.top_p < 1.0f) {
+  if (topp) {
     const double P = (double)p.top_p;
     int fd = n;
     double run = ex;
 #pragma unroll
     for (int q = 0; q < FIN_Q; ++q) {
       const int pos = t * FIN_Q + q;
-      if (pos < n_pre) {
-        const double before = s_P1[binv[q]] + run;
-        if (before / sig_pre - P > 0.0 && pos < fd) fd = pos;
-        run += wv[q];
-      }
+      if (pos >= n_pre) break;
+      uint32_t cb;
+      double pb, kb;
+      seg_before(gbin(m - fkey_desc_inv((uint32_t)(s_key[pos] >> 32))), cb, pb, kb);
+      const double before = pb + run;
+      if (before / sig_pre - P > 0.0 && pos < fd) fd = pos;
+      run += s_w[pos];
     }
-    fd = wave_min_i(fd);
-    __syncthreads();
-    if ((t & (WAVE - 1)) == 0) s_ired[t / WAVE] = fd;
-    __syncthreads();
-    if (t == 0) {
-      int v = n_pre;
-      for (int q = 0; q < FIN_T / WAVE; ++q) v = min(v, s_ired[q]);
-      s_int[1] = v;
-    }
-    __syncthreads();
-    n_keep = s_int[1];
+    n_keep = block_min<FIN_T>(min(fd, n_pre), s_ired);
   }
-  // 5. kept mass and the kept prefix
   loc = 0.0;
 #pragma unroll
-  for (int q = 0; q < FIN_Q; ++q) loc += (t * FIN_Q + q < n_keep) ? wv[q] : 0.0;
+  for (int q = 0; q < FIN_Q; ++q) {
+    const int pos = t * FIN_Q + q;
+    if (pos < n_keep) loc += s_w[pos];
+  }
   double tot_keep;
   const double exk = block_excl_scan_f64<FIN_T>(loc, s_dred, &tot_keep);
-  const double sig_k = s_P2[NBINS] + tot_keep;
+  const double sig_k = seg_kept + tot_keep;
   const uint64_t last_key = n_keep > 0 ? s_key[n_keep - 1] : 0ull;
 
-  // draft (verify rows): kept? and its mass
+  // the draft (verify rows): kept? and its mass
   double w_d = 0.0;
   uint64_t key_d = ~0ull;
-  if (verify_draft_row && rs.l_draft > -INFINITY) {
-    const int bd = dbin(m - rs.l_draft);
-    key_d = ckey(rs.l_draft, rs.draft);
-    const bool kept_d = in_ranges(rs, bd) ? (key_d <= last_key && last_key != 0ull) : (bd < rs.s);
-    if (kept_d) w_d = exp((double)rs.l_draft - (double)m);
+  if (verify_draft_row && rsp->l_draft > -INFINITY) {
+    const float ld = rsp->l_draft;
+    key_d = ckey(ld, draft);
+    bool kept_d;
+    if (fast) kept_d = last_key != 0ull && key_d <= last_key;
+    else {
+      const int g = gbin(m - ld);
+      kept_d = in_rng(s_bd, g) ? (last_key != 0ull && key_d <= last_key) : (g < s_bd.s);
+    }
+    if (kept_d) w_d = exp((double)ld - (double)m);
   }
-  const bool one_hot = verify_draft_row;  // general-q residuals are not built yet
-  const int excl_id = one_hot ? rs.draft : -1;
 
-  // 6. draw
+  // ---- draw --------------------------------------------------------------------------
   int token = -1;
   if (a.noise_mode == STRIM_NOISE_ICDF) {
     const float u = row_uniform(a, r, p, 0);
-    const double sig_r = sig_k - (one_hot ? w_d : 0.0);
+    const double sig_r = sig_k - w_d;
     const double tgt = (double)u * sig_r;
     int best = n;
     double run = exk;
 #pragma unroll
     for (int q = 0; q < FIN_Q; ++q) {
       const int pos = t * FIN_Q + q;
-      if (pos < n_keep) {
-        double before = s_P2[binv[q]] + run;
-        if (one_hot && key_d < keyv[q]) before -= w_d;
-        const double wq = (idv[q] == excl_id) ? 0.0 : wv[q];
-        if (before + wq > tgt && wq > 0.0 && pos < best) best = pos;
-        run += wv[q];
-      }
+      if (pos >= n_keep) break;
+      const uint64_t key = s_key[pos];
+      uint32_t cb;
+      double pb, kb;
+      seg_before(gbin(m - fkey_desc_inv((uint32_t)(key >> 32))), cb, pb, kb);
+      double before = kb + run;
+      if (key_d < key) before -= w_d;
+      const double wq = ((int)(uint32_t)key == excl_id) ? 0.0 : s_w[pos];
+      if (wq > 0.0 && before + wq > tgt && pos < best) best = pos;
+      run += s_w[pos];
     }
-    best = wave_min_i(best);
-    __syncthreads();
-    if ((t & (WAVE - 1)) == 0) s_ired[t / WAVE] = best;
-    __syncthreads();
-    if (t == 0) {
-      int v = n;
-      for (int q = 0; q < FIN_T / WAVE; ++q) v = min(v, s_ired[q]);
-      s_int[2] = v;
-    }
-    __syncthreads();
-    int bp = s_int[2];
+    int bp = block_min<FIN_T>(best, s_ired);
     if (bp >= n_keep) {
       // rounding pushed the target past the last collected kept token
-      if (rs.mode == MODE_A && n_keep > 0) bp = n_keep - 1;
-      else bp = -1;
+      const bool all_collected = fast || s_bd.mode == MODE_A;
+      bp = (all_collected && n_keep > 0) ? n_keep - 1 : -1;
+      if (bp >= 0 && (int)(uint32_t)s_key[bp] == excl_id) bp = bp > 0 ? bp - 1 : -1;
     }
     if (bp < 0) {
-      fail(STRIM_ECAPACITY);
+      finish(STRIM_ECAPACITY, -1, 0, 0.0, 0ull);
       return;
     }
     token = (int)(uint32_t)s_key[bp];
   } else {
-    const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
-    const bool topp = p.top_p < 1.0f;
-    const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
-    const bool cand_sorted = no_lse ? topp : (topk || topp);
     const double lse = log(sig_k);
-    const uint64_t pkey = mix64(p.seed, p.position);
     double bsc = -INFINITY;
     uint64_t btk = ~0ull;
     int bid = -1;
 #pragma unroll
     for (int q = 0; q < FIN_Q; ++q) {
       const int pos = t * FIN_Q + q;
-      if (pos >= n_keep || idv[q] == excl_id) continue;
-      const uint32_t rank = s_PC[binv[q]] + (uint32_t)pos;
-      const int64_t nidx = by_rank ? (int64_t)rank : (int64_t)idv[q];
+      if (pos >= n_keep) break;
+      const uint64_t key = s_key[pos];
+      const int id = (int)(uint32_t)key;
+      if (id == excl_id) continue;
+      const float l = fkey_desc_inv((uint32_t)(key >> 32));
+      int64_t nidx = id;
+      if (by_rank) {
+        uint32_t cb;
+        double pb, kb;
+        seg_before(gbin(m - l), cb, pb, kb);
+        nidx = (int64_t)(cb + (uint32_t)pos);
+      }
       const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + nidx]
                               : philox_uniform(pkey, (uint64_t)nidx);
-      const double base = no_lse ? (double)lv[q] : ((double)lv[q] - (double)m) - lse;
+      const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
       const double sc = base + gumbel64(u);
-      const uint64_t tk = cand_sorted ? keyv[q] : (uint64_t)idv[q];
-      if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) { bsc = sc; btk = tk; bid = idv[q]; }
+      const uint64_t tk = cand_sorted ? key : (uint64_t)id;
+      if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) { bsc = sc; btk = tk; bid = id; }
     }
-    if (rs.mode == MODE_B) {
-      for (int cc = t; cc < a.W; cc += FIN_T) {
-        const ChunkTop ct = a.s.ctop[(int64_t)r * a.s.wmax + cc];
+    if (!fast && s_bd.mode == MODE_B) {
+      for (int cc = t; cc < W; cc += FIN_T) {
+        const ChunkPart pt = a.s.part[(int64_t)r * a.s.wmax + cc];
         for (int h = 0; h < 2; ++h) {
-          const int id = h == 0 ? ct.id0 : ct.id1;
-          const float l = h == 0 ? ct.l0 : ct.l1;
+          const int id = h == 0 ? pt.id0 : pt.id1;
+          const float l = h == 0 ? pt.l0 : pt.l1;
           if (id < 0 || id == excl_id) continue;
           const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
                                   : philox_uniform(pkey, (uint64_t)id);
@@ -871,34 +1077,21 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
         }
       }
     }
-    double bsc_out, second;
-    block_argmax_score(bsc, btk, bid, s_dred, s_ured, s_ired, &s_int[3], &bsc_out, &second);
+    block_argmax_score(bsc, btk, bid, s_dred, s_ured, s_ired, &s_int[3]);
     token = s_int[3];
-    if (token < 0) token = n_keep > 0 ? (int)(uint32_t)s_key[0] : -1;  // all scores -inf
+    if (token < 0) token = n_keep > 0 ? (int)(uint32_t)s_key[0] : -1;  // every score -inf
     if (token < 0) {
-      fail(STRIM_ECAPACITY);
+      finish(STRIM_ECAPACITY, -1, 0, 0.0, 0ull);
       return;
     }
   }
-
-  // 7. accept test (verify draft rows) and outputs
-  if (t == 0) {
-    RowState& o = a.s.rs[r];
-    o.sum_kept = sig_k;
-    o.last_key = last_key;
-    o.token = token;
-    if (verify_draft_row) {
-      const double q_d = 1.0;
-      const double p_d = w_d / sig_k;
-      const double ratio = q_d > 0.0 ? p_d / q_d : (p_d > 0.0 ? INFINITY : 0.0);
-      const float ua = row_uniform(a, r, p, a.noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V : 1);
-      o.accept = ((double)ua < ratio) ? 1 : 0;
-    }
-    if (!a.verify) {
-      a.out_ids[r] = token;
-      if (a.out_status) a.out_status[r] = STRIM_OK;
-    }
+  int acc = 0;
+  if (verify_draft_row) {
+    const double p_d = w_d / sig_k;
+    const float ua = row_uniform(a, r, p, a.noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V : 1);
+    acc = ((double)ua < p_d) ? 1 : 0;
   }
+  finish(STRIM_OK, token, acc, sig_k, last_key);
 }
 
 // ---------------------------------------------------------------------------------
@@ -908,32 +1101,38 @@ __global__ __launch_bounds__(TPB) void k_probs(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
   int r, c;
   map_block(a, blockIdx.x, r, c);
-  const RowState rs = a.s.rs[r];
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);
-  const int c0 = c * CHUNK;
-  const int t = threadIdx.x;
+  const RowState rs = a.s.rs[r];
+  const int c0 = c * CHUNK, i0 = c0 + (int)threadIdx.x * EPT;
   float* out = a.out_probs + (int64_t)r * a.V;
-  const int i0 = c0 + t * EPT;
-  if (rs.status != STRIM_OK || rs.greedy) {
+  if (rs.status != STRIM_OK || p.greedy) {
     for (int e = 0; e < EPT; ++e)
-      if (i0 + e < a.V)
-        out[i0 + e] = (rs.status == STRIM_OK && i0 + e == rs.argmax) ? 1.0f : 0.0f;
+      if (i0 + e < a.V) out[i0 + e] = (rs.status == STRIM_OK && i0 + e == rs.token) ? 1.0f : 0.0f;
     return;
   }
+  float x[EPT];
+  load_tokens(a, r, i0, x);
   if (p.pen) build_counts(a, b, j, c0, s_cnt);
   float l[EPT];
   bool nf = false;
-  process_tokens(a, r, c0, p, s_cnt, l, nf);
+  process_tokens(a, r, i0, p, s_cnt, x, l, nf);
+  const bool general_b = p.cls == CLS_GENERAL && rs.bd.mode == MODE_B &&
+                         !(a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V));
   for (int e = 0; e < EPT; ++e) {
     const int i = i0 + e;
     if (i >= a.V) break;
     float pv = 0.0f;
     if (l[e] > -INFINITY) {
-      const int bin = dbin(rs.m - l[e]);
-      const bool kept = in_ranges(rs, bin) ? (rs.last_key != 0ull && ckey(l[e], i) <= rs.last_key)
-                                           : (bin < rs.s);
+      bool kept;
+      const uint64_t ky = ckey(l[e], i);
+      if (general_b) {
+        const int g = gbin(rs.m - l[e]);
+        kept = in_rng(rs.bd, g) ? (rs.last_key != 0ull && ky <= rs.last_key) : (g < rs.bd.s);
+      } else {
+        kept = rs.last_key != 0ull && ky <= rs.last_key;
+      }
       if (kept) pv = (float)(exp((double)l[e] - (double)rs.m) / rs.sum_kept);
     }
     out[i] = pv;
@@ -957,16 +1156,14 @@ __global__ void k_verify_combine(Args a) {
       if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = -1;
       continue;
     }
-    int acc = 0;
-    if (j < k) acc = rs.greedy ? (rs.argmax == rs.draft) : rs.accept;
-    const int tok = rs.greedy ? rs.argmax : rs.token;
+    const int acc = j < k ? rs.accept : 0;
     if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = acc;
-    if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = tok;
+    if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = rs.token;
     if (alive) {
       if (j < k && acc) ++n;
       else {
         alive = false;
-        token = tok;
+        token = rs.token;
       }
     }
   }

@@ -33,7 +33,11 @@ EXPORTS = (
     "strim_verify",
     "strim_mask_logits",
     "strim_draft_argmax",
+    "strim_profile_begin",
+    "strim_profile_end",
+    "strim_kernel_name",
 )
+KERNEL_COUNT = 5
 
 
 class StrimError(RuntimeError):
@@ -113,6 +117,12 @@ def lib() -> ctypes.CDLL:
         L.strim_mask_logits.argtypes = [P, P, I32, I32, I32, I64, P, I64, P]
         L.strim_draft_argmax.restype = ctypes.c_int
         L.strim_draft_argmax.argtypes = [P, P, I32, I32, I32, I64, P, P]
+        L.strim_profile_begin.restype = ctypes.c_int
+        L.strim_profile_begin.argtypes = [P, I32]
+        L.strim_profile_end.restype = ctypes.c_int
+        L.strim_profile_end.argtypes = [P, P, P]
+        L.strim_kernel_name.restype = ctypes.c_char_p
+        L.strim_kernel_name.argtypes = [I32]
         _lib = L
     return _lib
 

@@ -30,18 +30,14 @@ def _dtype_code(t: torch.Tensor) -> int:
     raise TypeError(f"logits must be bfloat16 or float32, got {t.dtype}")
 
 
-def params_to_device(params: np.ndarray, device) -> torch.Tensor:
-    """Host strim_sampling_params rows -> a device byte tensor of the same layout."""
-    p = np.ascontiguousarray(params, dtype=N.PARAMS_DTYPE)
-    return torch.from_numpy(p.view(np.uint8).copy()).to(device)
+def host_params(params) -> np.ndarray:
+    """strim_sampling_params rows as a contiguous host array (the C ABI reads them at
+    call time; the caller may reuse the memory as soon as the call returns)."""
+    return np.ascontiguousarray(params, dtype=N.PARAMS_DTYPE).reshape(-1)
 
 
-def _as_params(params, device) -> torch.Tensor:
-    if isinstance(params, torch.Tensor):
-        if params.dtype != torch.uint8 or not params.is_cuda:
-            raise TypeError("device params must be a cuda uint8 tensor of 48-byte rows")
-        return params
-    return params_to_device(params, device)
+def _pp(p: np.ndarray) -> ctypes.c_void_p:
+    return p.ctypes.data_as(ctypes.c_void_p)
 
 
 def _check_cuda(*ts):
@@ -50,6 +46,14 @@ def _check_cuda(*ts):
             raise ValueError("every tensor argument must be on the GPU")
         if t is not None and not t.is_contiguous():
             raise ValueError("tensor arguments must be contiguous")
+
+
+def _check_rows(t: torch.Tensor) -> None:
+    """Logits may have a row stride > V, but each row must be contiguous."""
+    if not t.is_cuda:
+        raise ValueError("logits must be on the GPU")
+    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        raise ValueError("logits must be [R, V] with contiguous rows (row stride >= V)")
 
 
 class Context:
@@ -82,6 +86,19 @@ class Context:
             pass
 
     # -------------------------------------------------------------------------
+    def profile_begin(self, max_launches: int) -> None:
+        N.check(N.lib().strim_profile_begin(self._h, max_launches), "strim_profile_begin")
+
+    def profile_end(self) -> dict:
+        """{kernel name: (total ms, launches)} since profile_begin (synchronises)."""
+        tot = np.zeros(N.KERNEL_COUNT, np.float64)
+        cnt = np.zeros(N.KERNEL_COUNT, np.int64)
+        N.check(N.lib().strim_profile_end(self._h, tot.ctypes.data_as(ctypes.c_void_p),
+                                          cnt.ctypes.data_as(ctypes.c_void_p)),
+                "strim_profile_end")
+        return {N.lib().strim_kernel_name(i).decode(): (float(tot[i]), int(cnt[i]))
+                for i in range(N.KERNEL_COUNT)}
+
     def sample(self, logits: torch.Tensor, params, mask: torch.Tensor | None = None,
                history: torch.Tensor | None = None, history_len: torch.Tensor | None = None,
                noise_mode: int = N.NOISE_ICDF, noise: torch.Tensor | None = None,
@@ -93,8 +110,11 @@ class Context:
             logits = logits.unsqueeze(0)
         B, V = logits.shape
         dev = logits.device
-        p = _as_params(params, dev)
-        _check_cuda(logits, mask, history, history_len, noise)
+        p = host_params(params)
+        if p.size != B:
+            raise ValueError(f"need {B} param rows, got {p.size}")
+        _check_rows(logits)
+        _check_cuda(mask, history, history_len, noise)
         if out_ids is None:
             out_ids = torch.empty(B, dtype=torch.int32, device=dev)
         if out_status is None:
@@ -103,7 +123,7 @@ class Context:
         H = 0 if history is None else history.shape[-1]
         mstride = 0 if mask is None else mask.shape[-1]
         rc = N.lib().strim_sample(self._h, _stream(stream), _ptr(logits), _dtype_code(logits),
-                                  B, V, logits.stride(0), _ptr(p), _ptr(mask), mstride,
+                                  B, V, logits.stride(0), _pp(p), _ptr(mask), mstride,
                                   _ptr(history), _ptr(history_len), H, noise_mode, _ptr(noise),
                                   _ptr(out_ids), _ptr(out_status), _ptr(probs))
         N.check(rc, "strim_sample")
@@ -120,7 +140,9 @@ class Context:
         B, k1, V = target_logits.shape
         k = k1 - 1
         dev = target_logits.device
-        p = _as_params(params, dev)
+        p = host_params(params)
+        if p.size != B:
+            raise ValueError(f"need {B} param rows, got {p.size}")
         _check_cuda(target_logits, draft_tokens, draft_logits, draft_to_full, mask, history,
                     history_len, noise)
         acc = torch.empty(B, dtype=torch.int32, device=dev)
@@ -133,7 +155,7 @@ class Context:
         Vd = 0 if draft_logits is None else draft_logits.shape[-1]
         rc = N.lib().strim_verify(self._h, _stream(stream), _ptr(target_logits),
                                   _dtype_code(target_logits), B, k, V, _ptr(draft_logits), Vd,
-                                  _ptr(draft_to_full), _ptr(draft_tokens), _ptr(p), _ptr(mask),
+                                  _ptr(draft_to_full), _ptr(draft_tokens), _pp(p), _ptr(mask),
                                   mstride, _ptr(history), _ptr(history_len), H, noise_mode,
                                   _ptr(noise), _ptr(acc), _ptr(tok), _ptr(racc), _ptr(rtok),
                                   _ptr(st))
@@ -147,7 +169,8 @@ def mask_logits(logits: torch.Tensor, mask_words: torch.Tensor | None, stream=No
     if logits.dim() == 1:
         logits = logits.unsqueeze(0)
     R, V = logits.shape
-    _check_cuda(logits, mask_words)
+    _check_rows(logits)
+    _check_cuda(mask_words)
     out = torch.empty(R, V, dtype=torch.float32, device=logits.device)
     mstride = 0 if mask_words is None else mask_words.shape[-1]
     N.check(N.lib().strim_mask_logits(_stream(stream), _ptr(logits), _dtype_code(logits), R, V,
@@ -162,7 +185,8 @@ def draft_argmax(draft_logits: torch.Tensor, draft_to_full: torch.Tensor | None 
     if draft_logits.dim() == 1:
         draft_logits = draft_logits.unsqueeze(0)
     R, Vd = draft_logits.shape
-    _check_cuda(draft_logits, draft_to_full)
+    _check_rows(draft_logits)
+    _check_cuda(draft_to_full)
     out = torch.empty(R, dtype=torch.int32, device=draft_logits.device)
     N.check(N.lib().strim_draft_argmax(_stream(stream), _ptr(draft_logits),
                                        _dtype_code(draft_logits), R, Vd, draft_logits.stride(0),

@@ -155,13 +155,20 @@ def test_row_errors(ctx):
     x[4, 9] = np.inf
     allowed = np.ones((B, V), bool)
     allowed[3] = False
+    allowed[2, :100] = False  # row 2 stays valid
     p = O.make_params(B)
-    p["top_p"][2] = 0.0
     say("row errors")
     ids, st, ref = check_sample(ctx, x, p, "f32", W.pack_mask(allowed), label="errors")
-    assert st.tolist() == [0, O.STRIM_ENONFINITE, O.STRIM_EINVAL, O.STRIM_EEMPTY,
-                           O.STRIM_ENONFINITE]
-    assert (ids[1:] == -1).all()
+    assert st.tolist() == [0, O.STRIM_ENONFINITE, 0, O.STRIM_EEMPTY, O.STRIM_ENONFINITE]
+    assert (ids[[1, 3, 4]] == -1).all()
+    # invalid params fail the whole call synchronously, like ChatRequest validation
+    from strim_amd import _native as N
+
+    bad = p.copy()
+    bad["top_p"][2] = 0.0
+    with pytest.raises(N.StrimError) as ei:
+        run_sample(ctx, x, bad, "f32")
+    assert ei.value.code == N.EINVAL
 
 
 def test_strided_and_unaligned_rows(ctx):
@@ -273,7 +280,7 @@ def test_sampler_mirror_matches_oracle(ctx):
     rng = np.random.default_rng(8)
     V = 4000
     x = rng.normal(size=V).astype(np.float32)
-    xd = dev_logits(x, "f32")[0]
+    xd = dev_logits(x, "f32")
     s = Sampler(GenParams(temperature=0.9, top_k=20, top_p=0.9, seed=123), ctx=ctx)
     say("mirror Sampler.sample")
     for i in range(5):
