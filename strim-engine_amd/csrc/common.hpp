@@ -242,6 +242,51 @@ __device__ __forceinline__ double block_excl_scan_f64(double v, double* scratch,
   return base + inc - v;
 }
 
+// Inclusive scan of 64-bit integers over the wave (same pattern as the fp64 scan).
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
+  v += dpp_u64<DPP_SHR1>(v);
+  v += dpp_u64<DPP_SHR2>(v);
+  v += dpp_u64<DPP_SHR4>(v);
+  v += dpp_u64<DPP_SHR8>(v);
+  const uint64_t t0 = rl_u64(v, 15), t1 = rl_u64(v, 31), t2 = rl_u64(v, 47);
+  const int row = (threadIdx.x & (WAVE - 1)) >> 4;
+  if (row >= 1) v += t0;
+  if (row >= 2) v += t1;
+  if (row >= 3) v += t2;
+  return v;
+}
+
+// Block-wide exclusive scans of two 64-bit integers per thread (exact). `scratch` holds
+// >= 2 * NT / 64 values.
+template <int NT>
+__device__ __forceinline__ void block_excl_scan2_u64(uint64_t v1, uint64_t v2, uint64_t* scratch,
+                                                     uint64_t& ex1, uint64_t& ex2,
+                                                     uint64_t& tot1, uint64_t& tot2) {
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const uint64_t i1 = wave_incl_scan_u64(v1), i2 = wave_incl_scan_u64(v2);
+  if (lane == WAVE - 1) {
+    scratch[w] = i1;
+    scratch[NT / WAVE + w] = i2;
+  }
+  __syncthreads();
+  uint64_t b1 = 0, b2 = 0, t1 = 0, t2 = 0;
+#pragma unroll
+  for (int i = 0; i < NT / WAVE; ++i) {
+    const uint64_t s1 = scratch[i], s2 = scratch[NT / WAVE + i];
+    if (i < w) {
+      b1 += s1;
+      b2 += s2;
+    }
+    t1 += s1;
+    t2 += s2;
+  }
+  __syncthreads();
+  ex1 = b1 + i1 - v1;
+  ex2 = b2 + i2 - v2;
+  tot1 = t1;
+  tot2 = t2;
+}
+
 // Block-wide min of one int per thread; every thread gets the result.
 template <int NT>
 __device__ __forceinline__ int block_min(int v, int* scratch) {

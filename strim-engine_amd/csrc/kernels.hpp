@@ -181,7 +181,8 @@ __device__ __forceinline__ RowParams load_params(const Args& a, int b, int j) {
 }
 
 // Raw logits of this thread's EPT tokens (issued before anything waits on memory).
-__device__ __forceinline__ void load_tokens(const Args& a, int r, int i0, float (&x)[EPT]) {
+template <typename A>
+__device__ __forceinline__ void load_tokens(const A& a, int r, int i0, float (&x)[EPT]) {
   const int64_t base = (int64_t)r * a.row_stride;
   if (a.dtype == STRIM_DTYPE_BF16) {
     const uint16_t* xb = (const uint16_t*)a.logits + base;
@@ -211,35 +212,42 @@ __device__ __forceinline__ void load_tokens(const Args& a, int r, int i0, float 
   }
 }
 
-// History counts of the chunk [c0, c0 + CHUNK) in LDS (plus the verify draft prefix).
-// Called by every thread of the workgroup when p.pen.
-__device__ __forceinline__ void build_counts(const Args& a, int b, int j, int c0,
-                                             uint32_t* s_cnt) {
-  for (int i = threadIdx.x; i < CHUNK; i += TPB) s_cnt[i] = 0u;
+// History counts of the span [c0, c0 + SPAN) in LDS (plus the verify draft prefix).
+// Called by every thread of an NT-thread workgroup when p.pen.
+template <int NT, int SPAN, typename A>
+__device__ __forceinline__ void build_counts_span(const A& a, int b, int j, int c0,
+                                                  uint32_t* s_cnt) {
+  for (int i = threadIdx.x; i < SPAN; i += NT) s_cnt[i] = 0u;
   __syncthreads();
   if (a.hist) {
     int hl = a.hist_len ? a.hist_len[b] : a.H;
     hl = hl < 0 ? 0 : (hl > a.H ? a.H : hl);
     const int32_t* h = a.hist + (int64_t)b * a.H;
-    for (int i = threadIdx.x; i < hl; i += TPB) {
+    for (int i = threadIdx.x; i < hl; i += NT) {
       const int id = h[i];
       const unsigned o = (unsigned)(id - c0);
-      if (o < (unsigned)CHUNK && id < a.V) atomicAdd(&s_cnt[o], 1u);
+      if (o < (unsigned)SPAN && id < a.V) atomicAdd(&s_cnt[o], 1u);
     }
   }
   if (a.verify && (int)threadIdx.x < j) {
     const int id = a.drafts[(int64_t)b * a.k + threadIdx.x];
     const unsigned o = (unsigned)(id - c0);
-    if (o < (unsigned)CHUNK && id < a.V) atomicAdd(&s_cnt[o], 1u);
+    if (o < (unsigned)SPAN && id < a.V) atomicAdd(&s_cnt[o], 1u);
   }
   __syncthreads();
+}
+__device__ __forceinline__ void build_counts(const Args& a, int b, int j, int c0,
+                                             uint32_t* s_cnt) {
+  build_counts_span<TPB, CHUNK>(a, b, j, c0, s_cnt);
 }
 
 // Penalties -> mask -> temperature on raw values x. Masked / out-of-range tokens get
 // -inf. Greedy rows skip the temperature. Each step is one IEEE float32 operation (the
-// library is built with -ffp-contract=off).
-__device__ __forceinline__ void process_tokens(const Args& a, int r, int i0, const RowParams& p,
-                                               const uint32_t* s_cnt, const float (&x)[EPT],
+// library is built with -ffp-contract=off). `cnt` points at this thread's EPT history
+// counts.
+template <typename A>
+__device__ __forceinline__ void process_tokens(const A& a, int r, int i0, const RowParams& p,
+                                               const uint32_t* cnt, const float (&x)[EPT],
                                                float (&l)[EPT], bool& nonfinite) {
   uint32_t bits = 0xFFu;
   if (a.mask && i0 < a.V) {
@@ -250,10 +258,10 @@ __device__ __forceinline__ void process_tokens(const Args& a, int r, int i0, con
   for (int e = 0; e < EPT; ++e) {
     float v = x[e];
     if (p.pen) {
-      const uint32_t cnt = s_cnt[(i0 & (CHUNK - 1)) + e];
-      if (cnt > 0u) {
+      const uint32_t c = cnt[e];
+      if (c > 0u) {
         v = v > 0.0f ? v / p.rep : v * p.rep;
-        v = v - p.freq * (float)cnt;
+        v = v - p.freq * (float)c;
         v = v - p.pres;
       }
     }
@@ -285,7 +293,8 @@ __device__ __forceinline__ int seg_of(const Bounds& bd, int g) {
 
 // Uniform element `idx` of row r's noise vector: injected, or Philox at the row's
 // (seed, position) key.
-__device__ __forceinline__ float row_uniform(const Args& a, int r, const RowParams& p,
+template <typename A>
+__device__ __forceinline__ float row_uniform(const A& a, int r, const RowParams& p,
                                              int64_t idx) {
   if (a.noise) return a.noise[(int64_t)r * a.noise_stride + idx];
   return philox_uniform(mix64(p.seed, p.position), (uint64_t)idx);

@@ -55,11 +55,15 @@ def check_sample(ctx, x, params, dtype="bf16", mask=None, history=None, history_
     ref = O.sample(xh, params, mask=mask, history=history, history_len=history_len,
                    noise_mode=noise_mode, noise=noise, want_probs=probs)
     np.testing.assert_array_equal(st, ref["status"], err_msg=f"{label} status")
+    excused = 0
     for r in range(len(ids)):
         if ids[r] != ref["token"][r]:
             assert ref["margin"][r] < O.TIE_EPS, (
                 f"{label} row {r}: gpu {ids[r]} oracle {ref['token'][r]} "
                 f"margin {ref['margin'][r]:.3g} status {st[r]}")
+            excused += 1
+    # a documented fp tie is rare on random data; many of them would hide real errors
+    assert excused <= 1 + len(ids) // 8, f"{label}: {excused} rows differ at fp ties"
     if probs:
         for r in range(len(ids)):
             if ref["status"][r] != 0 or ref["margin"][r] < O.TIE_EPS:
@@ -96,10 +100,13 @@ def check_verify(ctx, target, k, drafts, params, dtype="bf16", mask=None, histor
                    draft_logits=dlh, draft_to_full=table, mask=mask, history=history,
                    history_len=history_len, noise_mode=noise_mode, noise=noise)
     np.testing.assert_array_equal(g["status"], ref["status"], err_msg=f"{label} status")
+    excused = 0
     for b in range(th.shape[0]):
         same = (g["accepted"][b] == ref["accepted"][b] and g["token"][b] == ref["token"][b])
         if not same:
             assert ref["margin"][b] < O.TIE_EPS, (
                 f"{label} seq {b}: gpu ({g['accepted'][b]},{g['token'][b]}) oracle "
                 f"({ref['accepted'][b]},{ref['token'][b]}) margin {ref['margin'][b]:.3g}")
+            excused += 1
+    assert excused <= 1 + th.shape[0] // 8, f"{label}: {excused} sequences differ at fp ties"
     return g, ref

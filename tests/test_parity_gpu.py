@@ -136,6 +136,68 @@ def test_large_nucleus_top_p(ctx):
         check_sample(ctx, x, p, "bf16", None, None, None, mode, None, label="nucleus")
 
 
+@pytest.mark.parametrize("injected", [False, True])
+def test_rank_noise_wide_nucleus(ctx, injected):
+    # Sampler-compat rows (ties kept, noise by rank, no log-sum-exp) whose nucleus holds
+    # tens of thousands of tokens: the rank-ordered walk of the exact path
+    rng = np.random.default_rng(33)
+    B, V = 4, W.V_DEFAULT
+    x = rng.normal(0, 0.7, size=(B, V)).astype(np.float32)
+    p = O.make_params(B, temperature=np.float32(1.3), top_p=[0.5, 0.9, 0.99, 0.7],
+                      top_k=[0, 0, 0, 60000], flags=O.FLAG_SAMPLER_COMPAT,
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                      position=np.arange(B, dtype=np.uint64))
+    noise = rng.random((B, V + 1), dtype=np.float32) if injected else None
+    say(f"rank noise wide nucleus injected={injected}")
+    check_sample(ctx, x, p, "bf16", None, None, None, O.NOISE_GUMBEL, noise, label="rank-wide")
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_ICDF, O.NOISE_GUMBEL])
+def test_minp_slot_overflow(ctx, mode):
+    # min-p rows (fast class) over near-flat logits: every chunk overflows its local
+    # candidate slots and the row is resolved by the exact path
+    rng = np.random.default_rng(34)
+    B, V = 8, W.V_DEFAULT
+    x = rng.normal(0, 0.2, size=(B, V)).astype(np.float32)
+    hist = rng.integers(0, V, size=(B, 512), dtype=np.int32)
+    p = O.make_params(B, temperature=np.float32(1.0), min_p=np.float32(0.05),
+                      top_k=[0, 0, 300, 5000, 0, 0, 0, 0],
+                      top_p=[1.0, 0.9, 1.0, 0.8, 1.0, 0.95, 1.0, 0.6],
+                      repetition_penalty=np.float32(1.2), frequency_penalty=np.float32(0.1),
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                      position=np.arange(B, dtype=np.uint64))
+    say(f"minp overflow mode={mode}")
+    check_sample(ctx, x, p, "bf16", None, hist, None, mode, None, label="minp-overflow")
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_ICDF, O.NOISE_GUMBEL])
+def test_tie_blocks(ctx, mode):
+    # logits quantised to a few values: huge exact-tie groups ordered by id
+    rng = np.random.default_rng(35)
+    B, V = 6, 50000
+    x = rng.integers(-3, 2, size=(B, V)).astype(np.float32)
+    p = O.make_params(B, top_k=[0, 20000, 0, 777, 0, 30000], top_p=[0.9, 1.0, 0.3, 0.99, 1.0, 0.5],
+                      flags=[0, 1, 7, 1, 0, 7], seed=rng.integers(0, 2**63, size=B, dtype=np.uint64))
+    say(f"tie blocks mode={mode}")
+    check_sample(ctx, x, p, "bf16", None, None, None, mode, None, label="ties")
+
+
+def test_verify_flat_exact(ctx):
+    # verification over near-flat target rows with penalties over history and the draft
+    # prefix: draft rows resolved by the exact path
+    rng = np.random.default_rng(36)
+    B, k, V = 3, 3, 60000
+    x = rng.normal(0, 0.3, size=(B, k + 1, V)).astype(np.float32)
+    drafts = rng.integers(0, V, size=(B, k), dtype=np.int32)
+    hist = rng.integers(0, V, size=(B, 300), dtype=np.int32)
+    p = O.make_params(B, temperature=np.float32(0.9), top_p=[0.95, 1.0, 0.8], min_p=[0.0, 0.05, 0.0],
+                      presence_penalty=np.float32(0.4),
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64))
+    for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+        say(f"verify flat mode={mode}")
+        check_verify(ctx, x, k, drafts, p, "bf16", None, hist, None, mode, None, label="verify-flat")
+
+
 def test_flat_row_ties(ctx):
     # every logit equal: order is by id; top-k keeps the K smallest ids
     V, B = 10000, 4
