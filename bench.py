@@ -159,7 +159,7 @@ def main():
     assert (st == 0).all(), f"row status {st}"
     kt2 = kernel_times(ctx, torch, step2, n_sets, args.steps)
     bytes2 = W.algorithmic_bytes(B, V, 2, mask=False, H=H, noise_floats=2)
-    stream_us = kt2["k_scan"][0]
+    stream_us = kt2["k_stream"][0]
     log(f"[bench] cfg2 {ms2 * 1e3:.2f} us/step; kernels (us/launch): "
         + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt2.items() if v[1]))
     del xs, hs, ns
@@ -207,7 +207,7 @@ def main():
                                "top-p U[0.8,1], min-p 0.05, presence 0.5, frequency 0.3 over "
                                "4096-token history, icdf draw (one uniform per row)",
                    "B": B, "V": V, "history": H},
-        "roofline": {"kernel": "k_scan", "bound": "hbm",
+        "roofline": {"kernel": "k_stream", "bound": "hbm",
                      "achieved": round(bytes2 / (stream_us * 1e-6) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(bytes2 / (stream_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
@@ -240,7 +240,7 @@ def main():
         assert (st5 == 0).all(), f"row status {st5}"
         kt5 = kernel_times(ctx, torch, step5, n5, args.steps)
         bytes5 = W.algorithmic_bytes(B5, V, 2, mask=True, H=H5, noise_floats=0)
-        us5 = kt5["k_scan"][0]
+        us5 = kt5["k_stream"][0]
         log(f"[bench] cfg5 {ms_5 * 1e3:.2f} us/step; kernels (us/launch): "
             + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt5.items() if v[1]))
         result["b64"] = {
@@ -248,7 +248,7 @@ def main():
                         "top-p 0.95, min-p 0.02, Philox per row",
             "us_per_step": round(ms_5 * 1e3, 3),
             "rows_per_s": round(B5 / (ms_5 * 1e-3), 1),
-            "roofline": {"kernel": "k_scan", "bound": "hbm",
+            "roofline": {"kernel": "k_stream", "bound": "hbm",
                          "achieved": round(bytes5 / (us5 * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(bytes5 / (us5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                          "bytes_per_launch": bytes5, "us_per_launch": round(us5, 3)},

@@ -182,7 +182,7 @@ int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, in
  * launches is bracketed by HIP events recorded on the call's stream; strim_profile_end
  * synchronises, sums the elapsed time per kernel and turns profiling off. Profiling
  * allocates its events in strim_profile_begin, never in the calls it times. */
-#define STRIM_KERNEL_COUNT 5 /* scan, collect, final, probs, verify_combine */
+#define STRIM_KERNEL_COUNT 6 /* stream, finalize, collect, final, probs, verify_combine */
 int strim_profile_begin(strim_ctx* ctx, int32_t max_launches);
 int strim_profile_end(strim_ctx* ctx, double* total_ms /* [STRIM_KERNEL_COUNT] */,
                       int64_t* launches /* [STRIM_KERNEL_COUNT] */);

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "strim_amd" / "libstrim_sampler.so"
-SOURCES = ["sample_kernels.hip", "aux_kernels.hip", "capi.hip"]
+SOURCES = ["stream_kernels.hip", "sample_kernels.hip", "aux_kernels.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

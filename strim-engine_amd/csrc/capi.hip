@@ -10,7 +10,8 @@
 #include "kernels.hpp"
 
 namespace strim {
-__global__ void k_scan(Args a);
+__global__ void k_stream(Args a);
+__global__ void k_finalize(Args a);
 __global__ void k_collect(Args a);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
@@ -66,9 +67,9 @@ int32_t vec_ok(const void* p, int64_t row_stride, int32_t dtype) {
   return ((uintptr_t)p % 16 == 0) && (row_stride % per16 == 0) ? 1 : 0;
 }
 
-enum KernelId { KID_SCAN = 0, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE };
-const char* const kKernelNames[STRIM_KERNEL_COUNT] = {"k_scan", "k_collect", "k_final",
-                                                      "k_probs", "k_verify_combine"};
+enum KernelId { KID_STREAM = 0, KID_FINALIZE, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE };
+const char* const kKernelNames[STRIM_KERNEL_COUNT] = {"k_stream", "k_finalize", "k_collect",
+                                                      "k_final", "k_probs", "k_verify_combine"};
 
 // Launches `launch()` on stream st, bracketed by profiling events when enabled.
 template <typename F>
@@ -88,21 +89,30 @@ bool nofilter(const strim_sampling_params& p, int32_t V) {
   return !(p.top_k > 0 && p.top_k < V) && !(p.min_p > 0.0f) && !(p.top_p < 1.0f);
 }
 
-// The launch sequence of one row group. k_collect runs only when a row of the group
-// needs the general path's second pass.
+// The launch sequence of one row group. k_stream + k_finalize decide greedy, fast and
+// unfiltered Gumbel rows; k_collect runs when a row needs the general path's second pass,
+// and k_final whenever a non-greedy row might still be undecided (general rows, or a
+// fast row whose candidates overflow k_stream's finalize).
 int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
-  bool need_collect = false;
-  for (int i = 0; i < nb; ++i)
-    if (row_class(a.p[i], a.V) == CLS_GENERAL &&
-        !(a.noise_mode == STRIM_NOISE_GUMBEL && nofilter(a.p[i], a.V)))
+  bool need_collect = false, need_final = false;
+  for (int i = 0; i < nb; ++i) {
+    const int32_t cls = row_class(a.p[i], a.V);
+    if (cls == CLS_GENERAL && !(a.noise_mode == STRIM_NOISE_GUMBEL && nofilter(a.p[i], a.V)))
       need_collect = true;
-  const dim3 grid_rc((unsigned)(a.R * a.W));
-  timed(ctx, st, KID_SCAN, [&] { hipLaunchKernelGGL(k_scan, grid_rc, dim3(TPB), 0, st, a); });
+    if (cls == CLS_GENERAL || cls == CLS_FAST) need_final = true;
+  }
+  if (need_collect) need_final = true;
+  const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
+  timed(ctx, st, KID_STREAM,
+        [&] { hipLaunchKernelGGL(k_stream, grid_rc, dim3(STPB), 0, st, a); });
+  timed(ctx, st, KID_FINALIZE,
+        [&] { hipLaunchKernelGGL(k_finalize, dim3((unsigned)a.R), dim3(STPB), 0, st, a); });
   if (need_collect)
     timed(ctx, st, KID_COLLECT,
           [&] { hipLaunchKernelGGL(k_collect, grid_rc, dim3(TPB), 0, st, a); });
-  timed(ctx, st, KID_FINAL,
-        [&] { hipLaunchKernelGGL(k_final, dim3((unsigned)a.R), dim3(FIN_T), 0, st, a); });
+  if (need_final)
+    timed(ctx, st, KID_FINAL,
+          [&] { hipLaunchKernelGGL(k_final, dim3((unsigned)a.R), dim3(FIN_T), 0, st, a); });
   if (probs)
     timed(ctx, st, KID_PROBS, [&] { hipLaunchKernelGGL(k_probs, grid_rc, dim3(TPB), 0, st, a); });
   return launch_status();
@@ -250,7 +260,6 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
       a.B = nb;
       a.k = 0;
       a.verify = 0;
-      a.xcd_map = (nb % 8 == 0) ? 1 : 0;
       a.mask = mask_words ? mask_words + (size_t)g0 * mask_stride : nullptr;
       a.mask_stride = mask_stride;
       a.hist = history ? history + (size_t)g0 * H : nullptr;
@@ -311,7 +320,6 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       a.B = nb;
       a.k = k;
       a.verify = 1;
-      a.xcd_map = (rows % 8 == 0) ? 1 : 0;
       a.mask = mask_words ? mask_words + (size_t)g0 * (k + 1) * mask_stride : nullptr;
       a.mask_stride = mask_stride;
       a.hist = history ? history + (size_t)g0 * H : nullptr;

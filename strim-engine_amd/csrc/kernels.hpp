@@ -1,13 +1,15 @@
 // kernels.hpp — argument block, scratch layout and per-row processing shared by the
 // gfx950 kernels.
 //
-// One call runs up to three kernels over R rows of V logits:
-//   k_scan    (rows x chunks)  single streaming pass: processed logits, chunk statistics,
-//                              and either the chunk's local candidates (fast rows) or a
-//                              64-bin coarse mass histogram (general rows);
-//   k_collect (rows x chunks)  general rows only: second pass that collects the tokens the
-//                              coarse bounds cannot resolve and sums the rest exactly;
-//   k_final   (one workgroup per row) exact decisions in fp64 over the sorted candidates.
+// One call runs up to four kernels over R rows of V logits:
+//   k_stream   (rows x chunks)  single streaming pass: processed logits, chunk statistics,
+//                               and either the chunk's local candidates (fast rows) or a
+//                               64-bin coarse mass histogram (general rows);
+//   k_finalize (one workgroup per row) decides greedy, fast and unfiltered Gumbel rows;
+//   k_collect  (rows x chunks)  general rows only: second pass that collects the tokens the
+//                               coarse bounds cannot resolve and sums the rest exactly;
+//   k_final    (one workgroup per row) general rows in fp64 over the sorted candidates,
+//                               and the exact streaming resolution of overflowing rows.
 // Workgroups never wait for or fence against each other: every partial result is a
 // plain store into a per-(row, chunk) slot that the next kernel reads.
 #pragma once
@@ -17,7 +19,11 @@
 namespace strim {
 
 constexpr int MAXP = 64;         // parameter rows carried inline per launch group
-constexpr int SLOT = 128;        // fast-path candidates per chunk
+constexpr int SLOTW = 64;        // fast-path candidates per wave of a k_stream workgroup
+constexpr int SLOT = 4 * SLOTW;  // ... per chunk (four waves)
+constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
+constexpr int STPB = 256;        // threads of a k_stream workgroup (16 tokens each)
+constexpr int FCAP = 4096;       // candidates k_finalize holds in LDS
 constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
 constexpr float CB_SCALE = 2.0f;
 constexpr int NGB = 129;         // global coarse bins: width 1/2 over [0, 64) + tail
@@ -28,6 +34,10 @@ constexpr int NSEG = 8;          // non-collected intervals summarised per chunk
 enum RowClass : int32_t { CLS_GREEDY = 0, CLS_FAST = 1, CLS_GENERAL = 2, CLS_INVALID = 3 };
 
 // How a row's candidates are resolved (set by k_collect for general rows).
+// Set by k_finalize: DONE rows are decided; PENDING rows (general path) go to
+// k_collect + k_final; EXACT rows (candidate overflow) to k_final's exact resolution.
+enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1, PH_EXACT = 2 };
+
 enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
 
 struct ChunkStat {
@@ -36,8 +46,9 @@ struct ChunkStat {
   int32_t n;       // allowed tokens
   int32_t flags;   // bit0: non-finite logit
   double S;        // sum exp(l - m) over the chunk (general rows)
-  uint32_t nslot;  // fast rows: local candidates written (SLOT + 1 = overflow)
-  int32_t pad;
+  uint32_t nslot;  // fast rows: candidates per wave, one byte each (255 = overflow)
+  float g;         // fast top-k rows: at least k of the chunk's tokens have v >= g (v is
+                   // the value before temperature); -inf when not certified
 };
 
 // General-path per-chunk summary of the tokens k_collect did not collect: fixed-point
@@ -50,6 +61,7 @@ struct ChunkPart {
   int32_t id0, id1;
 };
 
+// A candidate: fast rows store the value before temperature, general rows after it.
 struct Cand {
   float l;
   int32_t id;
@@ -71,7 +83,7 @@ struct RowState {
   int32_t accept;
   double sum_kept;
   float m;
-  int32_t pad;
+  int32_t phase;      // RowPhase: which kernel still has to decide the row
   uint64_t last_key;  // last kept token's order key (0 = none kept beyond bin rules)
   Bounds bd;          // general rows (k_collect)
 };
@@ -79,7 +91,8 @@ struct RowState {
 // Device scratch owned by a context (allocated once in strim_ctx_create).
 struct Scratch {
   ChunkStat* cstat;               // [rows][wmax]
-  Cand* slot;                     // [rows][wmax][SLOT]
+  Cand* slot;                     // [rows][wmax][4][SLOTW] fast-row candidates per wave
+                                  // (v before temperature, id)
   uint32_t* chc;                  // [rows][wmax][NCB] coarse counts
   unsigned long long* chm;        // [rows][wmax][NCB] coarse fixed-point masses
   ChunkPart* part;                // [rows][wmax]
@@ -98,7 +111,6 @@ struct Args {
   int32_t R, V, W;   // rows in this group, vocab, chunks per row
   int32_t B, k;      // batch rows in this group and draft length (k = 0: sample)
   int32_t verify;
-  int32_t xcd_map;
   const uint32_t* mask;
   int64_t mask_stride;
   const int32_t* hist;
@@ -147,17 +159,11 @@ __device__ __forceinline__ void row_bj(const Args& a, int r, int& b, int& j) {
   }
 }
 
-// Workgroup -> (row, chunk). With rows a multiple of 8, row r's chunks all run on
-// XCD r % 8 (workgroup i is dispatched to XCD i % 8), so re-reads stay in one L2.
-__device__ __forceinline__ void map_block(const Args& a, int bid, int& r, int& c) {
-  if (a.xcd_map) {
-    int x = bid & 7, slot = bid >> 3;
-    r = x + 8 * (slot / a.W);
-    c = slot - (slot / a.W) * a.W;
-  } else {
-    r = bid / a.W;
-    c = bid - r * a.W;
-  }
+// Workgroup -> (row, chunk): streaming kernels run on a (chunks, rows) grid, so the row
+// and its params are known from blockIdx without reading any kernel argument first.
+__device__ __forceinline__ void map_block(int& r, int& c) {
+  r = blockIdx.y;
+  c = blockIdx.x;
 }
 
 __device__ __forceinline__ RowParams load_params(const Args& a, int b, int j) {
@@ -275,6 +281,86 @@ __device__ __forceinline__ void process_tokens(const A& a, int r, int i0, const 
     if (lv == INFINITY) nonfinite = true;
     l[e] = lv;
   }
+}
+
+// Allow-bits of the 8 tokens [i0, i0 + 8) (i0 a multiple of 8): one byte of the packed
+// row, because bit (i & 31) of word (i >> 5) on a little-endian device is bit (i & 7) of
+// byte (i >> 3).
+template <typename A>
+__device__ __forceinline__ uint32_t load_mask8(const A& a, int r, int i0) {
+  if (!a.mask || i0 >= a.V) return 0xFFu;
+  return ((const uint8_t*)(a.mask + (int64_t)r * a.mask_stride))[i0 >> 3];
+}
+
+// process_tokens on preloaded allow-bits (see load_mask8).
+template <typename A>
+__device__ __forceinline__ void process_seg(const A& a, int i0, const RowParams& p, uint32_t bits,
+                                            const uint32_t* cnt, const float (&x)[EPT],
+                                            float (&l)[EPT], bool& nonfinite) {
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    float v = x[e];
+    if (p.pen) {
+      const uint32_t c = cnt[e];
+      if (c > 0u) {
+        v = v > 0.0f ? v / p.rep : v * p.rep;
+        v = v - p.freq * (float)c;
+        v = v - p.pres;
+      }
+    }
+    const bool ok = (i0 + e < a.V) && ((bits >> e) & 1u);
+    if (!ok) {
+      l[e] = -INFINITY;
+      continue;
+    }
+    if (isnan(v) || v == INFINITY) nonfinite = true;
+    const float lv = p.greedy ? v : v / p.T;
+    if (lv == INFINITY) nonfinite = true;
+    l[e] = lv;
+  }
+}
+
+// History counts of the span [c0, c0 + SPAN) in LDS, like build_counts_span, but the
+// first HPT * NT history ids are loaded before the table is cleared, so their latency
+// overlaps the clear and the caller's other loads.
+constexpr int HPT = 16;
+template <int NT, int SPAN, typename A>
+__device__ __forceinline__ void build_counts_pre(const A& a, int b, int j, int c0,
+                                                 uint32_t* s_cnt) {
+  const int t = threadIdx.x;
+  const int32_t* h = a.hist ? a.hist + (int64_t)b * a.H : nullptr;
+  int ids[HPT];
+#pragma unroll
+  for (int q = 0; q < HPT; ++q) {
+    const int i = q * NT + t;
+    ids[q] = (h && i < a.H) ? h[i] : -1;
+  }
+  int hl = h ? a.H : 0;
+  if (h && a.hist_len) {
+    hl = a.hist_len[b];
+    hl = hl < 0 ? 0 : (hl > a.H ? a.H : hl);
+  }
+  uint4* s4 = (uint4*)s_cnt;
+  for (int i = t; i < SPAN / 4; i += NT) s4[i] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+  const uint32_t uc0 = (uint32_t)c0;
+#pragma unroll
+  for (int q = 0; q < HPT; ++q) {
+    const int i = q * NT + t;
+    const uint32_t o = (uint32_t)ids[q] - uc0;
+    if (i < hl && o < (uint32_t)SPAN && ids[q] >= 0 && ids[q] < a.V) atomicAdd(&s_cnt[o], 1u);
+  }
+  for (int i = HPT * NT + t; i < hl; i += NT) {
+    const int id = h[i];
+    const uint32_t o = (uint32_t)id - uc0;
+    if (o < (uint32_t)SPAN && id >= 0 && id < a.V) atomicAdd(&s_cnt[o], 1u);
+  }
+  if (a.verify && t < j) {
+    const int id = a.drafts[(int64_t)b * a.k + t];
+    const uint32_t o = (uint32_t)id - uc0;
+    if (o < (uint32_t)SPAN && id >= 0 && id < a.V) atomicAdd(&s_cnt[o], 1u);
+  }
+  __syncthreads();
 }
 
 // Global coarse bin of d = m - l (monotone in l; equal l share a bin).

@@ -1,267 +1,23 @@
-// sample_kernels.hip — the gfx950 token-selection kernels.
+// sample_kernels.hip — the general path (k_collect, k_final), the validation output
+// (k_probs) and the verify combine.
 //
-// Fast rows (greedy, min-p >= e^-8, or 0 < top-k <= 256) are resolved by one streaming
-// pass (k_scan) and one finalize (k_final): each chunk keeps its local candidates —
-// every token that could survive min-p/top-k given only the chunk's own maximum — and
-// the finalize resolves them exactly. General rows (top-p alone, no filter, very small
-// min-p, large top-k) add k_collect: from k_scan's 64-bin coarse histograms it derives
-// conservative bin bounds, collects the tokens of the undecided bins and sums the rest
-// exactly. k_final sorts the candidates in LDS by (l desc, id asc) and takes every
-// decision in fp64.
-#include "kernels.hpp"
+// General rows (top-p alone, no filter, very small min-p, large top-k) cannot bound their
+// candidates from a chunk's own maximum. k_collect derives conservative bin bounds from
+// k_stream's 64-bin coarse histograms, collects the tokens of the undecided bins and sums
+// the rest exactly; k_final sorts the candidates in LDS by (l desc, id asc) and takes every
+// decision in fp64. Rows whose candidates overflow either finalize are decided by k_final's
+// exact streaming resolution.
+#include "select.hpp"
 
 namespace strim {
 
 // ---------------------------------------------------------------------------------
 // shared helpers
 // ---------------------------------------------------------------------------------
-// Ladder rung of d >= 0: 0 for d == 0, else ceil(2 log2 d) + 13 clamped to [1, 31].
-// Monotone in d (equal d -> equal rung); used only to bound a chunk's top-k.
-__device__ __forceinline__ int ladder_rung(float d) {
-  if (!(d > 0.0f)) return 0;
-  if (!(d < 1e30f)) return 31;
-  const int r = (int)ceilf(2.0f * __log2f(d)) + 13;
-  return r < 1 ? 1 : (r > 31 ? 31 : r);
-}
-
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   const uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
   const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
   return ((uint64_t)hi << 32) | lo;
-}
-
-// Merge (t0, t1) into the pair (s0 >= s1) of fp32 proxy scores; ids break ties.
-__device__ __forceinline__ void top2_merge(float& s0, float& l0, int& i0, float& s1, float& l1,
-                                           int& i1, float t0, float tl0, int ti0, float t1,
-                                           float tl1, int ti1) {
-  auto better = [](float a, int ia, float b, int ib) {
-    return ia >= 0 && (ib < 0 || a > b || (a == b && ia < ib));
-  };
-  float cs[4] = {s0, s1, t0, t1}, cl[4] = {l0, l1, tl0, tl1};
-  int ci[4] = {i0, i1, ti0, ti1};
-  int bi = 0;
-#pragma unroll
-  for (int q = 1; q < 4; ++q)
-    if (better(cs[q], ci[q], cs[bi], ci[bi])) bi = q;
-  int si = bi == 0 ? 1 : 0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    if (q != bi && better(cs[q], ci[q], cs[si], ci[si])) si = q;
-  float ns0 = -INFINITY, nl0 = 0.f, ns1 = -INFINITY, nl1 = 0.f;
-  int ni0 = -1, ni1 = -1;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    if (q == bi) { ns0 = cs[q]; nl0 = cl[q]; ni0 = ci[q]; }
-    if (q == si) { ns1 = cs[q]; nl1 = cl[q]; ni1 = ci[q]; }
-  }
-  s0 = ns0; l0 = nl0; i0 = ni0;
-  s1 = ns1; l1 = nl1; i1 = ni1;
-}
-
-// Wave-then-block reduction of the two best (score, l, id); result in thread 0.
-template <int NT>
-__device__ __forceinline__ void block_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
-                                           int& i1, float* sf, int* si) {
-  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ts0 = __shfl_xor(s0, o, WAVE), tl0 = __shfl_xor(l0, o, WAVE);
-    const float ts1 = __shfl_xor(s1, o, WAVE), tl1 = __shfl_xor(l1, o, WAVE);
-    const int ti0 = __shfl_xor(i0, o, WAVE), ti1 = __shfl_xor(i1, o, WAVE);
-    top2_merge(s0, l0, i0, s1, l1, i1, ts0, tl0, ti0, ts1, tl1, ti1);
-  }
-  if (lane == 0) {
-    sf[4 * w + 0] = s0; sf[4 * w + 1] = l0; sf[4 * w + 2] = s1; sf[4 * w + 3] = l1;
-    si[2 * w + 0] = i0; si[2 * w + 1] = i1;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0)
-    for (int q = 1; q < NT / WAVE; ++q)
-      top2_merge(s0, l0, i0, s1, l1, i1, sf[4 * q], sf[4 * q + 1], si[2 * q], sf[4 * q + 2],
-                 sf[4 * q + 3], si[2 * q + 1]);
-}
-
-__device__ __forceinline__ bool row_nofilter(const RowParams& p, int V) {
-  return !(p.top_k > 0 && p.top_k < V) && !(p.min_p > 0.0f) && !(p.top_p < 1.0f);
-}
-
-// ---------------------------------------------------------------------------------
-// k_scan: the single streaming pass
-// ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(TPB) void k_scan(Args a) {
-  __shared__ uint32_t s_cnt[CHUNK];
-  __shared__ uint32_t s_hc[NCB];
-  __shared__ unsigned long long s_hm[NCB];
-  __shared__ uint32_t s_lad[32];
-  __shared__ float s_v[TPB / WAVE];
-  __shared__ int s_i[TPB / WAVE], s_n[TPB / WAVE], s_f[TPB / WAVE];
-  __shared__ double s_d[TPB / WAVE];
-  __shared__ int s_off[TPB / WAVE];
-  __shared__ float s_tf[4 * TPB / WAVE];
-  __shared__ int s_ti[2 * TPB / WAVE];
-
-  int r, c;
-  map_block(a, blockIdx.x, r, c);
-  int b, j;
-  row_bj(a, r, b, j);
-  const RowParams p = load_params(a, b, j);
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
-  const int c0 = c * CHUNK, i0 = c0 + t * EPT;
-  const bool topk_lad = p.cls == CLS_FAST && p.top_k > 0 && p.top_k < a.V;
-
-  float x[EPT];
-  load_tokens(a, r, i0, x);
-  if (p.pen) build_counts(a, b, j, c0, s_cnt);
-  float l[EPT];
-  bool nf = false;
-  process_tokens(a, r, i0, p, s_cnt + (i0 & (CHUNK - 1)), x, l, nf);
-
-  if (a.verify && j < a.k) {
-    const int d = a.drafts[(int64_t)b * a.k + j];
-    const int o = d - i0;
-    if (o >= 0 && o < EPT) {
-      float ld = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e)
-        if (e == o) ld = l[e];
-      a.s.rs[r].l_draft = ld;
-    }
-  }
-  if (c == 0 && t == 0) a.s.ncand[r] = 0u;
-
-  // chunk max (first id on ties), allowed count, non-finite flag
-  float mv = -INFINITY;
-  int mi = -1, n = 0;
-#pragma unroll
-  for (int e = 0; e < EPT; ++e)
-    if (l[e] > -INFINITY) {
-      ++n;
-      argmax_merge(mv, mi, l[e], i0 + e);
-    }
-  wave_argmax(mv, mi);
-  n = wave_sum(n);
-  const int f = __any(nf) ? 1 : 0;
-  if (topk_lad) s_lad[t & 31] = 0u;  // cleared before the barrier below
-  if (lane == 0) {
-    s_v[w] = mv;
-    s_i[w] = mi;
-    s_n[w] = n;
-    s_f[w] = f;
-  }
-  __syncthreads();
-  float m_w = s_v[0];
-  int a_w = s_i[0], n_w = s_n[0], f_w = s_f[0];
-#pragma unroll
-  for (int q = 1; q < TPB / WAVE; ++q) {
-    argmax_merge(m_w, a_w, s_v[q], s_i[q]);
-    n_w += s_n[q];
-    f_w |= s_f[q];
-  }
-  ChunkStat cs{m_w, a_w, n_w, f_w, 0.0, 0u, 0};
-  const bool live = n_w > 0 && !f_w;
-
-  if (p.cls == CLS_FAST && live) {
-    // Local candidates: every token that can pass min-p and top-k given m >= m_w.
-    const bool topk = p.top_k > 0 && p.top_k < a.V;
-    const bool minp = p.min_p > 0.0f;
-    const float dmp = minp ? (float)(-log((double)p.min_p)) * 1.000002f : INFINITY;
-    int rstar = 31;
-    if (topk) {
-      // counts per ladder rung (s_lad was cleared before the previous barrier)
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const float d = m_w - l[e];
-        if (l[e] > -INFINITY && d <= dmp) atomicAdd(&s_lad[ladder_rung(d)], 1u);
-      }
-      __syncthreads();
-      uint32_t cum = 0;
-#pragma unroll
-      for (int q = 0; q < 32; ++q) {
-        cum += s_lad[q];
-        if (cum >= (uint32_t)p.top_k && rstar == 31) rstar = q;
-      }
-    }
-    uint32_t sel = 0u;
-    int mycnt = 0;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      if (!(l[e] > -INFINITY)) continue;
-      const float d = m_w - l[e];
-      if (d <= dmp && (!topk || ladder_rung(d) <= rstar)) {
-        sel |= 1u << e;
-        ++mycnt;
-      }
-    }
-    int wtot;
-    const int wex = wave_excl_count(mycnt, &wtot);
-    if (lane == 0) s_off[w] = wtot;
-    __syncthreads();
-    int base = 0, total = 0;
-#pragma unroll
-    for (int q = 0; q < TPB / WAVE; ++q) {
-      if (q < w) base += s_off[q];
-      total += s_off[q];
-    }
-    if (total <= SLOT) {
-      int pos = base + wex;
-      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e)
-        if ((sel >> e) & 1u) dst[pos++] = Cand{l[e], i0 + e};
-    }
-    cs.nslot = total <= SLOT ? (uint32_t)total : (uint32_t)(SLOT + 1);
-  } else if (p.cls == CLS_GENERAL && live) {
-    // chunk sum exp(l - m_w) and a 64-bin coarse histogram of d_w = m_w - l
-    if (t < NCB) {
-      s_hc[t] = 0u;
-      s_hm[t] = 0ull;
-    }
-    __syncthreads();
-    double ssum = 0.0;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      if (!(l[e] > -INFINITY)) continue;
-      const float d = m_w - l[e];
-      const float wgt = expf(-d);
-      ssum += (double)wgt;
-      const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
-      atomicAdd(&s_hc[bb], 1u);
-      const unsigned long long fx = __float2ull_rn(wgt * FIX_SCALE_F);
-      if (fx) atomicAdd(&s_hm[bb], fx);
-    }
-    ssum = wave_sum(ssum);
-    if (lane == 0) s_d[w] = ssum;
-    __syncthreads();
-    double S = 0.0;
-#pragma unroll
-    for (int q = 0; q < TPB / WAVE; ++q) S += s_d[q];
-    cs.S = S;
-    if (t < NCB) {
-      const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
-      a.s.chc[o] = s_hc[t];
-      a.s.chm[o] = s_hm[t];
-    }
-    // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
-    if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) {
-      const uint64_t key = mix64(p.seed, p.position);
-      float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-      int id0 = -1, id1 = -1;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        if (!(l[e] > -INFINITY)) continue;
-        const int id = i0 + e;
-        const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
-                                : philox_uniform(key, (uint64_t)id);
-        top2_merge(s0, l0, id0, s1, l1, id1, l[e] + gumbel32(u), l[e], id, -INFINITY, 0.f, -1);
-      }
-      block_top2<TPB>(s0, l0, id0, s1, l1, id1, s_tf, s_ti);
-      if (t == 0) {
-        ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
-        pt.l0 = l0; pt.id0 = id0; pt.l1 = l1; pt.id1 = id1;
-      }
-    }
-  }
-  if (t == 0) a.s.cstat[(int64_t)r * a.s.wmax + c] = cs;
 }
 
 // ---------------------------------------------------------------------------------
@@ -441,7 +197,7 @@ __global__ __launch_bounds__(TPB) void k_collect(Args a) {
   __shared__ int s_ti[2 * TPB / WAVE];
 
   int r, c;
-  map_block(a, blockIdx.x, r, c);
+  map_block(r, c);
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);
@@ -609,46 +365,6 @@ __device__ void bitonic_sort(uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key) {
 #pragma unroll
   for (int q = 0; q < FIN_Q; ++q)
     if (q * FIN_T < n2) s_key[q * FIN_T + t] = k[q];
-  __syncthreads();
-}
-
-// Block argmax over (score desc, tie key asc); the winner's id lands in *out_id.
-__device__ void block_argmax_score(double sc, uint64_t tk, int id, double* s_sc, uint64_t* s_tk,
-                                   int* s_id, int* out_id) {
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
-  auto take = [](double& a, uint64_t& ak, int& ai, double b, uint64_t bk, int bi) {
-    if (bi >= 0 && (ai < 0 || b > a || (b == a && bk < ak))) { a = b; ak = bk; ai = bi; }
-  };
-#define STRIM_ARG_STEP(C) take(sc, tk, id, dpp_d<C>(sc), dpp_u64<C>(tk), dpp_i<C>(id))
-  STRIM_ARG_STEP(DPP_XOR1);
-  STRIM_ARG_STEP(DPP_XOR2);
-  STRIM_ARG_STEP(DPP_HALF_MIRROR);
-  STRIM_ARG_STEP(DPP_MIRROR);
-#undef STRIM_ARG_STEP
-  {
-    double bs = rl_d(sc, 0);
-    uint64_t bk = rl_u64(tk, 0);
-    int bi = rl_i(id, 0);
-    take(bs, bk, bi, rl_d(sc, 16), rl_u64(tk, 16), rl_i(id, 16));
-    take(bs, bk, bi, rl_d(sc, 32), rl_u64(tk, 32), rl_i(id, 32));
-    take(bs, bk, bi, rl_d(sc, 48), rl_u64(tk, 48), rl_i(id, 48));
-    sc = bs; tk = bk; id = bi;
-  }
-  __syncthreads();
-  if (lane == 0) { s_sc[w] = sc; s_tk[w] = tk; s_id[w] = id; }
-  __syncthreads();
-  if (t == 0) {
-    double bs = s_sc[0];
-    uint64_t btk = s_tk[0];
-    int bid = s_id[0];
-    for (int q = 1; q < FIN_T / WAVE; ++q) {
-      if (s_id[q] < 0) continue;
-      if (bid < 0 || s_sc[q] > bs || (s_sc[q] == bs && s_tk[q] < btk)) {
-        bs = s_sc[q]; btk = s_tk[q]; bid = s_id[q];
-      }
-    }
-    *out_id = bid;
-  }
   __syncthreads();
 }
 
@@ -1107,7 +823,7 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
             take(l[e], i0 + e, i0 + e, cand_sorted ? ckey(l[e], i0 + e) : (uint64_t)(i0 + e));
       });
     }
-    block_argmax_score(bsc, btk, bid, xs.dred, xs.ured, xs.ired, &s_x.token);
+    block_argmax_score<FIN_T>(bsc, btk, bid, xs.dred, xs.ured, xs.ired, &s_x.token);
     token = s_x.token >= 0 ? s_x.token : arg;
   }
   int acc = 0;
@@ -1154,6 +870,10 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   const int V = a.V;
   const bool verify_draft_row = a.verify && j < a.k;
   RowState* rsp = &a.s.rs[r];
+  // k_stream decided every row except general rows (PENDING) and rows whose candidates
+  // overflowed its finalize (EXACT)
+  const int phase = rsp->phase;
+  if (phase == PH_DONE) return;
 
   const RowStats st = merge_chunks<FIN_T>(a, r, s_v, s_i, s_n, s_f);
   int status = STRIM_OK;
@@ -1164,14 +884,12 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   }
   if (status == STRIM_OK && st.flags) status = STRIM_ENONFINITE;
   if (status == STRIM_OK && st.n == 0) status = STRIM_EEMPTY;
-  const bool tops = p.cls == CLS_GENERAL && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, V);
-  if (status == STRIM_OK && !p.greedy && p.cls == CLS_GENERAL && !tops) {
+  if (status == STRIM_OK && !p.greedy && phase == PH_PENDING) {
     if (t == 0) s_bd = rsp->bd;
     __syncthreads();
   }
   // rows the candidate path cannot hold go to the exact streaming resolution
-  bool exact = status == STRIM_OK && !p.greedy && p.cls == CLS_GENERAL && !tops &&
-               s_bd.mode == MODE_NONE;
+  bool exact = status == STRIM_OK && !p.greedy && (phase == PH_EXACT || s_bd.mode == MODE_NONE);
   auto finish = [&](int stt, int token, int accept, double sig, uint64_t lk) {
     if (t == 0) {
       rsp->status = stt;
@@ -1204,82 +922,10 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   const uint64_t pkey = mix64(p.seed, p.position);
   const int excl_id = verify_draft_row ? draft : -1;
 
-  // ---- unfiltered Gumbel rows: the chunks' two best tokens -------------------------
-  if (tops) {
-    // row mass: each chunk's contribution loaded in parallel, summed in chunk order
-    for (int cc = t; cc < W; cc += FIN_T) {
-      const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + cc];
-      s_w[cc] = cs.n > 0 ? cs.S * exp((double)cs.m - (double)m) : 0.0;
-    }
-    __syncthreads();
-    if (t == 0) {
-      double sig = 0.0;
-      for (int cc = 0; cc < W; ++cc) sig += s_w[cc];
-      s_dred[0] = sig;
-    }
-    __syncthreads();
-    const double sig = s_dred[0];
-    const double lse = log(sig);
-    double bsc = -INFINITY;
-    uint64_t btk = ~0ull;
-    int bid = -1;
-    for (int cc = t; cc < W; cc += FIN_T) {
-      const ChunkPart pt = a.s.part[(int64_t)r * a.s.wmax + cc];
-      for (int h = 0; h < 2; ++h) {
-        const int id = h == 0 ? pt.id0 : pt.id1;
-        const float l = h == 0 ? pt.l0 : pt.l1;
-        if (id < 0 || id == excl_id) continue;
-        const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
-                                : philox_uniform(pkey, (uint64_t)id);
-        const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
-        const double sc = base + gumbel64(u);
-        if (bid < 0 || sc > bsc || (sc == bsc && (uint64_t)id < btk)) {
-          bsc = sc; btk = (uint64_t)id; bid = id;
-        }
-      }
-    }
-    __syncthreads();
-    block_argmax_score(bsc, btk, bid, s_dred, s_ured, s_ired, &s_int[3]);
-    int token = s_int[3];
-    int acc = 0;
-    if (verify_draft_row) {
-      double w_d = 0.0;
-      if (rsp->l_draft > -INFINITY) w_d = exp((double)rsp->l_draft - (double)m);
-      const float ua = row_uniform(a, r, p, (int64_t)V);
-      acc = ((double)ua < w_d / sig) ? 1 : 0;
-      if (token < 0) token = st.arg;  // the draft is the only allowed token
-    }
-    finish(STRIM_OK, token, acc, sig, ~0ull);
-    return;
-  }
-
   if (!exact) do {
   // ---- gather candidates --------------------------------------------------------
   int n = 0;
-  const bool fast = p.cls == CLS_FAST;
-  if (fast) {
-    // chunk-order prefix of the local candidate counts (ids ascending overall)
-    for (int cc = t; cc < W && cc < 256; cc += FIN_T)
-      s_ns[cc] = a.s.cstat[(int64_t)r * a.s.wmax + cc].nslot;
-    __syncthreads();
-    if (t == 0) {
-      uint32_t acc = 0;
-      int over = W > 256 ? 1 : 0;
-      for (int cc = 0; cc < W && !over; ++cc) {
-        const uint32_t ns = s_ns[cc];
-        if (ns > (uint32_t)SLOT) over = 1;
-        s_pre[cc] = acc;
-        acc += ns;
-      }
-      s_int[0] = (over || acc > (uint32_t)CAP) ? -1 : (int)acc;
-    }
-    __syncthreads();
-    n = s_int[0];
-    if (n < 0) {
-      exact = true;
-      break;
-    }
-  } else {
+  {
     n = (int)a.s.ncand[r];
     if (n > CAP) {
       exact = true;
@@ -1313,31 +959,13 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   int n2 = 64;
   while (n2 < n) n2 <<= 1;
   uint64_t kk[FIN_Q];
-  if (fast) {
-    // slot entries of chunk cc land at s_pre[cc] + i; scatter into LDS, then load
-    for (int e = t; e < W * SLOT; e += FIN_T) {
-      const int cc = e / SLOT, i = e - cc * SLOT;
-      if ((uint32_t)i < s_ns[cc]) {
-        const Cand cd = a.s.slot[((int64_t)r * a.s.wmax + cc) * SLOT + i];
-        s_key[s_pre[cc] + i] = ckey(cd.l, cd.id);
-      }
-    }
-    __syncthreads();
 #pragma unroll
-    for (int q = 0; q < FIN_Q; ++q) {
-      const int idx = q * FIN_T + t;
-      kk[q] = idx < n ? s_key[idx] : ~0ull;
-    }
-    __syncthreads();
-  } else {
-#pragma unroll
-    for (int q = 0; q < FIN_Q; ++q) {
-      const int idx = q * FIN_T + t;
-      kk[q] = ~0ull;
-      if (idx < n) {
-        const Cand cd = a.s.cand[(int64_t)r * CAP + idx];
-        kk[q] = ckey(cd.l, cd.id);
-      }
+  for (int q = 0; q < FIN_Q; ++q) {
+    const int idx = q * FIN_T + t;
+    kk[q] = ~0ull;
+    if (idx < n) {
+      const Cand cd = a.s.cand[(int64_t)r * CAP + idx];
+      kk[q] = ckey(cd.l, cd.id);
     }
   }
   if (t == 0) s_kth = -INFINITY;
@@ -1369,7 +997,6 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     cb = 0u;
     pb = 0.0;
     kb = 0.0;
-    if (fast) return;
 #pragma unroll
     for (int s = 0; s < NSEG; ++s)
       if (s_bd.seg_lo[s] <= s_bd.seg_hi[s] && s_bd.seg_hi[s] < g) {
@@ -1395,7 +1022,6 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   __syncthreads();
   const float kth = s_kth;
   double seg_pre = 0.0, seg_kept = 0.0;
-  if (!fast)
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) {
       if (s_segk[s] >= 1) seg_pre += s_segm[s];
@@ -1472,11 +1098,8 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     const float ld = rsp->l_draft;
     key_d = ckey(ld, draft);
     bool kept_d;
-    if (fast) kept_d = last_key != 0ull && key_d <= last_key;
-    else {
-      const int g = gbin(m - ld);
-      kept_d = in_rng(s_bd, g) ? (last_key != 0ull && key_d <= last_key) : (g < s_bd.s);
-    }
+    const int g = gbin(m - ld);
+    kept_d = in_rng(s_bd, g) ? (last_key != 0ull && key_d <= last_key) : (g < s_bd.s);
     if (kept_d) w_d = exp((double)ld - (double)m);
   }
 
@@ -1505,7 +1128,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     int bp = block_min<FIN_T>(best, s_ired);
     if (bp >= n_keep) {
       // rounding pushed the target past the last collected kept token
-      const bool all_collected = fast || s_bd.mode == MODE_A;
+      const bool all_collected = s_bd.mode == MODE_A;
       bp = (all_collected && n_keep > 0) ? n_keep - 1 : -1;
       if (bp >= 0 && (int)(uint32_t)s_key[bp] == excl_id) bp = bp > 0 ? bp - 1 : -1;
     }
@@ -1541,7 +1164,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
       const uint64_t tk = cand_sorted ? key : (uint64_t)id;
       if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) { bsc = sc; btk = tk; bid = id; }
     }
-    if (!fast && s_bd.mode == MODE_B) {
+    if (s_bd.mode == MODE_B) {
       for (int cc = t; cc < W; cc += FIN_T) {
         const ChunkPart pt = a.s.part[(int64_t)r * a.s.wmax + cc];
         for (int h = 0; h < 2; ++h) {
@@ -1557,7 +1180,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
         }
       }
     }
-    block_argmax_score(bsc, btk, bid, s_dred, s_ured, s_ired, &s_int[3]);
+    block_argmax_score<FIN_T>(bsc, btk, bid, s_dred, s_ured, s_ired, &s_int[3]);
     token = s_int[3];
     if (token < 0) token = n_keep > 0 ? (int)(uint32_t)s_key[0] : -1;  // every score -inf
     if (token < 0) {
@@ -1613,7 +1236,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
 __global__ __launch_bounds__(TPB) void k_probs(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
   int r, c;
-  map_block(a, blockIdx.x, r, c);
+  map_block(r, c);
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);

@@ -1,0 +1,518 @@
+// select.hpp — workgroup-level building blocks of the finalize steps: block scans and
+// reductions, top-2 merges, the ladder bound of a chunk's top-k, rank and bitonic sorts
+// of order keys in LDS, and the radix select of the k-th smallest key.
+//
+// Every helper is called by all NT threads of the workgroup (it contains barriers).
+// Floating-point reductions use a fixed combination order, so results do not depend on
+// scheduling.
+#pragma once
+
+#include "kernels.hpp"
+
+namespace strim {
+
+// Ladder rung of d >= 0: 0 for d == 0, else ceil(4 log2 d) + 29 clamped to [1, 63].
+// Monotone in d (equal d -> equal rung), width ratio 2^(1/4); bounds a chunk's top-k.
+constexpr int NRUNG = 64;
+__device__ __forceinline__ int ladder_rung(float d) {
+  if (!(d > 0.0f)) return 0;
+  if (!(d < 1e30f)) return NRUNG - 1;
+  const int r = (int)ceilf(4.0f * __log2f(d)) + 29;
+  return r < 1 ? 1 : (r > NRUNG - 1 ? NRUNG - 1 : r);
+}
+
+__device__ __forceinline__ bool row_nofilter(const RowParams& p, int V) {
+  return !(p.top_k > 0 && p.top_k < V) && !(p.min_p > 0.0f) && !(p.top_p < 1.0f);
+}
+
+// Exclusive prefix and wave total of per-lane counts in [0, 31] via ballots.
+__device__ __forceinline__ int wave_excl_count32(int c, int* total) {
+  int ex = 0, tot = 0;
+#pragma unroll
+  for (int bit = 0; bit < 5; ++bit) {
+    const uint64_t m = __ballot((c >> bit) & 1);
+    ex += lanes_below(m) << bit;
+    tot += __popcll(m) << bit;
+  }
+  *total = tot;
+  return ex;
+}
+
+// Block exclusive scan of one uint32 per thread; *total gets the sum. scratch >= NT/64.
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* scratch,
+                                                        uint32_t* total) {
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  uint32_t inc = v;
+  // Hillis-Steele within the wave on shuffles (integer: order does not matter)
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const uint32_t u = (uint32_t)__shfl_up((int)inc, o, WAVE);
+    if (lane >= o) inc += u;
+  }
+  if (lane == WAVE - 1) scratch[w] = inc;
+  __syncthreads();
+  uint32_t base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < NT / WAVE; ++i) {
+    const uint32_t s = scratch[i];
+    if (i < w) base += s;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return base + inc - v;
+}
+
+template <int NT>
+__device__ __forceinline__ int block_or(int v, int* scratch) {
+  v = wave_or_i(v);
+  if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x / WAVE] = v;
+  __syncthreads();
+  int b = 0;
+#pragma unroll
+  for (int q = 0; q < NT / WAVE; ++q) b |= scratch[q];
+  __syncthreads();
+  return b;
+}
+
+template <int NT>
+__device__ __forceinline__ uint64_t block_or_u64(uint64_t v, uint64_t* scratch) {
+  const uint32_t lo = (uint32_t)wave_or_i((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)wave_or_i((int)(uint32_t)(v >> 32));
+  if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x / WAVE] = ((uint64_t)hi << 32) | lo;
+  __syncthreads();
+  uint64_t b = 0;
+#pragma unroll
+  for (int q = 0; q < NT / WAVE; ++q) b |= scratch[q];
+  __syncthreads();
+  return b;
+}
+
+template <int NT>
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
+    const uint64_t u = ((uint64_t)hi << 32) | lo;
+    v = u > v ? u : v;
+  }
+  if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x / WAVE] = v;
+  __syncthreads();
+  uint64_t b = 0;
+#pragma unroll
+  for (int q = 0; q < NT / WAVE; ++q) b = scratch[q] > b ? scratch[q] : b;
+  __syncthreads();
+  return b;
+}
+
+// Block sum of one double per thread in a fixed order (deterministic).
+template <int NT>
+__device__ __forceinline__ double block_sum_f64(double v, double* scratch) {
+  v = wave_sum(v);
+  if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x / WAVE] = v;
+  __syncthreads();
+  double s = 0.0;
+#pragma unroll
+  for (int q = 0; q < NT / WAVE; ++q) s += scratch[q];
+  __syncthreads();
+  return s;
+}
+
+// Merge (t0, t1) into the pair (s0 >= s1) of fp32 proxy scores; ids break ties.
+__device__ __forceinline__ void top2_merge(float& s0, float& l0, int& i0, float& s1, float& l1,
+                                           int& i1, float t0, float tl0, int ti0, float t1,
+                                           float tl1, int ti1) {
+  auto better = [](float a, int ia, float b, int ib) {
+    return ia >= 0 && (ib < 0 || a > b || (a == b && ia < ib));
+  };
+  float cs[4] = {s0, s1, t0, t1}, cl[4] = {l0, l1, tl0, tl1};
+  int ci[4] = {i0, i1, ti0, ti1};
+  int bi = 0;
+#pragma unroll
+  for (int q = 1; q < 4; ++q)
+    if (better(cs[q], ci[q], cs[bi], ci[bi])) bi = q;
+  int si = bi == 0 ? 1 : 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (q != bi && better(cs[q], ci[q], cs[si], ci[si])) si = q;
+  float ns0 = -INFINITY, nl0 = 0.f, ns1 = -INFINITY, nl1 = 0.f;
+  int ni0 = -1, ni1 = -1;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (q == bi) { ns0 = cs[q]; nl0 = cl[q]; ni0 = ci[q]; }
+    if (q == si) { ns1 = cs[q]; nl1 = cl[q]; ni1 = ci[q]; }
+  }
+  s0 = ns0; l0 = nl0; i0 = ni0;
+  s1 = ns1; l1 = nl1; i1 = ni1;
+}
+
+// Wave-then-block reduction of the two best (score, l, id); result in thread 0.
+template <int NT>
+__device__ __forceinline__ void block_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
+                                           int& i1, float* sf, int* si) {
+  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ts0 = __shfl_xor(s0, o, WAVE), tl0 = __shfl_xor(l0, o, WAVE);
+    const float ts1 = __shfl_xor(s1, o, WAVE), tl1 = __shfl_xor(l1, o, WAVE);
+    const int ti0 = __shfl_xor(i0, o, WAVE), ti1 = __shfl_xor(i1, o, WAVE);
+    top2_merge(s0, l0, i0, s1, l1, i1, ts0, tl0, ti0, ts1, tl1, ti1);
+  }
+  if (lane == 0) {
+    sf[4 * w + 0] = s0; sf[4 * w + 1] = l0; sf[4 * w + 2] = s1; sf[4 * w + 3] = l1;
+    si[2 * w + 0] = i0; si[2 * w + 1] = i1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int q = 1; q < NT / WAVE; ++q)
+      top2_merge(s0, l0, i0, s1, l1, i1, sf[4 * q], sf[4 * q + 1], si[2 * q], sf[4 * q + 2],
+                 sf[4 * q + 3], si[2 * q + 1]);
+}
+
+// Block argmax over (score desc, tie key asc); the winner's id lands in *out_id (-1 when
+// no thread holds a candidate).
+template <int NT>
+__device__ void block_argmax_score(double sc, uint64_t tk, int id, double* s_sc, uint64_t* s_tk,
+                                   int* s_id, int* out_id) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  auto take = [](double& a, uint64_t& ak, int& ai, double b, uint64_t bk, int bi) {
+    if (bi >= 0 && (ai < 0 || b > a || (b == a && bk < ak))) { a = b; ak = bk; ai = bi; }
+  };
+#define STRIM_ARG_STEP(C) take(sc, tk, id, dpp_d<C>(sc), dpp_u64<C>(tk), dpp_i<C>(id))
+  STRIM_ARG_STEP(DPP_XOR1);
+  STRIM_ARG_STEP(DPP_XOR2);
+  STRIM_ARG_STEP(DPP_HALF_MIRROR);
+  STRIM_ARG_STEP(DPP_MIRROR);
+#undef STRIM_ARG_STEP
+  {
+    double bs = rl_d(sc, 0);
+    uint64_t bk = rl_u64(tk, 0);
+    int bi = rl_i(id, 0);
+    take(bs, bk, bi, rl_d(sc, 16), rl_u64(tk, 16), rl_i(id, 16));
+    take(bs, bk, bi, rl_d(sc, 32), rl_u64(tk, 32), rl_i(id, 32));
+    take(bs, bk, bi, rl_d(sc, 48), rl_u64(tk, 48), rl_i(id, 48));
+    sc = bs; tk = bk; id = bi;
+  }
+  __syncthreads();
+  if (lane == 0) { s_sc[w] = sc; s_tk[w] = tk; s_id[w] = id; }
+  __syncthreads();
+  if (t == 0) {
+    double bs = s_sc[0];
+    uint64_t btk = s_tk[0];
+    int bid = s_id[0];
+    for (int q = 1; q < NT / WAVE; ++q) {
+      if (s_id[q] < 0) continue;
+      if (bid < 0 || s_sc[q] > bs || (s_sc[q] == bs && s_tk[q] < btk)) {
+        bs = s_sc[q]; btk = s_tk[q]; bid = s_id[q];
+      }
+    }
+    *out_id = bid;
+  }
+  __syncthreads();
+}
+
+// Ascending sort of the n unique keys s_key[0, n), n <= NT: each thread ranks one key
+// by counting the smaller ones (broadcast LDS reads), then scatters it.
+template <int NT>
+__device__ __forceinline__ void rank_sort(uint64_t* s_key, int n) {
+  const int t = threadIdx.x;
+  const uint64_t k0 = t < n ? s_key[t] : ~0ull;
+  uint32_t rank = 0;
+  int jj = 0;
+  for (; jj + 4 <= n; jj += 4)
+    rank += (uint32_t)(s_key[jj] < k0) + (uint32_t)(s_key[jj + 1] < k0) +
+            (uint32_t)(s_key[jj + 2] < k0) + (uint32_t)(s_key[jj + 3] < k0);
+  for (; jj < n; ++jj) rank += (uint32_t)(s_key[jj] < k0);
+  __syncthreads();
+  if (t < n) s_key[rank] = k0;
+  __syncthreads();
+}
+
+// Ascending bitonic sort of s_key[0, n) in LDS, padded with ~0 up to the next power of
+// two n2 (s_key must hold n2 entries). One compare-exchange pair per thread per step.
+template <int NT>
+__device__ __forceinline__ void bitonic_sort_lds(uint64_t* s_key, int n) {
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (int i = n + (int)threadIdx.x; i < n2; i += NT) s_key[i] = ~0ull;
+  __syncthreads();
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int pidx = threadIdx.x; pidx < n2 / 2; pidx += NT) {
+        const int lo = 2 * pidx - (pidx & (stride - 1));
+        const int hi = lo + stride;
+        const uint64_t a = s_key[lo], b = s_key[hi];
+        const bool asc = (lo & size) == 0;
+        if ((a > b) == asc) {
+          s_key[lo] = b;
+          s_key[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// The k-th smallest (k >= 1) of the keys a thread holds in kk[0, Q) (~0 = empty), by an
+// MSD radix select over 8-bit digits starting at the highest bit where the keys differ.
+// `ref` is any present key (the same in every thread). s_hist holds 256 counters,
+// s_u64 >= NT/64 + 4 entries, s_int >= 4. Keys are unique; the caller guarantees at
+// least k present keys.
+template <int NT, int Q>
+__device__ uint64_t radix_select_kth(const uint64_t (&kk)[Q], uint64_t ref, uint32_t k,
+                                     uint32_t* s_hist, uint64_t* s_u64, int* s_int) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1);
+  uint64_t diff = 0ull;
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+    if (kk[q] != ~0ull) diff |= kk[q] ^ ref;
+  diff = block_or_u64<NT>(diff, s_u64);
+  if (diff == 0ull) return ref;  // a single key
+  const int hb = 63 - __clzll((long long)diff);
+  uint64_t pmask = hb == 63 ? 0ull : ~((2ull << hb) - 1ull);
+  uint64_t prefix = ref & pmask;
+  int shift = hb >= 7 ? hb - 7 : 0;
+  uint32_t need = k;
+  for (;;) {
+    for (int i = t; i < 256; i += NT) s_hist[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+      if (kk[q] != ~0ull && (kk[q] & pmask) == prefix)
+        atomicAdd(&s_hist[(uint32_t)(kk[q] >> shift) & 255u], 1u);
+    __syncthreads();
+    if (t < WAVE) {
+      // lane owns digits 4*lane .. 4*lane+3
+      const uint32_t h0 = s_hist[4 * lane], h1 = s_hist[4 * lane + 1], h2 = s_hist[4 * lane + 2],
+                     h3 = s_hist[4 * lane + 3];
+      const uint32_t own = h0 + h1 + h2 + h3;
+      uint32_t inc = own;
+#pragma unroll
+      for (int o = 1; o < WAVE; o <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)inc, o, WAVE);
+        if (lane >= o) inc += u;
+      }
+      uint32_t cum = inc - own;
+      const uint32_t hs[4] = {h0, h1, h2, h3};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (cum < need && need <= cum + hs[e]) {
+          s_int[0] = 4 * lane + e;
+          s_int[1] = (int)cum;
+          s_int[2] = (int)hs[e];
+        }
+        cum += hs[e];
+      }
+    }
+    __syncthreads();
+    const int dsel = s_int[0];
+    const uint32_t below = (uint32_t)s_int[1], cnt = (uint32_t)s_int[2];
+    __syncthreads();
+    need -= below;
+    prefix = (prefix & ~(255ull << shift)) | ((uint64_t)dsel << shift);
+    pmask |= 255ull << shift;
+    if (cnt == need) {
+      // every key of the bucket is selected: the k-th is the bucket's largest
+      uint64_t mx = 0ull;
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+        if (kk[q] != ~0ull && (kk[q] & pmask) == prefix && kk[q] > mx) mx = kk[q];
+      return block_max_u64<NT>(mx, s_u64);
+    }
+    if (shift == 0) return prefix;
+    shift = shift >= 8 ? shift - 8 : 0;
+  }
+}
+
+}  // namespace strim
+
+// ---------------------------------------------------------------------------------
+// single-wave helpers (a 64-thread workgroup: no barriers between its steps)
+// ---------------------------------------------------------------------------------
+namespace strim {
+
+// Orders the LDS accesses of one wave around this point (other waves of the workgroup
+// may have exited, so no workgroup barrier is used). A wave's LDS instructions execute
+// in issue order; the fences keep the compiler from moving accesses across.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, WAVE);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64v(uint64_t v, int o) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, WAVE);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Exclusive prefix over the wave (integer: exact); *total = wave sum.
+__device__ __forceinline__ uint32_t wave_excl_scan_u32(uint32_t v, uint32_t* total) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  uint32_t inc = v;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const uint32_t u = (uint32_t)__shfl_up((int)inc, o, WAVE);
+    if (lane >= o) inc += u;
+  }
+  *total = (uint32_t)__shfl((int)inc, WAVE - 1, WAVE);
+  return inc - v;
+}
+
+// Exclusive prefix of doubles over the wave in a fixed association order
+// (deterministic); *total = wave sum.
+__device__ __forceinline__ double wave_excl_scan_f64(double v, double* total) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const double inc = wave_incl_scan(v);
+  *total = rl_d(inc, WAVE - 1);
+  const uint64_t bits = (uint64_t)__double_as_longlong(inc);
+  const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)bits, 1, WAVE);
+  const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(bits >> 32), 1, WAVE);
+  return lane == 0 ? 0.0 : __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+__device__ __forceinline__ uint64_t wave_or_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)wave_or_i((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)wave_or_i((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t u = shfl_xor_u64v(v, o);
+    v = u > v ? u : v;
+  }
+  return v;
+}
+
+// Wave argmax over (score desc, tie key asc); returns the winner's id (-1 if none),
+// the same in every lane.
+__device__ __forceinline__ int wave_argmax_score(double sc, uint64_t tk, int id) {
+  auto take = [](double& a, uint64_t& ak, int& ai, double b, uint64_t bk, int bi) {
+    if (bi >= 0 && (ai < 0 || b > a || (b == a && bk < ak))) { a = b; ak = bk; ai = bi; }
+  };
+#define STRIM_ARG_STEP(C) take(sc, tk, id, dpp_d<C>(sc), dpp_u64<C>(tk), dpp_i<C>(id))
+  STRIM_ARG_STEP(DPP_XOR1);
+  STRIM_ARG_STEP(DPP_XOR2);
+  STRIM_ARG_STEP(DPP_HALF_MIRROR);
+  STRIM_ARG_STEP(DPP_MIRROR);
+#undef STRIM_ARG_STEP
+  double bs = rl_d(sc, 0);
+  uint64_t bk = rl_u64(tk, 0);
+  int bi = rl_i(id, 0);
+  take(bs, bk, bi, rl_d(sc, 16), rl_u64(tk, 16), rl_i(id, 16));
+  take(bs, bk, bi, rl_d(sc, 32), rl_u64(tk, 32), rl_i(id, 32));
+  take(bs, bk, bi, rl_d(sc, 48), rl_u64(tk, 48), rl_i(id, 48));
+  return bi;
+}
+
+// Ascending bitonic sort of one key per lane (~0 = empty sorts last).
+__device__ __forceinline__ uint64_t wave_sort_u64(uint64_t k) {
+  const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+  for (int size = 2; size <= WAVE; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t o = shfl_xor_u64v(k, stride);
+      const bool asc = (lane & size) == 0;
+      const bool lower = (lane & stride) == 0;
+      const uint64_t lo = k < o ? k : o, hi = k < o ? o : k;
+      k = (lower == asc) ? lo : hi;
+    }
+  return k;
+}
+
+// Ascending bitonic sort of key[0, n) in LDS by one wave (key holds the next power of
+// two entries; padding with ~0).
+__device__ __forceinline__ void wave_sort_lds(uint64_t* key, int n) {
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  const int lane = threadIdx.x & (WAVE - 1);
+  for (int i = n + lane; i < n2; i += WAVE) key[i] = ~0ull;
+  wave_sync();
+  for (int size = 2; size <= n2; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int pidx = lane; pidx < n2 / 2; pidx += WAVE) {
+        const int lo = 2 * pidx - (pidx & (stride - 1));
+        const int hi = lo + stride;
+        const uint64_t x = key[lo], y = key[hi];
+        const bool asc = (lo & size) == 0;
+        if ((x > y) == asc) {
+          key[lo] = y;
+          key[hi] = x;
+        }
+      }
+      wave_sync();
+    }
+}
+
+// The k-th smallest (k >= 1) of the n unique keys key[0, n) in LDS, by an MSD radix
+// select over 8-bit digits from the highest bit where the keys differ. One wave; hist
+// holds 256 counters. The caller guarantees n >= k.
+__device__ uint64_t wave_radix_kth(const uint64_t* key, int n, uint32_t k, uint32_t* hist) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const uint64_t ref = key[0];
+  uint64_t diff = 0ull;
+  for (int i = lane; i < n; i += WAVE) diff |= key[i] ^ ref;
+  diff = wave_or_u64(diff);
+  if (diff == 0ull) return ref;
+  const int hb = 63 - __clzll((long long)diff);
+  uint64_t pmask = hb == 63 ? 0ull : ~((2ull << hb) - 1ull);
+  uint64_t prefix = ref & pmask;
+  int shift = hb >= 7 ? hb - 7 : 0;
+  uint32_t need = k;
+  for (;;) {
+    *(uint4*)&hist[4 * lane] = make_uint4(0u, 0u, 0u, 0u);
+    wave_sync();
+    for (int i = lane; i < n; i += WAVE) {
+      const uint64_t kv = key[i];
+      if ((kv & pmask) == prefix) atomicAdd(&hist[(uint32_t)(kv >> shift) & 255u], 1u);
+    }
+    wave_sync();
+    const uint4 h = *(const uint4*)&hist[4 * lane];
+    const uint32_t own = h.x + h.y + h.z + h.w;
+    uint32_t tot;
+    uint32_t cum = wave_excl_scan_u32(own, &tot);
+    const uint32_t hs[4] = {h.x, h.y, h.z, h.w};
+    int dl = -1;
+    uint32_t bl = 0u, cl = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (dl < 0 && cum < need && need <= cum + hs[e]) {
+        dl = 4 * lane + e;
+        bl = cum;
+        cl = hs[e];
+      }
+      cum += hs[e];
+    }
+    const uint64_t who = __ballot(dl >= 0);
+    const int src = (int)__ffsll((long long)who) - 1;
+    const int dsel = __shfl(dl, src, WAVE);
+    const uint32_t below = (uint32_t)__shfl((int)bl, src, WAVE);
+    const uint32_t cnt = (uint32_t)__shfl((int)cl, src, WAVE);
+    wave_sync();
+    need -= below;
+    prefix = (prefix & ~(255ull << shift)) | ((uint64_t)dsel << shift);
+    pmask |= 255ull << shift;
+    if (cnt == need) {
+      // every key of the bucket is selected: the k-th is the bucket's largest
+      uint64_t mx = 0ull;
+      for (int i = lane; i < n; i += WAVE) {
+        const uint64_t kv = key[i];
+        if ((kv & pmask) == prefix && kv > mx) mx = kv;
+      }
+      return wave_max_u64(mx);
+    }
+    if (shift == 0) return prefix;
+    shift = shift >= 8 ? shift - 8 : 0;
+  }
+}
+
+}  // namespace strim
