@@ -3,13 +3,22 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-A step is one strim_sample call over one batch of synthetic logits already resident
-in HBM. The headline workload is configuration 2 (B=8, V=151,936 bf16, per-row
-T / top-k / top-p, min-p 0.05, presence/frequency penalties over a 4,096-token history,
-one uniform per row). Inputs rotate through a pool larger than 512 MB (twice the
-256 MB Infinity Cache) so the streaming kernels read HBM, not the cache. The B=64
-stress configuration (5) is reported beside it. Per-kernel durations come from HIP
-events recorded on the launch stream over a second pass of the same steps.
+A step is one strim_sample call over one batch of synthetic logits already resident in
+HBM. The headline workload is configuration 2 of the benchmark table: B=8, V=151,936
+bf16, per-row T / top-k / top-p, min-p 0.05, presence/frequency penalties over a
+4,096-token history, one uniform per row (icdf draw). Inputs rotate through a pool
+larger than 512 MB (twice the 256 MB Infinity Cache), so the streaming kernel reads HBM.
+
+Timing:
+  value        K steps captured once in a HIP graph (the way a decode loop launches a
+               fixed step) and replayed: wall clock between two device synchronisations,
+               divided by K. Host launch overhead is outside the measurement.
+  kernel_us    per-kernel durations from HIP events recorded on the launch stream around
+               every kernel, with the steps queued behind a bounded GPU sleep so they run
+               back to back; the roofline uses the streaming kernel's average.
+  eager_us     the same steps launched one by one from Python (host-bound reference).
+The B=64 stress configuration (5) is reported beside it (rows/s, roofline), and the CPU
+oracle (a C port of the reference sampler, OpenMP over rows) on the host cores.
 
 Prints ONE JSON line on stdout; diagnostics go to stderr.
 """
@@ -36,7 +45,8 @@ def log(*a):
 
 
 def make_pool_cfg2(torch, dev, n_sets, B, V, H, seed=2):
-    """Distinct cfg2-shaped inputs: N(0, 2.5^2) + Zipf(1.1) rank bias over a permutation."""
+    """Distinct cfg2-shaped inputs: N(0, 2.5^2) + Zipf(1.1) rank bias over a permutation,
+    Zipf-distributed histories, one uniform per row."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     rng = np.random.default_rng(seed)
@@ -45,7 +55,7 @@ def make_pool_cfg2(torch, dev, n_sets, B, V, H, seed=2):
     bias[perm] = -1.1 * torch.log(torch.arange(V, device=dev, dtype=torch.float32) + 1.0)
     xs, hs, ns = [], [], []
     perm_np = perm.cpu().numpy()
-    for s in range(n_sets):
+    for _ in range(n_sets):
         x = torch.randn(B, V, device=dev, generator=g) * 2.5 + bias
         xs.append(x.to(torch.bfloat16).contiguous())
         r = rng.zipf(1.1, size=(B, H)).astype(np.int64) - 1
@@ -55,12 +65,14 @@ def make_pool_cfg2(torch, dev, n_sets, B, V, H, seed=2):
 
 
 def make_pool_cfg5(torch, dev, n_sets, B, V, H, seed=5):
+    """cfg5-shaped inputs: 70 % rows N(0, 2^2), 30 % rows with one +20 logit; uniform
+    2,048-token histories; 5 %-density allow masks."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     from strim_amd.ops import pack_mask
 
     xs, hs, ms = [], [], []
-    for s in range(n_sets):
+    for _ in range(n_sets):
         x = torch.randn(B, V, device=dev, generator=g) * 2.0
         dom = torch.rand(B, device=dev, generator=g) < 0.3
         col = torch.randint(0, V, (B,), device=dev, generator=g)
@@ -71,23 +83,60 @@ def make_pool_cfg5(torch, dev, n_sets, B, V, H, seed=5):
     return xs, hs, ms
 
 
-def time_steps(torch, fn, n_sets, steps, warmup):
-    for i in range(warmup):
-        fn(i % n_sets)
+def graph_us_per_step(torch, calls, steps, warmup):
+    """Capture `calls` (one step each) into a HIP graph; replay until `steps` steps ran;
+    wall clock between device synchronisations / steps."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls[: min(3, len(calls))]:  # warm the launch path outside capture
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    reps = max(1, (steps + len(calls) - 1) // len(calls))
+    for _ in range(max(1, warmup // len(calls))):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    return el * 1e6 / (reps * len(calls)), reps * len(calls), g
+
+
+def kernel_times(torch, ctx, calls, steps, window=96, sleep_cycles=30_000_000):
+    """Per-kernel average durations (µs) from HIP events around each launch, the steps
+    queued behind a bounded GPU sleep so they execute back to back."""
+    tot = {}
+    done = 0
+    while done < steps:
+        n = min(window, steps - done)
+        torch.cuda.synchronize()
+        ctx.profile_begin(8 * n + 8)
+        torch.cuda._sleep(sleep_cycles)
+        for i in range(n):
+            calls[(done + i) % len(calls)]()
+        prof = ctx.profile_end()
+        for k, (ms, cnt) in prof.items():
+            a = tot.setdefault(k, [0.0, 0])
+            a[0] += ms
+            a[1] += cnt
+        done += n
+    return {k: (v[0] * 1e3 / v[1], v[1]) for k, v in tot.items() if v[1]}
+
+
+def eager_us_per_step(torch, calls, steps):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        fn(i % n_sets)
+        calls[i % len(calls)]()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
-
-
-def kernel_times(ctx, torch, fn, n_sets, steps):
-    ctx.profile_begin(6 * steps + 16)
-    for i in range(steps):
-        fn(i % n_sets)
-    prof = ctx.profile_end()
-    return {k: (ms / n * 1e3 if n else 0.0, n) for k, (ms, n) in prof.items()}
+    return (time.perf_counter() - t0) * 1e6 / steps
 
 
 def cpu_baseline_cfg2(seconds: float):
@@ -115,30 +164,75 @@ def cpu_baseline_cfg2(seconds: float):
                       f"OpenMP over rows"}
 
 
+def roofline(bytes_per_launch, us):
+    gbs = bytes_per_launch / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_stream",
+            "bytes_per_launch": int(bytes_per_launch), "us_per_launch": round(us, 3)}
+
+
+def pmc_pass(torch, ops, W, dev, steps, pool_mb):
+    """A short eager run for hardware-counter passes: cfg2 steps, cfg5 steps, then one
+    copy of 256 MiB (read 256 MiB + write 256 MiB) to scale FETCH_SIZE / WRITE_SIZE."""
+    V = W.V_DEFAULT
+    ctx = ops.Context(0, max_rows=64, max_vocab=V)
+    n2 = int(np.ceil(pool_mb * 2**20 / (8 * V * 2 + 8 * 4096 * 4)))
+    xs, hs, ns = make_pool_cfg2(torch, dev, n2, 8, V, 4096)
+    hl = torch.full((8,), 4096, dtype=torch.int32, device=dev)
+    p2 = W.cfg2()["params"]
+    calls = [ctx.bind_sample(xs[i], p2, history=hs[i], history_len=hl, noise=ns[i])
+             for i in range(n2)]
+    for i in range(steps):
+        calls[i % n2]()
+    torch.cuda.synchronize()
+    del calls, xs, hs, ns
+    n5 = int(np.ceil(pool_mb * 2**20 / (64 * V * 2 + 64 * 4748 * 4 + 64 * 2048 * 4)))
+    xs5, hs5, ms5 = make_pool_cfg5(torch, dev, n5, 64, V, 2048)
+    hl5 = torch.full((64,), 2048, dtype=torch.int32, device=dev)
+    p5 = W.cfg5()["params"]
+    calls5 = [ctx.bind_sample(xs5[i], p5, mask=ms5[i], history=hs5[i], history_len=hl5)
+              for i in range(n5)]
+    for i in range(steps):
+        calls5[i % n5]()
+    torch.cuda.synchronize()
+    src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    ctx.close()
+    print(f"pmc pass: {steps} cfg2 steps, {steps} cfg5 steps, one 256 MiB copy", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--pool-mb", type=float, default=600.0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b64", action="store_true")
+    ap.add_argument("--pmc-pass", type=int, default=0, metavar="N",
+                    help="profiling pass for rocprofv3 counters: N eager steps of cfg2 and "
+                         "cfg5 over a pool, then a 256 MiB device copy (the calibration "
+                         "kernel for FETCH_SIZE / WRITE_SIZE); prints a summary line only")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the token "
-              "selection shards over rows with no communication); run with --gpus 1.",
+        print("bench.py measures one GPU: every box here has one GPU, and this path shards "
+              "over rows with no communication (see the sharding design); run --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
     import torch
 
-    from strim_amd import _native as N
     from strim_amd import ops
     from strim_amd import workloads as W
 
     dev = torch.device("cuda:0")
+    if args.pmc_pass:
+        pmc_pass(torch, ops, W, dev, args.pmc_pass, args.pool_mb)
+        return
     V, B, H = W.V_DEFAULT, 8, 4096
     per_set = B * V * 2 + B * H * 4 + B * 8
     n_sets = int(np.ceil(args.pool_mb * 2**20 / per_set))
@@ -147,76 +241,48 @@ def main():
     params = W.cfg2()["params"]
     hl = torch.full((B,), H, dtype=torch.int32, device=dev)
     ctx = ops.Context(0, max_rows=64, max_vocab=V)
-    out_ids = torch.empty(B, dtype=torch.int32, device=dev)
-    out_st = torch.empty(B, dtype=torch.int32, device=dev)
-
-    def step2(i):
-        ctx.sample(xs[i], params, history=hs[i], history_len=hl, noise_mode=N.NOISE_ICDF,
-                   noise=ns[i], out_ids=out_ids, out_status=out_st)
-
-    ms2 = time_steps(torch, step2, n_sets, args.steps, args.warmup)
-    st = out_st.cpu().numpy()
+    calls = [ctx.bind_sample(xs[i], params, history=hs[i], history_len=hl, noise=ns[i])
+             for i in range(n_sets)]
+    for i in range(args.warmup):
+        calls[i % n_sets]()
+    torch.cuda.synchronize()
+    eager = [c.out_ids.clone() for c in calls[:4]]
+    us2, k2, graph2 = graph_us_per_step(torch, calls, args.steps, args.warmup)
+    # the graph replays must reproduce the eager results
+    for c, e in zip(calls[:4], eager):
+        assert torch.equal(c.out_ids, e), "graph replay differs from eager launch"
+    st = torch.stack([c.out_status for c in calls]).cpu().numpy()
     assert (st == 0).all(), f"row status {st}"
-    kt2 = kernel_times(ctx, torch, step2, n_sets, args.steps)
+    del graph2
+    kt2 = kernel_times(torch, ctx, calls, min(args.steps, 480))
+    eg2 = eager_us_per_step(torch, calls, min(args.steps, 500))
     bytes2 = W.algorithmic_bytes(B, V, 2, mask=False, H=H, noise_floats=2)
-    stream_us = kt2["k_stream"][0]
-    log(f"[bench] cfg2 {ms2 * 1e3:.2f} us/step; kernels (us/launch): "
-        + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt2.items() if v[1]))
-    del xs, hs, ns
-    torch.cuda.empty_cache()
-
-    # cfg3: grammar masks + T 0.8 + top-p 0.9 (the general path: scan, collect, finalize)
-    w3 = W.cfg3()
-    per3 = B * V * 2 + B * ((V + 31) // 32) * 4
-    n3 = int(np.ceil(args.pool_mb * 2**20 / per3))
-    g3 = torch.Generator(device=dev)
-    g3.manual_seed(3)
-    m3 = torch.from_numpy(w3["mask"].view(np.int32)).to(dev)
-    x3 = [(torch.randn(B, V, device=dev, generator=g3) * 2.5).to(torch.bfloat16) for _ in range(n3)]
-    n3s = [torch.from_numpy(np.random.default_rng(i).random((B, 2), dtype=np.float32)).to(dev)
-           for i in range(n3)]
-
-    def step3(i):
-        ctx.sample(x3[i], w3["params"], mask=m3, noise_mode=N.NOISE_ICDF, noise=n3s[i],
-                   out_ids=out_ids, out_status=out_st)
-
-    ms3 = time_steps(torch, step3, n3, args.steps, args.warmup)
-    st3 = out_st.cpu().numpy()
-    assert (st3 == 0).all(), f"row status {st3}"
-    kt3 = kernel_times(ctx, torch, step3, n3, args.steps)
-    log(f"[bench] cfg3 {ms3 * 1e3:.2f} us/step; kernels (us/launch): "
-        + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt3.items() if v[1]))
-    del x3, n3s
+    log(f"[bench] cfg2 graph {us2:.2f} us/step (eager {eg2:.2f}); kernels (us): "
+        + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt2.items()))
+    del xs, hs, ns, calls
     torch.cuda.empty_cache()
 
     result = {
         "metric": METRIC,
-        "value": round(ms2 * 1e3, 3),
+        "value": round(us2, 3),
         "unit": "us/step",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": k2,
         "warmup": args.warmup,
-        "ms_per_step": round(ms2, 6),
+        "ms_per_step": round(us2 * 1e-3, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 in, f32/f64 math",
-        "data": "synthetic (seeded N(0,2.5^2)+Zipf bias logits, Zipf histories), rotating "
+        "dtype": "bf16 logits; f32 processing, f64 decisions",
+        "data": f"synthetic (seeded N(0,2.5^2)+Zipf bias logits, Zipf histories), rotating "
                 f"{n_sets}-set pool > 512 MB",
         "config": {"workload": "cfg2: B=8 V=151936 bf16, per-row T{0.6,0.8,1.0} top-k{0,20,50} "
                                "top-p U[0.8,1], min-p 0.05, presence 0.5, frequency 0.3 over "
                                "4096-token history, icdf draw (one uniform per row)",
-                   "B": B, "V": V, "history": H},
-        "roofline": {"kernel": "k_stream", "bound": "hbm",
-                     "achieved": round(bytes2 / (stream_us * 1e-6) / 1e9, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(bytes2 / (stream_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "bytes_per_launch": bytes2, "us_per_launch": round(stream_us, 3)},
-        "kernel_us": {k: round(v[0], 3) for k, v in kt2.items() if v[1]},
-        "cfg3": {"workload": "cfg3: B=8 bf16 + packed grammar masks (0.01-30% density), "
-                             "T 0.8, top-p 0.9, icdf", "us_per_step": round(ms3 * 1e3, 3),
-                 "kernel_us": {k: round(v[0], 3) for k, v in kt3.items() if v[1]}},
+                   "B": B, "V": V, "history": H, "timing": "hip-graph replay"},
+        "roofline": roofline(bytes2, kt2["k_stream"][0]),
+        "kernel_us": {k: round(v[0], 3) for k, v in kt2.items()},
+        "eager_us_per_step": round(eg2, 3),
     }
 
     if not args.no_b64:
@@ -227,35 +293,29 @@ def main():
         xs5, hs5, ms5 = make_pool_cfg5(torch, dev, n5, B5, V, H5)
         p5 = W.cfg5()["params"]
         hl5 = torch.full((B5,), H5, dtype=torch.int32, device=dev)
-        o5 = torch.empty(B5, dtype=torch.int32, device=dev)
-        s5 = torch.empty(B5, dtype=torch.int32, device=dev)
-        pos = W.cfg5()["params"].copy()
-
-        def step5(i):
-            ctx.sample(xs5[i], p5, mask=ms5[i], history=hs5[i], history_len=hl5,
-                       noise_mode=N.NOISE_ICDF, noise=None, out_ids=o5, out_status=s5)
-
-        ms_5 = time_steps(torch, step5, n5, args.steps, args.warmup)
-        st5 = s5.cpu().numpy()
+        calls5 = [ctx.bind_sample(xs5[i], p5, mask=ms5[i], history=hs5[i], history_len=hl5)
+                  for i in range(n5)]
+        for i in range(min(args.warmup, 50)):
+            calls5[i % n5]()
+        us5, k5, g5 = graph_us_per_step(torch, calls5, min(args.steps, 1000), 50)
+        del g5
+        st5 = torch.stack([c.out_status for c in calls5]).cpu().numpy()
         assert (st5 == 0).all(), f"row status {st5}"
-        kt5 = kernel_times(ctx, torch, step5, n5, args.steps)
+        kt5 = kernel_times(torch, ctx, calls5, min(args.steps, 480))
         bytes5 = W.algorithmic_bytes(B5, V, 2, mask=True, H=H5, noise_floats=0)
-        us5 = kt5["k_stream"][0]
-        log(f"[bench] cfg5 {ms_5 * 1e3:.2f} us/step; kernels (us/launch): "
-            + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt5.items() if v[1]))
+        log(f"[bench] cfg5 graph {us5:.2f} us/step; kernels (us): "
+            + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt5.items()))
         result["b64"] = {
             "workload": "cfg5: B=64 bf16, 2048-token history, 5% masks, T 0.8, top-k 40, "
                         "top-p 0.95, min-p 0.02, Philox per row",
-            "us_per_step": round(ms_5 * 1e3, 3),
-            "rows_per_s": round(B5 / (ms_5 * 1e-3), 1),
-            "roofline": {"kernel": "k_stream", "bound": "hbm",
-                         "achieved": round(bytes5 / (us5 * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(bytes5 / (us5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                         "bytes_per_launch": bytes5, "us_per_launch": round(us5, 3)},
-            "step_hbm_frac": round(bytes5 / (ms_5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "kernel_us": {k: round(v[0], 3) for k, v in kt5.items() if v[1]},
+            "us_per_step": round(us5, 3),
+            "rows_per_s": round(B5 / (us5 * 1e-6), 1),
+            "steps": k5,
+            "roofline": roofline(bytes5, kt5["k_stream"][0]),
+            "step_hbm_frac": round(bytes5 / (us5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel_us": {k: round(v[0], 3) for k, v in kt5.items()},
         }
-        del xs5, hs5, ms5, pos
+        del xs5, hs5, ms5, calls5
     ctx.close()
 
     if not args.no_cpu:

@@ -10,7 +10,7 @@
 #include "kernels.hpp"
 
 namespace strim {
-__global__ void k_stream(Args a);
+hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen);
 __global__ void k_finalize(Args a);
 __global__ void k_collect(Args a);
 __global__ void k_final(Args a);
@@ -90,21 +90,23 @@ bool nofilter(const strim_sampling_params& p, int32_t V) {
 }
 
 // The launch sequence of one row group. k_stream + k_finalize decide greedy, fast and
-// unfiltered Gumbel rows; k_collect runs when a row needs the general path's second pass,
-// and k_final whenever a non-greedy row might still be undecided (general rows, or a
-// fast row whose candidates overflow k_stream's finalize).
+// unfiltered Gumbel rows (overflowing fast rows too, by the exact path); general rows
+// add k_collect (second pass) and k_final.
 int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
-  bool need_collect = false, need_final = false;
+  bool need_collect = false, need_final = false, any_pen = false;
   for (int i = 0; i < nb; ++i) {
+    const strim_sampling_params& q = a.p[i];
+    if ((q.repetition_penalty != 1.0f || q.presence_penalty != 0.0f ||
+         q.frequency_penalty != 0.0f) && (a.hist != nullptr || a.verify))
+      any_pen = true;
     const int32_t cls = row_class(a.p[i], a.V);
     if (cls == CLS_GENERAL && !(a.noise_mode == STRIM_NOISE_GUMBEL && nofilter(a.p[i], a.V)))
       need_collect = true;
-    if (cls == CLS_GENERAL || cls == CLS_FAST) need_final = true;
   }
-  if (need_collect) need_final = true;
+  // k_final decides the general rows (k_finalize leaves them pending)
+  need_final = need_collect;
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
-  timed(ctx, st, KID_STREAM,
-        [&] { hipLaunchKernelGGL(k_stream, grid_rc, dim3(STPB), 0, st, a); });
+  timed(ctx, st, KID_STREAM, [&] { (void)launch_stream(a, grid_rc, st, any_pen); });
   timed(ctx, st, KID_FINALIZE,
         [&] { hipLaunchKernelGGL(k_finalize, dim3((unsigned)a.R), dim3(STPB), 0, st, a); });
   if (need_collect)

@@ -35,8 +35,8 @@ enum RowClass : int32_t { CLS_GREEDY = 0, CLS_FAST = 1, CLS_GENERAL = 2, CLS_INV
 
 // How a row's candidates are resolved (set by k_collect for general rows).
 // Set by k_finalize: DONE rows are decided; PENDING rows (general path) go to
-// k_collect + k_final; EXACT rows (candidate overflow) to k_final's exact resolution.
-enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1, PH_EXACT = 2 };
+// k_collect + k_final.
+enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1 };
 
 enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
 
@@ -321,19 +321,27 @@ __device__ __forceinline__ void process_seg(const A& a, int i0, const RowParams&
 }
 
 // History counts of the span [c0, c0 + SPAN) in LDS, like build_counts_span, but the
-// first HPT * NT history ids are loaded before the table is cleared, so their latency
-// overlaps the clear and the caller's other loads.
+// first HPT * NT history ids are loaded (16 bytes at a time when aligned) before the
+// table is cleared, so their latency overlaps the clear and the caller's other loads.
 constexpr int HPT = 16;
 template <int NT, int SPAN, typename A>
 __device__ __forceinline__ void build_counts_pre(const A& a, int b, int j, int c0,
                                                  uint32_t* s_cnt) {
   const int t = threadIdx.x;
   const int32_t* h = a.hist ? a.hist + (int64_t)b * a.H : nullptr;
+  // ids [4 (q NT + t), +4) as one 16-byte load when the row is aligned, else one by one
+  const bool h4 = h && ((uintptr_t)h & 15u) == 0;
   int ids[HPT];
 #pragma unroll
-  for (int q = 0; q < HPT; ++q) {
-    const int i = q * NT + t;
-    ids[q] = (h && i < a.H) ? h[i] : -1;
+  for (int q = 0; q < HPT / 4; ++q) {
+    const int i = 4 * (q * NT + t);
+    if (h4 && i + 4 <= a.H) {
+      const int4 v = *(const int4*)(h + i);
+      ids[4 * q] = v.x; ids[4 * q + 1] = v.y; ids[4 * q + 2] = v.z; ids[4 * q + 3] = v.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ids[4 * q + e] = (h && i + e < a.H) ? h[i + e] : -1;
+    }
   }
   int hl = h ? a.H : 0;
   if (h && a.hist_len) {
@@ -346,7 +354,7 @@ __device__ __forceinline__ void build_counts_pre(const A& a, int b, int j, int c
   const uint32_t uc0 = (uint32_t)c0;
 #pragma unroll
   for (int q = 0; q < HPT; ++q) {
-    const int i = q * NT + t;
+    const int i = 4 * ((q >> 2) * NT + t) + (q & 3);
     const uint32_t o = (uint32_t)ids[q] - uc0;
     if (i < hl && o < (uint32_t)SPAN && ids[q] >= 0 && ids[q] < a.V) atomicAdd(&s_cnt[o], 1u);
   }

@@ -7,7 +7,7 @@
 // the rest exactly; k_final sorts the candidates in LDS by (l desc, id asc) and takes every
 // decision in fp64. Rows whose candidates overflow either finalize are decided by k_final's
 // exact streaming resolution.
-#include "select.hpp"
+#include "exact.hpp"
 
 namespace strim {
 
@@ -368,481 +368,6 @@ __device__ void bitonic_sort(uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key) {
   __syncthreads();
 }
 
-// ---------------------------------------------------------------------------------
-// Exact streaming resolution of one row by its finalize workgroup
-// ---------------------------------------------------------------------------------
-// Rows whose candidates do not fit the finalize (flat or tie-heavy rows, nuclei wider
-// than CAP, local candidate overflow) are decided here. Every decision is a weighted
-// radix select over the order keys: level 0 bins d = m - l at 1/64 nat; deeper levels
-// take 12 bits at a time of the compact key (fkey_desc(l) << 20 | id) inside the chosen
-// bucket, until it holds at most XCOL tokens, which are gathered, sorted in LDS and
-// resolved exactly. Each level is one streaming pass over the raw logits that recomputes
-// the processing chain (history counts per window of XWIN tokens). Masses are fixed
-// point, 2^43 per unit of exp(l - m), so every sum is exact and independent of order.
-constexpr int XB = 4096;            // digits per level
-constexpr int XWIN = FIN_T * EPT;   // tokens per window of a pass
-constexpr int XCOL = 4096;          // bucket size resolved in LDS
-constexpr double XFIX = 8796093022208.0;  // 2^43
-
-struct XState {
-  uint64_t below_m, key, key_w, tot_m;
-  uint32_t below_c, cnt, tot_c, ncol;
-  int32_t found, token;
-};
-
-// The tokens a select ranges over: allowed, passing min-p (lmp = log(min_p), -inf for
-// none), with order key in [lo, bound], other than `excl`.
-struct XUni {
-  float m;
-  double lmp;
-  uint64_t lo, bound;
-  int excl;
-};
-
-// The fields of Args the streaming passes read (the exact path is one out-of-line call,
-// so the 3 KB launch block is not copied to private memory).
-struct XArgs {
-  const void* logits;
-  int64_t row_stride;
-  int32_t dtype, vec_ok, V, H, verify, k, noise_mode;
-  const uint32_t* mask;
-  int64_t mask_stride;
-  const int32_t* hist;
-  const int32_t* hist_len;
-  const int32_t* drafts;
-  const float* noise;
-  int64_t noise_stride;
-};
-
-__device__ __forceinline__ bool x_in(const XUni& u, float l, int id) {
-  if (!(l > -INFINITY) || !((double)l - (double)u.m >= u.lmp) || id == u.excl) return false;
-  const uint64_t k = ckey(l, id);
-  return k >= u.lo && k <= u.bound;
-}
-__device__ __forceinline__ uint64_t x_weight(float l, float m) {
-  return (uint64_t)__double2ull_rn(exp((double)l - (double)m) * XFIX);
-}
-// Level-0 digit: floor(64 (m - l)), tail at XB - 1; monotone in the order.
-__device__ __forceinline__ int x_dbin(float l, float m) {
-  const double d = (double)m - (double)l;
-  return d < (double)(XB - 1) / 64.0 ? (int)(d * 64.0) : XB - 1;
-}
-__device__ __forceinline__ uint64_t x_ck(float l, int id) {
-  return ((uint64_t)fkey_desc(l) << 20) | (uint32_t)id;
-}
-// First fkey in [lo, hi] whose float satisfies a predicate that is monotone (false, then
-// true) along the order; hi + 1 if none.
-template <typename F>
-__device__ __forceinline__ uint32_t x_first_fkey(uint32_t lo, uint32_t hi, F pred) {
-  uint64_t L = lo, H = (uint64_t)hi + 1;
-  while (L < H) {
-    const uint64_t mid = (L + H) >> 1;
-    if (pred(fkey_desc_inv((uint32_t)mid))) H = mid;
-    else L = mid + 1;
-  }
-  return (uint32_t)L;
-}
-
-// One streaming pass over the row: fn(i0, l) for every thread and window.
-template <typename F>
-__device__ __forceinline__ void x_pass(const XArgs& a, int r, int b, int j, const RowParams& p,
-                                       uint32_t* s_cnt, F&& fn) {
-  const int t = threadIdx.x;
-  for (int w0 = 0; w0 < a.V; w0 += XWIN) {
-    const int i0 = w0 + t * EPT;
-    float x[EPT];
-    load_tokens(a, r, i0, x);
-    if (p.pen) build_counts_span<FIN_T, XWIN>(a, b, j, w0, s_cnt);
-    float l[EPT];
-    bool nf = false;
-    process_tokens(a, r, i0, p, s_cnt + t * EPT, x, l, nf);
-    fn(i0, l);
-    if (p.pen) __syncthreads();  // the next window rebuilds the counts
-  }
-}
-
-// Interval of one select level: mode 0 = level-0 bins, 1 = compact-key digits of
-// [klo, khi] shifted right by `shift`, 2 = everything in digit 0.
-struct XLevel {
-  int mode, shift;
-  uint64_t klo, khi;
-};
-__device__ __forceinline__ int x_digit(const XLevel& lv, float l, int id, float m) {
-  if (lv.mode == 0) return x_dbin(l, m);
-  if (lv.mode == 2) return 0;
-  const uint64_t ck = x_ck(l, id);
-  return (ck >= lv.klo && ck <= lv.khi) ? (int)((ck - lv.klo) >> lv.shift) : -1;
-}
-
-// Count and fixed-point mass per digit of the universe's tokens inside the level.
-// Each thread accumulates runs of equal digits and flushes a run with one LDS atomic.
-__device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, const RowParams& p, const XUni& u,
-                       const XLevel& lv, uint32_t* s_cnt, uint32_t* s_hc, uint64_t* s_hm) {
-  for (int i = threadIdx.x; i < XB; i += FIN_T) {
-    s_hc[i] = 0u;
-    s_hm[i] = 0ull;
-  }
-  __syncthreads();
-  int cur = -1;
-  uint32_t ac = 0u;
-  uint64_t am = 0ull;
-  x_pass(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT]) {
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      if (!x_in(u, l[e], i0 + e)) continue;
-      const int dg = x_digit(lv, l[e], i0 + e, u.m);
-      if (dg < 0) continue;
-      if (dg != cur) {
-        if (cur >= 0) {
-          atomicAdd(&s_hc[cur], ac);
-          atomicAdd((unsigned long long*)&s_hm[cur], (unsigned long long)am);
-        }
-        cur = dg;
-        ac = 0u;
-        am = 0ull;
-      }
-      ac += 1u;
-      am += x_weight(l[e], u.m);
-    }
-  });
-  if (cur >= 0) {
-    atomicAdd(&s_hc[cur], ac);
-    atomicAdd((unsigned long long*)&s_hm[cur], (unsigned long long)am);
-  }
-  __syncthreads();
-}
-
-// Gathers the order keys of the universe's tokens inside the level's digit `dg` (all of
-// them for mode 2) into s_col; returns their number (<= XCOL by construction).
-__device__ __forceinline__ int x_collect(const XArgs& a, int r, int b, int j, const RowParams& p, const XUni& u,
-                         const XLevel& lv, int dg, uint32_t* s_cnt, uint64_t* s_col,
-                         XState& s_x) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  if (threadIdx.x == 0) s_x.ncol = 0u;
-  __syncthreads();
-  x_pass(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT]) {
-    uint32_t sel = 0u;
-    int c = 0;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e)
-      if (x_in(u, l[e], i0 + e) && x_digit(lv, l[e], i0 + e, u.m) == dg) {
-        sel |= 1u << e;
-        ++c;
-      }
-    int tot;
-    const int ex = wave_excl_count(c, &tot);
-    if (tot > 0) {
-      uint32_t base = 0u;
-      if (lane == 0) base = atomicAdd(&s_x.ncol, (uint32_t)tot);
-      base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
-      uint32_t pos = base + (uint32_t)ex;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e)
-        if ((sel >> e) & 1u) {
-          if (pos < (uint32_t)XCOL) s_col[pos] = ckey(l[e], i0 + e);
-          ++pos;
-        }
-    }
-  });
-  __syncthreads();
-  const int n = (int)s_x.ncol;
-  return n < XCOL ? n : XCOL;
-}
-
-// Ascending in-place sort of s_col[0, n), n <= XCOL (keys are unique).
-__device__ __forceinline__ void x_sort(uint64_t* s_col, int n) {
-  const int t = threadIdx.x;
-  if (n <= FIN_T) {
-    const uint64_t k0 = t < n ? s_col[t] : ~0ull;
-    uint32_t rank = 0;
-    int jj = 0;
-    for (; jj + 4 <= n; jj += 4)
-      rank += (uint32_t)(s_col[jj] < k0) + (uint32_t)(s_col[jj + 1] < k0) +
-              (uint32_t)(s_col[jj + 2] < k0) + (uint32_t)(s_col[jj + 3] < k0);
-    for (; jj < n; ++jj) rank += (uint32_t)(s_col[jj] < k0);
-    __syncthreads();
-    if (t < n) s_col[rank] = k0;
-    __syncthreads();
-  } else {
-    int n2 = 2 * FIN_T;
-    while (n2 < n) n2 <<= 1;
-    uint64_t kk[FIN_Q];
-#pragma unroll
-    for (int q = 0; q < FIN_Q; ++q) {
-      const int idx = q * FIN_T + t;
-      kk[q] = idx < n ? s_col[idx] : ~0ull;
-    }
-    __syncthreads();
-    bitonic_sort(kk, n2, s_col);
-  }
-}
-
-struct XScratch {
-  uint64_t* key;    // XB u64 histogram masses, then the gathered bucket
-  uint32_t* hc;     // XB u32 histogram counts
-  uint32_t* cnt;    // XWIN u32 history counts of a window
-  uint64_t* u2;     // 2 * FIN_T / WAVE
-  double* dred;
-  uint64_t* ured;
-  int* ired;
-};
-
-// Weighted select: the last universe token x in the order whose universe mass before it
-// (by_mass) or count before it is <= T, where T = floor(coef * total mass) of the
-// universe, or T = cst when coef < 0. Result in s_x (found = 0 for an empty universe).
-__device__ __noinline__ void x_select(const XArgs& a, int r, int b, int j, const RowParams p,
-                                      const XUni u, bool by_mass, double coef, uint64_t cst,
-                                      const XScratch xs, XState& s_x) {
-  const int t = threadIdx.x;
-  XLevel lv{0, 0, 0ull, 0ull};
-  uint64_t below_m = 0ull, below_c = 0ull, T = 0ull;
-  int dsel = -1;
-  for (;;) {
-    x_hist(a, r, b, j, p, u, lv, xs.cnt, xs.hc, xs.key);
-    uint32_t c4[4];
-    uint64_t m4[4], lc = 0ull, lm = 0ull;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = xs.hc[4 * t + q];
-      m4[q] = xs.key[4 * t + q];
-      lc += c4[q];
-      lm += m4[q];
-    }
-    uint64_t exc, exm, totc, totm;
-    block_excl_scan2_u64<FIN_T>(lc, lm, xs.u2, exc, exm, totc, totm);
-    if (lv.mode == 0) {
-      T = coef < 0.0 ? cst : (uint64_t)floor(coef * (double)totm);
-      if (t == 0) {
-        s_x.tot_c = (uint32_t)totc;
-        s_x.tot_m = totm;
-      }
-    }
-    int best = -1;
-    uint64_t bc = 0ull, bm = 0ull;
-    uint32_t bn = 0u;
-    uint64_t fc = below_c + exc, fm = below_m + exm;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (c4[q] > 0u && (by_mass ? fm : fc) <= T) {
-        best = 4 * t + q;
-        bc = fc;
-        bm = fm;
-        bn = c4[q];
-      }
-      fc += c4[q];
-      fm += m4[q];
-    }
-    dsel = -block_min<FIN_T>(-best, xs.ired);
-    if (dsel < 0) {
-      if (t == 0) s_x.found = 0;
-      __syncthreads();
-      return;
-    }
-    if (best == dsel) {
-      s_x.below_c = (uint32_t)bc;
-      s_x.below_m = bm;
-      s_x.cnt = bn;
-    }
-    __syncthreads();
-    below_c = s_x.below_c;
-    below_m = s_x.below_m;
-    const uint32_t cnt = s_x.cnt;
-    __syncthreads();
-    if (cnt <= (uint32_t)XCOL) break;
-    // narrow to the chosen digit (every thread computes the same interval)
-    XLevel nx;
-    nx.mode = 1;
-    if (lv.mode == 0) {
-      const uint32_t f_m = fkey_desc(u.m), f_end = fkey_desc(-INFINITY);
-      const float m = u.m;
-      const uint32_t f_lo = x_first_fkey(f_m, f_end, [&](float l) { return x_dbin(l, m) >= dsel; });
-      const uint32_t f_hi =
-          x_first_fkey(f_m, f_end, [&](float l) { return x_dbin(l, m) >= dsel + 1; }) - 1u;
-      nx.klo = (uint64_t)f_lo << 20;
-      nx.khi = ((uint64_t)f_hi << 20) | 0xFFFFFull;
-    } else {
-      nx.klo = lv.klo + ((uint64_t)dsel << lv.shift);
-      const uint64_t hi = nx.klo + ((1ull << lv.shift) - 1ull);
-      nx.khi = hi < lv.khi ? hi : lv.khi;
-    }
-    const uint64_t width = nx.khi - nx.klo;
-    const int bits = width == 0ull ? 0 : 64 - __clzll((long long)width);
-    nx.shift = bits > 12 ? bits - 12 : 0;
-    lv = nx;
-  }
-  // resolve the bucket exactly
-  const int n = x_collect(a, r, b, j, p, u, lv, dsel, xs.cnt, xs.key, s_x);
-  x_sort(xs.key, n);
-  uint64_t w4[4], lm = 0ull;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int pos = 4 * t + q;
-    w4[q] = 0ull;
-    if (pos < n) {
-      w4[q] = x_weight(fkey_desc_inv((uint32_t)(xs.key[pos] >> 32)), u.m);
-      lm += w4[q];
-    }
-  }
-  uint64_t ex0, exm, tot0, totm;
-  block_excl_scan2_u64<FIN_T>(0ull, lm, xs.u2, ex0, exm, tot0, totm);
-  int best = -1;
-  uint64_t bm = 0ull, bw = 0ull;
-  uint64_t fm = below_m + exm;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int pos = 4 * t + q;
-    if (pos < n) {
-      if ((by_mass ? fm : below_c + (uint64_t)pos) <= T) {
-        best = pos;
-        bm = fm;
-        bw = w4[q];
-      }
-      fm += w4[q];
-    }
-  }
-  const int psel = -block_min<FIN_T>(-best, xs.ired);
-  if (t == 0) s_x.found = psel >= 0 ? 1 : 0;
-  if (psel >= 0 && best == psel) {
-    s_x.key = xs.key[psel];
-    s_x.key_w = bw;
-    s_x.below_m = bm;
-    s_x.below_c = (uint32_t)(below_c + (uint64_t)psel);
-  }
-  __syncthreads();
-}
-
-struct XOut {
-  int status, token, accept;
-  double sig;
-  uint64_t last_key;
-};
-
-// The whole decision chain of one row from streaming passes (see above).
-__device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const RowParams p, float m, int arg,
-                          int draft, bool vdr, float l_draft, const XScratch xs, XState& s_x) {
-  const int V = a.V;
-  const bool topk = p.top_k > 0 && p.top_k < V;
-  const bool topp = p.top_p < 1.0f;
-  const bool keep_ties = (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) != 0;
-  const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
-  const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
-  const bool cand_sorted = no_lse ? topp : (topk || topp);
-  XUni u{m, p.min_p > 0.0f ? log((double)p.min_p) : -INFINITY, 0ull, ~0ull, -1};
-  uint64_t S = 0ull;
-  bool haveS = false;
-  uint32_t nkeep = 0u;
-  if (topk) {
-    const uint64_t K1 = (uint64_t)(p.top_k - 1);
-    x_select(a, r, b, j, p, u, false, -1.0, K1, xs, s_x);
-    if (!s_x.found) return XOut{STRIM_EEMPTY, -1, 0, 0.0, 0ull};
-    if (keep_ties) {
-      u.bound = (s_x.key & 0xFFFFFFFF00000000ull) | 0xFFFFFFFFull;
-    } else {
-      u.bound = s_x.key;
-      S = s_x.below_m + s_x.key_w;
-      haveS = true;
-      nkeep = s_x.below_c + 1u;
-    }
-  }
-  if (topp) {
-    const double P = (double)p.top_p;
-    x_select(a, r, b, j, p, u, true, P, 0ull, xs, s_x);
-    if (!s_x.found) return XOut{STRIM_EEMPTY, -1, 0, 0.0, 0ull};
-    u.bound = s_x.key;
-    S = s_x.below_m + s_x.key_w;
-    haveS = true;
-    nkeep = s_x.below_c + 1u;
-  }
-  double w_d = 0.0;
-  uint64_t W_d = 0ull;
-  if (vdr && l_draft > -INFINITY && x_in(u, l_draft, draft)) {
-    w_d = exp((double)l_draft - (double)m);
-    W_d = x_weight(l_draft, m);
-  }
-  XUni ud = u;
-  ud.excl = vdr ? draft : -1;
-  int token = -1;
-  if (a.noise_mode == STRIM_NOISE_ICDF) {
-    const double uu = (double)row_uniform(a, r, p, 0);
-    x_select(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
-    S = s_x.tot_m + W_d;
-    // an empty residual (only the draft kept) draws the first kept token
-    token = s_x.found ? (int)(uint32_t)s_x.key : arg;
-  } else {
-    if (!haveS) {
-      const XLevel all{2, 0, 0ull, 0ull};
-      x_hist(a, r, b, j, p, u, all, xs.cnt, xs.hc, xs.key);
-      S = xs.key[0];
-      __syncthreads();
-    }
-    const double lse = log((double)S / XFIX);
-    const uint64_t pkey = mix64(p.seed, p.position);
-    double bsc = -INFINITY;
-    uint64_t btk = ~0ull;
-    int bid = -1;
-    auto take = [&](float l, int id, int64_t nidx, uint64_t tk) {
-      const float uq = a.noise ? a.noise[(int64_t)r * a.noise_stride + nidx]
-                               : philox_uniform(pkey, (uint64_t)nidx);
-      const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
-      const double sc = base + gumbel64(uq);
-      if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) {
-        bsc = sc;
-        btk = tk;
-        bid = id;
-      }
-    };
-    if (by_rank) {
-      // noise indexed by the rank in the order: the kept set is walked in rank order,
-      // XCOL keys at a time (a count select finds each bucket's last key, a gather pass
-      // collects and sorts the bucket)
-      const XLevel all{2, 0, 0ull, 0ull};
-      XUni ub = ud;
-      uint32_t below = 0u;
-      while (below < nkeep) {
-        x_select(a, r, b, j, p, ub, false, -1.0, (uint64_t)(XCOL - 1), xs, s_x);
-        if (!s_x.found) break;
-        XUni uc = ub;
-        uc.bound = s_x.key;
-        const int n = x_collect(a, r, b, j, p, uc, all, 0, xs.cnt, xs.key, s_x);
-        x_sort(xs.key, n);
-        for (int pos = threadIdx.x; pos < n; pos += FIN_T) {
-          const uint64_t key = xs.key[pos];
-          take(fkey_desc_inv((uint32_t)(key >> 32)), (int)(uint32_t)key,
-               (int64_t)below + pos, key);
-        }
-        __syncthreads();
-        if (n <= 0) break;
-        below += (uint32_t)n;
-        ub.lo = uc.bound + 1ull;
-      }
-    } else {
-      x_pass(a, r, b, j, p, xs.cnt, [&](int i0, const float (&l)[EPT]) {
-#pragma unroll
-        for (int e = 0; e < EPT; ++e)
-          if (x_in(ud, l[e], i0 + e))
-            take(l[e], i0 + e, i0 + e, cand_sorted ? ckey(l[e], i0 + e) : (uint64_t)(i0 + e));
-      });
-    }
-    block_argmax_score<FIN_T>(bsc, btk, bid, xs.dred, xs.ured, xs.ired, &s_x.token);
-    token = s_x.token >= 0 ? s_x.token : arg;
-  }
-  int acc = 0;
-  const double sig = (double)S / XFIX;
-  if (vdr) {
-    const float ua = row_uniform(a, r, p, a.noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V : 1);
-    acc = ((double)ua < w_d / sig) ? 1 : 0;
-  }
-  uint64_t last = u.bound;
-  if (last == ~0ull && p.min_p > 0.0f) {
-    const double lmp = u.lmp;
-    const uint32_t f_thr = x_first_fkey(fkey_desc(m), fkey_desc(-INFINITY), [&](float l) {
-                             return !((double)l - (double)m >= lmp);
-                           }) - 1u;
-    last = ((uint64_t)f_thr << 32) | 0xFFFFFFFFull;
-  }
-  return XOut{STRIM_OK, token, acc, sig, last};
-}
-
 __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   __shared__ uint64_t s_key[CAP];
   __shared__ double s_w[CAP];
@@ -870,8 +395,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   const int V = a.V;
   const bool verify_draft_row = a.verify && j < a.k;
   RowState* rsp = &a.s.rs[r];
-  // k_stream decided every row except general rows (PENDING) and rows whose candidates
-  // overflowed its finalize (EXACT)
+  // k_finalize decided every row except the general rows (PENDING)
   const int phase = rsp->phase;
   if (phase == PH_DONE) return;
 
@@ -889,7 +413,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     __syncthreads();
   }
   // rows the candidate path cannot hold go to the exact streaming resolution
-  bool exact = status == STRIM_OK && !p.greedy && (phase == PH_EXACT || s_bd.mode == MODE_NONE);
+  bool exact = status == STRIM_OK && !p.greedy && s_bd.mode == MODE_NONE;
   auto finish = [&](int stt, int token, int accept, double sig, uint64_t lk) {
     if (t == 0) {
       rsp->status = stt;
@@ -1224,7 +748,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   xa.drafts = a.drafts;
   xa.noise = a.noise;
   xa.noise_stride = a.noise_stride;
-  const XOut xo = exact_row(xa, r, b, j, p, m, st.arg, draft, verify_draft_row,
+  const XOut xo = exact_row<FIN_T>(xa, r, b, j, p, m, st.arg, draft, verify_draft_row,
                             verify_draft_row ? rsp->l_draft : -INFINITY, xs, s_x);
   if (t == 0) rsp->bd.mode = MODE_A;  // kept set = order prefix up to last_key
   finish(xo.status, xo.token, xo.accept, xo.sig, xo.last_key);

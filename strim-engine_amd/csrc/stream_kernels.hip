@@ -12,8 +12,9 @@
 //                    the survivors, the top-p cut and the draw, all in LDS;
 //   unfiltered Gumbel rows  from the chunks' two best scores;
 //   general rows     left to k_collect / k_final (pass-1 histograms are written here).
-// A row whose candidates do not fit the LDS finalize is marked for k_final's exact path.
-#include "select.hpp"
+// A row whose candidates do not fit the LDS finalize is decided there by the exact
+// streaming resolution (exact.hpp).
+#include "exact.hpp"
 
 namespace strim {
 
@@ -56,74 +57,153 @@ __device__ __forceinline__ void finish_row(const Args& a, int r, int status, int
 }
 
 // LDS of one k_finalize workgroup.
-// Histogram bin of d = m - l (1/16 nat, last bin open) for k_finalize's top-k cut;
-// monotone in l.
-__device__ __forceinline__ int dbin(float m, float l) {
-  return (int)fminf((m - l) * 16.0f, 255.0f);
-}
+constexpr int FSEG = FCAP / (STPB / WAVE);  // survivors per wave segment in phase 2
 struct FinalShared {
   uint64_t key[FCAP];       // the row's surviving candidate keys (32 KB)
-  uint16_t owner[FCAND];    // candidate position -> wave region (4 * chunk + wave)
-  uint32_t rpre[4 * 256];   // first position of each wave region
-  uint32_t hist[256];       // radix digits / d-histogram
-  float v[STPB / WAVE];
-  int i[STPB / WAVE], n[STPB / WAVE], f[STPB / WAVE];
-  float g[STPB / WAVE];
-  uint32_t off[STPB / WAVE];
+  uint32_t rpre[4 * 256];   // per wave region: first candidate position within its
+                            // 64-chunk block (add the block offsets in off[])
+  uint32_t hist[256];       // d-histogram / radix digits
+  float v[STPB / WAVE], g[STPB / WAVE];
+  int i[STPB / WAVE], f[STPB / WAVE];
+  uint32_t off[STPB / WAVE], cnt[STPB / WAVE];
   double d[STPB / WAVE];
   uint64_t u[STPB / WAVE];
   int misc[8];
-  uint32_t nsurv;
+  // the exact streaming resolution (rows whose candidates overflow): its histogram
+  // masses and gathered buckets use key[] (XB entries)
+  uint32_t xhc[XB];
+  uint32_t xcnt[STPB * EPT];
+  uint64_t xu2[2 * STPB / WAVE];
+  XState x;
 };
+static_assert(FCAP >= XB && FCAP >= XCOL, "the exact path reuses the candidate keys");
 
-// One row per 256-thread workgroup. All threads merge the chunk statistics and gather
-// the candidates (every load in flight at once), pruning with the row maximum (min-p)
-// and with G = max over chunks of the certified k-th value bound; the survivors are
-// decided by wave 0 alone with wave-wide operations (no further barriers).
+// Histogram bin of d = m - l at `scale` bins per nat (last bin open) for the top-k cut;
+// monotone in l.
+__device__ __forceinline__ int dbin(float m, float l, float scale) {
+  return (int)fminf((m - l) * scale, 255.0f);
+}
+
+// Decides a row whose candidates overflow the finalize by the exact streaming
+// resolution (all threads of the workgroup call it). Inlined: only exact_row is an
+// out-of-line call, taking the few launch fields it needs by value, so the 3 KB launch
+// block is never copied to private memory.
+__device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int j,
+                                            const RowParams& p, float m, int arg, int draft,
+                                            bool vdr, float l_draft, FinalShared& S) {
+  XScratch xs;
+  xs.key = S.key;
+  xs.hc = S.xhc;
+  xs.cnt = S.xcnt;
+  xs.u2 = S.xu2;
+  xs.dred = S.d;
+  xs.ured = S.u;
+  xs.ired = S.i;
+  XArgs xa;
+  xa.logits = a.logits;
+  xa.row_stride = a.row_stride;
+  xa.dtype = a.dtype;
+  xa.vec_ok = a.vec_ok;
+  xa.V = a.V;
+  xa.H = a.H;
+  xa.verify = a.verify;
+  xa.k = a.k;
+  xa.noise_mode = a.noise_mode;
+  xa.mask = a.mask;
+  xa.mask_stride = a.mask_stride;
+  xa.hist = a.hist;
+  xa.hist_len = a.hist_len;
+  xa.drafts = a.drafts;
+  xa.noise = a.noise;
+  xa.noise_stride = a.noise_stride;
+  __syncthreads();
+  const XOut xo = exact_row<STPB>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
+  finish_row(a, r, xo.status, xo.token, xo.accept, xo.sig, m, xo.last_key, PH_DONE);
+}
+
+// One row per 256-thread workgroup, in three phases with two barriers:
+//   1. merge the chunk statistics (max, argmax, flags, k-th value bound G, candidate
+//      counts);
+//   2. every thread gathers candidate positions t, t + 256, ... (eight loads in flight;
+//      a binary search over the wave-region prefixes finds each slot), divides by T,
+//      prunes with min-p on the row maximum and with G, compacts the survivors into its
+//      wave's LDS segment and, for top-k rows, counts them in a histogram of m - l over
+//      the survivors' span;
+//   3. wave 0 alone: top-k (from the histogram), sort, top-p, draw, with wave-wide
+//      operations only.
 __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams& p,
                              FinalShared& S) {
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int V = a.V, W = a.W;
   const bool vdr = a.verify && j < a.k;  // a verify row with a draft
   RowState* rsp = &a.s.rs[r];
+  // the row's remaining global inputs, requested before anything waits
+  const int draft = vdr ? a.drafts[(int64_t)b * a.k + j] : -1;
+  const float l_draft = vdr ? rsp->l_draft : -INFINITY;
+  float u_draw = 0.0f, u_acc = 0.0f;
+  if (a.noise && !p.greedy) {
+    const float* nz = a.noise + (int64_t)r * a.noise_stride;
+    if (a.noise_mode == STRIM_NOISE_ICDF) {
+      u_draw = nz[0];
+      u_acc = nz[1];
+    } else {
+      u_acc = nz[V];
+    }
+  }
 
-  // ---- merge the chunk statistics (W <= 256: one chunk per thread) ----------------
+  // ---- phase 1: chunk statistics (W <= 256: one chunk per thread) -----------------
   ChunkStat cs{-INFINITY, -1, 0, 0, 0.0, 0u, -INFINITY};
   if (t < W) cs = a.s.cstat[(int64_t)r * a.s.wmax + t];
+  uint32_t ctot = 0u;
+  int ff = cs.flags | (cs.n > 0 ? 4 : 0);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t ce = (cs.nslot >> (8 * e)) & 255u;
+    if (ce > (uint32_t)SLOTW) ff |= 2;  // a wave region overflowed
+    ctot += ce;
+  }
   float mv = cs.m, gv = cs.g;
-  int mi = cs.arg, nn = cs.n, ff = cs.flags;
+  int mi = cs.arg;
   wave_argmax(mv, mi);
-  nn = wave_sum(nn);
   ff = wave_or_i(ff);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, WAVE));
+  uint32_t wtot;
+  const uint32_t wex = wave_excl_scan_u32(ctot, &wtot);
+  if (t < W) {
+    uint32_t o = wex;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      S.rpre[4 * t + e] = o;
+      o += (cs.nslot >> (8 * e)) & 255u;
+    }
+  }
+  if (t < 256) S.hist[t] = 0u;
   if (lane == 0) {
     S.v[w] = mv;
     S.i[w] = mi;
-    S.n[w] = nn;
     S.f[w] = ff;
     S.g[w] = gv;
+    S.off[w] = wtot;
   }
-  if (t < 256) S.hist[t] = 0u;
-  if (t == 0) S.nsurv = 0u;
   __syncthreads();
   float m = S.v[0], G = S.g[0];
-  int arg = S.i[0], n_all = S.n[0], flags = S.f[0];
+  int arg = S.i[0], flags = S.f[0];
+  uint32_t n_c = 0u;
 #pragma unroll
-  for (int q = 1; q < STPB / WAVE; ++q) {
-    argmax_merge(m, arg, S.v[q], S.i[q]);
-    n_all += S.n[q];
-    flags |= S.f[q];
-    G = fmaxf(G, S.g[q]);
+  for (int q = 0; q < STPB / WAVE; ++q) {
+    if (q > 0) {
+      argmax_merge(m, arg, S.v[q], S.i[q]);
+      flags |= S.f[q];
+      G = fmaxf(G, S.g[q]);
+    }
+    n_c += S.off[q];
   }
 
-  int status = STRIM_OK, draft = -1;
-  if (vdr) {
-    draft = a.drafts[(int64_t)b * a.k + j];
-    if (draft < 0 || draft >= V) status = STRIM_EINVAL;
-  }
-  if (status == STRIM_OK && flags) status = STRIM_ENONFINITE;
-  if (status == STRIM_OK && n_all == 0) status = STRIM_EEMPTY;
+  int status = STRIM_OK;
+  if (vdr && (draft < 0 || draft >= V)) status = STRIM_EINVAL;
+  if (status == STRIM_OK && (flags & 1)) status = STRIM_ENONFINITE;
+  if (status == STRIM_OK && !(flags & 4)) status = STRIM_EEMPTY;
   if (status != STRIM_OK) {
     finish_row(a, r, status, -1, 0, 0.0, m, 0ull, PH_DONE);
     return;
@@ -139,7 +219,10 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   const bool cand_sorted = no_lse ? topp : (topk || topp);
   const uint64_t pkey = mix64(p.seed, p.position);
   const int excl_id = vdr ? draft : -1;
-  const float l_draft = vdr ? rsp->l_draft : -INFINITY;
+  if (!a.noise) {
+    u_draw = philox_uniform(pkey, 0);
+    u_acc = philox_uniform(pkey, a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
+  }
 
   // ---- unfiltered Gumbel rows: the chunks' two best tokens ------------------------
   if (p.cls == CLS_GENERAL && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, V)) {
@@ -170,8 +253,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     int acc = 0;
     if (vdr) {
       const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
-      const float ua = row_uniform(a, r, p, (int64_t)V);
-      acc = ((double)ua < w_d / sig) ? 1 : 0;
+      acc = ((double)u_acc < w_d / sig) ? 1 : 0;
       if (token < 0) token = arg;  // the draft is the only allowed token
     }
     finish_row(a, r, STRIM_OK, token, acc, sig, m, ~0ull, PH_DONE);
@@ -181,81 +263,94 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     finish_row(a, r, STRIM_OK, -1, 0, 0.0, m, 0ull, PH_PENDING);
     return;
   }
-
-  // ---- fast rows: gather, divide, prune and compact the candidates -------------------
-  // chunk c's candidates sit in four per-wave regions of SLOTW entries; cs.nslot holds
-  // the four counts as bytes (255 = the wave overflowed its region)
-  uint32_t ctot = 0u;
-  int over = 0;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t ce = t < W ? (cs.nslot >> (8 * e)) & 255u : 0u;
-    if (ce > (uint32_t)SLOTW) over = 1;
-    ctot += ce;
-  }
-  uint32_t n_c;
-  const uint32_t pre = block_excl_scan_u32<STPB>(over ? 0u : ctot, S.off, &n_c);
-  over = block_or<STPB>(over, S.i);
-  if (over || n_c > (uint32_t)FCAND) {
-    finish_row(a, r, STRIM_OK, -1, 0, 0.0, m, 0ull, PH_EXACT);
+  if ((flags & 2) || n_c > (uint32_t)FCAND) {
+    finalize_exact(a, r, b, j, p, m, arg, draft, vdr, l_draft, S);
     return;
   }
-  if (t < W) {
-    // the owner table maps each candidate position to its region
-    uint32_t o = pre;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t ce = (cs.nslot >> (8 * e)) & 255u;
-      S.rpre[4 * t + e] = o;
-      for (uint32_t i = 0; i < ce; ++i) S.owner[o + i] = (uint16_t)(4 * t + e);
-      o += ce;
-    }
-  }
-  __syncthreads();
+
+  // ---- phase 2: gather, divide, prune, compact --------------------------------------
   // every kept token has v >= G (the k-th value bound), minus the l-tie margin
   const float Gm = topk && G > -INFINITY ? G - (fabsf(G) * 1e-6f + 1e-30f) : -INFINITY;
-  const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
   const bool minp = p.min_p > 0.0f;
   const double lmp = minp ? log((double)p.min_p) : 0.0;
-  constexpr int GQ = FCAP / STPB;
-  for (int base = 0; base < (int)n_c; base += FCAP) {
-    Cand cd[GQ];
+  // top-k histogram of d = m - l over the survivors' span (bounded by G or min-p)
+  float dspan = 16.0f;
+  if (Gm > -INFINITY) dspan = fminf(dspan, m - Gm / p.T);
+  if (minp) dspan = fminf(dspan, (float)-lmp);
+  const float scale = 255.0f / fmaxf(dspan * 1.0001f, 1e-6f);
+  const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
+  const int nreg = 4 * W;
+  // global position of region rg's first candidate
+  auto gpre = [&](int rg) {
+    uint32_t o = S.rpre[rg];
+    const int blk = rg >> 8;  // 64 chunks (256 regions) per wave of phase 1
 #pragma unroll
-    for (int q = 0; q < GQ; ++q) {
+    for (int q = 0; q < STPB / WAVE; ++q)
+      if (q < blk) o += S.off[q];
+    return o;
+  };
+  constexpr int GB = 8;  // loads in flight per thread per batch
+  uint32_t n_w = 0u;     // survivors in this wave's segment
+  for (int base = 0; base < (int)n_c; base += GB * STPB) {
+    Cand cd[GB];
+#pragma unroll
+    for (int q = 0; q < GB; ++q) {
       const int pos = base + q * STPB + t;
       cd[q] = Cand{-INFINITY, -1};
       if (pos < (int)n_c) {
-        const int rg = S.owner[pos];
-        cd[q] = slots[(int64_t)rg * SLOTW + (pos - (int)S.rpre[rg])];
+        int lo = 0, hi = nreg - 1;  // last region whose first position <= pos
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if ((int)gpre(mid) <= pos) lo = mid;
+          else hi = mid - 1;
+        }
+        cd[q] = slots[(int64_t)lo * SLOTW + (pos - (int)gpre(lo))];
       }
     }
 #pragma unroll
-    for (int q = 0; q < GQ; ++q) {
+    for (int q = 0; q < GB; ++q) {
       // l = v / T as the oracle rounds it
-      bool keep = cd[q].id >= 0 && cd[q].l >= Gm;
-      const float l = keep ? cd[q].l / p.T : -INFINITY;
-      keep = keep && l > -INFINITY && (!minp || ((double)l - (double)m) >= lmp);
-      const uint64_t msk = __ballot(keep);
+      bool k = cd[q].id >= 0 && cd[q].l >= Gm;
+      const float l = k ? cd[q].l / p.T : -INFINITY;
+      k = k && l > -INFINITY && (!minp || ((double)l - (double)m) >= lmp);
+      const uint64_t msk = __ballot(k);
       if (msk) {
-        uint32_t wbase = 0u;
-        if (lane == 0) wbase = atomicAdd(&S.nsurv, (uint32_t)__popcll(msk));
-        wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
-        const uint32_t dst = wbase + (uint32_t)lanes_below(msk);
-        if (keep && dst < (uint32_t)FCAP) S.key[dst] = ckey(l, cd[q].id);
-        // histogram of d = m - l for the top-k cut
-        if (keep && topk) atomicAdd(&S.hist[dbin(m, l)], 1u);
+        const uint32_t dst = n_w + (uint32_t)lanes_below(msk);
+        if (k && dst < (uint32_t)FSEG) S.key[w * FSEG + dst] = ckey(l, cd[q].id);
+        if (k && topk) atomicAdd(&S.hist[dbin(m, l, scale)], 1u);
+        n_w += (uint32_t)__popcll(msk);
       }
     }
   }
+  if (lane == 0) S.off[w] = n_w;
   __syncthreads();
-  int n = (int)S.nsurv;
-  if (n > FCAP) {
-    finish_row(a, r, STRIM_OK, -1, 0, 0.0, m, 0ull, PH_EXACT);
+  uint32_t segn[STPB / WAVE];
+  int over = 0;
+  uint32_t n_s = 0u;
+#pragma unroll
+  for (int q = 0; q < STPB / WAVE; ++q) {
+    segn[q] = S.off[q];
+    over |= segn[q] > (uint32_t)FSEG;
+    n_s += segn[q];
+  }
+  if (over) {
+    finalize_exact(a, r, b, j, p, m, arg, draft, vdr, l_draft, S);
     return;
   }
-  if (w != 0) return;  // the rest is one wave
+  if (w != 0) return;  // phase 3 is one wave
+  // concatenate the wave segments
+  {
+    uint32_t o = segn[0];
+#pragma unroll
+    for (int q = 1; q < STPB / WAVE; ++q) {
+      for (uint32_t i = lane; i < segn[q]; i += WAVE) S.key[o + i] = S.key[q * FSEG + i];
+      o += segn[q];
+    }
+    wave_sync();
+  }
+  int n = (int)n_s;
 
-  // ---- top-k: the survivors up to the histogram bin holding the k-th, sorted ---------
+  // ---- phase 3a: top-k -- the survivors up to the histogram bin holding the k-th ----
   bool sorted = false;
   if (topk && n > p.top_k) {
     const uint4 h = *(const uint4*)&S.hist[4 * lane];
@@ -270,13 +365,12 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
       cum += hs[e];
     }
     const int bstar = wave_min_i(bl);
-    // keep the keys in bins <= bstar (a superset of the top k, ordered by key)
+    // keep the keys in bins <= bstar (a superset of the top k)
     uint32_t n2 = 0u;
     for (int base = 0; base < n; base += WAVE) {
       const int pos = base + lane;
       const uint64_t kv = pos < n ? S.key[pos] : ~0ull;
-      const float l = fkey_desc_inv((uint32_t)(kv >> 32));
-      const bool keep = pos < n && dbin(m, l) <= bstar;
+      const bool keep = pos < n && dbin(m, fkey_desc_inv((uint32_t)(kv >> 32)), scale) <= bstar;
       const uint64_t msk = __ballot(keep);
       wave_sync();
       if (keep) S.key[n2 + (uint32_t)lanes_below(msk)] = kv;
@@ -314,14 +408,14 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     // the kept prefix: k keys, or with ties every key sharing the k-th value
     const bool ties = (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) != 0;
     const uint64_t bound = ties ? (kth | 0xFFFFFFFFull) : kth;
-    int cnt = 0;
+    int c = 0;
     for (int base = 0; base < n; base += WAVE) {
       const int pos = base + lane;
-      cnt += (pos < n && S.key[pos] <= bound) ? 1 : 0;
+      c += (pos < n && S.key[pos] <= bound) ? 1 : 0;
     }
-    n = wave_sum(cnt);
+    n = wave_sum(c);
   }
-  // sort the survivors
+  // ---- phase 3b: sort the survivors ---------------------------------------------
   if (!sorted) {
     if (n <= WAVE) {
       const uint64_t kv = wave_sort_u64(lane < n ? S.key[lane] : ~0ull);
@@ -333,13 +427,18 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     }
   }
 
-  // ---- top-p over the sorted survivors: lane owns positions [lane*Qn, lane*Qn + Qn) --
+  // ---- phase 3c: top-p over the sorted survivors ----------------------------------
+  // lane owns positions [lane*Qn, lane*Qn + Qn); with n <= 64 (Qn = 1) its weight is
+  // computed once
   const int Qn = (n + WAVE - 1) / WAVE;
   const int p0 = lane * Qn, p1 = min(n, p0 + Qn);
   const uint64_t* keys = S.key;
-  double loc = 0.0;
-  for (int q = p0; q < p1; ++q)
-    loc += exp((double)fkey_desc_inv((uint32_t)(keys[q] >> 32)) - (double)m);
+  auto weight = [&](int q) {
+    return exp((double)fkey_desc_inv((uint32_t)(keys[q] >> 32)) - (double)m);
+  };
+  const double w0 = p0 < p1 ? weight(p0) : 0.0;
+  double loc = w0;
+  for (int q = p0 + 1; q < p1; ++q) loc += weight(q);
   double S_pre;
   const double ex = wave_excl_scan_f64(loc, &S_pre);
   int n_keep = n;
@@ -352,14 +451,13 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
         fd = q;
         break;
       }
-      run += exp((double)fkey_desc_inv((uint32_t)(keys[q] >> 32)) - (double)m);
+      run += q == p0 ? w0 : weight(q);
     }
     n_keep = wave_min_i(fd);
   }
   const int k1 = min(p1, n_keep);
   loc = 0.0;
-  for (int q = p0; q < k1; ++q)
-    loc += exp((double)fkey_desc_inv((uint32_t)(keys[q] >> 32)) - (double)m);
+  for (int q = p0; q < k1; ++q) loc += q == p0 ? w0 : weight(q);
   double S_kept;
   const double exk = wave_excl_scan_f64(loc, &S_kept);
   const uint64_t last_key = keys[n_keep - 1];
@@ -372,16 +470,15 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     if (key_d <= last_key) w_d = exp((double)l_draft - (double)m);
   }
 
-  // ---- draw ---------------------------------------------------------------------
+  // ---- phase 3d: draw -----------------------------------------------------------
   int token;
   if (a.noise_mode == STRIM_NOISE_ICDF) {
-    const float u = row_uniform(a, r, p, 0);
-    const double tgt = (double)u * (S_kept - w_d);
+    const double tgt = (double)u_draw * (S_kept - w_d);
     int best = n_keep;
     double run = exk;
     for (int q = p0; q < k1; ++q) {
       const uint64_t key = keys[q];
-      const double wq = exp((double)fkey_desc_inv((uint32_t)(key >> 32)) - (double)m);
+      const double wq = q == p0 ? w0 : weight(q);
       double before = run;
       if (key_d < key) before -= w_d;
       if ((int)(uint32_t)key != excl_id && wq > 0.0 && before + wq > tgt) {
@@ -420,11 +517,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     token = wave_argmax_score(bsc, btk, bid);
     if (token < 0) token = (int)(uint32_t)keys[0];  // every score -inf / only the draft kept
   }
-  int acc = 0;
-  if (vdr) {
-    const float ua = row_uniform(a, r, p, a.noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V : 1);
-    acc = ((double)ua < w_d / S_kept) ? 1 : 0;
-  }
+  const int acc = vdr && ((double)u_acc < w_d / S_kept) ? 1 : 0;
   finish_row(a, r, STRIM_OK, token, acc, S_kept, m, last_key, PH_DONE);
 }
 
@@ -445,6 +538,43 @@ __device__ __forceinline__ float dv_rung_end(int r) {
   return __uint_as_float(((uint32_t)r + 1u + VRUNG0) << 20);
 }
 
+// The 8 tokens [i0, i0 + 8) of row r as float32 (bf16 widened exactly). FULL: the
+// chunk lies inside the row and rows are 16-byte aligned, so one or two vector loads.
+template <int DT, bool FULL>
+__device__ __forceinline__ void load_seg(const Args& a, int r, int i0, float (&x)[EPT]) {
+  const int64_t base = (int64_t)r * a.row_stride;
+  if constexpr (DT == STRIM_DTYPE_BF16) {
+    const uint16_t* xb = (const uint16_t*)a.logits + base;
+    if constexpr (FULL) {
+      const uint4 v = *(const uint4*)(xb + i0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = __uint_as_float(w[e] << 16);
+        x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? bf16_to_f32(xb[i0 + e]) : -INFINITY;
+    }
+  } else {
+    const float* xf = (const float*)a.logits + base;
+    if constexpr (FULL) {
+      const float4 v0 = *(const float4*)(xf + i0);
+      const float4 v1 = *(const float4*)(xf + i0 + 4);
+      x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+      x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? xf[i0 + e] : -INFINITY;
+    }
+  }
+}
+
+// DT: logits dtype; VEC: rows are 16-byte aligned; PEN: some row of the launch has
+// penalties; MASK: allow-bits are given. The host picks the instantiation, so each
+// launch runs straight-line per-token code.
+template <int DT, bool VEC, bool PEN, bool MASK>
 __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   __shared__ StreamShared S;
   uint32_t* s_cnt = S.cnt;
@@ -456,47 +586,56 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   const RowParams p = load_params(a, b, j);
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int c0 = c * CHUNK;
+  const bool full = VEC && c0 + CHUNK <= a.V;
   int i0[SSEG];
   float v[SSEG][EPT];
   uint32_t bits[SSEG];
 #pragma unroll
   for (int s = 0; s < SSEG; ++s) {
     i0[s] = c0 + (s * STPB + t) * EPT;
-    load_tokens(a, r, i0[s], v[s]);
-    bits[s] = load_mask8(a, r, i0[s]);
+    if (full) load_seg<DT, true>(a, r, i0[s], v[s]);
+    else load_seg<DT, false>(a, r, i0[s], v[s]);
+    bits[s] = 0xFFu;
+    if constexpr (MASK) {
+      if (a.mask && i0[s] < a.V)
+        bits[s] = ((const uint8_t*)(a.mask + (int64_t)r * a.mask_stride))[i0[s] >> 3];
+    }
   }
   for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
   if (t < NCB) {
     S.hc[t] = 0u;
     S.hm[t] = 0ull;
   }
-  if (p.pen) build_counts_pre<STPB, CHUNK>(a, b, j, c0, s_cnt);
+  const bool pen = PEN && p.pen;
+  if (pen) build_counts_pre<STPB, CHUNK>(a, b, j, c0, s_cnt);
 
   // ---- penalties and mask, before temperature ("v space") ------------------------
   // Dividing by T > 0 is monotone, so maxima and candidate bounds are found on v; only
-  // the chunk maximum and (in k_finalize) the candidates are divided.
+  // the chunk maximum and (in k_finalize) the candidates are divided. Tokens past the
+  // row end load as -inf (not allowed).
   bool nf = false;
   float vmax = -INFINITY;
-  int vid = -1, n = 0;
+  int vid = -1;
 #pragma unroll
   for (int s = 0; s < SSEG; ++s) {
-    const uint32_t* cnt = s_cnt + (i0[s] - c0);
+    uint32_t cnt[EPT];
+    if (pen) {
+      const uint4 c4a = *(const uint4*)(s_cnt + (i0[s] - c0));
+      const uint4 c4b = *(const uint4*)(s_cnt + (i0[s] - c0) + 4);
+      cnt[0] = c4a.x; cnt[1] = c4a.y; cnt[2] = c4a.z; cnt[3] = c4a.w;
+      cnt[4] = c4b.x; cnt[5] = c4b.y; cnt[6] = c4b.z; cnt[7] = c4b.w;
+    }
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       float y = v[s][e];
-      if (p.pen) {
-        const uint32_t cc = cnt[e];
-        if (cc > 0u) {
-          y = y > 0.0f ? y / p.rep : y * p.rep;
-          y = y - p.freq * (float)cc;
-          y = y - p.pres;
-        }
+      if (pen && cnt[e] > 0u) {
+        y = y > 0.0f ? y / p.rep : y * p.rep;
+        y = y - p.freq * (float)cnt[e];
+        y = y - p.pres;
       }
-      const bool ok = (i0[s] + e < a.V) && ((bits[s] >> e) & 1u);
-      y = ok ? y : -INFINITY;
-      nf |= !(y < INFINITY) && ok;  // NaN or +inf in an allowed position
+      if constexpr (MASK) y = ((bits[s] >> e) & 1u) ? y : -INFINITY;
+      nf |= !(y < INFINITY);  // NaN or +inf in an allowed position
       v[s][e] = y;
-      n += y > -INFINITY ? 1 : 0;
       // ids rise with (s, e): a strict compare keeps the first maximum
       if (y > vmax) {
         vmax = y;
@@ -522,7 +661,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
 
   // ---- chunk max (first id on ties), allowed count, non-finite flag ---------------
   wave_argmax(vmax, vid);
-  n = wave_sum(n);
+  int n = vmax > -INFINITY ? 1 : 0;  // "some token allowed"; general rows count below
   const int f = __any(nf) ? 1 : 0;
   if (lane == 0) {
     S.v[w] = vmax;
@@ -536,7 +675,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
 #pragma unroll
   for (int q = 1; q < STPB / WAVE; ++q) {
     argmax_merge(vm, a_w, S.v[q], S.i[q]);
-    n_w += S.n[q];
+    n_w |= S.n[q];
     f_w |= S.f[q];
   }
   // chunk max after temperature; an overflow to +inf is a non-finite logit, one to -inf
@@ -631,11 +770,13 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) l[s][e] = v[s][e] > -INFINITY ? v[s][e] / p.T : -INFINITY;
     double ssum = 0.0;
+    int na = 0;
 #pragma unroll
     for (int s = 0; s < SSEG; ++s)
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         if (!(l[s][e] > -INFINITY)) continue;
+        ++na;
         const float d = m_w - l[s][e];
         const float wgt = expf(-d);
         ssum += (double)wgt;
@@ -645,6 +786,10 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
         if (fx) atomicAdd(&S.hm[bb], fx);
       }
     cs.S = block_sum_f64<STPB>(ssum, S.d);
+    na = wave_sum(na);
+    if (lane == 0) S.n[w] = na;
+    __syncthreads();
+    cs.n = S.n[0] + S.n[1] + S.n[2] + S.n[3];
     if (t < NCB) {
       const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
       a.s.chc[o] = S.hc[t];
@@ -674,6 +819,35 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
     }
   }
   if (t == 0) a.s.cstat[(int64_t)r * a.s.wmax + c] = cs;
+}
+
+// Launches the k_stream instantiation matching the call: dtype, alignment, whether
+// any row has penalties, whether a mask is given.
+hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen) {
+  const bool vec = a.vec_ok != 0, mask = a.mask != nullptr;
+#define STRIM_STREAM(DT, VEC, PEN, MASK) \
+  hipLaunchKernelGGL((k_stream<DT, VEC, PEN, MASK>), grid, dim3(STPB), 0, st, a)
+  if (a.dtype == STRIM_DTYPE_BF16) {
+    if (!vec) STRIM_STREAM(STRIM_DTYPE_BF16, false, true, true);
+    else if (any_pen) {
+      if (mask) STRIM_STREAM(STRIM_DTYPE_BF16, true, true, true);
+      else STRIM_STREAM(STRIM_DTYPE_BF16, true, true, false);
+    } else {
+      if (mask) STRIM_STREAM(STRIM_DTYPE_BF16, true, false, true);
+      else STRIM_STREAM(STRIM_DTYPE_BF16, true, false, false);
+    }
+  } else {
+    if (!vec) STRIM_STREAM(STRIM_DTYPE_F32, false, true, true);
+    else if (any_pen) {
+      if (mask) STRIM_STREAM(STRIM_DTYPE_F32, true, true, true);
+      else STRIM_STREAM(STRIM_DTYPE_F32, true, true, false);
+    } else {
+      if (mask) STRIM_STREAM(STRIM_DTYPE_F32, true, false, true);
+      else STRIM_STREAM(STRIM_DTYPE_F32, true, false, false);
+    }
+  }
+#undef STRIM_STREAM
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------

@@ -129,6 +129,35 @@ class Context:
         N.check(rc, "strim_sample")
         return out_ids, out_status, probs
 
+    def bind_sample(self, logits: torch.Tensor, params, mask: torch.Tensor | None = None,
+                    history: torch.Tensor | None = None,
+                    history_len: torch.Tensor | None = None, noise_mode: int = N.NOISE_ICDF,
+                    noise: torch.Tensor | None = None, out_ids: torch.Tensor | None = None,
+                    out_status: torch.Tensor | None = None, stream=None) -> "BoundCall":
+        """strim_sample with every argument converted once: calling the result launches
+        the step again on the same buffers (the tensors must stay alive). For loops that
+        reuse buffers, such as a decode loop or HIP-graph capture."""
+        if logits.dim() == 1:
+            logits = logits.unsqueeze(0)
+        B, V = logits.shape
+        dev = logits.device
+        p = host_params(params)
+        if p.size != B:
+            raise ValueError(f"need {B} param rows, got {p.size}")
+        _check_rows(logits)
+        _check_cuda(mask, history, history_len, noise)
+        if out_ids is None:
+            out_ids = torch.empty(B, dtype=torch.int32, device=dev)
+        if out_status is None:
+            out_status = torch.empty(B, dtype=torch.int32, device=dev)
+        H = 0 if history is None else history.shape[-1]
+        mstride = 0 if mask is None else mask.shape[-1]
+        args = [self._h, None, _ptr(logits), _dtype_code(logits), B, V,
+                logits.stride(0), _pp(p), _ptr(mask), mstride, _ptr(history), _ptr(history_len),
+                H, noise_mode, _ptr(noise), _ptr(out_ids), _ptr(out_status), None]
+        keep = (logits, p, mask, history, history_len, noise, out_ids, out_status)
+        return BoundCall(N.lib().strim_sample, args, keep, out_ids, out_status, stream)
+
     def verify(self, target_logits: torch.Tensor, draft_tokens: torch.Tensor | None, params,
                draft_logits: torch.Tensor | None = None,
                draft_to_full: torch.Tensor | None = None, mask: torch.Tensor | None = None,
@@ -210,3 +239,23 @@ def _to_i32(words: torch.Tensor) -> torch.Tensor:
     w = words & 0xFFFFFFFF
     w = torch.where(w >= (1 << 31), w - (1 << 32), w)
     return w.to(torch.int32)
+
+
+class BoundCall:
+    """A strim_sample call with its ctypes arguments prepared (see Context.bind_sample).
+    It launches on the given stream, or on the current stream at call time (so a graph
+    capture records it)."""
+
+    def __init__(self, fn, args, keep, out_ids, out_status, stream=None):
+        self._fn = fn
+        self._args = args
+        self._keep = keep
+        self._stream = stream
+        self.out_ids = out_ids
+        self.out_status = out_status
+
+    def __call__(self) -> None:
+        self._args[1] = _stream(self._stream)
+        rc = self._fn(*self._args)
+        if rc != N.OK:
+            raise N.StrimError(rc, "strim_sample")
