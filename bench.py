@@ -164,11 +164,102 @@ def cpu_baseline_cfg2(seconds: float):
                       f"OpenMP over rows"}
 
 
-def roofline(bytes_per_launch, us):
+# k_stream instantiation -> workload (cfg2 has penalties and no mask, cfg5 the reverse)
+STREAM_CASES = {"k_stream<1, true, true, false>": "cfg2", "k_stream<1, true, false, true>": "cfg5"}
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_k_stream_cfg2_cfg5.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of k_stream per workload, from the committed rocprofv3 counter
+    summary (lines `traffic <kernel> <workload> <bytes>`); {} when absent."""
+    out = {}
+    if TRAFFIC_FILE.exists():
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            f = line.strip().strip("`").split()
+            if len(f) == 4 and f[0] == "traffic" and f[3].isdigit():
+                out[(f[1], f[2])] = int(f[3])
+    return out
+
+
+def roofline(bytes_per_launch, us, traffic=None):
     gbs = bytes_per_launch / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_stream",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_stream",
             "bytes_per_launch": int(bytes_per_launch), "us_per_launch": round(us, 3)}
+
+
+def _kname(n):
+    import re
+    return re.sub(r"\(.*", "", n).replace("strim::", "").replace("void ", "").strip()
+
+
+def summarize(d):
+    """Markdown summary of a profile directory made by the commands it prints: kernel
+    trace statistics of the bench (d/trace), and FETCH_SIZE / WRITE_SIZE per dispatch of a
+    counter pass (d/fetch, d/write) scaled by the 256 MiB copy's counters."""
+    import csv
+    import glob
+    d = Path(d)
+    print("## Kernel trace (rocprofv3 --kernel-trace --stats)\n")
+    print("| kernel | calls | avg us | min us | max us |\n|---|---|---|---|---|")
+    for f in glob.glob(str(d / "trace" / "*kernel_stats.csv")):
+        for r in csv.DictReader(open(f)):
+            if "strim::" in r["Name"]:
+                print(f"| {_kname(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                      f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
+    for f in glob.glob(str(d / "trace" / "*kernel_trace.csv")):
+        rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
+        acc, case = {}, None
+        for r in rows:
+            if "strim::" not in r["Kernel_Name"]:
+                continue
+            k = _kname(r["Kernel_Name"])
+            if k.startswith("k_stream"):
+                case = STREAM_CASES.get(k, k)
+            kk = "k_stream" if k.startswith("k_stream") else k
+            acc.setdefault((kk, case), []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        print("\nThe same trace per workload (a kernel belongs to the k_stream variant it "
+              "follows):\n")
+        print("| kernel | workload | calls | avg us | median us |\n|---|---|---|---|---|")
+        for (k, c), v in sorted(acc.items(), key=lambda t: (str(t[0][1]), t[0][0])):
+            v = sorted(v)
+            print(f"| {k} | {c} | {len(v)} | {sum(v) / len(v):.2f} | {v[len(v) // 2]:.2f} |")
+    per = {}
+    scale = {}
+    for cn in ("FETCH_SIZE", "WRITE_SIZE"):
+        sub = "fetch" if cn == "FETCH_SIZE" else "write"
+        for f in glob.glob(str(d / sub / "*counter_collection.csv")):
+            rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Dispatch_Id"]))
+            case = None
+            for r in rows:
+                k = _kname(r["Kernel_Name"])
+                v = float(r["Counter_Value"])
+                if k.startswith("k_stream"):
+                    case = STREAM_CASES.get(k, k)
+                if "copyBuffer" in k and int(r["Grid_Size"]) >= 131072:
+                    scale[cn] = 256 * 1024 / v  # KiB moved / KiB counted
+                if "strim::" in r["Kernel_Name"]:
+                    kk = "k_stream" if k.startswith("k_stream") else k
+                    per.setdefault((kk, case, cn), []).append(v)
+    print("\n## HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)\n")
+    print(f"Calibration: a 256 MiB device copy reads FETCH_SIZE x {scale.get('FETCH_SIZE', 0):.3f} "
+          f"and writes WRITE_SIZE x {scale.get('WRITE_SIZE', 0):.3f} KiB; the factors scale "
+          "the counters below to bytes.\n")
+    print("| kernel | workload | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | bytes/launch |")
+    print("|---|---|---|---|---|---|")
+    keys = sorted({(k, c) for k, c, _ in per})
+    lines = []
+    for k, c in keys:
+        fe = per.get((k, c, "FETCH_SIZE"), [0.0])
+        wr = per.get((k, c, "WRITE_SIZE"), [0.0])
+        fa, wa = sum(fe) / len(fe), sum(wr) / len(wr)
+        b = int((fa * scale.get("FETCH_SIZE", 1.0) + wa * scale.get("WRITE_SIZE", 1.0)) * 1024)
+        print(f"| {k} | {c} | {len(fe)} | {fa:.0f} | {wa:.0f} | {b} |")
+        lines.append(f"traffic {k} {c} {b}")
+    print("\nMachine-readable (bench.py reads these lines):\n")
+    for ln in lines:
+        print(f"    {ln}")
 
 
 def pmc_pass(torch, ops, W, dev, steps, pool_mb):
@@ -212,11 +303,17 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b64", action="store_true")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="print the markdown summary of a profile directory (trace/, fetch/, "
+                         "write/ as made by the commands in profiles/) and exit")
     ap.add_argument("--pmc-pass", type=int, default=0, metavar="N",
                     help="profiling pass for rocprofv3 counters: N eager steps of cfg2 and "
                          "cfg5 over a pool, then a 256 MiB device copy (the calibration "
                          "kernel for FETCH_SIZE / WRITE_SIZE); prints a summary line only")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: every box here has one GPU, and this path shards "
@@ -233,6 +330,7 @@ def main():
     if args.pmc_pass:
         pmc_pass(torch, ops, W, dev, args.pmc_pass, args.pool_mb)
         return
+    traffic = measured_traffic()
     V, B, H = W.V_DEFAULT, 8, 4096
     per_set = B * V * 2 + B * H * 4 + B * 8
     n_sets = int(np.ceil(args.pool_mb * 2**20 / per_set))
@@ -280,7 +378,7 @@ def main():
                                "top-p U[0.8,1], min-p 0.05, presence 0.5, frequency 0.3 over "
                                "4096-token history, icdf draw (one uniform per row)",
                    "B": B, "V": V, "history": H, "timing": "hip-graph replay"},
-        "roofline": roofline(bytes2, kt2["k_stream"][0]),
+        "roofline": roofline(bytes2, kt2["k_stream"][0], traffic.get(("k_stream", "cfg2"))),
         "kernel_us": {k: round(v[0], 3) for k, v in kt2.items()},
         "eager_us_per_step": round(eg2, 3),
     }
@@ -311,7 +409,7 @@ def main():
             "us_per_step": round(us5, 3),
             "rows_per_s": round(B5 / (us5 * 1e-6), 1),
             "steps": k5,
-            "roofline": roofline(bytes5, kt5["k_stream"][0]),
+            "roofline": roofline(bytes5, kt5["k_stream"][0], traffic.get(("k_stream", "cfg5"))),
             "step_hbm_frac": round(bytes5 / (us5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "kernel_us": {k: round(v[0], 3) for k, v in kt5.items()},
         }

@@ -179,9 +179,11 @@ int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, in
 /* ---- per-kernel timing -------------------------------------------------------------
  * Counterpart of the reference's fenced per-region GPU timer OpTimer
  * (Sources/StrimCore/OpTimer.swift:1-60). While profiling is on, every kernel a call
- * launches is bracketed by HIP events recorded on the call's stream; strim_profile_end
- * synchronises, sums the elapsed time per kernel and turns profiling off. Profiling
- * allocates its events in strim_profile_begin, never in the calls it times. */
+ * launches carries a pair of HIP events bound to its dispatch's own start and end
+ * timestamps (hipExtLaunchKernel), so the elapsed time is the kernel's execution alone;
+ * strim_profile_end synchronises, sums the elapsed time per kernel and turns profiling
+ * off. Profiling allocates its events in strim_profile_begin, never in the calls it
+ * times. Do not profile calls that are being captured into a graph. */
 #define STRIM_KERNEL_COUNT 6 /* stream, finalize, collect, final, probs, verify_combine */
 int strim_profile_begin(strim_ctx* ctx, int32_t max_launches);
 int strim_profile_end(strim_ctx* ctx, double* total_ms /* [STRIM_KERNEL_COUNT] */,

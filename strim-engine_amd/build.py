@@ -2,8 +2,11 @@
 
     python strim-engine_amd/build.py
 
-Always recompiles. The library lands next to the Python binding
-(strim-engine_amd/strim_amd/libstrim_sampler.so) so it travels with the tree.
+Always recompiles. Every translation unit is compiled to an object in parallel (the
+k_stream variants are split over one object per (dtype, penalties) pair), then the
+objects are linked into strim-engine_amd/strim_amd/libstrim_sampler.so, next to the
+Python binding, so the library travels with the tree. Objects go to a temporary
+directory that is removed afterwards.
 """
 from __future__ import annotations
 
@@ -11,20 +14,32 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "strim_amd" / "libstrim_sampler.so"
-SOURCES = ["stream_kernels.hip", "sample_kernels.hip", "aux_kernels.hip", "capi.hip"]
+
+# (source, extra defines): k_stream variants per (dtype, penalties) pair
+UNITS = [
+    ("stream_kernels.hip", ["-DSTRIM_DT=1", "-DSTRIM_PEN=1"]),
+    ("stream_kernels.hip", ["-DSTRIM_DT=1", "-DSTRIM_PEN=0"]),
+    ("stream_kernels.hip", ["-DSTRIM_DT=0", "-DSTRIM_PEN=1"]),
+    ("stream_kernels.hip", ["-DSTRIM_DT=0", "-DSTRIM_PEN=0"]),
+    ("finalize_kernels.hip", []),
+    ("sample_kernels.hip", []),
+    ("aux_kernels.hip", []),
+    ("capi.hip", []),
+]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # every float32 step is one IEEE rounding (the parity contract relies on it)
     "-ffp-contract=off",
     # no packed fp32 instructions
@@ -40,16 +55,30 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", *[str(CSRC / s) for s in SOURCES],
-           "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed")
+        raise RuntimeError("hipcc failed: " + " ".join(cmd))
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    cc = hipcc()
+    jobs = jobs or min(len(UNITS), os.cpu_count() or 1, 16)
+    with tempfile.TemporaryDirectory(prefix="strim_build_") as tmpdir:
+        objs, cmds = [], []
+        for i, (src, defs) in enumerate(UNITS):
+            obj = str(Path(tmpdir) / f"{i}_{Path(src).stem}.o")
+            objs.append(obj)
+            cmds.append([cc, *HIPCC_FLAGS, *defs, f"-I{ROOT / 'include'}", "-c",
+                         str(CSRC / src), "-o", obj])
+        with ThreadPoolExecutor(max_workers=jobs) as ex:
+            for f in [ex.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        tmp = OUT.with_suffix(".so.tmp")
+        _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
     os.replace(tmp, OUT)
     return OUT
 

@@ -7,10 +7,9 @@
 #include <math.h>
 #include <string.h>
 
-#include "kernels.hpp"
+#include "stream.hpp"
 
 namespace strim {
-hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen);
 __global__ void k_finalize(Args a);
 __global__ void k_collect(Args a);
 __global__ void k_final(Args a);
@@ -71,18 +70,30 @@ enum KernelId { KID_STREAM = 0, KID_FINALIZE, KID_COLLECT, KID_FINAL, KID_PROBS,
 const char* const kKernelNames[STRIM_KERNEL_COUNT] = {"k_stream", "k_finalize", "k_collect",
                                                       "k_final", "k_probs", "k_verify_combine"};
 
-// Launches `launch()` on stream st, bracketed by profiling events when enabled.
+// Runs `launch(e0, e1)`: with profiling on, e0/e1 are the next event pair, which the
+// launch binds to its dispatch's timestamps; otherwise both are null.
 template <typename F>
-void timed(strim_ctx* ctx, hipStream_t st, int kind, F launch) {
+void timed(strim_ctx* ctx, int kind, F launch) {
   if (ctx && ctx->prof_on && ctx->prof_n < ctx->prof_cap) {
     const int i = ctx->prof_n++;
     ctx->prof_kind[i] = kind;
-    (void)hipEventRecord(ctx->prof_ev[2 * i], st);
-    launch();
-    (void)hipEventRecord(ctx->prof_ev[2 * i + 1], st);
+    launch(ctx->prof_ev[2 * i], ctx->prof_ev[2 * i + 1]);
   } else {
-    launch();
+    launch(nullptr, nullptr);
   }
+}
+
+// Launches the k_stream variant for the call: dtype, alignment, whether any row has
+// penalties, whether a mask is given (unaligned calls take the penalties object, whose
+// unaligned variant checks penalties and mask per row).
+hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen, hipEvent_t e0,
+                         hipEvent_t e1) {
+  const bool pen = any_pen || a.vec_ok == 0;
+  if (a.dtype == STRIM_DTYPE_BF16)
+    return pen ? launch_stream_group<STRIM_DTYPE_BF16, true>(a, grid, st, e0, e1)
+               : launch_stream_group<STRIM_DTYPE_BF16, false>(a, grid, st, e0, e1);
+  return pen ? launch_stream_group<STRIM_DTYPE_F32, true>(a, grid, st, e0, e1)
+             : launch_stream_group<STRIM_DTYPE_F32, false>(a, grid, st, e0, e1);
 }
 
 bool nofilter(const strim_sampling_params& p, int32_t V) {
@@ -106,17 +117,26 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
   // k_final decides the general rows (k_finalize leaves them pending)
   need_final = need_collect;
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
-  timed(ctx, st, KID_STREAM, [&] { (void)launch_stream(a, grid_rc, st, any_pen); });
-  timed(ctx, st, KID_FINALIZE,
-        [&] { hipLaunchKernelGGL(k_finalize, dim3((unsigned)a.R), dim3(STPB), 0, st, a); });
+  hipError_t e = hipSuccess;
+  auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };
+  timed(ctx, KID_STREAM,
+        [&](hipEvent_t e0, hipEvent_t e1) { keep(launch_stream(a, grid_rc, st, any_pen, e0, e1)); });
+  timed(ctx, KID_FINALIZE, [&](hipEvent_t e0, hipEvent_t e1) {
+    keep(launch_args((const void*)k_finalize, dim3((unsigned)a.R), dim3(STPB), a, st, e0, e1));
+  });
   if (need_collect)
-    timed(ctx, st, KID_COLLECT,
-          [&] { hipLaunchKernelGGL(k_collect, grid_rc, dim3(TPB), 0, st, a); });
+    timed(ctx, KID_COLLECT, [&](hipEvent_t e0, hipEvent_t e1) {
+      keep(launch_args((const void*)k_collect, grid_rc, dim3(TPB), a, st, e0, e1));
+    });
   if (need_final)
-    timed(ctx, st, KID_FINAL,
-          [&] { hipLaunchKernelGGL(k_final, dim3((unsigned)a.R), dim3(FIN_T), 0, st, a); });
+    timed(ctx, KID_FINAL, [&](hipEvent_t e0, hipEvent_t e1) {
+      keep(launch_args((const void*)k_final, dim3((unsigned)a.R), dim3(FIN_T), a, st, e0, e1));
+    });
   if (probs)
-    timed(ctx, st, KID_PROBS, [&] { hipLaunchKernelGGL(k_probs, grid_rc, dim3(TPB), 0, st, a); });
+    timed(ctx, KID_PROBS, [&](hipEvent_t e0, hipEvent_t e1) {
+      keep(launch_args((const void*)k_probs, grid_rc, dim3(TPB), a, st, e0, e1));
+    });
+  if (e != hipSuccess) return STRIM_EHIP;
   return launch_status();
 }
 
@@ -340,10 +360,12 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       for (int i = 0; i < nb; ++i) a.p[i] = params[g0 + i];
       int rc = run_group(ctx, st, a, nb, false);
       if (rc != STRIM_OK) return rc;
-      timed(ctx, st, KID_COMBINE, [&] {
-        hipLaunchKernelGGL(k_verify_combine, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, st, a);
+      hipError_t e = hipSuccess;
+      timed(ctx, KID_COMBINE, [&](hipEvent_t e0, hipEvent_t e1) {
+        e = launch_args((const void*)k_verify_combine, dim3((unsigned)((nb + 63) / 64)), dim3(64),
+                        a, st, e0, e1);
       });
-      rc = launch_status();
+      rc = e != hipSuccess ? STRIM_EHIP : launch_status();
       if (rc != STRIM_OK) return rc;
     }
     return STRIM_OK;

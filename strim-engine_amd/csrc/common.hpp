@@ -1,13 +1,13 @@
 // common.hpp — device-side building blocks of the gfx950 token-selection kernels.
 //
 // Layout of one call: R rows of V logits. Every streaming kernel splits a row into
-// chunks of CHUNK tokens; a 512-thread workgroup owns one (row, chunk) and each thread
-// owns EPT consecutive tokens (one 16-byte load of bf16, two of fp32). Rows that are a
-// multiple of 8 are mapped XCD-locally: all chunks of a row land on the same XCD
-// (workgroups are dispatched round-robin over the 8 XCDs), so the row's re-reads and
-// its atomics stay in one L2.
+// chunks of CHUNK tokens and launches a (chunks, rows) grid; one workgroup owns one
+// (row, chunk) and each thread owns runs of EPT consecutive tokens (one 16-byte load of
+// bf16, two of fp32): k_stream with 256 threads (two runs each), k_collect and k_probs
+// with TPB threads (one run each).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

@@ -1,0 +1,517 @@
+// finalize_kernels.hip — k_finalize: the per-row decision from k_stream's results.
+//
+// One workgroup per row:
+//   greedy rows      argmax of the merged chunk maxima;
+//   fast rows        (0 < top-k <= 256, or min-p >= e^-8) from the chunks' candidates:
+//                    min-p on the row maximum, a radix select of the k-th key, a sort of
+//                    the survivors, the top-p cut and the draw, all in LDS;
+//   unfiltered Gumbel rows  from the chunks' two best scores;
+//   general rows     left to k_collect / k_final (pass-1 histograms are written by
+//                    k_stream).
+// A row whose candidates do not fit the LDS finalize is decided here by the exact
+// streaming resolution (exact.hpp).
+#include "exact.hpp"
+
+namespace strim {
+
+// ---------------------------------------------------------------------------------
+// finalize of one row (k_finalize)
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ void finish_row(const Args& a, int r, int status, int token,
+                                           int accept, double sig, float m, uint64_t last_key,
+                                           int phase) {
+  if (threadIdx.x != 0) return;
+  RowState* rs = &a.s.rs[r];
+  rs->status = status;
+  rs->token = token;
+  rs->accept = accept;
+  rs->sum_kept = sig;
+  rs->m = m;
+  rs->last_key = last_key;
+  rs->phase = phase;
+  if (!a.verify && phase == PH_DONE) {
+    a.out_ids[r] = status == STRIM_OK ? token : -1;
+    if (a.out_status) a.out_status[r] = status;
+  }
+}
+
+// LDS of one k_finalize workgroup.
+constexpr int FSEG = FCAP / (STPB / WAVE);  // survivors per wave segment in phase 2
+struct FinalShared {
+  uint64_t key[FCAP];       // the row's surviving candidate keys (32 KB)
+  uint32_t rpre[4 * 256];   // per wave region: first candidate position within its
+                            // 64-chunk block (add the block offsets in off[])
+  uint32_t hist[256];       // d-histogram / radix digits
+  float v[STPB / WAVE], g[STPB / WAVE];
+  int i[STPB / WAVE], f[STPB / WAVE];
+  uint32_t off[STPB / WAVE], cnt[STPB / WAVE];
+  double d[STPB / WAVE];
+  uint64_t u[STPB / WAVE];
+  int misc[8];
+  // the exact streaming resolution (rows whose candidates overflow): its histogram
+  // masses and gathered buckets use key[] (XB entries)
+  uint32_t xhc[XB];
+  uint32_t xcnt[STPB * EPT];
+  uint64_t xu2[2 * STPB / WAVE];
+  XState x;
+};
+static_assert(FCAP >= XB && FCAP >= XCOL, "the exact path reuses the candidate keys");
+
+// Histogram bin of d = m - l at `scale` bins per nat (last bin open) for the top-k cut;
+// monotone in l.
+__device__ __forceinline__ int dbin(float m, float l, float scale) {
+  return (int)fminf((m - l) * scale, 255.0f);
+}
+
+// Decides a row whose candidates overflow the finalize by the exact streaming
+// resolution (all threads of the workgroup call it). Inlined: only exact_row is an
+// out-of-line call, taking the few launch fields it needs by value, so the 3 KB launch
+// block is never copied to private memory.
+__device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int j,
+                                            const RowParams& p, float m, int arg, int draft,
+                                            bool vdr, float l_draft, FinalShared& S) {
+  XScratch xs;
+  xs.key = S.key;
+  xs.hc = S.xhc;
+  xs.cnt = S.xcnt;
+  xs.u2 = S.xu2;
+  xs.dred = S.d;
+  xs.ured = S.u;
+  xs.ired = S.i;
+  XArgs xa;
+  xa.logits = a.logits;
+  xa.row_stride = a.row_stride;
+  xa.dtype = a.dtype;
+  xa.vec_ok = a.vec_ok;
+  xa.V = a.V;
+  xa.H = a.H;
+  xa.verify = a.verify;
+  xa.k = a.k;
+  xa.noise_mode = a.noise_mode;
+  xa.mask = a.mask;
+  xa.mask_stride = a.mask_stride;
+  xa.hist = a.hist;
+  xa.hist_len = a.hist_len;
+  xa.drafts = a.drafts;
+  xa.noise = a.noise;
+  xa.noise_stride = a.noise_stride;
+  __syncthreads();
+  const XOut xo = exact_row<STPB>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
+  finish_row(a, r, xo.status, xo.token, xo.accept, xo.sig, m, xo.last_key, PH_DONE);
+}
+
+// One row per 256-thread workgroup, in three phases with two barriers:
+//   1. merge the chunk statistics (max, argmax, flags, k-th value bound G, candidate
+//      counts);
+//   2. every thread gathers candidate positions t, t + 256, ... (eight loads in flight;
+//      a binary search over the wave-region prefixes finds each slot), divides by T,
+//      prunes with min-p on the row maximum and with G, compacts the survivors into its
+//      wave's LDS segment and, for top-k rows, counts them in a histogram of m - l over
+//      the survivors' span;
+//   3. wave 0 alone: top-k (from the histogram), sort, top-p, draw, with wave-wide
+//      operations only.
+__device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams& p,
+                             FinalShared& S) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int V = a.V, W = a.W;
+  const bool vdr = a.verify && j < a.k;  // a verify row with a draft
+  RowState* rsp = &a.s.rs[r];
+  // the row's remaining global inputs, requested before anything waits
+  const int draft = vdr ? a.drafts[(int64_t)b * a.k + j] : -1;
+  const float l_draft = vdr ? rsp->l_draft : -INFINITY;
+  float u_draw = 0.0f, u_acc = 0.0f;
+  if (a.noise && !p.greedy) {
+    const float* nz = a.noise + (int64_t)r * a.noise_stride;
+    if (a.noise_mode == STRIM_NOISE_ICDF) {
+      u_draw = nz[0];
+      u_acc = nz[1];
+    } else {
+      u_acc = nz[V];
+    }
+  }
+
+  // ---- phase 1: chunk statistics (W <= 256: one chunk per thread) -----------------
+  ChunkStat cs{-INFINITY, -1, 0, 0, 0.0, 0u, -INFINITY};
+  if (t < W) cs = a.s.cstat[(int64_t)r * a.s.wmax + t];
+  uint32_t ctot = 0u;
+  int ff = cs.flags | (cs.n > 0 ? 4 : 0);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t ce = (cs.nslot >> (8 * e)) & 255u;
+    if (ce > (uint32_t)SLOTW) ff |= 2;  // a wave region overflowed
+    ctot += ce;
+  }
+  float mv = cs.m, gv = cs.g;
+  int mi = cs.arg;
+  wave_argmax(mv, mi);
+  ff = wave_or_i(ff);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, WAVE));
+  uint32_t wtot;
+  const uint32_t wex = wave_excl_scan_u32(ctot, &wtot);
+  if (t < W) {
+    uint32_t o = wex;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      S.rpre[4 * t + e] = o;
+      o += (cs.nslot >> (8 * e)) & 255u;
+    }
+  }
+  if (t < 256) S.hist[t] = 0u;
+  if (lane == 0) {
+    S.v[w] = mv;
+    S.i[w] = mi;
+    S.f[w] = ff;
+    S.g[w] = gv;
+    S.off[w] = wtot;
+  }
+  __syncthreads();
+  float m = S.v[0], G = S.g[0];
+  int arg = S.i[0], flags = S.f[0];
+  uint32_t n_c = 0u;
+#pragma unroll
+  for (int q = 0; q < STPB / WAVE; ++q) {
+    if (q > 0) {
+      argmax_merge(m, arg, S.v[q], S.i[q]);
+      flags |= S.f[q];
+      G = fmaxf(G, S.g[q]);
+    }
+    n_c += S.off[q];
+  }
+
+  int status = STRIM_OK;
+  if (vdr && (draft < 0 || draft >= V)) status = STRIM_EINVAL;
+  if (status == STRIM_OK && (flags & 1)) status = STRIM_ENONFINITE;
+  if (status == STRIM_OK && !(flags & 4)) status = STRIM_EEMPTY;
+  if (status != STRIM_OK) {
+    finish_row(a, r, status, -1, 0, 0.0, m, 0ull, PH_DONE);
+    return;
+  }
+  if (p.greedy) {
+    finish_row(a, r, STRIM_OK, arg, vdr && arg == draft, 1.0, m, 0ull, PH_DONE);
+    return;
+  }
+  const bool topk = p.top_k > 0 && p.top_k < V;
+  const bool topp = p.top_p < 1.0f;
+  const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
+  const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
+  const bool cand_sorted = no_lse ? topp : (topk || topp);
+  const uint64_t pkey = mix64(p.seed, p.position);
+  const int excl_id = vdr ? draft : -1;
+  if (!a.noise) {
+    u_draw = philox_uniform(pkey, 0);
+    u_acc = philox_uniform(pkey, a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
+  }
+
+  // ---- unfiltered Gumbel rows: the chunks' two best tokens ------------------------
+  if (p.cls == CLS_GENERAL && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, V)) {
+    const double wc = (t < W && cs.n > 0) ? cs.S * exp((double)cs.m - (double)m) : 0.0;
+    const double sig = block_sum_f64<STPB>(wc, S.d);
+    const double lse = log(sig);
+    double bsc = -INFINITY;
+    uint64_t btk = ~0ull;
+    int bid = -1;
+    if (t < W) {
+      const ChunkPart pt = a.s.part[(int64_t)r * a.s.wmax + t];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int id = h == 0 ? pt.id0 : pt.id1;
+        const float l = h == 0 ? pt.l0 : pt.l1;
+        if (id < 0 || id == excl_id) continue;
+        const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
+                                : philox_uniform(pkey, (uint64_t)id);
+        const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
+        const double sc = base + gumbel64(u);
+        if (bid < 0 || sc > bsc || (sc == bsc && (uint64_t)id < btk)) {
+          bsc = sc; btk = (uint64_t)id; bid = id;
+        }
+      }
+    }
+    block_argmax_score<STPB>(bsc, btk, bid, S.d, S.u, S.i, &S.misc[3]);
+    int token = S.misc[3];
+    int acc = 0;
+    if (vdr) {
+      const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
+      acc = ((double)u_acc < w_d / sig) ? 1 : 0;
+      if (token < 0) token = arg;  // the draft is the only allowed token
+    }
+    finish_row(a, r, STRIM_OK, token, acc, sig, m, ~0ull, PH_DONE);
+    return;
+  }
+  if (p.cls != CLS_FAST) {
+    finish_row(a, r, STRIM_OK, -1, 0, 0.0, m, 0ull, PH_PENDING);
+    return;
+  }
+  if ((flags & 2) || n_c > (uint32_t)FCAND) {
+    finalize_exact(a, r, b, j, p, m, arg, draft, vdr, l_draft, S);
+    return;
+  }
+
+  // ---- phase 2: gather, divide, prune, compact --------------------------------------
+  // every kept token has v >= G (the k-th value bound), minus the l-tie margin
+  const float Gm = topk && G > -INFINITY ? G - (fabsf(G) * 1e-6f + 1e-30f) : -INFINITY;
+  const bool minp = p.min_p > 0.0f;
+  const double lmp = minp ? log((double)p.min_p) : 0.0;
+  // top-k histogram of d = m - l over the survivors' span (bounded by G or min-p)
+  float dspan = 16.0f;
+  if (Gm > -INFINITY) dspan = fminf(dspan, m - Gm / p.T);
+  if (minp) dspan = fminf(dspan, (float)-lmp);
+  const float scale = 255.0f / fmaxf(dspan * 1.0001f, 1e-6f);
+  const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
+  const int nreg = 4 * W;
+  // global position of region rg's first candidate
+  auto gpre = [&](int rg) {
+    uint32_t o = S.rpre[rg];
+    const int blk = rg >> 8;  // 64 chunks (256 regions) per wave of phase 1
+#pragma unroll
+    for (int q = 0; q < STPB / WAVE; ++q)
+      if (q < blk) o += S.off[q];
+    return o;
+  };
+  constexpr int GB = 8;  // loads in flight per thread per batch
+  uint32_t n_w = 0u;     // survivors in this wave's segment
+  for (int base = 0; base < (int)n_c; base += GB * STPB) {
+    Cand cd[GB];
+#pragma unroll
+    for (int q = 0; q < GB; ++q) {
+      const int pos = base + q * STPB + t;
+      cd[q] = Cand{-INFINITY, -1};
+      if (pos < (int)n_c) {
+        int lo = 0, hi = nreg - 1;  // last region whose first position <= pos
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if ((int)gpre(mid) <= pos) lo = mid;
+          else hi = mid - 1;
+        }
+        cd[q] = slots[(int64_t)lo * SLOTW + (pos - (int)gpre(lo))];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < GB; ++q) {
+      // l = v / T as the oracle rounds it
+      bool k = cd[q].id >= 0 && cd[q].l >= Gm;
+      const float l = k ? cd[q].l / p.T : -INFINITY;
+      k = k && l > -INFINITY && (!minp || ((double)l - (double)m) >= lmp);
+      const uint64_t msk = __ballot(k);
+      if (msk) {
+        const uint32_t dst = n_w + (uint32_t)lanes_below(msk);
+        if (k && dst < (uint32_t)FSEG) S.key[w * FSEG + dst] = ckey(l, cd[q].id);
+        if (k && topk) atomicAdd(&S.hist[dbin(m, l, scale)], 1u);
+        n_w += (uint32_t)__popcll(msk);
+      }
+    }
+  }
+  if (lane == 0) S.off[w] = n_w;
+  __syncthreads();
+  uint32_t segn[STPB / WAVE];
+  int over = 0;
+  uint32_t n_s = 0u;
+#pragma unroll
+  for (int q = 0; q < STPB / WAVE; ++q) {
+    segn[q] = S.off[q];
+    over |= segn[q] > (uint32_t)FSEG;
+    n_s += segn[q];
+  }
+  if (over) {
+    finalize_exact(a, r, b, j, p, m, arg, draft, vdr, l_draft, S);
+    return;
+  }
+  if (w != 0) return;  // phase 3 is one wave
+  // concatenate the wave segments
+  {
+    uint32_t o = segn[0];
+#pragma unroll
+    for (int q = 1; q < STPB / WAVE; ++q) {
+      for (uint32_t i = lane; i < segn[q]; i += WAVE) S.key[o + i] = S.key[q * FSEG + i];
+      o += segn[q];
+    }
+    wave_sync();
+  }
+  int n = (int)n_s;
+
+  // ---- phase 3a: top-k -- the survivors up to the histogram bin holding the k-th ----
+  bool sorted = false;
+  if (topk && n > p.top_k) {
+    const uint4 h = *(const uint4*)&S.hist[4 * lane];
+    const uint32_t own = h.x + h.y + h.z + h.w;
+    uint32_t tot;
+    uint32_t cum = wave_excl_scan_u32(own, &tot);
+    const uint32_t hs[4] = {h.x, h.y, h.z, h.w};
+    int bl = 256;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (bl == 256 && cum + hs[e] >= (uint32_t)p.top_k) bl = 4 * lane + e;
+      cum += hs[e];
+    }
+    const int bstar = wave_min_i(bl);
+    // keep the keys in bins <= bstar (a superset of the top k)
+    uint32_t n2 = 0u;
+    for (int base = 0; base < n; base += WAVE) {
+      const int pos = base + lane;
+      const uint64_t kv = pos < n ? S.key[pos] : ~0ull;
+      const bool keep = pos < n && dbin(m, fkey_desc_inv((uint32_t)(kv >> 32)), scale) <= bstar;
+      const uint64_t msk = __ballot(keep);
+      wave_sync();
+      if (keep) S.key[n2 + (uint32_t)lanes_below(msk)] = kv;
+      n2 += (uint32_t)__popcll(msk);
+      wave_sync();
+    }
+    n = (int)n2;
+    uint64_t kth;
+    if (n <= WAVE) {
+      const uint64_t kv = wave_sort_u64(lane < n ? S.key[lane] : ~0ull);
+      wave_sync();
+      S.key[lane] = kv;
+      wave_sync();
+      kth = shfl_u64(kv, p.top_k - 1);
+    } else if (n <= 1024) {
+      wave_sort_lds(S.key, n);
+      kth = S.key[p.top_k - 1];
+    } else {
+      kth = wave_radix_kth(S.key, n, (uint32_t)p.top_k, S.hist);
+      uint32_t n3 = 0u;
+      for (int base = 0; base < n; base += WAVE) {
+        const int pos = base + lane;
+        const uint64_t kv = pos < n ? S.key[pos] : ~0ull;
+        const bool keep = pos < n && (uint32_t)(kv >> 32) <= (uint32_t)(kth >> 32);
+        const uint64_t msk = __ballot(keep);
+        wave_sync();
+        if (keep) S.key[n3 + (uint32_t)lanes_below(msk)] = kv;
+        n3 += (uint32_t)__popcll(msk);
+        wave_sync();
+      }
+      n = (int)n3;
+      wave_sort_lds(S.key, n);
+    }
+    sorted = true;
+    // the kept prefix: k keys, or with ties every key sharing the k-th value
+    const bool ties = (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) != 0;
+    const uint64_t bound = ties ? (kth | 0xFFFFFFFFull) : kth;
+    int c = 0;
+    for (int base = 0; base < n; base += WAVE) {
+      const int pos = base + lane;
+      c += (pos < n && S.key[pos] <= bound) ? 1 : 0;
+    }
+    n = wave_sum(c);
+  }
+  // ---- phase 3b: sort the survivors ---------------------------------------------
+  if (!sorted) {
+    if (n <= WAVE) {
+      const uint64_t kv = wave_sort_u64(lane < n ? S.key[lane] : ~0ull);
+      wave_sync();
+      S.key[lane] = kv;
+      wave_sync();
+    } else {
+      wave_sort_lds(S.key, n);
+    }
+  }
+
+  // ---- phase 3c: top-p over the sorted survivors ----------------------------------
+  // lane owns positions [lane*Qn, lane*Qn + Qn); with n <= 64 (Qn = 1) its weight is
+  // computed once
+  const int Qn = (n + WAVE - 1) / WAVE;
+  const int p0 = lane * Qn, p1 = min(n, p0 + Qn);
+  const uint64_t* keys = S.key;
+  auto weight = [&](int q) {
+    return exp((double)fkey_desc_inv((uint32_t)(keys[q] >> 32)) - (double)m);
+  };
+  const double w0 = p0 < p1 ? weight(p0) : 0.0;
+  double loc = w0;
+  for (int q = p0 + 1; q < p1; ++q) loc += weight(q);
+  double S_pre;
+  const double ex = wave_excl_scan_f64(loc, &S_pre);
+  int n_keep = n;
+  if (topp) {
+    const double P = (double)p.top_p;
+    int fd = n;
+    double run = ex;
+    for (int q = p0; q < p1; ++q) {
+      if (run / S_pre - P > 0.0) {
+        fd = q;
+        break;
+      }
+      run += q == p0 ? w0 : weight(q);
+    }
+    n_keep = wave_min_i(fd);
+  }
+  const int k1 = min(p1, n_keep);
+  loc = 0.0;
+  for (int q = p0; q < k1; ++q) loc += q == p0 ? w0 : weight(q);
+  double S_kept;
+  const double exk = wave_excl_scan_f64(loc, &S_kept);
+  const uint64_t last_key = keys[n_keep - 1];
+
+  // the draft of a verify row: kept iff its key is inside the kept prefix
+  double w_d = 0.0;
+  uint64_t key_d = ~0ull;
+  if (vdr && l_draft > -INFINITY) {
+    key_d = ckey(l_draft, draft);
+    if (key_d <= last_key) w_d = exp((double)l_draft - (double)m);
+  }
+
+  // ---- phase 3d: draw -----------------------------------------------------------
+  int token;
+  if (a.noise_mode == STRIM_NOISE_ICDF) {
+    const double tgt = (double)u_draw * (S_kept - w_d);
+    int best = n_keep;
+    double run = exk;
+    for (int q = p0; q < k1; ++q) {
+      const uint64_t key = keys[q];
+      const double wq = q == p0 ? w0 : weight(q);
+      double before = run;
+      if (key_d < key) before -= w_d;
+      if ((int)(uint32_t)key != excl_id && wq > 0.0 && before + wq > tgt) {
+        best = q;
+        break;
+      }
+      run += wq;
+    }
+    int bp = wave_min_i(best);
+    if (bp >= n_keep) {
+      // rounding pushed the target past the end, or the residual is empty (only the
+      // draft kept): the last kept token other than the draft, else the first kept
+      bp = n_keep - 1;
+      if ((int)(uint32_t)keys[bp] == excl_id) bp = bp > 0 ? bp - 1 : 0;
+      if (S_kept - w_d <= 0.0) bp = 0;
+    }
+    token = (int)(uint32_t)keys[bp];
+  } else {
+    const double lse = log(S_kept);
+    double bsc = -INFINITY;
+    uint64_t btk = ~0ull;
+    int bid = -1;
+    for (int q = p0; q < k1; ++q) {
+      const uint64_t key = keys[q];
+      const int id = (int)(uint32_t)key;
+      if (id == excl_id) continue;
+      const float l = fkey_desc_inv((uint32_t)(key >> 32));
+      const int64_t nidx = by_rank ? (int64_t)q : (int64_t)id;
+      const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + nidx]
+                              : philox_uniform(pkey, (uint64_t)nidx);
+      const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
+      const double sc = base + gumbel64(u);
+      const uint64_t tk = cand_sorted ? key : (uint64_t)id;
+      if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) { bsc = sc; btk = tk; bid = id; }
+    }
+    token = wave_argmax_score(bsc, btk, bid);
+    if (token < 0) token = (int)(uint32_t)keys[0];  // every score -inf / only the draft kept
+  }
+  const int acc = vdr && ((double)u_acc < w_d / S_kept) ? 1 : 0;
+  finish_row(a, r, STRIM_OK, token, acc, S_kept, m, last_key, PH_DONE);
+}
+
+// ---------------------------------------------------------------------------------
+// k_finalize: one workgroup per row, after k_stream (the kernel boundary makes every
+// chunk's results visible; an in-kernel device-scope release per workgroup costs far
+// more on gfx950 than the second launch)
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(STPB) void k_finalize(Args a) {
+  __shared__ FinalShared S;
+  const int r = blockIdx.x;
+  int b, j;
+  row_bj(a, r, b, j);
+  const RowParams p = load_params(a, b, j);
+  finalize_row(a, r, b, j, p, S);
+}
+
+}  // namespace strim

@@ -131,6 +131,16 @@ struct Args {
   strim_sampling_params p[MAXP];  // per batch row of the group
 };
 
+// Launches kernel `fn(Args)` on st. Given a start/stop event pair, the events take the
+// dispatch's own begin and end timestamps (hipExtLaunchKernel), so their elapsed time is
+// the kernel's execution alone, without the queue's gap before it.
+inline hipError_t launch_args(const void* fn, dim3 grid, dim3 block, const Args& a,
+                              hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  void* args[] = {const_cast<Args*>(&a)};
+  if (e0 && e1) return hipExtLaunchKernel(fn, grid, block, args, 0, st, e0, e1, 0);
+  return hipLaunchKernel(fn, grid, block, args, 0, st);
+}
+
 struct RowParams {
   float T, rep, pres, freq, min_p, top_p;
   int32_t top_k;

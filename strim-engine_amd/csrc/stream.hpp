@@ -1,0 +1,343 @@
+// stream.hpp — k_stream: the single streaming pass over the logits.
+//
+// A 256-thread workgroup owns one (row, chunk of 4096 tokens); thread t owns the two
+// 8-token segments t and t + 256, so every wave-wide load is 1 KB (bf16) of contiguous
+// logits. All global loads of a workgroup (logits, allow-bits, history ids) are issued
+// before its first barrier. The workgroup writes its chunk statistics and either its
+// local candidates (fast rows) or the pass-1 histograms of general rows; k_finalize
+// (finalize_kernels.hip) then decides each row.
+//
+// The kernel is a template over the logits dtype, 16-byte alignment, penalties and the
+// allow-mask, so each launch runs straight-line per-token code. stream_kernels.hip is
+// built once per (dtype, penalties) pair, each object holding that pair's launcher.
+#pragma once
+
+#include "select.hpp"
+
+namespace strim {
+
+constexpr int SSEG = CHUNK / (STPB * EPT);  // 8-token segments per thread
+static_assert(SSEG == 2, "k_stream geometry");
+
+// LDS of one k_stream workgroup.
+struct StreamShared {
+  uint32_t cnt[CHUNK];          // history counts of the chunk's tokens (16 KB)
+  uint32_t hc[NCB];
+  unsigned long long hm[NCB];
+  uint32_t lad[2 * WAVE];
+  float v[STPB / WAVE];
+  int i[STPB / WAVE], n[STPB / WAVE], f[STPB / WAVE];
+  uint32_t off[STPB / WAVE];
+  double d[STPB / WAVE];
+  float tf[4 * STPB / WAVE];
+  int ti[2 * STPB / WAVE];
+};
+
+// ---------------------------------------------------------------------------------
+// k_stream
+// ---------------------------------------------------------------------------------
+// Ladder rung of dv = vmax - v >= 0 read from the float's bits: exponent and the top
+// three mantissa bits, so consecutive rungs differ by 2^(1/8) in dv. Rung 0 holds
+// dv < 2^-10, the last rung everything from 2^5.875 on. Monotone in dv.
+constexpr int VRUNG = 128;
+constexpr uint32_t VRUNG0 = (127u - 10u) << 3;
+__device__ __forceinline__ int dv_rung(float dv) {
+  const int r = (int)(__float_as_uint(dv) >> 20) - (int)VRUNG0;
+  return r < 0 ? 0 : (r > VRUNG - 1 ? VRUNG - 1 : r);
+}
+// Smallest dv above rung r (r < VRUNG - 1).
+__device__ __forceinline__ float dv_rung_end(int r) {
+  return __uint_as_float(((uint32_t)r + 1u + VRUNG0) << 20);
+}
+
+// The 8 tokens [i0, i0 + 8) of row r as float32 (bf16 widened exactly). FULL: the
+// chunk lies inside the row and rows are 16-byte aligned, so one or two vector loads.
+template <int DT, bool FULL>
+__device__ __forceinline__ void load_seg(const Args& a, int r, int i0, float (&x)[EPT]) {
+  const int64_t base = (int64_t)r * a.row_stride;
+  if constexpr (DT == STRIM_DTYPE_BF16) {
+    const uint16_t* xb = (const uint16_t*)a.logits + base;
+    if constexpr (FULL) {
+      const uint4 v = *(const uint4*)(xb + i0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = __uint_as_float(w[e] << 16);
+        x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? bf16_to_f32(xb[i0 + e]) : -INFINITY;
+    }
+  } else {
+    const float* xf = (const float*)a.logits + base;
+    if constexpr (FULL) {
+      const float4 v0 = *(const float4*)(xf + i0);
+      const float4 v1 = *(const float4*)(xf + i0 + 4);
+      x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+      x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? xf[i0 + e] : -INFINITY;
+    }
+  }
+}
+
+// DT: logits dtype; VEC: rows are 16-byte aligned; PEN: some row of the launch has
+// penalties; MASK: allow-bits are given. The host picks the instantiation, so each
+// launch runs straight-line per-token code.
+template <int DT, bool VEC, bool PEN, bool MASK>
+__global__ __launch_bounds__(STPB) void k_stream(Args a) {
+  __shared__ StreamShared S;
+  uint32_t* s_cnt = S.cnt;
+
+  int r, c;
+  map_block(r, c);
+  int b, j;
+  row_bj(a, r, b, j);
+  const RowParams p = load_params(a, b, j);
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int c0 = c * CHUNK;
+  const bool full = VEC && c0 + CHUNK <= a.V;
+  int i0[SSEG];
+  float v[SSEG][EPT];
+  uint32_t bits[SSEG];
+#pragma unroll
+  for (int s = 0; s < SSEG; ++s) {
+    i0[s] = c0 + (s * STPB + t) * EPT;
+    if (full) load_seg<DT, true>(a, r, i0[s], v[s]);
+    else load_seg<DT, false>(a, r, i0[s], v[s]);
+    bits[s] = 0xFFu;
+    if constexpr (MASK) {
+      if (a.mask && i0[s] < a.V)
+        bits[s] = ((const uint8_t*)(a.mask + (int64_t)r * a.mask_stride))[i0[s] >> 3];
+    }
+  }
+  for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
+  if (t < NCB) {
+    S.hc[t] = 0u;
+    S.hm[t] = 0ull;
+  }
+  const bool pen = PEN && p.pen;
+  if (pen) build_counts_pre<STPB, CHUNK>(a, b, j, c0, s_cnt);
+
+  // ---- penalties and mask, before temperature ("v space") ------------------------
+  // Dividing by T > 0 is monotone, so maxima and candidate bounds are found on v; only
+  // the chunk maximum and (in k_finalize) the candidates are divided. Tokens past the
+  // row end load as -inf (not allowed).
+  bool nf = false;
+  float vmax = -INFINITY;
+  int vid = -1;
+#pragma unroll
+  for (int s = 0; s < SSEG; ++s) {
+    uint32_t cnt[EPT];
+    if (pen) {
+      const uint4 c4a = *(const uint4*)(s_cnt + (i0[s] - c0));
+      const uint4 c4b = *(const uint4*)(s_cnt + (i0[s] - c0) + 4);
+      cnt[0] = c4a.x; cnt[1] = c4a.y; cnt[2] = c4a.z; cnt[3] = c4a.w;
+      cnt[4] = c4b.x; cnt[5] = c4b.y; cnt[6] = c4b.z; cnt[7] = c4b.w;
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      float y = v[s][e];
+      if (pen && cnt[e] > 0u) {
+        y = y > 0.0f ? y / p.rep : y * p.rep;
+        y = y - p.freq * (float)cnt[e];
+        y = y - p.pres;
+      }
+      if constexpr (MASK) y = ((bits[s] >> e) & 1u) ? y : -INFINITY;
+      nf |= !(y < INFINITY);  // NaN or +inf in an allowed position
+      v[s][e] = y;
+      // ids rise with (s, e): a strict compare keeps the first maximum
+      if (y > vmax) {
+        vmax = y;
+        vid = i0[s] + e;
+      }
+    }
+  }
+  if (a.verify && j < a.k) {
+    const int d = a.drafts[(int64_t)b * a.k + j];
+#pragma unroll
+    for (int s = 0; s < SSEG; ++s) {
+      const int o = d - i0[s];
+      if (o >= 0 && o < EPT) {
+        float ld = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          if (e == o) ld = v[s][e];
+        a.s.rs[r].l_draft = (ld > -INFINITY && !p.greedy) ? ld / p.T : ld;
+      }
+    }
+  }
+  if (c == 0 && t == 0) a.s.ncand[r] = 0u;
+
+  // ---- chunk max (first id on ties), allowed count, non-finite flag ---------------
+  wave_argmax(vmax, vid);
+  int n = vmax > -INFINITY ? 1 : 0;  // "some token allowed"; general rows count below
+  const int f = __any(nf) ? 1 : 0;
+  if (lane == 0) {
+    S.v[w] = vmax;
+    S.i[w] = vid;
+    S.n[w] = n;
+    S.f[w] = f;
+  }
+  __syncthreads();
+  float vm = S.v[0];
+  int a_w = S.i[0], n_w = S.n[0], f_w = S.f[0];
+#pragma unroll
+  for (int q = 1; q < STPB / WAVE; ++q) {
+    argmax_merge(vm, a_w, S.v[q], S.i[q]);
+    n_w |= S.n[q];
+    f_w |= S.f[q];
+  }
+  // chunk max after temperature; an overflow to +inf is a non-finite logit, one to -inf
+  // leaves nothing allowed
+  const float m_w = (p.greedy || !(vm > -INFINITY)) ? vm : vm / p.T;
+  if (m_w == INFINITY) f_w = 1;
+  if (!(m_w > -INFINITY)) n_w = 0;
+  ChunkStat cs{m_w, a_w, n_w, f_w, 0.0, 0u, -INFINITY};
+  const bool live = n_w > 0 && !f_w;
+
+  if (p.cls == CLS_FAST && live) {
+    // Local candidates, in v space: every token that can pass min-p (on the row maximum
+    // m >= m_w) and the chunk's top-k, written as (v, id) to the wave's slot region.
+    const bool topk = p.top_k > 0 && p.top_k < a.V;
+    // v >= vlo keeps every token with v / T >= m_w + log(min_p) (rounding margin 4e-7)
+    float vlo = -INFINITY;
+    if (p.min_p > 0.0f) {
+      const double L = (double)m_w + log((double)p.min_p);
+      const double tl = L * (double)p.T;
+      vlo = (float)(tl - fabs(tl) * 4e-7 - 1e-37);
+    }
+    if (topk) {
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          if (v[s][e] >= vlo && v[s][e] > -INFINITY) atomicAdd(&S.lad[dv_rung(vm - v[s][e])], 1u);
+      __syncthreads();
+      // every wave finds the first rung whose cumulative count reaches k (lane owns
+      // rungs 2 lane and 2 lane + 1)
+      const uint32_t h0 = S.lad[2 * lane], h1 = S.lad[2 * lane + 1];
+      uint32_t cum = h0 + h1;
+#pragma unroll
+      for (int o = 1; o < WAVE; o <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)cum, o, WAVE);
+        if (lane >= o) cum += u;
+      }
+      const uint64_t reach = __ballot(cum >= (uint32_t)p.top_k);
+      if (reach) {
+        const int ln = (int)__ffsll((long long)reach) - 1;
+        const uint32_t before = (uint32_t)__shfl((int)(cum - h0 - h1), ln, WAVE);
+        const uint32_t hl0 = (uint32_t)__shfl((int)h0, ln, WAVE);
+        const int rstar = 2 * ln + (before + hl0 >= (uint32_t)p.top_k ? 0 : 1);
+        if (rstar < VRUNG - 1) {
+          // v > vm - end(rstar) holds the rung; the margin (a few ulps of the values
+          // involved) keeps tokens whose l = v / T ties with one inside it
+          const float bnd = dv_rung_end(rstar);
+          const float thr = vm - bnd;
+          const float margin = (fabsf(vm) + fabsf(thr)) * 1e-6f + bnd * 1.6e-5f + 1e-30f;
+          vlo = fmaxf(vlo, thr - margin);
+          // the rungs up to rstar hold >= k tokens of the window, all with v >= g
+          cs.g = thr - margin;
+        }
+      }
+    }
+    uint32_t sel[SSEG];
+    int mycnt = 0;
+#pragma unroll
+    for (int s = 0; s < SSEG; ++s) {
+      sel[s] = 0u;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float y = v[s][e];
+        if (y >= vlo && y > -INFINITY) {
+          sel[s] |= 1u << e;
+          ++mycnt;
+        }
+      }
+    }
+    // each wave writes its candidates to its own region of the chunk (no atomics, no
+    // barrier); the region counts travel in cs.nslot, one byte per wave
+    int wtot;
+    const int wex = wave_excl_count32(mycnt, &wtot);
+    if (wtot <= SLOTW) {
+      Cand* dst = a.s.slot + (((int64_t)r * a.s.wmax + c) * 4 + w) * SLOTW;
+      int pos = wex;
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          if ((sel[s] >> e) & 1u) dst[pos++] = Cand{v[s][e], i0[s] + e};
+    }
+    if (lane == 0) S.off[w] = wtot <= SLOTW ? (uint32_t)wtot : 255u;
+    __syncthreads();
+    cs.nslot = S.off[0] | (S.off[1] << 8) | (S.off[2] << 16) | (S.off[3] << 24);
+  } else if (p.cls == CLS_GENERAL && live) {
+    // processed logits; chunk sum exp(l - m_w) and a coarse histogram of m_w - l
+    // (k_collect's bounds)
+    float (&l)[SSEG][EPT] = v;  // v is not needed after this
+#pragma unroll
+    for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) l[s][e] = v[s][e] > -INFINITY ? v[s][e] / p.T : -INFINITY;
+    double ssum = 0.0;
+    int na = 0;
+#pragma unroll
+    for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        if (!(l[s][e] > -INFINITY)) continue;
+        ++na;
+        const float d = m_w - l[s][e];
+        const float wgt = expf(-d);
+        ssum += (double)wgt;
+        const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
+        atomicAdd(&S.hc[bb], 1u);
+        const unsigned long long fx = __float2ull_rn(wgt * FIX_SCALE_F);
+        if (fx) atomicAdd(&S.hm[bb], fx);
+      }
+    cs.S = block_sum_f64<STPB>(ssum, S.d);
+    na = wave_sum(na);
+    if (lane == 0) S.n[w] = na;
+    __syncthreads();
+    cs.n = S.n[0] + S.n[1] + S.n[2] + S.n[3];
+    if (t < NCB) {
+      const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
+      a.s.chc[o] = S.hc[t];
+      a.s.chm[o] = S.hm[t];
+    }
+    // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
+    if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) {
+      const uint64_t key = mix64(p.seed, p.position);
+      float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
+      int id0 = -1, id1 = -1;
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          if (!(l[s][e] > -INFINITY)) continue;
+          const int id = i0[s] + e;
+          const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
+                                  : philox_uniform(key, (uint64_t)id);
+          top2_merge(s0, l0, id0, s1, l1, id1, l[s][e] + gumbel32(u), l[s][e], id, -INFINITY,
+                     0.f, -1);
+        }
+      block_top2<STPB>(s0, l0, id0, s1, l1, id1, S.tf, S.ti);
+      if (t == 0) {
+        ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
+        pt.l0 = l0; pt.id0 = id0; pt.l1 = l1; pt.id1 = id1;
+      }
+    }
+  }
+  if (t == 0) a.s.cstat[(int64_t)r * a.s.wmax + c] = cs;
+}
+
+// Launches the k_stream variant of one (dtype, penalties) pair that matches the call's
+// alignment and mask. Defined in stream_kernels.hip, one object per pair; unaligned
+// calls always take the penalties object.
+template <int DT, bool PEN>
+hipError_t launch_stream_group(const Args& a, dim3 grid, hipStream_t st, hipEvent_t e0,
+                               hipEvent_t e1);
+
+}  // namespace strim
