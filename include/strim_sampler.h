@@ -142,8 +142,10 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
  *                 reference's argmax drafter, SpecSampling.swift:17-22). Otherwise the
  *                 draft distribution q = softmax(draft_logits / T) over the draft vocab,
  *                 mapped to full-vocab ids by draft_to_full.
- *   draft_to_full [Vd] strictly ascending ids < V (Weights.swift:196-209); used only
- *                 with draft_logits.
+ *   draft_to_full [Vd] strictly ascending ids in [0, V) (Weights.swift:196-209); used
+ *                 only with draft_logits (then 0 < Vd <= V). A table that is not strictly
+ *                 ascending, or a sampled row's draft that is not in it, gives that
+ *                 sequence STRIM_EINVAL in out_status (accepted 0, token -1).
  *   draft_tokens  [B][k] full-vocab ids.
  *   params        HOST [B], as strim_sample.
  *   mask_words    [B][k+1][mask_stride] or NULL (VerifyConstraint, TokenMask.swift:7-12).
@@ -184,7 +186,8 @@ int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, in
  * strim_profile_end synchronises, sums the elapsed time per kernel and turns profiling
  * off. Profiling allocates its events in strim_profile_begin, never in the calls it
  * times. Do not profile calls that are being captured into a graph. */
-#define STRIM_KERNEL_COUNT 6 /* stream, finalize, collect, final, probs, verify_combine */
+#define STRIM_KERNEL_COUNT 7 /* stream, finalize, collect, final, probs, verify_combine,
+                                qprep */
 int strim_profile_begin(strim_ctx* ctx, int32_t max_launches);
 int strim_profile_end(strim_ctx* ctx, double* total_ms /* [STRIM_KERNEL_COUNT] */,
                       int64_t* launches /* [STRIM_KERNEL_COUNT] */);

@@ -15,6 +15,7 @@ __global__ void k_collect(Args a);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
+__global__ void k_qprep(Args a);
 __global__ void k_mask_logits(const void* logits, int dtype, int V, int64_t row_stride,
                               const uint32_t* mask, int64_t mask_stride, float* out);
 __global__ void k_draft_argmax(const void* logits, int dtype, int Vd, int64_t row_stride,
@@ -66,9 +67,11 @@ int32_t vec_ok(const void* p, int64_t row_stride, int32_t dtype) {
   return ((uintptr_t)p % 16 == 0) && (row_stride % per16 == 0) ? 1 : 0;
 }
 
-enum KernelId { KID_STREAM = 0, KID_FINALIZE, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE };
-const char* const kKernelNames[STRIM_KERNEL_COUNT] = {"k_stream", "k_finalize", "k_collect",
-                                                      "k_final", "k_probs", "k_verify_combine"};
+enum KernelId {
+  KID_STREAM = 0, KID_FINALIZE, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE, KID_QPREP
+};
+const char* const kKernelNames[STRIM_KERNEL_COUNT] = {
+    "k_stream", "k_finalize", "k_collect", "k_final", "k_probs", "k_verify_combine", "k_qprep"};
 
 // Runs `launch(e0, e1)`: with profiling on, e0/e1 are the next event pair, which the
 // launch binds to its dispatch's timestamps; otherwise both are null.
@@ -217,6 +220,11 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   const size_t o_rs = carve(R * sizeof(RowState));
   const size_t o_cand = carve(R * CAP * sizeof(Cand));
   const size_t o_nc = carve(R * sizeof(uint32_t));
+  const size_t words = ((size_t)max_vocab + 31) / 32;
+  const size_t o_dbits = carve(words * sizeof(uint32_t));
+  const size_t o_dpre = carve(words * sizeof(int32_t));
+  const size_t o_qst = carve(R * sizeof(QStat));
+  const size_t o_qflag = carve(sizeof(int32_t));
   ctx->bytes = off;
   int rc = on_device(device, [&]() -> int {
     if (hipMalloc(&ctx->base, ctx->bytes) != hipSuccess) return STRIM_ENOMEM;
@@ -238,6 +246,10 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   ctx->s.rs = (RowState*)(b + o_rs);
   ctx->s.cand = (Cand*)(b + o_cand);
   ctx->s.ncand = (uint32_t*)(b + o_nc);
+  ctx->s.dbits = (uint32_t*)(b + o_dbits);
+  ctx->s.dpre = (int32_t*)(b + o_dpre);
+  ctx->s.qst = (QStat*)(b + o_qst);
+  ctx->s.qflag = (int32_t*)(b + o_qflag);
   ctx->s.wmax = wmax;
   *out = ctx;
   return STRIM_OK;
@@ -315,9 +327,7 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
   if (B <= 0 || k < 0 || k > 64 || V <= 0 || V > ctx->max_vocab) return STRIM_EINVAL;
   if (k + 1 > ctx->max_rows) return STRIM_EINVAL;
   if (k > 0 && !draft_tokens) return STRIM_EINVAL;
-  if (draft_logits) return STRIM_EINVAL;  // general-q drafts: not supported yet
-  (void)Vd;
-  (void)draft_to_full;
+  if (draft_logits && (!draft_to_full || Vd <= 0 || Vd > V)) return STRIM_EINVAL;
   if (mask_words && mask_stride < ((int64_t)V + 31) / 32) return STRIM_EINVAL;
   if (H < 0 || (H > 0 && !history) || (history && H == 0)) return STRIM_EINVAL;
   if (noise_mode != STRIM_NOISE_ICDF && noise_mode != STRIM_NOISE_GUMBEL) return STRIM_EINVAL;
@@ -348,6 +358,11 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       a.hist_len = (history && history_len) ? history_len + g0 : nullptr;
       a.H = H;
       a.drafts = draft_tokens ? draft_tokens + (size_t)g0 * k : nullptr;
+      if (draft_logits && k > 0) {
+        a.dlog = (const char*)draft_logits + (size_t)g0 * k * Vd * dtype_size(dtype);
+        a.dtable = draft_to_full;
+        a.Vd = Vd;
+      }
       a.noise_mode = noise_mode;
       a.noise = noise ? noise + (size_t)g0 * (k + 1) * nstride : nullptr;
       a.noise_stride = nstride;
@@ -358,9 +373,19 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       a.out_row_token = out_row_token ? out_row_token + (size_t)g0 * (k + 1) : nullptr;
       a.out_status = out_status ? out_status + g0 : nullptr;
       for (int i = 0; i < nb; ++i) a.p[i] = params[g0 + i];
+      hipError_t e = hipSuccess;
+      if (a.dlog) {
+        // draft distributions (one workgroup per draft row) and, with the first group,
+        // the draft-vocab bitmap and rank prefix of the table
+        const int nwb = g0 == 0 ? (int)((((V + 31) / 32) + 255) / 256) : 0;
+        timed(ctx, KID_QPREP, [&](hipEvent_t e0, hipEvent_t e1) {
+          e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k + nwb)), dim3(256), a, st,
+                          e0, e1);
+        });
+        if (e != hipSuccess) return STRIM_EHIP;
+      }
       int rc = run_group(ctx, st, a, nb, false);
       if (rc != STRIM_OK) return rc;
-      hipError_t e = hipSuccess;
       timed(ctx, KID_COMBINE, [&](hipEvent_t e0, hipEvent_t e1) {
         e = launch_args((const void*)k_verify_combine, dim3((unsigned)((nb + 63) / 64)), dim3(64),
                         a, st, e0, e1);

@@ -28,13 +28,36 @@ struct XState {
 };
 
 // The tokens a select ranges over: allowed, passing min-p (lmp = log(min_p), -inf for
-// none), with order key in [lo, bound], other than `excl`.
+// none), with order key in [lo, bound], other than `excl`. rS != 0: the weights are the
+// general-q residual max(0, p - q) scaled by the kept mass rS (see x_wt).
 struct XUni {
   float m;
   double lmp;
   uint64_t lo, bound;
   int excl;
+  uint64_t rS;
 };
+
+// The draft distribution q of a general-q verify row: softmax(draft logits / T) over the
+// draft vocabulary, whose ids are the ascending table behind dbits / dpre.
+struct XQ {
+  const uint32_t* dbits;  // membership bitmap of the table's ids
+  const int32_t* dpre;    // table entries below each 32-token word
+  const void* dl;         // the row's draft logits [Vd]
+  int32_t dtype;
+  float T, mq;
+  double Z;
+};
+// q(id): exp(v - mq) / Z with v = draft_logit / T (fp32), 0 outside the table.
+__device__ __forceinline__ double xq_prob(const XQ& q, int id) {
+  const uint32_t bits = q.dbits[id >> 5];
+  const uint32_t bit = 1u << (id & 31);
+  if (!(bits & bit)) return 0.0;
+  const int a = q.dpre[id >> 5] + __popc(bits & (bit - 1u));
+  const float x = q.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)q.dl)[a])
+                                              : ((const float*)q.dl)[a];
+  return exp((double)(x / q.T) - (double)q.mq) / q.Z;
+}
 
 // The fields of Args the streaming passes read (the exact path is one out-of-line call,
 // so the 3 KB launch block is not copied to private memory).
@@ -49,6 +72,8 @@ struct XArgs {
   const int32_t* drafts;
   const float* noise;
   int64_t noise_stride;
+  int32_t has_q;  // a general-q verify row (q below)
+  XQ q;
 };
 
 __device__ __forceinline__ bool x_in(const XUni& u, float l, int id) {
@@ -58,6 +83,16 @@ __device__ __forceinline__ bool x_in(const XUni& u, float l, int id) {
 }
 __device__ __forceinline__ uint64_t x_weight(float l, float m) {
   return (uint64_t)__double2ull_rn(exp((double)l - (double)m) * XFIX);
+}
+// Weight of a universe token: exp(l - m) in fixed point, or, for a residual universe,
+// max(0, W - round(q * rS)): the residual (p - q)^+ in units of the kept mass rS.
+__device__ __forceinline__ uint64_t x_wt(const XArgs& a, const XUni& u, float l, int id) {
+  const uint64_t W = x_weight(l, u.m);
+  if (u.rS == 0ull) return W;
+  const double q = xq_prob(a.q, id);
+  if (q == 0.0) return W;
+  const uint64_t qS = (uint64_t)__double2ull_rn(q * (double)u.rS);
+  return W > qS ? W - qS : 0ull;
 }
 // Level-0 digit: floor(64 (m - l)), tail at XB - 1; monotone in the order.
 __device__ __forceinline__ int x_dbin(float l, float m) {
@@ -140,7 +175,7 @@ __device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, cons
         am = 0ull;
       }
       ac += 1u;
-      am += x_weight(l[e], u.m);
+      am += x_wt(a, u, l[e], i0 + e);
     }
   });
   if (cur >= 0) {
@@ -299,7 +334,8 @@ __device__ __noinline__ void x_select(const XArgs& a, int r, int b, int j, const
     const int pos = XQ * t + q;
     w4[q] = 0ull;
     if (pos < n) {
-      w4[q] = x_weight(fkey_desc_inv((uint32_t)(xs.key[pos] >> 32)), u.m);
+      const uint64_t key = xs.key[pos];
+      w4[q] = x_wt(a, u, fkey_desc_inv((uint32_t)(key >> 32)), (int)(uint32_t)key);
       lm += w4[q];
     }
   }
@@ -348,7 +384,9 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
   const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
   const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
   const bool cand_sorted = no_lse ? topp : (topk || topp);
-  XUni u{m, p.min_p > 0.0f ? log((double)p.min_p) : -INFINITY, 0ull, ~0ull, -1};
+  XUni u{m, p.min_p > 0.0f ? log((double)p.min_p) : -INFINITY, 0ull, ~0ull, -1, 0ull};
+  // general-q verify rows draw from the residual (p - q)^+ over the whole kept set
+  const bool resid = vdr && a.has_q;
   uint64_t S = 0ull;
   bool haveS = false;
   uint32_t nkeep = 0u;
@@ -381,14 +419,28 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
     W_d = x_weight(l_draft, m);
   }
   XUni ud = u;
-  ud.excl = vdr ? draft : -1;
+  ud.excl = vdr && !resid ? draft : -1;
+  if (resid && !haveS) {
+    const XLevel all{2, 0, 0ull, 0ull};
+    x_hist<NT>(a, r, b, j, p, u, all, xs.cnt, xs.hc, xs.key);
+    S = xs.key[0];
+    haveS = true;
+    __syncthreads();
+  }
   int token = -1;
   if (a.noise_mode == STRIM_NOISE_ICDF) {
     const double uu = (double)row_uniform(a, r, p, 0);
-    x_select<NT>(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
-    S = s_x.tot_m + W_d;
-    // an empty residual (only the draft kept) draws the first kept token
-    token = s_x.found ? (int)(uint32_t)s_x.key : arg;
+    if (resid) {
+      ud.rS = S;
+      x_select<NT>(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
+      // an all-zero residual draws the first kept token
+      token = (s_x.found && s_x.tot_m > 0ull) ? (int)(uint32_t)s_x.key : arg;
+    } else {
+      x_select<NT>(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
+      S = s_x.tot_m + W_d;
+      // an empty residual (only the draft kept) draws the first kept token
+      token = s_x.found ? (int)(uint32_t)s_x.key : arg;
+    }
   } else {
     if (!haveS) {
       const XLevel all{2, 0, 0ull, 0ull};
@@ -404,7 +456,16 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
     auto take = [&](float l, int id, int64_t nidx, uint64_t tk) {
       const float uq = a.noise ? a.noise[(int64_t)r * a.noise_stride + nidx]
                                : philox_uniform(pkey, (uint64_t)nidx);
-      const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
+      double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
+      if (resid) {
+        // residual score: log(p - q) where q > 0, excluded where p <= q
+        const double q = xq_prob(a.q, id);
+        if (q != 0.0) {
+          const double rr = exp(base) - q;
+          if (!(rr > 0.0)) return;
+          base = log(rr);
+        }
+      }
       const double sc = base + gumbel64(uq);
       if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) {
         bsc = sc;
@@ -451,7 +512,13 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
   const double sig = (double)S / XFIX;
   if (vdr) {
     const float ua = row_uniform(a, r, p, a.noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V : 1);
-    acc = ((double)ua < w_d / sig) ? 1 : 0;
+    double ratio = w_d / sig;
+    if (resid) {
+      // accept iff u < p(d) / q(d)
+      const double qd = xq_prob(a.q, draft);
+      ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
+    }
+    acc = ((double)ua < ratio) ? 1 : 0;
   }
   uint64_t last = u.bound;
   if (last == ~0ull && p.min_p > 0.0f) {

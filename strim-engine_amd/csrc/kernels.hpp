@@ -88,6 +88,13 @@ struct RowState {
   Bounds bd;          // general rows (k_collect)
 };
 
+// Draft distribution of one general-q verify row: q = softmax(draft logits / T).
+struct QStat {
+  float mq;     // max of draft_logit / T (fp32 division)
+  int32_t td;   // table index of the row's draft token, -1 if absent
+  double Z;     // sum of exp(v - mq), fp64
+};
+
 // Device scratch owned by a context (allocated once in strim_ctx_create).
 struct Scratch {
   ChunkStat* cstat;               // [rows][wmax]
@@ -99,6 +106,10 @@ struct Scratch {
   RowState* rs;                   // [rows]
   Cand* cand;                     // [rows][CAP]
   uint32_t* ncand;                // [rows]
+  uint32_t* dbits;                // [ceil(V/32)] general-q verify: draft-vocab membership
+  int32_t* dpre;                  // [ceil(V/32)] table entries below id 32 w
+  QStat* qst;                     // [rows] per draft row (b * k + j)
+  int32_t* qflag;                 // [1] 1 when the draft table is valid
   int32_t wmax;
 };
 
@@ -117,6 +128,9 @@ struct Args {
   const int32_t* hist_len;
   int32_t H;
   const int32_t* drafts;  // [B][k] (group-relative)
+  const void* dlog;       // general-q verify: draft logits [B][k][Vd] (dtype), or NULL
+  const int32_t* dtable;  // [Vd] strictly ascending full-vocab ids
+  int32_t Vd;
   int32_t noise_mode;
   const float* noise;
   int64_t noise_stride;

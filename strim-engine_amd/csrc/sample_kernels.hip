@@ -203,6 +203,7 @@ __global__ __launch_bounds__(TPB) void k_collect(Args a) {
   const RowParams p = load_params(a, b, j);
   if (p.cls != CLS_GENERAL) return;
   if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) return;
+  if (a.s.rs[r].phase == PH_DONE) return;  // decided by k_finalize (errors, general-q rows)
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int c0 = c * CHUNK, i0 = c0 + t * EPT;
 
@@ -748,6 +749,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   xa.drafts = a.drafts;
   xa.noise = a.noise;
   xa.noise_stride = a.noise_stride;
+  xa.has_q = 0;  // general-q rows are decided in k_finalize
   const XOut xo = exact_row<FIN_T>(xa, r, b, j, p, m, st.arg, draft, verify_draft_row,
                             verify_draft_row ? rsp->l_draft : -INFINITY, xs, s_x);
   if (t == 0) rsp->bd.mode = MODE_A;  // kept set = order prefix up to last_key
@@ -834,6 +836,83 @@ __global__ void k_verify_combine(Args a) {
   a.out_accepted[b] = n;
   a.out_token[b] = token;
   if (a.out_status) a.out_status[b] = status;
+}
+
+// ---------------------------------------------------------------------------------
+// k_qprep: general-q verify inputs (runs before k_stream)
+// ---------------------------------------------------------------------------------
+// Lower bound of `id` in the ascending table [0, n).
+__device__ __forceinline__ int table_lower_bound(const int32_t* tab, int n, int id) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (tab[mid] < id) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// Blocks [0, B*k): one draft row each: mq = max(draft_logit / T) (fp32 division, as the
+// target's temperature), Z = sum exp(v - mq) in fp64, and the table index of the row's
+// draft token (the draft distribution of SpecSampling's general-q extension). Block 0
+// also checks that the table is strictly ascending inside [0, V). Blocks after them: one
+// thread per 32-token word of the vocabulary: the bitmap of table ids and the number of
+// table entries below the word (so a member's table index is that prefix plus the
+// popcount of the lower bits).
+__global__ __launch_bounds__(256) void k_qprep(Args a) {
+  __shared__ float s_m[256 / WAVE];
+  __shared__ double s_d[256 / WAVE];
+  __shared__ int s_bad[256 / WAVE];
+  const int t = threadIdx.x;
+  const int nq = a.B * a.k, Vd = a.Vd;
+  const int blk = blockIdx.x;
+  if (blk < nq) {
+    const int b = blk / a.k, j = blk % a.k;
+    if (blk == 0) {
+      int bad = 0;
+      for (int i = t; i < Vd; i += 256) {
+        const int id = a.dtable[i];
+        if (id < 0 || id >= a.V || (i + 1 < Vd && !(id < a.dtable[i + 1]))) bad = 1;
+      }
+      bad = block_or<256>(bad, s_bad);
+      if (t == 0) *a.s.qflag = bad ? 0 : 1;
+    }
+    const float T = a.p[b].temperature;
+    QStat q{-INFINITY, -1, 0.0};
+    if (T > 0.0f) {
+      const size_t base = (size_t)blk * (size_t)Vd;
+      auto ld = [&](int i) -> float {
+        return a.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.dlog)[base + i])
+                                           : ((const float*)a.dlog)[base + i];
+      };
+      float mx = -INFINITY;
+      for (int i = t; i < Vd; i += 256) mx = fmaxf(mx, ld(i) / T);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, WAVE));
+      if ((t & (WAVE - 1)) == 0) s_m[t / WAVE] = mx;
+      __syncthreads();
+      mx = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+      double z = 0.0;
+      for (int i = t; i < Vd; i += 256) z += exp((double)(ld(i) / T) - (double)mx);
+      z = block_sum_f64<256>(z, s_d);
+      q.mq = mx;
+      q.Z = z;
+      const int d = a.drafts[(int64_t)b * a.k + j];
+      const int pos = table_lower_bound(a.dtable, Vd, d);
+      q.td = (pos < Vd && a.dtable[pos] == d) ? pos : -1;
+    }
+    if (t == 0) a.s.qst[blk] = q;
+    return;
+  }
+  const int w = (blk - nq) * 256 + t;
+  const int words = (a.V + 31) / 32;
+  if (w >= words) return;
+  const int lo = table_lower_bound(a.dtable, Vd, 32 * w);
+  const int hi = table_lower_bound(a.dtable, Vd, 32 * w + 32);
+  uint32_t bits = 0u;
+  for (int i = lo; i < hi; ++i) bits |= 1u << ((a.dtable[i] - 32 * w) & 31);
+  a.s.dbits[w] = bits;
+  a.s.dpre[w] = lo;
 }
 
 }  // namespace strim

@@ -37,7 +37,7 @@ EXPORTS = (
     "strim_profile_end",
     "strim_kernel_name",
 )
-KERNEL_COUNT = 6
+KERNEL_COUNT = 7
 
 
 class StrimError(RuntimeError):

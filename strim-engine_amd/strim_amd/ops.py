@@ -182,6 +182,13 @@ class Context:
         H = 0 if history is None else history.shape[-1]
         mstride = 0 if mask is None else mask.shape[-1]
         Vd = 0 if draft_logits is None else draft_logits.shape[-1]
+        if draft_logits is not None:
+            if draft_logits.dtype != target_logits.dtype:
+                raise ValueError("draft_logits must have the target logits' dtype")
+            if tuple(draft_logits.shape) != (B, k, Vd) or not draft_logits.is_contiguous():
+                raise ValueError(f"draft_logits must be contiguous [{B}, {k}, Vd]")
+            if draft_to_full is None or draft_to_full.numel() != Vd:
+                raise ValueError("draft_to_full must hold Vd ids")
         rc = N.lib().strim_verify(self._h, _stream(stream), _ptr(target_logits),
                                   _dtype_code(target_logits), B, k, V, _ptr(draft_logits), Vd,
                                   _ptr(draft_to_full), _ptr(draft_tokens), _pp(p), _ptr(mask),

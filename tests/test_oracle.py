@@ -319,6 +319,40 @@ def test_general_q_reduces_to_one_hot(oracle_mod):
             np.testing.assert_array_equal(one[key], gen[key])
 
 
+@pytest.mark.parametrize("t,k,pp", [(1.0, 0, 1.0), (0.7, 0, 1.0), (1.0, 6, 0.9)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_general_q_marginal_matches_target(oracle_mod, t, k, pp, mode):
+    # Speculative sampling with a non-degenerate draft distribution q: the draft is drawn
+    # from q, accepted with probability min(1, p(d)/q(d)), else replaced by a draw from
+    # (p - q)^+. The emitted token must follow the filtered target P, and the acceptance
+    # rate must be sum_i min(p_i, q_i). A dropped max(0, .), a residual normalised by the
+    # wrong mass or an accept ratio inverted fails one of the two checks.
+    rng = np.random.default_rng(31 + mode)
+    V, n = 16, 200_000
+    row = (rng.normal(size=V) * 1.5).astype(np.float32)
+    P = _probs(oracle_mod, row, temperature=t, top_k=k, top_p=pp)
+    table = np.sort(rng.choice(V, size=11, replace=False)).astype(np.int32)
+    dlog = (rng.normal(size=table.size) * 1.5).astype(np.float32)
+    qd = np.exp(dlog.astype(np.float64) / t - (dlog / np.float32(t)).max())
+    qd /= qd.sum()
+    Q = np.zeros(V)
+    Q[table] = qd
+    draft = table[rng.choice(table.size, size=n, p=qd)].astype(np.int32)
+    tgt = np.repeat(np.repeat(row[None, None], 2, 1), n, 0)
+    dl = np.repeat(dlog[None, None], n, 0)
+    p = oracle_mod.make_params(n, temperature=t, top_k=k, top_p=pp, seed=4000 + mode)
+    p["position"] = np.arange(n, dtype=np.uint64) * 2
+    out = oracle_mod.verify(tgt, 1, draft[:, None], p, draft_logits=dl, draft_to_full=table,
+                            noise_mode=mode)
+    assert (out["status"] == 0).all()
+    acc = out["row_accept"][:, 0].astype(bool)
+    emitted = np.where(acc, draft, out["row_token"][:, 0])
+    stat, crit = _chi2(np.bincount(emitted, minlength=V).astype(np.float64), P)
+    assert stat < crit, (t, k, pp, mode, stat, crit)
+    expect = np.minimum(P, Q).sum()
+    assert abs(acc.mean() - expect) < 4 * math.sqrt(expect * (1 - expect) / n) + 1e-3
+
+
 def test_bf16_round_matches_torch():
     import torch
 

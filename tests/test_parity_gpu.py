@@ -8,7 +8,8 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import check_sample, check_verify, dev, dev_logits, run_sample
+from gpu_util import (check_sample, check_verify, dev, dev_logits, host_logits, run_sample,
+                      run_verify)
 from strim_amd import ops
 from strim_amd import workloads as W
 
@@ -309,6 +310,75 @@ def test_verify_random(ctx, k):
             say(f"verify k={k} it={it} B={B} V={V} mode={mode}")
             check_verify(ctx, tgt, k, drafts, p, "bf16", mask, hist, None, mode,
                          label=f"verify k={k} it={it}")
+
+
+# ------------------------------------------------------------ general-q verify ----
+@pytest.mark.parametrize("mode", [O.NOISE_ICDF, O.NOISE_GUMBEL])
+def test_verify_general_q_cfg4(ctx, mode):
+    # configuration 4: target [4,4,V] bf16, draft logits [4,3,32768] over an ascending
+    # injective table, drafts sampled from q, T 0.7, Philox uniforms per position
+    w = W.cfg4()
+    say(f"verify general-q cfg4 mode={mode}")
+    check_verify(ctx, w["target"], w["k"], w["drafts"], w["params"], "bf16", noise_mode=mode,
+                 draft_logits=w["draft_logits"], table=w["table"], label=f"cfg4 mode={mode}")
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_verify_general_q_random(ctx, k):
+    rng = np.random.default_rng(70 + k)
+    for it in range(4):
+        B = int(rng.choice([2, 5]))
+        V = int(rng.choice([300, 5000, 20000]))
+        Vd = int(rng.choice([V // 4, V // 2]))
+        table = np.sort(rng.choice(V, size=Vd, replace=False)).astype(np.int32)
+        tgt = rng.normal(0, 2.0, size=(B, k + 1, V)).astype(np.float32)
+        dl = (0.6 * tgt[:, :k, :][:, :, table]
+              + rng.normal(0, 1.0, size=(B, k, Vd))).astype(np.float32)
+        T = rng.choice([0.0, 0.7, 1.0], size=B)
+        Tq = np.where(T > 0, T, 1.0)
+        q = W.bf16_round(dl).astype(np.float64) / Tq[:, None, None]
+        q = np.exp(q - q.max(-1, keepdims=True))
+        q /= q.sum(-1, keepdims=True)
+        drafts = np.zeros((B, k), np.int32)
+        for b in range(B):
+            for j in range(k):
+                drafts[b, j] = table[rng.choice(Vd, p=q[b, j])]
+        p = O.make_params(B, temperature=T, top_k=rng.choice([0, 20], size=B),
+                          top_p=rng.choice([1.0, 0.9], size=B),
+                          min_p=rng.choice([0.0, 0.05], size=B),
+                          seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                          position=rng.integers(0, 100, size=B).astype(np.uint64))
+        mask = W.pack_mask(rng.random((B, k + 1, V)) < 0.6) if it % 2 else None
+        hist = rng.integers(0, V, size=(B, 8)).astype(np.int32) if it == 2 else None
+        if hist is not None:
+            p["presence_penalty"] = 0.4
+        for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+            say(f"verify general-q k={k} it={it} B={B} V={V} Vd={Vd} mode={mode}")
+            check_verify(ctx, tgt, k, drafts, p, "bf16", mask, hist, None, mode,
+                         draft_logits=dl, table=table, label=f"general-q k={k} it={it}")
+
+
+def test_verify_general_q_table_errors(ctx):
+    rng = np.random.default_rng(90)
+    B, k, V, Vd = 3, 2, 400, 100
+    table = np.sort(rng.choice(V, size=Vd, replace=False)).astype(np.int32)
+    tgt = rng.normal(size=(B, k + 1, V)).astype(np.float32)
+    dl = rng.normal(size=(B, k, Vd)).astype(np.float32)
+    drafts = rng.choice(table, size=(B, k)).astype(np.int32)
+    outside = np.setdiff1d(np.arange(V), table)
+    drafts[1, 1] = outside[0]  # sequence 1: a draft the draft vocabulary cannot produce
+    p = O.make_params(B, temperature=0.8, seed=np.arange(B, dtype=np.uint64))
+    say("verify general-q draft outside the table")
+    g, ref = check_verify(ctx, tgt, k, drafts, p, "f32", draft_logits=dl, table=table,
+                          label="draft outside table")
+    assert g["status"][1] == O.STRIM_EINVAL and g["status"][0] == 0
+    bad = table.copy()
+    bad[[10, 11]] = bad[[11, 10]]  # not ascending
+    say("verify general-q unsorted table")
+    g = run_verify(ctx, host_logits(tgt, "f32"), k, drafts, p, "f32", draft_logits=dl,
+                   table=bad)
+    assert (g["status"] == O.STRIM_EINVAL).all()
+    assert (g["accepted"] == 0).all() and (g["token"] == -1).all()
 
 
 # ------------------------------------------------------------------ aux ops ----
