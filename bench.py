@@ -83,6 +83,30 @@ def make_pool_cfg5(torch, dev, n_sets, B, V, H, seed=5):
     return xs, hs, ms
 
 
+def make_pool_cfg4(torch, dev, n_sets, B, k, V, Vd, T=0.7, seed=4):
+    """cfg4-shaped verify inputs: target [B,k+1,V] bf16 (cfg2-style logits), draft logits
+    [B,k,Vd] bf16 biased toward the target, an ascending injective table, drafts drawn
+    from q = softmax(draft / T)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    perm = torch.from_numpy(rng.permutation(V)).to(dev)
+    bias = torch.empty(V, device=dev)
+    bias[perm] = -1.1 * torch.log(torch.arange(V, device=dev, dtype=torch.float32) + 1.0)
+    table = torch.from_numpy(np.sort(rng.choice(V, size=Vd, replace=False)).astype(np.int32)).to(dev)
+    ts, ds, dr = [], [], []
+    for _ in range(n_sets):
+        t = (torch.randn(B, k + 1, V, device=dev, generator=g) * 2.5 + bias).to(torch.bfloat16)
+        d = (0.5 * torch.randn(B, k, Vd, device=dev, generator=g) * 2.5
+             + 0.8 * t[:, :k, :].float()[:, :, table.long()]).to(torch.bfloat16)
+        q = torch.softmax(d.float() / T, dim=-1).reshape(B * k, Vd)
+        pick = torch.multinomial(q, 1, generator=g).reshape(B, k)
+        ts.append(t.contiguous())
+        ds.append(d.contiguous())
+        dr.append(table[pick].to(torch.int32).contiguous())
+    return ts, ds, dr, table
+
+
 def graph_us_per_step(torch, calls, steps, warmup):
     """Capture `calls` (one step each) into a HIP graph; replay until `steps` steps ran;
     wall clock between device synchronisations / steps."""
@@ -303,6 +327,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b64", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the cfg3 (grammar masks, top-p) and cfg4 (general-q verify) "
+                         "timings")
     ap.add_argument("--summarize", metavar="DIR",
                     help="print the markdown summary of a profile directory (trace/, fetch/, "
                          "write/ as made by the commands in profiles/) and exit")
@@ -414,6 +441,54 @@ def main():
             "kernel_us": {k: round(v[0], 3) for k, v in kt5.items()},
         }
         del xs5, hs5, ms5, calls5
+
+    if not args.no_extra:
+        # cfg3: B=8 bf16 + grammar masks of the configuration, T 0.8, top-p 0.9, icdf
+        w3 = W.cfg3()
+        n3 = int(np.ceil(args.pool_mb * 2**20 / (B * V * 2)))
+        xs3, _, ns3 = make_pool_cfg2(torch, dev, n3, B, V, 1, seed=3)
+        m3 = torch.from_numpy(w3["mask"].view(np.int32)).to(dev)
+        calls3 = [ctx.bind_sample(xs3[i], w3["params"], mask=m3, noise=ns3[i])
+                  for i in range(n3)]
+        us3, k3, g3 = graph_us_per_step(torch, calls3, min(args.steps, 400), 20)
+        del g3
+        kt3 = kernel_times(torch, ctx, calls3, min(args.steps, 192))
+        log(f"[bench] cfg3 graph {us3:.2f} us/step; kernels (us): "
+            + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt3.items()))
+        result["cfg3"] = {
+            "workload": "cfg3: B=8 bf16 + packed allow masks (0.01-30% density, clustered and "
+                        "scattered, a one-token row, a row whose nucleus is masked), T 0.8, "
+                        "top-p 0.9, icdf",
+            "us_per_step": round(us3, 3), "steps": k3,
+            "kernel_us": {k: round(v[0], 3) for k, v in kt3.items()}}
+        del xs3, ns3, calls3
+        # cfg4: general-q verify, B=4, k=3, Vd=32768, T 0.7, Philox Gumbel (the reference's
+        # verify noise scheme)
+        B4, K4, VD4 = 4, 3, W.VD_DEFAULT
+        n4 = int(np.ceil(args.pool_mb * 2**20 / (B4 * (K4 + 1) * V * 2 + B4 * K4 * VD4 * 2)))
+        ts4, ds4, dr4, tab4 = make_pool_cfg4(torch, dev, n4, B4, K4, V, VD4)
+        p4 = W.params_array(B4, temperature=0.7, seed=np.arange(B4, dtype=np.uint64) + 40,
+                            position=3)
+        outs = [dict(acc=torch.empty(B4, dtype=torch.int32, device=dev),
+                     tok=torch.empty(B4, dtype=torch.int32, device=dev)) for _ in range(n4)]
+
+        def vcall(i):
+            return lambda: ctx.verify(ts4[i], dr4[i], p4, draft_logits=ds4[i],
+                                      draft_to_full=tab4, noise_mode=1, row_outputs=False)
+        calls4 = [vcall(i) for i in range(n4)]
+        for c in calls4[:4]:
+            c()
+        torch.cuda.synchronize()
+        eg4 = eager_us_per_step(torch, calls4, min(args.steps, 200))
+        kt4 = kernel_times(torch, ctx, calls4, min(args.steps, 96), window=32)
+        log(f"[bench] cfg4 eager {eg4:.2f} us/step; kernels (us): "
+            + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt4.items()))
+        result["cfg4"] = {
+            "workload": "cfg4: general-q verify B=4 k=3 V=151936 bf16, draft logits "
+                        "[4,3,32768] bf16 + ascending table, T 0.7, Philox Gumbel",
+            "eager_us_per_step": round(eg4, 3),
+            "kernel_us": {k: round(v[0], 3) for k, v in kt4.items()}}
+        del ts4, ds4, dr4, calls4, outs
     ctx.close()
 
     if not args.no_cpu:

@@ -125,7 +125,7 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
   timed(ctx, KID_STREAM,
         [&](hipEvent_t e0, hipEvent_t e1) { keep(launch_stream(a, grid_rc, st, any_pen, e0, e1)); });
   timed(ctx, KID_FINALIZE, [&](hipEvent_t e0, hipEvent_t e1) {
-    keep(launch_args((const void*)k_finalize, dim3((unsigned)a.R), dim3(STPB), a, st, e0, e1));
+    keep(launch_args((const void*)k_finalize, dim3((unsigned)a.R), dim3(FTPB), a, st, e0, e1));
   });
   if (need_collect)
     timed(ctx, KID_COLLECT, [&](hipEvent_t e0, hipEvent_t e1) {
@@ -306,7 +306,10 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
       a.out_ids = out_ids + g0;
       a.out_status = out_status ? out_status + g0 : nullptr;
       a.out_probs = out_probs ? out_probs + (size_t)g0 * V : nullptr;
-      for (int i = 0; i < nb; ++i) a.p[i] = params[g0 + i];
+      for (int i = 0; i < nb; ++i) {
+        a.p[i] = params[g0 + i];
+        a.lmp[i] = params[g0 + i].min_p > 0.0f ? log((double)params[g0 + i].min_p) : -INFINITY;
+      }
       const int rc = run_group(ctx, (hipStream_t)stream, a, nb, out_probs != nullptr);
       if (rc != STRIM_OK) return rc;
     }
@@ -372,7 +375,10 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       a.out_row_accept = out_row_accept ? out_row_accept + (size_t)g0 * k : nullptr;
       a.out_row_token = out_row_token ? out_row_token + (size_t)g0 * (k + 1) : nullptr;
       a.out_status = out_status ? out_status + g0 : nullptr;
-      for (int i = 0; i < nb; ++i) a.p[i] = params[g0 + i];
+      for (int i = 0; i < nb; ++i) {
+        a.p[i] = params[g0 + i];
+        a.lmp[i] = params[g0 + i].min_p > 0.0f ? log((double)params[g0 + i].min_p) : -INFINITY;
+      }
       hipError_t e = hipSuccess;
       if (a.dlog) {
         // draft distributions (one workgroup per draft row) and, with the first group,

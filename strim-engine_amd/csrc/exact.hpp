@@ -384,7 +384,7 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
   const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
   const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
   const bool cand_sorted = no_lse ? topp : (topk || topp);
-  XUni u{m, p.min_p > 0.0f ? log((double)p.min_p) : -INFINITY, 0ull, ~0ull, -1, 0ull};
+  XUni u{m, p.min_p > 0.0f ? p.lmp : -INFINITY, 0ull, ~0ull, -1, 0ull};
   // general-q verify rows draw from the residual (p - q)^+ over the whole kept set
   const bool resid = vdr && a.has_q;
   uint64_t S = 0ull;

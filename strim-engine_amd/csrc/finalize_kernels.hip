@@ -36,23 +36,23 @@ __device__ __forceinline__ void finish_row(const Args& a, int r, int status, int
 }
 
 // LDS of one k_finalize workgroup.
-constexpr int FSEG = FCAP / (STPB / WAVE);  // survivors per wave segment in phase 2
+constexpr int FSEG = FCAP / (FTPB / WAVE);  // survivors per wave segment in phase 2
 struct FinalShared {
   uint64_t key[FCAP];       // the row's surviving candidate keys (32 KB)
-  uint32_t rpre[4 * 256];   // per wave region: first candidate position within its
-                            // 64-chunk block (add the block offsets in off[])
+  uint32_t rpre[SWAVES * 256];  // per k_stream wave region: first candidate position
+                               // within its 64-chunk block (add the block offsets in off[])
   uint32_t hist[256];       // d-histogram / radix digits
-  float v[STPB / WAVE], g[STPB / WAVE];
-  int i[STPB / WAVE], f[STPB / WAVE];
-  uint32_t off[STPB / WAVE], cnt[STPB / WAVE];
-  double d[STPB / WAVE];
-  uint64_t u[STPB / WAVE];
+  float v[FTPB / WAVE], g[FTPB / WAVE];
+  int i[FTPB / WAVE], f[FTPB / WAVE];
+  uint32_t off[FTPB / WAVE], cnt[FTPB / WAVE];
+  double d[FTPB / WAVE];
+  uint64_t u[FTPB / WAVE];
   int misc[8];
   // the exact streaming resolution (rows whose candidates overflow): its histogram
   // masses and gathered buckets use key[] (XB entries)
   uint32_t xhc[XB];
-  uint32_t xcnt[STPB * EPT];
-  uint64_t xu2[2 * STPB / WAVE];
+  uint32_t xcnt[FTPB * EPT];
+  uint64_t xu2[2 * FTPB / WAVE];
   XState x;
 };
 static_assert(FCAP >= XB && FCAP >= XCOL, "the exact path reuses the candidate keys");
@@ -108,7 +108,7 @@ __device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int 
     xa.q.Z = qs.Z;
   }
   __syncthreads();
-  const XOut xo = exact_row<STPB>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
+  const XOut xo = exact_row<FTPB>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
   finish_row(a, r, xo.status, xo.token, xo.accept, xo.sig, m, xo.last_key, PH_DONE);
 }
 
@@ -143,13 +143,13 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   }
 
   // ---- phase 1: chunk statistics (W <= 256: one chunk per thread) -----------------
-  ChunkStat cs{-INFINITY, -1, 0, 0, 0.0, 0u, -INFINITY};
+  ChunkStat cs{-INFINITY, 0, 0, -INFINITY, 0.0, -1, {}};
   if (t < W) cs = a.s.cstat[(int64_t)r * a.s.wmax + t];
   uint32_t ctot = 0u;
   int ff = cs.flags | (cs.n > 0 ? 4 : 0);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t ce = (cs.nslot >> (8 * e)) & 255u;
+  for (int e = 0; e < SWAVES; ++e) {
+    const uint32_t ce = cs.nslot[e];
     if (ce > (uint32_t)SLOTW) ff |= 2;  // a wave region overflowed
     ctot += ce;
   }
@@ -164,9 +164,9 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   if (t < W) {
     uint32_t o = wex;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      S.rpre[4 * t + e] = o;
-      o += (cs.nslot >> (8 * e)) & 255u;
+    for (int e = 0; e < SWAVES; ++e) {
+      S.rpre[SWAVES * t + e] = o;
+      o += cs.nslot[e];
     }
   }
   if (t < 256) S.hist[t] = 0u;
@@ -182,7 +182,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   int arg = S.i[0], flags = S.f[0];
   uint32_t n_c = 0u;
 #pragma unroll
-  for (int q = 0; q < STPB / WAVE; ++q) {
+  for (int q = 0; q < FTPB / WAVE; ++q) {
     if (q > 0) {
       argmax_merge(m, arg, S.v[q], S.i[q]);
       flags |= S.f[q];
@@ -228,7 +228,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   // ---- unfiltered Gumbel rows: the chunks' two best tokens ------------------------
   if (p.cls == CLS_GENERAL && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, V)) {
     const double wc = (t < W && cs.n > 0) ? cs.S * exp((double)cs.m - (double)m) : 0.0;
-    const double sig = block_sum_f64<STPB>(wc, S.d);
+    const double sig = block_sum_f64<FTPB>(wc, S.d);
     const double lse = log(sig);
     double bsc = -INFINITY;
     uint64_t btk = ~0ull;
@@ -249,7 +249,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
         }
       }
     }
-    block_argmax_score<STPB>(bsc, btk, bid, S.d, S.u, S.i, &S.misc[3]);
+    block_argmax_score<FTPB>(bsc, btk, bid, S.d, S.u, S.i, &S.misc[3]);
     int token = S.misc[3];
     int acc = 0;
     if (vdr) {
@@ -273,30 +273,30 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   // every kept token has v >= G (the k-th value bound), minus the l-tie margin
   const float Gm = topk && G > -INFINITY ? G - (fabsf(G) * 1e-6f + 1e-30f) : -INFINITY;
   const bool minp = p.min_p > 0.0f;
-  const double lmp = minp ? log((double)p.min_p) : 0.0;
+  const double lmp = p.lmp;
   // top-k histogram of d = m - l over the survivors' span (bounded by G or min-p)
   float dspan = 16.0f;
   if (Gm > -INFINITY) dspan = fminf(dspan, m - Gm / p.T);
   if (minp) dspan = fminf(dspan, (float)-lmp);
   const float scale = 255.0f / fmaxf(dspan * 1.0001f, 1e-6f);
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
-  const int nreg = 4 * W;
+  const int nreg = SWAVES * W;
   // global position of region rg's first candidate
   auto gpre = [&](int rg) {
     uint32_t o = S.rpre[rg];
-    const int blk = rg >> 8;  // 64 chunks (256 regions) per wave of phase 1
+    const int blk = rg / (WAVE * SWAVES);  // 64 chunks per wave of phase 1
 #pragma unroll
-    for (int q = 0; q < STPB / WAVE; ++q)
+    for (int q = 0; q < FTPB / WAVE; ++q)
       if (q < blk) o += S.off[q];
     return o;
   };
   constexpr int GB = 8;  // loads in flight per thread per batch
   uint32_t n_w = 0u;     // survivors in this wave's segment
-  for (int base = 0; base < (int)n_c; base += GB * STPB) {
+  for (int base = 0; base < (int)n_c; base += GB * FTPB) {
     Cand cd[GB];
 #pragma unroll
     for (int q = 0; q < GB; ++q) {
-      const int pos = base + q * STPB + t;
+      const int pos = base + q * FTPB + t;
       cd[q] = Cand{-INFINITY, -1};
       if (pos < (int)n_c) {
         int lo = 0, hi = nreg - 1;  // last region whose first position <= pos
@@ -325,11 +325,11 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   }
   if (lane == 0) S.off[w] = n_w;
   __syncthreads();
-  uint32_t segn[STPB / WAVE];
+  uint32_t segn[FTPB / WAVE];
   int over = 0;
   uint32_t n_s = 0u;
 #pragma unroll
-  for (int q = 0; q < STPB / WAVE; ++q) {
+  for (int q = 0; q < FTPB / WAVE; ++q) {
     segn[q] = S.off[q];
     over |= segn[q] > (uint32_t)FSEG;
     n_s += segn[q];
@@ -343,7 +343,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   {
     uint32_t o = segn[0];
 #pragma unroll
-    for (int q = 1; q < STPB / WAVE; ++q) {
+    for (int q = 1; q < FTPB / WAVE; ++q) {
       for (uint32_t i = lane; i < segn[q]; i += WAVE) S.key[o + i] = S.key[q * FSEG + i];
       o += segn[q];
     }
@@ -527,7 +527,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
 // chunk's results visible; an in-kernel device-scope release per workgroup costs far
 // more on gfx950 than the second launch)
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(STPB) void k_finalize(Args a) {
+__global__ __launch_bounds__(FTPB) void k_finalize(Args a) {
   __shared__ FinalShared S;
   const int r = blockIdx.x;
   int b, j;

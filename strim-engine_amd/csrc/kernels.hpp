@@ -19,10 +19,12 @@
 namespace strim {
 
 constexpr int MAXP = 64;         // parameter rows carried inline per launch group
+constexpr int STPB = 512;        // threads of a k_stream workgroup (8 tokens each)
+constexpr int SWAVES = STPB / 64;  // waves of a k_stream workgroup
 constexpr int SLOTW = 64;        // fast-path candidates per wave of a k_stream workgroup
-constexpr int SLOT = 4 * SLOTW;  // ... per chunk (four waves)
+constexpr int SLOT = SWAVES * SLOTW;  // ... per chunk
+constexpr int FTPB = 256;        // threads of a k_finalize workgroup (one row)
 constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
-constexpr int STPB = 256;        // threads of a k_stream workgroup (16 tokens each)
 constexpr int FCAP = 4096;       // candidates k_finalize holds in LDS
 constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
 constexpr float CB_SCALE = 2.0f;
@@ -40,16 +42,19 @@ enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1 };
 
 enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
 
+// Written by k_stream without a closing barrier: m, n, flags and g by the first wave,
+// arg by the wave holding the first maximum, each nslot byte by its own wave.
 struct ChunkStat {
   float m;         // chunk max of processed logits (-inf if none allowed)
-  int32_t arg;     // first id reaching m
-  int32_t n;       // allowed tokens
+  int32_t n;       // allowed tokens (fast and greedy rows: 1 if any)
   int32_t flags;   // bit0: non-finite logit
-  double S;        // sum exp(l - m) over the chunk (general rows)
-  uint32_t nslot;  // fast rows: candidates per wave, one byte each (255 = overflow)
   float g;         // fast top-k rows: at least k of the chunk's tokens have v >= g (v is
                    // the value before temperature); -inf when not certified
+  double S;        // sum exp(l - m) over the chunk (general rows)
+  int32_t arg;     // first id reaching m
+  uint8_t nslot[SWAVES];  // fast rows: candidates of each wave (255 = overflow)
 };
+static_assert(sizeof(ChunkStat) == 40, "ChunkStat layout");
 
 // General-path per-chunk summary of the tokens k_collect did not collect: fixed-point
 // mass and count per non-collected interval, and the two best surely-kept tokens by the
@@ -98,7 +103,7 @@ struct QStat {
 // Device scratch owned by a context (allocated once in strim_ctx_create).
 struct Scratch {
   ChunkStat* cstat;               // [rows][wmax]
-  Cand* slot;                     // [rows][wmax][4][SLOTW] fast-row candidates per wave
+  Cand* slot;                     // [rows][wmax][SWAVES][SLOTW] fast-row candidates per wave
                                   // (v before temperature, id)
   uint32_t* chc;                  // [rows][wmax][NCB] coarse counts
   unsigned long long* chm;        // [rows][wmax][NCB] coarse fixed-point masses
@@ -143,6 +148,7 @@ struct Args {
   int32_t* out_row_accept;
   int32_t* out_row_token;
   strim_sampling_params p[MAXP];  // per batch row of the group
+  double lmp[MAXP];               // log(min_p) per batch row (host libm), -inf when off
 };
 
 // Launches kernel `fn(Args)` on st. Given a start/stop event pair, the events take the
@@ -156,6 +162,7 @@ inline hipError_t launch_args(const void* fn, dim3 grid, dim3 block, const Args&
 }
 
 struct RowParams {
+  double lmp;  // log(min_p), -inf when min-p is off
   float T, rep, pres, freq, min_p, top_p;
   int32_t top_k;
   uint32_t flags;
@@ -198,6 +205,7 @@ __device__ __forceinline__ RowParams load_params(const Args& a, int b, int j) {
   p.pres = sp.presence_penalty;
   p.freq = sp.frequency_penalty;
   p.min_p = sp.min_p;
+  p.lmp = a.lmp[b];
   p.top_p = sp.top_p;
   p.top_k = sp.top_k;
   p.flags = a.verify ? (sp.flags & STRIM_FLAG_TOPK_KEEP_TIES) : sp.flags;
@@ -344,34 +352,47 @@ __device__ __forceinline__ void process_seg(const A& a, int i0, const RowParams&
   }
 }
 
-// History counts of the span [c0, c0 + SPAN) in LDS, like build_counts_span, but the
-// first HPT * NT history ids are loaded (16 bytes at a time when aligned) before the
-// table is cleared, so their latency overlaps the clear and the caller's other loads.
-constexpr int HPT = 16;
-template <int NT, int SPAN, typename A>
-__device__ __forceinline__ void build_counts_pre(const A& a, int b, int j, int c0,
-                                                 uint32_t* s_cnt) {
+// History counts of a span in LDS in two steps, so the history loads can be issued
+// before the caller's logits loads and their latency overlaps them: hist_load requests
+// this thread's first HPT history ids (16 bytes at a time when aligned) and returns the
+// row's history length; hist_count clears the table for [c0, c0 + SPAN), counts every
+// history id inside it (plus the verify draft prefix) and ends with a barrier.
+constexpr int HPT = 4096 / STPB;  // history ids each k_stream thread preloads
+template <int NT, typename A>
+__device__ __forceinline__ int hist_load(const A& a, int b, int (&ids)[HPT]) {
   const int t = threadIdx.x;
   const int32_t* h = a.hist ? a.hist + (int64_t)b * a.H : nullptr;
-  // ids [4 (q NT + t), +4) as one 16-byte load when the row is aligned, else one by one
-  const bool h4 = h && ((uintptr_t)h & 15u) == 0;
-  int ids[HPT];
+  // loads from clamped indices with no branch between them (see load_chunk)
+  if (h && ((uintptr_t)h & 15u) == 0 && (a.H & 3) == 0) {
+    // (positions past the history length are ignored by hist_count, so the loaded
+    // values are not touched here and no instruction waits for them yet)
 #pragma unroll
-  for (int q = 0; q < HPT / 4; ++q) {
-    const int i = 4 * (q * NT + t);
-    if (h4 && i + 4 <= a.H) {
-      const int4 v = *(const int4*)(h + i);
+    for (int q = 0; q < HPT / 4; ++q) {
+      const int i = 4 * (q * NT + t);
+      const int4 v = *(const int4*)(h + (i < a.H ? i : 0));
       ids[4 * q] = v.x; ids[4 * q + 1] = v.y; ids[4 * q + 2] = v.z; ids[4 * q + 3] = v.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ids[4 * q + e] = (h && i + e < a.H) ? h[i + e] : -1;
     }
+  } else if (h) {
+#pragma unroll
+    for (int q = 0; q < HPT; ++q) {
+      const int i = 4 * ((q >> 2) * NT + t) + (q & 3);
+      ids[q] = h[i < a.H ? i : 0];
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < HPT; ++q) ids[q] = -1;
   }
   int hl = h ? a.H : 0;
   if (h && a.hist_len) {
     hl = a.hist_len[b];
     hl = hl < 0 ? 0 : (hl > a.H ? a.H : hl);
   }
+  return hl;
+}
+template <int NT, int SPAN, typename A>
+__device__ __forceinline__ void hist_count(const A& a, int b, int j, int c0, const int (&ids)[HPT],
+                                           int hl, uint32_t* s_cnt) {
+  const int t = threadIdx.x;
   uint4* s4 = (uint4*)s_cnt;
   for (int i = t; i < SPAN / 4; i += NT) s4[i] = make_uint4(0u, 0u, 0u, 0u);
   __syncthreads();
@@ -382,10 +403,13 @@ __device__ __forceinline__ void build_counts_pre(const A& a, int b, int j, int c
     const uint32_t o = (uint32_t)ids[q] - uc0;
     if (i < hl && o < (uint32_t)SPAN && ids[q] >= 0 && ids[q] < a.V) atomicAdd(&s_cnt[o], 1u);
   }
-  for (int i = HPT * NT + t; i < hl; i += NT) {
-    const int id = h[i];
-    const uint32_t o = (uint32_t)id - uc0;
-    if (o < (uint32_t)SPAN && id >= 0 && id < a.V) atomicAdd(&s_cnt[o], 1u);
+  if (hl > HPT * NT) {
+    const int32_t* h = a.hist + (int64_t)b * a.H;
+    for (int i = HPT * NT + t; i < hl; i += NT) {
+      const int id = h[i];
+      const uint32_t o = (uint32_t)id - uc0;
+      if (o < (uint32_t)SPAN && id >= 0 && id < a.V) atomicAdd(&s_cnt[o], 1u);
+    }
   }
   if (a.verify && t < j) {
     const int id = a.drafts[(int64_t)b * a.k + t];

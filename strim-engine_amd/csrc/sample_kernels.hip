@@ -87,7 +87,7 @@ __device__ void compute_bounds(const Args& a, int r, const RowParams& p, float m
   auto ML = [&](int g) { return g < 0 ? 0.0 : (double)cL[g] * inv * (1.0 - EPS) - SLACK; };
   int s1 = NGB, e1 = NGB - 1;
   if (p.min_p > 0.0f) {
-    const double thr = -log((double)p.min_p);
+    const double thr = -p.lmp;
     const int gt = thr < 63.0 ? (int)(thr * (double)CB_SCALE) : NGB - 1;
     s1 = min(s1, max(0, gt - 1));
     e1 = min(e1, min(NGB - 1, gt + 1));
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
 
   // ---- per-position data lives in LDS: keys in s_key, fp64 masses in s_w ----------
   const bool minp = p.min_p > 0.0f;
-  const double lmp = minp ? log((double)p.min_p) : 0.0;
+  const double lmp = p.lmp;
   const bool keep_ties = (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) != 0;
   // non-collected tokens before global coarse bin g: count, pre-kept mass, kept mass
   auto seg_before = [&](int g, uint32_t& cb, double& pb, double& kb) {

@@ -17,7 +17,7 @@
 namespace strim {
 
 constexpr int SSEG = CHUNK / (STPB * EPT);  // 8-token segments per thread
-static_assert(SSEG == 2, "k_stream geometry");
+static_assert(SSEG >= 1 && SSEG * STPB * EPT == CHUNK, "k_stream geometry");
 
 // LDS of one k_stream workgroup.
 struct StreamShared {
@@ -50,47 +50,88 @@ __device__ __forceinline__ float dv_rung_end(int r) {
   return __uint_as_float(((uint32_t)r + 1u + VRUNG0) << 20);
 }
 
-// The 8 tokens [i0, i0 + 8) of row r as float32 (bf16 widened exactly). FULL: the
-// chunk lies inside the row and rows are 16-byte aligned, so one or two vector loads.
-template <int DT, bool FULL>
-__device__ __forceinline__ void load_seg(const Args& a, int r, int i0, float (&x)[EPT]) {
+// The raw values of this thread's SSEG 8-token segments as float32 (bf16 widens
+// exactly). Every load is issued with no control flow between them: a divergent branch
+// around a load makes the compiler wait for the load at the join, which would serialise
+// the memory round trips. Aligned full chunks take 16-byte loads; otherwise each token
+// is loaded from a clamped index and out-of-row tokens become -inf.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)[SSEG], bool full,
+                                           float (&x)[SSEG][EPT]) {
   const int64_t base = (int64_t)r * a.row_stride;
   if constexpr (DT == STRIM_DTYPE_BF16) {
     const uint16_t* xb = (const uint16_t*)a.logits + base;
-    if constexpr (FULL) {
-      const uint4 v = *(const uint4*)(xb + i0);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    if (VEC && full) {
+      uint4 q[SSEG];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[2 * e] = __uint_as_float(w[e] << 16);
-        x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+      for (int s = 0; s < SSEG; ++s) q[s] = *(const uint4*)(xb + i0[s]);
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) {
+        const uint32_t w[4] = {q[s].x, q[s].y, q[s].z, q[s].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[s][2 * e] = __uint_as_float(w[e] << 16);
+          x[s][2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+        }
       }
     } else {
+      uint16_t h[SSEG][EPT];
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? bf16_to_f32(xb[i0 + e]) : -INFINITY;
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) h[s][e] = xb[i0[s] + e < a.V ? i0[s] + e : 0];
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          x[s][e] = i0[s] + e < a.V ? bf16_to_f32(h[s][e]) : -INFINITY;
     }
   } else {
     const float* xf = (const float*)a.logits + base;
-    if constexpr (FULL) {
-      const float4 v0 = *(const float4*)(xf + i0);
-      const float4 v1 = *(const float4*)(xf + i0 + 4);
-      x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
-      x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
-    } else {
+    if (VEC && full) {
+      float4 q[SSEG][2];
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) x[e] = (i0 + e < a.V) ? xf[i0 + e] : -INFINITY;
+      for (int s = 0; s < SSEG; ++s) {
+        q[s][0] = *(const float4*)(xf + i0[s]);
+        q[s][1] = *(const float4*)(xf + i0[s] + 4);
+      }
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) {
+        x[s][0] = q[s][0].x; x[s][1] = q[s][0].y; x[s][2] = q[s][0].z; x[s][3] = q[s][0].w;
+        x[s][4] = q[s][1].x; x[s][5] = q[s][1].y; x[s][6] = q[s][1].z; x[s][7] = q[s][1].w;
+      }
+    } else {
+      float h[SSEG][EPT];
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) h[s][e] = xf[i0[s] + e < a.V ? i0[s] + e : 0];
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) x[s][e] = i0[s] + e < a.V ? h[s][e] : -INFINITY;
     }
   }
+}
+
+// Smallest v that can pass min-p against a maximum mv (v space, before temperature):
+// v >= (mv / T + log(min_p)) T, less a rounding margin of a few ulps.
+__device__ __forceinline__ float minp_vlo(float mv_t, const RowParams& p) {
+  const double tl = ((double)mv_t + p.lmp) * (double)p.T;
+  return (float)(tl - fabs(tl) * 4e-7 - 1e-37);
 }
 
 // DT: logits dtype; VEC: rows are 16-byte aligned; PEN: some row of the launch has
 // penalties; MASK: allow-bits are given. The host picks the instantiation, so each
 // launch runs straight-line per-token code.
+//
+// Wave w owns the 1024 tokens [c0 + 1024 w, +1024) of the chunk; lane l holds the two
+// 8-token segments at +8 l and +512 + 8 l, so each wave-wide load is 1 KB contiguous
+// and the first maximum of the chunk lies in the lowest wave that holds the maximum.
+// The chunk statistics are written without a closing barrier (see ChunkStat).
 template <int DT, bool VEC, bool PEN, bool MASK>
 __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   __shared__ StreamShared S;
-  uint32_t* s_cnt = S.cnt;
-
   int r, c;
   map_block(r, c);
   int b, j;
@@ -99,27 +140,40 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int c0 = c * CHUNK;
   const bool full = VEC && c0 + CHUNK <= a.V;
+  const bool pen = PEN && p.pen;
+  ChunkStat* csp = &a.s.cstat[(int64_t)r * a.s.wmax + c];
+
+  // history ids first: the counts are built while the logits are still in flight
+  int hid[HPT];
+  int hl = 0;
+  if (pen) hl = hist_load<STPB>(a, b, hid);
   int i0[SSEG];
+#pragma unroll
+  for (int s = 0; s < SSEG; ++s)
+    i0[s] = c0 + w * (SSEG * WAVE * EPT) + s * (WAVE * EPT) + lane * EPT;
   float v[SSEG][EPT];
+  load_chunk<DT, VEC>(a, r, i0, full, v);
   uint32_t bits[SSEG];
 #pragma unroll
-  for (int s = 0; s < SSEG; ++s) {
-    i0[s] = c0 + (s * STPB + t) * EPT;
-    if (full) load_seg<DT, true>(a, r, i0[s], v[s]);
-    else load_seg<DT, false>(a, r, i0[s], v[s]);
-    bits[s] = 0xFFu;
-    if constexpr (MASK) {
-      if (a.mask && i0[s] < a.V)
-        bits[s] = ((const uint8_t*)(a.mask + (int64_t)r * a.mask_stride))[i0[s] >> 3];
+  for (int s = 0; s < SSEG; ++s) bits[s] = 0xFFu;
+  if constexpr (MASK) {
+    if (a.mask) {
+      // allow-bits byte of each segment (a segment starts on a multiple of 8), from a
+      // clamped index; tokens past the row end are -inf already
+      const uint8_t* mb = (const uint8_t*)(a.mask + (int64_t)r * a.mask_stride);
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) bits[s] = mb[i0[s] < a.V ? (i0[s] >> 3) : 0];
     }
   }
-  for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
-  if (t < NCB) {
+  const bool fast = p.cls == CLS_FAST;
+  const bool topk = p.top_k > 0 && p.top_k < a.V;
+  if (fast && topk)
+    for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
+  if (p.cls == CLS_GENERAL && t < NCB) {
     S.hc[t] = 0u;
     S.hm[t] = 0ull;
   }
-  const bool pen = PEN && p.pen;
-  if (pen) build_counts_pre<STPB, CHUNK>(a, b, j, c0, s_cnt);
+  if (pen) hist_count<STPB, CHUNK>(a, b, j, c0, hid, hl, S.cnt);
 
   // ---- penalties and mask, before temperature ("v space") ------------------------
   // Dividing by T > 0 is monotone, so maxima and candidate bounds are found on v; only
@@ -127,32 +181,35 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   // row end load as -inf (not allowed).
   bool nf = false;
   float vmax = -INFINITY;
-  int vid = -1;
 #pragma unroll
   for (int s = 0; s < SSEG; ++s) {
     uint32_t cnt[EPT];
     if (pen) {
-      const uint4 c4a = *(const uint4*)(s_cnt + (i0[s] - c0));
-      const uint4 c4b = *(const uint4*)(s_cnt + (i0[s] - c0) + 4);
+      const uint4 c4a = *(const uint4*)(S.cnt + (i0[s] - c0));
+      const uint4 c4b = *(const uint4*)(S.cnt + (i0[s] - c0) + 4);
       cnt[0] = c4a.x; cnt[1] = c4a.y; cnt[2] = c4a.z; cnt[3] = c4a.w;
       cnt[4] = c4b.x; cnt[5] = c4b.y; cnt[6] = c4b.z; cnt[7] = c4b.w;
     }
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       float y = v[s][e];
-      if (pen && cnt[e] > 0u) {
-        y = y > 0.0f ? y / p.rep : y * p.rep;
-        y = y - p.freq * (float)cnt[e];
-        y = y - p.pres;
+      if (pen) {
+        // a repetition penalty of 1 is exact identity (x / 1 = x * 1 = x), so the
+        // common case is branch-free; otherwise only tokens in the history divide
+        if (p.rep == 1.0f) {
+          float yp = y - p.freq * (float)cnt[e];
+          yp = yp - p.pres;
+          y = cnt[e] > 0u ? yp : y;
+        } else if (cnt[e] > 0u) {
+          y = y > 0.0f ? y / p.rep : y * p.rep;
+          y = y - p.freq * (float)cnt[e];
+          y = y - p.pres;
+        }
       }
       if constexpr (MASK) y = ((bits[s] >> e) & 1u) ? y : -INFINITY;
       nf |= !(y < INFINITY);  // NaN or +inf in an allowed position
       v[s][e] = y;
-      // ids rise with (s, e): a strict compare keeps the first maximum
-      if (y > vmax) {
-        vmax = y;
-        vid = i0[s] + e;
-      }
+      vmax = fmaxf(vmax, y);
     }
   }
   if (a.verify && j < a.k) {
@@ -171,45 +228,73 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   }
   if (c == 0 && t == 0) a.s.ncand[r] = 0u;
 
-  // ---- chunk max (first id on ties), allowed count, non-finite flag ---------------
-  wave_argmax(vmax, vid);
-  int n = vmax > -INFINITY ? 1 : 0;  // "some token allowed"; general rows count below
-  const int f = __any(nf) ? 1 : 0;
+  // ---- wave maxima; for fast top-k rows, an upper bound on each wave's min-p band ----
+  // (the band against the wave maximum holds the band against the chunk maximum)
+  const float wmv = wave_max_f(vmax);
+  int band = 1 << 20;
+  if (fast && topk && p.min_p > 0.0f) {
+    band = 0;
+    if (wmv > -INFINITY) {
+      const float vlo_w = minp_vlo(wmv / p.T, p);
+      int cb = 0;
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) cb += v[s][e] >= vlo_w ? 1 : 0;
+      band = wave_sum(cb);
+    }
+  }
+  const int fw = __any(nf) ? 1 : 0;
   if (lane == 0) {
-    S.v[w] = vmax;
-    S.i[w] = vid;
-    S.n[w] = n;
-    S.f[w] = f;
+    S.v[w] = wmv;
+    S.f[w] = fw;
+    S.n[w] = band;
   }
   __syncthreads();
   float vm = S.v[0];
-  int a_w = S.i[0], n_w = S.n[0], f_w = S.f[0];
+  int f_w = S.f[0], band_max = S.n[0], band_tot = S.n[0];
 #pragma unroll
   for (int q = 1; q < STPB / WAVE; ++q) {
-    argmax_merge(vm, a_w, S.v[q], S.i[q]);
-    n_w |= S.n[q];
+    vm = fmaxf(vm, S.v[q]);
     f_w |= S.f[q];
+    band_max = max(band_max, S.n[q]);
+    band_tot += S.n[q];
   }
+  // the first maximum: the lowest wave holding it finds its first token and records it
+  {
+    int wfirst = -1;
+#pragma unroll
+    for (int q = STPB / WAVE - 1; q >= 0; --q)
+      if (vm > -INFINITY && S.v[q] == vm) wfirst = q;
+    if (w == (wfirst < 0 ? 0 : wfirst)) {
+      int fid = 0x7FFFFFFF;
+      if (wfirst >= 0) {
+#pragma unroll
+        for (int s = SSEG - 1; s >= 0; --s)
+#pragma unroll
+          for (int e = EPT - 1; e >= 0; --e)
+            if (v[s][e] == vm) fid = i0[s] + e;
+      }
+      fid = wave_min_i(fid);
+      if (lane == 0) csp->arg = wfirst < 0 ? -1 : fid;
+    }
+  }
+  int n_w = vm > -INFINITY ? 1 : 0;  // "some token allowed"; general rows count below
   // chunk max after temperature; an overflow to +inf is a non-finite logit, one to -inf
   // leaves nothing allowed
   const float m_w = (p.greedy || !(vm > -INFINITY)) ? vm : vm / p.T;
   if (m_w == INFINITY) f_w = 1;
   if (!(m_w > -INFINITY)) n_w = 0;
-  ChunkStat cs{m_w, a_w, n_w, f_w, 0.0, 0u, -INFINITY};
+  ChunkStat cs{m_w, n_w, f_w, -INFINITY, 0.0, -1, {}};
   const bool live = n_w > 0 && !f_w;
 
-  if (p.cls == CLS_FAST && live) {
+  if (fast && live) {
     // Local candidates, in v space: every token that can pass min-p (on the row maximum
     // m >= m_w) and the chunk's top-k, written as (v, id) to the wave's slot region.
-    const bool topk = p.top_k > 0 && p.top_k < a.V;
-    // v >= vlo keeps every token with v / T >= m_w + log(min_p) (rounding margin 4e-7)
-    float vlo = -INFINITY;
-    if (p.min_p > 0.0f) {
-      const double L = (double)m_w + log((double)p.min_p);
-      const double tl = L * (double)p.T;
-      vlo = (float)(tl - fabs(tl) * 4e-7 - 1e-37);
-    }
-    if (topk) {
+    float vlo = p.min_p > 0.0f ? minp_vlo(m_w, p) : -INFINITY;
+    // the ladder bounds the chunk's top-k when the min-p band alone could hold more
+    // than 2k tokens or overflow a wave's region
+    if (topk && (band_max > SLOTW || band_tot > max(2 * p.top_k, 2 * SLOTW))) {
 #pragma unroll
       for (int s = 0; s < SSEG; ++s)
 #pragma unroll
@@ -258,11 +343,11 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
       }
     }
     // each wave writes its candidates to its own region of the chunk (no atomics, no
-    // barrier); the region counts travel in cs.nslot, one byte per wave
+    // barrier) and its count to its byte of nslot (255 = overflow)
     int wtot;
     const int wex = wave_excl_count32(mycnt, &wtot);
     if (wtot <= SLOTW) {
-      Cand* dst = a.s.slot + (((int64_t)r * a.s.wmax + c) * 4 + w) * SLOTW;
+      Cand* dst = a.s.slot + (((int64_t)r * a.s.wmax + c) * SWAVES + w) * SLOTW;
       int pos = wex;
 #pragma unroll
       for (int s = 0; s < SSEG; ++s)
@@ -270,9 +355,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
         for (int e = 0; e < EPT; ++e)
           if ((sel[s] >> e) & 1u) dst[pos++] = Cand{v[s][e], i0[s] + e};
     }
-    if (lane == 0) S.off[w] = wtot <= SLOTW ? (uint32_t)wtot : 255u;
-    __syncthreads();
-    cs.nslot = S.off[0] | (S.off[1] << 8) | (S.off[2] << 16) | (S.off[3] << 24);
+    if (lane == 0) csp->nslot[w] = (uint8_t)(wtot <= SLOTW ? wtot : 255);
   } else if (p.cls == CLS_GENERAL && live) {
     // processed logits; chunk sum exp(l - m_w) and a coarse histogram of m_w - l
     // (k_collect's bounds)
@@ -301,7 +384,9 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
     na = wave_sum(na);
     if (lane == 0) S.n[w] = na;
     __syncthreads();
-    cs.n = S.n[0] + S.n[1] + S.n[2] + S.n[3];
+    cs.n = 0;
+#pragma unroll
+    for (int q = 0; q < SWAVES; ++q) cs.n += S.n[q];
     if (t < NCB) {
       const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
       a.s.chc[o] = S.hc[t];
@@ -330,7 +415,11 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
       }
     }
   }
-  if (t == 0) a.s.cstat[(int64_t)r * a.s.wmax + c] = cs;
+  if (t == 0) {
+    *(float4*)csp = make_float4(cs.m, __int_as_float(cs.n), __int_as_float(cs.flags), cs.g);
+    csp->S = cs.S;
+    if (!(fast && live)) *(uint64_t*)csp->nslot = 0ull;
+  }
 }
 
 // Launches the k_stream variant of one (dtype, penalties) pair that matches the call's
