@@ -122,8 +122,17 @@ __device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int 
 //      the survivors' span;
 //   3. wave 0 alone: top-k (from the histogram), sort, top-p, draw, with wave-wide
 //      operations only.
-__device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams& p,
-                             FinalShared& S) {
+// What the exact streaming resolution needs when a row cannot be finished in LDS.
+struct ExactReq {
+  int need;
+  float m;
+  int arg, draft;
+  float l_draft;
+};
+
+__device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, int j,
+                                                 const RowParams& p, FinalShared& S) {
+  const ExactReq done{0, 0.0f, -1, -1, 0.0f};
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int V = a.V, W = a.W;
   const bool vdr = a.verify && j < a.k;  // a verify row with a draft
@@ -197,21 +206,20 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   if (status == STRIM_OK && !(flags & 4)) status = STRIM_EEMPTY;
   if (status != STRIM_OK) {
     finish_row(a, r, status, -1, 0, 0.0, m, 0ull, PH_DONE);
-    return;
+    return done;
   }
   if (p.greedy) {
     finish_row(a, r, STRIM_OK, arg, vdr && arg == draft, 1.0, m, 0ull, PH_DONE);
-    return;
+    return done;
   }
   if (vdr && a.dlog) {
     // general-q draft row: the draft must be in a valid table; the residual draw and the
     // p / q accept run on the exact streaming resolution
     if (*a.s.qflag == 0 || a.s.qst[b * a.k + j].td < 0) {
       finish_row(a, r, STRIM_EINVAL, -1, 0, 0.0, m, 0ull, PH_DONE);
-      return;
+      return done;
     }
-    finalize_exact(a, r, b, j, p, m, arg, draft, vdr, l_draft, S);
-    return;
+    return ExactReq{1, m, arg, draft, l_draft};
   }
   const bool topk = p.top_k > 0 && p.top_k < V;
   const bool topp = p.top_p < 1.0f;
@@ -258,15 +266,14 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
       if (token < 0) token = arg;  // the draft is the only allowed token
     }
     finish_row(a, r, STRIM_OK, token, acc, sig, m, ~0ull, PH_DONE);
-    return;
+    return done;
   }
   if (p.cls != CLS_FAST) {
     finish_row(a, r, STRIM_OK, -1, 0, 0.0, m, 0ull, PH_PENDING);
-    return;
+    return done;
   }
   if ((flags & 2) || n_c > (uint32_t)FCAND) {
-    finalize_exact(a, r, b, j, p, m, arg, draft, vdr, l_draft, S);
-    return;
+    return ExactReq{1, m, arg, draft, l_draft};
   }
 
   // ---- phase 2: gather, divide, prune, compact --------------------------------------
@@ -335,10 +342,9 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     n_s += segn[q];
   }
   if (over) {
-    finalize_exact(a, r, b, j, p, m, arg, draft, vdr, l_draft, S);
-    return;
+    return ExactReq{1, m, arg, draft, l_draft};
   }
-  if (w != 0) return;  // phase 3 is one wave
+  if (w != 0) return done;  // phase 3 is one wave
   // concatenate the wave segments
   {
     uint32_t o = segn[0];
@@ -381,11 +387,8 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
     n = (int)n2;
     uint64_t kth;
     if (n <= WAVE) {
-      const uint64_t kv = wave_sort_u64(lane < n ? S.key[lane] : ~0ull);
-      wave_sync();
-      S.key[lane] = kv;
-      wave_sync();
-      kth = shfl_u64(kv, p.top_k - 1);
+      wave_rank_sort(S.key, n);
+      kth = S.key[p.top_k - 1];
     } else if (n <= 1024) {
       wave_sort_lds(S.key, n);
       kth = S.key[p.top_k - 1];
@@ -419,10 +422,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   // ---- phase 3b: sort the survivors ---------------------------------------------
   if (!sorted) {
     if (n <= WAVE) {
-      const uint64_t kv = wave_sort_u64(lane < n ? S.key[lane] : ~0ull);
-      wave_sync();
-      S.key[lane] = kv;
-      wave_sync();
+      wave_rank_sort(S.key, n);
     } else {
       wave_sort_lds(S.key, n);
     }
@@ -520,6 +520,7 @@ __device__ void finalize_row(const Args& a, int r, int b, int j, const RowParams
   }
   const int acc = vdr && ((double)u_acc < w_d / S_kept) ? 1 : 0;
   finish_row(a, r, STRIM_OK, token, acc, S_kept, m, last_key, PH_DONE);
+  return done;
 }
 
 // ---------------------------------------------------------------------------------
@@ -533,7 +534,10 @@ __global__ __launch_bounds__(FTPB) void k_finalize(Args a) {
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);
-  finalize_row(a, r, b, j, p, S);
+  const ExactReq q = finalize_row(a, r, b, j, p, S);
+  // one call site for the exact resolution (an out-of-line call), reached by every
+  // thread of a row that needs it
+  if (q.need) finalize_exact(a, r, b, j, p, q.m, q.arg, q.draft, a.verify && j < a.k, q.l_draft, S);
 }
 
 }  // namespace strim

@@ -413,6 +413,27 @@ __device__ __forceinline__ int wave_argmax_score(double sc, uint64_t tk, int id)
   return bi;
 }
 
+// Ascending sort of key[0, n), n <= 64 distinct keys in LDS, by one wave: each lane
+// counts the keys below its own (broadcast LDS reads, eight in flight) and stores its key
+// at that rank. Cheaper than a bitonic network of cross-lane exchanges for small n.
+__device__ __forceinline__ void wave_rank_sort(uint64_t* key, int n) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const uint64_t k = lane < n ? key[lane] : ~0ull;
+  int rank = 0;
+  int q = 0;
+  for (; q + 8 <= n; q += 8) {
+    uint64_t c[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c[e] = key[q + e];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rank += c[e] < k ? 1 : 0;
+  }
+  for (; q < n; ++q) rank += key[q] < k ? 1 : 0;
+  wave_sync();
+  if (lane < n) key[rank] = k;
+  wave_sync();
+}
+
 // Ascending bitonic sort of one key per lane (~0 = empty sorts last).
 __device__ __forceinline__ uint64_t wave_sort_u64(uint64_t k) {
   const int lane = threadIdx.x & (WAVE - 1);
