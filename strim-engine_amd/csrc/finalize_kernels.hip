@@ -152,8 +152,10 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   }
 
   // ---- phase 1: chunk statistics (W <= 256: one chunk per thread) -----------------
-  ChunkStat cs{-INFINITY, 0, 0, -INFINITY, 0.0, -1, {}};
-  if (t < W) cs = a.s.cstat[(int64_t)r * a.s.wmax + t];
+  // (every load of phase 1 is issued before any of them is used: a load inside a
+  // divergent branch would be waited for at the branch's end)
+  ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (t < W ? t : 0)];
+  if (t >= W) cs = ChunkStat{-INFINITY, 0, 0, -INFINITY, 0.0, -1, {}};
   uint32_t ctot = 0u;
   int ff = cs.flags | (cs.n > 0 ? 4 : 0);
 #pragma unroll
@@ -299,6 +301,25 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   };
   constexpr int GB = 8;  // loads in flight per thread per batch
   uint32_t n_w = 0u;     // survivors in this wave's segment
+  // Candidates below the v-space bound of G and min-p (most of them: the chunks bound
+  // min-p on their own maximum) leave after one compare, without the division.
+  const float vthr = fmaxf(Gm, minp ? minp_vlo(m, p) : -INFINITY);
+  // one candidate of this lane (id < 0: none): l = v / T as the oracle rounds it, pruned
+  // by G and min-p, compacted into the wave's LDS segment (called by the whole wave)
+  auto take = [&](const Cand cd) {
+    bool k = cd.id >= 0 && cd.l >= vthr;
+    if (!__any(k)) return;
+    k = k && cd.l >= Gm;
+    const float l = k ? cd.l / p.T : -INFINITY;
+    k = k && l > -INFINITY && (!minp || ((double)l - (double)m) >= lmp);
+    const uint64_t msk = __ballot(k);
+    if (msk) {
+      const uint32_t dst = n_w + (uint32_t)lanes_below(msk);
+      if (k && dst < (uint32_t)FSEG) S.key[w * FSEG + dst] = ckey(l, cd.id);
+      if (k && topk) atomicAdd(&S.hist[dbin(m, l, scale)], 1u);
+      n_w += (uint32_t)__popcll(msk);
+    }
+  };
   for (int base = 0; base < (int)n_c; base += GB * FTPB) {
     Cand cd[GB];
 #pragma unroll
@@ -316,19 +337,7 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
       }
     }
 #pragma unroll
-    for (int q = 0; q < GB; ++q) {
-      // l = v / T as the oracle rounds it
-      bool k = cd[q].id >= 0 && cd[q].l >= Gm;
-      const float l = k ? cd[q].l / p.T : -INFINITY;
-      k = k && l > -INFINITY && (!minp || ((double)l - (double)m) >= lmp);
-      const uint64_t msk = __ballot(k);
-      if (msk) {
-        const uint32_t dst = n_w + (uint32_t)lanes_below(msk);
-        if (k && dst < (uint32_t)FSEG) S.key[w * FSEG + dst] = ckey(l, cd[q].id);
-        if (k && topk) atomicAdd(&S.hist[dbin(m, l, scale)], 1u);
-        n_w += (uint32_t)__popcll(msk);
-      }
-    }
+    for (int q = 0; q < GB; ++q) take(cd[q]);
   }
   if (lane == 0) S.off[w] = n_w;
   __syncthreads();

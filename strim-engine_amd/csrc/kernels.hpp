@@ -171,6 +171,14 @@ struct RowParams {
   int32_t cls;
 };
 
+// Smallest v (the value before temperature) whose l = RN(v / T) can pass min-p against
+// a maximum mt after temperature: v >= (mt + log(min_p)) T, less a rounding margin of a
+// few ulps.
+__device__ __forceinline__ float minp_vlo(float mt, const RowParams& p) {
+  const double tl = ((double)mt + p.lmp) * (double)p.T;
+  return (float)(tl - fabs(tl) * 4e-7 - 1e-37);
+}
+
 // Classification shared by host and device: which path resolves the row.
 __host__ __device__ inline int32_t row_class(const strim_sampling_params& p, int32_t V) {
   if (!(p.temperature > 0.0f)) return CLS_GREEDY;

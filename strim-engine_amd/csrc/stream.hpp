@@ -114,13 +114,6 @@ __device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)
   }
 }
 
-// Smallest v that can pass min-p against a maximum mv (v space, before temperature):
-// v >= (mv / T + log(min_p)) T, less a rounding margin of a few ulps.
-__device__ __forceinline__ float minp_vlo(float mv_t, const RowParams& p) {
-  const double tl = ((double)mv_t + p.lmp) * (double)p.T;
-  return (float)(tl - fabs(tl) * 4e-7 - 1e-37);
-}
-
 // DT: logits dtype; VEC: rows are 16-byte aligned; PEN: some row of the launch has
 // penalties; MASK: allow-bits are given. The host picks the instantiation, so each
 // launch runs straight-line per-token code.
