@@ -23,12 +23,11 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "strim_amd" / "libstrim_sampler.so"
 
-# (source, extra defines): k_stream variants per (dtype, penalties) pair
+# (source, extra defines): k_stream variants per (dtype, penalties, segments) triple
 UNITS = [
-    ("stream_kernels.hip", ["-DSTRIM_DT=1", "-DSTRIM_PEN=1"]),
-    ("stream_kernels.hip", ["-DSTRIM_DT=1", "-DSTRIM_PEN=0"]),
-    ("stream_kernels.hip", ["-DSTRIM_DT=0", "-DSTRIM_PEN=1"]),
-    ("stream_kernels.hip", ["-DSTRIM_DT=0", "-DSTRIM_PEN=0"]),
+    ("stream_kernels.hip", [f"-DSTRIM_DT={dt}", f"-DSTRIM_PEN={pen}", f"-DSTRIM_SSEG={sseg}"])
+    for dt in (1, 0) for pen in (1, 0) for sseg in (1, 4)
+] + [
     ("finalize_kernels.hip", []),
     ("sample_kernels.hip", []),
     ("aux_kernels.hip", []),

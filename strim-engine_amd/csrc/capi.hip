@@ -10,7 +10,7 @@
 #include "stream.hpp"
 
 namespace strim {
-__global__ void k_finalize(Args a);
+hipError_t launch_finalize(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 __global__ void k_collect(Args a);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
@@ -89,14 +89,24 @@ void timed(strim_ctx* ctx, int kind, F launch) {
 // Launches the k_stream variant for the call: dtype, alignment, whether any row has
 // penalties, whether a mask is given (unaligned calls take the penalties object, whose
 // unaligned variant checks penalties and mask per row).
+// Segments per thread of the k_stream launch: one (512-thread workgroups) while the
+// launch is small and its time is latency, four (128 threads) once the rows alone fill
+// the chip and instructions per token decide.
+constexpr int LARGE_ROWS = 32;
+int stream_sseg(const Args& a) { return a.R >= LARGE_ROWS ? 4 : 1; }
+
 hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen, hipEvent_t e0,
                          hipEvent_t e1) {
   const bool pen = any_pen || a.vec_ok == 0;
-  if (a.dtype == STRIM_DTYPE_BF16)
-    return pen ? launch_stream_group<STRIM_DTYPE_BF16, true>(a, grid, st, e0, e1)
-               : launch_stream_group<STRIM_DTYPE_BF16, false>(a, grid, st, e0, e1);
-  return pen ? launch_stream_group<STRIM_DTYPE_F32, true>(a, grid, st, e0, e1)
-             : launch_stream_group<STRIM_DTYPE_F32, false>(a, grid, st, e0, e1);
+  const bool big = stream_sseg(a) == 4;
+#define STRIM_GROUP(DT, PEN, SSEG) launch_stream_group<DT, PEN, SSEG>(a, grid, st, e0, e1)
+  if (a.dtype == STRIM_DTYPE_BF16) {
+    if (pen) return big ? STRIM_GROUP(STRIM_DTYPE_BF16, true, 4) : STRIM_GROUP(STRIM_DTYPE_BF16, true, 1);
+    return big ? STRIM_GROUP(STRIM_DTYPE_BF16, false, 4) : STRIM_GROUP(STRIM_DTYPE_BF16, false, 1);
+  }
+  if (pen) return big ? STRIM_GROUP(STRIM_DTYPE_F32, true, 4) : STRIM_GROUP(STRIM_DTYPE_F32, true, 1);
+  return big ? STRIM_GROUP(STRIM_DTYPE_F32, false, 4) : STRIM_GROUP(STRIM_DTYPE_F32, false, 1);
+#undef STRIM_GROUP
 }
 
 bool nofilter(const strim_sampling_params& p, int32_t V) {
@@ -120,12 +130,13 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
   // k_final decides the general rows (k_finalize leaves them pending)
   need_final = need_collect;
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
+  a.swaves = CHUNK / (EPT * stream_sseg(a)) / WAVE;
   hipError_t e = hipSuccess;
   auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };
   timed(ctx, KID_STREAM,
         [&](hipEvent_t e0, hipEvent_t e1) { keep(launch_stream(a, grid_rc, st, any_pen, e0, e1)); });
   timed(ctx, KID_FINALIZE, [&](hipEvent_t e0, hipEvent_t e1) {
-    keep(launch_args((const void*)k_finalize, dim3((unsigned)a.R), dim3(FTPB), a, st, e0, e1));
+    keep(launch_finalize(a, st, e0, e1));
   });
   if (need_collect)
     timed(ctx, KID_COLLECT, [&](hipEvent_t e0, hipEvent_t e1) {

@@ -73,11 +73,14 @@ __device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1
 __device__ __forceinline__ float u01(uint32_t w) {
   return (float)(w >> 8) * 5.9604644775390625e-08f;
 }
+// Block `blk` of the uniform stream of position key `key`: elements 4 blk .. 4 blk + 3.
+__device__ __forceinline__ uint4 philox_block(uint64_t key, uint64_t blk) {
+  return philox4x32_10(make_uint4((uint32_t)blk, (uint32_t)(blk >> 32), 0u, 0u),
+                       (uint32_t)key, (uint32_t)(key >> 32));
+}
 // Element `idx` of the [V+1] uniform vector of position key `key`.
 __device__ __forceinline__ float philox_uniform(uint64_t key, uint64_t idx) {
-  uint64_t blk = idx >> 2;
-  uint4 w = philox4x32_10(make_uint4((uint32_t)blk, (uint32_t)(blk >> 32), 0u, 0u),
-                          (uint32_t)key, (uint32_t)(key >> 32));
+  const uint4 w = philox_block(key, idx >> 2);
   uint32_t j = (uint32_t)(idx & 3u);
   return u01(j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w);
 }

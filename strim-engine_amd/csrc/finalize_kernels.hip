@@ -39,8 +39,8 @@ __device__ __forceinline__ void finish_row(const Args& a, int r, int status, int
 constexpr int FSEG = FCAP / (FTPB / WAVE);  // survivors per wave segment in phase 2
 struct FinalShared {
   uint64_t key[FCAP];       // the row's surviving candidate keys (32 KB)
-  uint32_t rpre[SWAVES * 256];  // per k_stream wave region: first candidate position
-                               // within its 64-chunk block (add the block offsets in off[])
+  uint32_t rpre[SMAXW * 256];  // per k_stream wave region: first candidate position
+                              // within its 64-chunk block (add the block offsets in off[])
   uint32_t hist[256];       // d-histogram / radix digits
   float v[FTPB / WAVE], g[FTPB / WAVE];
   int i[FTPB / WAVE], f[FTPB / WAVE];
@@ -130,6 +130,7 @@ struct ExactReq {
   float l_draft;
 };
 
+template <int SW>
 __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, int j,
                                                  const RowParams& p, FinalShared& S) {
   const ExactReq done{0, 0.0f, -1, -1, 0.0f};
@@ -158,10 +159,12 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   if (t >= W) cs = ChunkStat{-INFINITY, 0, 0, -INFINITY, 0.0, -1, {}};
   uint32_t ctot = 0u;
   int ff = cs.flags | (cs.n > 0 ? 4 : 0);
+  // candidate regions per chunk: one per k_stream wave, SLOT / sw entries each
+  constexpr int sw = SW, lsw = SW == 8 ? 3 : SW == 4 ? 2 : SW == 2 ? 1 : 0, slotw = SLOT / SW;
 #pragma unroll
-  for (int e = 0; e < SWAVES; ++e) {
-    const uint32_t ce = cs.nslot[e];
-    if (ce > (uint32_t)SLOTW) ff |= 2;  // a wave region overflowed
+  for (int e = 0; e < SMAXW; ++e) {
+    const uint32_t ce = e < sw ? cs.nslot[e] : 0u;
+    if (ce > (uint32_t)slotw) ff |= 2;  // a wave region overflowed
     ctot += ce;
   }
   float mv = cs.m, gv = cs.g;
@@ -175,9 +178,11 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   if (t < W) {
     uint32_t o = wex;
 #pragma unroll
-    for (int e = 0; e < SWAVES; ++e) {
-      S.rpre[SWAVES * t + e] = o;
-      o += cs.nslot[e];
+    for (int e = 0; e < SMAXW; ++e) {
+      if (e < sw) {
+        S.rpre[sw * t + e] = o;
+        o += cs.nslot[e];
+      }
     }
   }
   if (t < 256) S.hist[t] = 0u;
@@ -289,11 +294,11 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   if (minp) dspan = fminf(dspan, (float)-lmp);
   const float scale = 255.0f / fmaxf(dspan * 1.0001f, 1e-6f);
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
-  const int nreg = SWAVES * W;
+  const int nreg = sw * W;
   // global position of region rg's first candidate
   auto gpre = [&](int rg) {
     uint32_t o = S.rpre[rg];
-    const int blk = rg / (WAVE * SWAVES);  // 64 chunks per wave of phase 1
+    const int blk = rg >> (6 + lsw);  // 64 chunks per wave of phase 1
 #pragma unroll
     for (int q = 0; q < FTPB / WAVE; ++q)
       if (q < blk) o += S.off[q];
@@ -333,7 +338,7 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
           if ((int)gpre(mid) <= pos) lo = mid;
           else hi = mid - 1;
         }
-        cd[q] = slots[(int64_t)lo * SLOTW + (pos - (int)gpre(lo))];
+        cd[q] = slots[(int64_t)lo * slotw + (pos - (int)gpre(lo))];
       }
     }
 #pragma unroll
@@ -537,16 +542,23 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
 // chunk's results visible; an in-kernel device-scope release per workgroup costs far
 // more on gfx950 than the second launch)
 // ---------------------------------------------------------------------------------
+// SW: candidate regions per chunk (the waves of the call's k_stream workgroups)
+template <int SW>
 __global__ __launch_bounds__(FTPB) void k_finalize(Args a) {
   __shared__ FinalShared S;
   const int r = blockIdx.x;
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);
-  const ExactReq q = finalize_row(a, r, b, j, p, S);
+  const ExactReq q = finalize_row<SW>(a, r, b, j, p, S);
   // one call site for the exact resolution (an out-of-line call), reached by every
   // thread of a row that needs it
   if (q.need) finalize_exact(a, r, b, j, p, q.m, q.arg, q.draft, a.verify && j < a.k, q.l_draft, S);
+}
+
+hipError_t launch_finalize(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  const void* fn = a.swaves == 2 ? (const void*)k_finalize<2> : (const void*)k_finalize<8>;
+  return launch_args(fn, dim3((unsigned)a.R), dim3(FTPB), a, st, e0, e1);
 }
 
 }  // namespace strim

@@ -19,10 +19,12 @@
 namespace strim {
 
 constexpr int MAXP = 64;         // parameter rows carried inline per launch group
-constexpr int STPB = 512;        // threads of a k_stream workgroup (8 tokens each)
-constexpr int SWAVES = STPB / 64;  // waves of a k_stream workgroup
-constexpr int SLOTW = 64;        // fast-path candidates per wave of a k_stream workgroup
-constexpr int SLOT = SWAVES * SLOTW;  // ... per chunk
+// k_stream runs one chunk per workgroup with 8 SSEG tokens per thread: SSEG = 1 (512
+// threads, 8 waves) for small batches, whose time is latency, and SSEG = 4 (128 threads,
+// 2 waves) for large ones, whose time is instructions per token. Each wave writes its
+// fast-row candidates to its own region of the chunk's SLOT entries.
+constexpr int SMAXW = 8;         // most waves of a k_stream workgroup (regions per chunk)
+constexpr int SLOT = 512;        // fast-path candidate entries per chunk
 constexpr int FTPB = 256;        // threads of a k_finalize workgroup (one row)
 constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
 constexpr int FCAP = 4096;       // candidates k_finalize holds in LDS
@@ -52,9 +54,9 @@ struct ChunkStat {
                    // the value before temperature); -inf when not certified
   double S;        // sum exp(l - m) over the chunk (general rows)
   int32_t arg;     // first id reaching m
-  uint8_t nslot[SWAVES];  // fast rows: candidates of each wave (255 = overflow)
+  uint16_t nslot[SMAXW];  // fast rows: candidates of each wave region (0xFFFF = overflow)
 };
-static_assert(sizeof(ChunkStat) == 40, "ChunkStat layout");
+static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
 
 // General-path per-chunk summary of the tokens k_collect did not collect: fixed-point
 // mass and count per non-collected interval, and the two best surely-kept tokens by the
@@ -103,7 +105,8 @@ struct QStat {
 // Device scratch owned by a context (allocated once in strim_ctx_create).
 struct Scratch {
   ChunkStat* cstat;               // [rows][wmax]
-  Cand* slot;                     // [rows][wmax][SWAVES][SLOTW] fast-row candidates per wave
+  Cand* slot;                     // [rows][wmax][SLOT] fast-row candidates, one region per
+                                  // k_stream wave (SLOT / waves entries each)
                                   // (v before temperature, id)
   uint32_t* chc;                  // [rows][wmax][NCB] coarse counts
   unsigned long long* chm;        // [rows][wmax][NCB] coarse fixed-point masses
@@ -127,6 +130,7 @@ struct Args {
   int32_t R, V, W;   // rows in this group, vocab, chunks per row
   int32_t B, k;      // batch rows in this group and draft length (k = 0: sample)
   int32_t verify;
+  int32_t swaves;  // waves of the k_stream launch of this call (candidate regions per chunk)
   const uint32_t* mask;
   int64_t mask_stride;
   const int32_t* hist;
@@ -365,9 +369,11 @@ __device__ __forceinline__ void process_seg(const A& a, int i0, const RowParams&
 // this thread's first HPT history ids (16 bytes at a time when aligned) and returns the
 // row's history length; hist_count clears the table for [c0, c0 + SPAN), counts every
 // history id inside it (plus the verify draft prefix) and ends with a barrier.
-constexpr int HPT = 4096 / STPB;  // history ids each k_stream thread preloads
+template <int NT>
+constexpr int hpt() { return 4096 / NT; }  // history ids each thread preloads
 template <int NT, typename A>
-__device__ __forceinline__ int hist_load(const A& a, int b, int (&ids)[HPT]) {
+__device__ __forceinline__ int hist_load(const A& a, int b, int (&ids)[hpt<NT>()]) {
+  constexpr int HPT = hpt<NT>();
   const int t = threadIdx.x;
   const int32_t* h = a.hist ? a.hist + (int64_t)b * a.H : nullptr;
   // loads from clamped indices with no branch between them (see load_chunk)
@@ -398,8 +404,9 @@ __device__ __forceinline__ int hist_load(const A& a, int b, int (&ids)[HPT]) {
   return hl;
 }
 template <int NT, int SPAN, typename A>
-__device__ __forceinline__ void hist_count(const A& a, int b, int j, int c0, const int (&ids)[HPT],
-                                           int hl, uint32_t* s_cnt) {
+__device__ __forceinline__ void hist_count(const A& a, int b, int j, int c0,
+                                           const int (&ids)[hpt<NT>()], int hl, uint32_t* s_cnt) {
+  constexpr int HPT = hpt<NT>();
   const int t = threadIdx.x;
   uint4* s4 = (uint4*)s_cnt;
   for (int i = t; i < SPAN / 4; i += NT) s4[i] = make_uint4(0u, 0u, 0u, 0u);

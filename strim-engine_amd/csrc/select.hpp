@@ -26,6 +26,20 @@ __device__ __forceinline__ bool row_nofilter(const RowParams& p, int V) {
 }
 
 // Exclusive prefix and wave total of per-lane counts in [0, 31] via ballots.
+// Exclusive prefix over the wave of a per-lane count c < 2^BITS (one ballot per bit).
+template <int BITS>
+__device__ __forceinline__ int wave_excl_count_bits(int c, int* total) {
+  int ex = 0, tot = 0;
+#pragma unroll
+  for (int bit = 0; bit < BITS; ++bit) {
+    const uint64_t m = __ballot((c >> bit) & 1);
+    ex += lanes_below(m) << bit;
+    tot += __popcll(m) << bit;
+  }
+  *total = tot;
+  return ex;
+}
+
 __device__ __forceinline__ int wave_excl_count32(int c, int* total) {
   int ex = 0, tot = 0;
 #pragma unroll

@@ -8,16 +8,18 @@
 // (finalize_kernels.hip) then decides each row.
 //
 // The kernel is a template over the logits dtype, 16-byte alignment, penalties and the
-// allow-mask, so each launch runs straight-line per-token code. stream_kernels.hip is
-// built once per (dtype, penalties) pair, each object holding that pair's launcher.
+// allow-mask, so each launch runs straight-line per-token code, and over the segments
+// per thread (workgroup size). stream_kernels.hip is built once per (dtype, penalties,
+// segments) triple, each object holding that triple's launcher.
 #pragma once
 
 #include "select.hpp"
 
 namespace strim {
 
-constexpr int SSEG = CHUNK / (STPB * EPT);  // 8-token segments per thread
-static_assert(SSEG >= 1 && SSEG * STPB * EPT == CHUNK, "k_stream geometry");
+// threads of a k_stream workgroup with SSEG 8-token segments per thread
+template <int SSEG>
+constexpr int stpb() { return CHUNK / (EPT * SSEG); }
 
 // LDS of one k_stream workgroup.
 struct StreamShared {
@@ -25,12 +27,12 @@ struct StreamShared {
   uint32_t hc[NCB];
   unsigned long long hm[NCB];
   uint32_t lad[2 * WAVE];
-  float v[STPB / WAVE];
-  int i[STPB / WAVE], n[STPB / WAVE], f[STPB / WAVE];
-  uint32_t off[STPB / WAVE];
-  double d[STPB / WAVE];
-  float tf[4 * STPB / WAVE];
-  int ti[2 * STPB / WAVE];
+  float v[SMAXW];
+  int i[SMAXW], n[SMAXW], f[SMAXW];
+  uint32_t off[SMAXW];
+  double d[SMAXW];
+  float tf[4 * SMAXW];
+  int ti[2 * SMAXW];
 };
 
 // ---------------------------------------------------------------------------------
@@ -55,7 +57,7 @@ __device__ __forceinline__ float dv_rung_end(int r) {
 // around a load makes the compiler wait for the load at the join, which would serialise
 // the memory round trips. Aligned full chunks take 16-byte loads; otherwise each token
 // is loaded from a clamped index and out-of-row tokens become -inf.
-template <int DT, bool VEC>
+template <int DT, bool VEC, int SSEG>
 __device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)[SSEG], bool full,
                                            float (&x)[SSEG][EPT]) {
   const int64_t base = (int64_t)r * a.row_stride;
@@ -122,8 +124,11 @@ __device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)
 // 8-token segments at +8 l and +512 + 8 l, so each wave-wide load is 1 KB contiguous
 // and the first maximum of the chunk lies in the lowest wave that holds the maximum.
 // The chunk statistics are written without a closing barrier (see ChunkStat).
-template <int DT, bool VEC, bool PEN, bool MASK>
-__global__ __launch_bounds__(STPB) void k_stream(Args a) {
+template <int DT, bool VEC, bool PEN, bool MASK, int SSEG>
+__global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
+  constexpr int STPB = stpb<SSEG>();       // threads
+  constexpr int NW = STPB / WAVE;          // waves = candidate regions of the chunk
+  constexpr int SLOTW = SLOT / NW;         // candidates per wave region
   __shared__ StreamShared S;
   int r, c;
   map_block(r, c);
@@ -137,25 +142,33 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   ChunkStat* csp = &a.s.cstat[(int64_t)r * a.s.wmax + c];
 
   // history ids first: the counts are built while the logits are still in flight
-  int hid[HPT];
+  int hid[hpt<STPB>()];
   int hl = 0;
   if (pen) hl = hist_load<STPB>(a, b, hid);
   int i0[SSEG];
 #pragma unroll
   for (int s = 0; s < SSEG; ++s)
     i0[s] = c0 + w * (SSEG * WAVE * EPT) + s * (WAVE * EPT) + lane * EPT;
-  float v[SSEG][EPT];
-  load_chunk<DT, VEC>(a, r, i0, full, v);
+  // allow-bits byte of each segment (a segment starts on a multiple of 8), from a
+  // clamped index (tokens past the row end are -inf already); requested before the
+  // logits so that unpacking the logits does not wait for it separately
+  // (no branch around the loads: without a mask the unaligned variant reads a byte of
+  // the logits instead and ignores it)
   uint32_t bits[SSEG];
 #pragma unroll
   for (int s = 0; s < SSEG; ++s) bits[s] = 0xFFu;
   if constexpr (MASK) {
-    if (a.mask) {
-      // allow-bits byte of each segment (a segment starts on a multiple of 8), from a
-      // clamped index; tokens past the row end are -inf already
-      const uint8_t* mb = (const uint8_t*)(a.mask + (int64_t)r * a.mask_stride);
+    const uint8_t* mb = a.mask ? (const uint8_t*)(a.mask + (int64_t)r * a.mask_stride)
+                               : (const uint8_t*)a.logits;
 #pragma unroll
-      for (int s = 0; s < SSEG; ++s) bits[s] = mb[i0[s] < a.V ? (i0[s] >> 3) : 0];
+    for (int s = 0; s < SSEG; ++s) bits[s] = mb[a.mask && i0[s] < a.V ? (i0[s] >> 3) : 0];
+  }
+  float v[SSEG][EPT];
+  load_chunk<DT, VEC, SSEG>(a, r, i0, full, v);
+  if constexpr (MASK) {
+    if (!a.mask) {
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) bits[s] = 0xFFu;
     }
   }
   const bool fast = p.cls == CLS_FAST;
@@ -247,7 +260,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   float vm = S.v[0];
   int f_w = S.f[0], band_max = S.n[0], band_tot = S.n[0];
 #pragma unroll
-  for (int q = 1; q < STPB / WAVE; ++q) {
+  for (int q = 1; q < NW; ++q) {
     vm = fmaxf(vm, S.v[q]);
     f_w |= S.f[q];
     band_max = max(band_max, S.n[q]);
@@ -257,7 +270,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   {
     int wfirst = -1;
 #pragma unroll
-    for (int q = STPB / WAVE - 1; q >= 0; --q)
+    for (int q = NW - 1; q >= 0; --q)
       if (vm > -INFINITY && S.v[q] == vm) wfirst = q;
     if (w == (wfirst < 0 ? 0 : wfirst)) {
       int fid = 0x7FFFFFFF;
@@ -287,7 +300,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
     float vlo = p.min_p > 0.0f ? minp_vlo(m_w, p) : -INFINITY;
     // the ladder bounds the chunk's top-k when the min-p band alone could hold more
     // than 2k tokens or overflow a wave's region
-    if (topk && (band_max > SLOTW || band_tot > max(2 * p.top_k, 2 * SLOTW))) {
+    if (topk && (band_max > SLOTW || band_tot > max(2 * p.top_k, 128))) {
 #pragma unroll
       for (int s = 0; s < SSEG; ++s)
 #pragma unroll
@@ -338,9 +351,9 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
     // each wave writes its candidates to its own region of the chunk (no atomics, no
     // barrier) and its count to its byte of nslot (255 = overflow)
     int wtot;
-    const int wex = wave_excl_count32(mycnt, &wtot);
+    const int wex = wave_excl_count_bits<(SSEG == 1 ? 4 : SSEG == 2 ? 5 : 6)>(mycnt, &wtot);
     if (wtot <= SLOTW) {
-      Cand* dst = a.s.slot + (((int64_t)r * a.s.wmax + c) * SWAVES + w) * SLOTW;
+      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT + w * SLOTW;
       int pos = wex;
 #pragma unroll
       for (int s = 0; s < SSEG; ++s)
@@ -348,7 +361,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
         for (int e = 0; e < EPT; ++e)
           if ((sel[s] >> e) & 1u) dst[pos++] = Cand{v[s][e], i0[s] + e};
     }
-    if (lane == 0) csp->nslot[w] = (uint8_t)(wtot <= SLOTW ? wtot : 255);
+    if (lane == 0) csp->nslot[w] = (uint16_t)(wtot <= SLOTW ? wtot : 0xFFFF);
   } else if (p.cls == CLS_GENERAL && live) {
     // processed logits; chunk sum exp(l - m_w) and a coarse histogram of m_w - l
     // (k_collect's bounds)
@@ -379,7 +392,7 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
     __syncthreads();
     cs.n = 0;
 #pragma unroll
-    for (int q = 0; q < SWAVES; ++q) cs.n += S.n[q];
+    for (int q = 0; q < NW; ++q) cs.n += S.n[q];
     if (t < NCB) {
       const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
       a.s.chc[o] = S.hc[t];
@@ -391,16 +404,36 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
       float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
       int id0 = -1, id1 = -1;
 #pragma unroll
-      for (int s = 0; s < SSEG; ++s)
+      for (int s = 0; s < SSEG; ++s) {
+        // the segment's 8 uniforms: two Philox blocks (a segment starts on a multiple of 8)
+        float u[EPT];
+        if (a.noise) {
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) {
+            const int id = i0[s] + e < a.V ? i0[s] + e : 0;
+            u[e] = a.noise[(int64_t)r * a.noise_stride + id];
+          }
+        } else {
+#pragma unroll
+          for (int hb = 0; hb < 2; ++hb) {
+            const uint4 wb = philox_block(key, (uint64_t)((i0[s] >> 2) + hb));
+            u[4 * hb] = u01(wb.x); u[4 * hb + 1] = u01(wb.y);
+            u[4 * hb + 2] = u01(wb.z); u[4 * hb + 3] = u01(wb.w);
+          }
+        }
+        // ids rise along the thread's tokens: a strict compare keeps the first of ties
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-          if (!(l[s][e] > -INFINITY)) continue;
+          const float sc = l[s][e] > -INFINITY ? l[s][e] + gumbel32(u[e]) : -INFINITY;
           const int id = i0[s] + e;
-          const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
-                                  : philox_uniform(key, (uint64_t)id);
-          top2_merge(s0, l0, id0, s1, l1, id1, l[s][e] + gumbel32(u), l[s][e], id, -INFINITY,
-                     0.f, -1);
+          if (sc > s0) {
+            s1 = s0; l1 = l0; id1 = id0;
+            s0 = sc; l0 = l[s][e]; id0 = id;
+          } else if (sc > s1) {
+            s1 = sc; l1 = l[s][e]; id1 = id;
+          }
         }
+      }
       block_top2<STPB>(s0, l0, id0, s1, l1, id1, S.tf, S.ti);
       if (t == 0) {
         ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
@@ -411,14 +444,17 @@ __global__ __launch_bounds__(STPB) void k_stream(Args a) {
   if (t == 0) {
     *(float4*)csp = make_float4(cs.m, __int_as_float(cs.n), __int_as_float(cs.flags), cs.g);
     csp->S = cs.S;
-    if (!(fast && live)) *(uint64_t*)csp->nslot = 0ull;
+    if (!(fast && live)) {
+      *(uint64_t*)&csp->nslot[0] = 0ull;
+      *(uint64_t*)&csp->nslot[4] = 0ull;
+    }
   }
 }
 
-// Launches the k_stream variant of one (dtype, penalties) pair that matches the call's
-// alignment and mask. Defined in stream_kernels.hip, one object per pair; unaligned
-// calls always take the penalties object.
-template <int DT, bool PEN>
+// Launches the k_stream variant of one (dtype, penalties, segments) triple that matches
+// the call's alignment and mask. Defined in stream_kernels.hip, one object per triple;
+// unaligned calls always take the penalties object.
+template <int DT, bool PEN, int SSEG>
 hipError_t launch_stream_group(const Args& a, dim3 grid, hipStream_t st, hipEvent_t e0,
                                hipEvent_t e1);
 
