@@ -47,6 +47,21 @@ __device__ __forceinline__ int dv_rung(float dv) {
   const int r = (int)(__float_as_uint(dv) >> 20) - (int)VRUNG0;
   return r < 0 ? 0 : (r > VRUNG - 1 ? VRUNG - 1 : r);
 }
+// x[e] for a lane-varying e, by a three-level merge under bit masks of e. Integer
+// merges, not selects: a select between two elements of one array may be folded into
+// an indexed load, which would move the whole array to scratch memory.
+__device__ __forceinline__ uint32_t merge_bits(uint32_t lo, uint32_t hi, uint32_t m) {
+  return lo ^ ((lo ^ hi) & m);
+}
+__device__ __forceinline__ float pick8(const float (&x)[EPT], int e) {
+  const uint32_t m0 = 0u - ((uint32_t)e & 1u), m1 = 0u - (((uint32_t)e >> 1) & 1u);
+  const uint32_t m2 = 0u - (((uint32_t)e >> 2) & 1u);
+  uint32_t a[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    a[q] = merge_bits(__float_as_uint(x[2 * q]), __float_as_uint(x[2 * q + 1]), m0);
+  return __uint_as_float(merge_bits(merge_bits(a[0], a[1], m1), merge_bits(a[2], a[3], m1), m2));
+}
 // Smallest dv above rung r (r < VRUNG - 1).
 __device__ __forceinline__ float dv_rung_end(int r) {
   return __uint_as_float(((uint32_t)r + 1u + VRUNG0) << 20);
@@ -185,7 +200,6 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   // Dividing by T > 0 is monotone, so maxima and candidate bounds are found on v; only
   // the chunk maximum and (in k_finalize) the candidates are divided. Tokens past the
   // row end load as -inf (not allowed).
-  bool nf = false;
   float vmax = -INFINITY;
 #pragma unroll
   for (int s = 0; s < SSEG; ++s) {
@@ -212,12 +226,17 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
           y = y - p.pres;
         }
       }
-      if constexpr (MASK) y = ((bits[s] >> e) & 1u) ? y : -INFINITY;
-      nf |= !(y < INFINITY);  // NaN or +inf in an allowed position
+      if constexpr (MASK) {
+        // all ones where the token is allowed: y or -inf by a bit merge, no compare
+        const uint32_t keep = (uint32_t)((int32_t)(bits[s] << (31 - e)) >> 31);
+        y = __uint_as_float((__float_as_uint(y) & keep) | (0xFF800000u & ~keep));
+      }
       v[s][e] = y;
-      vmax = fmaxf(vmax, y);
+      vmax = __builtin_elementwise_maximum(vmax, y);  // NaN-propagating
     }
   }
+  // NaN or +inf in an allowed position (the maximum above keeps a NaN)
+  const bool nf = !(vmax < INFINITY);
   if (a.verify && j < a.k) {
     const int d = a.drafts[(int64_t)b * a.k + j];
 #pragma unroll
@@ -234,37 +253,20 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   }
   if (c == 0 && t == 0) a.s.ncand[r] = 0u;
 
-  // ---- wave maxima; for fast top-k rows, an upper bound on each wave's min-p band ----
-  // (the band against the wave maximum holds the band against the chunk maximum)
+  // ---- wave maxima ----------------------------------------------------------------
   const float wmv = wave_max_f(vmax);
-  int band = 1 << 20;
-  if (fast && topk && p.min_p > 0.0f) {
-    band = 0;
-    if (wmv > -INFINITY) {
-      const float vlo_w = minp_vlo(wmv / p.T, p);
-      int cb = 0;
-#pragma unroll
-      for (int s = 0; s < SSEG; ++s)
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) cb += v[s][e] >= vlo_w ? 1 : 0;
-      band = wave_sum(cb);
-    }
-  }
   const int fw = __any(nf) ? 1 : 0;
   if (lane == 0) {
     S.v[w] = wmv;
     S.f[w] = fw;
-    S.n[w] = band;
   }
   __syncthreads();
   float vm = S.v[0];
-  int f_w = S.f[0], band_max = S.n[0], band_tot = S.n[0];
+  int f_w = S.f[0];
 #pragma unroll
   for (int q = 1; q < NW; ++q) {
     vm = fmaxf(vm, S.v[q]);
     f_w |= S.f[q];
-    band_max = max(band_max, S.n[q]);
-    band_tot += S.n[q];
   }
   // the first maximum: the lowest wave holding it finds its first token and records it
   {
@@ -297,69 +299,86 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   if (fast && live) {
     // Local candidates, in v space: every token that can pass min-p (on the row maximum
     // m >= m_w) and the chunk's top-k, written as (v, id) to the wave's slot region.
-    float vlo = p.min_p > 0.0f ? minp_vlo(m_w, p) : -INFINITY;
-    // the ladder bounds the chunk's top-k when the min-p band alone could hold more
-    // than 2k tokens or overflow a wave's region
-    if (topk && (band_max > SLOTW || band_tot > max(2 * p.top_k, 128))) {
+    // A lower bound of -FLT_MAX keeps the -inf of disallowed tokens out in one compare.
+    float vlo = p.min_p > 0.0f ? fmaxf(minp_vlo(m_w, p), -__FLT_MAX__) : -__FLT_MAX__;
+    uint32_t sel[SSEG];  // bit e of sel[s]: token i0[s] + e is a candidate
+    int wtot, wex;
+    auto select = [&]() {
+      int mycnt = 0;
 #pragma unroll
-      for (int s = 0; s < SSEG; ++s)
+      for (int s = 0; s < SSEG; ++s) {
+        sel[s] = 0u;
 #pragma unroll
-        for (int e = 0; e < EPT; ++e)
-          if (v[s][e] >= vlo && v[s][e] > -INFINITY) atomicAdd(&S.lad[dv_rung(vm - v[s][e])], 1u);
+        for (int e = 0; e < EPT; ++e) sel[s] |= (v[s][e] >= vlo ? 1u : 0u) << e;
+        mycnt += __popc(sel[s]);
+      }
+      wex = wave_excl_count_bits<(SSEG == 1 ? 4 : SSEG == 2 ? 5 : 6)>(mycnt, &wtot);
+    };
+    select();
+    if (topk) {
+      // the ladder bounds the chunk's top-k when the min-p band alone holds more than
+      // 2k tokens or overflows a wave's region
+      if (lane == 0) S.n[w] = wtot;
       __syncthreads();
-      // every wave finds the first rung whose cumulative count reaches k (lane owns
-      // rungs 2 lane and 2 lane + 1)
-      const uint32_t h0 = S.lad[2 * lane], h1 = S.lad[2 * lane + 1];
-      uint32_t cum = h0 + h1;
+      int band_max = S.n[0], band_tot = S.n[0];
 #pragma unroll
-      for (int o = 1; o < WAVE; o <<= 1) {
-        const uint32_t u = (uint32_t)__shfl_up((int)cum, o, WAVE);
-        if (lane >= o) cum += u;
+      for (int q = 1; q < NW; ++q) {
+        band_max = max(band_max, S.n[q]);
+        band_tot += S.n[q];
       }
-      const uint64_t reach = __ballot(cum >= (uint32_t)p.top_k);
-      if (reach) {
-        const int ln = (int)__ffsll((long long)reach) - 1;
-        const uint32_t before = (uint32_t)__shfl((int)(cum - h0 - h1), ln, WAVE);
-        const uint32_t hl0 = (uint32_t)__shfl((int)h0, ln, WAVE);
-        const int rstar = 2 * ln + (before + hl0 >= (uint32_t)p.top_k ? 0 : 1);
-        if (rstar < VRUNG - 1) {
-          // v > vm - end(rstar) holds the rung; the margin (a few ulps of the values
-          // involved) keeps tokens whose l = v / T ties with one inside it
-          const float bnd = dv_rung_end(rstar);
-          const float thr = vm - bnd;
-          const float margin = (fabsf(vm) + fabsf(thr)) * 1e-6f + bnd * 1.6e-5f + 1e-30f;
-          vlo = fmaxf(vlo, thr - margin);
-          // the rungs up to rstar hold >= k tokens of the window, all with v >= g
-          cs.g = thr - margin;
+      if (band_max > SLOTW || band_tot > max(2 * p.top_k, 128)) {
+#pragma unroll
+        for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+          for (int e = 0; e < EPT; ++e)
+            if ((sel[s] >> e) & 1u) atomicAdd(&S.lad[dv_rung(vm - v[s][e])], 1u);
+        __syncthreads();
+        // every wave finds the first rung whose cumulative count reaches k (lane owns
+        // rungs 2 lane and 2 lane + 1)
+        const uint32_t h0 = S.lad[2 * lane], h1 = S.lad[2 * lane + 1];
+        uint32_t cum = h0 + h1;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+          const uint32_t u = (uint32_t)__shfl_up((int)cum, o, WAVE);
+          if (lane >= o) cum += u;
         }
-      }
-    }
-    uint32_t sel[SSEG];
-    int mycnt = 0;
-#pragma unroll
-    for (int s = 0; s < SSEG; ++s) {
-      sel[s] = 0u;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const float y = v[s][e];
-        if (y >= vlo && y > -INFINITY) {
-          sel[s] |= 1u << e;
-          ++mycnt;
+        const uint64_t reach = __ballot(cum >= (uint32_t)p.top_k);
+        if (reach) {
+          const int ln = (int)__ffsll((long long)reach) - 1;
+          const uint32_t before = (uint32_t)__shfl((int)(cum - h0 - h1), ln, WAVE);
+          const uint32_t hl0 = (uint32_t)__shfl((int)h0, ln, WAVE);
+          const int rstar = 2 * ln + (before + hl0 >= (uint32_t)p.top_k ? 0 : 1);
+          if (rstar < VRUNG - 1) {
+            // v > vm - end(rstar) holds the rung; the margin (a few ulps of the values
+            // involved) keeps tokens whose l = v / T ties with one inside it
+            const float bnd = dv_rung_end(rstar);
+            const float thr = vm - bnd;
+            const float margin = (fabsf(vm) + fabsf(thr)) * 1e-6f + bnd * 1.6e-5f + 1e-30f;
+            // the rungs up to rstar hold >= k tokens of the window, all with v >= g
+            cs.g = thr - margin;
+            if (cs.g > vlo) {
+              vlo = cs.g;
+              select();
+            }
+          }
         }
       }
     }
     // each wave writes its candidates to its own region of the chunk (no atomics, no
-    // barrier) and its count to its byte of nslot (255 = overflow)
-    int wtot;
-    const int wex = wave_excl_count_bits<(SSEG == 1 ? 4 : SSEG == 2 ? 5 : 6)>(mycnt, &wtot);
+    // barrier) and its count to its entry of nslot (0xFFFF = overflow); a lane loops
+    // over its set bits only, so waves without candidates skip the writes entirely
     if (wtot <= SLOTW) {
       Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT + w * SLOTW;
       int pos = wex;
 #pragma unroll
-      for (int s = 0; s < SSEG; ++s)
-#pragma unroll
-        for (int e = 0; e < EPT; ++e)
-          if ((sel[s] >> e) & 1u) dst[pos++] = Cand{v[s][e], i0[s] + e};
+      for (int s = 0; s < SSEG; ++s) {
+        uint32_t m = sel[s];
+        while (m) {
+          const int e = __builtin_ctz(m);
+          m &= m - 1u;
+          dst[pos++] = Cand{pick8(v[s], e), i0[s] + e};
+        }
+      }
     }
     if (lane == 0) csp->nslot[w] = (uint16_t)(wtot <= SLOTW ? wtot : 0xFFFF);
   } else if (p.cls == CLS_GENERAL && live) {
