@@ -39,12 +39,14 @@ __device__ __forceinline__ void finish_row(const Args& a, int r, int status, int
 constexpr int FSEG = FCAP / (FTPB / WAVE);  // survivors per wave segment in phase 2
 struct FinalShared {
   uint64_t key[FCAP];       // the row's surviving candidate keys (32 KB)
-  uint32_t rpre[SMAXW * 256];  // per k_stream wave region: first candidate position
-                              // within its 64-chunk block (add the block offsets in off[])
+  uint32_t rpre[SMAXW * 256];  // per k_stream wave region: first position of its entries
+                              // past the speculative depth, within its 64-chunk block
+                              // (add the block offsets in off[])
+  uint16_t rcnt[SMAXW * 256];  // per region: candidates written by k_stream
   uint32_t hist[256];       // d-histogram / radix digits
   float v[FTPB / WAVE], g[FTPB / WAVE];
   int i[FTPB / WAVE], f[FTPB / WAVE];
-  uint32_t off[FTPB / WAVE], cnt[FTPB / WAVE];
+  uint32_t off[FTPB / WAVE], cnt[FTPB / WAVE], seg[FTPB / WAVE];
   double d[FTPB / WAVE];
   uint64_t u[FTPB / WAVE];
   int misc[8];
@@ -122,6 +124,56 @@ __device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int 
 //      the survivors' span;
 //   3. wave 0 alone: top-k (from the histogram), sort, top-p, draw, with wave-wide
 //      operations only.
+// The row's global inputs that do not depend on its parameters, requested before the
+// parameters are waited for: the chunk statistics (one chunk per thread), the first
+// entries of every candidate region (a speculative gather; the region counts arrive with
+// the statistics, so the common row needs one memory round trip, not two), the noise
+// and the draft. There is no branch between the loads (see load_chunk); a missing
+// optional input reads the row's own state instead and is ignored.
+constexpr int PRE_E = 8;  // speculative candidate entries per thread
+struct RowPre {
+  ChunkStat cs;
+  Cand c[PRE_E];
+  float n0, n1, l_draft;
+  int draft;
+  int lk;  // log2 of the speculative depth K per region
+};
+template <int SW>
+__device__ __forceinline__ RowPre prefetch_row(const Args& a, int r, int b, int j) {
+  constexpr int slotw = SLOT / SW;
+  RowPre f;
+  const int t = threadIdx.x;
+  f.cs = a.s.cstat[(int64_t)r * a.s.wmax + (t < a.W ? t : 0)];
+  // depth K: the largest power of two with K * regions <= the entries of the workgroup,
+  // at least 2 (one 16-byte load), at most a region
+  const int nreg = SW * a.W;
+  const int fit = (FTPB * PRE_E) / nreg;
+  int lk = fit >= 2 ? 31 - __clz(fit) : 1;
+  lk = min(lk, 31 - __clz(slotw));
+  f.lk = lk;
+  const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
+#pragma unroll
+  for (int q = 0; q < PRE_E / 2; ++q) {
+    const int e = t * PRE_E + 2 * q;
+    const int g = e >> lk, o = e & ((1 << lk) - 1);
+    const uint4 v = *(const uint4*)(slots + (g < nreg ? (int64_t)g * slotw + o : 0));
+    f.c[2 * q] = Cand{__uint_as_float(v.x), (int32_t)v.y};
+    f.c[2 * q + 1] = Cand{__uint_as_float(v.z), (int32_t)v.w};
+  }
+  RowState* rsp = &a.s.rs[r];
+  const bool gum = a.noise && a.noise_mode != STRIM_NOISE_ICDF;
+  const float* nz = a.noise ? a.noise + (int64_t)r * a.noise_stride : (const float*)rsp;
+  f.n0 = nz[gum ? a.V : 0];
+  f.n1 = nz[gum ? a.V : 1];
+  const bool vdr = a.verify && j < a.k;
+  const int32_t* dp = vdr ? a.drafts + (int64_t)b * a.k + j : (const int32_t*)rsp;
+  const int d = *dp;
+  f.draft = vdr ? d : -1;
+  const float ld = rsp->l_draft;
+  f.l_draft = vdr ? ld : -INFINITY;
+  return f;
+}
+
 // What the exact streaming resolution needs when a row cannot be finished in LDS.
 struct ExactReq {
   int need;
@@ -132,56 +184,58 @@ struct ExactReq {
 
 template <int SW>
 __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, int j,
-                                                 const RowParams& p, FinalShared& S) {
+                                                 const RowParams& p, const RowPre& pf,
+                                                 FinalShared& S) {
   const ExactReq done{0, 0.0f, -1, -1, 0.0f};
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int V = a.V, W = a.W;
   const bool vdr = a.verify && j < a.k;  // a verify row with a draft
-  RowState* rsp = &a.s.rs[r];
-  // the row's remaining global inputs, requested before anything waits
-  const int draft = vdr ? a.drafts[(int64_t)b * a.k + j] : -1;
-  const float l_draft = vdr ? rsp->l_draft : -INFINITY;
+  const int draft = pf.draft;
+  const float l_draft = pf.l_draft;
   float u_draw = 0.0f, u_acc = 0.0f;
   if (a.noise && !p.greedy) {
-    const float* nz = a.noise + (int64_t)r * a.noise_stride;
-    if (a.noise_mode == STRIM_NOISE_ICDF) {
-      u_draw = nz[0];
-      u_acc = nz[1];
-    } else {
-      u_acc = nz[V];
-    }
+    if (a.noise_mode == STRIM_NOISE_ICDF) u_draw = pf.n0;
+    u_acc = pf.n1;
   }
 
   // ---- phase 1: chunk statistics (W <= 256: one chunk per thread) -----------------
-  // (every load of phase 1 is issued before any of them is used: a load inside a
-  // divergent branch would be waited for at the branch's end)
-  ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (t < W ? t : 0)];
-  if (t >= W) cs = ChunkStat{-INFINITY, 0, 0, -INFINITY, 0.0, -1, {}};
-  uint32_t ctot = 0u;
-  int ff = cs.flags | (cs.n > 0 ? 4 : 0);
-  // candidate regions per chunk: one per k_stream wave, SLOT / sw entries each
+  // (threads past the row's chunks select neutral values; no branch around the loads)
+  const ChunkStat& cs = pf.cs;
+  const bool own = t < W;
+  int ff = own ? (cs.flags | (cs.n > 0 ? 4 : 0)) : 0;
+  // candidate regions per chunk: one per k_stream wave, SLOT / sw entries each; the
+  // first K entries of regions below npre were gathered speculatively, the rest of a
+  // region ("residual" entries) is gathered by position in phase 2
   constexpr int sw = SW, lsw = SW == 8 ? 3 : SW == 4 ? 2 : SW == 2 ? 1 : 0, slotw = SLOT / SW;
+  const int lk = pf.lk, npre = (FTPB * PRE_E) >> lk;
+  auto depth = [&](int g) { return g < npre ? (1u << lk) : 0u; };
+  uint32_t ctot = 0u, rtot = 0u;
 #pragma unroll
   for (int e = 0; e < SMAXW; ++e) {
-    const uint32_t ce = e < sw ? cs.nslot[e] : 0u;
+    const uint32_t ce = (e < sw && own) ? cs.nslot[e] : 0u;
     if (ce > (uint32_t)slotw) ff |= 2;  // a wave region overflowed
     ctot += ce;
+    const uint32_t dp = depth(sw * t + e);
+    rtot += ce > dp ? ce - dp : 0u;
   }
-  float mv = cs.m, gv = cs.g;
-  int mi = cs.arg;
+  float mv = own ? cs.m : -INFINITY, gv = own ? cs.g : -INFINITY;
+  int mi = own ? cs.arg : -1;
   wave_argmax(mv, mi);
   ff = wave_or_i(ff);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, WAVE));
+  const uint32_t wall = (uint32_t)wave_sum((int)ctot);
   uint32_t wtot;
-  const uint32_t wex = wave_excl_scan_u32(ctot, &wtot);
+  const uint32_t wex = wave_excl_scan_u32(rtot, &wtot);
   if (t < W) {
     uint32_t o = wex;
 #pragma unroll
     for (int e = 0; e < SMAXW; ++e) {
       if (e < sw) {
+        const uint32_t ce = cs.nslot[e], dp = depth(sw * t + e);
         S.rpre[sw * t + e] = o;
-        o += cs.nslot[e];
+        S.rcnt[sw * t + e] = (uint16_t)ce;
+        o += ce > dp ? ce - dp : 0u;
       }
     }
   }
@@ -192,11 +246,12 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     S.f[w] = ff;
     S.g[w] = gv;
     S.off[w] = wtot;
+    S.cnt[w] = wall;
   }
   __syncthreads();
   float m = S.v[0], G = S.g[0];
   int arg = S.i[0], flags = S.f[0];
-  uint32_t n_c = 0u;
+  uint32_t n_c = 0u, n_r = 0u;  // all candidates; residual entries
 #pragma unroll
   for (int q = 0; q < FTPB / WAVE; ++q) {
     if (q > 0) {
@@ -204,7 +259,8 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
       flags |= S.f[q];
       G = fmaxf(G, S.g[q]);
     }
-    n_c += S.off[q];
+    n_c += S.cnt[q];
+    n_r += S.off[q];
   }
 
   int status = STRIM_OK;
@@ -325,33 +381,44 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
       n_w += (uint32_t)__popcll(msk);
     }
   };
-  for (int base = 0; base < (int)n_c; base += GB * FTPB) {
+  // the speculative entries, valid below their region's count
+  {
+#pragma unroll
+    for (int i = 0; i < PRE_E; ++i) {
+      const int e = t * PRE_E + i;
+      const int g = e >> lk, o = e & ((1 << lk) - 1);
+      const bool ok = g < nreg && o < (int)S.rcnt[g < nreg ? g : 0];
+      take(ok ? pf.c[i] : Cand{-INFINITY, -1});
+    }
+  }
+  // the residual entries, by position
+  for (int base = 0; base < (int)n_r; base += GB * FTPB) {
     Cand cd[GB];
 #pragma unroll
     for (int q = 0; q < GB; ++q) {
       const int pos = base + q * FTPB + t;
       cd[q] = Cand{-INFINITY, -1};
-      if (pos < (int)n_c) {
+      if (pos < (int)n_r) {
         int lo = 0, hi = nreg - 1;  // last region whose first position <= pos
         while (lo < hi) {
           const int mid = (lo + hi + 1) >> 1;
           if ((int)gpre(mid) <= pos) lo = mid;
           else hi = mid - 1;
         }
-        cd[q] = slots[(int64_t)lo * slotw + (pos - (int)gpre(lo))];
+        cd[q] = slots[(int64_t)lo * slotw + depth(lo) + (pos - (int)gpre(lo))];
       }
     }
 #pragma unroll
     for (int q = 0; q < GB; ++q) take(cd[q]);
   }
-  if (lane == 0) S.off[w] = n_w;
+  if (lane == 0) S.seg[w] = n_w;
   __syncthreads();
   uint32_t segn[FTPB / WAVE];
   int over = 0;
   uint32_t n_s = 0u;
 #pragma unroll
   for (int q = 0; q < FTPB / WAVE; ++q) {
-    segn[q] = S.off[q];
+    segn[q] = S.seg[q];
     over |= segn[q] > (uint32_t)FSEG;
     n_s += segn[q];
   }
@@ -549,8 +616,9 @@ __global__ __launch_bounds__(FTPB) void k_finalize(Args a) {
   const int r = blockIdx.x;
   int b, j;
   row_bj(a, r, b, j);
+  const RowPre pf = prefetch_row<SW>(a, r, b, j);
   const RowParams p = load_params(a, b, j);
-  const ExactReq q = finalize_row<SW>(a, r, b, j, p, S);
+  const ExactReq q = finalize_row<SW>(a, r, b, j, p, pf, S);
   // one call site for the exact resolution (an out-of-line call), reached by every
   // thread of a row that needs it
   if (q.need) finalize_exact(a, r, b, j, p, q.m, q.arg, q.draft, a.verify && j < a.k, q.l_draft, S);
