@@ -365,19 +365,16 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   // Candidates below the v-space bound of G and min-p (most of them: the chunks bound
   // min-p on their own maximum) leave after one compare, without the division.
   const float vthr = fmaxf(Gm, minp ? minp_vlo(m, p) : -INFINITY);
-  // one candidate of this lane (id < 0: none): l = v / T as the oracle rounds it, pruned
-  // by G and min-p, compacted into the wave's LDS segment (called by the whole wave)
+  // One candidate of this lane (id < 0: none), called by the whole wave: the v-space
+  // pretest only; (v, id) pairs that pass are compacted into the wave's LDS segment.
+  // The division and the exact tests run once per survivor after the gathers.
   auto take = [&](const Cand cd) {
-    bool k = cd.id >= 0 && cd.l >= vthr;
-    if (!__any(k)) return;
-    k = k && cd.l >= Gm;
-    const float l = k ? cd.l / p.T : -INFINITY;
-    k = k && l > -INFINITY && (!minp || ((double)l - (double)m) >= lmp);
+    const bool k = cd.id >= 0 && cd.l >= vthr;
     const uint64_t msk = __ballot(k);
     if (msk) {
       const uint32_t dst = n_w + (uint32_t)lanes_below(msk);
-      if (k && dst < (uint32_t)FSEG) S.key[w * FSEG + dst] = ckey(l, cd.id);
-      if (k && topk) atomicAdd(&S.hist[dbin(m, l, scale)], 1u);
+      if (k && dst < (uint32_t)FSEG)
+        S.key[w * FSEG + dst] = ((uint64_t)__float_as_uint(cd.l) << 32) | (uint32_t)cd.id;
       n_w += (uint32_t)__popcll(msk);
     }
   };
@@ -410,6 +407,27 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     }
 #pragma unroll
     for (int q = 0; q < GB; ++q) take(cd[q]);
+  }
+  // l = v / T as the oracle rounds it, min-p on the row maximum and the top-k histogram
+  // for the wave's pretest survivors, compacted in place into order keys
+  if (n_w <= (uint32_t)FSEG) {
+    uint64_t* seg = S.key + w * FSEG;
+    uint32_t n2 = 0u;
+    for (uint32_t base = 0; base < n_w; base += WAVE) {
+      const uint32_t i = base + (uint32_t)lane;
+      bool k = i < n_w;
+      const uint64_t raw = k ? seg[i] : 0ull;
+      const int id = (int)(uint32_t)raw;
+      const float l = k ? __uint_as_float((uint32_t)(raw >> 32)) / p.T : -INFINITY;
+      k = k && l > -INFINITY && (!minp || ((double)l - (double)m) >= lmp);
+      const uint64_t msk = __ballot(k);
+      wave_sync();  // every read of the block precedes the writes (positions only fall)
+      if (k) seg[n2 + (uint32_t)lanes_below(msk)] = ckey(l, id);
+      if (k && topk) atomicAdd(&S.hist[dbin(m, l, scale)], 1u);
+      n2 += (uint32_t)__popcll(msk);
+      wave_sync();
+    }
+    n_w = n2;
   }
   if (lane == 0) S.seg[w] = n_w;
   __syncthreads();
