@@ -130,7 +130,6 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
   // k_final decides the general rows (k_finalize leaves them pending)
   need_final = need_collect;
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
-  a.swaves = CHUNK / (EPT * stream_sseg(a)) / WAVE;
   hipError_t e = hipSuccess;
   auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };
   timed(ctx, KID_STREAM,

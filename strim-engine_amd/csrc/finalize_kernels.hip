@@ -39,10 +39,10 @@ __device__ __forceinline__ void finish_row(const Args& a, int r, int status, int
 constexpr int FSEG = FCAP / (FTPB / WAVE);  // survivors per wave segment in phase 2
 struct FinalShared {
   uint64_t key[FCAP];       // the row's surviving candidate keys (32 KB)
-  uint32_t rpre[SMAXW * 256];  // per k_stream wave region: first position of its entries
-                              // past the speculative depth, within its 64-chunk block
-                              // (add the block offsets in off[])
-  uint16_t rcnt[SMAXW * 256];  // per region: candidates written by k_stream
+  uint32_t rpre[256];       // per chunk: first position of its candidates past the
+                            // speculative depth, within its 64-chunk block (add the block
+                            // offsets in off[])
+  uint16_t rcnt[256];       // per chunk: candidates written by k_stream
   uint32_t hist[256];       // d-histogram / radix digits
   float v[FTPB / WAVE], g[FTPB / WAVE];
   int i[FTPB / WAVE], f[FTPB / WAVE];
@@ -136,27 +136,26 @@ struct RowPre {
   Cand c[PRE_E];
   float n0, n1, l_draft;
   int draft;
-  int lk;  // log2 of the speculative depth K per region
+  int kd;          // speculative depth K per chunk region (even)
+  uint32_t kmag;   // entry e lies in region umulhi(e, kmag) = e / K
 };
-template <int SW>
 __device__ __forceinline__ RowPre prefetch_row(const Args& a, int r, int b, int j) {
-  constexpr int slotw = SLOT / SW;
   RowPre f;
   const int t = threadIdx.x;
   f.cs = a.s.cstat[(int64_t)r * a.s.wmax + (t < a.W ? t : 0)];
-  // depth K: the largest power of two with K * regions <= the entries of the workgroup,
-  // at least 2 (one 16-byte load), at most a region
-  const int nreg = SW * a.W;
-  const int fit = (FTPB * PRE_E) / nreg;
-  int lk = fit >= 2 ? 31 - __clz(fit) : 1;
-  lk = min(lk, 31 - __clz(slotw));
-  f.lk = lk;
+  // depth K: the largest even number with K * chunks <= the entries of the workgroup, at
+  // least 2 (one 16-byte load), at most a region. e / K = umulhi(e, ceil(2^32 / K)) is
+  // exact while e * K < 2^32.
+  const int kd = min(SLOT, max(2, ((FTPB * PRE_E) / a.W) & ~1));
+  const uint32_t kmag = 0xFFFFFFFFu / (uint32_t)kd + 1u;
+  f.kd = kd;
+  f.kmag = kmag;
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
 #pragma unroll
   for (int q = 0; q < PRE_E / 2; ++q) {
     const int e = t * PRE_E + 2 * q;
-    const int g = e >> lk, o = e & ((1 << lk) - 1);
-    const uint4 v = *(const uint4*)(slots + (g < nreg ? (int64_t)g * slotw + o : 0));
+    const int g = (int)__umulhi((uint32_t)e, kmag), o = e - g * kd;
+    const uint4 v = *(const uint4*)(slots + (g < a.W ? (int64_t)g * SLOT + o : 0));
     f.c[2 * q] = Cand{__uint_as_float(v.x), (int32_t)v.y};
     f.c[2 * q + 1] = Cand{__uint_as_float(v.z), (int32_t)v.w};
   }
@@ -182,7 +181,6 @@ struct ExactReq {
   float l_draft;
 };
 
-template <int SW>
 __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, int j,
                                                  const RowParams& p, const RowPre& pf,
                                                  FinalShared& S) {
@@ -203,21 +201,15 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   const ChunkStat& cs = pf.cs;
   const bool own = t < W;
   int ff = own ? (cs.flags | (cs.n > 0 ? 4 : 0)) : 0;
-  // candidate regions per chunk: one per k_stream wave, SLOT / sw entries each; the
-  // first K entries of regions below npre were gathered speculatively, the rest of a
-  // region ("residual" entries) is gathered by position in phase 2
-  constexpr int sw = SW, lsw = SW == 8 ? 3 : SW == 4 ? 2 : SW == 2 ? 1 : 0, slotw = SLOT / SW;
-  const int lk = pf.lk, npre = (FTPB * PRE_E) >> lk;
-  auto depth = [&](int g) { return g < npre ? (1u << lk) : 0u; };
-  uint32_t ctot = 0u, rtot = 0u;
-#pragma unroll
-  for (int e = 0; e < SMAXW; ++e) {
-    const uint32_t ce = (e < sw && own) ? cs.nslot[e] : 0u;
-    if (ce > (uint32_t)slotw) ff |= 2;  // a wave region overflowed
-    ctot += ce;
-    const uint32_t dp = depth(sw * t + e);
-    rtot += ce > dp ? ce - dp : 0u;
-  }
+  // one candidate region per chunk, SLOT entries: the first K entries of the regions
+  // below npre were gathered speculatively, the rest ("residual" entries) are gathered by
+  // position in phase 2
+  const int kd = pf.kd, npre = (FTPB * PRE_E) / kd;
+  auto depth = [&](int g) { return g < npre ? (uint32_t)kd : 0u; };
+  const uint32_t ce = own ? cs.ncand : 0u;
+  if (ce > (uint32_t)SLOT) ff |= 2;  // the region overflowed
+  const uint32_t ctot = ce <= (uint32_t)SLOT ? ce : 0u;
+  const uint32_t rtot = ctot > depth(t) ? ctot - depth(t) : 0u;
   float mv = own ? cs.m : -INFINITY, gv = own ? cs.g : -INFINITY;
   int mi = own ? cs.arg : -1;
   wave_argmax(mv, mi);
@@ -227,17 +219,9 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   const uint32_t wall = (uint32_t)wave_sum((int)ctot);
   uint32_t wtot;
   const uint32_t wex = wave_excl_scan_u32(rtot, &wtot);
-  if (t < W) {
-    uint32_t o = wex;
-#pragma unroll
-    for (int e = 0; e < SMAXW; ++e) {
-      if (e < sw) {
-        const uint32_t ce = cs.nslot[e], dp = depth(sw * t + e);
-        S.rpre[sw * t + e] = o;
-        S.rcnt[sw * t + e] = (uint16_t)ce;
-        o += ce > dp ? ce - dp : 0u;
-      }
-    }
+  if (own) {
+    S.rpre[t] = wex;
+    S.rcnt[t] = (uint16_t)ctot;
   }
   if (t < 256) S.hist[t] = 0u;
   if (lane == 0) {
@@ -350,11 +334,10 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   if (minp) dspan = fminf(dspan, (float)-lmp);
   const float scale = 255.0f / fmaxf(dspan * 1.0001f, 1e-6f);
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
-  const int nreg = sw * W;
-  // global position of region rg's first candidate
+  // global position of region rg's first residual entry
   auto gpre = [&](int rg) {
     uint32_t o = S.rpre[rg];
-    const int blk = rg >> (6 + lsw);  // 64 chunks per wave of phase 1
+    const int blk = rg >> 6;  // 64 chunks per wave of phase 1
 #pragma unroll
     for (int q = 0; q < FTPB / WAVE; ++q)
       if (q < blk) o += S.off[q];
@@ -383,8 +366,8 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
 #pragma unroll
     for (int i = 0; i < PRE_E; ++i) {
       const int e = t * PRE_E + i;
-      const int g = e >> lk, o = e & ((1 << lk) - 1);
-      const bool ok = g < nreg && o < (int)S.rcnt[g < nreg ? g : 0];
+      const int g = (int)__umulhi((uint32_t)e, pf.kmag), o = e - g * kd;
+      const bool ok = g < W && o < (int)S.rcnt[g < W ? g : 0];
       take(ok ? pf.c[i] : Cand{-INFINITY, -1});
     }
   }
@@ -396,13 +379,13 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
       const int pos = base + q * FTPB + t;
       cd[q] = Cand{-INFINITY, -1};
       if (pos < (int)n_r) {
-        int lo = 0, hi = nreg - 1;  // last region whose first position <= pos
+        int lo = 0, hi = W - 1;  // last region whose first position <= pos
         while (lo < hi) {
           const int mid = (lo + hi + 1) >> 1;
           if ((int)gpre(mid) <= pos) lo = mid;
           else hi = mid - 1;
         }
-        cd[q] = slots[(int64_t)lo * slotw + depth(lo) + (pos - (int)gpre(lo))];
+        cd[q] = slots[(int64_t)lo * SLOT + depth(lo) + (pos - (int)gpre(lo))];
       }
     }
 #pragma unroll
@@ -627,24 +610,21 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
 // chunk's results visible; an in-kernel device-scope release per workgroup costs far
 // more on gfx950 than the second launch)
 // ---------------------------------------------------------------------------------
-// SW: candidate regions per chunk (the waves of the call's k_stream workgroups)
-template <int SW>
 __global__ __launch_bounds__(FTPB) void k_finalize(Args a) {
   __shared__ FinalShared S;
   const int r = blockIdx.x;
   int b, j;
   row_bj(a, r, b, j);
-  const RowPre pf = prefetch_row<SW>(a, r, b, j);
+  const RowPre pf = prefetch_row(a, r, b, j);
   const RowParams p = load_params(a, b, j);
-  const ExactReq q = finalize_row<SW>(a, r, b, j, p, pf, S);
+  const ExactReq q = finalize_row(a, r, b, j, p, pf, S);
   // one call site for the exact resolution (an out-of-line call), reached by every
   // thread of a row that needs it
   if (q.need) finalize_exact(a, r, b, j, p, q.m, q.arg, q.draft, a.verify && j < a.k, q.l_draft, S);
 }
 
 hipError_t launch_finalize(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-  const void* fn = a.swaves == 2 ? (const void*)k_finalize<2> : (const void*)k_finalize<8>;
-  return launch_args(fn, dim3((unsigned)a.R), dim3(FTPB), a, st, e0, e1);
+  return launch_args((const void*)k_finalize, dim3((unsigned)a.R), dim3(FTPB), a, st, e0, e1);
 }
 
 }  // namespace strim

@@ -23,7 +23,7 @@ constexpr int MAXP = 64;         // parameter rows carried inline per launch gro
 // threads, 8 waves) for small batches, whose time is latency, and SSEG = 4 (128 threads,
 // 2 waves) for large ones, whose time is instructions per token. Each wave writes its
 // fast-row candidates to its own region of the chunk's SLOT entries.
-constexpr int SMAXW = 8;         // most waves of a k_stream workgroup (regions per chunk)
+constexpr int SMAXW = 8;         // most waves of a k_stream workgroup
 constexpr int SLOT = 512;        // fast-path candidate entries per chunk
 constexpr int FTPB = 256;        // threads of a k_finalize workgroup (one row)
 constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
@@ -44,8 +44,8 @@ enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1 };
 
 enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
 
-// Written by k_stream without a closing barrier: m, n, flags and g by the first wave,
-// arg by the wave holding the first maximum, each nslot byte by its own wave.
+// Written by k_stream without a closing barrier: m, n, flags, g and ncand by the first
+// wave, arg by the wave holding the first maximum.
 struct ChunkStat {
   float m;         // chunk max of processed logits (-inf if none allowed)
   int32_t n;       // allowed tokens (fast and greedy rows: 1 if any)
@@ -54,7 +54,8 @@ struct ChunkStat {
                    // the value before temperature); -inf when not certified
   double S;        // sum exp(l - m) over the chunk (general rows)
   int32_t arg;     // first id reaching m
-  uint16_t nslot[SMAXW];  // fast rows: candidates of each wave region (0xFFFF = overflow)
+  uint32_t ncand;  // fast rows: candidates in the chunk's slot region (> SLOT: overflow)
+  uint32_t pad_[3];
 };
 static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
 
@@ -130,7 +131,6 @@ struct Args {
   int32_t R, V, W;   // rows in this group, vocab, chunks per row
   int32_t B, k;      // batch rows in this group and draft length (k = 0: sample)
   int32_t verify;
-  int32_t swaves;  // waves of the k_stream launch of this call (candidate regions per chunk)
   const uint32_t* mask;
   int64_t mask_stride;
   const int32_t* hist;

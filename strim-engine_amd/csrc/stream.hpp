@@ -142,8 +142,7 @@ __device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)
 template <int DT, bool VEC, bool PEN, bool MASK, int SSEG>
 __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   constexpr int STPB = stpb<SSEG>();       // threads
-  constexpr int NW = STPB / WAVE;          // waves = candidate regions of the chunk
-  constexpr int SLOTW = SLOT / NW;         // candidates per wave region
+  constexpr int NW = STPB / WAVE;          // waves
   __shared__ StreamShared S;
   int r, c;
   map_block(r, c);
@@ -293,12 +292,13 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   const float m_w = (p.greedy || !(vm > -INFINITY)) ? vm : vm / p.T;
   if (m_w == INFINITY) f_w = 1;
   if (!(m_w > -INFINITY)) n_w = 0;
-  ChunkStat cs{m_w, n_w, f_w, -INFINITY, 0.0, -1, {}};
+  ChunkStat cs{m_w, n_w, f_w, -INFINITY, 0.0, -1, 0u, {}};
+  uint32_t cs_ncand = 0u;
   const bool live = n_w > 0 && !f_w;
 
   if (fast && live) {
     // Local candidates, in v space: every token that can pass min-p (on the row maximum
-    // m >= m_w) and the chunk's top-k, written as (v, id) to the wave's slot region.
+    // m >= m_w) and the chunk's top-k, written as (v, id) to the chunk's slot region.
     // A lower bound of -FLT_MAX keeps the -inf of disallowed tokens out in one compare.
     float vlo = p.min_p > 0.0f ? fmaxf(minp_vlo(m_w, p), -__FLT_MAX__) : -__FLT_MAX__;
     uint32_t sel[SSEG];  // bit e of sel[s]: token i0[s] + e is a candidate
@@ -312,63 +312,67 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         for (int e = 0; e < EPT; ++e) sel[s] |= (v[s][e] >= vlo ? 1u : 0u) << e;
         mycnt += __popc(sel[s]);
       }
-      wex = wave_excl_count_bits<(SSEG == 1 ? 4 : SSEG == 2 ? 5 : 6)>(mycnt, &wtot);
+      wex = wave_excl_count_bits<(SSEG == 1 ? 4 : SSEG == 2 ? 5 : SSEG == 4 ? 6 : 7)>(mycnt, &wtot);
     };
-    select();
-    if (topk) {
-      // the ladder bounds the chunk's top-k when the min-p band alone holds more than
-      // 2k tokens or overflows a wave's region
+    // every wave publishes its count; a wave's candidates follow those of the waves
+    // before it (the conditions below are uniform over the workgroup)
+    int tot, before;
+    auto place = [&]() {
       if (lane == 0) S.n[w] = wtot;
       __syncthreads();
-      int band_max = S.n[0], band_tot = S.n[0];
+      tot = 0;
+      before = 0;
 #pragma unroll
-      for (int q = 1; q < NW; ++q) {
-        band_max = max(band_max, S.n[q]);
-        band_tot += S.n[q];
+      for (int q = 0; q < NW; ++q) {
+        before += q < w ? S.n[q] : 0;
+        tot += S.n[q];
       }
-      if (band_max > SLOTW || band_tot > max(2 * p.top_k, 128)) {
+    };
+    select();
+    place();
+    // the ladder bounds the chunk's top-k when the min-p band alone holds more than 2k
+    // tokens or overflows the region
+    if (topk && (tot > SLOT || tot > max(2 * p.top_k, 128))) {
 #pragma unroll
-        for (int s = 0; s < SSEG; ++s)
+      for (int s = 0; s < SSEG; ++s)
 #pragma unroll
-          for (int e = 0; e < EPT; ++e)
-            if ((sel[s] >> e) & 1u) atomicAdd(&S.lad[dv_rung(vm - v[s][e])], 1u);
-        __syncthreads();
-        // every wave finds the first rung whose cumulative count reaches k (lane owns
-        // rungs 2 lane and 2 lane + 1)
-        const uint32_t h0 = S.lad[2 * lane], h1 = S.lad[2 * lane + 1];
-        uint32_t cum = h0 + h1;
+        for (int e = 0; e < EPT; ++e)
+          if ((sel[s] >> e) & 1u) atomicAdd(&S.lad[dv_rung(vm - v[s][e])], 1u);
+      __syncthreads();  // (also orders every read of S.n above before its rewrite)
+      // every wave finds the first rung whose cumulative count reaches k (lane owns
+      // rungs 2 lane and 2 lane + 1)
+      const uint32_t h0 = S.lad[2 * lane], h1 = S.lad[2 * lane + 1];
+      uint32_t cum = h0 + h1;
 #pragma unroll
-        for (int o = 1; o < WAVE; o <<= 1) {
-          const uint32_t u = (uint32_t)__shfl_up((int)cum, o, WAVE);
-          if (lane >= o) cum += u;
-        }
-        const uint64_t reach = __ballot(cum >= (uint32_t)p.top_k);
-        if (reach) {
-          const int ln = (int)__ffsll((long long)reach) - 1;
-          const uint32_t before = (uint32_t)__shfl((int)(cum - h0 - h1), ln, WAVE);
-          const uint32_t hl0 = (uint32_t)__shfl((int)h0, ln, WAVE);
-          const int rstar = 2 * ln + (before + hl0 >= (uint32_t)p.top_k ? 0 : 1);
-          if (rstar < VRUNG - 1) {
-            // v > vm - end(rstar) holds the rung; the margin (a few ulps of the values
-            // involved) keeps tokens whose l = v / T ties with one inside it
-            const float bnd = dv_rung_end(rstar);
-            const float thr = vm - bnd;
-            const float margin = (fabsf(vm) + fabsf(thr)) * 1e-6f + bnd * 1.6e-5f + 1e-30f;
-            // the rungs up to rstar hold >= k tokens of the window, all with v >= g
-            cs.g = thr - margin;
-            if (cs.g > vlo) {
-              vlo = cs.g;
-              select();
-            }
+      for (int o = 1; o < WAVE; o <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)cum, o, WAVE);
+        if (lane >= o) cum += u;
+      }
+      const uint64_t reach = __ballot(cum >= (uint32_t)p.top_k);
+      if (reach) {
+        const int ln = (int)__ffsll((long long)reach) - 1;
+        const uint32_t bef = (uint32_t)__shfl((int)(cum - h0 - h1), ln, WAVE);
+        const uint32_t hl0 = (uint32_t)__shfl((int)h0, ln, WAVE);
+        const int rstar = 2 * ln + (bef + hl0 >= (uint32_t)p.top_k ? 0 : 1);
+        if (rstar < VRUNG - 1) {
+          // v > vm - end(rstar) holds the rung; the margin (a few ulps of the values
+          // involved) keeps tokens whose l = v / T ties with one inside it
+          const float bnd = dv_rung_end(rstar);
+          const float thr = vm - bnd;
+          const float margin = (fabsf(vm) + fabsf(thr)) * 1e-6f + bnd * 1.6e-5f + 1e-30f;
+          // the rungs up to rstar hold >= k tokens of the window, all with v >= g
+          cs.g = thr - margin;
+          if (cs.g > vlo) {
+            vlo = cs.g;
+            select();
           }
         }
       }
+      place();
     }
-    // each wave writes its candidates to its own region of the chunk (no atomics, no
-    // barrier) and its count to its entry of nslot (0xFFFF = overflow); a lane loops
-    // over its set bits only, so waves without candidates skip the writes entirely
-    if (wtot <= SLOTW) {
-      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT + w * SLOTW;
+    // a lane loops over its set bits only, so waves without candidates skip the writes
+    if (tot <= SLOT) {
+      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT + before;
       int pos = wex;
 #pragma unroll
       for (int s = 0; s < SSEG; ++s) {
@@ -380,7 +384,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         }
       }
     }
-    if (lane == 0) csp->nslot[w] = (uint16_t)(wtot <= SLOTW ? wtot : 0xFFFF);
+    cs_ncand = tot <= SLOT ? (uint32_t)tot : 0xFFFFFFFFu;
   } else if (p.cls == CLS_GENERAL && live) {
     // processed logits; chunk sum exp(l - m_w) and a coarse histogram of m_w - l
     // (k_collect's bounds)
@@ -463,10 +467,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   if (t == 0) {
     *(float4*)csp = make_float4(cs.m, __int_as_float(cs.n), __int_as_float(cs.flags), cs.g);
     csp->S = cs.S;
-    if (!(fast && live)) {
-      *(uint64_t*)&csp->nslot[0] = 0ull;
-      *(uint64_t*)&csp->nslot[4] = 0ull;
-    }
+    csp->ncand = cs_ncand;
   }
 }
 
