@@ -214,6 +214,19 @@ __device__ __forceinline__ int wave_excl_count(int c, int* total) {
 
 // Inclusive scan of doubles over the wave in a fixed order (deterministic): row_shr
 // steps within 16-lane rows, then the row totals through readlane.
+// Inclusive prefix sum over the wave (integer: exact): row_shr steps within each 16-lane
+// row, then the earlier rows' totals through readlane.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  int x = (int)v;
+  x += dpp_i<DPP_SHR1>(x);
+  x += dpp_i<DPP_SHR2>(x);
+  x += dpp_i<DPP_SHR4>(x);
+  x += dpp_i<DPP_SHR8>(x);
+  const int t0 = rl_i(x, 15), t1 = rl_i(x, 31), t2 = rl_i(x, 47);
+  const int row = (threadIdx.x & (WAVE - 1)) >> 4;
+  x += (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
+  return (uint32_t)x;
+}
 __device__ __forceinline__ double wave_incl_scan(double v) {
   v += dpp_d<DPP_SHR1>(v);
   v += dpp_d<DPP_SHR2>(v);

@@ -214,8 +214,7 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   int mi = own ? cs.arg : -1;
   wave_argmax(mv, mi);
   ff = wave_or_i(ff);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, WAVE));
+  gv = wave_max_f(gv);
   const uint32_t wall = (uint32_t)wave_sum((int)ctot);
   uint32_t wtot;
   const uint32_t wex = wave_excl_scan_u32(rtot, &wtot);

@@ -57,13 +57,7 @@ template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* scratch,
                                                         uint32_t* total) {
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-  uint32_t inc = v;
-  // Hillis-Steele within the wave on shuffles (integer: order does not matter)
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const uint32_t u = (uint32_t)__shfl_up((int)inc, o, WAVE);
-    if (lane >= o) inc += u;
-  }
+  const uint32_t inc = wave_incl_scan_u32(v);
   if (lane == WAVE - 1) scratch[w] = inc;
   __syncthreads();
   uint32_t base = 0, tot = 0;
@@ -302,13 +296,7 @@ __device__ uint64_t radix_select_kth(const uint64_t (&kk)[Q], uint64_t ref, uint
       const uint32_t h0 = s_hist[4 * lane], h1 = s_hist[4 * lane + 1], h2 = s_hist[4 * lane + 2],
                      h3 = s_hist[4 * lane + 3];
       const uint32_t own = h0 + h1 + h2 + h3;
-      uint32_t inc = own;
-#pragma unroll
-      for (int o = 1; o < WAVE; o <<= 1) {
-        const uint32_t u = (uint32_t)__shfl_up((int)inc, o, WAVE);
-        if (lane >= o) inc += u;
-      }
-      uint32_t cum = inc - own;
+      uint32_t cum = wave_incl_scan_u32(own) - own;
       const uint32_t hs[4] = {h0, h1, h2, h3};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -369,14 +357,8 @@ __device__ __forceinline__ uint64_t shfl_xor_u64v(uint64_t v, int o) {
 
 // Exclusive prefix over the wave (integer: exact); *total = wave sum.
 __device__ __forceinline__ uint32_t wave_excl_scan_u32(uint32_t v, uint32_t* total) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  uint32_t inc = v;
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const uint32_t u = (uint32_t)__shfl_up((int)inc, o, WAVE);
-    if (lane >= o) inc += u;
-  }
-  *total = (uint32_t)__shfl((int)inc, WAVE - 1, WAVE);
+  const uint32_t inc = wave_incl_scan_u32(v);
+  *total = (uint32_t)rl_i((int)inc, WAVE - 1);
   return inc - v;
 }
 
@@ -386,10 +368,13 @@ __device__ __forceinline__ double wave_excl_scan_f64(double v, double* total) {
   const int lane = threadIdx.x & (WAVE - 1);
   const double inc = wave_incl_scan(v);
   *total = rl_d(inc, WAVE - 1);
-  const uint64_t bits = (uint64_t)__double_as_longlong(inc);
-  const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)bits, 1, WAVE);
-  const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(bits >> 32), 1, WAVE);
-  return lane == 0 ? 0.0 : __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+  // the previous lane's inclusive value: row_shr within a row, readlane across rows
+  double prev = dpp_d<DPP_SHR1>(inc);
+  const double e15 = rl_d(inc, 15), e31 = rl_d(inc, 31), e47 = rl_d(inc, 47);
+  if (lane == 16) prev = e15;
+  if (lane == 32) prev = e31;
+  if (lane == 48) prev = e47;
+  return lane == 0 ? 0.0 : prev;
 }
 
 __device__ __forceinline__ uint64_t wave_or_u64(uint64_t v) {
@@ -529,9 +514,9 @@ __device__ uint64_t wave_radix_kth(const uint64_t* key, int n, uint32_t k, uint3
     }
     const uint64_t who = __ballot(dl >= 0);
     const int src = (int)__ffsll((long long)who) - 1;
-    const int dsel = __shfl(dl, src, WAVE);
-    const uint32_t below = (uint32_t)__shfl((int)bl, src, WAVE);
-    const uint32_t cnt = (uint32_t)__shfl((int)cl, src, WAVE);
+    const int dsel = rl_i(dl, src);
+    const uint32_t below = (uint32_t)rl_i((int)bl, src);
+    const uint32_t cnt = (uint32_t)rl_i((int)cl, src);
     wave_sync();
     need -= below;
     prefix = (prefix & ~(255ull << shift)) | ((uint64_t)dsel << shift);

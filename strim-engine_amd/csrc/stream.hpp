@@ -342,17 +342,12 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       // every wave finds the first rung whose cumulative count reaches k (lane owns
       // rungs 2 lane and 2 lane + 1)
       const uint32_t h0 = S.lad[2 * lane], h1 = S.lad[2 * lane + 1];
-      uint32_t cum = h0 + h1;
-#pragma unroll
-      for (int o = 1; o < WAVE; o <<= 1) {
-        const uint32_t u = (uint32_t)__shfl_up((int)cum, o, WAVE);
-        if (lane >= o) cum += u;
-      }
+      const uint32_t cum = wave_incl_scan_u32(h0 + h1);
       const uint64_t reach = __ballot(cum >= (uint32_t)p.top_k);
       if (reach) {
         const int ln = (int)__ffsll((long long)reach) - 1;
-        const uint32_t bef = (uint32_t)__shfl((int)(cum - h0 - h1), ln, WAVE);
-        const uint32_t hl0 = (uint32_t)__shfl((int)h0, ln, WAVE);
+        const uint32_t bef = (uint32_t)rl_i((int)(cum - h0 - h1), ln);
+        const uint32_t hl0 = (uint32_t)rl_i((int)h0, ln);
         const int rstar = 2 * ln + (bef + hl0 >= (uint32_t)p.top_k ? 0 : 1);
         if (rstar < VRUNG - 1) {
           // v > vm - end(rstar) holds the rung; the margin (a few ulps of the values
