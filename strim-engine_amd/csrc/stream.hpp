@@ -155,10 +155,11 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   const bool pen = PEN && p.pen;
   ChunkStat* csp = &a.s.cstat[(int64_t)r * a.s.wmax + c];
 
-  // history ids first: the counts are built while the logits are still in flight
+  // history ids first: the counts are built while the logits are still in flight (the
+  // ids are requested before the row's parameters are known, so no load waits for them)
   int hid[hpt<STPB>()];
   int hl = 0;
-  if (pen) hl = hist_load<STPB>(a, b, hid);
+  if constexpr (PEN) hl = hist_load<STPB>(a, b, hid);
   int i0[SSEG];
 #pragma unroll
   for (int s = 0; s < SSEG; ++s)
