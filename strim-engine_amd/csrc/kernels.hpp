@@ -224,8 +224,9 @@ __device__ __forceinline__ RowParams load_params(const Args& a, int b, int j) {
   p.seed = sp.seed;
   p.position = sp.position + (uint64_t)j;
   p.greedy = !(p.T > 0.0f);
-  const bool active = p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f;
-  p.pen = active && (a.hist != nullptr || (a.verify && j > 0));
+  // (bitwise, not short-circuit: no branch on the parameters here)
+  const bool active = (p.rep != 1.0f) | (p.pres != 0.0f) | (p.freq != 0.0f);
+  p.pen = active & ((a.hist != nullptr) | ((a.verify != 0) & (j > 0)));
   p.cls = row_class(sp, a.V);
   return p;
 }
@@ -366,13 +367,13 @@ __device__ __forceinline__ void process_seg(const A& a, int i0, const RowParams&
 
 // History counts of a span in LDS in two steps, so the history loads can be issued
 // before the caller's logits loads and their latency overlaps them: hist_load requests
-// this thread's first HPT history ids (16 bytes at a time when aligned) and returns the
-// row's history length; hist_count clears the table for [c0, c0 + SPAN), counts every
-// history id inside it (plus the verify draft prefix) and ends with a barrier.
+// this thread's first HPT history ids (16 bytes at a time when aligned); hist_count
+// clears the table for [c0, c0 + SPAN), counts every history id inside it (plus the
+// verify draft prefix) and ends with a barrier.
 template <int NT>
 constexpr int hpt() { return 4096 / NT; }  // history ids each thread preloads
 template <int NT, typename A>
-__device__ __forceinline__ int hist_load(const A& a, int b, int (&ids)[hpt<NT>()]) {
+__device__ __forceinline__ void hist_load(const A& a, int b, int (&ids)[hpt<NT>()]) {
   constexpr int HPT = hpt<NT>();
   const int t = threadIdx.x;
   const int32_t* h = a.hist ? a.hist + (int64_t)b * a.H : nullptr;
@@ -396,12 +397,15 @@ __device__ __forceinline__ int hist_load(const A& a, int b, int (&ids)[hpt<NT>()
 #pragma unroll
     for (int q = 0; q < HPT; ++q) ids[q] = -1;
   }
-  int hl = h ? a.H : 0;
-  if (h && a.hist_len) {
-    hl = a.hist_len[b];
-    hl = hl < 0 ? 0 : (hl > a.H ? a.H : hl);
-  }
-  return hl;
+}
+// The row's history length. Read after the caller's other loads are issued: the
+// compiler moves the uniform value to a scalar register at once, which waits for it.
+template <typename A>
+__device__ __forceinline__ int hist_len(const A& a, int b) {
+  if (!a.hist) return 0;
+  if (!a.hist_len) return a.H;
+  const int raw = a.hist_len[b];
+  return raw < 0 ? 0 : (raw > a.H ? a.H : raw);
 }
 template <int NT, int SPAN, typename A>
 __device__ __forceinline__ void hist_count(const A& a, int b, int j, int c0,

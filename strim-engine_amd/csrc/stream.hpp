@@ -144,22 +144,24 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   constexpr int STPB = stpb<SSEG>();       // threads
   constexpr int NW = STPB / WAVE;          // waves
   __shared__ StreamShared S;
+  // the launch fields used before the first global load, read together: a field first
+  // read inside a branch would be its own scalar-load round trip
+  asm volatile("" ::"s"(a.logits), "s"(a.row_stride), "s"(a.V), "s"(a.verify), "s"(a.k),
+               "s"(a.hist), "s"(a.H), "s"(a.hist_len), "s"(a.mask), "s"(a.mask_stride),
+               "s"(a.s.cstat), "s"(a.s.wmax));
   int r, c;
   map_block(r, c);
   int b, j;
   row_bj(a, r, b, j);
-  const RowParams p = load_params(a, b, j);
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int c0 = c * CHUNK;
   const bool full = VEC && c0 + CHUNK <= a.V;
-  const bool pen = PEN && p.pen;
   ChunkStat* csp = &a.s.cstat[(int64_t)r * a.s.wmax + c];
 
   // history ids first: the counts are built while the logits are still in flight (the
   // ids are requested before the row's parameters are known, so no load waits for them)
   int hid[hpt<STPB>()];
-  int hl = 0;
-  if constexpr (PEN) hl = hist_load<STPB>(a, b, hid);
+  if constexpr (PEN) hist_load<STPB>(a, b, hid);
   int i0[SSEG];
 #pragma unroll
   for (int s = 0; s < SSEG; ++s)
@@ -180,6 +182,11 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   }
   float v[SSEG][EPT];
   load_chunk<DT, VEC, SSEG>(a, r, i0, full, v);
+  // the row's parameters only now: a scalar-load wait for them before this point would
+  // also hold back the loads above
+  const RowParams p = load_params(a, b, j);
+  const bool pen = PEN && p.pen;
+  const int hl = PEN ? hist_len(a, b) : 0;
   if constexpr (MASK) {
     if (!a.mask) {
 #pragma unroll
