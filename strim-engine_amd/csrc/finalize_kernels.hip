@@ -611,6 +611,10 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(FTPB) void k_finalize(Args a) {
   __shared__ FinalShared S;
+  // the launch fields of the prefetch, read together (see k_stream)
+  asm volatile("" ::"s"(a.s.cstat), "s"(a.s.wmax), "s"(a.s.slot), "s"(a.s.rs), "s"(a.W),
+               "s"(a.V), "s"(a.noise), "s"(a.noise_stride), "s"(a.noise_mode), "s"(a.verify),
+               "s"(a.k), "s"(a.drafts));
   const int r = blockIdx.x;
   int b, j;
   row_bj(a, r, b, j);
