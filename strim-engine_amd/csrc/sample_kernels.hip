@@ -23,15 +23,20 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
 // ---------------------------------------------------------------------------------
 // k_collect: general rows
 // ---------------------------------------------------------------------------------
+// First g in [lo, hi] with pred(g), hi + 1 if none, for a predicate monotone in g
+// (false ... false true ... true). One wave: lane l tests bins l, l + 64, l + 128.
+static_assert(NGB <= 3 * WAVE, "three bins per lane");
 template <typename F>
 __device__ __forceinline__ int first_true(int lo, int hi, F pred) {
-  int L = lo, H = hi + 1;
-  while (L < H) {
-    const int mid = (L + H) >> 1;
-    if (pred(mid)) H = mid;
-    else L = mid + 1;
+  const int lane = threadIdx.x & (WAVE - 1);
+  int res = hi + 1;
+#pragma unroll
+  for (int k = 2; k >= 0; --k) {
+    const int g = lane + k * WAVE;
+    const uint64_t bal = __ballot(g >= lo && g <= hi && g < NGB && pred(g));
+    if (bal) res = k * WAVE + (int)__ffsll((long long)bal) - 1;
   }
-  return L;
+  return res;
 }
 
 // Row statistics merged from the chunk statistics, identically in every workgroup.
@@ -75,12 +80,15 @@ __device__ __forceinline__ RowStats merge_chunks(const Args& a, int r, float* sv
 }
 
 // Conservative bin bounds of a general row from the coarse chunk histograms
-// (thread 0; the same arithmetic in every workgroup of the row gives the same result).
+// (one wave, every lane computing the same scalars; the same arithmetic in every
+// workgroup of the row gives the same result).
 // cU/cL: cumulative fixed-point mass with each chunk bin placed at its earliest /
 // latest possible global bin; kU/kL: the same for counts.
 __device__ void compute_bounds(const Args& a, int r, const RowParams& p, float m, uint32_t N,
                                const unsigned long long* cU, const unsigned long long* cL,
-                               const uint32_t* kU, const uint32_t* kL, Bounds& bd) {
+                               const uint32_t* kU, const uint32_t* kL, Bounds& out) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  Bounds bd;  // built in registers (uniform), stored by lane 0
   const double inv = 1.0 / FIX_SCALE, EPS = 1e-5;
   const double SLACK = (double)(a.W * NCB + 16) * 4.0 * inv;
   auto MU = [&](int g) { return g < 0 ? 0.0 : (double)cU[g] * inv * (1.0 + EPS) + SLACK; };
@@ -150,38 +158,60 @@ __device__ void compute_bounds(const Args& a, int r, const RowParams& p, float m
       bd.rng[2][1] = dhi;
     }
     // upper bound of the tokens in the collected bins: per contiguous run [lo, hi],
-    // kU[hi] - kL[lo - 1]
-    uint32_t total = 0;
-    int g = 0;
-    while (g < NGB) {
-      if (!in_rng(bd, g)) { ++g; continue; }
-      const int lo = g;
-      while (g + 1 < NGB && in_rng(bd, g + 1)) ++g;
-      const uint32_t below = lo > 0 ? kL[lo - 1] : 0u;
-      total += kU[g] > below ? kU[g] - below : 0u;
-      ++g;
+    // kU[hi] - kL[lo - 1] (never negative: kU >= kL bin by bin, and both are cumulative)
+    uint32_t part = 0u;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int g = lane + k * WAVE;
+      if (g >= NGB || !in_rng(bd, g)) continue;
+      if (g + 1 >= NGB || !in_rng(bd, g + 1)) part += kU[g];
+      if (g > 0 && !in_rng(bd, g - 1)) part -= kL[g - 1];
     }
+    const uint32_t total = (uint32_t)wave_sum((int)part);
     if (total > (uint32_t)CAP) mode = MODE_NONE;
   }
   // non-collected intervals, split where the kept / pre-kept classification changes
-  int ns = 0;
+  // (a new interval starts after a collected bin and at s and s1); more than NSEG
+  // intervals leave the row to the exact resolution
   for (int q = 0; q < NSEG; ++q) { bd.seg_lo[q] = 1; bd.seg_hi[q] = 0; }
-  int g = 0;
-  while (g < NGB && mode != MODE_NONE) {
-    if (in_rng(bd, g)) { ++g; continue; }
-    const int lo = g;
-    while (g + 1 < NGB && !in_rng(bd, g + 1) && g + 1 != s && g + 1 != s1) ++g;
-    if (ns == NSEG) { mode = MODE_NONE; break; }
-    bd.seg_lo[ns] = lo;
-    bd.seg_hi[ns] = g;
-    ++ns;
-    ++g;
+  if (mode != MODE_NONE) {
+    uint64_t stm[3], enm[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int g = lane + k * WAVE;
+      const bool out_g = g < NGB && !in_rng(bd, g);
+      stm[k] = __ballot(out_g && (g == 0 || in_rng(bd, g - 1) || g == s || g == s1));
+      enm[k] = __ballot(out_g && (g == NGB - 1 || in_rng(bd, g + 1) || g + 1 == s || g + 1 == s1));
+    }
+    // the q-th start and the q-th end delimit interval q (they alternate bin by bin)
+    int q = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      uint64_t ms = stm[k];
+      while (ms) {
+        if (q < NSEG) bd.seg_lo[q] = k * WAVE + (int)__ffsll((long long)ms) - 1;
+        ms &= ms - 1ull;
+        ++q;
+      }
+    }
+    if (q > NSEG) mode = MODE_NONE;
+    q = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      uint64_t me = enm[k];
+      while (me) {
+        if (q < NSEG) bd.seg_hi[q] = k * WAVE + (int)__ffsll((long long)me) - 1;
+        me &= me - 1ull;
+        ++q;
+      }
+    }
   }
   bd.mode = mode;
   bd.s = s;
   bd.e = e;
   bd.s1 = s1;
   bd.e1 = e1;
+  if (lane == 0) out = bd;
 }
 
 __global__ __launch_bounds__(TPB) void k_collect(Args a) {
@@ -218,31 +248,79 @@ __global__ __launch_bounds__(TPB) void k_collect(Args a) {
     s_U[g] = 0ull; s_L[g] = 0ull; s_kU[g] = 0u; s_kL[g] = 0u;
   }
   __syncthreads();
-  for (int e = t; e < a.W * NCB; e += TPB) {
-    const int cc = e / NCB, bb = e - cc * NCB;
-    const int64_t o = ((int64_t)r * a.s.wmax + cc) * NCB + bb;
-    const uint32_t cn = a.s.chc[o];
-    if (!cn) continue;
-    const float mw = a.s.cstat[(int64_t)r * a.s.wmax + cc].m;
-    const double dlt = (double)m - (double)mw;
-    const double lo = (dlt + 0.5 * bb) * (1.0 - 2e-6) * CB_SCALE;
-    const double hi = bb == NCB - 1 ? 1e300 : (dlt + 0.5 * (bb + 1)) * (1.0 + 2e-6) * CB_SCALE;
-    const int glo = lo < (double)(NGB - 1) ? max(0, (int)floor(lo)) : NGB - 1;
-    const int ghi = hi < (double)(NGB - 1) ? max(0, (int)floor(hi)) : NGB - 1;
-    const double ms = (double)a.s.chm[o] * exp(-dlt);
-    atomicAdd(&s_U[glo], (unsigned long long)(ms + 1.0));
-    atomicAdd(&s_L[ghi], (unsigned long long)ms);
-    atomicAdd(&s_kU[glo], cn);
-    atomicAdd(&s_kL[ghi], cn);
+  // (batches of loads from clamped indices with no branch between them)
+  constexpr int BB = 8;
+  const int nbin = a.W * NCB;
+  for (int e0 = t; e0 < nbin; e0 += BB * TPB) {
+    uint32_t cn[BB];
+    unsigned long long hm[BB];
+    float mw[BB];
+#pragma unroll
+    for (int q = 0; q < BB; ++q) {
+      const int e = e0 + q * TPB < nbin ? e0 + q * TPB : 0;
+      const int cc = e / NCB;
+      const int64_t o = ((int64_t)r * a.s.wmax + cc) * NCB + (e - cc * NCB);
+      cn[q] = a.s.chc[o];
+      hm[q] = a.s.chm[o];
+      mw[q] = a.s.cstat[(int64_t)r * a.s.wmax + cc].m;
+    }
+#pragma unroll
+    for (int q = 0; q < BB; ++q) {
+      const int e = e0 + q * TPB;
+      if (e >= nbin || !cn[q]) continue;
+      const int cc = e / NCB, bb = e - cc * NCB;
+      const double dlt = (double)m - (double)mw[q];
+      const double lo = (dlt + 0.5 * bb) * (1.0 - 2e-6) * CB_SCALE;
+      const double hi = bb == NCB - 1 ? 1e300 : (dlt + 0.5 * (bb + 1)) * (1.0 + 2e-6) * CB_SCALE;
+      const int glo = lo < (double)(NGB - 1) ? max(0, (int)floor(lo)) : NGB - 1;
+      const int ghi = hi < (double)(NGB - 1) ? max(0, (int)floor(hi)) : NGB - 1;
+      const double ms = (double)hm[q] * exp(-dlt);
+      atomicAdd(&s_U[glo], (unsigned long long)(ms + 1.0));
+      atomicAdd(&s_L[ghi], (unsigned long long)ms);
+      atomicAdd(&s_kU[glo], cn[q]);
+      atomicAdd(&s_kL[ghi], cn[q]);
+    }
   }
   if (p.pen) build_counts(a, b, j, c0, s_cnt);
   else __syncthreads();
-  if (t == 0) {
-    for (int g = 1; g < NGB; ++g) {
-      s_U[g] += s_U[g - 1]; s_L[g] += s_L[g - 1];
-      s_kU[g] += s_kU[g - 1]; s_kL[g] += s_kL[g - 1];
+  // inclusive prefixes over the global bins, one array per wave: a lane owns bins
+  // 3 lane .. 3 lane + 2
+  static_assert(NGB <= 3 * WAVE && TPB / WAVE >= 4, "prefix layout");
+  if (w < 4) {
+    const int g0 = 3 * lane;
+    if (w < 2) {
+      unsigned long long* arr = w == 0 ? s_U : s_L;
+      unsigned long long v3[3], own = 0ull;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        v3[q] = g0 + q < NGB ? arr[g0 + q] : 0ull;
+        own += v3[q];
+      }
+      unsigned long long run = wave_incl_scan_u64(own) - own;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        run += v3[q];
+        if (g0 + q < NGB) arr[g0 + q] = run;
+      }
+    } else {
+      uint32_t* arr = w == 2 ? s_kU : s_kL;
+      uint32_t v3[3], own = 0u;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        v3[q] = g0 + q < NGB ? arr[g0 + q] : 0u;
+        own += v3[q];
+      }
+      uint32_t run = wave_incl_scan_u32(own) - own;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        run += v3[q];
+        if (g0 + q < NGB) arr[g0 + q] = run;
+      }
     }
-    compute_bounds(a, r, p, m, (uint32_t)st.n, s_U, s_L, s_kU, s_kL, s_bd);
+  }
+  __syncthreads();
+  if (w == 0) compute_bounds(a, r, p, m, (uint32_t)st.n, s_U, s_L, s_kU, s_kL, s_bd);
+  if (t == 0) {
     if (c == 0) a.s.rs[r].bd = s_bd;
   }
   __syncthreads();
@@ -495,18 +573,36 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   }
   if (t == 0) s_kth = -INFINITY;
   if (n <= FIN_T) {
-    // rank by counting: one key per thread, broadcast reads of every key (keys are
-    // unique, so the ranks are a permutation of 0..n-1)
-    if (t < n) s_key[t] = kk[0];
+    // one key per thread: every wave ranks its 64 keys among themselves and writes them
+    // as a sorted run; a key's rank is its rank in its run plus its lower bound in each
+    // other run (keys are unique, so the ranks are a permutation of 0..n-1). Pads sort
+    // after every key (a finite l has key bits below 0xFF800000 << 32).
+    const int w = t / WAVE, lane = t & (WAVE - 1);
+    const uint64_t k0 = t < n ? kk[0] : (0xFFFFFFFF00000000ull | (uint32_t)t);
+    uint64_t* run = s_key + FIN_T;  // FIN_T sorted keys, 64 per run
+    s_key[t] = k0;
+    wave_sync();
+    uint32_t rw = 0;
+#pragma unroll 8
+    for (int q = 0; q < WAVE; q += 2) {
+      const ulonglong2 xy = *(const ulonglong2*)&s_key[w * WAVE + q];
+      rw += (uint32_t)(xy.x < k0) + (uint32_t)(xy.y < k0);
+    }
+    run[w * WAVE + rw] = k0;
     __syncthreads();
-    const uint64_t k0 = kk[0];
-    uint32_t rank = 0;
-    int jj = 0;
-    for (; jj + 4 <= n; jj += 4)
-      rank += (uint32_t)(s_key[jj] < k0) + (uint32_t)(s_key[jj + 1] < k0) +
-              (uint32_t)(s_key[jj + 2] < k0) + (uint32_t)(s_key[jj + 3] < k0);
-    for (; jj < n; ++jj) rank += (uint32_t)(s_key[jj] < k0);
-    __syncthreads();
+    uint32_t rank = rw;
+    const int nrun = (n + WAVE - 1) / WAVE;
+#pragma unroll
+    for (int q = 0; q < FIN_T / WAVE; ++q) {
+      if (q >= nrun || q == w) continue;
+      const uint64_t* rq = run + q * WAVE;
+      uint32_t pos = 0;
+#pragma unroll
+      for (int st = WAVE / 2; st >= 1; st >>= 1)
+        if (rq[pos + st - 1] < k0) pos += st;
+      pos += rq[pos] < k0 ? 1u : 0u;
+      rank += pos;
+    }
     if (t < n) s_key[rank] = k0;
     __syncthreads();
   } else {
