@@ -405,46 +405,61 @@ __global__ __launch_bounds__(TPB) void k_collect(Args a) {
 // ---------------------------------------------------------------------------------
 // k_final
 // ---------------------------------------------------------------------------------
-// Bitonic sort of the first n2 (power of two, >= 64) keys. Keys live in registers,
-// striped (element e = q * FIN_T + t); strides >= 64 exchange through LDS, smaller ones
-// through wave shuffles. Register arrays are only indexed by unrolled constants.
-__device__ void bitonic_sort(uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key) {
-  const int t = threadIdx.x;
-  for (int size = 2; size <= n2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= WAVE) {
-#pragma unroll
-        for (int q = 0; q < FIN_Q; ++q)
-          if (q * FIN_T < n2) s_key[q * FIN_T + t] = k[q];
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < FIN_Q; ++q) {
-          if (q * FIN_T >= n2) continue;
-          const int e = q * FIN_T + t;
-          const int pe = e ^ stride;
-          const uint64_t o = s_key[pe];
-          const bool asc = (e & size) == 0;
-          const bool lower = e < pe;
-          k[q] = (lower == asc) ? (k[q] < o ? k[q] : o) : (k[q] > o ? k[q] : o);
-        }
-        __syncthreads();
-      } else {
-#pragma unroll
-        for (int q = 0; q < FIN_Q; ++q) {
-          if (q * FIN_T >= n2) continue;
-          const int e = q * FIN_T + t;
-          const uint64_t o = shfl_xor_u64(k[q], stride);
-          const bool asc = (e & size) == 0;
-          const bool lower = (e & stride) == 0;
-          k[q] = (lower == asc) ? (k[q] < o ? k[q] : o) : (k[q] > o ? k[q] : o);
-        }
-      }
-    }
-  }
+// Ascending sort of the n2 (power of two, 64 <= n2 <= CAP) unique keys k[q] (element
+// q * FIN_T + t) into s_key, with s_tmp (n2 entries) as the second buffer. Runs of 64
+// are sorted by rank within the run, then merged pairwise: a key's place in the merged
+// run is its place in its own run plus its lower bound in the partner run (keys are
+// unique, so every round is a permutation).
+__device__ void merge_sort(const uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key,
+                           uint64_t* s_tmp) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1);
 #pragma unroll
   for (int q = 0; q < FIN_Q; ++q)
     if (q * FIN_T < n2) s_key[q * FIN_T + t] = k[q];
   __syncthreads();
+  uint64_t* A = s_key;
+  uint64_t* B = s_tmp;
+  // runs of 64: the wave's 64 consecutive positions of each stripe q
+#pragma unroll
+  for (int q = 0; q < FIN_Q; ++q) {
+    if (q * FIN_T >= n2) continue;
+    const int base = q * FIN_T + (t - lane);
+    const uint64_t k0 = A[base + lane];
+    uint32_t rk = 0;
+#pragma unroll 8
+    for (int i = 0; i < WAVE; i += 2) {
+      const ulonglong2 xy = *(const ulonglong2*)&A[base + i];
+      rk += (uint32_t)(xy.x < k0) + (uint32_t)(xy.y < k0);
+    }
+    B[base + rk] = k0;
+  }
+  __syncthreads();
+  {
+    uint64_t* T = A; A = B; B = T;
+  }
+  for (int R = WAVE; R < n2; R <<= 1) {
+#pragma unroll
+    for (int q = 0; q < FIN_Q; ++q) {
+      const int idx = q * FIN_T + t;
+      if (idx >= n2) continue;
+      const uint64_t k0 = A[idx];
+      const int ri = idx / R, pi = idx & (R - 1);
+      const uint64_t* P = A + (ri ^ 1) * R;
+      int pos = 0;
+      for (int st = R >> 1; st >= 1; st >>= 1)
+        if (P[pos + st - 1] < k0) pos += st;
+      pos += P[pos] < k0 ? 1 : 0;
+      B[(ri & ~1) * R + pi + pos] = k0;
+    }
+    __syncthreads();
+    uint64_t* T = A; A = B; B = T;
+  }
+  if (A != s_key) {
+#pragma unroll
+    for (int q = 0; q < FIN_Q; ++q)
+      if (q * FIN_T < n2) s_key[q * FIN_T + t] = A[q * FIN_T + t];
+    __syncthreads();
+  }
 }
 
 __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
@@ -606,7 +621,13 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     if (t < n) s_key[rank] = k0;
     __syncthreads();
   } else {
-    bitonic_sort(kk, n2, s_key);
+    // pads (after every key, see above) fill the power of two
+#pragma unroll
+    for (int q = 0; q < FIN_Q; ++q) {
+      const int idx = q * FIN_T + t;
+      if (idx >= n) kk[q] = 0xFFFFFFFF00000000ull | (uint32_t)idx;
+    }
+    merge_sort(kk, n2, s_key, (uint64_t*)s_w);
   }
 
   // ---- per-position data lives in LDS: keys in s_key, fp64 masses in s_w ----------
