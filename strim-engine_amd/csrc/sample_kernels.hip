@@ -477,6 +477,8 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   __shared__ double s_segm[NSEG];
   __shared__ uint32_t s_segc[NSEG];
   __shared__ int s_segk[NSEG];  // 2 = kept, 1 = pre-kept only, 0 = neither
+  __shared__ uint32_t s_bcb[NGB];   // per global bin g: seg_before(g), tabulated
+  __shared__ double s_bpb[NGB], s_bkb[NGB];
   __shared__ Bounds s_bd;
   __shared__ uint64_t s_u2[2 * FIN_T / WAVE];
   __shared__ XState s_x;
@@ -634,11 +636,11 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   const bool minp = p.min_p > 0.0f;
   const double lmp = p.lmp;
   const bool keep_ties = (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) != 0;
-  // non-collected tokens before global coarse bin g: count, pre-kept mass, kept mass
-  auto seg_before = [&](int g, uint32_t& cb, double& pb, double& kb) {
-    cb = 0u;
-    pb = 0.0;
-    kb = 0.0;
+  // non-collected tokens before global coarse bin g: count, pre-kept mass, kept mass,
+  // summed in interval order once per bin
+  for (int g = t; g < NGB; g += FIN_T) {
+    uint32_t cb = 0u;
+    double pb = 0.0, kb = 0.0;
 #pragma unroll
     for (int s = 0; s < NSEG; ++s)
       if (s_bd.seg_lo[s] <= s_bd.seg_hi[s] && s_bd.seg_hi[s] < g) {
@@ -646,6 +648,15 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
         if (s_segk[s] >= 1) pb += s_segm[s];
         if (s_segk[s] == 2) kb += s_segm[s];
       }
+    s_bcb[g] = cb;
+    s_bpb[g] = pb;
+    s_bkb[g] = kb;
+  }
+  __syncthreads();
+  auto seg_before = [&](int g, uint32_t& cb, double& pb, double& kb) {
+    cb = s_bcb[g];
+    pb = s_bpb[g];
+    kb = s_bkb[g];
   };
 #pragma unroll
   for (int q = 0; q < FIN_Q; ++q) {
