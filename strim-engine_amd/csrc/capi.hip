@@ -127,8 +127,9 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
     if (cls == CLS_GENERAL && !(a.noise_mode == STRIM_NOISE_GUMBEL && nofilter(a.p[i], a.V)))
       need_collect = true;
   }
-  // k_final decides the general rows (k_finalize leaves them pending)
-  need_final = need_collect;
+  // k_final decides the general rows (k_finalize leaves them pending) and the general-q
+  // verify rows
+  need_final = need_collect || (a.verify && a.dlog != nullptr);
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
   hipError_t e = hipSuccess;
   auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };
@@ -232,7 +233,7 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   const size_t o_nc = carve(R * sizeof(uint32_t));
   const size_t words = ((size_t)max_vocab + 31) / 32;
   const size_t o_dbits = carve(words * sizeof(uint32_t));
-  const size_t o_dpre = carve(words * sizeof(int32_t));
+  const size_t o_vq = carve(R * wmax * CHUNK * sizeof(float));
   const size_t o_qst = carve(R * sizeof(QStat));
   const size_t o_qflag = carve(sizeof(int32_t));
   ctx->bytes = off;
@@ -257,7 +258,7 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   ctx->s.cand = (Cand*)(b + o_cand);
   ctx->s.ncand = (uint32_t*)(b + o_nc);
   ctx->s.dbits = (uint32_t*)(b + o_dbits);
-  ctx->s.dpre = (int32_t*)(b + o_dpre);
+  ctx->s.vq = (float*)(b + o_vq);
   ctx->s.qst = (QStat*)(b + o_qst);
   ctx->s.qflag = (int32_t*)(b + o_qflag);
   ctx->s.wmax = wmax;
@@ -392,8 +393,8 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       hipError_t e = hipSuccess;
       if (a.dlog) {
         // draft distributions (one workgroup per draft row) and, with the first group,
-        // the draft-vocab bitmap and rank prefix of the table
-        const int nwb = g0 == 0 ? (int)((((V + 31) / 32) + 255) / 256) : 0;
+        // the draft-vocab bitmap (one thread per table entry)
+        const int nwb = g0 == 0 ? (int)((Vd + 255) / 256) : 0;
         timed(ctx, KID_QPREP, [&](hipEvent_t e0, hipEvent_t e1) {
           e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k + nwb)), dim3(256), a, st,
                           e0, e1);

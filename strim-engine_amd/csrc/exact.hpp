@@ -39,24 +39,19 @@ struct XUni {
 };
 
 // The draft distribution q of a general-q verify row: softmax(draft logits / T) over the
-// draft vocabulary, whose ids are the ascending table behind dbits / dpre.
+// draft vocabulary, whose ids are the table's (membership bitmap dbits; vq holds
+// v = draft_logit / T at each member id).
 struct XQ {
-  const uint32_t* dbits;  // membership bitmap of the table's ids
-  const int32_t* dpre;    // table entries below each 32-token word
-  const void* dl;         // the row's draft logits [Vd]
-  int32_t dtype;
-  float T, mq;
+  const uint32_t* dbits;
+  const float* vq;
+  float mq;
   double Z;
 };
-// q(id): exp(v - mq) / Z with v = draft_logit / T (fp32), 0 outside the table.
+// q(id): exp(v - mq) / Z, 0 outside the table.
 __device__ __forceinline__ double xq_prob(const XQ& q, int id) {
   const uint32_t bits = q.dbits[id >> 5];
-  const uint32_t bit = 1u << (id & 31);
-  if (!(bits & bit)) return 0.0;
-  const int a = q.dpre[id >> 5] + __popc(bits & (bit - 1u));
-  const float x = q.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)q.dl)[a])
-                                              : ((const float*)q.dl)[a];
-  return exp((double)(x / q.T) - (double)q.mq) / q.Z;
+  if (!((bits >> (id & 31)) & 1u)) return 0.0;
+  return exp((double)q.vq[id] - (double)q.mq) / q.Z;
 }
 
 // The fields of Args the streaming passes read (the exact path is one out-of-line call,
@@ -86,13 +81,18 @@ __device__ __forceinline__ uint64_t x_weight(float l, float m) {
 }
 // Weight of a universe token: exp(l - m) in fixed point, or, for a residual universe,
 // max(0, W - round(q * rS)): the residual (p - q)^+ in units of the kept mass rS.
-__device__ __forceinline__ uint64_t x_wt(const XArgs& a, const XUni& u, float l, int id) {
+__device__ __forceinline__ uint64_t x_wt_q(const XUni& u, float l, double q) {
   const uint64_t W = x_weight(l, u.m);
-  if (u.rS == 0ull) return W;
-  const double q = xq_prob(a.q, id);
-  if (q == 0.0) return W;
+  if (u.rS == 0ull || q == 0.0) return W;
   const uint64_t qS = (uint64_t)__double2ull_rn(q * (double)u.rS);
   return W > qS ? W - qS : 0ull;
+}
+__device__ __forceinline__ uint64_t x_wt(const XArgs& a, const XUni& u, float l, int id) {
+  return x_wt_q(u, l, u.rS == 0ull ? 0.0 : xq_prob(a.q, id));
+}
+// q from a streamed draft value (-inf: not in the table)
+__device__ __forceinline__ double xq_of(const XQ& q, float v) {
+  return v > -INFINITY ? exp((double)v - (double)q.mq) / q.Z : 0.0;
 }
 // Level-0 digit: floor(64 (m - l)), tail at XB - 1; monotone in the order.
 __device__ __forceinline__ int x_dbin(float l, float m) {
@@ -115,20 +115,138 @@ __device__ __forceinline__ uint32_t x_first_fkey(uint32_t lo, uint32_t hi, F pre
   return (uint32_t)L;
 }
 
-// One streaming pass over the row: fn(i0, l) for every thread and window.
+// One streaming pass over the row: fn(i0, l, qv) for every thread and window, with qv
+// the draft values v of a general-q row's tokens (-inf outside the table; all -inf for
+// other rows). Aligned rows without penalties keep XPD windows of loads in flight; the
+// others load each window when they reach it (the history counts are rebuilt per
+// window).
+constexpr int XPD = 4;
+template <int NT, bool BF16, bool Q, typename F>
+__device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, const RowParams& p, F&& fn) {
+  constexpr int WIN = NT * EPT;
+  const int t = threadIdx.x;
+  const int64_t base = (int64_t)r * a.row_stride;
+  const int nwin = (a.V + WIN - 1) / WIN;
+  const uint8_t* mrow = a.mask ? (const uint8_t*)(a.mask + (int64_t)r * a.mask_stride)
+                               : (const uint8_t*)a.logits;
+  struct Slot {
+    uint4 x0, x1;
+    uint32_t mb, qb;
+    float4 q0, q1;
+  };
+  Slot sl[XPD];
+  // every load of a window from a clamped index, no branch between them; a segment that
+  // ends past the row end (V not a multiple of 8) is left to the tail step below
+  auto issue = [&](Slot& sd, int w) {
+    const int i0 = w * WIN + t * EPT;
+    const int ii = i0 + EPT <= a.V ? i0 : 0;
+    if constexpr (BF16) {
+      sd.x0 = *(const uint4*)((const uint16_t*)a.logits + base + ii);
+    } else {
+      sd.x0 = *(const uint4*)((const float*)a.logits + base + ii);
+      sd.x1 = *(const uint4*)((const float*)a.logits + base + ii + 4);
+    }
+    sd.mb = mrow[a.mask ? (ii >> 3) : 0];
+    if constexpr (Q) {
+      sd.qb = a.q.dbits[ii >> 5];
+      sd.q0 = *(const float4*)(a.q.vq + ii);
+      sd.q1 = *(const float4*)(a.q.vq + ii + 4);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < XPD; ++d) issue(sl[d], d);
+  for (int w = 0; w < nwin; w += XPD) {
+#pragma unroll
+    for (int d = 0; d < XPD; ++d) {
+      if (w + d < nwin) {
+        const int i0 = (w + d) * WIN + t * EPT;
+        const Slot& sd = sl[d];
+        float x[EPT];
+        if constexpr (BF16) {
+          const uint32_t wv[4] = {sd.x0.x, sd.x0.y, sd.x0.z, sd.x0.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[2 * e] = __uint_as_float(wv[e] << 16);
+            x[2 * e + 1] = __uint_as_float(wv[e] & 0xFFFF0000u);
+          }
+        } else {
+          const uint32_t wv[8] = {sd.x0.x, sd.x0.y, sd.x0.z, sd.x0.w,
+                                  sd.x1.x, sd.x1.y, sd.x1.z, sd.x1.w};
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) x[e] = __uint_as_float(wv[e]);
+        }
+        const uint32_t bits = a.mask ? ((uint32_t)sd.mb & 0xFFu) : 0xFFu;
+        float l[EPT], qv[EPT];
+        const float qa[EPT] = {sd.q0.x, sd.q0.y, sd.q0.z, sd.q0.w,
+                               sd.q1.x, sd.q1.y, sd.q1.z, sd.q1.w};
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const bool ok = (i0 + EPT <= a.V) && ((bits >> e) & 1u);
+          l[e] = ok ? (p.greedy ? x[e] : x[e] / p.T) : -INFINITY;
+          qv[e] = -INFINITY;
+          if constexpr (Q) {
+            const int id = i0 + e;
+            if ((sd.qb >> (id & 31)) & 1u) qv[e] = qa[e];
+          }
+        }
+        fn(i0, l, qv);
+      }
+      issue(sl[d], w + d + XPD);
+    }
+  }
+  // tail: the partial last segment, by its owner with element loads (all -inf elsewhere)
+  if (a.V % EPT) {
+    const int iP = a.V & ~(EPT - 1);
+    const bool own = t == (iP % WIN) / EPT;
+    const uint32_t bits = (own && a.mask) ? (uint32_t)mrow[iP >> 3] : 0xFFu;
+    float l[EPT], qv[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int id = iP + e;
+      const bool ok = own && id < a.V && ((bits >> e) & 1u);
+      const int ic = ok ? id : 0;
+      const float x = BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[base + ic])
+                           : ((const float*)a.logits)[base + ic];
+      l[e] = ok ? (p.greedy ? x : x / p.T) : -INFINITY;
+      qv[e] = -INFINITY;
+      if constexpr (Q) {
+        if (ok && ((a.q.dbits[id >> 5] >> (id & 31)) & 1u)) qv[e] = a.q.vq[id];
+      }
+    }
+    fn(iP, l, qv);
+  }
+}
 template <int NT, typename F>
 __device__ __forceinline__ void x_pass(const XArgs& a, int r, int b, int j, const RowParams& p,
                                        uint32_t* s_cnt, F&& fn) {
+  if (a.vec_ok && !p.pen) {
+    if (a.dtype == STRIM_DTYPE_BF16) {
+      if (a.has_q) x_pass_pipe<NT, true, true>(a, r, p, fn);
+      else x_pass_pipe<NT, true, false>(a, r, p, fn);
+    } else {
+      if (a.has_q) x_pass_pipe<NT, false, true>(a, r, p, fn);
+      else x_pass_pipe<NT, false, false>(a, r, p, fn);
+    }
+    return;
+  }
   const int t = threadIdx.x;
   for (int w0 = 0; w0 < a.V; w0 += NT * EPT) {
     const int i0 = w0 + t * EPT;
     float x[EPT];
     load_tokens(a, r, i0, x);
     if (p.pen) build_counts_span<NT, NT * EPT>(a, b, j, w0, s_cnt);
-    float l[EPT];
+    float l[EPT], qv[EPT];
     bool nf = false;
     process_tokens(a, r, i0, p, s_cnt + t * EPT, x, l, nf);
-    fn(i0, l);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      qv[e] = -INFINITY;
+      if (a.has_q && i0 + e < a.V) {
+        const int id = i0 + e;
+        if ((a.q.dbits[id >> 5] >> (id & 31)) & 1u) qv[e] = a.q.vq[id];
+      }
+    }
+    fn(i0, l, qv);
     if (p.pen) __syncthreads();  // the next window rebuilds the counts
   }
 }
@@ -159,7 +277,7 @@ __device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, cons
   int cur = -1;
   uint32_t ac = 0u;
   uint64_t am = 0ull;
-  x_pass<NT>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT]) {
+  x_pass<NT>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT], const float (&qv)[EPT]) {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       if (!x_in(u, l[e], i0 + e)) continue;
@@ -175,7 +293,7 @@ __device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, cons
         am = 0ull;
       }
       ac += 1u;
-      am += x_wt(a, u, l[e], i0 + e);
+      am += x_wt_q(u, l[e], u.rS == 0ull ? 0.0 : xq_of(a.q, qv[e]));
     }
   });
   if (cur >= 0) {
@@ -194,7 +312,7 @@ __device__ __forceinline__ int x_collect(const XArgs& a, int r, int b, int j, co
   const int lane = threadIdx.x & (WAVE - 1);
   if (threadIdx.x == 0) s_x.ncol = 0u;
   __syncthreads();
-  x_pass<NT>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT]) {
+  x_pass<NT>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT], const float (&)[EPT]) {
     uint32_t sel = 0u;
     int c = 0;
 #pragma unroll
@@ -453,13 +571,12 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
     double bsc = -INFINITY;
     uint64_t btk = ~0ull;
     int bid = -1;
-    auto take = [&](float l, int id, int64_t nidx, uint64_t tk) {
+    auto take = [&](float l, int id, int64_t nidx, uint64_t tk, double q) {
       const float uq = a.noise ? a.noise[(int64_t)r * a.noise_stride + nidx]
                                : philox_uniform(pkey, (uint64_t)nidx);
       double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
       if (resid) {
         // residual score: log(p - q) where q > 0, excluded where p <= q
-        const double q = xq_prob(a.q, id);
         if (q != 0.0) {
           const double rr = exp(base) - q;
           if (!(rr > 0.0)) return;
@@ -490,7 +607,7 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
         for (int pos = threadIdx.x; pos < n; pos += NT) {
           const uint64_t key = xs.key[pos];
           take(fkey_desc_inv((uint32_t)(key >> 32)), (int)(uint32_t)key,
-               (int64_t)below + pos, key);
+               (int64_t)below + pos, key, resid ? xq_prob(a.q, (int)(uint32_t)key) : 0.0);
         }
         __syncthreads();
         if (n <= 0) break;
@@ -498,11 +615,12 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
         ub.lo = uc.bound + 1ull;
       }
     } else {
-      x_pass<NT>(a, r, b, j, p, xs.cnt, [&](int i0, const float (&l)[EPT]) {
+      x_pass<NT>(a, r, b, j, p, xs.cnt, [&](int i0, const float (&l)[EPT], const float (&qv)[EPT]) {
 #pragma unroll
         for (int e = 0; e < EPT; ++e)
           if (x_in(ud, l[e], i0 + e))
-            take(l[e], i0 + e, i0 + e, cand_sorted ? ckey(l[e], i0 + e) : (uint64_t)(i0 + e));
+            take(l[e], i0 + e, i0 + e, cand_sorted ? ckey(l[e], i0 + e) : (uint64_t)(i0 + e),
+                 resid ? xq_of(a.q, qv[e]) : 0.0);
       });
     }
     block_argmax_score<NT>(bsc, btk, bid, xs.dred, xs.ured, xs.ired, &s_x.token);

@@ -97,18 +97,7 @@ __device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int 
   xa.drafts = a.drafts;
   xa.noise = a.noise;
   xa.noise_stride = a.noise_stride;
-  xa.has_q = (a.dlog != nullptr && vdr) ? 1 : 0;
-  if (xa.has_q) {
-    const int qr = b * a.k + j;
-    const QStat qs = a.s.qst[qr];
-    xa.q.dbits = a.s.dbits;
-    xa.q.dpre = a.s.dpre;
-    xa.q.dl = (const char*)a.dlog + (size_t)qr * (size_t)a.Vd * (a.dtype == STRIM_DTYPE_BF16 ? 2 : 4);
-    xa.q.dtype = a.dtype;
-    xa.q.T = p.T;
-    xa.q.mq = qs.mq;
-    xa.q.Z = qs.Z;
-  }
+  xa.has_q = 0;  // general-q rows are decided by k_final
   __syncthreads();
   const XOut xo = exact_row<FTPB>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
   finish_row(a, r, xo.status, xo.token, xo.accept, xo.sig, m, xo.last_key, PH_DONE);
@@ -260,12 +249,13 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   }
   if (vdr && a.dlog) {
     // general-q draft row: the draft must be in a valid table; the residual draw and the
-    // p / q accept run on the exact streaming resolution
+    // p / q accept run on k_final's exact streaming resolution
     if (*a.s.qflag == 0 || a.s.qst[b * a.k + j].td < 0) {
       finish_row(a, r, STRIM_EINVAL, -1, 0, 0.0, m, 0ull, PH_DONE);
       return done;
     }
-    return ExactReq{1, m, arg, draft, l_draft};
+    finish_row(a, r, STRIM_OK, -1, 0, 0.0, m, 0ull, PH_EXACT);
+    return done;
   }
   const bool topk = p.top_k > 0 && p.top_k < V;
   const bool topp = p.top_p < 1.0f;

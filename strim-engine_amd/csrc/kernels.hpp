@@ -39,8 +39,9 @@ enum RowClass : int32_t { CLS_GREEDY = 0, CLS_FAST = 1, CLS_GENERAL = 2, CLS_INV
 
 // How a row's candidates are resolved (set by k_collect for general rows).
 // Set by k_finalize: DONE rows are decided; PENDING rows (general path) go to
-// k_collect + k_final.
-enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1 };
+// k_collect + k_final; EXACT rows (general-q verify rows) go to k_final's exact streaming
+// resolution, whose workgroups are four times wider than k_finalize's.
+enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1, PH_EXACT = 2 };
 
 enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
 
@@ -116,7 +117,8 @@ struct Scratch {
   Cand* cand;                     // [rows][CAP]
   uint32_t* ncand;                // [rows]
   uint32_t* dbits;                // [ceil(V/32)] general-q verify: draft-vocab membership
-  int32_t* dpre;                  // [ceil(V/32)] table entries below id 32 w
+  float* vq;                      // [rows][wmax * CHUNK] general-q verify: draft logit / T
+                                  // at each table id (other entries are not written)
   QStat* qst;                     // [rows] per draft row (b * k + j)
   int32_t* qflag;                 // [1] 1 when the draft table is valid
   int32_t wmax;

@@ -233,7 +233,7 @@ __global__ __launch_bounds__(TPB) void k_collect(Args a) {
   const RowParams p = load_params(a, b, j);
   if (p.cls != CLS_GENERAL) return;
   if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) return;
-  if (a.s.rs[r].phase == PH_DONE) return;  // decided by k_finalize (errors, general-q rows)
+  if (a.s.rs[r].phase != PH_PENDING) return;  // decided, or a general-q row (k_final)
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int c0 = c * CHUNK, i0 = c0 + t * EPT;
 
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     __syncthreads();
   }
   // rows the candidate path cannot hold go to the exact streaming resolution
-  bool exact = status == STRIM_OK && !p.greedy && s_bd.mode == MODE_NONE;
+  bool exact = status == STRIM_OK && !p.greedy && (phase == PH_EXACT || s_bd.mode == MODE_NONE);
   auto finish = [&](int stt, int token, int accept, double sig, uint64_t lk) {
     if (t == 0) {
       rsp->status = stt;
@@ -877,10 +877,19 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   xa.drafts = a.drafts;
   xa.noise = a.noise;
   xa.noise_stride = a.noise_stride;
-  xa.has_q = 0;  // general-q rows are decided in k_finalize
-  const XOut xo = exact_row<FIN_T>(xa, r, b, j, p, m, st.arg, draft, verify_draft_row,
+  xa.has_q = phase == PH_EXACT ? 1 : 0;
+  if (xa.has_q) {
+    // the draft distribution q of a general-q verify row (k_qprep)
+    const int qr = b * a.k + j;
+    const QStat qs = a.s.qst[qr];
+    xa.q.dbits = a.s.dbits;
+    xa.q.vq = a.s.vq + (size_t)qr * (size_t)a.s.wmax * CHUNK;
+    xa.q.mq = qs.mq;
+    xa.q.Z = qs.Z;
+  }
+  const XOut xo = exact_row<FIN_T>(xa, r, b, j, p, st.m, st.arg, draft, verify_draft_row,
                             verify_draft_row ? rsp->l_draft : -INFINITY, xs, s_x);
-  if (t == 0) rsp->bd.mode = MODE_A;  // kept set = order prefix up to last_key
+  if (t == 0 && phase == PH_PENDING) rsp->bd.mode = MODE_A;  // kept set = order prefix up to last_key
   finish(xo.status, xo.token, xo.accept, xo.sig, xo.last_key);
 }
 
@@ -981,12 +990,13 @@ __device__ __forceinline__ int table_lower_bound(const int32_t* tab, int n, int 
 }
 
 // Blocks [0, B*k): one draft row each: mq = max(draft_logit / T) (fp32 division, as the
-// target's temperature), Z = sum exp(v - mq) in fp64, and the table index of the row's
-// draft token (the draft distribution of SpecSampling's general-q extension). Block 0
-// also checks that the table is strictly ascending inside [0, V). Blocks after them: one
-// thread per 32-token word of the vocabulary: the bitmap of table ids and the number of
-// table entries below the word (so a member's table index is that prefix plus the
-// popcount of the lower bits).
+// target's temperature), Z = sum exp(v - mq) in fp64, the table index of the row's
+// draft token, and v = draft_logit / T stored at each table id of the row's dense array
+// (the draft distribution of SpecSampling's general-q extension). Block 0 also checks
+// that the table is strictly ascending inside [0, V). Blocks after them: one thread per
+// table entry builds the membership bitmap: the first entry of each 32-id word writes
+// the word's bits and zeroes the empty words before it (the last entry also those
+// after it), so every word is written once.
 __global__ __launch_bounds__(256) void k_qprep(Args a) {
   __shared__ float s_m[256 / WAVE];
   __shared__ double s_d[256 / WAVE];
@@ -996,51 +1006,91 @@ __global__ __launch_bounds__(256) void k_qprep(Args a) {
   const int blk = blockIdx.x;
   if (blk < nq) {
     const int b = blk / a.k, j = blk % a.k;
-    if (blk == 0) {
-      int bad = 0;
-      for (int i = t; i < Vd; i += 256) {
-        const int id = a.dtable[i];
-        if (id < 0 || id >= a.V || (i + 1 < Vd && !(id < a.dtable[i + 1]))) bad = 1;
+    const int d = a.drafts[(int64_t)b * a.k + j];
+    const float T = a.p[b].temperature;
+    const size_t base = (size_t)blk * (size_t)Vd;
+    float* vq = a.s.vq + (size_t)blk * (size_t)a.s.wmax * CHUNK;
+    auto ld = [&](int i) -> float {
+      return a.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.dlog)[base + i])
+                                         : ((const float*)a.dlog)[base + i];
+    };
+    // batches of QB entries per thread: every load of a batch is issued before its
+    // stores (a store could alias a later load, which would serialise the loop). One
+    // pass: the table check (block 0), the draft's table index, v = logit / T at each id
+    // and the maximum.
+    constexpr int QB = 16;
+    const bool live = T > 0.0f;
+    float mx = -INFINITY;
+    int bad = 0, td = -1;
+    for (int i0 = t; i0 < Vd; i0 += QB * 256) {
+      float v[QB];
+      int id[QB], idn[QB];
+#pragma unroll
+      for (int q = 0; q < QB; ++q) {
+        const int i = i0 + q * 256 < Vd ? i0 + q * 256 : 0;
+        v[q] = ld(i);
+        id[q] = a.dtable[i];
+        idn[q] = a.dtable[i + 1 < Vd ? i + 1 : i];
       }
+#pragma unroll
+      for (int q = 0; q < QB; ++q) {
+        const int i = i0 + q * 256;
+        if (i >= Vd) continue;
+        if (id[q] < 0 || id[q] >= a.V || (i + 1 < Vd && !(id[q] < idn[q]))) bad = 1;
+        if (id[q] == d) td = i;
+        if (live) {
+          v[q] = v[q] / T;
+          mx = fmaxf(mx, v[q]);
+          if (id[q] >= 0 && id[q] < a.V) vq[id[q]] = v[q];
+        }
+      }
+    }
+    if (blk == 0) {
       bad = block_or<256>(bad, s_bad);
       if (t == 0) *a.s.qflag = bad ? 0 : 1;
     }
-    const float T = a.p[b].temperature;
+    td = -block_min<256>(-td, s_bad);  // at most one entry holds the draft
     QStat q{-INFINITY, -1, 0.0};
-    if (T > 0.0f) {
-      const size_t base = (size_t)blk * (size_t)Vd;
-      auto ld = [&](int i) -> float {
-        return a.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.dlog)[base + i])
-                                           : ((const float*)a.dlog)[base + i];
-      };
-      float mx = -INFINITY;
-      for (int i = t; i < Vd; i += 256) mx = fmaxf(mx, ld(i) / T);
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, WAVE));
+    if (live) {
+      mx = wave_max_f(mx);
       if ((t & (WAVE - 1)) == 0) s_m[t / WAVE] = mx;
       __syncthreads();
       mx = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
       double z = 0.0;
-      for (int i = t; i < Vd; i += 256) z += exp((double)(ld(i) / T) - (double)mx);
+      for (int i0 = t; i0 < Vd; i0 += QB * 256) {
+        float v[QB];
+#pragma unroll
+        for (int q = 0; q < QB; ++q) v[q] = ld(i0 + q * 256 < Vd ? i0 + q * 256 : 0);
+#pragma unroll
+        for (int q = 0; q < QB; ++q)
+          if (i0 + q * 256 < Vd) z += exp((double)(v[q] / T) - (double)mx);
+      }
       z = block_sum_f64<256>(z, s_d);
       q.mq = mx;
       q.Z = z;
-      const int d = a.drafts[(int64_t)b * a.k + j];
-      const int pos = table_lower_bound(a.dtable, Vd, d);
-      q.td = (pos < Vd && a.dtable[pos] == d) ? pos : -1;
+      q.td = td;
     }
     if (t == 0) a.s.qst[blk] = q;
     return;
   }
-  const int w = (blk - nq) * 256 + t;
+  const int i = (blk - nq) * 256 + t;
+  if (i >= Vd) return;
   const int words = (a.V + 31) / 32;
-  if (w >= words) return;
-  const int lo = table_lower_bound(a.dtable, Vd, 32 * w);
-  const int hi = table_lower_bound(a.dtable, Vd, 32 * w + 32);
+  const int id = a.dtable[i];
+  if (id < 0 || id >= a.V) return;  // an invalid table: every general-q row is rejected
+  const int w = id >> 5;
+  const int pw = i > 0 ? (a.dtable[i - 1] >> 5) : -1;
+  if (pw == w) return;
   uint32_t bits = 0u;
-  for (int i = lo; i < hi; ++i) bits |= 1u << ((a.dtable[i] - 32 * w) & 31);
+  for (int e = i; e < Vd; ++e) {
+    const int ide = a.dtable[e];
+    if (ide < 0 || (ide >> 5) != w) break;
+    bits |= 1u << (ide & 31);
+  }
   a.s.dbits[w] = bits;
-  a.s.dpre[w] = lo;
+  for (int z = max(pw + 1, 0); z < w; ++z) a.s.dbits[z] = 0u;
+  if (i == Vd - 1)
+    for (int z = w + 1; z < words; ++z) a.s.dbits[z] = 0u;
 }
 
 }  // namespace strim
