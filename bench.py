@@ -189,7 +189,8 @@ def cpu_baseline_cfg2(seconds: float):
 
 
 # k_stream instantiation -> workload (cfg2 has penalties and no mask, cfg5 the reverse)
-STREAM_CASES = {"k_stream<1, true, true, false>": "cfg2", "k_stream<1, true, false, true>": "cfg5"}
+STREAM_CASES = {"k_stream<1, true, true, false, 1>": "cfg2", "k_stream<1, true, false, true, 4>": "cfg5",
+                "k_stream<1, true, false, true, 1>": "cfg3", "k_stream<1, true, false, false, 1>": "cfg4"}
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_k_stream_cfg2_cfg5.md"
 
 
@@ -233,18 +234,24 @@ def summarize(d):
                       f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
     for f in glob.glob(str(d / "trace" / "*kernel_trace.csv")):
         rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
-        acc, case = {}, None
+        acc, case, pending = {}, None, []
         for r in rows:
             if "strim::" not in r["Kernel_Name"]:
                 continue
             k = _kname(r["Kernel_Name"])
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            if k == "k_qprep":  # runs before its call's k_stream
+                pending.append(us)
+                continue
             if k.startswith("k_stream"):
                 case = STREAM_CASES.get(k, k)
+                acc.setdefault(("k_qprep", case), []).extend(pending)
+                pending = []
             kk = "k_stream" if k.startswith("k_stream") else k
-            acc.setdefault((kk, case), []).append(
-                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            acc.setdefault((kk, case), []).append(us)
+        acc = {key: v for key, v in acc.items() if v}
         print("\nThe same trace per workload (a kernel belongs to the k_stream variant it "
-              "follows):\n")
+              "follows; k_qprep to the one after it):\n")
         print("| kernel | workload | calls | avg us | median us |\n|---|---|---|---|---|")
         for (k, c), v in sorted(acc.items(), key=lambda t: (str(t[0][1]), t[0][0])):
             v = sorted(v)
