@@ -3,7 +3,7 @@
     python strim-engine_amd/build.py
 
 Always recompiles. Every translation unit is compiled to an object in parallel (the
-k_stream variants are split over one object per (dtype, penalties) pair), then the
+k_stream variants are split over one object per (dtype, penalties, segments) triple), then the
 objects are linked into strim-engine_amd/strim_amd/libstrim_sampler.so, next to the
 Python binding, so the library travels with the tree. Objects go to a temporary
 directory that is removed afterwards.

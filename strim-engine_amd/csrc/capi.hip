@@ -91,14 +91,14 @@ void timed(strim_ctx* ctx, int kind, F launch) {
 // unaligned variant checks penalties and mask per row).
 // Segments per thread of the k_stream launch: one (512-thread workgroups) while the
 // launch is small and its time is latency, four (128 threads) once the rows alone fill
-// the chip and instructions per token decide.
+// the chip and instructions per token decide. (Eight segments in one-wave workgroups
+// measured slower at B=64: 11.1 against 9.9 us.)
 constexpr int LARGE_ROWS = 32;
-int stream_sseg(const Args& a) { return a.R >= LARGE_ROWS ? 4 : 1; }
 
 hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen, hipEvent_t e0,
                          hipEvent_t e1) {
   const bool pen = any_pen || a.vec_ok == 0;
-  const bool big = stream_sseg(a) == 4;
+  const bool big = a.R >= LARGE_ROWS;
 #define STRIM_GROUP(DT, PEN, SSEG) launch_stream_group<DT, PEN, SSEG>(a, grid, st, e0, e1)
   if (a.dtype == STRIM_DTYPE_BF16) {
     if (pen) return big ? STRIM_GROUP(STRIM_DTYPE_BF16, true, 4) : STRIM_GROUP(STRIM_DTYPE_BF16, true, 1);

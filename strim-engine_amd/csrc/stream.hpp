@@ -21,9 +21,11 @@ namespace strim {
 template <int SSEG>
 constexpr int stpb() { return CHUNK / (EPT * SSEG); }
 
-// LDS of one k_stream workgroup.
+// LDS of one k_stream workgroup (the history table only in the penalties variants, so
+// the narrow workgroups of large launches fit many to a CU).
+template <bool PEN>
 struct StreamShared {
-  uint32_t cnt[CHUNK];          // history counts of the chunk's tokens (16 KB)
+  uint32_t cnt[PEN ? CHUNK : 4];  // history counts of the chunk's tokens (16 KB)
   uint32_t hc[NCB];
   unsigned long long hm[NCB];
   uint32_t lad[2 * WAVE];
@@ -143,7 +145,7 @@ template <int DT, bool VEC, bool PEN, bool MASK, int SSEG>
 __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   constexpr int STPB = stpb<SSEG>();       // threads
   constexpr int NW = STPB / WAVE;          // waves
-  __shared__ StreamShared S;
+  __shared__ StreamShared<PEN> S;
   // the launch fields used before the first global load, read together: a field first
   // read inside a branch would be its own scalar-load round trip
   asm volatile("" ::"s"(a.logits), "s"(a.row_stride), "s"(a.V), "s"(a.verify), "s"(a.k),

@@ -67,6 +67,24 @@ def test_sweep_small(ctx, V):
                              label=f"V={V} it={it} mode={mode}")
 
 
+@pytest.mark.parametrize("V", [1000, 9001, 40000])
+def test_sweep_large_batch(ctx, V):
+    # 40 rows take the large-launch k_stream variants (128-thread workgroups, four
+    # segments per thread), with and without penalties
+    rng = np.random.default_rng(3000 + V)
+    for it in range(4):
+        x, p, mask, hist, hl = _sweep_case(rng, V, 40)
+        if it % 2 == 1:  # no penalty anywhere: the variant without the history table
+            p["repetition_penalty"] = 1.0
+            p["presence_penalty"] = 0.0
+            p["frequency_penalty"] = 0.0
+        for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+            dt = "bf16" if it < 2 else "f32"
+            say(f"sweep-large V={V} it={it} mode={mode} dtype={dt}")
+            check_sample(ctx, x, p, dt, mask, hist, hl, mode, None,
+                         label=f"large V={V} it={it} mode={mode}")
+
+
 # ------------------------------------------------------------- configs ----
 def test_cfg1_fp32_chain_and_greedy(ctx):
     w = W.cfg1()
