@@ -30,6 +30,7 @@ UNITS = [
 ] + [
     ("finalize_kernels.hip", []),
     ("sample_kernels.hip", []),
+    ("qres_kernels.hip", []),
     ("aux_kernels.hip", []),
     ("capi.hip", []),
 ]

@@ -16,6 +16,13 @@ __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
 __global__ void k_qprep(Args a);
+__global__ void k_qsum(Args a);
+__global__ void k_qhist(Args a);
+__global__ void k_qpick(Args a);
+__global__ void k_qcollect(Args a);
+__global__ void k_qfinal(Args a);
+__global__ void k_qgumbel(Args a);
+__global__ void k_qgpick(Args a);
 __global__ void k_mask_logits(const void* logits, int dtype, int V, int64_t row_stride,
                               const uint32_t* mask, int64_t mask_stride, float* out);
 __global__ void k_draft_argmax(const void* logits, int dtype, int Vd, int64_t row_stride,
@@ -68,10 +75,12 @@ int32_t vec_ok(const void* p, int64_t row_stride, int32_t dtype) {
 }
 
 enum KernelId {
-  KID_STREAM = 0, KID_FINALIZE, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE, KID_QPREP
+  KID_STREAM = 0, KID_FINALIZE, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE, KID_QPREP,
+  KID_QRES
 };
 const char* const kKernelNames[STRIM_KERNEL_COUNT] = {
-    "k_stream", "k_finalize", "k_collect", "k_final", "k_probs", "k_verify_combine", "k_qprep"};
+    "k_stream", "k_finalize", "k_collect", "k_final", "k_probs", "k_verify_combine", "k_qprep",
+    "k_qres"};
 
 // Runs `launch(e0, e1)`: with profiling on, e0/e1 are the next event pair, which the
 // launch binds to its dispatch's timestamps; otherwise both are null.
@@ -142,6 +151,22 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
     timed(ctx, KID_COLLECT, [&](hipEvent_t e0, hipEvent_t e1) {
       keep(launch_args((const void*)k_collect, grid_rc, dim3(TPB), a, st, e0, e1));
     });
+  if (a.verify && a.dlog != nullptr) {
+    // the residual draw of unfiltered general-q rows (rows in other phases return)
+    const dim3 grid_r((unsigned)a.R);
+    timed(ctx, KID_QRES, [&](hipEvent_t e0, hipEvent_t e1) {
+      keep(launch_args((const void*)k_qsum, grid_rc, dim3(TPB), a, st, e0, nullptr));
+      if (a.noise_mode == STRIM_NOISE_ICDF) {
+        keep(launch_args((const void*)k_qhist, grid_rc, dim3(TPB), a, st, nullptr, nullptr));
+        keep(launch_args((const void*)k_qpick, grid_r, dim3(QNB), a, st, nullptr, nullptr));
+        keep(launch_args((const void*)k_qcollect, grid_rc, dim3(TPB), a, st, nullptr, nullptr));
+        keep(launch_args((const void*)k_qfinal, grid_r, dim3(FIN_T), a, st, nullptr, e1));
+      } else {
+        keep(launch_args((const void*)k_qgumbel, grid_rc, dim3(TPB), a, st, nullptr, nullptr));
+        keep(launch_args((const void*)k_qgpick, grid_r, dim3(WAVE), a, st, nullptr, e1));
+      }
+    });
+  }
   if (need_final)
     timed(ctx, KID_FINAL, [&](hipEvent_t e0, hipEvent_t e1) {
       keep(launch_args((const void*)k_final, dim3((unsigned)a.R), dim3(FIN_T), a, st, e0, e1));
@@ -233,7 +258,12 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   const size_t o_nc = carve(R * sizeof(uint32_t));
   const size_t words = ((size_t)max_vocab + 31) / 32;
   const size_t o_dbits = carve(words * sizeof(uint32_t));
-  const size_t o_vq = carve(R * wmax * CHUNK * sizeof(float));
+  // general-q draft rows: at most MAXP per launch group
+  const size_t RQ = R < (size_t)MAXP ? R : (size_t)MAXP;
+  const size_t o_vq = carve(RQ * wmax * CHUNK * sizeof(float));
+  const size_t o_qpart = carve(RQ * wmax * sizeof(unsigned long long));
+  const size_t o_qhc = carve(RQ * wmax * QNB * sizeof(uint32_t));
+  const size_t o_qhm = carve(RQ * wmax * QNB * sizeof(unsigned long long));
   const size_t o_qst = carve(R * sizeof(QStat));
   const size_t o_qflag = carve(sizeof(int32_t));
   ctx->bytes = off;
@@ -259,6 +289,9 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   ctx->s.ncand = (uint32_t*)(b + o_nc);
   ctx->s.dbits = (uint32_t*)(b + o_dbits);
   ctx->s.vq = (float*)(b + o_vq);
+  ctx->s.qpart = (unsigned long long*)(b + o_qpart);
+  ctx->s.qhc = (uint32_t*)(b + o_qhc);
+  ctx->s.qhm = (unsigned long long*)(b + o_qhm);
   ctx->s.qst = (QStat*)(b + o_qst);
   ctx->s.qflag = (int32_t*)(b + o_qflag);
   ctx->s.wmax = wmax;
@@ -349,6 +382,8 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
   const int64_t nstride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
   int gmax = ctx->max_rows / (k + 1);
   if (gmax > MAXP) gmax = MAXP;
+  // general-q: at most MAXP draft rows per group (their per-row scratch)
+  if (draft_logits && k > 0 && gmax * k > MAXP) gmax = MAXP / k > 0 ? MAXP / k : 1;
   return on_device(ctx->device, [&]() -> int {
     hipStream_t st = (hipStream_t)stream;
     for (int32_t g0 = 0; g0 < B; g0 += gmax) {

@@ -254,7 +254,10 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
       finish_row(a, r, STRIM_EINVAL, -1, 0, 0.0, m, 0ull, PH_DONE);
       return done;
     }
-    finish_row(a, r, STRIM_OK, -1, 0, 0.0, m, 0ull, PH_EXACT);
+    // unfiltered rows: the grid-wide residual draw (qres_kernels.hip); the others: k_final's
+    // exact resolution (the row's first maximum is kept as the fallback token)
+    const bool unfiltered = !(p.top_k > 0 && p.top_k < V) && !(p.top_p < 1.0f) && !(p.min_p > 0.0f);
+    finish_row(a, r, STRIM_OK, arg, 0, 0.0, m, 0ull, unfiltered ? PH_QRES : PH_EXACT);
     return done;
   }
   const bool topk = p.top_k > 0 && p.top_k < V;

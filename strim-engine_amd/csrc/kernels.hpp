@@ -19,6 +19,7 @@
 namespace strim {
 
 constexpr int MAXP = 64;         // parameter rows carried inline per launch group
+constexpr int QNB = 256;         // QRES coarse bins of d = m - l, 1/4 nat wide
 // k_stream runs one chunk per workgroup with 8 SSEG tokens per thread: SSEG = 1 (512
 // threads, 8 waves) for small batches, whose time is latency, and SSEG = 4 (128 threads,
 // 2 waves) for large ones, whose time is instructions per token. Each wave writes its
@@ -41,7 +42,9 @@ enum RowClass : int32_t { CLS_GREEDY = 0, CLS_FAST = 1, CLS_GENERAL = 2, CLS_INV
 // Set by k_finalize: DONE rows are decided; PENDING rows (general path) go to
 // k_collect + k_final; EXACT rows (general-q verify rows) go to k_final's exact streaming
 // resolution, whose workgroups are four times wider than k_finalize's.
-enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1, PH_EXACT = 2 };
+// QRES rows (unfiltered general-q verify rows) are decided by the grid-wide residual
+// draw (qres_kernels.hip), which demotes an icdf row to EXACT when its bucket overflows.
+enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1, PH_EXACT = 2, PH_QRES = 3 };
 
 enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
 
@@ -95,6 +98,10 @@ struct RowState {
   int32_t phase;      // RowPhase: which kernel still has to decide the row
   uint64_t last_key;  // last kept token's order key (0 = none kept beyond bin rules)
   Bounds bd;          // general rows (k_collect)
+  // QRES rows: plain mass S, residual mass, draw target T (fixed point), the chosen
+  // coarse bin and the residual mass before it
+  uint64_t qS, qR, qT, qbelow;
+  int32_t qbin, pad_;
 };
 
 // Draft distribution of one general-q verify row: q = softmax(draft logits / T).
@@ -117,8 +124,11 @@ struct Scratch {
   Cand* cand;                     // [rows][CAP]
   uint32_t* ncand;                // [rows]
   uint32_t* dbits;                // [ceil(V/32)] general-q verify: draft-vocab membership
-  float* vq;                      // [rows][wmax * CHUNK] general-q verify: draft logit / T
-                                  // at each table id (other entries are not written)
+  float* vq;                      // [MAXP][wmax * CHUNK] general-q verify, per draft row:
+                                  // draft logit / T at each table id (others not written)
+  unsigned long long* qpart;      // [MAXP][wmax] QRES rows: plain mass per chunk
+  uint32_t* qhc;                  // [MAXP][wmax][QNB] QRES rows: residual counts per bin
+  unsigned long long* qhm;        // [MAXP][wmax][QNB] QRES rows: residual masses per bin
   QStat* qst;                     // [rows] per draft row (b * k + j)
   int32_t* qflag;                 // [1] 1 when the draft table is valid
   int32_t wmax;
@@ -159,11 +169,12 @@ struct Args {
 
 // Launches kernel `fn(Args)` on st. Given a start/stop event pair, the events take the
 // dispatch's own begin and end timestamps (hipExtLaunchKernel), so their elapsed time is
-// the kernel's execution alone, without the queue's gap before it.
+// the kernel's execution alone, without the queue's gap before it; a sequence of
+// launches passes the start event to its first and the stop event to its last.
 inline hipError_t launch_args(const void* fn, dim3 grid, dim3 block, const Args& a,
                               hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   void* args[] = {const_cast<Args*>(&a)};
-  if (e0 && e1) return hipExtLaunchKernel(fn, grid, block, args, 0, st, e0, e1, 0);
+  if (e0 || e1) return hipExtLaunchKernel(fn, grid, block, args, 0, st, e0, e1, 0);
   return hipLaunchKernel(fn, grid, block, args, 0, st);
 }
 

@@ -1,0 +1,418 @@
+// qres_kernels.hip — the residual draw of general-q verify rows on the whole chip.
+//
+// An unfiltered general-q draft row with an icdf draw (phase QRES) draws from the
+// residual max(0, p - q) over every allowed token, in the token order (l descending, id
+// ascending), with the fixed-point masses of the exact streaming resolution (exact.hpp:
+// 2^43 per unit of exp(l - m), so every sum is exact and independent of order): the
+// drawn token is the last one whose residual mass before it is <= T = floor(u R), R the
+// row's residual mass. The exact resolution makes these passes with one workgroup per
+// row; here each pass runs on a (chunks, rows) grid:
+//   k_qsum      per chunk: plain mass W = round(exp(l - m) 2^43) summed      -> S
+//   k_qhist     per chunk: residual weights (they need S), counts and masses in QNB
+//               coarse bins of d = m - l (1/4 nat; monotone along the order)
+//   k_qpick     per row: R, T, the last non-empty bin whose mass before it is <= T
+//   k_qcollect  per chunk: the tokens of that bin
+//   k_qfinal    per row: sorts them, finds the token, the p(d) / q(d) accept
+// A bin with more than CAP tokens leaves the row to k_final's exact resolution.
+//
+// With Gumbel noise the draw is the argmax over the row of log(p - q) + g (log p where
+// q = 0, tokens with p <= q excluded), ties to the smaller id: after k_qsum,
+//   k_qgumbel   per chunk: the chunk's best (score, id)
+//   k_qgpick    per row: the best over the chunks, the p(d) / q(d) accept.
+#include "exact.hpp"
+
+namespace strim {
+
+// Coarse bin of a token: floor(4 (m - l)), the last bin open.
+__device__ __forceinline__ int q_bin(float l, float m) {
+  const double d = (double)m - (double)l;
+  return d < (double)(QNB - 1) / 4.0 ? (int)(d * 4.0) : QNB - 1;
+}
+
+// The draft distribution of draft row qr = b * k + j (k_qprep).
+__device__ __forceinline__ XQ q_of_row(const Args& a, int qr) {
+  const QStat qs = a.s.qst[qr];
+  XQ q;
+  q.dbits = a.s.dbits;
+  q.vq = a.s.vq + (size_t)qr * (size_t)a.s.wmax * CHUNK;
+  q.mq = qs.mq;
+  q.Z = qs.Z;
+  return q;
+}
+
+// Residual weight of a token of plain weight W: max(0, W - round(q S)) where q > 0
+// (x_wt's rule with the kept mass S).
+__device__ __forceinline__ uint64_t q_resid(uint64_t W, double q, uint64_t S) {
+  if (q == 0.0) return W;
+  const uint64_t qS = (uint64_t)__double2ull_rn(q * (double)S);
+  return W > qS ? W - qS : 0ull;
+}
+
+// The processed logits of this thread's EPT tokens of chunk c, as k_collect computes
+// them (every thread of the workgroup calls it: the history counts use barriers).
+__device__ __forceinline__ void q_tokens(const Args& a, int r, int b, int j, const RowParams& p,
+                                         int c, uint32_t* s_cnt, float (&l)[EPT]) {
+  const int c0 = c * CHUNK, i0 = c0 + (int)threadIdx.x * EPT;
+  float x[EPT];
+  load_tokens(a, r, i0, x);
+  if (p.pen) build_counts(a, b, j, c0, s_cnt);
+  bool nf = false;
+  process_tokens(a, r, i0, p, s_cnt + (i0 & (CHUNK - 1)), x, l, nf);
+}
+
+template <int NT>
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* scratch) {
+  v = wave_sum_u64(v);
+  if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x / WAVE] = v;
+  __syncthreads();
+  uint64_t s = 0ull;
+#pragma unroll
+  for (int q = 0; q < NT / WAVE; ++q) s += scratch[q];
+  __syncthreads();
+  return s;
+}
+
+__global__ __launch_bounds__(TPB) void k_qsum(Args a) {
+  __shared__ uint32_t s_cnt[CHUNK];
+  __shared__ uint64_t s_red[TPB / WAVE];
+  int r, c;
+  map_block(r, c);
+  int b, j;
+  row_bj(a, r, b, j);
+  if (a.s.rs[r].phase != PH_QRES) return;
+  const RowParams p = load_params(a, b, j);
+  const float m = a.s.rs[r].m;
+  float l[EPT];
+  q_tokens(a, r, b, j, p, c, s_cnt, l);
+  uint64_t w = 0ull;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e)
+    if (l[e] > -INFINITY) w += x_weight(l[e], m);
+  w = block_sum_u64<TPB>(w, s_red);
+  if (threadIdx.x == 0) a.s.qpart[(size_t)(b * a.k + j) * a.s.wmax + c] = w;
+}
+
+__global__ __launch_bounds__(TPB) void k_qhist(Args a) {
+  __shared__ uint32_t s_cnt[CHUNK];
+  __shared__ uint64_t s_red[TPB / WAVE];
+  __shared__ uint32_t s_hc[QNB];
+  __shared__ uint64_t s_hm[QNB];
+  int r, c;
+  map_block(r, c);
+  int b, j;
+  row_bj(a, r, b, j);
+  if (a.s.rs[r].phase != PH_QRES) return;
+  const int t = threadIdx.x, qr = b * a.k + j;
+  const RowParams p = load_params(a, b, j);
+  const float m = a.s.rs[r].m;
+  // S: the plain masses of the row's chunks (integers, so any order)
+  const uint64_t sp = t < a.W ? a.s.qpart[(size_t)qr * a.s.wmax + t] : 0ull;
+  float l[EPT];
+  q_tokens(a, r, b, j, p, c, s_cnt, l);
+  if (t < QNB) {
+    s_hc[t] = 0u;
+    s_hm[t] = 0ull;
+  }
+  const uint64_t S = block_sum_u64<TPB>(sp, s_red);
+  const XQ q = q_of_row(a, qr);
+  const int i0 = c * CHUNK + t * EPT;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    if (!(l[e] > -INFINITY)) continue;
+    const uint64_t rr = q_resid(x_weight(l[e], m), xq_prob(q, i0 + e), S);
+    const int g = q_bin(l[e], m);
+    atomicAdd(&s_hc[g], 1u);
+    atomicAdd((unsigned long long*)&s_hm[g], (unsigned long long)rr);
+  }
+  __syncthreads();
+  if (t < QNB) {
+    const size_t o = ((size_t)qr * a.s.wmax + c) * QNB + t;
+    a.s.qhc[o] = s_hc[t];
+    a.s.qhm[o] = s_hm[t];
+  }
+}
+
+// One row per QNB-thread workgroup: thread g owns coarse bin g.
+__global__ __launch_bounds__(QNB) void k_qpick(Args a) {
+  __shared__ uint64_t s_red[QNB / WAVE];
+  __shared__ uint64_t s_u2[2 * QNB / WAVE];
+  __shared__ int s_i[QNB / WAVE];
+  __shared__ uint32_t s_bc;
+  __shared__ uint64_t s_bm;
+  const int r = blockIdx.x;
+  int b, j;
+  row_bj(a, r, b, j);
+  RowState* rs = &a.s.rs[r];
+  if (rs->phase != PH_QRES) return;
+  const int t = threadIdx.x, qr = b * a.k + j, W = a.W;
+  const RowParams p = load_params(a, b, j);
+  const uint64_t sp = t < W ? a.s.qpart[(size_t)qr * a.s.wmax + t] : 0ull;
+  uint32_t cc = 0u;
+  uint64_t cm = 0ull;
+  for (int c = 0; c < W; ++c) {
+    const size_t o = ((size_t)qr * a.s.wmax + c) * QNB + t;
+    cc += a.s.qhc[o];
+    cm += a.s.qhm[o];
+  }
+  const uint64_t S = block_sum_u64<QNB>(sp, s_red);
+  uint64_t exc, exm, totc, totm;
+  block_excl_scan2_u64<QNB>(cc, cm, s_u2, exc, exm, totc, totm);
+  const double uu = (double)row_uniform(a, r, p, 0);
+  const uint64_t T = (uint64_t)floor(uu * (double)totm);
+  // the last non-empty bin whose residual mass before it is <= T
+  const int mine = (cc > 0u && exm <= T) ? t : -1;
+  const int best = -block_min<QNB>(-mine, s_i);
+  if (t == best) {
+    s_bc = cc;
+    s_bm = exm;
+  }
+  __syncthreads();
+  if (t == 0) {
+    rs->qS = S;
+    rs->qR = totm;
+    rs->qT = T;
+    rs->qbin = best;
+    rs->qbelow = best >= 0 ? s_bm : 0ull;
+    if (best >= 0 && s_bc > (uint32_t)CAP) rs->phase = PH_EXACT;  // k_final resolves it
+  }
+}
+
+__global__ __launch_bounds__(TPB) void k_qcollect(Args a) {
+  __shared__ uint32_t s_cnt[CHUNK];
+  int r, c;
+  map_block(r, c);
+  int b, j;
+  row_bj(a, r, b, j);
+  const RowState* rs = &a.s.rs[r];
+  if (rs->phase != PH_QRES) return;
+  const int qbin = rs->qbin;
+  if (qbin < 0) return;
+  const int t = threadIdx.x, lane = t & (WAVE - 1);
+  const RowParams p = load_params(a, b, j);
+  const float m = rs->m;
+  float l[EPT];
+  q_tokens(a, r, b, j, p, c, s_cnt, l);
+  const int i0 = c * CHUNK + t * EPT;
+  uint32_t sel = 0u;
+  int mycnt = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e)
+    if (l[e] > -INFINITY && q_bin(l[e], m) == qbin) {
+      sel |= 1u << e;
+      ++mycnt;
+    }
+  int tot;
+  const int wex = wave_excl_count(mycnt, &tot);
+  if (tot > 0) {
+    unsigned base = 0;
+    if (lane == 0) base = atomicAdd(&a.s.ncand[r], (unsigned)tot);
+    base = (unsigned)__builtin_amdgcn_readlane((int)base, 0);
+    unsigned pos = base + (unsigned)wex;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if ((sel >> e) & 1u) {
+        if (pos < (unsigned)CAP) a.s.cand[(int64_t)r * CAP + pos] = Cand{l[e], i0 + e};
+        ++pos;
+      }
+  }
+}
+
+__global__ __launch_bounds__(FIN_T) void k_qfinal(Args a) {
+  __shared__ uint64_t s_key[CAP];
+  __shared__ uint64_t s_tmp[CAP];
+  __shared__ uint64_t s_u2[2 * FIN_T / WAVE];
+  __shared__ int s_i[FIN_T / WAVE];
+  const int r = blockIdx.x;
+  int b, j;
+  row_bj(a, r, b, j);
+  RowState* rs = &a.s.rs[r];
+  if (rs->phase != PH_QRES) return;
+  const int t = threadIdx.x, qr = b * a.k + j;
+  const RowParams p = load_params(a, b, j);
+  const float m = rs->m;
+  const uint64_t S = rs->qS, R = rs->qR, T = rs->qT, below = rs->qbelow;
+  const int qbin = rs->qbin, arg = rs->token;
+  const int draft = a.drafts[(int64_t)b * a.k + j];
+  const float l_draft = rs->l_draft;
+  const XQ q = q_of_row(a, qr);
+  int token = arg;
+  if (qbin >= 0) {
+    const int n = min((int)a.s.ncand[r], CAP);
+    uint64_t kk[FIN_Q];
+#pragma unroll
+    for (int e = 0; e < FIN_Q; ++e) {
+      const int idx = e * FIN_T + t;
+      kk[e] = ~0ull;
+      if (idx < n) {
+        const Cand cd = a.s.cand[(int64_t)r * CAP + idx];
+        kk[e] = ckey(cd.l, cd.id);
+      }
+    }
+    sort_keys(kk, n, s_key, s_tmp);
+    // residual weights in order; thread t owns positions FIN_Q t .. FIN_Q t + FIN_Q - 1
+    uint64_t w[FIN_Q], lm = 0ull;
+#pragma unroll
+    for (int e = 0; e < FIN_Q; ++e) {
+      const int pos = FIN_Q * t + e;
+      w[e] = 0ull;
+      if (pos < n) {
+        const uint64_t key = s_key[pos];
+        const int id = (int)(uint32_t)key;
+        w[e] = q_resid(x_weight(fkey_desc_inv((uint32_t)(key >> 32)), m), xq_prob(q, id), S);
+        lm += w[e];
+      }
+    }
+    uint64_t ex0, exm, tot0, totm;
+    block_excl_scan2_u64<FIN_T>(0ull, lm, s_u2, ex0, exm, tot0, totm);
+    // the last token whose residual mass before it is <= T
+    int best = -1;
+    uint64_t fm = below + exm;
+#pragma unroll
+    for (int e = 0; e < FIN_Q; ++e) {
+      const int pos = FIN_Q * t + e;
+      if (pos < n) {
+        if (fm <= T) best = pos;
+        fm += w[e];
+      }
+    }
+    best = -block_min<FIN_T>(-best, s_i);
+    // an all-zero residual draws the row's first maximum
+    if (best >= 0 && R > 0ull) token = (int)(uint32_t)s_key[best];
+  }
+  // accept iff u < p(d) / q(d)
+  const double sig = (double)S / XFIX;
+  const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
+  double ratio = w_d / sig;
+  const double qd = xq_prob(q, draft);
+  ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
+  const float ua = row_uniform(a, r, p, 1);
+  const int acc = ((double)ua < ratio) ? 1 : 0;
+  if (t == 0) {
+    rs->status = STRIM_OK;
+    rs->token = token;
+    rs->accept = acc;
+    rs->sum_kept = sig;
+    rs->last_key = ~0ull;
+    rs->phase = PH_DONE;
+  }
+}
+
+// (score, id) argmax, larger score first, then the smaller id; id < 0 is empty.
+__device__ __forceinline__ void q_take(double& a, int& ai, double b, int bi) {
+  if (bi >= 0 && (ai < 0 || b > a || (b == a && bi < ai))) {
+    a = b;
+    ai = bi;
+  }
+}
+__device__ __forceinline__ void q_wave_best(double& sc, int& id) {
+#define STRIM_Q_STEP(C) q_take(sc, id, dpp_d<C>(sc), dpp_i<C>(id))
+  STRIM_Q_STEP(DPP_XOR1);
+  STRIM_Q_STEP(DPP_XOR2);
+  STRIM_Q_STEP(DPP_HALF_MIRROR);
+  STRIM_Q_STEP(DPP_MIRROR);
+#undef STRIM_Q_STEP
+  double bs = rl_d(sc, 0);
+  int bi = rl_i(id, 0);
+  q_take(bs, bi, rl_d(sc, 16), rl_i(id, 16));
+  q_take(bs, bi, rl_d(sc, 32), rl_i(id, 32));
+  q_take(bs, bi, rl_d(sc, 48), rl_i(id, 48));
+  sc = bs;
+  id = bi;
+}
+
+__global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
+  __shared__ uint32_t s_cnt[CHUNK];
+  __shared__ uint64_t s_red[TPB / WAVE];
+  __shared__ double s_sc[TPB / WAVE];
+  __shared__ int s_id[TPB / WAVE];
+  int r, c;
+  map_block(r, c);
+  int b, j;
+  row_bj(a, r, b, j);
+  if (a.s.rs[r].phase != PH_QRES) return;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE, qr = b * a.k + j;
+  const RowParams p = load_params(a, b, j);
+  const float m = a.s.rs[r].m;
+  const uint64_t sp = t < a.W ? a.s.qpart[(size_t)qr * a.s.wmax + t] : 0ull;
+  float l[EPT];
+  q_tokens(a, r, b, j, p, c, s_cnt, l);
+  const uint64_t S = block_sum_u64<TPB>(sp, s_red);
+  const double lse = log((double)S / XFIX);
+  const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
+  const uint64_t pkey = mix64(p.seed, p.position);
+  const XQ q = q_of_row(a, qr);
+  const int i0 = c * CHUNK + t * EPT;
+  double bsc = -INFINITY;
+  int bid = -1;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    if (!(l[e] > -INFINITY)) continue;
+    const int id = i0 + e;
+    double base = no_lse ? (double)l[e] : ((double)l[e] - (double)m) - lse;
+    const double qq = xq_prob(q, id);
+    if (qq != 0.0) {
+      // residual score: log(p - q), excluded where p <= q
+      const double rr = exp(base) - qq;
+      if (!(rr > 0.0)) continue;
+      base = log(rr);
+    }
+    const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
+                            : philox_uniform(pkey, (uint64_t)id);
+    q_take(bsc, bid, base + gumbel64(u), id);
+  }
+  q_wave_best(bsc, bid);
+  if (lane == 0) {
+    s_sc[w] = bsc;
+    s_id[w] = bid;
+  }
+  __syncthreads();
+  if (t == 0) {
+#pragma unroll
+    for (int k = 1; k < TPB / WAVE; ++k) q_take(bsc, bid, s_sc[k], s_id[k]);
+    const size_t o = ((size_t)qr * a.s.wmax + c) * QNB;
+    a.s.qhm[o] = (unsigned long long)__double_as_longlong(bsc);
+    a.s.qhc[o] = (uint32_t)bid;
+  }
+}
+
+// One row per wave.
+__global__ __launch_bounds__(WAVE) void k_qgpick(Args a) {
+  const int r = blockIdx.x;
+  int b, j;
+  row_bj(a, r, b, j);
+  RowState* rs = &a.s.rs[r];
+  if (rs->phase != PH_QRES) return;
+  const int t = threadIdx.x, qr = b * a.k + j;
+  const RowParams p = load_params(a, b, j);
+  uint64_t sp = 0ull;
+  double bsc = -INFINITY;
+  int bid = -1;
+  for (int c = t; c < a.W; c += WAVE) {
+    sp += a.s.qpart[(size_t)qr * a.s.wmax + c];
+    const size_t o = ((size_t)qr * a.s.wmax + c) * QNB;
+    q_take(bsc, bid, __longlong_as_double((long long)a.s.qhm[o]), (int)a.s.qhc[o]);
+  }
+  const uint64_t S = wave_sum_u64(sp);
+  q_wave_best(bsc, bid);
+  const float m = rs->m;
+  const int draft = a.drafts[(int64_t)b * a.k + j];
+  const float l_draft = rs->l_draft;
+  const XQ q = q_of_row(a, qr);
+  const double sig = (double)S / XFIX;
+  const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
+  double ratio = w_d / sig;
+  const double qd = xq_prob(q, draft);
+  ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
+  const float ua = row_uniform(a, r, p, (int64_t)a.V);
+  const int acc = ((double)ua < ratio) ? 1 : 0;
+  if (t == 0) {
+    rs->status = STRIM_OK;
+    rs->token = bid >= 0 ? bid : rs->token;  // the row's first maximum when nothing scores
+    rs->accept = acc;
+    rs->sum_kept = sig;
+    rs->last_key = ~0ull;
+    rs->phase = PH_DONE;
+  }
+}
+
+}  // namespace strim

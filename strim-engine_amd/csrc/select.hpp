@@ -535,4 +535,114 @@ __device__ uint64_t wave_radix_kth(const uint64_t* key, int n, uint32_t k, uint3
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Sorting the candidates of a 1024-thread finalize workgroup (k_final, k_qfinal)
+// ---------------------------------------------------------------------------------
+// Ascending sort of the n2 (power of two, 64 <= n2 <= CAP) unique keys k[q] (element
+// q * FIN_T + t) into s_key, with s_tmp (n2 entries) as the second buffer. Runs of 64
+// are sorted by rank within the run, then merged pairwise: a key's place in the merged
+// run is its place in its own run plus its lower bound in the partner run (keys are
+// unique, so every round is a permutation).
+__device__ inline void merge_sort(const uint64_t (&k)[FIN_Q], int n2, uint64_t* s_key,
+                           uint64_t* s_tmp) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1);
+#pragma unroll
+  for (int q = 0; q < FIN_Q; ++q)
+    if (q * FIN_T < n2) s_key[q * FIN_T + t] = k[q];
+  __syncthreads();
+  uint64_t* A = s_key;
+  uint64_t* B = s_tmp;
+  // runs of 64: the wave's 64 consecutive positions of each stripe q
+#pragma unroll
+  for (int q = 0; q < FIN_Q; ++q) {
+    if (q * FIN_T >= n2) continue;
+    const int base = q * FIN_T + (t - lane);
+    const uint64_t k0 = A[base + lane];
+    uint32_t rk = 0;
+#pragma unroll 8
+    for (int i = 0; i < WAVE; i += 2) {
+      const ulonglong2 xy = *(const ulonglong2*)&A[base + i];
+      rk += (uint32_t)(xy.x < k0) + (uint32_t)(xy.y < k0);
+    }
+    B[base + rk] = k0;
+  }
+  __syncthreads();
+  {
+    uint64_t* T = A; A = B; B = T;
+  }
+  for (int R = WAVE; R < n2; R <<= 1) {
+#pragma unroll
+    for (int q = 0; q < FIN_Q; ++q) {
+      const int idx = q * FIN_T + t;
+      if (idx >= n2) continue;
+      const uint64_t k0 = A[idx];
+      const int ri = idx / R, pi = idx & (R - 1);
+      const uint64_t* P = A + (ri ^ 1) * R;
+      int pos = 0;
+      for (int st = R >> 1; st >= 1; st >>= 1)
+        if (P[pos + st - 1] < k0) pos += st;
+      pos += P[pos] < k0 ? 1 : 0;
+      B[(ri & ~1) * R + pi + pos] = k0;
+    }
+    __syncthreads();
+    uint64_t* T = A; A = B; B = T;
+  }
+  if (A != s_key) {
+#pragma unroll
+    for (int q = 0; q < FIN_Q; ++q)
+      if (q * FIN_T < n2) s_key[q * FIN_T + t] = A[q * FIN_T + t];
+    __syncthreads();
+  }
+}
+
+// Ascending sort of the n <= CAP unique keys kk[q] (element q * FIN_T + t) into s_key
+// (2 * FIN_T entries at least); s_tmp (CAP entries) is the merge sort's second buffer.
+__device__ inline void sort_keys(uint64_t (&kk)[FIN_Q], int n, uint64_t* s_key, uint64_t* s_tmp) {
+  const int t = threadIdx.x;
+  int n2 = 64;
+  while (n2 < n) n2 <<= 1;
+  if (n <= FIN_T) {
+    // one key per thread: every wave ranks its 64 keys among themselves and writes them
+    // as a sorted run; a key's rank is its rank in its run plus its lower bound in each
+    // other run (keys are unique, so the ranks are a permutation of 0..n-1). Pads sort
+    // after every key (a finite l has key bits below 0xFF800000 << 32).
+    const int w = t / WAVE, lane = t & (WAVE - 1);
+    const uint64_t k0 = t < n ? kk[0] : (0xFFFFFFFF00000000ull | (uint32_t)t);
+    uint64_t* run = s_key + FIN_T;  // FIN_T sorted keys, 64 per run
+    s_key[t] = k0;
+    wave_sync();
+    uint32_t rw = 0;
+#pragma unroll 8
+    for (int q = 0; q < WAVE; q += 2) {
+      const ulonglong2 xy = *(const ulonglong2*)&s_key[w * WAVE + q];
+      rw += (uint32_t)(xy.x < k0) + (uint32_t)(xy.y < k0);
+    }
+    run[w * WAVE + rw] = k0;
+    __syncthreads();
+    uint32_t rank = rw;
+    const int nrun = (n + WAVE - 1) / WAVE;
+#pragma unroll
+    for (int q = 0; q < FIN_T / WAVE; ++q) {
+      if (q >= nrun || q == w) continue;
+      const uint64_t* rq = run + q * WAVE;
+      uint32_t pos = 0;
+#pragma unroll
+      for (int st = WAVE / 2; st >= 1; st >>= 1)
+        if (rq[pos + st - 1] < k0) pos += st;
+      pos += rq[pos] < k0 ? 1u : 0u;
+      rank += pos;
+    }
+    if (t < n) s_key[rank] = k0;
+    __syncthreads();
+  } else {
+    // pads (after every key, see above) fill the power of two
+#pragma unroll
+    for (int q = 0; q < FIN_Q; ++q) {
+      const int idx = q * FIN_T + t;
+      if (idx >= n) kk[q] = 0xFFFFFFFF00000000ull | (uint32_t)idx;
+    }
+    merge_sort(kk, n2, s_key, s_tmp);
+  }
+}
+
 }  // namespace strim

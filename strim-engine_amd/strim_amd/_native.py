@@ -37,7 +37,7 @@ EXPORTS = (
     "strim_profile_end",
     "strim_kernel_name",
 )
-KERNEL_COUNT = 7
+KERNEL_COUNT = 8
 
 
 class StrimError(RuntimeError):
