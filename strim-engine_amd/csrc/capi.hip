@@ -429,9 +429,9 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       if (a.dlog) {
         // draft distributions (one workgroup per draft row) and, with the first group,
         // the draft-vocab bitmap (one thread per table entry)
-        const int nwb = g0 == 0 ? (int)((Vd + 255) / 256) : 0;
+        const int nwb = g0 == 0 ? (int)((Vd + QPT - 1) / QPT) : 0;
         timed(ctx, KID_QPREP, [&](hipEvent_t e0, hipEvent_t e1) {
-          e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k + nwb)), dim3(256), a, st,
+          e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k + nwb)), dim3(QPT), a, st,
                           e0, e1);
         });
         if (e != hipSuccess) return STRIM_EHIP;

@@ -20,6 +20,7 @@ namespace strim {
 
 constexpr int MAXP = 64;         // parameter rows carried inline per launch group
 constexpr int QNB = 256;         // QRES coarse bins of d = m - l, 1/4 nat wide
+constexpr int QPT = 1024;        // threads of a k_qprep workgroup
 // k_stream runs one chunk per workgroup with 8 SSEG tokens per thread: SSEG = 1 (512
 // threads, 8 waves) for small batches, whose time is latency, and SSEG = 4 (128 threads,
 // 2 waves) for large ones, whose time is instructions per token. Each wave writes its

@@ -889,7 +889,7 @@ __device__ __forceinline__ int table_lower_bound(const int32_t* tab, int n, int 
   return lo;
 }
 
-// Blocks [0, B*k): one draft row each: mq = max(draft_logit / T) (fp32 division, as the
+// QPT-thread workgroups. Blocks [0, B*k): one draft row each: mq = max(draft_logit / T) (fp32 division, as the
 // target's temperature), Z = sum exp(v - mq) in fp64, the table index of the row's
 // draft token, and v = draft_logit / T stored at each table id of the row's dense array
 // (the draft distribution of SpecSampling's general-q extension). Block 0 also checks
@@ -897,10 +897,10 @@ __device__ __forceinline__ int table_lower_bound(const int32_t* tab, int n, int 
 // table entry builds the membership bitmap: the first entry of each 32-id word writes
 // the word's bits and zeroes the empty words before it (the last entry also those
 // after it), so every word is written once.
-__global__ __launch_bounds__(256) void k_qprep(Args a) {
-  __shared__ float s_m[256 / WAVE];
-  __shared__ double s_d[256 / WAVE];
-  __shared__ int s_bad[256 / WAVE];
+__global__ __launch_bounds__(QPT) void k_qprep(Args a) {
+  __shared__ float s_m[QPT / WAVE];
+  __shared__ double s_d[QPT / WAVE];
+  __shared__ int s_bad[QPT / WAVE];
   const int t = threadIdx.x;
   const int nq = a.B * a.k, Vd = a.Vd;
   const int blk = blockIdx.x;
@@ -922,19 +922,19 @@ __global__ __launch_bounds__(256) void k_qprep(Args a) {
     const bool live = T > 0.0f;
     float mx = -INFINITY;
     int bad = 0, td = -1;
-    for (int i0 = t; i0 < Vd; i0 += QB * 256) {
+    for (int i0 = t; i0 < Vd; i0 += QB * QPT) {
       float v[QB];
       int id[QB], idn[QB];
 #pragma unroll
       for (int q = 0; q < QB; ++q) {
-        const int i = i0 + q * 256 < Vd ? i0 + q * 256 : 0;
+        const int i = i0 + q * QPT < Vd ? i0 + q * QPT : 0;
         v[q] = ld(i);
         id[q] = a.dtable[i];
         idn[q] = a.dtable[i + 1 < Vd ? i + 1 : i];
       }
 #pragma unroll
       for (int q = 0; q < QB; ++q) {
-        const int i = i0 + q * 256;
+        const int i = i0 + q * QPT;
         if (i >= Vd) continue;
         if (id[q] < 0 || id[q] >= a.V || (i + 1 < Vd && !(id[q] < idn[q]))) bad = 1;
         if (id[q] == d) td = i;
@@ -946,26 +946,28 @@ __global__ __launch_bounds__(256) void k_qprep(Args a) {
       }
     }
     if (blk == 0) {
-      bad = block_or<256>(bad, s_bad);
+      bad = block_or<QPT>(bad, s_bad);
       if (t == 0) *a.s.qflag = bad ? 0 : 1;
     }
-    td = -block_min<256>(-td, s_bad);  // at most one entry holds the draft
+    td = -block_min<QPT>(-td, s_bad);  // at most one entry holds the draft
     QStat q{-INFINITY, -1, 0.0};
     if (live) {
       mx = wave_max_f(mx);
       if ((t & (WAVE - 1)) == 0) s_m[t / WAVE] = mx;
       __syncthreads();
-      mx = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+      mx = s_m[0];
+#pragma unroll
+      for (int q = 1; q < QPT / WAVE; ++q) mx = fmaxf(mx, s_m[q]);
       double z = 0.0;
-      for (int i0 = t; i0 < Vd; i0 += QB * 256) {
+      for (int i0 = t; i0 < Vd; i0 += QB * QPT) {
         float v[QB];
 #pragma unroll
-        for (int q = 0; q < QB; ++q) v[q] = ld(i0 + q * 256 < Vd ? i0 + q * 256 : 0);
+        for (int q = 0; q < QB; ++q) v[q] = ld(i0 + q * QPT < Vd ? i0 + q * QPT : 0);
 #pragma unroll
         for (int q = 0; q < QB; ++q)
-          if (i0 + q * 256 < Vd) z += exp((double)(v[q] / T) - (double)mx);
+          if (i0 + q * QPT < Vd) z += exp((double)(v[q] / T) - (double)mx);
       }
-      z = block_sum_f64<256>(z, s_d);
+      z = block_sum_f64<QPT>(z, s_d);
       q.mq = mx;
       q.Z = z;
       q.td = td;
@@ -973,7 +975,7 @@ __global__ __launch_bounds__(256) void k_qprep(Args a) {
     if (t == 0) a.s.qst[blk] = q;
     return;
   }
-  const int i = (blk - nq) * 256 + t;
+  const int i = (blk - nq) * QPT + t;
   if (i >= Vd) return;
   const int words = (a.V + 31) / 32;
   const int id = a.dtable[i];
