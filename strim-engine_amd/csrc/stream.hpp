@@ -26,8 +26,8 @@ constexpr int stpb() { return CHUNK / (EPT * SSEG); }
 template <bool PEN>
 struct StreamShared {
   uint32_t cnt[PEN ? CHUNK : 4];  // history counts of the chunk's tokens (16 KB)
-  uint32_t hc[NCB];
-  unsigned long long hm[NCB];
+  uint32_t hc[SMAXW][NCB];            // general rows: per-wave coarse histograms (one copy
+  unsigned long long hm[SMAXW][NCB];  // per wave spreads the atomics' contention)
   uint32_t lad[2 * WAVE];
   float v[SMAXW];
   int i[SMAXW], n[SMAXW], f[SMAXW];
@@ -199,10 +199,11 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   const bool topk = p.top_k > 0 && p.top_k < a.V;
   if (fast && topk)
     for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
-  if (p.cls == CLS_GENERAL && t < NCB) {
-    S.hc[t] = 0u;
-    S.hm[t] = 0ull;
-  }
+  if (p.cls == CLS_GENERAL)
+    for (int q = t; q < NW * NCB; q += STPB) {
+      S.hc[q / NCB][q % NCB] = 0u;
+      S.hm[q / NCB][q % NCB] = 0ull;
+    }
   if (pen) hist_count<STPB, CHUNK>(a, b, j, c0, hid, hl, S.cnt);
 
   // ---- penalties and mask, before temperature ("v space") ------------------------
@@ -390,9 +391,10 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       }
     }
     cs_ncand = tot <= SLOT ? (uint32_t)tot : 0xFFFFFFFFu;
-  } else if (p.cls == CLS_GENERAL && live) {
+  } else if (p.cls == CLS_GENERAL && live && !(a.dlog && a.verify && j < a.k)) {
     // processed logits; chunk sum exp(l - m_w) and a coarse histogram of m_w - l
-    // (k_collect's bounds)
+    // (k_collect's bounds). General-q draft rows skip this: their draw makes its own
+    // passes (qres_kernels.hip, exact.hpp).
     float (&l)[SSEG][EPT] = v;  // v is not needed after this
 #pragma unroll
     for (int s = 0; s < SSEG; ++s)
@@ -410,9 +412,9 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         const float wgt = expf(-d);
         ssum += (double)wgt;
         const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
-        atomicAdd(&S.hc[bb], 1u);
+        atomicAdd(&S.hc[w][bb], 1u);
         const unsigned long long fx = __float2ull_rn(wgt * FIX_SCALE_F);
-        if (fx) atomicAdd(&S.hm[bb], fx);
+        if (fx) atomicAdd(&S.hm[w][bb], fx);
       }
     cs.S = block_sum_f64<STPB>(ssum, S.d);
     na = wave_sum(na);
@@ -422,9 +424,16 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
 #pragma unroll
     for (int q = 0; q < NW; ++q) cs.n += S.n[q];
     if (t < NCB) {
+      uint32_t hc = 0u;
+      unsigned long long hm = 0ull;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        hc += S.hc[q][t];
+        hm += S.hm[q][t];
+      }
       const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
-      a.s.chc[o] = S.hc[t];
-      a.s.chm[o] = S.hm[t];
+      a.s.chc[o] = hc;
+      a.s.chm[o] = hm;
     }
     // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
     if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) {
