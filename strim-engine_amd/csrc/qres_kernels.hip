@@ -342,6 +342,22 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   const uint64_t pkey = mix64(p.seed, p.position);
   const XQ q = q_of_row(a, qr);
   const int i0 = c * CHUNK + t * EPT;
+  // the thread's 8 uniforms (two Philox blocks: i0 is a multiple of 8) and its table
+  // membership bits (one 32-id word)
+  float u[EPT];
+  if (a.noise) {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      u[e] = a.noise[(int64_t)r * a.noise_stride + (i0 + e < a.V ? i0 + e : 0)];
+  } else {
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const uint4 wb = philox_block(pkey, (uint64_t)((i0 >> 2) + hb));
+      u[4 * hb] = u01(wb.x); u[4 * hb + 1] = u01(wb.y);
+      u[4 * hb + 2] = u01(wb.z); u[4 * hb + 3] = u01(wb.w);
+    }
+  }
+  const uint32_t qbits = q.dbits[(i0 < a.V ? i0 : 0) >> 5] >> (i0 & 31);
   double bsc = -INFINITY;
   int bid = -1;
 #pragma unroll
@@ -349,16 +365,16 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
     if (!(l[e] > -INFINITY)) continue;
     const int id = i0 + e;
     double base = no_lse ? (double)l[e] : ((double)l[e] - (double)m) - lse;
-    const double qq = xq_prob(q, id);
-    if (qq != 0.0) {
-      // residual score: log(p - q), excluded where p <= q
-      const double rr = exp(base) - qq;
-      if (!(rr > 0.0)) continue;
-      base = log(rr);
+    if ((qbits >> e) & 1u) {
+      const double qq = exp((double)q.vq[id] - (double)q.mq) / q.Z;
+      if (qq != 0.0) {
+        // residual score: log(p - q), excluded where p <= q
+        const double rr = exp(base) - qq;
+        if (!(rr > 0.0)) continue;
+        base = log(rr);
+      }
     }
-    const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
-                            : philox_uniform(pkey, (uint64_t)id);
-    q_take(bsc, bid, base + gumbel64(u), id);
+    q_take(bsc, bid, base + gumbel64(u[e]), id);
   }
   q_wave_best(bsc, bid);
   if (lane == 0) {
