@@ -2,9 +2,9 @@
 // (k_probs) and the verify combine.
 //
 // General rows (top-p alone, no filter, very small min-p, large top-k) cannot bound their
-// candidates from a chunk's own maximum. k_collect derives conservative bin bounds from
-// k_stream's 64-bin coarse histograms, collects the tokens of the undecided bins and sums
-// the rest exactly; k_final sorts the candidates in LDS by (l desc, id asc) and takes every
+// candidates from a chunk's own maximum. k_finalize derives conservative bin bounds from
+// k_stream's 64-bin coarse histograms once per row (general.hpp); k_collect collects the
+// tokens of the undecided bins and sums the rest exactly; k_final sorts the candidates in LDS by (l desc, id asc) and takes every
 // decision in fp64. Rows whose candidates overflow either finalize are decided by k_final's
 // exact streaming resolution.
 #include "exact.hpp"
@@ -23,204 +23,8 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
 // ---------------------------------------------------------------------------------
 // k_collect: general rows
 // ---------------------------------------------------------------------------------
-// First g in [lo, hi] with pred(g), hi + 1 if none, for a predicate monotone in g
-// (false ... false true ... true). One wave: lane l tests bins l, l + 64, l + 128.
-static_assert(NGB <= 3 * WAVE, "three bins per lane");
-template <typename F>
-__device__ __forceinline__ int first_true(int lo, int hi, F pred) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  int res = hi + 1;
-#pragma unroll
-  for (int k = 2; k >= 0; --k) {
-    const int g = lane + k * WAVE;
-    const uint64_t bal = __ballot(g >= lo && g <= hi && g < NGB && pred(g));
-    if (bal) res = k * WAVE + (int)__ffsll((long long)bal) - 1;
-  }
-  return res;
-}
-
-// Row statistics merged from the chunk statistics, identically in every workgroup.
-struct RowStats {
-  float m;
-  int32_t arg;
-  int32_t n;
-  int32_t flags;
-};
-
-template <int NT>
-__device__ __forceinline__ RowStats merge_chunks(const Args& a, int r, float* sv, int* si,
-                                                 int* sn, int* sf) {
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
-  float bv = -INFINITY;
-  int bi = -1, bn = 0, bf = 0;
-  for (int cc = t; cc < a.W; cc += NT) {
-    const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + cc];
-    argmax_merge(bv, bi, cs.m, cs.arg);
-    bn += cs.n;
-    bf |= cs.flags;
-  }
-  wave_argmax(bv, bi);
-  bn = wave_sum(bn);
-  bf = wave_or_i(bf);
-  if (lane == 0) {
-    sv[w] = bv;
-    si[w] = bi;
-    sn[w] = bn;
-    sf[w] = bf;
-  }
-  __syncthreads();
-  RowStats rs{sv[0], si[0], sn[0], sf[0]};
-  for (int q = 1; q < NT / WAVE; ++q) {
-    argmax_merge(rs.m, rs.arg, sv[q], si[q]);
-    rs.n += sn[q];
-    rs.flags |= sf[q];
-  }
-  __syncthreads();
-  return rs;
-}
-
-// Conservative bin bounds of a general row from the coarse chunk histograms
-// (one wave, every lane computing the same scalars; the same arithmetic in every
-// workgroup of the row gives the same result).
-// cU/cL: cumulative fixed-point mass with each chunk bin placed at its earliest /
-// latest possible global bin; kU/kL: the same for counts.
-__device__ void compute_bounds(const Args& a, int r, const RowParams& p, float m, uint32_t N,
-                               const unsigned long long* cU, const unsigned long long* cL,
-                               const uint32_t* kU, const uint32_t* kL, Bounds& out) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  Bounds bd;  // built in registers (uniform), stored by lane 0
-  const double inv = 1.0 / FIX_SCALE, EPS = 1e-5;
-  const double SLACK = (double)(a.W * NCB + 16) * 4.0 * inv;
-  auto MU = [&](int g) { return g < 0 ? 0.0 : (double)cU[g] * inv * (1.0 + EPS) + SLACK; };
-  auto ML = [&](int g) { return g < 0 ? 0.0 : (double)cL[g] * inv * (1.0 - EPS) - SLACK; };
-  int s1 = NGB, e1 = NGB - 1;
-  if (p.min_p > 0.0f) {
-    const double thr = -p.lmp;
-    const int gt = thr < 63.0 ? (int)(thr * (double)CB_SCALE) : NGB - 1;
-    s1 = min(s1, max(0, gt - 1));
-    e1 = min(e1, min(NGB - 1, gt + 1));
-  }
-  const bool topk = p.top_k > 0 && p.top_k < a.V;
-  if (topk && N > (uint32_t)p.top_k) {
-    const uint32_t K = (uint32_t)p.top_k;
-    const int glo = first_true(0, NGB - 1, [&](int g) { return kU[g] >= K; });
-    const int ghi = first_true(0, NGB - 1, [&](int g) { return kL[g] >= K; });
-    s1 = min(s1, glo);
-    e1 = min(e1, ghi);
-  }
-  int s = s1, e = e1;
-  const bool topp = p.top_p < 1.0f;
-  if (topp) {
-    const double P = (double)p.top_p;
-    const double hi = MU(e1), lo = ML(s1 - 1);
-    const int lim = min(e1, s1 - 1);
-    int ep = e1;
-    if (lim >= 0) {
-      const int f = first_true(0, lim, [&](int g) { return ML(g) > P * hi; });
-      if (f <= lim) ep = f;
-    }
-    const int sp = first_true(0, NGB - 1, [&](int g) { return MU(g) > P * lo; });
-    e = min(e1, ep);
-    s = min(s1, sp);
-  }
-  if (s > e + 1) s = e + 1;
-  const bool icdf = a.noise_mode == STRIM_NOISE_ICDF;
-  const bool by_rank = (p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp;
-  for (int q = 0; q < 3; ++q) { bd.rng[q][0] = 1; bd.rng[q][1] = 0; }
-  int mode;
-  if (kU[e1] <= (uint32_t)CAP) {
-    mode = MODE_A;  // everything possibly pre-kept is collected
-    bd.rng[0][0] = 0;
-    bd.rng[0][1] = e1;
-    s = 0;
-  } else if (by_rank) {
-    mode = MODE_NONE;
-  } else {
-    mode = MODE_B;
-    bd.rng[0][0] = s;
-    bd.rng[0][1] = e;
-    if (s1 <= e1) { bd.rng[1][0] = s1; bd.rng[1][1] = e1; }
-    if (icdf) {
-      const double u = (double)row_uniform(a, r, p, 0);
-      double wd = 0.0;
-      if (a.verify) {
-        int bb, jj;
-        row_bj(a, r, bb, jj);
-        const float ld = a.s.rs[r].l_draft;
-        if (jj < a.k && ld > -INFINITY) wd = exp((double)ld - (double)m);
-      }
-      const double tlo = u * (ML(s - 1) - wd) - SLACK;
-      const double thi = u * MU(e) + wd + SLACK;
-      const int dlo = first_true(0, NGB - 1, [&](int g) { return MU(g) > tlo; });
-      int dhi = first_true(0, NGB - 1, [&](int g) { return ML(g) > thi; });
-      dhi = min(dhi, e);
-      bd.rng[2][0] = dlo;
-      bd.rng[2][1] = dhi;
-    }
-    // upper bound of the tokens in the collected bins: per contiguous run [lo, hi],
-    // kU[hi] - kL[lo - 1] (never negative: kU >= kL bin by bin, and both are cumulative)
-    uint32_t part = 0u;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      const int g = lane + k * WAVE;
-      if (g >= NGB || !in_rng(bd, g)) continue;
-      if (g + 1 >= NGB || !in_rng(bd, g + 1)) part += kU[g];
-      if (g > 0 && !in_rng(bd, g - 1)) part -= kL[g - 1];
-    }
-    const uint32_t total = (uint32_t)wave_sum((int)part);
-    if (total > (uint32_t)CAP) mode = MODE_NONE;
-  }
-  // non-collected intervals, split where the kept / pre-kept classification changes
-  // (a new interval starts after a collected bin and at s and s1); more than NSEG
-  // intervals leave the row to the exact resolution
-  for (int q = 0; q < NSEG; ++q) { bd.seg_lo[q] = 1; bd.seg_hi[q] = 0; }
-  if (mode != MODE_NONE) {
-    uint64_t stm[3], enm[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      const int g = lane + k * WAVE;
-      const bool out_g = g < NGB && !in_rng(bd, g);
-      stm[k] = __ballot(out_g && (g == 0 || in_rng(bd, g - 1) || g == s || g == s1));
-      enm[k] = __ballot(out_g && (g == NGB - 1 || in_rng(bd, g + 1) || g + 1 == s || g + 1 == s1));
-    }
-    // the q-th start and the q-th end delimit interval q (they alternate bin by bin)
-    int q = 0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      uint64_t ms = stm[k];
-      while (ms) {
-        if (q < NSEG) bd.seg_lo[q] = k * WAVE + (int)__ffsll((long long)ms) - 1;
-        ms &= ms - 1ull;
-        ++q;
-      }
-    }
-    if (q > NSEG) mode = MODE_NONE;
-    q = 0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      uint64_t me = enm[k];
-      while (me) {
-        if (q < NSEG) bd.seg_hi[q] = k * WAVE + (int)__ffsll((long long)me) - 1;
-        me &= me - 1ull;
-        ++q;
-      }
-    }
-  }
-  bd.mode = mode;
-  bd.s = s;
-  bd.e = e;
-  bd.s1 = s1;
-  bd.e1 = e1;
-  if (lane == 0) out = bd;
-}
-
 __global__ __launch_bounds__(TPB) void k_collect(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
-  __shared__ unsigned long long s_U[NGB], s_L[NGB];
-  __shared__ uint32_t s_kU[NGB], s_kL[NGB];
-  __shared__ Bounds s_bd;
-  __shared__ float s_v[TPB / WAVE];
-  __shared__ int s_i[TPB / WAVE], s_n[TPB / WAVE], s_f[TPB / WAVE];
   __shared__ unsigned long long s_sm[TPB / WAVE][NSEG];
   __shared__ uint32_t s_sc[TPB / WAVE][NSEG];
   __shared__ float s_tf[4 * TPB / WAVE];
@@ -239,93 +43,11 @@ __global__ __launch_bounds__(TPB) void k_collect(Args a) {
 
   float x[EPT];
   load_tokens(a, r, i0, x);
-  const RowStats st = merge_chunks<TPB>(a, r, s_v, s_i, s_n, s_f);
-  if (st.n == 0 || st.flags) return;  // k_final reports the row status
-  const float m = st.m;
-
-  // global coarse bounds: each chunk bin lands in [g_lo, g_hi] of the global bins
-  for (int g = t; g < NGB; g += TPB) {
-    s_U[g] = 0ull; s_L[g] = 0ull; s_kU[g] = 0u; s_kL[g] = 0u;
-  }
-  __syncthreads();
-  // (batches of loads from clamped indices with no branch between them)
-  constexpr int BB = 8;
-  const int nbin = a.W * NCB;
-  for (int e0 = t; e0 < nbin; e0 += BB * TPB) {
-    uint32_t cn[BB];
-    unsigned long long hm[BB];
-    float mw[BB];
-#pragma unroll
-    for (int q = 0; q < BB; ++q) {
-      const int e = e0 + q * TPB < nbin ? e0 + q * TPB : 0;
-      const int cc = e / NCB;
-      const int64_t o = ((int64_t)r * a.s.wmax + cc) * NCB + (e - cc * NCB);
-      cn[q] = a.s.chc[o];
-      hm[q] = a.s.chm[o];
-      mw[q] = a.s.cstat[(int64_t)r * a.s.wmax + cc].m;
-    }
-#pragma unroll
-    for (int q = 0; q < BB; ++q) {
-      const int e = e0 + q * TPB;
-      if (e >= nbin || !cn[q]) continue;
-      const int cc = e / NCB, bb = e - cc * NCB;
-      const double dlt = (double)m - (double)mw[q];
-      const double lo = (dlt + 0.5 * bb) * (1.0 - 2e-6) * CB_SCALE;
-      const double hi = bb == NCB - 1 ? 1e300 : (dlt + 0.5 * (bb + 1)) * (1.0 + 2e-6) * CB_SCALE;
-      const int glo = lo < (double)(NGB - 1) ? max(0, (int)floor(lo)) : NGB - 1;
-      const int ghi = hi < (double)(NGB - 1) ? max(0, (int)floor(hi)) : NGB - 1;
-      const double ms = (double)hm[q] * exp(-dlt);
-      atomicAdd(&s_U[glo], (unsigned long long)(ms + 1.0));
-      atomicAdd(&s_L[ghi], (unsigned long long)ms);
-      atomicAdd(&s_kU[glo], cn[q]);
-      atomicAdd(&s_kL[ghi], cn[q]);
-    }
-  }
-  if (p.pen) build_counts(a, b, j, c0, s_cnt);
-  else __syncthreads();
-  // inclusive prefixes over the global bins, one array per wave: a lane owns bins
-  // 3 lane .. 3 lane + 2
-  static_assert(NGB <= 3 * WAVE && TPB / WAVE >= 4, "prefix layout");
-  if (w < 4) {
-    const int g0 = 3 * lane;
-    if (w < 2) {
-      unsigned long long* arr = w == 0 ? s_U : s_L;
-      unsigned long long v3[3], own = 0ull;
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        v3[q] = g0 + q < NGB ? arr[g0 + q] : 0ull;
-        own += v3[q];
-      }
-      unsigned long long run = wave_incl_scan_u64(own) - own;
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        run += v3[q];
-        if (g0 + q < NGB) arr[g0 + q] = run;
-      }
-    } else {
-      uint32_t* arr = w == 2 ? s_kU : s_kL;
-      uint32_t v3[3], own = 0u;
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        v3[q] = g0 + q < NGB ? arr[g0 + q] : 0u;
-        own += v3[q];
-      }
-      uint32_t run = wave_incl_scan_u32(own) - own;
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        run += v3[q];
-        if (g0 + q < NGB) arr[g0 + q] = run;
-      }
-    }
-  }
-  __syncthreads();
-  if (w == 0) compute_bounds(a, r, p, m, (uint32_t)st.n, s_U, s_L, s_kU, s_kL, s_bd);
-  if (t == 0) {
-    if (c == 0) a.s.rs[r].bd = s_bd;
-  }
-  __syncthreads();
-  const Bounds bd = s_bd;
+  // the row maximum and the bin bounds, from k_finalize
+  const float m = a.s.rs[r].m;
+  const Bounds bd = a.s.rs[r].bd;
   if (bd.mode == MODE_NONE) return;
+  if (p.pen) build_counts(a, b, j, c0, s_cnt);
 
   float l[EPT];
   bool nf = false;
@@ -411,8 +133,6 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   __shared__ double s_dred[FIN_T / WAVE];
   __shared__ uint64_t s_ured[FIN_T / WAVE];
   __shared__ int s_ired[FIN_T / WAVE];
-  __shared__ float s_v[FIN_T / WAVE];
-  __shared__ int s_i[FIN_T / WAVE], s_n[FIN_T / WAVE], s_f[FIN_T / WAVE];
   __shared__ int s_int[8];
   __shared__ float s_kth;
   __shared__ uint32_t s_pre[256];
@@ -438,15 +158,15 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   const int phase = rsp->phase;
   if (phase == PH_DONE) return;
 
-  const RowStats st = merge_chunks<FIN_T>(a, r, s_v, s_i, s_n, s_f);
+  // k_finalize has checked the row (status, draft) and left its maximum and first argmax
+  const float m = rsp->m;
+  const int arg = rsp->token;
   int status = STRIM_OK;
   int draft = -1;
   if (verify_draft_row) {
     draft = a.drafts[(int64_t)b * a.k + j];
     if (draft < 0 || draft >= V) status = STRIM_EINVAL;
   }
-  if (status == STRIM_OK && st.flags) status = STRIM_ENONFINITE;
-  if (status == STRIM_OK && st.n == 0) status = STRIM_EEMPTY;
   if (status == STRIM_OK && !p.greedy && phase == PH_PENDING) {
     if (t == 0) s_bd = rsp->bd;
     __syncthreads();
@@ -459,7 +179,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
       rsp->token = token;
       rsp->accept = accept;
       rsp->sum_kept = sig;
-      rsp->m = st.m;
+      rsp->m = m;
       rsp->last_key = lk;
       if (!a.verify) {
         a.out_ids[r] = stt == STRIM_OK ? token : -1;
@@ -472,10 +192,9 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     return;
   }
   if (p.greedy) {
-    finish(STRIM_OK, st.arg, verify_draft_row && st.arg == draft, 1.0, 0ull);
+    finish(STRIM_OK, arg, verify_draft_row && arg == draft, 1.0, 0ull);
     return;
   }
-  const float m = st.m;
   const int W = a.W;
   const bool topk = p.top_k > 0 && p.top_k < V;
   const bool topp = p.top_p < 1.0f;
@@ -787,7 +506,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
     xa.q.mq = qs.mq;
     xa.q.Z = qs.Z;
   }
-  const XOut xo = exact_row<FIN_T>(xa, r, b, j, p, st.m, st.arg, draft, verify_draft_row,
+  const XOut xo = exact_row<FIN_T>(xa, r, b, j, p, m, arg, draft, verify_draft_row,
                             verify_draft_row ? rsp->l_draft : -INFINITY, xs, s_x);
   if (t == 0 && phase == PH_PENDING) rsp->bd.mode = MODE_A;  // kept set = order prefix up to last_key
   finish(xo.status, xo.token, xo.accept, xo.sig, xo.last_key);
