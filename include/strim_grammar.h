@@ -1,0 +1,88 @@
+/*
+ * strim_grammar.h — on-device grammar-mask production for the token-selection path.
+ *
+ * The reference builds a token mask on the host: a byte trie over the tokenizer vocabulary
+ * is walked through the grammar's DFA for each state, cached as a bitset per state and
+ * expanded into a bool array per upload (GrammarVocab.swift:3-113,
+ * RequestConstraint.swift:5-60). Here the vocabulary bytes, the DFA transition table and
+ * the per-state mask cache live in HBM. A mask row is produced by one launch straight into
+ * the packed u32 words that strim_sample / strim_verify read (bit i of word w allows token
+ * 32 w + i), and the verify rows' states are stepped by the drafts' bytes on the device.
+ *
+ * Row keys (RequestConstraint.Key, RequestConstraint.swift:65,85-92,113-119):
+ *   key >= 0    grammar state `key`: the tokens whose bytes keep the DFA alive from it,
+ *               when the state consumes, plus the end-of-turn ids when it accepts;
+ *   key == -1   free: every token below width allowed;
+ *   key <= -2   forced: only token (-2 - key) allowed (the thinking-budget close id).
+ * A state at or above the DFA's state count gives an all-zero row, which strim_sample
+ * reports as STRIM_EEMPTY.
+ *
+ * All calls are stream-ordered; keys, tokens and outputs are device memory. Calls on one
+ * strim_grammar that overlap on different streams race on its mask cache only when one of
+ * them is strim_grammar_set_dfa.
+ */
+#ifndef STRIM_GRAMMAR_H
+#define STRIM_GRAMMAR_H
+
+#include <stdint.h>
+
+#include "strim_sampler.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct strim_grammar strim_grammar;
+
+#define STRIM_DFA_ACCEPTING 1 /* flags bit: the state may end (GrammarDFA.accepting)     */
+#define STRIM_DFA_CONSUMING 2 /* flags bit: the state can take bytes (GrammarDFA.consuming) */
+
+/* Uploads the vocabulary (replaces GrammarVocab.init, GrammarVocab.swift:16-51, and the
+ * GrammarEngine construction, GrammarVocab.swift:116-130).
+ *   count       tokens with byte strings; token i has bytes[offsets[i] .. offsets[i+1])
+ *               (host arrays, offsets non-decreasing, offsets[0] = 0)
+ *   skip        host [count] or NULL: nonzero ids never appear in a grammar mask
+ *               (control tokens); empty byte strings never appear either
+ *   width       logits width, the mask's bit count (ids at or above width are dropped)
+ *   eos, n_eos  host end-of-turn ids, allowed in an accepting state's mask
+ *   cache_states  states whose mask rows are cached in HBM (width / 8 bytes each);
+ *               states at or above it are produced on every call
+ * The DFA is empty until strim_grammar_set_dfa. */
+int strim_grammar_create(strim_grammar** out, int32_t device, int32_t count,
+                         const uint32_t* offsets, const uint8_t* bytes, const uint8_t* skip,
+                         int32_t width, const int32_t* eos, int32_t n_eos,
+                         int32_t cache_states);
+int strim_grammar_destroy(strim_grammar* g);
+
+/* Installs a DFA (replaces the compiled GrammarDFA of GrammarRuntime.init,
+ * GrammarVocab.swift:57-69, GrammarDFA.swift:13-58) and clears the mask cache.
+ *   next   host [n_states][256]: the state after byte b, -1 = dead. Every entry must be
+ *          materialised (the reference's lazily expanded -2 entries are rejected)
+ *   flags  host [n_states]: STRIM_DFA_ACCEPTING | STRIM_DFA_CONSUMING
+ * Returns STRIM_EINVAL for an entry outside [-1, n_states). */
+int strim_grammar_set_dfa(strim_grammar* g, void* stream, int32_t n_states,
+                          const int32_t* next, const uint8_t* flags);
+
+/* Mask rows for n keys (replaces GrammarRuntime.mask, GrammarVocab.swift:75-102, and
+ * DeviceMasks.allowed / only / all with their bool expansion,
+ * RequestConstraint.swift:16-58): out[r][0 .. ceil(width / 32)) packed words, out_stride
+ * words apart. keys device [n]. */
+int strim_grammar_masks(strim_grammar* g, void* stream, const int32_t* keys, int32_t n,
+                        uint32_t* out, int64_t out_stride);
+
+/* Verify-row keys (replaces RequestConstraint.verifyMask's key walk and
+ * GrammarRuntime.advance, RequestConstraint.swift:94-102,134-145,
+ * GrammarVocab.swift:107-112). For request b, keys_out[b][0] = key(state[b]) and
+ * keys_out[b][i + 1] is the key after tokens[b][0 .. i]: each token's bytes step the
+ * state; a step to dead makes that row and every later row free (-1). Free and forced
+ * keys are left as they are (the thinking phase is the caller's). Ids outside
+ * [0, count) have no bytes and leave the state unchanged. state device [B] (keys),
+ * tokens device [B][k], keys_out device [B][k + 1]. */
+int strim_grammar_advance(strim_grammar* g, void* stream, const int32_t* state, int32_t B,
+                          const int32_t* tokens, int32_t k, int32_t* keys_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRIM_GRAMMAR_H */

@@ -112,6 +112,15 @@ def lib():
         L.so_sample_batch.argtypes = [P, I32, I32, P, P, I64, P, P, I32, I32, P, P, P, I32]
         L.so_verify_batch.argtypes = [P, I32, I32, I32, P, I32, P, P, P, P, I64, P, P, I32, I32,
                                       P, P, P, P, P, P, P, P, I32]
+        L.so_trie_build.restype = P
+        L.so_trie_build.argtypes = [I32, P, P, P]
+        L.so_trie_free.argtypes = [P]
+        L.so_trie_nodes.restype = I32
+        L.so_trie_nodes.argtypes = [P]
+        L.so_grammar_mask.argtypes = [P, I32, P, I32, I32, P, P, I32, P]
+        L.so_grammar_advance_bytes.restype = I32
+        L.so_grammar_advance_bytes.argtypes = [I32, P, ctypes.c_uint32, P]
+        L.so_grammar_verify_keys.argtypes = [I32, P, P, I32, P, P, I32, P, I32, P]
         _lib = L
     return _lib
 
@@ -247,3 +256,59 @@ def bf16_bits(x_f32_bf16exact: np.ndarray) -> np.ndarray:
 
 if __name__ == "__main__":  # pragma: no cover
     print(os.fspath(build(force=True)))
+
+
+# ---------------------------------------------------------------------------------
+# grammar masks (oracle/grammar_oracle.c)
+# ---------------------------------------------------------------------------------
+class GrammarOracle:
+    """The reference's host mask production (GrammarVocab.swift:16-112) over a vocabulary
+    given as byte strings; masks are packed u32 words like strim_grammar_masks."""
+
+    def __init__(self, tokens, width: int, eos=(), skip=None):
+        self.count = len(tokens)
+        lens = np.array([len(t) for t in tokens], dtype=np.int64)
+        self.offsets = np.zeros(self.count + 1, dtype=np.uint32)
+        self.offsets[1:] = np.cumsum(lens)
+        self.bytes = np.frombuffer(b"".join(bytes(t) for t in tokens) + b"\0", dtype=np.uint8).copy()
+        self.skip = None if skip is None else np.ascontiguousarray(skip, dtype=np.uint8)
+        self.width = int(width)
+        self.eos = np.ascontiguousarray(eos, dtype=np.int32)
+        self._trie = lib().so_trie_build(self.count, _ptr(self.offsets), _ptr(self.bytes),
+                                         _ptr(self.skip))
+        self.next = None
+        self.flags = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        if getattr(self, "_trie", None):
+            lib().so_trie_free(self._trie)
+            self._trie = None
+
+    def nodes(self) -> int:
+        return int(lib().so_trie_nodes(self._trie))
+
+    def set_dfa(self, next_table, flags):
+        self.next = np.ascontiguousarray(next_table, dtype=np.int32)
+        self.flags = np.ascontiguousarray(flags, dtype=np.uint8)
+
+    def mask(self, key: int) -> np.ndarray:
+        out = np.zeros((self.width + 31) // 32, dtype=np.uint32)
+        lib().so_grammar_mask(self._trie, self.width, _ptr(self.eos), len(self.eos),
+                              len(self.flags), _ptr(self.next), _ptr(self.flags), int(key),
+                              _ptr(out))
+        return out
+
+    def advance(self, state: int, token_bytes: bytes) -> int:
+        b = np.frombuffer(bytes(token_bytes) + b"\0", dtype=np.uint8).copy()
+        return int(lib().so_grammar_advance_bytes(int(state), _ptr(b), len(token_bytes),
+                                                  _ptr(self.next)))
+
+    def verify_keys(self, state, tokens) -> np.ndarray:
+        st = np.ascontiguousarray(state, dtype=np.int32)
+        tk = np.ascontiguousarray(tokens, dtype=np.int32).reshape(len(st), -1)
+        k = tk.shape[1]
+        out = np.zeros((len(st), k + 1), dtype=np.int32)
+        lib().so_grammar_verify_keys(self.count, _ptr(self.offsets), _ptr(self.bytes),
+                                     len(self.flags), _ptr(self.next), _ptr(st), len(st),
+                                     _ptr(tk), k, _ptr(out))
+        return out

@@ -32,6 +32,7 @@ UNITS = [
     ("sample_kernels.hip", []),
     ("qres_kernels.hip", []),
     ("aux_kernels.hip", []),
+    ("grammar_kernels.hip", []),
     ("capi.hip", []),
 ]
 

@@ -1,0 +1,338 @@
+// grammar_kernels.hip — on-device grammar masks (include/strim_grammar.h).
+//
+// The reference walks a byte trie of the vocabulary through the grammar DFA on the host,
+// once per new state, and uploads a bool row per use (GrammarVocab.swift:75-102,
+// RequestConstraint.swift:16-43). Here a mask row is one launch: every thread takes one
+// token and steps the DFA by the token's bytes (a token is allowed iff no step reaches the
+// dead state, which is what the trie walk decides for every token below a live trie
+// path); a wave ballot packs 64 decisions into the two u32 words that k_stream reads.
+// Produced blocks of a cached state are kept in HBM, so a state seen before costs a copy.
+//
+// HBM layout of a strim_grammar:
+//   head   [count] uint4      the first 16 bytes of each token, zero padded
+//   meta   [count] uint2      {offset of the token's bytes, length | eligible << 31}
+//   bytes  [total] u8         every token's bytes (read past the first 16)
+//   eosw   [words] u32        end-of-turn ids as mask words
+//   next   [n_states][256] i32, flags [n_states] u8   the DFA
+//   cache  [cache_states][words] u32, ready [cache_states][nblk] u32
+#include <stdlib.h>
+#include <string.h>
+
+#include "common.hpp"
+#include "../../include/strim_grammar.h"
+
+namespace strim {
+
+constexpr int GM_T = 256;              // tokens per k_gmask workgroup
+constexpr int GM_W = GM_T / 32;        // mask words per workgroup
+constexpr int GM_HEAD = 16;            // bytes held in a token's head
+
+struct GView {
+  const uint4* head;
+  const uint2* meta;
+  const uint8_t* bytes;
+  const uint32_t* eosw;
+  const int32_t* next;
+  const uint8_t* flags;
+  uint32_t* cache;
+  uint32_t* ready;
+  int32_t count, width, words, nblk, cache_states, n_states;
+};
+
+// The state after token `id`'s bytes from live state s (-1 = dead). The first 16 bytes
+// come from the head in registers; longer tokens continue from the byte array.
+__device__ __forceinline__ int walk_token(const GView& g, int s, uint4 h, uint32_t off,
+                                          uint32_t len) {
+  const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+  int st = s;
+#pragma unroll
+  for (int i = 0; i < GM_HEAD; ++i) {
+    if ((uint32_t)i < len && st >= 0) {
+      const uint32_t b = (hw[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      st = g.next[(int64_t)st * 256 + b];
+    }
+  }
+  for (uint32_t i = GM_HEAD; i < len && st >= 0; ++i)
+    st = g.next[(int64_t)st * 256 + g.bytes[off + i]];
+  return st;
+}
+
+// Grid (nblk, n): workgroup (blk, r) produces mask words blk * 8 .. blk * 8 + 7 of row r.
+__global__ __launch_bounds__(GM_T) void k_gmask(GView g, const int32_t* keys, uint32_t* out,
+                                                int64_t out_stride) {
+  __shared__ uint32_t s_hit;
+  const int blk = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+  const int lane = t & (WAVE - 1), w = t / WAVE;
+  const int id = blk * GM_T + t;
+  const int key = keys[r];
+  uint32_t* orow = out + (int64_t)r * out_stride;
+  const int wi = blk * GM_W + 2 * w + (lane & 1);  // the word lanes 0 / 1 write
+  const bool writer = lane < 2 && wi < g.words;
+  const bool grammar = key >= 0 && key < g.n_states;
+  const bool cached = grammar && key < g.cache_states;
+  if (cached) {
+    if (t == 0)
+      s_hit = __hip_atomic_load(&g.ready[(int64_t)key * g.nblk + blk], __ATOMIC_ACQUIRE,
+                                __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_hit) {
+      if (writer) orow[wi] = g.cache[(int64_t)key * g.words + wi];
+      return;
+    }
+  }
+  bool ok;
+  uint32_t extra = 0u;
+  if (key == -1) {
+    ok = id < g.width;
+  } else if (key < -1) {
+    ok = id == -2 - key && id < g.width;
+  } else if (!grammar) {
+    ok = false;
+  } else {
+    const uint32_t f = g.flags[key];
+    ok = false;
+    if ((f & STRIM_DFA_CONSUMING) && id < g.count && id < g.width) {
+      const uint2 m = g.meta[id];
+      if (m.y >> 31) ok = walk_token(g, key, g.head[id], m.x, m.y & 0x7FFFFFFFu) >= 0;
+    }
+    if ((f & STRIM_DFA_ACCEPTING) && writer) extra = g.eosw[wi];
+  }
+  const uint64_t bal = __ballot(ok);
+  if (writer) {
+    const uint32_t word = (lane == 0 ? (uint32_t)bal : (uint32_t)(bal >> 32)) | extra;
+    orow[wi] = word;
+    if (cached) g.cache[(int64_t)key * g.words + wi] = word;
+  }
+  if (cached) {
+    __syncthreads();
+    if (t == 0) {
+      __threadfence();
+      __hip_atomic_store(&g.ready[(int64_t)key * g.nblk + blk], 1u, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// One thread per request: the keys of its k + 1 verify rows.
+__global__ void k_gadvance(GView g, const int32_t* state, int B, const int32_t* tokens, int k,
+                           int32_t* keys_out) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  int s = state[b];
+  int32_t* o = keys_out + (int64_t)b * (k + 1);
+  o[0] = s;
+  for (int i = 0; i < k; ++i) {
+    if (s >= 0 && s < g.n_states) {
+      const int d = tokens[(int64_t)b * k + i];
+      if (d >= 0 && d < g.count) {
+        const uint2 m = g.meta[d];
+        s = walk_token(g, s, g.head[d], m.x, m.y & 0x7FFFFFFFu);  // dead: -1 = free
+      }
+    }
+    o[i + 1] = s;
+  }
+}
+
+__global__ void k_gclear(uint32_t* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+}  // namespace strim
+
+using namespace strim;
+
+struct strim_grammar {
+  int32_t device = 0;
+  int32_t count = 0, width = 0, words = 0, nblk = 0, cache_states = 0, n_states = 0;
+  void* base = nullptr;  // vocabulary, end-of-turn words, cache, ready flags
+  int32_t* next = nullptr;
+  uint8_t* flags = nullptr;
+  uint4* head = nullptr;
+  uint2* meta = nullptr;
+  uint8_t* bytes = nullptr;
+  uint32_t* eosw = nullptr;
+  uint32_t* cache = nullptr;
+  uint32_t* ready = nullptr;
+};
+
+namespace {
+
+template <typename F>
+int g_on_device(int32_t device, F fn) {
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return STRIM_EHIP;
+  if (cur != device && hipSetDevice(device) != hipSuccess) return STRIM_EHIP;
+  const int rc = fn();
+  if (cur != device) (void)hipSetDevice(cur);
+  return rc;
+}
+
+size_t g_align(size_t x) { return (x + 255) / 256 * 256; }
+
+GView view(const strim_grammar* g) {
+  return GView{g->head, g->meta, g->bytes, g->eosw, g->next, g->flags, g->cache, g->ready,
+               g->count, g->width, g->words, g->nblk, g->cache_states, g->n_states};
+}
+
+int g_status() { return hipGetLastError() == hipSuccess ? STRIM_OK : STRIM_EHIP; }
+
+}  // namespace
+
+extern "C" {
+
+int strim_grammar_create(strim_grammar** out, int32_t device, int32_t count,
+                         const uint32_t* offsets, const uint8_t* bytes, const uint8_t* skip,
+                         int32_t width, const int32_t* eos, int32_t n_eos,
+                         int32_t cache_states) {
+  if (!out) return STRIM_EINVAL;
+  *out = nullptr;
+  if (count <= 0 || !offsets || width <= 0 || n_eos < 0 || (n_eos > 0 && !eos) ||
+      cache_states < 0 || offsets[0] != 0u)
+    return STRIM_EINVAL;
+  for (int32_t i = 0; i < count; ++i)
+    if (offsets[i + 1] < offsets[i]) return STRIM_EINVAL;
+  const uint32_t total = offsets[count];
+  if (total > 0 && !bytes) return STRIM_EINVAL;
+  for (int32_t e = 0; e < n_eos; ++e)
+    if (eos[e] < 0) return STRIM_EINVAL;
+  const int32_t words = (width + 31) / 32;
+  const int32_t nblk = (width + GM_T - 1) / GM_T;
+  // host staging of the device layout
+  uint4* h_head = (uint4*)calloc((size_t)count, sizeof(uint4));
+  uint2* h_meta = (uint2*)calloc((size_t)count, sizeof(uint2));
+  uint32_t* h_eosw = (uint32_t*)calloc((size_t)words, sizeof(uint32_t));
+  if (!h_head || !h_meta || !h_eosw) {
+    free(h_head); free(h_meta); free(h_eosw);
+    return STRIM_ENOMEM;
+  }
+  for (int32_t i = 0; i < count; ++i) {
+    const uint32_t o = offsets[i], len = offsets[i + 1] - o;
+    uint8_t hb[16] = {0};
+    if (len) memcpy(hb, bytes + o, len < 16u ? len : 16u);
+    memcpy(&h_head[i], hb, 16);
+    const bool elig = len > 0 && !(skip && skip[i]);
+    h_meta[i] = make_uint2(o, (len & 0x7FFFFFFFu) | (elig ? 0x80000000u : 0u));
+  }
+  for (int32_t e = 0; e < n_eos; ++e)
+    if (eos[e] < width) h_eosw[eos[e] >> 5] |= 1u << (eos[e] & 31);
+
+  strim_grammar* g = new strim_grammar();
+  g->device = device;
+  g->count = count;
+  g->width = width;
+  g->words = words;
+  g->nblk = nblk;
+  g->cache_states = cache_states;
+  const size_t o_head = 0;
+  const size_t o_meta = g_align(o_head + (size_t)count * sizeof(uint4));
+  const size_t o_bytes = g_align(o_meta + (size_t)count * sizeof(uint2));
+  const size_t o_eos = g_align(o_bytes + (size_t)total + 16);
+  const size_t o_cache = g_align(o_eos + (size_t)words * 4);
+  const size_t o_ready = g_align(o_cache + (size_t)cache_states * words * 4);
+  const size_t size = g_align(o_ready + (size_t)cache_states * nblk * 4);
+  const int rc = g_on_device(device, [&]() -> int {
+    if (hipMalloc(&g->base, size) != hipSuccess) {
+      g->base = nullptr;
+      return STRIM_ENOMEM;
+    }
+    char* p = (char*)g->base;
+    g->head = (uint4*)(p + o_head);
+    g->meta = (uint2*)(p + o_meta);
+    g->bytes = (uint8_t*)(p + o_bytes);
+    g->eosw = (uint32_t*)(p + o_eos);
+    g->cache = (uint32_t*)(p + o_cache);
+    g->ready = (uint32_t*)(p + o_ready);
+    if (hipMemcpy(g->head, h_head, (size_t)count * sizeof(uint4), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g->meta, h_meta, (size_t)count * sizeof(uint2), hipMemcpyHostToDevice) != hipSuccess ||
+        (total > 0 && hipMemcpy(g->bytes, bytes, total, hipMemcpyHostToDevice) != hipSuccess) ||
+        hipMemcpy(g->eosw, h_eosw, (size_t)words * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(g->ready, 0, (size_t)cache_states * nblk * 4) != hipSuccess)
+      return STRIM_EHIP;
+    return STRIM_OK;
+  });
+  free(h_head);
+  free(h_meta);
+  free(h_eosw);
+  if (rc != STRIM_OK) {
+    strim_grammar_destroy(g);
+    return rc;
+  }
+  *out = g;
+  return STRIM_OK;
+}
+
+int strim_grammar_destroy(strim_grammar* g) {
+  if (!g) return STRIM_EINVAL;
+  const int rc = g_on_device(g->device, [&]() -> int {
+    if (g->next) (void)hipFree(g->next);
+    if (g->flags) (void)hipFree(g->flags);
+    if (g->base) (void)hipFree(g->base);
+    return STRIM_OK;
+  });
+  delete g;
+  return rc;
+}
+
+int strim_grammar_set_dfa(strim_grammar* g, void* stream, int32_t n_states,
+                          const int32_t* next, const uint8_t* flags) {
+  if (!g || n_states <= 0 || !next || !flags) return STRIM_EINVAL;
+  const int64_t n = (int64_t)n_states * 256;
+  for (int64_t i = 0; i < n; ++i)
+    if (next[i] < -1 || next[i] >= n_states) return STRIM_EINVAL;
+  return g_on_device(g->device, [&]() -> int {
+    hipStream_t st = (hipStream_t)stream;
+    // the previous table may still be read by queued work on this stream
+    if (hipStreamSynchronize(st) != hipSuccess) return STRIM_EHIP;
+    if (g->next) (void)hipFree(g->next);
+    if (g->flags) (void)hipFree(g->flags);
+    g->next = nullptr;
+    g->flags = nullptr;
+    g->n_states = 0;
+    if (hipMalloc(&g->next, (size_t)n * 4) != hipSuccess) {
+      g->next = nullptr;
+      return STRIM_ENOMEM;
+    }
+    if (hipMalloc(&g->flags, (size_t)n_states) != hipSuccess) {
+      g->flags = nullptr;
+      return STRIM_ENOMEM;
+    }
+    if (hipMemcpy(g->next, next, (size_t)n * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g->flags, flags, (size_t)n_states, hipMemcpyHostToDevice) != hipSuccess)
+      return STRIM_EHIP;
+    const int64_t nr = (int64_t)g->cache_states * g->nblk;
+    if (nr > 0) {
+      hipLaunchKernelGGL(k_gclear, dim3((unsigned)((nr + 255) / 256 < 1024 ? (nr + 255) / 256 : 1024)),
+                         dim3(256), 0, st, g->ready, nr);
+      if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+        return STRIM_EHIP;
+    }
+    g->n_states = n_states;
+    return STRIM_OK;
+  });
+}
+
+int strim_grammar_masks(strim_grammar* g, void* stream, const int32_t* keys, int32_t n,
+                        uint32_t* out, int64_t out_stride) {
+  if (!g || !keys || !out || n <= 0 || n > 65535 || out_stride < g->words) return STRIM_EINVAL;
+  if (g->n_states <= 0) return STRIM_EINVAL;  // no DFA installed
+  return g_on_device(g->device, [&]() -> int {
+    hipLaunchKernelGGL(k_gmask, dim3((unsigned)g->nblk, (unsigned)n), dim3(GM_T), 0,
+                       (hipStream_t)stream, view(g), keys, out, out_stride);
+    return g_status();
+  });
+}
+
+int strim_grammar_advance(strim_grammar* g, void* stream, const int32_t* state, int32_t B,
+                          const int32_t* tokens, int32_t k, int32_t* keys_out) {
+  if (!g || !state || !keys_out || B <= 0 || k < 0 || (k > 0 && !tokens)) return STRIM_EINVAL;
+  if (g->n_states <= 0) return STRIM_EINVAL;
+  return g_on_device(g->device, [&]() -> int {
+    hipLaunchKernelGGL(k_gadvance, dim3((unsigned)((B + 63) / 64)), dim3(64), 0,
+                       (hipStream_t)stream, view(g), state, B, tokens, k, keys_out);
+    return g_status();
+  });
+}
+
+}  // extern "C"

@@ -36,6 +36,11 @@ EXPORTS = (
     "strim_profile_begin",
     "strim_profile_end",
     "strim_kernel_name",
+    "strim_grammar_create",
+    "strim_grammar_destroy",
+    "strim_grammar_set_dfa",
+    "strim_grammar_masks",
+    "strim_grammar_advance",
 )
 KERNEL_COUNT = 8
 
@@ -123,6 +128,17 @@ def lib() -> ctypes.CDLL:
         L.strim_profile_end.argtypes = [P, P, P]
         L.strim_kernel_name.restype = ctypes.c_char_p
         L.strim_kernel_name.argtypes = [I32]
+        L.strim_grammar_create.restype = ctypes.c_int
+        L.strim_grammar_create.argtypes = [ctypes.POINTER(ctypes.c_void_p), I32, I32, P, P, P,
+                                           I32, P, I32, I32]
+        L.strim_grammar_destroy.restype = ctypes.c_int
+        L.strim_grammar_destroy.argtypes = [P]
+        L.strim_grammar_set_dfa.restype = ctypes.c_int
+        L.strim_grammar_set_dfa.argtypes = [P, P, I32, P, P]
+        L.strim_grammar_masks.restype = ctypes.c_int
+        L.strim_grammar_masks.argtypes = [P, P, P, I32, P, I64]
+        L.strim_grammar_advance.restype = ctypes.c_int
+        L.strim_grammar_advance.argtypes = [P, P, P, I32, P, I32, P]
         _lib = L
     return _lib
 
