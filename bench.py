@@ -163,6 +163,91 @@ def eager_us_per_step(torch, calls, steps):
     return (time.perf_counter() - t0) * 1e6 / steps
 
 
+GRAMMAR_ROWS = 8  # mask rows per launch (one per row of the B=8 configuration)
+
+
+def grammar_mask_bench(torch, dev, args):
+    """strim_grammar_masks at the configuration's width (V=151,936, 151,665 byte strings,
+    JSON-string DFA): 8 rows per launch in the in-string state, where nearly every token
+    walks all its bytes. "produce" runs with the mask cache off (every launch walks the
+    vocabulary), "cached" with it on (every launch after the first copies the rows)."""
+    from strim_amd import workloads as W
+    from strim_amd.grammar import DeviceGrammar
+
+    toks, skip = W.grammar_vocab()
+    nt, fl = W.json_string_dfa()
+    keys = torch.full((GRAMMAR_ROWS,), 1, dtype=torch.int32, device=dev)
+    out = {}
+    for name, cache in (("produce", 0), ("cached", 4)):
+        g = DeviceGrammar(toks, W.V_DEFAULT, eos=W.GRAMMAR_EOS, skip=skip, cache_states=cache)
+        g.set_dfa(nt, fl)
+        m = g.masks(keys)
+        # 32 launches captured in a HIP graph (the host's per-call cost stays out of the
+        # timing); each replay's launches carry their captured sequence numbers
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(4):
+                g.masks(keys, out=m)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        per = 32
+        with torch.cuda.graph(graph):
+            for _ in range(per):
+                g.masks(keys, out=m)
+        for _ in range(3):
+            graph.replay()
+        n = max(1, min(args.steps, 500) // per)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e3 / (n * per)
+        del graph
+        g.close()
+    words = (W.V_DEFAULT + 31) // 32
+    # algorithmic bytes per row: each token's 16-byte head and 8-byte meta, the words out
+    row_bytes = len(toks) * 24 + words * 4
+    gbs = row_bytes * GRAMMAR_ROWS / (out["produce"] * 1e-6) / 1e9
+    log(f"[bench] grammar masks: produce {out['produce']:.2f} us/launch, cached "
+        f"{out['cached']:.2f} us/launch ({GRAMMAR_ROWS} rows)")
+    return {"workload": f"strim_grammar_masks: {GRAMMAR_ROWS} rows x V=151936, 151665 byte "
+                        "strings (mean 6.5 bytes), JSON-string DFA, in-string state",
+            "produce_us_per_launch": round(out["produce"], 3),
+            "cached_us_per_launch": round(out["cached"], 3),
+            "produce_us_per_row": round(out["produce"] / GRAMMAR_ROWS, 3),
+            "roofline_produce": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0,
+                                 "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
+                                 "row_bytes": row_bytes}}
+
+
+def cpu_baseline_grammar(seconds: float):
+    """The reference's host mask production (the trie walk, restated in the oracle) for
+    the same state, one thread, repeated for about `seconds`."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+    from strim_amd import workloads as W
+
+    O.build()
+    toks, skip = W.grammar_vocab()
+    nt, fl = W.json_string_dfa()
+    o = O.GrammarOracle(toks, W.V_DEFAULT, W.GRAMMAR_EOS, skip)
+    o.set_dfa(nt, fl)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        o.mask(1)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(el * 1e6 / n, 1), "unit": "us/row", "cores": 1, "kind": "port",
+            "sample": f"trie walk of the in-string state, {n} rows in {el:.1f}s"}
+
+
 def cpu_baseline_cfg2(seconds: float):
     """The oracle (a C port of the reference sampler, OpenMP over rows) on host cores,
     on the cfg2 workload, repeated for about `seconds`."""
@@ -247,11 +332,18 @@ def summarize(d):
                 case = STREAM_CASES.get(k, k)
                 acc.setdefault(("k_qprep", case), []).extend(pending)
                 pending = []
+            # grammar masks: the cache-off grammar comes first; the cached one's set_dfa
+            # (its k_gclear) starts the cached launches
+            if k == "k_gclear":
+                case = "grammar cached"
+            elif k == "k_gmask" and not str(case).startswith("grammar"):
+                case = "grammar produce"
             kk = "k_stream" if k.startswith("k_stream") else k
             acc.setdefault((kk, case), []).append(us)
         acc = {key: v for key, v in acc.items() if v}
         print("\nThe same trace per workload (a kernel belongs to the k_stream variant it "
-              "follows; k_qprep to the one after it):\n")
+              "follows; k_qprep to the one after it; k_gmask to the grammar-mask timings, "
+              "cache off, then cache on):\n")
         print("| kernel | workload | calls | avg us | median us |\n|---|---|---|---|---|")
         for (k, c), v in sorted(acc.items(), key=lambda t: (str(t[0][1]), t[0][0])):
             v = sorted(v)
@@ -496,11 +588,14 @@ def main():
             "eager_us_per_step": round(eg4, 3),
             "kernel_us": {k: round(v[0], 3) for k, v in kt4.items()}}
         del ts4, ds4, dr4, calls4, outs
+        result["grammar_masks"] = grammar_mask_bench(torch, dev, args)
     ctx.close()
 
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle) ...")
         result["cpu_baseline"] = cpu_baseline_cfg2(args.cpu_seconds)
+        if "grammar_masks" in result:
+            result["grammar_masks"]["cpu_baseline"] = cpu_baseline_grammar(2.0)
     print(json.dumps(result), flush=True)
 
 

@@ -18,8 +18,9 @@
  * reports as STRIM_EEMPTY.
  *
  * All calls are stream-ordered; keys, tokens and outputs are device memory. Calls on one
- * strim_grammar that overlap on different streams race on its mask cache only when one of
- * them is strim_grammar_set_dfa.
+ * strim_grammar must not overlap (issue them on one stream): a mask call reads the cached
+ * blocks earlier calls produced, and one running alongside could read a block that is
+ * still being written.
  */
 #ifndef STRIM_GRAMMAR_H
 #define STRIM_GRAMMAR_H

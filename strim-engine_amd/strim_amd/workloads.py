@@ -169,3 +169,51 @@ def algorithmic_bytes(B, V, dtype_bytes, mask=False, H=0, noise_floats=0):
     noise and the output id (the out_probs validation output is excluded)."""
     return (B * V * dtype_bytes + (B * ((V + 31) // 32) * 4 if mask else 0) + B * H * 4
             + B * (48 + 4 * noise_floats + 4))
+
+
+# ---------------------------------------------------------------------------------
+# grammar masks: a vocabulary of the configuration's size and a JSON-string DFA
+# ---------------------------------------------------------------------------------
+GRAMMAR_COUNT = 151_665  # ids with byte strings; the logits width stays V_DEFAULT
+GRAMMAR_EOS = (151_643, 151_645)
+
+
+def grammar_vocab(seed=12, count=GRAMMAR_COUNT):
+    """Synthetic byte-level BPE vocabulary: the 256 single bytes, then pieces of 2..64
+    bytes (mean about 6.5) over printable ASCII with a leading space on a third of them
+    and a sprinkling of quotes, backslashes and UTF-8 continuation bytes; the end-of-turn
+    ids are control tokens (skipped by the mask)."""
+    rng = np.random.default_rng(seed)
+    toks = [bytes([b]) for b in range(256)]
+    n = count - 256
+    lens = np.minimum(64, 2 + rng.geometric(0.22, size=n))
+    alpha = np.frombuffer(b"abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ0123456789"
+                          b"_.,:;-+=()[]{}<>/!?'", dtype=np.uint8)
+    special = np.frombuffer(b"\"\\\x80\xa0\xc3\xe4", dtype=np.uint8)
+    for i in range(n):
+        L = int(lens[i])
+        b = alpha[rng.integers(len(alpha), size=L)]
+        if rng.random() < 0.33:
+            b[0] = 0x20
+        if rng.random() < 0.08:
+            b[rng.integers(L)] = special[rng.integers(len(special))]
+        toks.append(b.tobytes())
+    skip = np.zeros(count, dtype=np.uint8)
+    for e in GRAMMAR_EOS:
+        toks[e] = b"<|ctrl%d|>" % e
+        skip[e] = 1
+    return toks, skip
+
+
+def json_string_dfa():
+    """A JSON string value: 0 -"-> 1 (inside); 1: bytes >= 0x20 except quote and backslash
+    stay, backslash -> 2, quote -> 3 (accepting, done); 2: one escape character -> 1."""
+    nt = np.full((4, 256), -1, dtype=np.int32)
+    nt[0, ord('"')] = 1
+    nt[1, 0x20:] = 1
+    nt[1, ord('"')] = 3
+    nt[1, ord("\\")] = 2
+    for c in b'"\\/bfnrtu':
+        nt[2, c] = 1
+    flags = np.array([2, 2, 2, 1], dtype=np.uint8)
+    return nt, flags
