@@ -60,7 +60,7 @@ int strim_grammar_destroy(strim_grammar* g);
  *   next   host [n_states][256]: the state after byte b, -1 = dead. Every entry must be
  *          materialised (the reference's lazily expanded -2 entries are rejected)
  *   flags  host [n_states]: STRIM_DFA_ACCEPTING | STRIM_DFA_CONSUMING
- * Returns STRIM_EINVAL for an entry outside [-1, n_states). */
+ * Returns STRIM_EINVAL for an entry outside [-1, n_states) or more than 2^23 states. */
 int strim_grammar_set_dfa(strim_grammar* g, void* stream, int32_t n_states,
                           const int32_t* next, const uint8_t* flags);
 

@@ -59,18 +59,43 @@ __device__ __forceinline__ int walk_token(const GView& g, int s, uint4 h, uint32
   return st;
 }
 
+constexpr int GM_LDS_STATES = 16;      // DFAs up to this many states walk from LDS
+
+// Steps every token of the thread from st[q] through table `tab` (LDS or global).
+template <typename Tab>
+__device__ __forceinline__ void walk_all(Tab tab, const GView& g, const uint4* h,
+                                         const uint2* m, const uint32_t* len, int* st) {
+#pragma unroll
+  for (int i = 0; i < GM_HEAD; ++i) {
+#pragma unroll
+    for (int q = 0; q < GM_Q; ++q) {
+      if ((uint32_t)i < len[q] && st[q] >= 0) {
+        const uint32_t hw = i < 4 ? h[q].x : i < 8 ? h[q].y : i < 12 ? h[q].z : h[q].w;
+        const uint32_t b = (hw >> (8 * (i & 3))) & 0xFFu;
+        st[q] = tab[st[q] * 256 + (int)b];
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < GM_Q; ++q)
+    for (uint32_t i = GM_HEAD; i < len[q] && st[q] >= 0; ++i)
+      st[q] = tab[st[q] * 256 + (int)g.bytes[m[q].x + i]];
+}
+
 // Grid (nblk, n): workgroup (blk, r) produces mask words blk * GM_W .. of row r. Thread t
 // walks tokens blk * GM_TOK + q * 256 + t (q < GM_Q) in lockstep, one table lookup of each
 // in flight at a time; wave w's ballot for q gives words blk * GM_W + q * 8 + 2 w + {0, 1}.
 // (One token per thread measured fastest to produce: 8.0 us for a 151,936-token row of a
-// JSON-string state against 9.8 and 14.3 with two and four; the walk is a chain of
-// dependent table lookups, and more waves hide more of it than lockstep walks do.)
+// JSON-string state against 9.8 and 14.3 with two and four, before LDS staging; the walk
+// is a chain of dependent table lookups, and more waves hide more of it than lockstep
+// walks do. Staging a small DFA in LDS took 8 such rows from 18.6 to 12.4 us.)
 // A cached block is used only when an earlier launch produced it (ready holds the
 // producing launch's sequence number, never 0): the kernel boundary has made its words
 // visible, so plain loads and stores suffice. Blocks produced in this launch are produced
 // again by any other row that needs them (the same words, written twice).
 __global__ __launch_bounds__(GM_T) void k_gmask(GView g, const int32_t* keys, uint32_t* out,
                                                 int64_t out_stride, uint32_t seq) {
+  __shared__ int s_tab[GM_LDS_STATES * 256];
   const int blk = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
   const int lane = t & (WAVE - 1), w = t / WAVE;
   const int key = keys[r];
@@ -112,23 +137,19 @@ __global__ __launch_bounds__(GM_T) void k_gmask(GView g, const int32_t* keys, ui
       // a token takes part when it exists, is eligible and the state consumes
       st[q] = in && con && (m[q].y >> 31) ? key : -1;
     }
-#pragma unroll
-    for (int i = 0; i < GM_HEAD; ++i) {
-#pragma unroll
-      for (int q = 0; q < GM_Q; ++q) {
-        if ((uint32_t)i < len[q] && st[q] >= 0) {
-          const uint32_t hw = i < 4 ? h[q].x : i < 8 ? h[q].y : i < 12 ? h[q].z : h[q].w;
-          const uint32_t b = (hw >> (8 * (i & 3))) & 0xFFu;
-          st[q] = g.next[(int64_t)st[q] * 256 + b];
-        }
-      }
+    // a DFA of at most GM_LDS_STATES states is staged in LDS: the walk's chain of
+    // dependent lookups then costs LDS latency per byte instead of a cache hit's
+    if (g.n_states <= GM_LDS_STATES) {
+      const int4* src = (const int4*)g.next;
+      const int n4 = g.n_states * 64;
+      for (int e = t; e < n4; e += GM_T) ((int4*)s_tab)[e] = src[e];
+      __syncthreads();
+      walk_all(s_tab, g, h, m, len, st);
+    } else {
+      walk_all(g.next, g, h, m, len, st);
     }
 #pragma unroll
-    for (int q = 0; q < GM_Q; ++q) {
-      for (uint32_t i = GM_HEAD; i < len[q] && st[q] >= 0; ++i)
-        st[q] = g.next[(int64_t)st[q] * 256 + g.bytes[m[q].x + i]];
-      ok[q] = st[q] >= 0;
-    }
+    for (int q = 0; q < GM_Q; ++q) ok[q] = st[q] >= 0;
   }
   const bool acc = grammar && (g.flags[key] & STRIM_DFA_ACCEPTING);
 #pragma unroll
@@ -310,7 +331,8 @@ int strim_grammar_destroy(strim_grammar* g) {
 
 int strim_grammar_set_dfa(strim_grammar* g, void* stream, int32_t n_states,
                           const int32_t* next, const uint8_t* flags) {
-  if (!g || n_states <= 0 || !next || !flags) return STRIM_EINVAL;
+  // table offsets stay below 2^31 (the reference caps its DFA at 200,000 states)
+  if (!g || n_states <= 0 || n_states > (1 << 23) || !next || !flags) return STRIM_EINVAL;
   const int64_t n = (int64_t)n_states * 256;
   for (int64_t i = 0; i < n; ++i)
     if (next[i] < -1 || next[i] >= n_states) return STRIM_EINVAL;
