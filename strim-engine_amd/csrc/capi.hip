@@ -16,6 +16,7 @@ __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
 __global__ void k_qprep(Args a);
+__global__ void k_qcombine(Args a);
 __global__ void k_qsum(Args a);
 __global__ void k_qhist(Args a);
 __global__ void k_qpick(Args a);
@@ -265,6 +266,7 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   const size_t o_qhc = carve(RQ * wmax * QNB * sizeof(uint32_t));
   const size_t o_qhm = carve(RQ * wmax * QNB * sizeof(unsigned long long));
   const size_t o_qst = carve(R * sizeof(QStat));
+  const size_t o_qpp = carve(RQ * QSPLIT * sizeof(QPart));
   const size_t o_qflag = carve(sizeof(int32_t));
   ctx->bytes = off;
   int rc = on_device(device, [&]() -> int {
@@ -293,6 +295,7 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   ctx->s.qhc = (uint32_t*)(b + o_qhc);
   ctx->s.qhm = (unsigned long long*)(b + o_qhm);
   ctx->s.qst = (QStat*)(b + o_qst);
+  ctx->s.qpp = (QPart*)(b + o_qpp);
   ctx->s.qflag = (int32_t*)(b + o_qflag);
   ctx->s.wmax = wmax;
   *out = ctx;
@@ -427,12 +430,14 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       }
       hipError_t e = hipSuccess;
       if (a.dlog) {
-        // draft distributions (one workgroup per draft row) and, with the first group,
-        // the draft-vocab bitmap (one thread per table entry)
+        // draft distributions (QSPLIT workgroups per draft row, merged by k_qcombine)
+        // and, with the first group, the draft-vocab bitmap (one thread per table entry)
         const int nwb = g0 == 0 ? (int)((Vd + QPT - 1) / QPT) : 0;
         timed(ctx, KID_QPREP, [&](hipEvent_t e0, hipEvent_t e1) {
-          e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k + nwb)), dim3(QPT), a, st,
-                          e0, e1);
+          e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k * QSPLIT + nwb)),
+                          dim3(QPT), a, st, e0, nullptr);
+          if (e == hipSuccess)
+            e = launch_args((const void*)k_qcombine, dim3(1), dim3(MAXP), a, st, nullptr, e1);
         });
         if (e != hipSuccess) return STRIM_EHIP;
       }

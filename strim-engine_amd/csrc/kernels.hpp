@@ -112,6 +112,16 @@ struct QStat {
   double Z;     // sum of exp(v - mq), fp64
 };
 
+// k_qprep's partial result over one of the QSPLIT slices of a draft row's table.
+constexpr int QSPLIT = 8;
+struct QPart {
+  float m;      // slice maximum of v (-inf if empty)
+  int32_t td;   // table index of the draft in the slice, -1 if absent
+  double z;     // sum over the slice of exp(v - m), fp64
+  int32_t bad;  // the slice breaks the table's order or range (row 0 only)
+  int32_t pad_;
+};
+
 // Device scratch owned by a context (allocated once in strim_ctx_create).
 struct Scratch {
   ChunkStat* cstat;               // [rows][wmax]
@@ -131,6 +141,7 @@ struct Scratch {
   uint32_t* qhc;                  // [MAXP][wmax][QNB] QRES rows: residual counts per bin
   unsigned long long* qhm;        // [MAXP][wmax][QNB] QRES rows: residual masses per bin
   QStat* qst;                     // [rows] per draft row (b * k + j)
+  QPart* qpp;                     // [MAXP][QSPLIT] k_qprep slices, merged by k_qcombine
   int32_t* qflag;                 // [1] 1 when the draft table is valid
   int32_t wmax;
 };

@@ -608,14 +608,16 @@ __device__ __forceinline__ int table_lower_bound(const int32_t* tab, int n, int 
   return lo;
 }
 
-// QPT-thread workgroups. Blocks [0, B*k): one draft row each: mq = max(draft_logit / T) (fp32 division, as the
-// target's temperature), Z = sum exp(v - mq) in fp64, the table index of the row's
-// draft token, and v = draft_logit / T stored at each table id of the row's dense array
-// (the draft distribution of SpecSampling's general-q extension). Block 0 also checks
-// that the table is strictly ascending inside [0, V). Blocks after them: one thread per
-// table entry builds the membership bitmap: the first entry of each 32-id word writes
-// the word's bits and zeroes the empty words before it (the last entry also those
-// after it), so every word is written once.
+// QPT-thread workgroups. Blocks [0, B*k*QSPLIT): slice sp of draft row qr (blk = qr *
+// QSPLIT + sp, 1/QSPLIT of the table each): the slice maximum of v = draft_logit / T
+// (fp32 division, as the target's temperature), the slice's sum of exp(v - max) in fp64,
+// the table index of the row's draft token if the slice holds it, and v stored at each
+// table id of the row's dense array (the draft distribution of SpecSampling's general-q
+// extension); row 0's slices also check that the table is strictly ascending inside
+// [0, V). k_qcombine merges the slices. Blocks after them: one thread per table entry
+// builds the membership bitmap: the first entry of each 32-id word writes the word's
+// bits and zeroes the empty words before it (the last entry also those after it), so
+// every word is written once.
 __global__ __launch_bounds__(QPT) void k_qprep(Args a) {
   __shared__ float s_m[QPT / WAVE];
   __shared__ double s_d[QPT / WAVE];
@@ -623,30 +625,34 @@ __global__ __launch_bounds__(QPT) void k_qprep(Args a) {
   const int t = threadIdx.x;
   const int nq = a.B * a.k, Vd = a.Vd;
   const int blk = blockIdx.x;
-  if (blk < nq) {
-    const int b = blk / a.k, j = blk % a.k;
+  if (blk < nq * QSPLIT) {
+    // slice sp of draft row qr: table entries [lo, hi)
+    const int qr = blk / QSPLIT, sp = blk - qr * QSPLIT;
+    const int span = (Vd + QSPLIT - 1) / QSPLIT;
+    const int lo = min(Vd, sp * span), hi = min(Vd, lo + span);
+    const int b = qr / a.k, j = qr % a.k;
     const int d = a.drafts[(int64_t)b * a.k + j];
     const float T = a.p[b].temperature;
-    const size_t base = (size_t)blk * (size_t)Vd;
-    float* vq = a.s.vq + (size_t)blk * (size_t)a.s.wmax * CHUNK;
+    const size_t base = (size_t)qr * (size_t)Vd;
+    float* vq = a.s.vq + (size_t)qr * (size_t)a.s.wmax * CHUNK;
     auto ld = [&](int i) -> float {
       return a.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.dlog)[base + i])
                                          : ((const float*)a.dlog)[base + i];
     };
     // batches of QB entries per thread: every load of a batch is issued before its
     // stores (a store could alias a later load, which would serialise the loop). One
-    // pass: the table check (block 0), the draft's table index, v = logit / T at each id
+    // pass: the table check (row 0), the draft's table index, v = logit / T at each id
     // and the maximum.
-    constexpr int QB = 16;
+    constexpr int QB = 4;
     const bool live = T > 0.0f;
     float mx = -INFINITY;
     int bad = 0, td = -1;
-    for (int i0 = t; i0 < Vd; i0 += QB * QPT) {
+    for (int i0 = lo + t; i0 < hi; i0 += QB * QPT) {
       float v[QB];
       int id[QB], idn[QB];
 #pragma unroll
       for (int q = 0; q < QB; ++q) {
-        const int i = i0 + q * QPT < Vd ? i0 + q * QPT : 0;
+        const int i = i0 + q * QPT < hi ? i0 + q * QPT : lo;
         v[q] = ld(i);
         id[q] = a.dtable[i];
         idn[q] = a.dtable[i + 1 < Vd ? i + 1 : i];
@@ -654,7 +660,7 @@ __global__ __launch_bounds__(QPT) void k_qprep(Args a) {
 #pragma unroll
       for (int q = 0; q < QB; ++q) {
         const int i = i0 + q * QPT;
-        if (i >= Vd) continue;
+        if (i >= hi) continue;
         if (id[q] < 0 || id[q] >= a.V || (i + 1 < Vd && !(id[q] < idn[q]))) bad = 1;
         if (id[q] == d) td = i;
         if (live) {
@@ -664,37 +670,33 @@ __global__ __launch_bounds__(QPT) void k_qprep(Args a) {
         }
       }
     }
-    if (blk == 0) {
-      bad = block_or<QPT>(bad, s_bad);
-      if (t == 0) *a.s.qflag = bad ? 0 : 1;
-    }
+    if (qr == 0) bad = block_or<QPT>(bad, s_bad);
     td = -block_min<QPT>(-td, s_bad);  // at most one entry holds the draft
-    QStat q{-INFINITY, -1, 0.0};
+    QPart q{-INFINITY, td, 0.0, bad, 0};
     if (live) {
       mx = wave_max_f(mx);
       if ((t & (WAVE - 1)) == 0) s_m[t / WAVE] = mx;
       __syncthreads();
       mx = s_m[0];
 #pragma unroll
-      for (int q = 1; q < QPT / WAVE; ++q) mx = fmaxf(mx, s_m[q]);
+      for (int w = 1; w < QPT / WAVE; ++w) mx = fmaxf(mx, s_m[w]);
       double z = 0.0;
-      for (int i0 = t; i0 < Vd; i0 += QB * QPT) {
+      for (int i0 = lo + t; i0 < hi; i0 += QB * QPT) {
         float v[QB];
 #pragma unroll
-        for (int q = 0; q < QB; ++q) v[q] = ld(i0 + q * QPT < Vd ? i0 + q * QPT : 0);
+        for (int w = 0; w < QB; ++w) v[w] = ld(i0 + w * QPT < hi ? i0 + w * QPT : lo);
 #pragma unroll
-        for (int q = 0; q < QB; ++q)
-          if (i0 + q * QPT < Vd) z += exp((double)(v[q] / T) - (double)mx);
+        for (int w = 0; w < QB; ++w)
+          if (i0 + w * QPT < hi) z += exp((double)(v[w] / T) - (double)mx);
       }
       z = block_sum_f64<QPT>(z, s_d);
-      q.mq = mx;
-      q.Z = z;
-      q.td = td;
+      q.m = mx;
+      q.z = z;
     }
-    if (t == 0) a.s.qst[blk] = q;
+    if (t == 0) a.s.qpp[blk] = q;
     return;
   }
-  const int i = (blk - nq) * QPT + t;
+  const int i = (blk - nq * QSPLIT) * QPT + t;
   if (i >= Vd) return;
   const int words = (a.V + 31) / 32;
   const int id = a.dtable[i];
@@ -712,6 +714,34 @@ __global__ __launch_bounds__(QPT) void k_qprep(Args a) {
   for (int z = max(pw + 1, 0); z < w; ++z) a.s.dbits[z] = 0u;
   if (i == Vd - 1)
     for (int z = w + 1; z < words; ++z) a.s.dbits[z] = 0u;
+}
+
+// k_qcombine: one thread per draft row merges its QSPLIT slices into the row's QStat
+// (maximum, Z rescaled to it, the draft's index) and row 0's table check into qflag.
+__global__ void k_qcombine(Args a) {
+  const int t = threadIdx.x;
+  const int nq = a.B * a.k;
+  if (t >= nq) return;
+  const QPart* pp = a.s.qpp + (size_t)t * QSPLIT;
+  const float T = a.p[t / a.k].temperature;
+  float m = -INFINITY;
+  int td = -1, bad = 0;
+  for (int s = 0; s < QSPLIT; ++s) {
+    m = fmaxf(m, pp[s].m);
+    td = max(td, pp[s].td);
+    bad |= pp[s].bad;
+  }
+  double z = 0.0;
+  for (int s = 0; s < QSPLIT; ++s)
+    if (pp[s].m > -INFINITY) z += pp[s].z * exp((double)pp[s].m - (double)m);
+  QStat q{-INFINITY, -1, 0.0};
+  if (T > 0.0f) {
+    q.mq = m;
+    q.td = td;
+    q.Z = z;
+  }
+  a.s.qst[t] = q;
+  if (t == 0) *a.s.qflag = bad ? 0 : 1;
 }
 
 }  // namespace strim
