@@ -358,11 +358,32 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
     }
   }
   const uint32_t qbits = q.dbits[(i0 < a.V ? i0 : 0) >> 5] >> (i0 & 31);
+  // fp32 screen: an upper bound ub of every token's score (log(p - q) <= log p, so a
+  // table token's p-score bounds its residual score) and, from the tokens outside the
+  // table (whose score is the p-score), a lower bound lb of the wave's best. Only tokens
+  // with ub >= the wave's largest lb can be the best; they alone are scored exactly in
+  // fp64, with the same arithmetic and tie rule as every token was before. The margin
+  // covers the fp32 rounding of l - m - lse and of the two logarithms (well below 1e-4
+  // at these magnitudes).
+  const float mf = m, lsef = (float)lse;
+  float ub[EPT];
+  float lbw = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    ub[e] = -INFINITY;
+    if (!(l[e] > -INFINITY)) continue;
+    const float bf = no_lse ? l[e] : (l[e] - mf) - lsef;
+    const float sf = bf - logf(-logf(fmaxf(u[e], 1e-30f)));
+    const float mg = 1e-3f + 1e-5f * fabsf(sf);
+    ub[e] = sf + mg;
+    if (!((qbits >> e) & 1u)) lbw = fmaxf(lbw, sf - mg);
+  }
+  lbw = wave_max_f(lbw);
   double bsc = -INFINITY;
   int bid = -1;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
-    if (!(l[e] > -INFINITY)) continue;
+    if (!(l[e] > -INFINITY) || !(ub[e] >= lbw)) continue;
     const int id = i0 + e;
     double base = no_lse ? (double)l[e] : ((double)l[e] - (double)m) - lse;
     if ((qbits >> e) & 1u) {
