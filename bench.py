@@ -319,19 +319,20 @@ def summarize(d):
                       f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
     for f in glob.glob(str(d / "trace" / "*kernel_trace.csv")):
         rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
-        acc, case, pending = {}, None, []
+        acc, case, pending = {}, None, {}
         for r in rows:
             if "strim::" not in r["Kernel_Name"]:
                 continue
             k = _kname(r["Kernel_Name"])
             us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-            if k == "k_qprep":  # runs before its call's k_stream
-                pending.append(us)
+            if k in ("k_qprep", "k_qcombine"):  # run before their call's k_stream
+                pending.setdefault(k, []).append(us)
                 continue
             if k.startswith("k_stream"):
                 case = STREAM_CASES.get(k, k)
-                acc.setdefault(("k_qprep", case), []).extend(pending)
-                pending = []
+                for kk, v in pending.items():
+                    acc.setdefault((kk, case), []).extend(v)
+                pending = {}
             # grammar masks: the cache-off grammar comes first; the cached one's set_dfa
             # (its k_gclear) starts the cached launches
             if k == "k_gclear":
@@ -342,7 +343,7 @@ def summarize(d):
             acc.setdefault((kk, case), []).append(us)
         acc = {key: v for key, v in acc.items() if v}
         print("\nThe same trace per workload (a kernel belongs to the k_stream variant it "
-              "follows; k_qprep to the one after it; k_gmask to the grammar-mask timings, "
+              "follows; k_qprep and k_qcombine to the one after them; k_gmask to the grammar-mask timings, "
               "cache off, then cache on):\n")
         print("| kernel | workload | calls | avg us | median us |\n|---|---|---|---|---|")
         for (k, c), v in sorted(acc.items(), key=lambda t: (str(t[0][1]), t[0][0])):
