@@ -400,6 +400,9 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     for (int s = 0; s < SSEG; ++s)
 #pragma unroll
       for (int e = 0; e < EPT; ++e) l[s][e] = v[s][e] > -INFINITY ? v[s][e] / p.T : -INFINITY;
+    // unfiltered Gumbel rows are decided from the chunks' two best tokens and the sum;
+    // only the other general rows need the histogram (k_finalize's bin bounds)
+    const bool gum_nf = a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V);
     double ssum = 0.0;
     int na = 0;
 #pragma unroll
@@ -411,6 +414,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         const float d = m_w - l[s][e];
         const float wgt = expf(-d);
         ssum += (double)wgt;
+        if (gum_nf) continue;
         const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
         atomicAdd(&S.hc[w][bb], 1u);
         const unsigned long long fx = __float2ull_rn(wgt * FIX_SCALE_F);
@@ -423,7 +427,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     cs.n = 0;
 #pragma unroll
     for (int q = 0; q < NW; ++q) cs.n += S.n[q];
-    if (t < NCB) {
+    if (t < NCB && !gum_nf) {
       uint32_t hc = 0u;
       unsigned long long hm = 0ull;
 #pragma unroll
@@ -436,7 +440,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       a.s.chm[o] = hm;
     }
     // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
-    if (a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V)) {
+    if (gum_nf) {
       const uint64_t key = mix64(p.seed, p.position);
       float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
       int id0 = -1, id1 = -1;
