@@ -1,8 +1,10 @@
 """strim_amd — MI355X-native (gfx950) token selection for strim.
 
 The work runs in libstrim_sampler.so (hand-written HIP kernels behind the C ABI in
-include/strim_sampler.h). This package binds it and mirrors the reference's Swift
-sampling API.
+include/strim_sampler.h and include/strim_grammar.h). This package binds it and mirrors
+the reference's Swift sampling API (sampler.py), its grammar-mask runtime (grammar.py),
+its batched decode pick and MTP accounting (batch.py) and its draft-vocabulary loader
+(draft_vocab.py).
 """
 from . import _native
 from ._native import (ECAPACITY, EEMPTY, EINVAL, ENONFINITE, FLAG_NOISE_BY_RANK,
