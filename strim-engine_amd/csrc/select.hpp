@@ -7,6 +7,8 @@
 // scheduling.
 #pragma once
 
+#include <climits>
+
 #include "kernels.hpp"
 
 namespace strim {
@@ -157,26 +159,59 @@ __device__ __forceinline__ void top2_merge(float& s0, float& l0, int& i0, float&
 }
 
 // Wave-then-block reduction of the two best (score, l, id); result in thread 0.
+// The wave's two best of every lane's (s0, l0, i0) >= (s1, l1, i1) pair under (valid
+// first, score desc, id asc), with DPP reductions, in every lane: the best is the largest
+// score, the smallest id among equal scores; the runner-up is the best of every lane's
+// remaining candidate (the winner lane's second, the others' first). Ids are unique, so
+// the winner lane is.
+__device__ __forceinline__ void wave_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
+                                          int& i1) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  auto best = [&](float sc, float lv, int id, float& bs, float& bl, int& bi) -> int {
+    const bool ok = id >= 0;
+    const float m = wave_max_f(ok ? sc : -INFINITY);
+    const int mid = wave_min_i(ok && sc == m ? id : INT_MAX);
+    if (mid == INT_MAX) {
+      bs = -INFINITY; bl = 0.f; bi = -1;
+      return -1;
+    }
+    const uint64_t bal = __ballot(ok && sc == m && id == mid);
+    const int wl = (int)__ffsll((long long)bal) - 1;
+    bs = m;
+    bi = mid;
+    bl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), wl));
+    return wl;
+  };
+  float bs0, bl0, bs1, bl1;
+  int bi0, bi1;
+  const int wl = best(s0, l0, i0, bs0, bl0, bi0);
+  const bool mine = lane == wl;
+  best(mine ? s1 : s0, mine ? l1 : l0, mine ? i1 : i0, bs1, bl1, bi1);
+  s0 = bs0; l0 = bl0; i0 = bi0;
+  s1 = bs1; l1 = bl1; i1 = bi1;
+}
+
+// Block top-2 (result in thread 0): each wave's two best, then wave 0 over the waves'
+// pairs. sf: [4 * NT / WAVE] floats, si: [2 * NT / WAVE] ints of LDS.
 template <int NT>
 __device__ __forceinline__ void block_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
                                            int& i1, float* sf, int* si) {
+  static_assert(NT / WAVE <= WAVE, "one lane per wave");
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ts0 = __shfl_xor(s0, o, WAVE), tl0 = __shfl_xor(l0, o, WAVE);
-    const float ts1 = __shfl_xor(s1, o, WAVE), tl1 = __shfl_xor(l1, o, WAVE);
-    const int ti0 = __shfl_xor(i0, o, WAVE), ti1 = __shfl_xor(i1, o, WAVE);
-    top2_merge(s0, l0, i0, s1, l1, i1, ts0, tl0, ti0, ts1, tl1, ti1);
-  }
+  wave_top2(s0, l0, i0, s1, l1, i1);
   if (lane == 0) {
     sf[4 * w + 0] = s0; sf[4 * w + 1] = l0; sf[4 * w + 2] = s1; sf[4 * w + 3] = l1;
     si[2 * w + 0] = i0; si[2 * w + 1] = i1;
   }
   __syncthreads();
-  if (threadIdx.x == 0)
-    for (int q = 1; q < NT / WAVE; ++q)
-      top2_merge(s0, l0, i0, s1, l1, i1, sf[4 * q], sf[4 * q + 1], si[2 * q], sf[4 * q + 2],
-                 sf[4 * q + 3], si[2 * q + 1]);
+  if (w == 0) {
+    const bool own = lane < NT / WAVE;
+    const int q = own ? lane : 0;
+    s0 = sf[4 * q]; l0 = sf[4 * q + 1]; s1 = sf[4 * q + 2]; l1 = sf[4 * q + 3];
+    i0 = own ? si[2 * q] : -1;
+    i1 = own ? si[2 * q + 1] : -1;
+    wave_top2(s0, l0, i0, s1, l1, i1);
+  }
 }
 
 // Block argmax over (score desc, tie key asc); the winner's id lands in *out_id (-1 when
