@@ -12,15 +12,6 @@
 namespace strim {
 
 // ---------------------------------------------------------------------------------
-// shared helpers
-// ---------------------------------------------------------------------------------
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-  const uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
-  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// ---------------------------------------------------------------------------------
 // k_collect: general rows
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(TPB) void k_collect(Args a) {

@@ -379,11 +379,6 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
-  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, WAVE);
-  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, WAVE);
-  return ((uint64_t)hi << 32) | lo;
-}
 __device__ __forceinline__ uint64_t shfl_xor_u64v(uint64_t v, int o) {
   const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, WAVE);
   const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, WAVE);
