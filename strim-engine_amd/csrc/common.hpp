@@ -156,6 +156,7 @@ __device__ __forceinline__ int op_or_i(int a, int b) { return a | b; }
 __device__ __forceinline__ double op_add_d(double a, double b) { return a + b; }
 __device__ __forceinline__ float op_max_f(float a, float b) { return fmaxf(a, b); }
 __device__ __forceinline__ uint64_t op_add_u64(uint64_t a, uint64_t b) { return a + b; }
+__device__ __forceinline__ uint64_t op_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ __forceinline__ int wave_sum(int v) { STRIM_WAVE_REDUCE(int, v, dpp_i, rl_i, op_add_i); return v; }
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v) { return (uint32_t)wave_sum((int)v); }
@@ -165,6 +166,7 @@ __device__ __forceinline__ int wave_or_i(int v) { STRIM_WAVE_REDUCE(int, v, dpp_
 __device__ __forceinline__ float wave_max_f(float v) { STRIM_WAVE_REDUCE(float, v, dpp_f, rl_f, op_max_f); return v; }
 __device__ __forceinline__ double wave_sum(double v) { STRIM_WAVE_REDUCE(double, v, dpp_d, rl_d, op_add_d); return v; }
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) { STRIM_WAVE_REDUCE(uint64_t, v, dpp_u64, rl_u64, op_add_u64); return v; }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { STRIM_WAVE_REDUCE(uint64_t, v, dpp_u64, rl_u64, op_max_u64); return v; }
 
 // (value, id) argmax: larger value wins, equal values -> smaller id; id < 0 is empty.
 __device__ __forceinline__ void argmax_merge(float& v, int& id, float v2, int id2) {

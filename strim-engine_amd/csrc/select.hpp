@@ -101,13 +101,7 @@ __device__ __forceinline__ uint64_t block_or_u64(uint64_t v, uint64_t* scratch) 
 
 template <int NT>
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
-    const uint64_t u = ((uint64_t)hi << 32) | lo;
-    v = u > v ? u : v;
-  }
+  v = wave_max_u64(v);
   if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x / WAVE] = v;
   __syncthreads();
   uint64_t b = 0;
@@ -411,14 +405,6 @@ __device__ __forceinline__ uint64_t wave_or_u64(uint64_t v) {
   const uint32_t lo = (uint32_t)wave_or_i((int)(uint32_t)v);
   const uint32_t hi = (uint32_t)wave_or_i((int)(uint32_t)(v >> 32));
   return ((uint64_t)hi << 32) | lo;
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t u = shfl_xor_u64v(v, o);
-    v = u > v ? u : v;
-  }
-  return v;
 }
 
 // Wave argmax over (score desc, tie key asc); returns the winner's id (-1 if none),
