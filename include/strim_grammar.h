@@ -76,11 +76,49 @@ int strim_grammar_masks(strim_grammar* g, void* stream, const int32_t* keys, int
  * GrammarVocab.swift:107-112). For request b, keys_out[b][0] = key(state[b]) and
  * keys_out[b][i + 1] is the key after tokens[b][0 .. i]: each token's bytes step the
  * state; a step to dead makes that row and every later row free (-1). Free and forced
- * keys are left as they are (the thinking phase is the caller's). Ids outside
- * [0, count) have no bytes and leave the state unchanged. state device [B] (keys),
- * tokens device [B][k], keys_out device [B][k + 1]. */
+ * keys are left as they are: a key carries no thinking-phase state, so a request in its
+ * thinking phase is walked with strim_request_keys below. Ids outside [0, count) have no
+ * bytes and leave the state unchanged. state device [B] (keys), tokens device [B][k],
+ * keys_out device [B][k + 1]. */
 int strim_grammar_advance(strim_grammar* g, void* stream, const int32_t* state, int32_t B,
                           const int32_t* tokens, int32_t k, int32_t* keys_out);
+
+/* ---- per-request constraint state ---------------------------------------------------
+ * RequestConstraint.State and its constants (RequestConstraint.swift:62-83), one per
+ * request in device memory. The key of a state (RequestConstraint.key, :85-92):
+ *   in_think and budget >= 0 and count >= budget  -> forced(close_id)   (-2 - close_id)
+ *   in_think otherwise                            -> free              (-1)
+ *   g >= 0                                        -> grammar state g
+ *   g < 0 (no grammar, or a step left it)         -> free
+ * A step by token t (RequestConstraint.step, :94-102): in the thinking phase, t ==
+ * close_id leaves it and any other token counts toward the budget; after it, a live
+ * grammar state is stepped by t's bytes (dead = -1, so the request degrades to free). */
+typedef struct strim_request_state {
+  int32_t g;        /* grammar state, < 0 for none / dead                 (State.g)        */
+  int32_t in_think; /* nonzero while the request is in its thinking phase (State.inThink)  */
+  int32_t count;    /* thinking tokens emitted so far                     (State.count)    */
+  int32_t budget;   /* thinking budget, < 0 for none                      (budget)         */
+  int32_t close_id; /* the token that ends the thinking phase             (closeId)        */
+  int32_t violated; /* set once an emitted token stepped the grammar dead (violated)       */
+} strim_request_state;
+
+/* Row keys of B requests without changing their states (RequestConstraint.key / verifyMask,
+ * RequestConstraint.swift:85-92,121-126,134-145): keys_out[b][0] = key(states[b]) (the
+ * next token's row) and keys_out[b][i + 1] the key after drafts[b][0 .. i]; once a draft
+ * steps the grammar dead, that row and every later row are free. k = 0 (drafts NULL)
+ * gives the next-token keys alone. states device [B], drafts device [B][k], keys_out
+ * device [B][k + 1]; the keys feed strim_grammar_masks. */
+int strim_request_keys(strim_grammar* g, void* stream, const strim_request_state* states,
+                       int32_t B, const int32_t* drafts, int32_t k, int32_t* keys_out);
+
+/* Steps each request by the tokens the engine emitted (RequestConstraint.advance,
+ * RequestConstraint.swift:104-109): drafts[b][0 .. accepted[b]) and then last[b], the
+ * outputs of strim_verify (accepted NULL: none, as after strim_sample, where k = 0 and
+ * drafts may be NULL). accepted[b] is clamped to [0, k]; last[b] < 0 (a row error) steps
+ * nothing. A grammar step to dead sets violated; the request is free from then on. */
+int strim_request_advance(strim_grammar* g, void* stream, strim_request_state* states,
+                          int32_t B, const int32_t* drafts, int32_t k, const int32_t* accepted,
+                          const int32_t* last);
 
 #ifdef __cplusplus
 }

@@ -51,7 +51,8 @@ extern "C" {
 #define STRIM_EINVAL (-1)     /* bad params / sizes / pointers / draft id not in table */
 #define STRIM_EEMPTY (-2)     /* the row allows no token (all-zero mask or all -inf)    */
 #define STRIM_ENONFINITE (-3) /* NaN or +inf logit in an allowed position              */
-#define STRIM_ECAPACITY (-4)  /* candidate set larger than the context capacity        */
+#define STRIM_ECAPACITY (-4)  /* the call exceeds a fixed capacity: V above the
+                                 context's max_vocab                                    */
 #define STRIM_EHIP (-5)       /* HIP runtime error                                      */
 #define STRIM_ENOMEM (-6)     /* device allocation failed                              */
 
@@ -103,14 +104,16 @@ typedef struct strim_ctx strim_ctx;
 /* Fill *p with the reference defaults: T=1, top_k=0, top_p=1, extensions off. Host. */
 void strim_default_params(strim_sampling_params* p);
 
-/* Validate n HOST param structs the way ChatRequest.parse does (temperature >= 0,
- * top_p in (0,1], top_k >= 0) plus the extensions (min_p in [0,1], repetition > 0,
- * finite penalties). Returns STRIM_OK or STRIM_EINVAL. */
+/* Validate n HOST param structs the way the engine consumes GenParams: temperature
+ * finite (T <= 0 is greedy, GenParams.isGreedy, EngineAPI.swift:66), top_p in (0,1],
+ * top_k >= 0 (ChatRequest.swift:148-161), plus the extensions (min_p in [0,1],
+ * repetition > 0, finite penalties, known flags). Returns STRIM_OK or STRIM_EINVAL. */
 int strim_check_params(const strim_sampling_params* host_params, int32_t n);
 
 /* Create a context on `device` for up to max_rows rows of up to max_vocab tokens per
  * call (max_vocab <= 2^20). Allocates scratch once (hipMalloc); no call below allocates.
- * Calls with more rows than max_rows are processed in groups. */
+ * Calls with more rows than max_rows are processed in groups; a call with V above
+ * max_vocab returns STRIM_ECAPACITY. */
 int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t max_vocab);
 int strim_ctx_destroy(strim_ctx* ctx);
 
@@ -125,7 +128,7 @@ int strim_ctx_destroy(strim_ctx* ctx);
  *   noise       see STRIM_NOISE_*.
  *   out_ids     device [B]; -1 on a row error.
  *   out_status  device [B] or NULL; STRIM_OK or a negative STRIM_E* per row
- *               (EEMPTY, ENONFINITE, ECAPACITY).
+ *               (EEMPTY, ENONFINITE).
  *   out_probs   device [B][V] float or NULL: the processed distribution (validation).
  * Replaces Sampler.sample / SpecSampling.sample (Sampler.swift:34-54,
  * SpecSampling.swift:109-116) and the batched pick loop (EngineCore.swift:998-1002). */

@@ -226,3 +226,69 @@ void so_grammar_verify_keys(int32_t count, const uint32_t* offsets, const uint8_
     }
   }
 }
+
+/* RequestConstraint.key (RequestConstraint.swift:85-92): in the thinking phase, free until
+ * the budget is spent, then forced(closeId); afterwards the grammar state while it lives,
+ * free once it is dead (or there is no grammar). */
+static int32_t so_rq_key(const so_request_state* s) {
+  if (s->in_think)
+    return (s->budget >= 0 && s->close_id >= 0 && s->count >= s->budget) ? -2 - s->close_id : -1;
+  return s->g >= 0 ? s->g : -1;
+}
+
+/* RequestConstraint.step (RequestConstraint.swift:94-102) */
+static so_request_state so_rq_step(int32_t count, const uint32_t* offsets, const uint8_t* bytes,
+                                   int32_t n_states, const int32_t* next, so_request_state s,
+                                   int32_t t) {
+  if (s.in_think) {
+    if (t == s.close_id) s.in_think = 0;
+    else s.count += 1;
+  } else if (s.g >= 0 && s.g < n_states && t >= 0 && t < count) {
+    s.g = so_grammar_advance_bytes(s.g, bytes + offsets[t], offsets[t + 1] - offsets[t], next);
+  }
+  return s;
+}
+
+static int so_rq_died(const so_request_state* prev, const so_request_state* nx) {
+  return !prev->in_think && prev->g >= 0 && nx->g < 0;
+}
+
+void so_request_keys(int32_t count, const uint32_t* offsets, const uint8_t* bytes,
+                     int32_t n_states, const int32_t* next, const so_request_state* states,
+                     int32_t B, const int32_t* drafts, int32_t k, int32_t* keys_out) {
+  for (int32_t b = 0; b < B; ++b) {
+    so_request_state s = states[b];
+    int32_t* o = keys_out + (int64_t)b * (k + 1);
+    o[0] = so_rq_key(&s);
+    int live = 1;
+    for (int32_t i = 0; i < k; ++i) {
+      if (live) {
+        so_request_state prev = s;
+        s = so_rq_step(count, offsets, bytes, n_states, next, s, drafts[(int64_t)b * k + i]);
+        if (so_rq_died(&prev, &s)) live = 0;
+      }
+      o[i + 1] = live ? so_rq_key(&s) : -1;
+    }
+  }
+}
+
+void so_request_advance(int32_t count, const uint32_t* offsets, const uint8_t* bytes,
+                        int32_t n_states, const int32_t* next, so_request_state* states,
+                        int32_t B, const int32_t* drafts, int32_t k, const int32_t* accepted,
+                        const int32_t* last) {
+  for (int32_t b = 0; b < B; ++b) {
+    so_request_state s = states[b];
+    if (last[b] >= 0) {
+      int32_t n = accepted ? accepted[b] : 0;
+      n = n < 0 ? 0 : (n > k ? k : n);
+      for (int32_t i = 0; i <= n; ++i) {
+        const int32_t t = i < n ? drafts[(int64_t)b * k + i] : last[b];
+        so_request_state nx = so_rq_step(count, offsets, bytes, n_states, next, s, t);
+        const int died = so_rq_died(&s, &nx);
+        s = nx;
+        if (died) s.violated = 1;
+      }
+    }
+    states[b] = s;
+  }
+}

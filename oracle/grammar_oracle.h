@@ -35,6 +35,25 @@ void so_grammar_verify_keys(int32_t count, const uint32_t* offsets, const uint8_
                             int32_t n_states, const int32_t* next, const int32_t* state,
                             int32_t B, const int32_t* tokens, int32_t k, int32_t* keys_out);
 
+/* RequestConstraint.State with its constants: {g, in_think, count, budget, close_id,
+ * violated}, six int32 per request (the layout of strim_request_state) */
+typedef struct {
+  int32_t g, in_think, count, budget, close_id, violated;
+} so_request_state;
+
+/* RequestConstraint.key / verifyMask (RequestConstraint.swift:85-92,134-145): the key of
+ * each request's next row and of its k verify rows */
+void so_request_keys(int32_t count, const uint32_t* offsets, const uint8_t* bytes,
+                     int32_t n_states, const int32_t* next, const so_request_state* states,
+                     int32_t B, const int32_t* drafts, int32_t k, int32_t* keys_out);
+
+/* RequestConstraint.advance (RequestConstraint.swift:104-109) over drafts[0 .. accepted)
+ * and then last, per request (accepted NULL: none; last < 0: no step) */
+void so_request_advance(int32_t count, const uint32_t* offsets, const uint8_t* bytes,
+                        int32_t n_states, const int32_t* next, so_request_state* states,
+                        int32_t B, const int32_t* drafts, int32_t k, const int32_t* accepted,
+                        const int32_t* last);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,7 +89,34 @@ def build(force: bool = False) -> Path:
     return LIB_PATH
 
 
+def build_mutant(mutant: int, out: Path) -> Path:
+    """A variant of the oracle compiled with SO_MUTANT=mutant (a planted indexing mistake,
+    see strim_oracle.c), written to `out`. For the tests' discrimination checks only."""
+    subprocess.run(["make", "-s", "-B", "-C", str(HERE), f"OUT={Path(out).resolve()}",
+                    f"EXTRA=-DSO_MUTANT={int(mutant)}"], check=True)
+    return Path(out)
+
+
 _lib = None
+
+
+class use_library:
+    """Context manager: route every oracle call through the library at `path` (a mutant
+    built by build_mutant) until the block ends."""
+
+    def __init__(self, path):
+        self.path = Path(path)
+
+    def __enter__(self):
+        global _lib
+        self._saved = _lib
+        _lib = _load(self.path)
+        return self
+
+    def __exit__(self, *exc):
+        global _lib
+        _lib = self._saved
+        return False
 
 
 def lib():
@@ -97,32 +124,38 @@ def lib():
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        L = ctypes.CDLL(str(LIB_PATH))
-        P, I32, I64, U64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
-        L.so_mix.restype = U64
-        L.so_mix.argtypes = [U64, U64]
-        L.so_philox4x32_10.argtypes = [P, P, P]
-        L.so_uniform.restype = ctypes.c_float
-        L.so_uniform.argtypes = [U64, U64, U64]
-        L.so_uniforms.argtypes = [U64, U64, I64, P]
-        L.so_gumbel.restype = ctypes.c_double
-        L.so_gumbel.argtypes = [ctypes.c_float]
-        L.so_process_row.restype = I32
-        L.so_process_row.argtypes = [P, I32, P, P, I32, P, I32, P, P]
-        L.so_sample_batch.argtypes = [P, I32, I32, P, P, I64, P, P, I32, I32, P, P, P, I32]
-        L.so_verify_batch.argtypes = [P, I32, I32, I32, P, I32, P, P, P, P, I64, P, P, I32, I32,
-                                      P, P, P, P, P, P, P, P, I32]
-        L.so_trie_build.restype = P
-        L.so_trie_build.argtypes = [I32, P, P, P]
-        L.so_trie_free.argtypes = [P]
-        L.so_trie_nodes.restype = I32
-        L.so_trie_nodes.argtypes = [P]
-        L.so_grammar_mask.argtypes = [P, I32, P, I32, I32, P, P, I32, P]
-        L.so_grammar_advance_bytes.restype = I32
-        L.so_grammar_advance_bytes.argtypes = [I32, P, ctypes.c_uint32, P]
-        L.so_grammar_verify_keys.argtypes = [I32, P, P, I32, P, P, I32, P, I32, P]
-        _lib = L
+        _lib = _load(LIB_PATH)
     return _lib
+
+
+def _load(path: Path):
+    L = ctypes.CDLL(str(path))
+    P, I32, I64, U64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
+    L.so_mix.restype = U64
+    L.so_mix.argtypes = [U64, U64]
+    L.so_philox4x32_10.argtypes = [P, P, P]
+    L.so_uniform.restype = ctypes.c_float
+    L.so_uniform.argtypes = [U64, U64, U64]
+    L.so_uniforms.argtypes = [U64, U64, I64, P]
+    L.so_gumbel.restype = ctypes.c_double
+    L.so_gumbel.argtypes = [ctypes.c_float]
+    L.so_process_row.restype = I32
+    L.so_process_row.argtypes = [P, I32, P, P, I32, P, I32, P, P]
+    L.so_sample_batch.argtypes = [P, I32, I32, P, P, I64, P, P, I32, I32, P, P, P, I32]
+    L.so_verify_batch.argtypes = [P, I32, I32, I32, P, I32, P, P, P, P, I64, P, P, I32, I32,
+                                  P, P, P, P, P, P, P, P, I32]
+    L.so_trie_build.restype = P
+    L.so_trie_build.argtypes = [I32, P, P, P]
+    L.so_trie_free.argtypes = [P]
+    L.so_trie_nodes.restype = I32
+    L.so_trie_nodes.argtypes = [P]
+    L.so_grammar_mask.argtypes = [P, I32, P, I32, I32, P, P, I32, P]
+    L.so_grammar_advance_bytes.restype = I32
+    L.so_grammar_advance_bytes.argtypes = [I32, P, ctypes.c_uint32, P]
+    L.so_grammar_verify_keys.argtypes = [I32, P, P, I32, P, P, I32, P, I32, P]
+    L.so_request_keys.argtypes = [I32, P, P, I32, P, P, I32, P, I32, P]
+    L.so_request_advance.argtypes = [I32, P, P, I32, P, P, I32, P, I32, P, P]
+    return L
 
 
 def _ptr(a):
@@ -312,3 +345,35 @@ class GrammarOracle:
                                      len(self.flags), _ptr(self.next), _ptr(st), len(st),
                                      _ptr(tk), k, _ptr(out))
         return out
+
+    def request_keys(self, states, drafts=None) -> np.ndarray:
+        """RequestConstraint.key / verifyMask keys [B][k + 1] of REQUEST_STATE_DTYPE rows."""
+        st = np.ascontiguousarray(states, dtype=REQUEST_STATE_DTYPE).reshape(-1)
+        B = len(st)
+        tk = (np.zeros((B, 0), np.int32) if drafts is None
+              else np.ascontiguousarray(drafts, dtype=np.int32).reshape(B, -1))
+        k = tk.shape[1]
+        out = np.zeros((B, k + 1), dtype=np.int32)
+        lib().so_request_keys(self.count, _ptr(self.offsets), _ptr(self.bytes), len(self.flags),
+                              _ptr(self.next), _ptr(st), B, _ptr(tk) if k else None, k,
+                              _ptr(out))
+        return out
+
+    def request_advance(self, states, last, drafts=None, accepted=None) -> np.ndarray:
+        """RequestConstraint.advance by drafts[0 .. accepted) then last; returns new states."""
+        st = np.ascontiguousarray(states, dtype=REQUEST_STATE_DTYPE).reshape(-1).copy()
+        B = len(st)
+        tk = (np.zeros((B, 0), np.int32) if drafts is None
+              else np.ascontiguousarray(drafts, dtype=np.int32).reshape(B, -1))
+        acc = None if accepted is None else np.ascontiguousarray(accepted, dtype=np.int32)
+        ls = np.ascontiguousarray(last, dtype=np.int32).reshape(B)
+        lib().so_request_advance(self.count, _ptr(self.offsets), _ptr(self.bytes),
+                                 len(self.flags), _ptr(self.next), _ptr(st), B,
+                                 _ptr(tk) if tk.shape[1] else None, tk.shape[1], _ptr(acc),
+                                 _ptr(ls))
+        return st
+
+
+# RequestConstraint.State and its constants (strim_request_state, 24 bytes)
+REQUEST_STATE_DTYPE = np.dtype([("g", "<i4"), ("in_think", "<i4"), ("count", "<i4"),
+                                ("budget", "<i4"), ("close_id", "<i4"), ("violated", "<i4")])

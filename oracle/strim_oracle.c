@@ -27,6 +27,18 @@
 #include <omp.h>
 #endif
 
+/* Mutation switch of the known-answer tests' discrimination check: the tests build
+ * variants of this file with SO_MUTANT set to one of the values below (a plausible
+ * indexing mistake each) and assert that the injected-uniform known-answer tests FAIL on
+ * every variant. The normal build leaves it 0. */
+#ifndef SO_MUTANT
+#define SO_MUTANT 0
+#endif
+#define SO_MUT_NOISE_INDEX 1  /* Gumbel noise by sorted position instead of token id, and
+                                 by token id instead of rank under NOISE_BY_RANK         */
+#define SO_MUT_ACCEPT_INDEX 2 /* accept uniform from element 0 instead of V (Gumbel)     */
+#define SO_MUT_ICDF_SWAP 3    /* icdf draw and accept elements exchanged                 */
+
 /* ------------------------------------------------------------------------------ */
 /* Random numbers                                                                  */
 /* ------------------------------------------------------------------------------ */
@@ -273,7 +285,7 @@ static void so_filter(const float* l, int32_t V, const strim_sampling_params* p,
     }
     qsort(d->keys, (size_t)n, sizeof(uint64_t), so_cmp_u64);
     sorted = 1;
-  } else if (topp || need_sorted || d->cand_sorted) {
+  } else if (topp || need_sorted || d->cand_sorted || SO_MUTANT == SO_MUT_NOISE_INDEX) {
     qsort(d->keys, (size_t)n, sizeof(uint64_t), so_cmp_u64);
     sorted = 1;
   }
@@ -346,7 +358,8 @@ static int32_t so_gumbel_max(const so_dist* d, const double* s, const so_noise* 
   double b1 = -INFINITY, b2 = -INFINITY;
   for (int32_t j = 0; j < d->n; ++j) {
     if (s[j] == -INFINITY) continue;
-    double g = so_gumbel(so_u(nz, by_rank ? j : d->ids[j]));
+    const int by_pos = SO_MUTANT == SO_MUT_NOISE_INDEX ? !by_rank : by_rank;
+    double g = so_gumbel(so_u(nz, by_pos ? j : d->ids[j]));
     double sc = s[j] + g;
     if (best < 0 || sc > b1) { b2 = b1; b1 = sc; best = j; }
     else if (sc > b2) b2 = sc;
@@ -374,12 +387,12 @@ static int32_t so_draw(so_dist* d, const float* l, const strim_sampling_params* 
                        const so_noise* nz, int64_t accept_idx_unused, double* scratch) {
   (void)accept_idx_unused;
   if (noise_mode == STRIM_NOISE_ICDF) {
-    int32_t j = so_icdf(d, d->w, so_u(nz, 0), &d->margin);
+    int32_t j = so_icdf(d, d->w, so_u(nz, SO_MUTANT == SO_MUT_ICDF_SWAP ? 1 : 0), &d->margin);
     return d->ids[j];
   }
   const int no_lse = (p->flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
   const int by_rank = (p->flags & STRIM_FLAG_NOISE_BY_RANK) && d->topp;
-  if (!d->cand_sorted && !by_rank) so_to_id_order(d, l);
+  if (!d->cand_sorted && !by_rank && SO_MUTANT != SO_MUT_NOISE_INDEX) so_to_id_order(d, l);
   const double lse = log(d->sumw);
   for (int32_t j = 0; j < d->n; ++j) {
     double lj = (double)l[d->ids[j]];
@@ -517,10 +530,21 @@ void so_verify_batch(const float* target, int32_t B, int32_t k, int32_t V,
         float* probs = out_probs ? out_probs + row * V : NULL;
         if (probs) for (int32_t i = 0; i < V; ++i) probs[i] = 0.0f;
         const int32_t dj = j < k ? drafts[j] : -1;
-        if (j < k && (dj < 0 || dj >= V)) { status = STRIM_EINVAL; break; }
-        int32_t st = so_process_row(x, V, mrow, hist, hl, drafts, j, p, lbuf);
-        if (st != STRIM_OK) { status = st; break; }
+        /* a row error ends the sequence only when the accept chain reaches the row (the
+         * reference consumes rows 0 .. n alone, SpecSampling.swift:101-105); a later
+         * row reports it in its own outputs */
+        int32_t st = (j < k && (dj < 0 || dj >= V)) ? STRIM_EINVAL
+                                                    : so_process_row(x, V, mrow, hist, hl, drafts, j, p, lbuf);
         int32_t acc = 0, tok = -1;
+        if (st == STRIM_OK && !greedy && j < k && draft_logits != NULL &&
+            so_table_find(draft_to_full, Vd, dj) < 0)
+          st = STRIM_EINVAL;
+        if (st != STRIM_OK) {
+          if (alive) { status = st; alive = 0; }
+          if (out_row_accept && j < k) out_row_accept[(int64_t)b * k + j] = 0;
+          if (out_row_token) out_row_token[(int64_t)b * (k + 1) + j] = -1;
+          continue;
+        }
         if (greedy) {
           /* SpecStream.swift:269-273: accept while argmax == draft */
           tok = so_argmax(lbuf, V);
@@ -542,8 +566,7 @@ void so_verify_batch(const float* target, int32_t B, int32_t k, int32_t V,
             int general = draft_logits != NULL;
             if (general) {
               const float* dl = draft_logits + ((int64_t)b * k + j) * Vd;
-              int32_t t = so_table_find(draft_to_full, Vd, dj);
-              if (t < 0) { status = STRIM_EINVAL; break; }
+              int32_t t = so_table_find(draft_to_full, Vd, dj); /* >= 0: checked above */
               float mq = -INFINITY;
               for (int32_t a = 0; a < Vd; ++a) {
                 float v = dl[a] / p->temperature;
@@ -561,7 +584,12 @@ void so_verify_batch(const float* target, int32_t B, int32_t k, int32_t V,
             for (int32_t t = 0; t < d.n; ++t)
               if (d.ids[t] == dj) { dpos = t; p_d = d.w[t] / d.sumw; break; }
             double ratio = q_d > 0.0 ? p_d / q_d : (p_d > 0.0 ? INFINITY : 0.0);
-            float ua = so_u(&nz, noise_mode == STRIM_NOISE_GUMBEL ? V : 1);
+            /* accept uniform: element V of the Gumbel vector (SpecSampling.swift:83),
+             * element 1 of the icdf pair */
+            const int64_t acc_idx =
+                noise_mode == STRIM_NOISE_GUMBEL ? (SO_MUTANT == SO_MUT_ACCEPT_INDEX ? 0 : V)
+                                                 : (SO_MUTANT == SO_MUT_ICDF_SWAP ? 0 : 1);
+            float ua = so_u(&nz, acc_idx);
             acc = (double)ua < ratio;
             if (isfinite(ratio)) margin = so_minabs(margin, fabs((double)ua - ratio));
             /* residual max(0, p - q) over the kept set */
@@ -576,7 +604,8 @@ void so_verify_batch(const float* target, int32_t B, int32_t k, int32_t V,
                 double r = pi - qi;
                 scratch[t] = r > 0.0 ? r : 0.0;
               }
-              int32_t sel = so_icdf(&d, scratch, so_u(&nz, 0), &d.margin);
+              int32_t sel =
+                  so_icdf(&d, scratch, so_u(&nz, SO_MUTANT == SO_MUT_ICDF_SWAP ? 1 : 0), &d.margin);
               tok = d.ids[sel];
             } else {
               if (!d.cand_sorted) {

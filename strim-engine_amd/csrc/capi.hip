@@ -49,7 +49,66 @@ struct strim_ctx {
 
 namespace {
 
-size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Byte offsets of the scratch buffers of R rows of up to max_vocab tokens, each 256-byte
+// aligned. The general-q verify buffers (dbits .. qflag) are sized only when `verify`.
+struct ScratchLayout {
+  size_t cstat, slot, chc, chm, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp,
+      qflag, bytes;
+};
+constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) {
+  const size_t wmax = (max_vocab + CHUNK - 1) / CHUNK;
+  const size_t words = (max_vocab + 31) / 32;
+  const size_t RQ = verify ? (R < (size_t)MAXP ? R : (size_t)MAXP) : 0;  // per group
+  const size_t RV = verify ? R : 0;
+  ScratchLayout L{};
+  size_t off = 0;
+  L.cstat = off; off = align_up(off + R * wmax * sizeof(ChunkStat), 256);
+  L.slot = off; off = align_up(off + R * wmax * SLOT * sizeof(Cand), 256);
+  L.chc = off; off = align_up(off + R * wmax * NCB * sizeof(uint32_t), 256);
+  L.chm = off; off = align_up(off + R * wmax * NCB * sizeof(unsigned long long), 256);
+  L.part = off; off = align_up(off + R * wmax * sizeof(ChunkPart), 256);
+  L.rs = off; off = align_up(off + R * sizeof(RowState), 256);
+  L.cand = off; off = align_up(off + R * CAP * sizeof(Cand), 256);
+  L.nc = off; off = align_up(off + R * sizeof(uint32_t), 256);
+  L.dbits = off; off = align_up(off + (verify ? words : 0) * sizeof(uint32_t), 256);
+  L.vq = off; off = align_up(off + RQ * wmax * CHUNK * sizeof(float), 256);
+  L.qpart = off; off = align_up(off + RQ * wmax * sizeof(unsigned long long), 256);
+  L.qhc = off; off = align_up(off + RQ * wmax * QNB * sizeof(uint32_t), 256);
+  L.qhm = off; off = align_up(off + RQ * wmax * QNB * sizeof(unsigned long long), 256);
+  L.qst = off; off = align_up(off + RV * sizeof(QStat), 256);
+  L.qpp = off; off = align_up(off + RQ * QSPLIT * sizeof(QPart), 256);
+  L.qflag = off; off = align_up(off + (verify ? sizeof(int32_t) : 0), 256);
+  L.bytes = off;
+  return L;
+}
+
+// The scratch pointers of a layout placed at device address `base` (the general-q
+// buffers are null when the layout has none).
+Scratch scratch_at(char* base, const ScratchLayout& L, size_t max_vocab, bool verify) {
+  Scratch s{};
+  s.cstat = (ChunkStat*)(base + L.cstat);
+  s.slot = (Cand*)(base + L.slot);
+  s.chc = (uint32_t*)(base + L.chc);
+  s.chm = (unsigned long long*)(base + L.chm);
+  s.part = (ChunkPart*)(base + L.part);
+  s.rs = (RowState*)(base + L.rs);
+  s.cand = (Cand*)(base + L.cand);
+  s.ncand = (uint32_t*)(base + L.nc);
+  if (verify) {
+    s.dbits = (uint32_t*)(base + L.dbits);
+    s.vq = (float*)(base + L.vq);
+    s.qpart = (unsigned long long*)(base + L.qpart);
+    s.qhc = (uint32_t*)(base + L.qhc);
+    s.qhm = (unsigned long long*)(base + L.qhm);
+    s.qst = (QStat*)(base + L.qst);
+    s.qpp = (QPart*)(base + L.qpp);
+    s.qflag = (int32_t*)(base + L.qflag);
+  }
+  s.wmax = (int32_t)((max_vocab + CHUNK - 1) / CHUNK);
+  return s;
+}
 
 int launch_status() {
   hipError_t e = hipGetLastError();
@@ -191,6 +250,66 @@ void profile_free(strim_ctx* ctx) {
   ctx->prof_cap = ctx->prof_n = ctx->prof_on = 0;
 }
 
+
+// Host-checkable arguments of a sample call (everything but the capacity).
+int check_sample_args(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_t row_stride,
+                      const strim_sampling_params* params, const uint32_t* mask_words,
+                      int64_t mask_stride, const int32_t* history, int32_t H, int32_t noise_mode,
+                      const int32_t* out_ids) {
+  if (!logits || !params || !out_ids || !dtype_ok(dtype)) return STRIM_EINVAL;
+  if (B <= 0 || V <= 0 || row_stride < V) return STRIM_EINVAL;
+  if (mask_words && mask_stride < ((int64_t)V + 31) / 32) return STRIM_EINVAL;
+  if (H < 0 || (H > 0 && !history) || (history && H == 0)) return STRIM_EINVAL;
+  if (noise_mode != STRIM_NOISE_ICDF && noise_mode != STRIM_NOISE_GUMBEL) return STRIM_EINVAL;
+  if (strim_check_params(params, B) != STRIM_OK) return STRIM_EINVAL;
+  return STRIM_OK;
+}
+
+// The launch groups of one sample call over scratch `sc` sized for gmax rows (ctx only
+// times the launches and may be null).
+int sample_groups(strim_ctx* ctx, const Scratch& sc, int gmax, void* stream, const void* logits,
+                  int32_t dtype, int32_t B, int32_t V, int64_t row_stride,
+                  const strim_sampling_params* params, const uint32_t* mask_words,
+                  int64_t mask_stride, const int32_t* history, const int32_t* history_len,
+                  int32_t H, int32_t noise_mode, const float* noise, int32_t* out_ids,
+                  int32_t* out_status, float* out_probs) {
+  const int64_t nstride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
+  for (int32_t g0 = 0; g0 < B; g0 += gmax) {
+    const int nb = (B - g0) < gmax ? (B - g0) : gmax;
+    Args a;
+    memset(&a, 0, sizeof(a));
+    a.logits = (const char*)logits + (size_t)g0 * row_stride * dtype_size(dtype);
+    a.row_stride = row_stride;
+    a.dtype = dtype;
+    a.vec_ok = vec_ok(a.logits, row_stride, dtype);
+    a.R = nb;
+    a.V = V;
+    a.W = (V + CHUNK - 1) / CHUNK;
+    a.B = nb;
+    a.k = 0;
+    a.verify = 0;
+    a.mask = mask_words ? mask_words + (size_t)g0 * mask_stride : nullptr;
+    a.mask_stride = mask_stride;
+    a.hist = history ? history + (size_t)g0 * H : nullptr;
+    a.hist_len = (history && history_len) ? history_len + g0 : nullptr;
+    a.H = H;
+    a.noise_mode = noise_mode;
+    a.noise = noise ? noise + (size_t)g0 * nstride : nullptr;
+    a.noise_stride = nstride;
+    a.s = sc;
+    a.out_ids = out_ids + g0;
+    a.out_status = out_status ? out_status + g0 : nullptr;
+    a.out_probs = out_probs ? out_probs + (size_t)g0 * V : nullptr;
+    for (int i = 0; i < nb; ++i) {
+      a.p[i] = params[g0 + i];
+      a.lmp[i] = params[g0 + i].min_p > 0.0f ? log((double)params[g0 + i].min_p) : -INFINITY;
+    }
+    const int rc = run_group(ctx, (hipStream_t)stream, a, nb, out_probs != nullptr);
+    if (rc != STRIM_OK) return rc;
+  }
+  return STRIM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -212,13 +331,14 @@ void strim_default_params(strim_sampling_params* p) {
   p->position = 0u;
 }
 
-// ChatRequest.parse (Sources/StrimServer/ChatRequest.swift:150-160): temperature >= 0,
-// top_p in (0,1], top_k >= 0; plus the extension ranges.
+// GenParams as the engine consumes it: a finite temperature, T <= 0 greedy
+// (GenParams.isGreedy, Sources/StrimEngine/EngineAPI.swift:66); top_p in (0,1] and
+// top_k >= 0 (ChatRequest.swift:150-160); plus the extension ranges.
 int strim_check_params(const strim_sampling_params* hp, int32_t n) {
   if (!hp || n < 0) return STRIM_EINVAL;
   for (int32_t i = 0; i < n; ++i) {
     const strim_sampling_params& p = hp[i];
-    if (!(p.temperature >= 0.0f) || isinf(p.temperature)) return STRIM_EINVAL;
+    if (isnan(p.temperature) || isinf(p.temperature)) return STRIM_EINVAL;
     if (!(p.top_p > 0.0f && p.top_p <= 1.0f)) return STRIM_EINVAL;
     if (p.top_k < 0) return STRIM_EINVAL;
     if (!(p.min_p >= 0.0f && p.min_p <= 1.0f)) return STRIM_EINVAL;
@@ -241,34 +361,8 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
   ctx->device = device;
   ctx->max_rows = max_rows;
   ctx->max_vocab = max_vocab;
-  const int32_t wmax = (max_vocab + CHUNK - 1) / CHUNK;
-  const size_t R = (size_t)max_rows;
-  size_t off = 0;
-  auto carve = [&](size_t bytes) {
-    size_t o = off;
-    off = align_up(off + bytes, 256);
-    return o;
-  };
-  const size_t o_cstat = carve(R * wmax * sizeof(ChunkStat));
-  const size_t o_slot = carve(R * wmax * SLOT * sizeof(Cand));
-  const size_t o_chc = carve(R * wmax * NCB * sizeof(uint32_t));
-  const size_t o_chm = carve(R * wmax * NCB * sizeof(unsigned long long));
-  const size_t o_part = carve(R * wmax * sizeof(ChunkPart));
-  const size_t o_rs = carve(R * sizeof(RowState));
-  const size_t o_cand = carve(R * CAP * sizeof(Cand));
-  const size_t o_nc = carve(R * sizeof(uint32_t));
-  const size_t words = ((size_t)max_vocab + 31) / 32;
-  const size_t o_dbits = carve(words * sizeof(uint32_t));
-  // general-q draft rows: at most MAXP per launch group
-  const size_t RQ = R < (size_t)MAXP ? R : (size_t)MAXP;
-  const size_t o_vq = carve(RQ * wmax * CHUNK * sizeof(float));
-  const size_t o_qpart = carve(RQ * wmax * sizeof(unsigned long long));
-  const size_t o_qhc = carve(RQ * wmax * QNB * sizeof(uint32_t));
-  const size_t o_qhm = carve(RQ * wmax * QNB * sizeof(unsigned long long));
-  const size_t o_qst = carve(R * sizeof(QStat));
-  const size_t o_qpp = carve(RQ * QSPLIT * sizeof(QPart));
-  const size_t o_qflag = carve(sizeof(int32_t));
-  ctx->bytes = off;
+  const ScratchLayout L = scratch_layout((size_t)max_rows, (size_t)max_vocab, true);
+  ctx->bytes = L.bytes;
   int rc = on_device(device, [&]() -> int {
     if (hipMalloc(&ctx->base, ctx->bytes) != hipSuccess) return STRIM_ENOMEM;
     if (hipMemset(ctx->base, 0, ctx->bytes) != hipSuccess) return STRIM_EHIP;
@@ -280,24 +374,7 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
     delete ctx;
     return rc;
   }
-  char* b = (char*)ctx->base;
-  ctx->s.cstat = (ChunkStat*)(b + o_cstat);
-  ctx->s.slot = (Cand*)(b + o_slot);
-  ctx->s.chc = (uint32_t*)(b + o_chc);
-  ctx->s.chm = (unsigned long long*)(b + o_chm);
-  ctx->s.part = (ChunkPart*)(b + o_part);
-  ctx->s.rs = (RowState*)(b + o_rs);
-  ctx->s.cand = (Cand*)(b + o_cand);
-  ctx->s.ncand = (uint32_t*)(b + o_nc);
-  ctx->s.dbits = (uint32_t*)(b + o_dbits);
-  ctx->s.vq = (float*)(b + o_vq);
-  ctx->s.qpart = (unsigned long long*)(b + o_qpart);
-  ctx->s.qhc = (uint32_t*)(b + o_qhc);
-  ctx->s.qhm = (unsigned long long*)(b + o_qhm);
-  ctx->s.qst = (QStat*)(b + o_qst);
-  ctx->s.qpp = (QPart*)(b + o_qpp);
-  ctx->s.qflag = (int32_t*)(b + o_qflag);
-  ctx->s.wmax = wmax;
+  ctx->s = scratch_at((char*)ctx->base, L, (size_t)max_vocab, true);
   *out = ctx;
   return STRIM_OK;
 }
@@ -318,49 +395,16 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
                  const uint32_t* mask_words, int64_t mask_stride, const int32_t* history,
                  const int32_t* history_len, int32_t H, int32_t noise_mode, const float* noise,
                  int32_t* out_ids, int32_t* out_status, float* out_probs) {
-  if (!ctx || !logits || !params || !out_ids || !dtype_ok(dtype)) return STRIM_EINVAL;
-  if (B <= 0 || V <= 0 || V > ctx->max_vocab || row_stride < V) return STRIM_EINVAL;
-  if (mask_words && mask_stride < ((int64_t)V + 31) / 32) return STRIM_EINVAL;
-  if (H < 0 || (H > 0 && !history) || (history && H == 0)) return STRIM_EINVAL;
-  if (noise_mode != STRIM_NOISE_ICDF && noise_mode != STRIM_NOISE_GUMBEL) return STRIM_EINVAL;
-  if (strim_check_params(params, B) != STRIM_OK) return STRIM_EINVAL;
-  const int64_t nstride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
+  if (!ctx) return STRIM_EINVAL;
+  const int rc = check_sample_args(logits, dtype, B, V, row_stride, params, mask_words,
+                                   mask_stride, history, H, noise_mode, out_ids);
+  if (rc != STRIM_OK) return rc;
+  if (V > ctx->max_vocab) return STRIM_ECAPACITY;
   const int gmax = ctx->max_rows < MAXP ? ctx->max_rows : MAXP;
   return on_device(ctx->device, [&]() -> int {
-    for (int32_t g0 = 0; g0 < B; g0 += gmax) {
-      const int nb = (B - g0) < gmax ? (B - g0) : gmax;
-      Args a;
-      memset(&a, 0, sizeof(a));
-      a.logits = (const char*)logits + (size_t)g0 * row_stride * dtype_size(dtype);
-      a.row_stride = row_stride;
-      a.dtype = dtype;
-      a.vec_ok = vec_ok(a.logits, row_stride, dtype);
-      a.R = nb;
-      a.V = V;
-      a.W = (V + CHUNK - 1) / CHUNK;
-      a.B = nb;
-      a.k = 0;
-      a.verify = 0;
-      a.mask = mask_words ? mask_words + (size_t)g0 * mask_stride : nullptr;
-      a.mask_stride = mask_stride;
-      a.hist = history ? history + (size_t)g0 * H : nullptr;
-      a.hist_len = (history && history_len) ? history_len + g0 : nullptr;
-      a.H = H;
-      a.noise_mode = noise_mode;
-      a.noise = noise ? noise + (size_t)g0 * nstride : nullptr;
-      a.noise_stride = nstride;
-      a.s = ctx->s;
-      a.out_ids = out_ids + g0;
-      a.out_status = out_status ? out_status + g0 : nullptr;
-      a.out_probs = out_probs ? out_probs + (size_t)g0 * V : nullptr;
-      for (int i = 0; i < nb; ++i) {
-        a.p[i] = params[g0 + i];
-        a.lmp[i] = params[g0 + i].min_p > 0.0f ? log((double)params[g0 + i].min_p) : -INFINITY;
-      }
-      const int rc = run_group(ctx, (hipStream_t)stream, a, nb, out_probs != nullptr);
-      if (rc != STRIM_OK) return rc;
-    }
-    return STRIM_OK;
+    return sample_groups(ctx, ctx->s, gmax, stream, logits, dtype, B, V, row_stride, params,
+                         mask_words, mask_stride, history, history_len, H, noise_mode, noise,
+                         out_ids, out_status, out_probs);
   });
 }
 
@@ -374,7 +418,7 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
                  int32_t* out_status) {
   if (!ctx || !target_logits || !params || !out_accepted || !out_token || !dtype_ok(dtype))
     return STRIM_EINVAL;
-  if (B <= 0 || k < 0 || k > 64 || V <= 0 || V > ctx->max_vocab) return STRIM_EINVAL;
+  if (B <= 0 || k < 0 || k > 64 || V <= 0) return STRIM_EINVAL;
   if (k + 1 > ctx->max_rows) return STRIM_EINVAL;
   if (k > 0 && !draft_tokens) return STRIM_EINVAL;
   if (draft_logits && (!draft_to_full || Vd <= 0 || Vd > V)) return STRIM_EINVAL;
@@ -382,6 +426,7 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
   if (H < 0 || (H > 0 && !history) || (history && H == 0)) return STRIM_EINVAL;
   if (noise_mode != STRIM_NOISE_ICDF && noise_mode != STRIM_NOISE_GUMBEL) return STRIM_EINVAL;
   if (strim_check_params(params, B) != STRIM_OK) return STRIM_EINVAL;
+  if (V > ctx->max_vocab) return STRIM_ECAPACITY;
   const int64_t nstride = noise_mode == STRIM_NOISE_GUMBEL ? (int64_t)V + 1 : 2;
   int gmax = ctx->max_rows / (k + 1);
   if (gmax > MAXP) gmax = MAXP;

@@ -186,6 +186,69 @@ __global__ void k_gadvance(GView g, const int32_t* state, int B, const int32_t* 
   }
 }
 
+// ---- per-request constraint state (RequestConstraint.key / step) --------------------
+__device__ __forceinline__ int rq_key(const strim_request_state& s) {
+  if (s.in_think)
+    return (s.budget >= 0 && s.close_id >= 0 && s.count >= s.budget) ? -2 - s.close_id : -1;
+  return s.g >= 0 ? s.g : -1;
+}
+__device__ __forceinline__ strim_request_state rq_step(const GView& g, strim_request_state s,
+                                                        int t) {
+  if (s.in_think) {
+    if (t == s.close_id) s.in_think = 0;
+    else s.count += 1;
+  } else if (s.g >= 0 && s.g < g.n_states && t >= 0 && t < g.count) {
+    const uint2 m = g.meta[t];
+    s.g = walk_token(g, s.g, g.head[t], m.x, m.y & 0x7FFFFFFFu);  // dead: -1
+  }
+  return s;
+}
+// the step left a live grammar state for dead (RequestConstraint.swift:107,142)
+__device__ __forceinline__ bool rq_died(const strim_request_state& prev,
+                                        const strim_request_state& next) {
+  return !prev.in_think && prev.g >= 0 && next.g < 0;
+}
+
+// One thread per request: the key of its next row and of its k verify rows.
+__global__ void k_rkeys(GView g, const strim_request_state* states, int B,
+                        const int32_t* drafts, int k, int32_t* keys_out) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  strim_request_state s = states[b];
+  int32_t* o = keys_out + (int64_t)b * (k + 1);
+  o[0] = rq_key(s);
+  bool live = true;
+  for (int i = 0; i < k; ++i) {
+    if (live) {
+      const strim_request_state prev = s;
+      s = rq_step(g, s, drafts[(int64_t)b * k + i]);
+      if (rq_died(prev, s)) live = false;
+    }
+    o[i + 1] = live ? rq_key(s) : -1;
+  }
+}
+
+// One thread per request: its state after drafts[0 .. accepted) and last.
+__global__ void k_radvance(GView g, strim_request_state* states, int B, const int32_t* drafts,
+                           int k, const int32_t* accepted, const int32_t* last) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  strim_request_state s = states[b];
+  const int t_last = last[b];
+  if (t_last >= 0) {
+    int n = accepted ? accepted[b] : 0;
+    n = n < 0 ? 0 : (n > k ? k : n);
+    for (int i = 0; i <= n; ++i) {
+      const int t = i < n ? drafts[(int64_t)b * k + i] : t_last;
+      const strim_request_state nx = rq_step(g, s, t);
+      const bool died = rq_died(s, nx);
+      s = nx;
+      if (died) s.violated = 1;
+    }
+  }
+  states[b] = s;
+}
+
 __global__ void k_gclear(uint32_t* p, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -387,6 +450,27 @@ int strim_grammar_advance(strim_grammar* g, void* stream, const int32_t* state, 
   return g_on_device(g->device, [&]() -> int {
     hipLaunchKernelGGL(k_gadvance, dim3((unsigned)((B + 63) / 64)), dim3(64), 0,
                        (hipStream_t)stream, view(g), state, B, tokens, k, keys_out);
+    return g_status();
+  });
+}
+
+int strim_request_keys(strim_grammar* g, void* stream, const strim_request_state* states,
+                       int32_t B, const int32_t* drafts, int32_t k, int32_t* keys_out) {
+  if (!g || !states || !keys_out || B <= 0 || k < 0 || (k > 0 && !drafts)) return STRIM_EINVAL;
+  return g_on_device(g->device, [&]() -> int {
+    hipLaunchKernelGGL(k_rkeys, dim3((unsigned)((B + 63) / 64)), dim3(64), 0,
+                       (hipStream_t)stream, view(g), states, B, drafts, k, keys_out);
+    return g_status();
+  });
+}
+
+int strim_request_advance(strim_grammar* g, void* stream, strim_request_state* states,
+                          int32_t B, const int32_t* drafts, int32_t k, const int32_t* accepted,
+                          const int32_t* last) {
+  if (!g || !states || !last || B <= 0 || k < 0 || (k > 0 && !drafts)) return STRIM_EINVAL;
+  return g_on_device(g->device, [&]() -> int {
+    hipLaunchKernelGGL(k_radvance, dim3((unsigned)((B + 63) / 64)), dim3(64), 0,
+                       (hipStream_t)stream, view(g), states, B, drafts, k, accepted, last);
     return g_status();
   });
 }

@@ -557,10 +557,16 @@ __global__ void k_verify_combine(Args a) {
   const int k = a.k;
   int status = STRIM_OK, n = 0, token = -1;
   bool alive = true;
+  // SpecSampling.verify consumes only the rows its accept chain reaches, 0 .. n
+  // (SpecSampling.swift:101-105): a row error counts for the sequence only when the chain
+  // reaches that row; later rows report theirs in the per-row outputs alone
   for (int j = 0; j <= k; ++j) {
     const RowState& rs = a.s.rs[(int64_t)b * (k + 1) + j];
     if (rs.status != STRIM_OK) {
-      if (status == STRIM_OK) status = rs.status;
+      if (alive) {
+        status = rs.status;
+        alive = false;
+      }
       if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = 0;
       if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = -1;
       continue;

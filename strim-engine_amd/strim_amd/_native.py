@@ -41,6 +41,8 @@ EXPORTS = (
     "strim_grammar_set_dfa",
     "strim_grammar_masks",
     "strim_grammar_advance",
+    "strim_request_keys",
+    "strim_request_advance",
 )
 KERNEL_COUNT = 8
 
@@ -139,6 +141,10 @@ def lib() -> ctypes.CDLL:
         L.strim_grammar_masks.argtypes = [P, P, P, I32, P, I64]
         L.strim_grammar_advance.restype = ctypes.c_int
         L.strim_grammar_advance.argtypes = [P, P, P, I32, P, I32, P]
+        L.strim_request_keys.restype = ctypes.c_int
+        L.strim_request_keys.argtypes = [P, P, P, I32, P, I32, P]
+        L.strim_request_advance.restype = ctypes.c_int
+        L.strim_request_advance.argtypes = [P, P, P, I32, P, I32, P, P]
         _lib = L
     return _lib
 

@@ -6,11 +6,13 @@ by its constraint and sampled (or argmaxed) on its own, one launch and one host 
 row (`EngineCore.pick` / `decodeBatch`, Sources/StrimEngine/EngineCore.swift:968-1011).
 `BatchPicker.pick` makes it one `strim_sample` call: greedy rows are T <= 0 rows of the
 same params array, constrained rows take their mask words from the device grammar
-(`strim_grammar_masks`) and their grammar states are stepped by the chosen tokens on
-the device (`strim_grammar_advance`), so the step needs no host sync at all.
+(`strim_request_keys` + `strim_grammar_masks`) and their request states (thinking
+budget, grammar state) are stepped by the chosen tokens on the device
+(`strim_request_advance`), so the step needs no host sync at all.
 `BatchPicker.verify_round` does the same for a speculative round (`strim_verify` with
 the verify-row masks) and records each request's round in its `MTPStats`, with one host
-read of the B accepted counts.
+read of the B accepted counts. `SpecRounds` keeps each request's output position
+(SpecStream's sampleIndex) across rounds.
 
 `MTPStats` mirrors the reference's completed-round accounting
 (Sources/StrimCore/QwenModel.swift:3-77): one-based positions, bounded counters for
@@ -85,49 +87,110 @@ class BatchPicker:
     """One call per decode step for the whole batch (see the module docstring).
 
     ctx: a `strim_amd.ops.Context`; grammar: a `strim_amd.grammar.DeviceGrammar` shared by
-    the constrained rows, or None.
+    the constrained requests, or None. Constrained requests carry a device tensor of
+    per-request states (`grammar.REQUEST_STATE` rows, int32 [B, 6]): the thinking phase
+    and budget, the grammar state and the violation flag of RequestConstraint
+    (RequestConstraint.swift:62-109). Each call reads the rows' keys from the states and
+    steps the states by the emitted tokens, on the device.
     """
 
     def __init__(self, ctx, grammar=None):
         self.ctx = ctx
         self.grammar = grammar
 
-    def pick(self, logits: torch.Tensor, params, keys: torch.Tensor | None = None,
+    def _need_grammar(self):
+        if self.grammar is None:
+            raise ValueError("request states need a grammar")
+
+    def pick(self, logits: torch.Tensor, params, states: torch.Tensor | None = None,
              noise_mode: int = 0):
-        """Tokens [B] for logits [B, V] and per-row params (T <= 0 = greedy). keys: device
-        int32 [B] grammar keys (state, -1 free, -2 - id forced) or None. Returns
-        (ids, status, next_keys); next_keys are the keys after each row's token."""
-        mask = None
-        if keys is not None:
-            if self.grammar is None:
-                raise ValueError("keys need a grammar")
+        """Tokens [B] for logits [B, V] and per-row params (T <= 0 = greedy), each row
+        masked by its request's next-token key (RequestConstraint.apply). states is
+        advanced in place by the picked tokens (RequestConstraint.advance). Returns
+        (ids, status, keys): the keys the rows were masked by."""
+        mask = keys = None
+        if states is not None:
+            self._need_grammar()
+            keys = self.grammar.request_keys(states)[:, 0].contiguous()
             mask = self.grammar.masks(keys)
         ids, status, _ = self.ctx.sample(logits, params, mask=mask, noise_mode=noise_mode)
-        nxt = None
-        if keys is not None:
-            nxt = self.grammar.advance(keys, ids.view(-1, 1))[:, 1].contiguous()
-        return ids, status, nxt
+        if states is not None:
+            self.grammar.request_advance(states, ids)
+        return ids, status, keys
 
     def verify_round(self, target: torch.Tensor, drafts: torch.Tensor, params,
-                     stats: list | None = None, keys: torch.Tensor | None = None,
+                     stats: list | None = None, states: torch.Tensor | None = None,
                      depth=None, noise_mode: int = 0, **kw):
-        """A speculative round over target [B, k + 1, V] and drafts [B, k]. With keys, the
-        k + 1 verify rows of each request are masked by its grammar (verifyMask on the
-        device). stats: a list of B MTPStats, one per request, each given its round
-        (depth defaults to k). Returns strim_verify's outputs plus "keys" [B, k + 1]."""
+        """A speculative round over target [B, k + 1, V] and drafts [B, k]. With states,
+        the k + 1 verify rows of each request are masked by its keys
+        (RequestConstraint.verifyMask on the device) and the states are advanced by the
+        accepted drafts and the decided token. stats: a list of B MTPStats, one per
+        request, each given its round (depth defaults to k). Returns strim_verify's
+        outputs plus "keys" [B, k + 1]."""
         B, k1, _ = target.shape
-        mask = None
-        vkeys = None
-        if keys is not None:
-            if self.grammar is None:
-                raise ValueError("keys need a grammar")
-            vkeys, words = self.grammar.verify_masks(keys, drafts)
-            mask = words.view(B, k1, -1)
+        mask = vkeys = None
+        if states is not None:
+            self._need_grammar()
+            vkeys = self.grammar.request_keys(states, drafts)
+            mask = self.grammar.masks(vkeys.reshape(-1)).view(B, k1, -1)
         out = self.ctx.verify(target, drafts, params, mask=mask, noise_mode=noise_mode, **kw)
         out["keys"] = vkeys
+        if states is not None:
+            self.grammar.request_advance(states, out["token"], drafts, out["accepted"])
         if stats is not None:
             acc = out["accepted"].cpu().numpy()  # the round's one host read
             d = np.full(B, k1 - 1) if depth is None else np.broadcast_to(np.asarray(depth), (B,))
             for b in range(B):
                 stats[b].record_round(int(d[b]), int(acc[b]))
         return out
+
+
+class SpecRounds:
+    """SpecStream's output-position bookkeeping for B sampled requests
+    (SpecStream.swift:48-55,248-256,310-317) on top of BatchPicker.
+
+    Every request keeps `sample_index`, the output position of the token its next round
+    decides first (enableSampling's nextIndex, 1 after sampleFirst took position 0). A
+    verify round samples its row j at position sample_index + j (SpecSampling.verify's
+    firstIndex) and then advances it by accepted + 1; a round without drafts samples at
+    sample_index and advances it by one. Greedy requests (T <= 0) keep their index, as the
+    reference's greedy branch has none. The per-request positions go into the params'
+    `position` field, so the noise of every decision is keyed exactly as the reference
+    keys it.
+    """
+
+    def __init__(self, picker: BatchPicker, params, states: torch.Tensor | None = None,
+                 next_index: int = 1):
+        self.picker = picker
+        self.params = np.array(params, copy=True)
+        self.states = states
+        self.sample_index = np.full(len(self.params), next_index, dtype=np.uint64)
+        self.stats = [MTPStats() for _ in range(len(self.params))]
+
+    def _sampled(self) -> np.ndarray:
+        return self.params["temperature"] > 0
+
+    def _params_now(self) -> np.ndarray:
+        p = self.params.copy()
+        p["position"] = self.sample_index
+        return p
+
+    def round(self, target: torch.Tensor, drafts: torch.Tensor, noise_mode: int = 1,
+              depth=None) -> dict:
+        """One verify round (SpecStream.round's verify branch); returns strim_verify's
+        outputs. Reads the B accepted counts on the host once."""
+        out = self.picker.verify_round(target, drafts, self._params_now(), stats=self.stats,
+                                       states=self.states, depth=depth, noise_mode=noise_mode)
+        acc = out["accepted"].cpu().numpy().astype(np.uint64)
+        self.sample_index += np.where(self._sampled(), acc + 1, 0).astype(np.uint64)
+        return out
+
+    def plain(self, logits: torch.Tensor, noise_mode: int = 1):
+        """A round without drafts (SpecStream.round's depth-0 branch): one token per
+        request at its sample_index."""
+        ids, status, keys = self.picker.pick(logits, self._params_now(), states=self.states,
+                                             noise_mode=noise_mode)
+        self.sample_index += self._sampled().astype(np.uint64)
+        for s in self.stats:
+            s.record_round(0, 0)
+        return ids, status, keys

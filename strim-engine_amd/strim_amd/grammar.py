@@ -7,6 +7,11 @@ vocabulary bytes, the DFA and the per-state mask cache live on the GPU, masks co
 the packed u32 words `Context.sample` / `Context.verify` take, and verify-row keys are
 stepped by the drafts on the device (RequestConstraint.verifyMask,
 RequestConstraint.swift:134-152). Keys: a DFA state (>= 0), FREE (-1) or forced(id).
+
+Per-request constraint state (RequestConstraint.State with its budget and close id,
+RequestConstraint.swift:62-109) is a device tensor of REQUEST_STATE rows: `request_keys`
+gives the next-token and verify-row keys (the thinking budget's forced close id included)
+and `request_advance` steps the states by the emitted tokens, both on the device.
 """
 from __future__ import annotations
 
@@ -20,6 +25,33 @@ from . import _native as N
 FREE = -1
 ACCEPTING = 1  # STRIM_DFA_ACCEPTING
 CONSUMING = 2  # STRIM_DFA_CONSUMING
+
+
+# strim_request_state: {g, in_think, count, budget, close_id, violated}
+REQUEST_STATE = np.dtype([("g", "<i4"), ("in_think", "<i4"), ("count", "<i4"),
+                          ("budget", "<i4"), ("close_id", "<i4"), ("violated", "<i4")])
+
+
+def request_states(n: int, grammar_state=-1, in_think=False, budget=None, close_id=-1):
+    """Host REQUEST_STATE rows for new requests (RequestConstraint.init,
+    RequestConstraint.swift:79-83): grammar_state is the DFA start (-1 for no grammar),
+    in_think the startsInThink flag, budget None for no thinking budget."""
+    s = np.zeros(n, dtype=REQUEST_STATE)
+    s["g"] = grammar_state
+    s["in_think"] = np.asarray(in_think, dtype=np.int32)
+    s["budget"] = -1 if budget is None else budget
+    s["close_id"] = close_id
+    return s
+
+
+def states_to_device(states: np.ndarray, device: int = 0) -> torch.Tensor:
+    """REQUEST_STATE rows -> int32 [n, 6] on the GPU (the C struct's layout)."""
+    a = np.ascontiguousarray(states, dtype=REQUEST_STATE).view(np.int32).reshape(-1, 6)
+    return torch.from_numpy(a.copy()).to(f"cuda:{device}")
+
+
+def states_from_device(t: torch.Tensor) -> np.ndarray:
+    return np.ascontiguousarray(t.cpu().numpy(), dtype=np.int32).view(REQUEST_STATE).reshape(-1)
 
 
 def forced(token_id: int) -> int:
@@ -139,3 +171,45 @@ class DeviceGrammar:
         masks [B * (k + 1)][words]) with the rows in the order strim_verify reads them."""
         keys = self.advance(state, drafts, stream)
         return keys, self.masks(keys.reshape(-1), stream=stream)
+
+    # ---- per-request constraint state --------------------------------------------
+    @staticmethod
+    def _check_states(states: torch.Tensor) -> int:
+        if states.dtype != torch.int32 or not states.is_cuda or states.dim() != 2 \
+                or states.shape[1] != 6 or not states.is_contiguous():
+            raise ValueError("states must be a contiguous int32 CUDA tensor [B, 6]")
+        return states.shape[0]
+
+    def request_keys(self, states: torch.Tensor, drafts: torch.Tensor | None = None,
+                     stream=None) -> torch.Tensor:
+        """RequestConstraint.key / verifyMask on the device: keys [B][k + 1] of the next
+        row and of the rows after each draft (states unchanged)."""
+        B = self._check_states(states)
+        if drafts is not None and drafts.numel() > 0:
+            drafts = drafts.reshape(B, -1).to(torch.int32).contiguous()
+            k = drafts.shape[1]
+        else:
+            drafts, k = None, 0
+        out = torch.empty((B, k + 1), dtype=torch.int32, device=states.device)
+        N.check(N.lib().strim_request_keys(self.handle, _stream(stream), _ptr(states), B,
+                                           _ptr(drafts), k, _ptr(out)),
+                "strim_request_keys")
+        return out
+
+    def request_advance(self, states: torch.Tensor, last: torch.Tensor,
+                        drafts: torch.Tensor | None = None,
+                        accepted: torch.Tensor | None = None, stream=None) -> None:
+        """RequestConstraint.advance on the device, in place: each request takes
+        drafts[b][0 .. accepted[b]) and then last[b] (strim_verify's outputs), or last[b]
+        alone (strim_sample's)."""
+        B = self._check_states(states)
+        last = last.reshape(B).to(torch.int32).contiguous()
+        if drafts is not None and drafts.numel() > 0:
+            drafts = drafts.reshape(B, -1).to(torch.int32).contiguous()
+            k = drafts.shape[1]
+        else:
+            drafts, k = None, 0
+        acc = None if accepted is None else accepted.reshape(B).to(torch.int32).contiguous()
+        N.check(N.lib().strim_request_advance(self.handle, _stream(stream), _ptr(states), B,
+                                              _ptr(drafts), k, _ptr(acc), _ptr(last)),
+                "strim_request_advance")

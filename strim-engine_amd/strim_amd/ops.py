@@ -48,11 +48,17 @@ def _check_cuda(*ts):
             raise ValueError("tensor arguments must be contiguous")
 
 
+def _row_stride(t: torch.Tensor) -> int:
+    """Elements between rows (a single row may carry any stride, e.g. 0 from a
+    broadcast view: its own length is passed)."""
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
 def _check_rows(t: torch.Tensor) -> None:
     """Logits may have a row stride > V, but each row must be contiguous."""
     if not t.is_cuda:
         raise ValueError("logits must be on the GPU")
-    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+    if t.dim() != 2 or t.stride(1) != 1 or _row_stride(t) < t.shape[1]:
         raise ValueError("logits must be [R, V] with contiguous rows (row stride >= V)")
 
 
@@ -123,7 +129,7 @@ class Context:
         H = 0 if history is None else history.shape[-1]
         mstride = 0 if mask is None else mask.shape[-1]
         rc = N.lib().strim_sample(self._h, _stream(stream), _ptr(logits), _dtype_code(logits),
-                                  B, V, logits.stride(0), _pp(p), _ptr(mask), mstride,
+                                  B, V, _row_stride(logits), _pp(p), _ptr(mask), mstride,
                                   _ptr(history), _ptr(history_len), H, noise_mode, _ptr(noise),
                                   _ptr(out_ids), _ptr(out_status), _ptr(probs))
         N.check(rc, "strim_sample")
@@ -153,7 +159,7 @@ class Context:
         H = 0 if history is None else history.shape[-1]
         mstride = 0 if mask is None else mask.shape[-1]
         args = [self._h, None, _ptr(logits), _dtype_code(logits), B, V,
-                logits.stride(0), _pp(p), _ptr(mask), mstride, _ptr(history), _ptr(history_len),
+                _row_stride(logits), _pp(p), _ptr(mask), mstride, _ptr(history), _ptr(history_len),
                 H, noise_mode, _ptr(noise), _ptr(out_ids), _ptr(out_status), None]
         keep = (logits, p, mask, history, history_len, noise, out_ids, out_status)
         return BoundCall(N.lib().strim_sample, args, keep, out_ids, out_status, stream)
@@ -210,7 +216,7 @@ def mask_logits(logits: torch.Tensor, mask_words: torch.Tensor | None, stream=No
     out = torch.empty(R, V, dtype=torch.float32, device=logits.device)
     mstride = 0 if mask_words is None else mask_words.shape[-1]
     N.check(N.lib().strim_mask_logits(_stream(stream), _ptr(logits), _dtype_code(logits), R, V,
-                                      logits.stride(0), _ptr(mask_words), mstride, _ptr(out)),
+                                      _row_stride(logits), _ptr(mask_words), mstride, _ptr(out)),
             "strim_mask_logits")
     return out
 
@@ -225,7 +231,7 @@ def draft_argmax(draft_logits: torch.Tensor, draft_to_full: torch.Tensor | None 
     _check_cuda(draft_to_full)
     out = torch.empty(R, dtype=torch.int32, device=draft_logits.device)
     N.check(N.lib().strim_draft_argmax(_stream(stream), _ptr(draft_logits),
-                                       _dtype_code(draft_logits), R, Vd, draft_logits.stride(0),
+                                       _dtype_code(draft_logits), R, Vd, _row_stride(draft_logits),
                                        _ptr(draft_to_full), _ptr(out)), "strim_draft_argmax")
     return out
 

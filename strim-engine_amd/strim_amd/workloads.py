@@ -15,6 +15,8 @@ any host-side check. Shapes and distributions follow the configuration table:
         ascending injective table, drafts sampled from q = softmax(draft/T), T 0.7
   cfg5  B=64 bf16: 70 % rows N(0,2^2), 30 % rows with one +20 logit; 2,048-token
         history; 5 % masks; T 0.8, top-k 40, top-p 0.95, min-p 0.02, per-row seed
+  n1    the north-star chain: cfg2 logits and penalty history + cfg3 masks, T 0.8,
+        top-p 0.9 (no top-k, no min-p)
 """
 from __future__ import annotations
 
@@ -95,9 +97,11 @@ def cfg2(seed=2, B=8, V=V_DEFAULT, H=4096):
                 history_len=np.full(B, H, np.int32), mask=None, noise=noise)
 
 
-def cfg3(seed=3, B=8, V=V_DEFAULT):
-    rng = np.random.default_rng(seed)
-    x, _ = _cfg2_logits(rng, B, V)
+def _cfg3_masks(rng, x_proc, T=0.8, P=0.9):
+    """cfg3's allow masks over B rows: densities 0.01/1/10/30 % (clustered runs of 64 for
+    the first four rows, scattered for the next four), one row allowing exactly one token
+    and one row whose top-p nucleus (of the penalised logits x_proc at T, P) is masked."""
+    B, V = x_proc.shape
     dens = [0.0001, 0.01, 0.10, 0.30]
     allowed = np.zeros((B, V), dtype=bool)
     for r in range(B):
@@ -113,19 +117,56 @@ def cfg3(seed=3, B=8, V=V_DEFAULT):
     # edge: one row allows exactly one token
     allowed[B - 2] = False
     allowed[B - 2, int(rng.integers(0, V))] = True
-    # edge: one row's top-p mass (at T 0.8, p 0.9) lies entirely in masked tokens
+    # edge: one row's top-p mass (at T, P) lies entirely in masked tokens
     r = B - 1
-    l = x[r] / np.float32(0.8)
+    l = x_proc[r] / np.float32(T)
     order = np.argsort(-l.astype(np.float64), kind="stable")
     w = np.exp(l[order].astype(np.float64) - l[order[0]])
-    cut = int(np.searchsorted(np.cumsum(w) / w.sum(), 0.9)) + 1
+    cut = int(np.searchsorted(np.cumsum(w) / w.sum(), P)) + 1
     allowed[r] = rng.random(V) < 0.3
     allowed[r, order[:cut]] = False
+    return allowed
+
+
+def cfg3(seed=3, B=8, V=V_DEFAULT):
+    rng = np.random.default_rng(seed)
+    x, _ = _cfg2_logits(rng, B, V)
+    allowed = _cfg3_masks(rng, x)
     params = params_array(B, temperature=0.8, top_p=0.9,
                           seed=rng.integers(0, 2**63, size=B, dtype=np.uint64), position=11)
     noise = rng.random((B, 2), dtype=np.float32)
     return dict(x=x, dtype="bf16", params=params, history=None, history_len=None,
                 mask=pack_mask(allowed), allowed=allowed, noise=noise)
+
+
+def penalised(x, history, presence=0.5, frequency=0.3):
+    """The penalty stage of the chain on float32 values (v - f*c - p for ids seen c > 0
+    times), each step one float32 rounding as the kernels round it."""
+    out = np.array(x, dtype=np.float32, copy=True)
+    for r in range(out.shape[0]):
+        c = np.bincount(history[r], minlength=out.shape[1])[:out.shape[1]].astype(np.float32)
+        hit = c > 0
+        v = out[r, hit] - np.float32(frequency) * c[hit]
+        out[r, hit] = v - np.float32(presence)
+    return out
+
+
+def n1(seed=6, B=8, V=V_DEFAULT, H=4096):
+    """The north-star chain: cfg2's logits and 4,096-id Zipf penalty history (presence
+    0.5, frequency 0.3), cfg3's masks (every density, both placements, the one-token row
+    and the masked-nucleus row), then T 0.8 and top-p 0.9 without top-k or min-p, one
+    uniform per row."""
+    rng = np.random.default_rng(seed)
+    x, perm = _cfg2_logits(rng, B, V)
+    hist = np.stack([zipf_ids(rng, H, V, perm) for _ in range(B)]).astype(np.int32)
+    allowed = _cfg3_masks(rng, penalised(x, hist))
+    params = params_array(B, temperature=0.8, top_p=0.9, presence_penalty=0.5,
+                          frequency_penalty=0.3,
+                          seed=rng.integers(0, 2**63, size=B, dtype=np.uint64), position=13)
+    noise = rng.random((B, 2), dtype=np.float32)
+    return dict(x=x, dtype="bf16", params=params, history=hist,
+                history_len=np.full(B, H, np.int32), mask=pack_mask(allowed), allowed=allowed,
+                noise=noise)
 
 
 def cfg4(seed=4, B=4, k=3, V=V_DEFAULT, Vd=VD_DEFAULT, T=0.7):

@@ -93,13 +93,72 @@ def test_bounded_counters_expose_overflow():
 
 
 # ------------------------------------------------------------------ GPU ----
+def _budget_oracle_states(O, G):
+    """RequestConstraint.budget test fixture (GrammarTests.swift:356-371) on the oracle."""
+    from strim_amd.grammar import request_states
+
+    V = G.FAKE_VOCAB
+    width = len(V) + 8
+    close = V.index(b"</think>")
+    go = O.GrammarOracle(V, width, [G.FAKE_EOS], G.FAKE_SKIP)
+    go.set_dfa(*G.object_int_dfa())
+    st = request_states(1, grammar_state=-1, in_think=True, budget=3, close_id=close)
+    return go, st, close
+
+
+def test_oracle_thinking_budget(oracle_mod):
+    # GrammarTests.swift:356-371: free while thinking under the budget, forced close id
+    # once three thinking tokens are spent, free again after the close id
+    import grammar_util as G
+
+    go, st, close = _budget_oracle_states(oracle_mod, G)
+    assert go.request_keys(st)[0, 0] == -1
+    st = go.request_advance(st, [65])
+    st = go.request_advance(st, [66])
+    assert go.request_keys(st)[0, 0] == -1
+    st = go.request_advance(st, [67])
+    key = int(go.request_keys(st)[0, 0])
+    assert key == -2 - close
+    m = go.mask(key)
+    bits = np.unpackbits(m.view(np.uint8), bitorder="little")
+    assert bits.sum() == 1 and bits[close] == 1
+    st = go.request_advance(st, [close])
+    assert go.request_keys(st)[0, 0] == -1 and st["in_think"][0] == 0 and st["count"][0] == 3
+
+
+def test_oracle_request_keys_walk(oracle_mod):
+    # the verify walk across the thinking boundary: drafts "a", close, "{" from a request
+    # one token short of its budget whose grammar starts at state 0
+    import grammar_util as G
+    from strim_amd.grammar import request_states
+
+    O = oracle_mod
+    V = G.FAKE_VOCAB
+    go = O.GrammarOracle(V, len(V) + 8, [G.FAKE_EOS], G.FAKE_SKIP)
+    nt, fl = G.object_int_dfa()
+    go.set_dfa(nt, fl)
+    close = V.index(b"</think>")
+    st = request_states(1, grammar_state=0, in_think=True, budget=2, close_id=close)
+    st["count"] = 1
+    a, op, x = V.index(b"a"), V.index(b"{"), V.index(b"x")
+    keys = go.request_keys(st, [[a, close, op, x]])[0].tolist()
+    g1 = go.advance(0, b"{")
+    # row 0 free (count 1 < 2); after "a" the budget is spent: forced close; after the
+    # close id the grammar's start state; after "{" its successor; "x" then kills it
+    assert keys == [-1, -2 - close, 0, g1, -1]
+    # advancing by the same tokens: "x" steps the grammar dead and marks the violation
+    st2 = go.request_advance(st, [x], [[a, close, op]], [3])
+    assert st2["in_think"][0] == 0 and st2["g"][0] == -1 and st2["violated"][0] == 1
+
+
 @pytest.mark.gpu
 def test_gpu_batch_pick_equals_per_row_loop(oracle_mod, ctx):
     import torch
 
     import grammar_util as G
     from strim_amd.batch import BatchPicker
-    from strim_amd.grammar import DeviceGrammar, FREE, forced
+    from strim_amd.grammar import (DeviceGrammar, request_states, states_from_device,
+                                   states_to_device)
 
     O = oracle_mod
     V = G.FAKE_VOCAB
@@ -111,23 +170,67 @@ def test_gpu_batch_pick_equals_per_row_loop(oracle_mod, ctx):
     go.set_dfa(nt, fl)
     rng = np.random.default_rng(21)
     B = 8
-    keys = np.array([0, 5, 7, FREE, forced(40), 1, FREE, 5], dtype=np.int32)
+    close = V.index(b"</think>")
+    # grammar rows, a row without grammar, thinking rows under and at their budget
+    st = request_states(B, grammar_state=[0, 5, 7, -1, 0, 1, 0, 5],
+                        in_think=[0, 0, 0, 0, 1, 0, 1, 0], budget=4, close_id=close)
+    st["count"] = [0, 0, 0, 0, 4, 0, 1, 0]
     T = np.array([0.0, 0.8, 1.0, 0.0, 0.7, 1.2, 0.9, 0.0])
     p = O.make_params(B, temperature=T, top_k=rng.choice([0, 20], size=B),
                       top_p=rng.choice([1.0, 0.9], size=B), seed=np.arange(B, dtype=np.uint64),
                       position=3)
     x = rng.normal(0, 2.0, size=(B, width)).astype(np.float32)
     picker = BatchPicker(ctx, g)
-    ids, status, nxt = picker.pick(torch.from_numpy(x).cuda(), p,
-                                   torch.from_numpy(keys).cuda())
-    ids, status, nxt = ids.cpu().numpy(), status.cpu().numpy(), nxt.cpu().numpy()
+    sd = states_to_device(st)
+    ids, status, keys = picker.pick(torch.from_numpy(x).cuda(), p, sd)
+    ids, status, keys = ids.cpu().numpy(), status.cpu().numpy(), keys.cpu().numpy()
+    ref_keys = go.request_keys(st)[:, 0]
+    np.testing.assert_array_equal(keys, ref_keys)
+    assert keys[4] == -2 - close and keys[6] == -1
     for b in range(B):  # the reference's loop: mask the row, then sample or argmax it
-        m = go.mask(int(keys[b]))[None]
+        m = go.mask(int(ref_keys[b]))[None]
         ref = O.sample(x[b:b + 1], p[b:b + 1], mask=m)
         assert status[b] == 0 and ids[b] == ref["token"][0], (b, ids[b], ref["token"][0])
-        k = int(keys[b])
-        want = go.advance(k, V[ids[b]]) if 0 <= k < len(fl) and ids[b] < len(V) else k
-        assert nxt[b] == want
+    assert ids[4] == close
+    want = go.request_advance(st, ids)
+    got = states_from_device(sd)
+    np.testing.assert_array_equal(got.view(np.int32), want.view(np.int32))
+    g.close()
+
+
+@pytest.mark.gpu
+def test_gpu_thinking_budget(oracle_mod, ctx):
+    # GrammarTests.swift:356-371 through the device state machine
+    import torch
+
+    import grammar_util as G
+    from strim_amd.grammar import DeviceGrammar, states_from_device, states_to_device
+
+    go, st, close = _budget_oracle_states(oracle_mod, G)
+    V = G.FAKE_VOCAB
+    g = DeviceGrammar(V, len(V) + 8, eos=[G.FAKE_EOS], skip=G.FAKE_SKIP)
+    g.set_dfa(*G.object_int_dfa())
+    sd = states_to_device(st)
+
+    def key():
+        return int(g.request_keys(sd)[0, 0].item())
+
+    def emit(t):
+        g.request_advance(sd, torch.tensor([t], dtype=torch.int32, device="cuda"))
+
+    assert key() == -1
+    emit(65)
+    emit(66)
+    assert key() == -1
+    emit(67)
+    assert key() == -2 - close
+    m = g.mask(key()).cpu().numpy()
+    bits = np.unpackbits(m.view(np.uint8), bitorder="little")
+    assert bits.sum() == 1 and bits[close] == 1
+    emit(close)
+    assert key() == -1
+    s = states_from_device(sd)
+    assert s["in_think"][0] == 0 and s["count"][0] == 3
     g.close()
 
 
@@ -137,8 +240,9 @@ def test_gpu_constrained_round_records_stats(oracle_mod, ctx):
 
     import grammar_util as G
     from gpu_util import dev_logits
-    from strim_amd.batch import BatchPicker
-    from strim_amd.grammar import DeviceGrammar, FREE
+    from strim_amd.batch import BatchPicker, SpecRounds
+    from strim_amd.grammar import (DeviceGrammar, request_states, states_from_device,
+                                   states_to_device)
 
     O = oracle_mod
     V = G.FAKE_VOCAB
@@ -152,25 +256,41 @@ def test_gpu_constrained_round_records_stats(oracle_mod, ctx):
     B, k = 3, 3
     op, q, a, x = V.index(b"{"), V.index(b"\""), V.index(b"a"), V.index(b"x")
     drafts = np.array([[op, q, a], [op, x, op], [1, 2, 3]], dtype=np.int32)
-    keys = np.array([0, 0, FREE], dtype=np.int32)
+    st = request_states(B, grammar_state=[0, 0, -1])
     tgt = rng.normal(0, 1.0, size=(B, k + 1, width)).astype(np.float32)
     for b in range(B):  # make the drafts likely so that some are accepted
         for j in range(k):
             tgt[b, j, drafts[b, j]] += 6.0
-    p = O.make_params(B, temperature=1.0, seed=np.array([3, 4, 5], dtype=np.uint64),
-                      position=1)
-    stats = [MTPStats() for _ in range(B)]
-    out = BatchPicker(ctx, g).verify_round(dev_logits(tgt, "f32"), torch.from_numpy(drafts).cuda(),
-                                           p, stats=stats, keys=torch.from_numpy(keys).cuda())
-    vk = go.verify_keys(keys, drafts)
+    p = O.make_params(B, temperature=1.0, seed=np.array([3, 4, 5], dtype=np.uint64))
+    sd = states_to_device(st)
+    rounds = SpecRounds(BatchPicker(ctx, g), p, states=sd, next_index=1)
+    out = rounds.round(dev_logits(tgt, "f32"), torch.from_numpy(drafts).cuda(), noise_mode=0)
+    vk = go.request_keys(st, drafts)
     assert np.array_equal(out["keys"].cpu().numpy(), vk)
     masks = np.stack([np.stack([go.mask(int(kk)) for kk in row]) for row in vk])
-    ref = O.verify(tgt, k, drafts, p, mask=masks)
+    p1 = p.copy()
+    p1["position"] = 1  # SpecSampling.verify's firstIndex = sampleIndex (SpecStream.swift:249)
+    ref = O.verify(tgt, k, drafts, p1, mask=masks)
     acc = out["accepted"].cpu().numpy()
     assert np.array_equal(acc, ref["accepted"]), (acc, ref["accepted"])
+    assert np.array_equal(out["token"].cpu().numpy(), ref["token"])
     assert acc[1] <= 1  # "x" after "{" is masked out: the second draft is never accepted
     for b in range(B):
         s = MTPStats()
         s.record_round(k, int(ref["accepted"][b]))
-        assert stats[b] == s
+        assert rounds.stats[b] == s
+    # sampleIndex += accepted + 1 (SpecStream.swift:255)
+    np.testing.assert_array_equal(rounds.sample_index, 1 + ref["accepted"] + 1)
+    want = go.request_advance(st, ref["token"], drafts, ref["accepted"])
+    np.testing.assert_array_equal(states_from_device(sd).view(np.int32), want.view(np.int32))
+    # a round without drafts samples at the advanced index (SpecStream.swift:315-317)
+    x0 = rng.normal(0, 1.0, size=(B, width)).astype(np.float32)
+    idx_before = rounds.sample_index.copy()
+    keys0 = go.request_keys(want)[:, 0]
+    ids, status, _ = rounds.plain(torch.from_numpy(x0).cuda(), noise_mode=0)
+    p2 = p.copy()
+    p2["position"] = idx_before
+    ref0 = O.sample(x0, p2, mask=np.stack([go.mask(int(kk)) for kk in keys0]))
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref0["token"])
+    np.testing.assert_array_equal(rounds.sample_index, idx_before + 1)
     g.close()

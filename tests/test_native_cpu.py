@@ -38,7 +38,7 @@ def test_default_params_are_reference_defaults():
 
 
 @pytest.mark.parametrize("field,value,ok", [
-    ("temperature", 0.0, True), ("temperature", -0.1, False), ("temperature", np.nan, False),
+    ("temperature", 0.0, True), ("temperature", -0.1, True), ("temperature", np.nan, False),
     ("top_p", 1.0, True), ("top_p", 0.0, False), ("top_p", 1.01, False),
     ("top_k", 0, True), ("top_k", -1, False),
     ("min_p", 1.0, True), ("min_p", -0.01, False),
@@ -46,7 +46,8 @@ def test_default_params_are_reference_defaults():
     ("flags", 7, True), ("flags", 8, False),
 ])
 def test_check_params_mirrors_request_validation(field, value, ok):
-    # ChatRequest.parse (Sources/StrimServer/ChatRequest.swift:150-160)
+    # GenParams as the engine takes it (T <= 0 greedy, EngineAPI.swift:66) and the
+    # ChatRequest.parse ranges (Sources/StrimServer/ChatRequest.swift:150-160)
     from strim_amd import _native as N
 
     p = N.params_array(3)

@@ -362,3 +362,24 @@ def test_bf16_round_matches_torch():
     ours = workloads.bf16_round(x)
     theirs = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
     np.testing.assert_array_equal(ours, theirs)
+
+
+def test_verify_row_error_counts_only_when_reached(oracle_mod):
+    # SpecSampling.verify consumes rows 0..n alone (SpecSampling.swift:101-105): a bad row
+    # after the first rejection leaves the sequence's result alone; a reached one fails it
+    O = oracle_mod
+    rng = np.random.default_rng(17)
+    V, k = 300, 3
+    tgt = rng.normal(size=(3, k + 1, V)).astype(np.float32)
+    allowed = np.ones((3, k + 1, V), bool)
+    allowed[:, 0, 9] = False           # draft 9 is masked at row 0: rejected for sure
+    allowed[1, 2, :] = False           # sequence 1: row 2 allows nothing
+    drafts = np.array([[9, V + 5, 7], [9, 5, 6], [V + 5, 1, 2]], np.int32)
+    p = O.make_params(3, temperature=1.0, seed=4)
+    for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+        r = O.verify(tgt, k, drafts, p, mask=O.pack_mask(allowed), noise_mode=mode)
+        assert r["status"].tolist() == [O.STRIM_OK, O.STRIM_OK, O.STRIM_EINVAL]
+        assert r["accepted"].tolist() == [0, 0, 0]
+        assert r["token"][0] >= 0 and r["token"][0] != 9 and r["token"][1] >= 0
+        assert r["token"][2] == -1
+        assert r["row_token"][0, 1] == -1 and r["row_token"][1, 2] == -1

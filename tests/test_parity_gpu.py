@@ -35,7 +35,7 @@ def _sweep_case(rng, V, B):
     hist = rng.integers(-2, V + 2, size=(B, H)).astype(np.int32) if H else None
     hl = rng.integers(0, H + 1, size=B).astype(np.int32) if H else None
     p = O.make_params(
-        B, temperature=rng.choice([0.0, 0.5, 0.8, 1.0, 1.5], size=B),
+        B, temperature=rng.choice([0.0, -0.5, 0.5, 0.8, 1.0, 1.5], size=B),
         top_k=rng.choice([0, 0, 1, 5, 40, V, V + 3], size=B),
         top_p=rng.choice([1.0, 0.95, 0.8, 0.3], size=B),
         min_p=rng.choice([0.0, 0.0, 0.02, 0.2], size=B),
@@ -122,6 +122,25 @@ def test_cfg3_masks(ctx, mode):
     for r in range(len(ids)):
         assert w["allowed"][r, ids[r]]
     assert ids[6] == int(np.nonzero(w["allowed"][6])[0][0])
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_ICDF, O.NOISE_GUMBEL])
+@pytest.mark.parametrize("injected", [False, True])
+def test_n1_north_star_chain(ctx, mode, injected):
+    # B=8 x V=151,936 bf16: presence/frequency penalties over 4,096 history ids, cfg3's
+    # masks (every density and edge row), T 0.8, top-p 0.9, no top-k or min-p
+    w = W.n1()
+    B, V = w["x"].shape
+    noise = None
+    if injected:
+        noise = w["noise"] if mode == O.NOISE_ICDF else np.random.default_rng(19).random(
+            (B, V + 1), dtype=np.float32)
+    say(f"n1 mode={mode} injected={injected}")
+    ids, st, ref = check_sample(ctx, w["x"], w["params"], "bf16", w["mask"], w["history"],
+                                w["history_len"], mode, noise, label="n1")
+    assert (st == 0).all()
+    for r in range(B):
+        assert w["allowed"][r, ids[r]]
 
 
 def test_cfg5_stress_batch(ctx):
@@ -328,6 +347,26 @@ def test_verify_random(ctx, k):
             say(f"verify k={k} it={it} B={B} V={V} mode={mode}")
             check_verify(ctx, tgt, k, drafts, p, "bf16", mask, hist, None, mode,
                          label=f"verify k={k} it={it}")
+
+
+def test_verify_error_after_rejection(ctx):
+    # a bad draft or an empty row after the first rejection leaves the sequence alone;
+    # only the rows the accept chain reaches count (SpecSampling.swift:101-105)
+    rng = np.random.default_rng(17)
+    V, k = 300, 3
+    tgt = rng.normal(size=(3, k + 1, V)).astype(np.float32)
+    allowed = np.ones((3, k + 1, V), bool)
+    allowed[:, 0, 9] = False
+    allowed[1, 2, :] = False
+    drafts = np.array([[9, V + 5, 7], [9, 5, 6], [V + 5, 1, 2]], np.int32)
+    p = O.make_params(3, temperature=1.0, seed=4)
+    for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+        say(f"verify error after rejection mode={mode}")
+        g, ref = check_verify(ctx, tgt, k, drafts, p, "f32", W.pack_mask(allowed),
+                              noise_mode=mode, label="error-after-reject")
+        assert g["status"].tolist() == [0, 0, O.STRIM_EINVAL]
+        assert g["token"][2] == -1 and g["token"][0] == ref["token"][0]
+        assert g["row_token"][0, 1] == -1 and g["row_token"][1, 2] == -1
 
 
 # ------------------------------------------------------------ general-q verify ----
