@@ -52,7 +52,7 @@ extern "C" {
 #define STRIM_EEMPTY (-2)     /* the row allows no token (all-zero mask or all -inf)    */
 #define STRIM_ENONFINITE (-3) /* NaN or +inf logit in an allowed position              */
 #define STRIM_ECAPACITY (-4)  /* the call exceeds a fixed capacity: V above the
-                                 context's max_vocab                                    */
+                                 context's max_vocab, or the no-allocation limits      */
 #define STRIM_EHIP (-5)       /* HIP runtime error                                      */
 #define STRIM_ENOMEM (-6)     /* device allocation failed                              */
 
@@ -137,6 +137,23 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
                  const uint32_t* mask_words, int64_t mask_stride, const int32_t* history,
                  const int32_t* history_len, int32_t H, int32_t noise_mode, const float* noise,
                  int32_t* out_ids, int32_t* out_status, float* out_probs);
+
+/* strim_sample without a context, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart
+ * in the reference. Arguments as strim_sample, without out_probs. Its scratch is a fixed
+ * device array inside the library, one per GPU (held until the process ends), so the call
+ * allocates nothing: V above STRIM_NOALLOC_MAX_VOCAB returns STRIM_ECAPACITY, and B rows
+ * run in groups of STRIM_NOALLOC_MAX_ROWS. Every call on a GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (two streams, two threads) race, so issue them on
+ * one stream. Runs on the current device. */
+#define STRIM_NOALLOC_MAX_ROWS 32
+#define STRIM_NOALLOC_MAX_VOCAB 262144
+int strim_sample_noalloc(void* stream, const void* logits, int32_t dtype, int32_t B, int32_t V,
+                         int64_t row_stride, const strim_sampling_params* params,
+                         const uint32_t* mask_words, int64_t mask_stride,
+                         const int32_t* history, const int32_t* history_len, int32_t H,
+                         int32_t noise_mode, const float* noise, int32_t* out_ids,
+                         int32_t* out_status);
 
 /* Speculative verification of k drafts for B independent sequences.
  *   target_logits [B][k+1][V] (row j = target distribution after the pending token and

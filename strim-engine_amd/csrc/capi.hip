@@ -7,6 +7,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "stream.hpp"
 
 namespace strim {
@@ -310,6 +312,38 @@ int sample_groups(strim_ctx* ctx, const Scratch& sc, int gmax, void* stream, con
   return STRIM_OK;
 }
 
+constexpr ScratchLayout kNoallocLayout =
+    scratch_layout((size_t)STRIM_NOALLOC_MAX_ROWS, (size_t)STRIM_NOALLOC_MAX_VOCAB, false);
+static_assert(kNoallocLayout.bytes <= (size_t)16 << 20, "no-allocation scratch stays modest");
+
+}  // namespace
+
+// ---- the no-allocation entry point's scratch -------------------------------------------
+// strim_sample_noalloc draws its scratch from this file-scope device array: one copy per
+// GPU, at its own address, held until the process ends, zero at load. Its host-side name
+// is not a device address: host code uses only the pointer noalloc_base returns.
+static __device__ __align__(256) unsigned char noalloc_scratch[kNoallocLayout.bytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+char* g_noalloc_ptr[kMaxDevices] = {};
+
+// The device address of `device`'s noalloc_scratch, looked up once per device with that
+// device current (the caller's current device).
+int noalloc_base(int device, char** out) {
+  if (device < 0 || device >= kMaxDevices) return STRIM_EINVAL;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[device]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch)) != hipSuccess || !p)
+      return STRIM_EHIP;
+    g_noalloc_ptr[device] = (char*)p;
+  }
+  *out = g_noalloc_ptr[device];
+  return STRIM_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -406,6 +440,27 @@ int strim_sample(strim_ctx* ctx, void* stream, const void* logits, int32_t dtype
                          mask_words, mask_stride, history, history_len, H, noise_mode, noise,
                          out_ids, out_status, out_probs);
   });
+}
+
+int strim_sample_noalloc(void* stream, const void* logits, int32_t dtype, int32_t B, int32_t V,
+                         int64_t row_stride, const strim_sampling_params* params,
+                         const uint32_t* mask_words, int64_t mask_stride,
+                         const int32_t* history, const int32_t* history_len, int32_t H,
+                         int32_t noise_mode, const float* noise, int32_t* out_ids,
+                         int32_t* out_status) {
+  const int rc = check_sample_args(logits, dtype, B, V, row_stride, params, mask_words,
+                                   mask_stride, history, H, noise_mode, out_ids);
+  if (rc != STRIM_OK) return rc;
+  if (V > STRIM_NOALLOC_MAX_VOCAB) return STRIM_ECAPACITY;
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess) return STRIM_EHIP;
+  char* base = nullptr;
+  const int brc = noalloc_base(device, &base);
+  if (brc != STRIM_OK) return brc;
+  const Scratch sc = scratch_at(base, kNoallocLayout, (size_t)STRIM_NOALLOC_MAX_VOCAB, false);
+  return sample_groups(nullptr, sc, STRIM_NOALLOC_MAX_ROWS, stream, logits, dtype, B, V,
+                       row_stride, params, mask_words, mask_stride, history, history_len, H,
+                       noise_mode, noise, out_ids, out_status, nullptr);
 }
 
 int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_t dtype,

@@ -30,6 +30,7 @@ EXPORTS = (
     "strim_ctx_create",
     "strim_ctx_destroy",
     "strim_sample",
+    "strim_sample_noalloc",
     "strim_verify",
     "strim_mask_logits",
     "strim_draft_argmax",
@@ -45,6 +46,7 @@ EXPORTS = (
     "strim_request_advance",
 )
 KERNEL_COUNT = 8
+NOALLOC_MAX_ROWS, NOALLOC_MAX_VOCAB = 32, 262144  # strim_sample_noalloc limits
 
 
 class StrimError(RuntimeError):
@@ -117,6 +119,9 @@ def lib() -> ctypes.CDLL:
         L.strim_sample.restype = ctypes.c_int
         L.strim_sample.argtypes = [P, P, P, I32, I32, I32, I64, P, P, I64, P, P, I32, I32, P,
                                    P, P, P]
+        L.strim_sample_noalloc.restype = ctypes.c_int
+        L.strim_sample_noalloc.argtypes = [P, P, I32, I32, I32, I64, P, P, I64, P, P, I32, I32,
+                                           P, P, P]
         L.strim_verify.restype = ctypes.c_int
         L.strim_verify.argtypes = [P, P, P, I32, I32, I32, I32, P, I32, P, P, P, P, I64, P, P,
                                    I32, I32, P, P, P, P, P, P]
