@@ -206,7 +206,7 @@ int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, in
  * strim_profile_end synchronises, sums the elapsed time per kernel and turns profiling
  * off. Profiling allocates its events in strim_profile_begin, never in the calls it
  * times. Do not profile calls that are being captured into a graph. */
-#define STRIM_KERNEL_COUNT 8 /* stream, finalize, collect, final, probs, verify_combine,
+#define STRIM_KERNEL_COUNT 8 /* stream, finalize, gfinal, final, probs, verify_combine,
                                 qprep, qres (the five launches of the residual draw of
                                 unfiltered general-q rows, timed together) */
 int strim_profile_begin(strim_ctx* ctx, int32_t max_launches);

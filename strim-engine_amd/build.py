@@ -29,6 +29,7 @@ UNITS = [
     for dt in (1, 0) for pen in (1, 0) for sseg in (1, 4)
 ] + [
     ("finalize_kernels.hip", []),
+    ("gfinal_kernels.hip", []),
     ("sample_kernels.hip", []),
     ("qres_kernels.hip", []),
     ("aux_kernels.hip", []),

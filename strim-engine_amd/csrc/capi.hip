@@ -13,7 +13,7 @@
 
 namespace strim {
 hipError_t launch_finalize(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
-__global__ void k_collect(Args a);
+__global__ void k_gfinal(Args a);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
@@ -137,11 +137,11 @@ int32_t vec_ok(const void* p, int64_t row_stride, int32_t dtype) {
 }
 
 enum KernelId {
-  KID_STREAM = 0, KID_FINALIZE, KID_COLLECT, KID_FINAL, KID_PROBS, KID_COMBINE, KID_QPREP,
+  KID_STREAM = 0, KID_FINALIZE, KID_GFINAL, KID_FINAL, KID_PROBS, KID_COMBINE, KID_QPREP,
   KID_QRES
 };
 const char* const kKernelNames[STRIM_KERNEL_COUNT] = {
-    "k_stream", "k_finalize", "k_collect", "k_final", "k_probs", "k_verify_combine", "k_qprep",
+    "k_stream", "k_finalize", "k_gfinal", "k_final", "k_probs", "k_verify_combine", "k_qprep",
     "k_qres"};
 
 // Runs `launch(e0, e1)`: with profiling on, e0/e1 are the next event pair, which the
@@ -184,34 +184,37 @@ bool nofilter(const strim_sampling_params& p, int32_t V) {
   return !(p.top_k > 0 && p.top_k < V) && !(p.min_p > 0.0f) && !(p.top_p < 1.0f);
 }
 
-// The launch sequence of one row group. k_stream + k_finalize decide greedy, fast and
-// unfiltered Gumbel rows (overflowing fast rows too, by the exact path); general rows
-// add k_collect (second pass) and k_final.
+// The launch sequence of one row group: k_stream, then k_finalize for the greedy, fast
+// and unfiltered Gumbel rows (and the marking of general-q draft rows) and k_gfinal for
+// the general rows, each launched only when some row of the group needs it; general-q
+// verify groups add the residual draw and k_final.
 int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
-  bool need_collect = false, need_final = false, any_pen = false;
+  bool need_fin = false, need_gfin = false, any_pen = false;
+  const bool gq = a.verify && a.dlog != nullptr && a.k > 0;  // general-q draft rows
   for (int i = 0; i < nb; ++i) {
     const strim_sampling_params& q = a.p[i];
     if ((q.repetition_penalty != 1.0f || q.presence_penalty != 0.0f ||
          q.frequency_penalty != 0.0f) && (a.hist != nullptr || a.verify))
       any_pen = true;
-    const int32_t cls = row_class(a.p[i], a.V);
-    if (cls == CLS_GENERAL && !(a.noise_mode == STRIM_NOISE_GUMBEL && nofilter(a.p[i], a.V)))
-      need_collect = true;
+    // the sample row, or a verify sequence's bonus row (and its draft rows without
+    // general-q drafts)
+    if (gfinal_row(q, a.V, a.noise_mode, false)) need_gfin = true;
+    else need_fin = true;
   }
-  // k_final decides the general rows (k_finalize leaves them pending) and the general-q
-  // verify rows
-  need_final = need_collect || (a.verify && a.dlog != nullptr);
+  if (gq) need_fin = true;
+  const bool need_final = gq;  // k_final decides the general-q verify rows
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
   hipError_t e = hipSuccess;
   auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };
   timed(ctx, KID_STREAM,
         [&](hipEvent_t e0, hipEvent_t e1) { keep(launch_stream(a, grid_rc, st, any_pen, e0, e1)); });
-  timed(ctx, KID_FINALIZE, [&](hipEvent_t e0, hipEvent_t e1) {
-    keep(launch_finalize(a, st, e0, e1));
-  });
-  if (need_collect)
-    timed(ctx, KID_COLLECT, [&](hipEvent_t e0, hipEvent_t e1) {
-      keep(launch_args((const void*)k_collect, grid_rc, dim3(TPB), a, st, e0, e1));
+  if (need_fin)
+    timed(ctx, KID_FINALIZE, [&](hipEvent_t e0, hipEvent_t e1) {
+      keep(launch_finalize(a, st, e0, e1));
+    });
+  if (need_gfin)
+    timed(ctx, KID_GFINAL, [&](hipEvent_t e0, hipEvent_t e1) {
+      keep(launch_args((const void*)k_gfinal, dim3((unsigned)a.R), dim3(FTPB), a, st, e0, e1));
     });
   if (a.verify && a.dlog != nullptr) {
     // the residual draw of unfiltered general-q rows (rows in other phases return)

@@ -37,9 +37,9 @@ __device__ __forceinline__ void finish_row(const Args& a, int r, int status, int
 }
 
 // LDS of one k_finalize workgroup.
-constexpr int FSEG = FCAP / (FTPB / WAVE);  // survivors per wave segment in phase 2
+constexpr int FSEG = FCAP_FAST / (FTPB / WAVE);  // survivors per wave segment in phase 2
 struct FinalShared {
-  uint64_t key[FCAP];       // the row's surviving candidate keys (32 KB)
+  uint64_t key[FCAP_FAST];  // the row's surviving candidate keys (32 KB)
   uint32_t rpre[256];       // per chunk: first position of its candidates past the
                             // speculative depth, within its 64-chunk block (add the block
                             // offsets in off[])
@@ -58,7 +58,7 @@ struct FinalShared {
   uint64_t xu2[2 * FTPB / WAVE];
   XState x;
 };
-static_assert(FCAP >= XB && FCAP >= XCOL, "the exact path reuses the candidate keys");
+static_assert(FCAP_FAST >= XB && FCAP_FAST >= XCOL, "the exact path reuses the candidate keys");
 
 // Histogram bin of d = m - l at `scale` bins per nat (last bin open) for the top-k cut;
 // monotone in l.
@@ -618,6 +618,8 @@ __global__ __launch_bounds__(FTPB) void k_finalize(Args a) {
   row_bj(a, r, b, j);
   const RowPre pf = prefetch_row(a, r, b, j);
   const RowParams p = load_params(a, b, j);
+  // the general rows are k_gfinal's
+  if (gfinal_row(a.p[b], a.V, a.noise_mode, a.dlog != nullptr && a.verify && j < a.k)) return;
   const ExactReq q = finalize_row(a, r, b, j, p, pf, S);
   // one call site for the exact resolution (an out-of-line call), reached by every
   // thread of a row that needs it

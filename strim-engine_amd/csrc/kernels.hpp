@@ -29,7 +29,9 @@ constexpr int SMAXW = 8;         // most waves of a k_stream workgroup
 constexpr int SLOT = 512;        // fast-path candidate entries per chunk
 constexpr int FTPB = 256;        // threads of a k_finalize workgroup (one row)
 constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
-constexpr int FCAP = 4096;       // candidates k_finalize holds in LDS
+constexpr int FCAP = 8192;       // candidate keys k_finalize holds in LDS
+constexpr int FCAP_FAST = 4096;  // of which fast rows use at most this many
+constexpr int GCAP = 128;        // candidates a general row's chunk collects (at most)
 constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
 constexpr float CB_SCALE = 2.0f;
 constexpr int NGB = 129;         // global coarse bins: width 1/2 over [0, 64) + tail
@@ -56,10 +58,12 @@ struct ChunkStat {
   int32_t n;       // allowed tokens (fast and greedy rows: 1 if any)
   int32_t flags;   // bit0: non-finite logit
   float g;         // fast top-k rows: at least k of the chunk's tokens have v >= g (v is
-                   // the value before temperature); -inf when not certified
+                   // the value before temperature), -inf when not certified; general
+                   // rows: the largest l the chunk left out of its candidates (-inf
+                   // when every allowed token is a candidate)
   double S;        // sum exp(l - m) over the chunk (general rows)
   int32_t arg;     // first id reaching m
-  uint32_t ncand;  // fast rows: candidates in the chunk's slot region (> SLOT: overflow)
+  uint32_t ncand;  // candidates in the chunk's slot region (> SLOT: overflow)
   uint32_t pad_[3];
 };
 static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
@@ -125,9 +129,9 @@ struct QPart {
 // Device scratch owned by a context (allocated once in strim_ctx_create).
 struct Scratch {
   ChunkStat* cstat;               // [rows][wmax]
-  Cand* slot;                     // [rows][wmax][SLOT] fast-row candidates, one region per
-                                  // k_stream wave (SLOT / waves entries each)
-                                  // (v before temperature, id)
+  Cand* slot;                     // [rows][wmax][SLOT] the chunks' candidates: (v before
+                                  // temperature, id) for fast rows, (l, id) for general
+                                  // rows
   uint32_t* chc;                  // [rows][wmax][NCB] coarse counts
   unsigned long long* chm;        // [rows][wmax][NCB] coarse fixed-point masses
   ChunkPart* part;                // [rows][wmax]
@@ -215,6 +219,16 @@ __host__ __device__ inline int32_t row_class(const strim_sampling_params& p, int
   if (topk && p.top_k <= KLOC) return CLS_FAST;
   if (p.min_p >= MINP_FAST) return CLS_FAST;
   return CLS_GENERAL;
+}
+
+// Rows k_gfinal decides (gfinal_kernels.hip): the general rows, except the unfiltered
+// Gumbel rows (k_finalize's two-best path) and the draft rows of a general-q verify
+// (k_finalize marks them for the residual draw and k_final).
+__host__ __device__ inline bool gfinal_row(const strim_sampling_params& p, int32_t V,
+                                           int32_t noise_mode, bool general_q_draft_row) {
+  if (row_class(p, V) != CLS_GENERAL || general_q_draft_row) return false;
+  const bool nofilter = !(p.top_k > 0 && p.top_k < V) && !(p.min_p > 0.0f) && !(p.top_p < 1.0f);
+  return !(noise_mode == STRIM_NOISE_GUMBEL && nofilter);
 }
 
 __device__ __forceinline__ void row_bj(const Args& a, int r, int& b, int& j) {

@@ -440,7 +440,68 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       a.s.chm[o] = hm;
     }
     // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
-    if (gum_nf) {
+    if (!gum_nf) {
+      // The chunk's candidates: the tokens of its first coarse bins (d = m_w - l below a
+      // bin edge), as many bins as keep them within GCAP, written as (l, id) to the
+      // chunk's slot region in wave order. cs.g is the largest l left out (-inf when every
+      // allowed token is a candidate): every token of the chunk with l > cs.g is a
+      // candidate, so k_finalize can decide the row from the candidates alone when its
+      // decisions fall above the largest cs.g of the row. (The coarse histogram is
+      // complete: the barriers of the sums above follow its atomics.)
+      uint32_t hsum = 0u;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) hsum += S.hc[q][lane];
+      const uint32_t hcum = wave_incl_scan_u32(hsum);
+      const int bstar = __popcll(__ballot(hcum <= (uint32_t)GCAP)) - 1;  // -1: no bin fits
+      uint32_t sel[SSEG];
+      float umax = -INFINITY;
+      int mycnt = 0;
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) {
+        sel[s] = 0u;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const float le = l[s][e];
+          const float d = m_w - le;
+          const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
+          const bool live_e = le > -INFINITY;
+          const bool take = live_e && bb <= bstar;
+          sel[s] |= (take ? 1u : 0u) << e;
+          mycnt += take ? 1 : 0;
+          if (live_e && !take) umax = fmaxf(umax, le);
+        }
+      }
+      int wtot;
+      const int wex =
+          wave_excl_count_bits<(SSEG == 1 ? 4 : SSEG == 2 ? 5 : SSEG == 4 ? 6 : 7)>(mycnt, &wtot);
+      umax = wave_max_f(umax);
+      if (lane == 0) {
+        S.off[w] = (uint32_t)wtot;
+        S.tf[w] = umax;
+      }
+      __syncthreads();
+      uint32_t before = 0u, tot = 0u;
+      float um = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        before += q < w ? S.off[q] : 0u;
+        tot += S.off[q];
+        um = fmaxf(um, S.tf[q]);
+      }
+      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT + before;
+      int pos = wex;
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) {
+        uint32_t msk = sel[s];
+        while (msk) {
+          const int e = __builtin_ctz(msk);
+          msk &= msk - 1u;
+          dst[pos++] = Cand{pick8(l[s], e), i0[s] + e};
+        }
+      }
+      cs_ncand = tot;
+      cs.g = um;
+    } else {
       const uint64_t key = mix64(p.seed, p.position);
       float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
       int id0 = -1, id1 = -1;
