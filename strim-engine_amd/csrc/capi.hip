@@ -56,7 +56,7 @@ constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // Byte offsets of the scratch buffers of R rows of up to max_vocab tokens, each 256-byte
 // aligned. The general-q verify buffers (dbits .. qflag) are sized only when `verify`.
 struct ScratchLayout {
-  size_t cstat, slot, chc, chm, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp,
+  size_t cstat, slot, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp,
       qflag, bytes;
 };
 constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) {
@@ -68,8 +68,6 @@ constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) 
   size_t off = 0;
   L.cstat = off; off = align_up(off + R * wmax * sizeof(ChunkStat), 256);
   L.slot = off; off = align_up(off + R * wmax * SLOT * sizeof(Cand), 256);
-  L.chc = off; off = align_up(off + R * wmax * NCB * sizeof(uint32_t), 256);
-  L.chm = off; off = align_up(off + R * wmax * NCB * sizeof(unsigned long long), 256);
   L.part = off; off = align_up(off + R * wmax * sizeof(ChunkPart), 256);
   L.rs = off; off = align_up(off + R * sizeof(RowState), 256);
   L.cand = off; off = align_up(off + R * CAP * sizeof(Cand), 256);
@@ -92,8 +90,6 @@ Scratch scratch_at(char* base, const ScratchLayout& L, size_t max_vocab, bool ve
   Scratch s{};
   s.cstat = (ChunkStat*)(base + L.cstat);
   s.slot = (Cand*)(base + L.slot);
-  s.chc = (uint32_t*)(base + L.chc);
-  s.chm = (unsigned long long*)(base + L.chm);
   s.part = (ChunkPart*)(base + L.part);
   s.rs = (RowState*)(base + L.rs);
   s.cand = (Cand*)(base + L.cand);

@@ -3,8 +3,8 @@
 // Layout of one call: R rows of V logits. Every streaming kernel splits a row into
 // chunks of CHUNK tokens and launches a (chunks, rows) grid; one workgroup owns one
 // (row, chunk) and each thread owns runs of EPT consecutive tokens (one 16-byte load of
-// bf16, two of fp32): k_stream with 256 threads (two runs each), k_collect and k_probs
-// with TPB threads (one run each).
+// bf16, two of fp32): k_stream with 512 or 128 threads (one or four runs each), k_probs
+// and the residual-draw passes with TPB threads (one run each).
 #pragma once
 
 #include <hip/hip_ext.h>
@@ -21,8 +21,6 @@ constexpr int EPT = 8;         // tokens per thread
 constexpr int CAP = 8192;      // candidates per row held by the finalize workgroup
 constexpr int FIN_T = 1024;    // finalize workgroup size
 constexpr int FIN_Q = CAP / FIN_T;
-constexpr double FIX_SCALE = 1099511627776.0;  // 2^40 fixed-point mass scale
-constexpr float FIX_SCALE_F = 1099511627776.0f;
 constexpr int WAVE = 64;
 
 static_assert(CHUNK == TPB * EPT, "chunk geometry");

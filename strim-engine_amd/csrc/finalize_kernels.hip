@@ -6,12 +6,12 @@
 //                    min-p on the row maximum, a radix select of the k-th key, a sort of
 //                    the survivors, the top-p cut and the draw, all in LDS;
 //   unfiltered Gumbel rows  from the chunks' two best scores;
-//   general rows     their bin bounds from k_stream's coarse histograms (general.hpp);
-//                    the rows are decided by k_collect / k_final.
+//   general-q draft rows    checked and handed to the residual draw (qres_kernels.hip)
+//                    or k_final's exact resolution.
+// The other general rows are k_gfinal's (gfinal_kernels.hip), which runs beside it.
 // A row whose candidates do not fit the LDS finalize is decided here by the exact
 // streaming resolution (exact.hpp).
 #include "exact.hpp"
-#include "general.hpp"
 
 namespace strim {
 
@@ -308,14 +308,9 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     finish_row(a, r, STRIM_OK, token, acc, sig, m, ~0ull, PH_DONE);
     return done;
   }
-  if (p.cls != CLS_FAST) {
-    // general rows: their bin bounds, once per row, for k_collect and k_final; the row's
-    // first maximum travels in token
-    static_assert(sizeof(GenShared) <= sizeof(S.key), "general bounds overlay");
-    general_bounds<FTPB>(a, r, p, m, cs, own, *reinterpret_cast<GenShared*>(S.key));
-    finish_row(a, r, STRIM_OK, arg, 0, 0.0, m, 0ull, PH_PENDING);
-    return done;
-  }
+  // General rows are k_gfinal's (this kernel returns before the row for them); should one
+  // arrive here, the exact resolution decides it.
+  if (p.cls != CLS_FAST) return ExactReq{1, m, arg, draft, l_draft};
   if ((flags & 2) || n_c > (uint32_t)FCAND) {
     return ExactReq{1, m, arg, draft, l_draft};
   }

@@ -262,7 +262,6 @@ __global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
     rsp->m = m;
     rsp->last_key = last_key;
     rsp->phase = PH_DONE;
-    rsp->bd.mode = MODE_NONE;
     if (!a.verify) {
       a.out_ids[r] = status == STRIM_OK ? token : -1;
       if (a.out_status) a.out_status[r] = status;

@@ -1,15 +1,15 @@
 // kernels.hpp — argument block, scratch layout and per-row processing shared by the
 // gfx950 kernels.
 //
-// One call runs up to four kernels over R rows of V logits:
-//   k_stream   (rows x chunks)  single streaming pass: processed logits, chunk statistics,
-//                               and either the chunk's local candidates (fast rows) or a
-//                               64-bin coarse mass histogram (general rows);
-//   k_finalize (one workgroup per row) decides greedy, fast and unfiltered Gumbel rows;
-//   k_collect  (rows x chunks)  general rows only: second pass that collects the tokens the
-//                               coarse bounds cannot resolve and sums the rest exactly;
-//   k_final    (one workgroup per row) general rows in fp64 over the sorted candidates,
-//                               and the exact streaming resolution of overflowing rows.
+// A sampling call runs two kernels over R rows of V logits:
+//   k_stream   (rows x chunks)  the single streaming pass: processed logits, chunk
+//                               statistics and the chunk's candidates;
+//   k_finalize (one workgroup per row) decides greedy, fast and unfiltered Gumbel rows,
+//   k_gfinal   (one workgroup per row) the general rows (each runs only when some row of
+//                               the call needs it).
+// A general-q verify adds k_qprep / k_qcombine before them and the residual draw
+// (qres_kernels.hip) and k_final after them. Rows whose candidates overflow are decided
+// by the exact streaming resolution (exact.hpp) inside the deciding workgroup.
 // Workgroups never wait for or fence against each other: every partial result is a
 // plain store into a per-(row, chunk) slot that the next kernel reads.
 #pragma once
@@ -34,22 +34,17 @@ constexpr int FCAP_FAST = 4096;  // of which fast rows use at most this many
 constexpr int GCAP = 128;        // candidates a general row's chunk collects (at most)
 constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
 constexpr float CB_SCALE = 2.0f;
-constexpr int NGB = 129;         // global coarse bins: width 1/2 over [0, 64) + tail
 constexpr int KLOC = 256;        // largest top-k served by local candidates
 constexpr float MINP_FAST = 3.3546262e-4f;  // e^-8: min-p at or above bounds candidates
-constexpr int NSEG = 8;          // non-collected intervals summarised per chunk
 
 enum RowClass : int32_t { CLS_GREEDY = 0, CLS_FAST = 1, CLS_GENERAL = 2, CLS_INVALID = 3 };
 
-// How a row's candidates are resolved (set by k_collect for general rows).
-// Set by k_finalize: DONE rows are decided; PENDING rows (general path) go to
-// k_collect + k_final; EXACT rows (general-q verify rows) go to k_final's exact streaming
-// resolution, whose workgroups are four times wider than k_finalize's.
-// QRES rows (unfiltered general-q verify rows) are decided by the grid-wide residual
-// draw (qres_kernels.hip), which demotes an icdf row to EXACT when its bucket overflows.
-enum RowPhase : int32_t { PH_PENDING = 0, PH_DONE = 1, PH_EXACT = 2, PH_QRES = 3 };
-
-enum RowMode : int32_t { MODE_NONE = 0, MODE_FAST = 1, MODE_A = 2, MODE_B = 3, MODE_TOPS = 4 };
+// Set by k_finalize and k_gfinal: DONE rows are decided; EXACT rows (filtered general-q
+// verify rows) go to k_final's exact streaming resolution, whose workgroups are four
+// times wider than k_finalize's; QRES rows (unfiltered general-q verify rows) are decided
+// by the grid-wide residual draw (qres_kernels.hip), which demotes an icdf row to EXACT
+// when its bucket overflows.
+enum RowPhase : int32_t { PH_DONE = 1, PH_EXACT = 2, PH_QRES = 3 };
 
 // Written by k_stream without a closing barrier: m, n, flags, g and ncand by the first
 // wave, arg by the wave holding the first maximum.
@@ -68,12 +63,8 @@ struct ChunkStat {
 };
 static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
 
-// General-path per-chunk summary of the tokens k_collect did not collect: fixed-point
-// mass and count per non-collected interval, and the two best surely-kept tokens by the
-// fp32 Gumbel proxy.
+// Unfiltered Gumbel rows: the chunk's two best tokens by the fp32 Gumbel proxy l + g.
 struct ChunkPart {
-  unsigned long long mass[NSEG];
-  uint32_t cnt[NSEG];
   float l0, l1;
   int32_t id0, id1;
 };
@@ -84,15 +75,6 @@ struct Cand {
   int32_t id;
 };
 
-// Bounds of a general row, in global coarse bins gd = floor(2 * (m - l)) (tail = 128).
-struct Bounds {
-  int32_t mode;
-  int32_t s, e;      // gd < s surely kept; gd > e (and not collected) surely dropped
-  int32_t s1, e1;    // gd < s1 surely pre-kept (min-p, top-k); gd > e1 surely not
-  int32_t rng[3][2]; // collected ranges
-  int32_t seg_lo[NSEG], seg_hi[NSEG];  // non-collected intervals (lo > hi = empty)
-};
-
 struct RowState {
   float l_draft;   // verify: processed logit of the row's draft (-inf if masked)
   int32_t status;
@@ -101,8 +83,8 @@ struct RowState {
   double sum_kept;
   float m;
   int32_t phase;      // RowPhase: which kernel still has to decide the row
-  uint64_t last_key;  // last kept token's order key (0 = none kept beyond bin rules)
-  Bounds bd;          // general rows (k_collect)
+  uint64_t last_key;  // last kept token's order key (the kept set is the prefix of the
+                      // (l desc, id asc) order up to it; 0 = none)
   // QRES rows: plain mass S, residual mass, draw target T (fixed point), the chosen
   // coarse bin and the residual mass before it
   uint64_t qS, qR, qT, qbelow;
@@ -132,12 +114,10 @@ struct Scratch {
   Cand* slot;                     // [rows][wmax][SLOT] the chunks' candidates: (v before
                                   // temperature, id) for fast rows, (l, id) for general
                                   // rows
-  uint32_t* chc;                  // [rows][wmax][NCB] coarse counts
-  unsigned long long* chm;        // [rows][wmax][NCB] coarse fixed-point masses
   ChunkPart* part;                // [rows][wmax]
   RowState* rs;                   // [rows]
-  Cand* cand;                     // [rows][CAP]
-  uint32_t* ncand;                // [rows]
+  Cand* cand;                     // [rows][CAP] QRES rows: the tokens of the draw's bin
+  uint32_t* ncand;                // [rows] their count
   uint32_t* dbits;                // [ceil(V/32)] general-q verify: draft-vocab membership
   float* vq;                      // [MAXP][wmax * CHUNK] general-q verify, per draft row:
                                   // draft logit / T at each table id (others not written)
@@ -475,20 +455,6 @@ __device__ __forceinline__ void hist_count(const A& a, int b, int j, int c0,
     if (o < (uint32_t)SPAN && id >= 0 && id < a.V) atomicAdd(&s_cnt[o], 1u);
   }
   __syncthreads();
-}
-
-// Global coarse bin of d = m - l (monotone in l; equal l share a bin).
-__device__ __forceinline__ int gbin(float d) { return d < 64.0f ? (int)(d * CB_SCALE) : NGB - 1; }
-
-__device__ __forceinline__ bool in_rng(const Bounds& bd, int g) {
-  return (g >= bd.rng[0][0] && g <= bd.rng[0][1]) || (g >= bd.rng[1][0] && g <= bd.rng[1][1]) ||
-         (g >= bd.rng[2][0] && g <= bd.rng[2][1]);
-}
-__device__ __forceinline__ int seg_of(const Bounds& bd, int g) {
-#pragma unroll
-  for (int q = 0; q < NSEG; ++q)
-    if (g >= bd.seg_lo[q] && g <= bd.seg_hi[q]) return q;
-  return -1;
 }
 
 // Uniform element `idx` of row r's noise vector: injected, or Philox at the row's

@@ -48,7 +48,7 @@ __device__ __forceinline__ uint64_t q_resid(uint64_t W, double q, uint64_t S) {
   return W > qS ? W - qS : 0ull;
 }
 
-// The processed logits of this thread's EPT tokens of chunk c, as k_collect computes
+// The processed logits of this thread's EPT tokens of chunk c, as k_stream computes
 // them (every thread of the workgroup calls it: the history counts use barriers).
 __device__ __forceinline__ void q_tokens(const Args& a, int r, int b, int j, const RowParams& p,
                                          int c, uint32_t* s_cnt, float (&l)[EPT]) {

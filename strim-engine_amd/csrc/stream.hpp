@@ -1,11 +1,13 @@
 // stream.hpp — k_stream: the single streaming pass over the logits.
 //
-// A 256-thread workgroup owns one (row, chunk of 4096 tokens); thread t owns the two
-// 8-token segments t and t + 256, so every wave-wide load is 1 KB (bf16) of contiguous
-// logits. All global loads of a workgroup (logits, allow-bits, history ids) are issued
-// before its first barrier. The workgroup writes its chunk statistics and either its
-// local candidates (fast rows) or the pass-1 histograms of general rows; k_finalize
-// (finalize_kernels.hip) then decides each row.
+// A workgroup owns one (row, chunk of 4096 tokens): 512 threads with one 8-token segment
+// each for small batches, 128 threads with four segments each for large ones; every
+// wave-wide load is 1 KB (bf16) of contiguous logits. All global loads of a workgroup
+// (logits, allow-bits, history ids) are issued before its first barrier. The workgroup
+// writes its chunk statistics and its candidates: (v, id) above a bound for fast rows,
+// the tokens of the chunk's first coarse bins as (l, id) for general rows. k_finalize
+// (finalize_kernels.hip) then decides the greedy, fast and unfiltered Gumbel rows,
+// k_gfinal (gfinal_kernels.hip) the general rows.
 //
 // The kernel is a template over the logits dtype, 16-byte alignment, penalties and the
 // allow-mask, so each launch runs straight-line per-token code, and over the segments
@@ -26,8 +28,8 @@ constexpr int stpb() { return CHUNK / (EPT * SSEG); }
 template <bool PEN>
 struct StreamShared {
   uint32_t cnt[PEN ? CHUNK : 4];  // history counts of the chunk's tokens (16 KB)
-  uint32_t hc[SMAXW][NCB];            // general rows: per-wave coarse histograms (one copy
-  unsigned long long hm[SMAXW][NCB];  // per wave spreads the atomics' contention)
+  uint32_t hc[SMAXW][NCB];  // general rows: per-wave coarse counts (one copy per wave
+                            // spreads the atomics' contention)
   uint32_t lad[2 * WAVE];
   float v[SMAXW];
   int i[SMAXW], n[SMAXW], f[SMAXW];
@@ -202,7 +204,6 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   if (p.cls == CLS_GENERAL)
     for (int q = t; q < NW * NCB; q += STPB) {
       S.hc[q / NCB][q % NCB] = 0u;
-      S.hm[q / NCB][q % NCB] = 0ull;
     }
   if (pen) hist_count<STPB, CHUNK>(a, b, j, c0, hid, hl, S.cnt);
 
@@ -392,16 +393,16 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     }
     cs_ncand = tot <= SLOT ? (uint32_t)tot : 0xFFFFFFFFu;
   } else if (p.cls == CLS_GENERAL && live && !(a.dlog && a.verify && j < a.k)) {
-    // processed logits; chunk sum exp(l - m_w) and a coarse histogram of m_w - l
-    // (k_collect's bounds). General-q draft rows skip this: their draw makes its own
-    // passes (qres_kernels.hip, exact.hpp).
+    // processed logits; chunk sum exp(l - m_w) and a coarse histogram of counts of
+    // m_w - l (which bins the chunk's candidates come from). General-q draft rows skip
+    // this: their draw makes its own passes (qres_kernels.hip, exact.hpp).
     float (&l)[SSEG][EPT] = v;  // v is not needed after this
 #pragma unroll
     for (int s = 0; s < SSEG; ++s)
 #pragma unroll
       for (int e = 0; e < EPT; ++e) l[s][e] = v[s][e] > -INFINITY ? v[s][e] / p.T : -INFINITY;
     // unfiltered Gumbel rows are decided from the chunks' two best tokens and the sum;
-    // only the other general rows need the histogram (k_finalize's bin bounds)
+    // only the other general rows need the histogram
     const bool gum_nf = a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V);
     double ssum = 0.0;
     int na = 0;
@@ -412,13 +413,10 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         if (!(l[s][e] > -INFINITY)) continue;
         ++na;
         const float d = m_w - l[s][e];
-        const float wgt = expf(-d);
-        ssum += (double)wgt;
+        ssum += (double)expf(-d);
         if (gum_nf) continue;
         const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
         atomicAdd(&S.hc[w][bb], 1u);
-        const unsigned long long fx = __float2ull_rn(wgt * FIX_SCALE_F);
-        if (fx) atomicAdd(&S.hm[w][bb], fx);
       }
     cs.S = block_sum_f64<STPB>(ssum, S.d);
     na = wave_sum(na);
@@ -427,25 +425,13 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     cs.n = 0;
 #pragma unroll
     for (int q = 0; q < NW; ++q) cs.n += S.n[q];
-    if (t < NCB && !gum_nf) {
-      uint32_t hc = 0u;
-      unsigned long long hm = 0ull;
-#pragma unroll
-      for (int q = 0; q < NW; ++q) {
-        hc += S.hc[q][t];
-        hm += S.hm[q][t];
-      }
-      const int64_t o = ((int64_t)r * a.s.wmax + c) * NCB + t;
-      a.s.chc[o] = hc;
-      a.s.chm[o] = hm;
-    }
     // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
     if (!gum_nf) {
       // The chunk's candidates: the tokens of its first coarse bins (d = m_w - l below a
       // bin edge), as many bins as keep them within GCAP, written as (l, id) to the
       // chunk's slot region in wave order. cs.g is the largest l left out (-inf when every
       // allowed token is a candidate): every token of the chunk with l > cs.g is a
-      // candidate, so k_finalize can decide the row from the candidates alone when its
+      // candidate, so k_gfinal can decide the row from the candidates alone when its
       // decisions fall above the largest cs.g of the row. (The coarse histogram is
       // complete: the barriers of the sums above follow its atomics.)
       uint32_t hsum = 0u;
