@@ -13,7 +13,7 @@
 
 namespace strim {
 hipError_t launch_finalize(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
-__global__ void k_gfinal(Args a);
+hipError_t launch_gfinal(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
@@ -210,7 +210,7 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
     });
   if (need_gfin)
     timed(ctx, KID_GFINAL, [&](hipEvent_t e0, hipEvent_t e1) {
-      keep(launch_args((const void*)k_gfinal, dim3((unsigned)a.R), dim3(FTPB), a, st, e0, e1));
+      keep(launch_gfinal(a, st, e0, e1));
     });
   if (a.verify && a.dlog != nullptr) {
     // the residual draw of unfiltered general-q rows (rows in other phases return)

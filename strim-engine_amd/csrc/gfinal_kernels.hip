@@ -9,184 +9,159 @@
 // lies above G, one workgroup takes them from the candidates alone; otherwise the row is
 // resolved by the exact streaming resolution (exact.hpp) in the same workgroup.
 //
-// One workgroup per row, in three steps:
+// One 1024-thread workgroup per row; each thread holds up to GNE candidates in registers:
 //   1. the chunk statistics and every candidate slot are loaded together (the slots of
 //      a region past its count are read and dropped, so nothing waits for the counts);
-//   2. the candidates above G are binned by d = m - l into a 256-bin histogram of counts
-//      and fixed-point masses, round(2^50 * expf(l - m)) (integer sums: every cumulative
-//      mass is independent of summation order, and 8192 unit masses stay below 2^63; the
-//      float exp keeps each mass within 2^-23 relative, far inside the 1e-6 decision and
-//      probability tolerances), and scattered with their masses into bin order (each
-//      candidate's place in its bin comes from the count atomic). The atomics are issued
-//      without branches: a lane without a candidate adds to a slot of its own;
-//   3. wave 0 alone finds the k-th token, the top-p cut and the icdf draw: the bin where
-//      a cumulative count or mass first exceeds the threshold comes from the histogram's
-//      prefix, and only that bin's keys are put in order and scanned. A Gumbel draw scores
-//      every kept candidate on all waves.
+//      the waves' maxima, flags, bounds and chunk mass sums are merged with one barrier;
+//   2. the candidates above G are binned by d = m - l into GNB bins of counts and
+//      fixed-point masses, round(2^50 * expf(l - m)) (integer sums: every cumulative mass
+//      is independent of summation order, and 8192 unit masses stay below 2^63; the float
+//      exp keeps each mass within 2^-23 relative, far inside the 1e-6 decision and
+//      probability tolerances). The count atomic returns each candidate's place in its
+//      bin. Each wave turns its 64 bins into inclusive prefixes (a bin's cumulative count
+//      or mass is its group's prefix plus the totals of the groups before it), and every
+//      candidate is stored with its mass in bin order;
+//   3. the decisions run in order (the k-th token, the top-p cut, the icdf draw) through
+//      one loop, so their shared code is fetched once: each finds the bin where its
+//      threshold is crossed from the prefixes, and each key of that bin counts the bin's
+//      keys before it in order; the key whose interval contains the threshold is the
+//      decision (one barrier per decision). A Gumbel draw scores every kept candidate.
+// The kernel's time is latency (dependent steps, barriers and the first fetch of its
+// code), so the code is kept short: loops that run once per decision are not repeated
+// per decision.
 #include "exact.hpp"
 
 namespace strim {
 
-constexpr int GNE = 32;        // candidate slots per thread: W * GCAP <= FTPB * GNE
-constexpr int GZCAP = 1024;    // keys of one bin put in order
+constexpr int GT = 1024;            // threads of a k_gfinal workgroup
+constexpr int GW = GT / WAVE;       // its waves; wave w owns the histogram bins of group w
+constexpr int GNE = 8;              // candidate slots per thread: W * GCAP <= GT * GNE
+constexpr int GCAND = GT * GNE;     // candidates of a row held in bin order
+constexpr int GNB = GW * WAVE;      // histogram bins of d = m - l (64 per group)
+constexpr int GZCAP = GT;           // keys of one bin a decision resolves (one per thread)
 constexpr double GFIX = 1125899906842624.0;  // 2^50: the fixed-point unit of mass
 static_assert(GCAP == 128, "candidate slot of an entry: e >> 7, e & 127");
-static_assert(FCAP >= FTPB * GNE, "every candidate fits the bin-ordered array");
+static_assert(GT % GCAP == 0, "whole regions per pass of the workgroup");
+static_assert(GNB == GT, "one bin per thread to clear");
 
 // LDS of one k_gfinal workgroup.
 struct GFinalShared {
-  uint64_t bkey[FCAP];   // the candidates above G in bin order (64 KB)
   union {
-    uint64_t bmass[FCAP];  // their fixed-point masses (64 KB)
-    struct {               // the exact streaming resolution (rows decided at or below G)
+    struct {                  // the decision from the candidates
+      uint64_t bkey[GCAND];   // the candidates above G in bin order (64 KB)
+      uint64_t bmass[GCAND];  // their fixed-point masses (64 KB)
+    };
+    struct {                  // the exact streaming resolution (rows decided at or below G)
+      uint64_t xkey[XB > XCOL ? XB : XCOL];
       uint32_t xhc[XB];
-      uint32_t xcnt[FTPB * EPT];
-      uint64_t xu2[2 * FTPB / WAVE];
+      uint32_t xcnt[GT * EPT];
+      uint64_t xu2[2 * GT / WAVE];
       XState x;
     };
   };
-  uint64_t zone[GZCAP];  // one bin's keys (with their zone index), in order
-  uint64_t zmass[GZCAP]; // their masses, by zone index
-  uint64_t hmass[256];   // fixed-point mass per bin, then the inclusive prefix
-  uint64_t dmass[FTPB];  // per thread: where a lane without a candidate adds its mass
-  uint32_t hist[256];    // count per bin, then the inclusive prefix
-  uint32_t dcnt[FTPB];   // per thread: where a lane without a candidate adds its count
-  uint32_t rcnt[256];    // per chunk: its candidates
-  float v[FTPB / WAVE], g[FTPB / WAVE];
-  int i[FTPB / WAVE], f[FTPB / WAVE];
-  double d[FTPB / WAVE];
-  uint64_t u[FTPB / WAVE];
+  uint64_t hmass[GNB];        // fixed-point mass per bin, then the group-local inclusive prefix
+  uint32_t hist[GNB];         // count per bin, then the group-local inclusive prefix
+  uint64_t gm[GW];            // per group: total mass
+  uint32_t gc[GW];            // per group: total count
+  uint32_t rcnt[GT];          // per chunk: its candidates
+  float v[GW], g[GW];
+  int i[GW], f[GW];
+  double sw[GW];              // per wave: its chunks' mass, relative to the wave's maximum
+  double d[GW];
+  uint64_t u[GW];
   int misc[8];
-  uint64_t res[8];       // wave 0's decisions, for the other waves
+  uint64_t res[2][4];         // a decision: key, count before, mass before, mass (two slots,
+  int32_t tag[2];             // alternating; tag = the decision's number when it holds one)
 };
-static_assert(FCAP >= XB && FCAP >= XCOL, "the exact path reuses the candidate keys");
-static_assert(GZCAP == 1024, "zone index: the low 10 bits of a zone key");
 
 // Fixed-point mass of a token: round(2^50 * exp(l - m)), from the float exp of the
 // float difference (l <= m).
 __device__ __forceinline__ uint64_t gmass(float l, float m) {
   return (uint64_t)(expf(l - m) * 1125899906842624.0f);
 }
-// A zone key: the order key with the id moved up by 10 bits and the zone index below it
-// (ids < 2^22), so sorting zone keys orders the tokens and keeps each one's index.
-__device__ __forceinline__ uint64_t zkey(uint64_t k, int idx) {
-  return (k & 0xFFFFFFFF00000000ull) | ((k & 0x3FFFFFull) << 10) | (uint64_t)idx;
-}
-__device__ __forceinline__ uint64_t zkey_key(uint64_t z) {
-  return (z & 0xFFFFFFFF00000000ull) | ((z >> 10) & 0x3FFFFFull);
-}
-__device__ __forceinline__ int gbin256(float m, float l, float hscale) {
-  return (int)fminf((m - l) * hscale, 255.0f);
+__device__ __forceinline__ int gbin(float m, float l, float hscale) {
+  return (int)fminf((m - l) * hscale, (float)(GNB - 1));
 }
 __device__ __forceinline__ float key_l(uint64_t k) { return fkey_desc_inv((uint32_t)(k >> 32)); }
 
-// Result of a search: the key found (~0: none), the prefix count and mass of the keys
-// before it and its own mass.
+// Cumulative count (mass == false) or mass of bins 0 .. b, from the group-local prefixes
+// and `ginc`, lane g's inclusive prefix of the group totals of the same kind (b is
+// wave-uniform).
+__device__ __forceinline__ uint64_t gcum(const GFinalShared& S, bool mass, uint64_t ginc, int b) {
+  if (b < 0) return 0ull;
+  const int g = b / WAVE;
+  const uint64_t before = g > 0 ? rl_u64(ginc, g - 1) : 0ull;
+  return before + (mass ? S.hmass[b] : (uint64_t)S.hist[b]);
+}
+
+// The first bin whose cumulative count or mass, less excl_w from bin excl_b on, exceeds
+// thr, among the bins before bb; bb when none does (every wave computes the same bin).
+__device__ __forceinline__ int gfind_bin(const GFinalShared& S, bool mass, uint64_t ginc,
+                                         double thr, int bb, uint64_t excl_w, int excl_b) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  // the first group whose cumulative total (with the exclusion) exceeds thr
+  const uint64_t gv = ginc - ((mass && excl_b <= WAVE * lane + WAVE - 1) ? excl_w : 0ull);
+  const uint64_t gh = __ballot(lane < GW && (double)gv > thr);
+  if (gh == 0ull) return bb;
+  const int g = (int)__ffsll((long long)gh) - 1;
+  if (g * WAVE >= bb) return bb;
+  // within the group: one bin per lane
+  const int b = g * WAVE + lane;
+  const uint64_t before = g > 0 ? rl_u64(ginc, g - 1) : 0ull;
+  const uint64_t bv = before + (mass ? S.hmass[b] : (uint64_t)S.hist[b]) -
+                      ((mass && b >= excl_b) ? excl_w : 0ull);
+  const uint64_t bh = __ballot((double)bv > thr);
+  const int bz = bh ? g * WAVE + (int)__ffsll((long long)bh) - 1 : bb;
+  return bz < bb ? bz : bb;
+}
+
+// A decision: the key (~0: none), the count and mass of the keys before it in the row's
+// order, and its own mass.
 struct GHit {
   uint64_t key, cnt_before, mass_before, mass;
 };
 
-// Wave 0 only: the first candidate in key order with key <= bound and id != excl whose
-// inclusive cumulative count (mass == false) or mass exceeds thr. hist / hmass hold the
-// inclusive bin prefixes of all candidates; excl_w and excl_b are the excluded key's mass
-// and bin when it is a candidate (0 and 256 otherwise). False when the bin to scan holds
-// more than GZCAP keys.
-__device__ __forceinline__ bool gsearch(GFinalShared& S, float m, float hscale, bool mass,
-                                        double thr, uint64_t bound, int excl, uint64_t excl_w,
-                                        int excl_b, GHit& hit) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  // (memory accesses are kept out of branches throughout: a load inside a branch is
-  // waited for at the branch's end, which would serialise them)
-  auto cumv = [&](int bq) -> uint64_t {  // uniform bq
-    if (bq < 0) return 0ull;
-    if (!mass) return (uint64_t)S.hist[bq];
-    return S.hmass[bq] - (bq >= excl_b ? excl_w : 0ull);
-  };
-  const int bb = bound == ~0ull ? 255 : gbin256(m, key_l(bound), hscale);
-  // the first bin below the bound's whose prefix exceeds thr, else the bound's bin
-  uint64_t c4[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    c4[q] = mass ? S.hmass[4 * lane + q] : (uint64_t)S.hist[4 * lane + q];
-  int bz = 256;
-#pragma unroll
-  for (int q = 3; q >= 0; --q) {
-    const int bq = 4 * lane + q;
-    const uint64_t v = c4[q] - ((mass && bq >= excl_b) ? excl_w : 0ull);
-    bz = ((bq < bb) & ((double)v > thr)) ? bq : bz;
-  }
-  bz = wave_min_i(bz);
-  if (bz > bb) bz = bb;
-  const uint32_t z0 = bz > 0 ? S.hist[bz - 1] : 0u, z1 = S.hist[bz];
-  const int nz = (int)(z1 - z0);
-  if (nz > GZCAP) return false;
-  for (int i = lane; i < nz; i += WAVE) {
-    S.zone[i] = zkey(S.bkey[z0 + i], i);
-    S.zmass[i] = S.bmass[z0 + i];
-  }
-  wave_sync();
-  if (nz <= WAVE) wave_rank_sort(S.zone, nz);
-  else wave_sort_lds(S.zone, nz);
-  // scan in order: a pass of 64 lanes x 4 keys at a time, each key counting 1 or its
-  // mass unless it lies past the bound or is the excluded one
-  uint64_t run = mass ? cumv(bz - 1) : (uint64_t)z0;
-  hit.key = ~0ull;
-  for (int p0 = 0; p0 < nz; p0 += 4 * WAVE) {
-    uint64_t val[4], own = 0ull;
-    uint64_t zz[4], zm[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) zz[q] = S.zone[min(p0 + 4 * lane + q, GZCAP - 1)];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) zm[q] = S.zmass[zz[q] & 1023u];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint64_t k = zkey_key(zz[q]);
-      const bool in = (p0 + 4 * lane + q < nz) & (k <= bound) & ((int)(uint32_t)k != excl);
-      val[q] = in ? (mass ? zm[q] : 1ull) : 0ull;
-      own += val[q];
+// Decision number n over the zone bkey/bmass[z0, z0 + nz) (one bin in bin order; every
+// thread, nz <= GT): the first zone key in key order, key <= bound and id != excl, whose
+// inclusive cumulative count (mass == false) or mass exceeds thr, starting from cnt0 /
+// mass0 before the zone. Thread t owns zone key t and counts the zone keys before it; the
+// unique key whose interval contains thr writes its result with tag n to slot n & 1 (a
+// slot is rewritten two decisions later, after every thread has read it). One barrier.
+__device__ __forceinline__ GHit gresolve(GFinalShared& S, int n, int z0, int nz, bool mass,
+                                         double thr, uint64_t bound, int excl, uint64_t cnt0,
+                                         uint64_t mass0) {
+  const int t = threadIdx.x;
+  const int slot = n & 1;
+  if (t < nz) {
+    const uint64_t k = S.bkey[z0 + t];
+    const uint64_t km = S.bmass[z0 + t];
+    const bool in = k <= bound && (int)(uint32_t)k != excl;
+    uint32_t rank = 0u;
+    uint64_t mb = 0ull;
+    for (int jj = 0; jj < nz; ++jj) {
+      const uint64_t kj = S.bkey[z0 + jj];
+      const uint64_t mj = S.bmass[z0 + jj];
+      const bool lt = kj < k;
+      rank += lt ? 1u : 0u;
+      mb += (lt && kj <= bound && (int)(uint32_t)kj != excl) ? mj : 0ull;
     }
-    const uint64_t incl = wave_incl_scan_u64(own);
-    uint64_t r0 = run + incl - own;
-    int fq = 4;
-    uint64_t fb = 0ull;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (fq == 4 && val[q] > 0ull && (double)(r0 + val[q]) > thr) {
-        fq = q;
-        fb = r0;
-      }
-      r0 += val[q];
+    // count mode counts every key (no bound, no exclusion)
+    const uint64_t before = mass ? mass0 + mb : cnt0 + rank;
+    const uint64_t own = mass ? (in ? km : 0ull) : 1ull;
+    if (own > 0ull && (double)before <= thr && (double)(before + own) > thr) {
+      S.res[slot][0] = k;
+      S.res[slot][1] = cnt0 + rank;
+      S.res[slot][2] = mass0 + mb;
+      S.res[slot][3] = km;
+      S.tag[slot] = n;
     }
-    const uint64_t hitm = __ballot(fq < 4);
-    if (hitm) {
-      const int fl = (int)__ffsll((long long)hitm) - 1;
-      const int i = p0 + 4 * fl + rl_i(fq, fl);
-      const uint64_t z = S.zone[i];
-      hit.key = zkey_key(z);
-      hit.cnt_before = (uint64_t)z0 + (uint64_t)i;
-      hit.mass_before = rl_u64(fb, fl);
-      hit.mass = mass ? S.zmass[z & 1023u] : 1ull;
-      break;
-    }
-    run += rl_u64(incl, WAVE - 1);
   }
-  return true;
+  __syncthreads();
+  if (S.tag[slot] != n) return GHit{~0ull, 0ull, 0ull, 0ull};
+  return GHit{S.res[slot][0], S.res[slot][1], S.res[slot][2], S.res[slot][3]};
 }
 
-// The mass of the candidates with key <= bound (wave 0 only): the bins before the
-// bound's, plus that bin's keys up to the bound.
-__device__ __forceinline__ uint64_t gmass_upto(GFinalShared& S, float m, float hscale,
-                                               uint64_t bound) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  const int bb = gbin256(m, key_l(bound), hscale);
-  const uint32_t z0 = bb > 0 ? S.hist[bb - 1] : 0u, z1 = S.hist[bb];
-  uint64_t loc = 0ull;
-  for (uint32_t i = z0 + (uint32_t)lane; i < z1; i += WAVE)
-    if (S.bkey[i] <= bound) loc += S.bmass[i];
-  return (bb > 0 ? S.hmass[bb - 1] : 0ull) + wave_sum_u64(loc);
-}
-
-__global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
+__global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   __shared__ GFinalShared S;
   // the launch fields of the first loads, read together (see k_stream)
   asm volatile("" ::"s"(a.s.cstat), "s"(a.s.wmax), "s"(a.s.rs), "s"(a.s.slot), "s"(a.W),
@@ -210,12 +185,12 @@ __global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
   const int32_t* dp = vdr ? a.drafts + (int64_t)b * a.k + j : (const int32_t*)rsp;
   const int d_raw = *dp;
   const float ld_raw = rsp->l_draft;
-  const int ne = W * GCAP;  // candidate slots of the row (<= FTPB * GNE)
+  const int ne = W * GCAP;  // candidate slots of the row
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
   Cand cd[GNE];
 #pragma unroll
   for (int q = 0; q < GNE; ++q) {
-    const int e = q * FTPB + t;
+    const int e = q * GT + t;
     cd[q] = slots[e < ne ? (int64_t)(e >> 7) * SLOT + (e & (GCAP - 1)) : 0];
   }
   const RowParams p = load_params(a, b, j);
@@ -223,36 +198,38 @@ __global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
   const int draft = vdr ? d_raw : -1;
   const float l_draft = vdr ? ld_raw : -INFINITY;
 
-  // ---- the chunk statistics ------------------------------------------------------
+  // ---- the chunk statistics: per wave, then every wave merges the waves' results --
   const bool own = t < W;
   int ff = own ? (cs.flags | (cs.n > 0 ? 4 : 0)) : 0;
   float mv = own ? cs.m : -INFINITY, gv = own ? cs.g : -INFINITY;
   int mi = own ? cs.arg : -1;
-  if (own) S.rcnt[t] = cs.ncand;
-  const double wS = (own && cs.n > 0) ? cs.S : 0.0;
-  const float wm = own ? cs.m : 0.0f;
+  S.rcnt[t] = own ? cs.ncand : 0u;
   wave_argmax(mv, mi);
   ff = wave_or_i(ff);
   gv = wave_max_f(gv);
+  // the wave's chunk masses sum exp(l - m_c) rescaled to the wave's maximum
+  const double sw = wave_sum((own && cs.n > 0) ? cs.S * exp((double)cs.m - (double)mv) : 0.0);
   if (lane == 0) {
     S.v[w] = mv;
     S.i[w] = mi;
     S.f[w] = ff;
     S.g[w] = gv;
+    S.sw[w] = sw;
   }
-  for (int q = t; q < 256; q += FTPB) {
-    S.hist[q] = 0u;
-    S.hmass[q] = 0ull;
-  }
+  S.hist[t] = 0u;
+  S.hmass[t] = 0ull;
+  if (t < 2) S.tag[t] = -1;
   __syncthreads();
-  float m = S.v[0], G = S.g[0];
-  int arg = S.i[0], flags = S.f[0];
-#pragma unroll
-  for (int q = 1; q < FTPB / WAVE; ++q) {
-    argmax_merge(m, arg, S.v[q], S.i[q]);
-    flags |= S.f[q];
-    G = fmaxf(G, S.g[q]);
-  }
+  // lane q holds wave q's results
+  const float vq = lane < GW ? S.v[lane] : -INFINITY;
+  const double swq = lane < GW ? S.sw[lane] : 0.0;
+  float m = vq, G = lane < GW ? S.g[lane] : -INFINITY;
+  int arg = lane < GW ? S.i[lane] : -1, flags = lane < GW ? S.f[lane] : 0;
+  wave_argmax(m, arg);
+  flags = wave_or_i(flags);
+  G = wave_max_f(G);
+  // the whole row's mass, relative to m (used while the kept set reaches below G)
+  const double S_all = wave_sum(swq > 0.0 ? swq * exp((double)vq - (double)m) : 0.0);
   auto finish = [&](int status, int token, int accept, double sig, uint64_t last_key) {
     if (t != 0) return;
     rsp->status = status;
@@ -295,190 +272,176 @@ __global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
     const bool icdf = a.noise_mode == STRIM_NOISE_ICDF;
     // rank-indexed noise needs every kept token's rank
     if ((p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp && !icdf) return false;
-    if (ne > FTPB * GNE) return false;
+    if (ne > GCAND) return false;
     const bool all_in = !(G > -INFINITY);  // every allowed token is a candidate
     // min-p keeps a set that lies above G only if G itself fails it
     if (minp && !all_in && ((double)G - (double)m) >= p.lmp) return false;
     const float span = all_in ? 64.0f : fminf(fmaxf(m - G, 1.0f / 64.0f), 64.0f);
-    const float hscale = 256.0f / span;
-    // which of this thread's slots hold a candidate: entry e = q FTPB + t lies in region
-    // 2 q + (t >> 7) (FTPB = 2 GCAP), at offset t & 127
-    static_assert(FTPB == 2 * GCAP, "two regions per pass of the workgroup");
+    const float hscale = (float)GNB / span;
+    // which of this thread's slots hold a candidate: entry e = q GT + t lies in region
+    // q (GT / GCAP) + (t >> 7), at offset t & 127
     uint32_t vmask = 0u;
     {
       uint32_t rc[GNE];
 #pragma unroll
-      for (int q = 0; q < GNE; ++q) rc[q] = S.rcnt[min(2 * q + (t >> 7), 255)];
+      for (int q = 0; q < GNE; ++q) rc[q] = S.rcnt[min(q * (GT / GCAP) + (t >> 7), GT - 1)];
 #pragma unroll
       for (int q = 0; q < GNE; ++q)
-        vmask |= ((q * FTPB + t < ne) & ((uint32_t)(t & (GCAP - 1)) < rc[q]) ? 1u : 0u) << q;
+        vmask |= (((q * GT + t < ne) & ((uint32_t)(t & (GCAP - 1)) < rc[q])) ? 1u : 0u) << q;
     }
     // bin every candidate above G (passing min-p); its count atomic returns its place in
-    // the bin. No branch around the atomics: a lane without a candidate adds to its own
-    // slot.
-    // (a wave skips the slots where none of its lanes has a candidate: LDS atomics are
-    // this step's cost)
-    uint32_t place[GNE];
+    // the bin (the places are taken after every atomic is issued)
+    uint32_t o[GNE];
+    int bn[GNE];
+    uint64_t cm[GNE];
 #pragma unroll
     for (int q = 0; q < GNE; ++q) {
       const float l = cd[q].l;
       const bool k = ((vmask >> q) & 1u) & (l > G) & (l > -INFINITY) &
                      (!minp | (((double)l - (double)m) >= p.lmp));
-      place[q] = 0xFFFFFFFFu;
-      if (__ballot(k)) {
-        const int bn = k ? gbin256(m, l, hscale) : 0;
-        const uint64_t cm = k ? gmass(l, m) : 0ull;
-        const uint32_t o = atomicAdd(k ? &S.hist[bn] : &S.dcnt[t], 1u);
-        atomicAdd(k ? &S.hmass[bn] : &S.dmass[t], (unsigned long long)cm);
-        place[q] = k ? (((uint32_t)bn << 24) | o) : 0xFFFFFFFFu;
-      }
-    }
-    // the whole row's mass from the chunk sums (used while the kept set reaches below
-    // G), folded with the barrier the histogram needs
-    const double S_all = block_sum_f64<FTPB>(wS * exp((double)wm - (double)m), S.d);
-    // inclusive bin prefixes (wave 0; a lane owns bins 4 lane .. 4 lane + 3), the counts'
-    // exclusive prefix kept for the scatter
-    if (w == 0) {
-      uint32_t c4[4], cs4 = 0u;
-      uint64_t m4[4], ms4 = 0ull;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        c4[q] = S.hist[4 * lane + q];
-        m4[q] = S.hmass[4 * lane + q];
-        cs4 += c4[q];
-        ms4 += m4[q];
-      }
-      uint32_t rc = wave_incl_scan_u32(cs4) - cs4;
-      uint64_t rm = wave_incl_scan_u64(ms4) - ms4;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        rc += c4[q];
-        rm += m4[q];
-        S.hist[4 * lane + q] = rc;
-        S.hmass[4 * lane + q] = rm;
+      bn[q] = k ? gbin(m, l, hscale) : -1;
+      cm[q] = k ? gmass(l, m) : 0ull;
+      o[q] = 0u;
+      if (k) {
+        o[q] = atomicAdd(&S.hist[bn[q]], 1u);
+        atomicAdd(&S.hmass[bn[q]], (unsigned long long)cm[q]);
       }
     }
     __syncthreads();
-    // scatter into bin order (bin bn starts at hist[bn - 1]); a lane without a candidate
-    // writes to its own slot
-    uint32_t start[GNE];
-#pragma unroll
-    for (int q = 0; q < GNE; ++q) {
-      const int bn = (int)(place[q] >> 24);
-      start[q] = S.hist[bn > 0 && bn < 256 ? bn - 1 : 0];
-    }
-#pragma unroll
-    for (int q = 0; q < GNE; ++q) {
-      const bool k = place[q] != 0xFFFFFFFFu;
-      if (__ballot(k)) {
-        const int bn = (int)(place[q] >> 24);
-        const uint32_t o = (bn > 0 ? start[q] : 0u) + (place[q] & 0xFFFFFFu);
-        uint64_t* kd = k ? &S.bkey[o] : &S.dmass[t];
-        uint64_t* md = k ? &S.bmass[o] : &S.dmass[t];
-        *kd = ckey(cd[q].l, cd[q].id);
-        *md = k ? gmass(cd[q].l, m) : 0ull;
+    // group-local inclusive prefixes: wave w over bins 64 w .. 64 w + 63
+    {
+      const int bb = w * WAVE + lane;
+      const uint32_t ci = wave_incl_scan_u32(S.hist[bb]);
+      const uint64_t mi2 = wave_incl_scan_u64(S.hmass[bb]);
+      S.hist[bb] = ci;
+      S.hmass[bb] = mi2;
+      if (lane == WAVE - 1) {
+        S.gc[w] = ci;
+        S.gm[w] = mi2;
       }
     }
     __syncthreads();
-    const uint32_t n_all = S.hist[255];
-    const uint64_t m_all = S.hmass[255];
-    if (n_all == 0u) return false;
-
-    // ---- wave 0: the k-th token, the top-p cut and the icdf draw ----------------
-    // res: [0] ok, [1] bound1 (last kept key), [2] S1 (kept mass), [3] token (icdf),
-    // [4] the draft's mass when kept
-    if (w == 0) {
-      uint64_t ok = 1ull, bound0 = ~0ull, bound1 = ~0ull, S0 = 0ull, S1 = 0ull, wd = 0ull;
-      int token = -1;
-      GHit hit;
-      bool known0 = all_in || minp;  // every token of the set is a candidate
-      do {
-        // top-k (after min-p)
-        if (topk) {
-          if (n_all >= (uint32_t)p.top_k) {
-            if (!gsearch(S, m, hscale, false, (double)(p.top_k - 1), ~0ull, -1, 0ull, 256, hit)) {
-              ok = 0ull;
-              break;
-            }
-            bound0 = (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) ? (hit.key | 0xFFFFFFFFull) : hit.key;
-            known0 = true;
-          } else if (!all_in) {
-            ok = 0ull;  // the k-th token lies at or below G
-            break;
-          }
+    // lane g: inclusive prefix of the group totals
+    const uint64_t gcl = lane < GW ? (uint64_t)S.gc[lane] : 0ull;
+    const uint64_t gcinc = wave_incl_scan_u64(gcl);
+    const uint64_t gminc = wave_incl_scan_u64(lane < GW ? S.gm[lane] : 0ull);
+    const uint64_t n_all = rl_u64(gcinc, GW - 1), m_all = rl_u64(gminc, GW - 1);
+    if (n_all == 0ull) return false;
+    // every candidate with its mass into bin order: bin b starts at the cumulative count
+    // of the bins before it (the group's exclusive prefix from lane g, plus the bins
+    // before b in the group)
+    {
+      const int gce = (int)(gcinc - gcl);
+#pragma unroll
+      for (int q = 0; q < GNE; ++q) {
+        const int bq = bn[q] < 0 ? 0 : bn[q];
+        const int before = __shfl(gce, bq / WAVE) + ((bq & (WAVE - 1)) ? (int)S.hist[bq - 1] : 0);
+        if (bn[q] >= 0) {
+          S.bkey[before + o[q]] = ckey(cd[q].l, cd[q].id);
+          S.bmass[before + o[q]] = cm[q];
         }
-        // the kept mass before top-p: candidates up to bound0, or the chunk sums
-        if (!known0) S0 = (uint64_t)__double2ull_rn(S_all * GFIX);
-        else if (bound0 == ~0ull) S0 = m_all;
-        else S0 = gmass_upto(S, m, hscale, bound0);
-        // top-p: the last kept token is the first whose inclusive mass exceeds P S0 (a
-        // token is dropped iff the mass before it exceeds P, SpecSampling.swift:62-66)
+      }
+    }
+    __syncthreads();
+
+    // ---- the decisions, in order: 0 the k-th token (count), 1 the top-p cut (mass), 2
+    // the icdf draw (mass, without the draft) -----------------------------------------
+    bool known0 = all_in || minp;  // every token of the set is a candidate
+    uint64_t bound0 = ~0ull, S0 = known0 ? m_all : (uint64_t)__double2ull_rn(S_all * GFIX);
+    uint64_t bound1 = ~0ull, S1 = S0, wd = 0ull;
+    bool known1 = known0;
+    int token = -1;
+    int nres = 0;  // decisions resolved so far (consecutive ones alternate result slots)
+    for (int step = 0; step < 3; ++step) {
+      bool mass = true;
+      double thr;
+      uint64_t bound, xw = 0ull;
+      int excl = -1, xb = GNB;
+      if (step == 0) {
+        if (!topk) continue;
+        if (n_all < (uint64_t)p.top_k) {
+          if (!all_in) return false;  // the k-th token lies at or below G
+          continue;                   // every allowed token is kept
+        }
+        mass = false;
+        thr = (double)(p.top_k - 1);
+        bound = ~0ull;
+      } else if (step == 1) {
         bound1 = bound0;
         S1 = S0;
-        bool known1 = known0;
-        if (topp) {
-          if (!gsearch(S, m, hscale, true, (double)p.top_p * (double)S0, bound0, -1, 0ull, 256,
-                       hit)) {
-            ok = 0ull;
-            break;
-          }
-          if (hit.key != ~0ull) {
-            bound1 = hit.key;
-            S1 = hit.mass_before + hit.mass;
-            known1 = true;
-          } else if (!known0) {
-            ok = 0ull;  // the cut lies at or below G
-            break;
-          }
-        }
-        if (!icdf && !known1) {
-          ok = 0ull;
-          break;
-        }
-        // the draft of a verify row
-        int db = 256;
+        known1 = known0;
+        if (!topp) continue;
+        // the last kept token is the first whose inclusive mass exceeds P S0 (a token is
+        // dropped iff the mass before it exceeds P, SpecSampling.swift:62-66)
+        thr = (double)p.top_p * (double)S0;
+        bound = bound0;
+      } else {
+        if (!icdf && !known1) return false;
+        // the draft of a verify row: kept? its mass, and its bin when a candidate
         if (vdr && l_draft > -INFINITY && ckey(l_draft, draft) <= bound1) {
           wd = gmass(l_draft, m);
-          if (l_draft > G && (!minp || ((double)l_draft - (double)m) >= p.lmp))
-            db = gbin256(m, l_draft, hscale);
-        }
-        if (icdf) {
-          const double thr = (double)u_draw * (double)(S1 - wd);
-          if (!gsearch(S, m, hscale, true, thr, bound1, vdr ? draft : -1, db < 256 ? wd : 0ull,
-                       db, hit)) {
-            ok = 0ull;
-            break;
+          if (l_draft > G && (!minp || ((double)l_draft - (double)m) >= p.lmp)) {
+            xb = gbin(m, l_draft, hscale);
+            xw = wd;
           }
-          if (hit.key != ~0ull) token = (int)(uint32_t)hit.key;
-          else if (!known1) { ok = 0ull; break; }  // the draw lies at or below G
-          else token = arg;                        // only the draft kept: the first kept
         }
-      } while (false);
-      if (lane == 0) {
-        S.res[0] = ok;
-        S.res[1] = bound1;
-        S.res[2] = S1;
-        S.res[3] = (uint64_t)(int64_t)token;
-        S.res[4] = wd;
+        if (!icdf) break;
+        thr = (double)u_draw * (double)(S1 - wd);
+        bound = bound1;
+        excl = draft;
+      }
+      const int bb = bound == ~0ull ? GNB - 1 : gbin(m, key_l(bound), hscale);
+      const uint64_t ginc = mass ? gminc : gcinc;
+      const int bz = gfind_bin(S, mass, ginc, thr, bb, xw, xb);
+      const uint64_t c0 = gcum(S, false, gcinc, bz - 1);
+      const int nzc = (int)(gcum(S, false, gcinc, bz) - c0);
+      if (nzc > GZCAP) return false;
+      const uint64_t m0 = gcum(S, true, gminc, bz - 1) - (bz - 1 >= xb ? xw : 0ull);
+      const GHit h = gresolve(S, nres++, (int)c0, nzc, mass, thr, bound, excl, c0, m0);
+      if (step == 0) {
+        if (h.key == ~0ull) return false;
+        known0 = true;
+        if (!(p.flags & STRIM_FLAG_TOPK_KEEP_TIES)) {
+          bound0 = h.key;
+          S0 = h.mass_before + h.mass;
+        } else {
+          // the keys tied with the k-th one are kept too (same value, same bin)
+          bound0 = h.key | 0xFFFFFFFFull;
+          uint64_t loc = (t < nzc && S.bkey[c0 + t] <= bound0) ? S.bmass[c0 + t] : 0ull;
+          loc = wave_sum_u64(loc);
+          if (lane == 0) S.u[w] = loc;
+          __syncthreads();
+          uint64_t s = 0ull;
+#pragma unroll
+          for (int q = 0; q < GW; ++q) s += S.u[q];
+          S0 = gcum(S, true, gminc, bz - 1) + s;
+        }
+      } else if (step == 1) {
+        if (h.key != ~0ull) {
+          bound1 = h.key;
+          S1 = h.mass_before + h.mass;
+          known1 = true;
+        } else if (!known0) {
+          return false;  // the cut lies at or below G
+        }
+      } else {
+        if (h.key != ~0ull) token = (int)(uint32_t)h.key;
+        else if (!known1) return false;  // the draw lies at or below G
+        else token = arg;                // only the draft kept: the first kept
       }
     }
-    __syncthreads();
-    if (S.res[0] == 0ull) return false;
-    const uint64_t bound1 = S.res[1], S1 = S.res[2], wd = S.res[4];
-    int token = (int)(int64_t)S.res[3];
     if (!icdf) {
-      // Gumbel: every kept candidate (key <= bound1, not the draft) scored on all waves
+      // ---- Gumbel: every kept candidate (key <= bound1, not the draft) ----------------
       const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
       const bool cand_sorted = no_lse ? topp : (topk || topp);
-      const int excl = vdr ? draft : -1;
       const double lse = log((double)S1 / GFIX);
       double bsc = -INFINITY;
       uint64_t btk = ~0ull;
       int bid = -1;
-      for (uint32_t i = t; i < n_all; i += FTPB) {
+      for (int i = t; i < (int)n_all; i += GT) {
         const uint64_t k = S.bkey[i];
         const int id = (int)(uint32_t)k;
-        if (k > bound1 || id == excl) continue;
+        if (k > bound1 || id == draft) continue;
         const float l = key_l(k);
         const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
                                 : philox_uniform(pkey, (uint64_t)id);
@@ -487,7 +450,7 @@ __global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
         const uint64_t tk = cand_sorted ? k : (uint64_t)id;
         if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) { bsc = sc; btk = tk; bid = id; }
       }
-      block_argmax_score<FTPB>(bsc, btk, bid, S.d, S.u, S.i, &S.misc[3]);
+      block_argmax_score<GT>(bsc, btk, bid, S.d, S.u, S.i, &S.misc[3]);
       token = S.misc[3];
       if (token < 0) token = arg;  // only the draft kept
     }
@@ -499,7 +462,7 @@ __global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
 
   // ---- a decision at or below G: the exact streaming resolution --------------------
   XScratch xs;
-  xs.key = S.bkey;
+  xs.key = S.xkey;
   xs.hc = S.xhc;
   xs.cnt = S.xcnt;
   xs.u2 = S.xu2;
@@ -525,8 +488,12 @@ __global__ __launch_bounds__(FTPB) void k_gfinal(Args a) {
   xa.noise_stride = a.noise_stride;
   xa.has_q = 0;
   __syncthreads();
-  const XOut xo = exact_row<FTPB>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
+  const XOut xo = exact_row<GT>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
   finish(xo.status, xo.token, xo.accept, xo.sig, xo.last_key);
+}
+
+hipError_t launch_gfinal(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  return launch_args((const void*)k_gfinal, dim3((unsigned)a.R), dim3(GT), a, st, e0, e1);
 }
 
 }  // namespace strim
