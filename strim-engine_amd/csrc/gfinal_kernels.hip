@@ -13,14 +13,17 @@
 //   1. the chunk statistics and every candidate slot are loaded together (the slots of
 //      a region past its count are read and dropped, so nothing waits for the counts);
 //      the waves' maxima, flags, bounds and chunk mass sums are merged with one barrier;
-//   2. the candidates above G are binned by d = m - l into GNB bins of counts and
-//      fixed-point masses, round(2^50 * expf(l - m)) (integer sums: every cumulative mass
-//      is independent of summation order, and 8192 unit masses stay below 2^63; the float
-//      exp keeps each mass within 2^-23 relative, far inside the 1e-6 decision and
-//      probability tolerances). The count atomic returns each candidate's place in its
-//      bin. Each wave turns its 64 bins into inclusive prefixes (a bin's cumulative count
-//      or mass is its group's prefix plus the totals of the groups before it), and every
-//      candidate is stored with its mass in bin order;
+//   2. the candidates above G are binned by d = m - l into GNB bins. A bin is one 64-bit
+//      word, count << 49 | mass, so each candidate costs one LDS atomic (they run about
+//      one lane per cycle, so their number sets this step's time), and the atomic's old
+//      count is the candidate's place in its bin. Masses are fixed point,
+//      round(2^35 * expf(l - m)): integer sums make every cumulative mass independent of
+//      summation order, 8192 unit masses stay below 2^48, and the per-token error (the
+//      float exp's 2^-23 relative plus 2^-36 absolute) keeps any cumulative mass within
+//      5e-7 relative of the exact one, inside the 1e-6 decision tolerance. Each wave turns
+//      its 64 bins into inclusive prefixes (a bin's cumulative count or mass is its
+//      group's prefix plus the totals of the groups before it), and every candidate is
+//      stored with its mass in bin order;
 //   3. the decisions run in order (the k-th token, the top-p cut, the icdf draw) through
 //      one loop, so their shared code is fetched once: each finds the bin where its
 //      threshold is crossed from the prefixes, and each key of that bin counts the bin's
@@ -39,7 +42,9 @@ constexpr int GNE = 8;              // candidate slots per thread: W * GCAP <= G
 constexpr int GCAND = GT * GNE;     // candidates of a row held in bin order
 constexpr int GNB = GW * WAVE;      // histogram bins of d = m - l (64 per group)
 constexpr int GZCAP = GT;           // keys of one bin a decision resolves (one per thread)
-constexpr double GFIX = 1125899906842624.0;  // 2^50: the fixed-point unit of mass
+constexpr double GFIX = 34359738368.0;  // 2^35: the fixed-point unit of mass
+constexpr int GCSH = 49;                // a bin word: count << GCSH | mass
+constexpr uint64_t GMMASK = (1ull << GCSH) - 1ull;
 static_assert(GCAP == 128, "candidate slot of an entry: e >> 7, e & 127");
 static_assert(GT % GCAP == 0, "whole regions per pass of the workgroup");
 static_assert(GNB == GT, "one bin per thread to clear");
@@ -48,8 +53,9 @@ static_assert(GNB == GT, "one bin per thread to clear");
 struct GFinalShared {
   union {
     struct {                  // the decision from the candidates
-      uint64_t bkey[GCAND];   // the candidates above G in bin order (64 KB)
-      uint64_t bmass[GCAND];  // their fixed-point masses (64 KB)
+      uint64_t bkey[GCAND + WAVE];   // the candidates above G in bin order (64 KB; the
+                                     // last WAVE entries take the writes of empty slots)
+      uint64_t bmass[GCAND + WAVE];  // their fixed-point masses
     };
     struct {                  // the exact streaming resolution (rows decided at or below G)
       uint64_t xkey[XB > XCOL ? XB : XCOL];
@@ -59,14 +65,13 @@ struct GFinalShared {
       XState x;
     };
   };
-  uint64_t hmass[GNB];        // fixed-point mass per bin, then the group-local inclusive prefix
-  uint32_t hist[GNB];         // count per bin, then the group-local inclusive prefix
-  uint64_t gm[GW];            // per group: total mass
-  uint32_t gc[GW];            // per group: total count
+  uint64_t hist[GNB];         // per bin count << GCSH | mass, then the group-local
+                              // inclusive prefix
+  uint64_t gt[GW];            // per group: its total
   uint32_t rcnt[GT];          // per chunk: its candidates
   float v[GW], g[GW];
   int i[GW], f[GW];
-  double sw[GW];              // per wave: its chunks' mass, relative to the wave's maximum
+  double sw[GW];              // per wave: its chunks' mass, relative to the row maximum
   double d[GW];
   uint64_t u[GW];
   int misc[8];
@@ -74,33 +79,37 @@ struct GFinalShared {
   int32_t tag[2];             // alternating; tag = the decision's number when it holds one)
 };
 
-// Fixed-point mass of a token: round(2^50 * exp(l - m)), from the float exp of the
+// Fixed-point mass of a token: round(2^35 * exp(l - m)), from the float exp of the
 // float difference (l <= m).
 __device__ __forceinline__ uint64_t gmass(float l, float m) {
-  return (uint64_t)(expf(l - m) * 1125899906842624.0f);
+  return (uint64_t)(expf(l - m) * 34359738368.0f + 0.5f);
 }
 __device__ __forceinline__ int gbin(float m, float l, float hscale) {
   return (int)fminf((m - l) * hscale, (float)(GNB - 1));
 }
 __device__ __forceinline__ float key_l(uint64_t k) { return fkey_desc_inv((uint32_t)(k >> 32)); }
 
-// Cumulative count (mass == false) or mass of bins 0 .. b, from the group-local prefixes
-// and `ginc`, lane g's inclusive prefix of the group totals of the same kind (b is
-// wave-uniform).
-__device__ __forceinline__ uint64_t gcum(const GFinalShared& S, bool mass, uint64_t ginc, int b) {
+// Cumulative bin word (count << GCSH | mass) of bins 0 .. b, from the group-local
+// prefixes and `ginc`, lane g's inclusive prefix of the group totals (b is wave-uniform).
+__device__ __forceinline__ uint64_t gcum(const GFinalShared& S, uint64_t ginc, int b) {
   if (b < 0) return 0ull;
   const int g = b / WAVE;
   const uint64_t before = g > 0 ? rl_u64(ginc, g - 1) : 0ull;
-  return before + (mass ? S.hmass[b] : (uint64_t)S.hist[b]);
+  return before + S.hist[b];
 }
+__device__ __forceinline__ uint64_t wcount(uint64_t x) { return x >> GCSH; }
+__device__ __forceinline__ uint64_t wmass(uint64_t x) { return x & GMMASK; }
 
 // The first bin whose cumulative count or mass, less excl_w from bin excl_b on, exceeds
 // thr, among the bins before bb; bb when none does (every wave computes the same bin).
 __device__ __forceinline__ int gfind_bin(const GFinalShared& S, bool mass, uint64_t ginc,
                                          double thr, int bb, uint64_t excl_w, int excl_b) {
   const int lane = threadIdx.x & (WAVE - 1);
+  auto val = [&](uint64_t x, bool ex) -> uint64_t {
+    return mass ? wmass(x) - (ex ? excl_w : 0ull) : wcount(x);
+  };
   // the first group whose cumulative total (with the exclusion) exceeds thr
-  const uint64_t gv = ginc - ((mass && excl_b <= WAVE * lane + WAVE - 1) ? excl_w : 0ull);
+  const uint64_t gv = val(ginc, excl_b <= WAVE * lane + WAVE - 1);
   const uint64_t gh = __ballot(lane < GW && (double)gv > thr);
   if (gh == 0ull) return bb;
   const int g = (int)__ffsll((long long)gh) - 1;
@@ -108,8 +117,7 @@ __device__ __forceinline__ int gfind_bin(const GFinalShared& S, bool mass, uint6
   // within the group: one bin per lane
   const int b = g * WAVE + lane;
   const uint64_t before = g > 0 ? rl_u64(ginc, g - 1) : 0ull;
-  const uint64_t bv = before + (mass ? S.hmass[b] : (uint64_t)S.hist[b]) -
-                      ((mass && b >= excl_b) ? excl_w : 0ull);
+  const uint64_t bv = val(before + S.hist[b], b >= excl_b);
   const uint64_t bh = __ballot((double)bv > thr);
   const int bz = bh ? g * WAVE + (int)__ffsll((long long)bh) - 1 : bb;
   return bz < bb ? bz : bb;
@@ -207,29 +215,21 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   wave_argmax(mv, mi);
   ff = wave_or_i(ff);
   gv = wave_max_f(gv);
-  // the wave's chunk masses sum exp(l - m_c) rescaled to the wave's maximum
-  const double sw = wave_sum((own && cs.n > 0) ? cs.S * exp((double)cs.m - (double)mv) : 0.0);
   if (lane == 0) {
     S.v[w] = mv;
     S.i[w] = mi;
     S.f[w] = ff;
     S.g[w] = gv;
-    S.sw[w] = sw;
   }
-  S.hist[t] = 0u;
-  S.hmass[t] = 0ull;
+  S.hist[t] = 0ull;
   if (t < 2) S.tag[t] = -1;
   __syncthreads();
   // lane q holds wave q's results
-  const float vq = lane < GW ? S.v[lane] : -INFINITY;
-  const double swq = lane < GW ? S.sw[lane] : 0.0;
-  float m = vq, G = lane < GW ? S.g[lane] : -INFINITY;
+  float m = lane < GW ? S.v[lane] : -INFINITY, G = lane < GW ? S.g[lane] : -INFINITY;
   int arg = lane < GW ? S.i[lane] : -1, flags = lane < GW ? S.f[lane] : 0;
   wave_argmax(m, arg);
   flags = wave_or_i(flags);
   G = wave_max_f(G);
-  // the whole row's mass, relative to m (used while the kept set reaches below G)
-  const double S_all = wave_sum(swq > 0.0 ? swq * exp((double)vq - (double)m) : 0.0);
   auto finish = [&](int status, int token, int accept, double sig, uint64_t last_key) {
     if (t != 0) return;
     rsp->status = status;
@@ -289,57 +289,76 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       for (int q = 0; q < GNE; ++q)
         vmask |= (((q * GT + t < ne) & ((uint32_t)(t & (GCAP - 1)) < rc[q])) ? 1u : 0u) << q;
     }
-    // bin every candidate above G (passing min-p); its count atomic returns its place in
-    // the bin (the places are taken after every atomic is issued)
-    uint32_t o[GNE];
+    // bin every candidate above G (passing min-p); the atomic's old count is its place in
+    // the bin. A lane without a candidate leaves old[q] unset and never reads it; the
+    // empty asm statements after the loop keep the compiler from reading any result
+    // before every atomic is issued (it would otherwise wait for each in turn).
+    uint64_t old[GNE], cm[GNE];
     int bn[GNE];
-    uint64_t cm[GNE];
 #pragma unroll
     for (int q = 0; q < GNE; ++q) {
       const float l = cd[q].l;
-      const bool k = ((vmask >> q) & 1u) & (l > G) & (l > -INFINITY) &
-                     (!minp | (((double)l - (double)m) >= p.lmp));
+      const bool k = ((vmask >> q) & 1u) && l > G && l > -INFINITY &&
+                     (!minp || ((double)l - (double)m) >= p.lmp);
       bn[q] = k ? gbin(m, l, hscale) : -1;
-      cm[q] = k ? gmass(l, m) : 0ull;
-      o[q] = 0u;
       if (k) {
-        o[q] = atomicAdd(&S.hist[bn[q]], 1u);
-        atomicAdd(&S.hmass[bn[q]], (unsigned long long)cm[q]);
+        cm[q] = gmass(l, m);
+        old[q] = atomicAdd(&S.hist[bn[q]], (unsigned long long)((1ull << GCSH) | cm[q]));
       }
+    }
+#pragma unroll
+    for (int q = 0; q < GNE; ++q) asm volatile("" : "+v"(old[q]));
+    // the whole row's mass relative to m, from the chunk sums (used while the kept set
+    // reaches below G), while the atomics complete
+    {
+      const double sw = wave_sum((own && cs.n > 0) ? cs.S * exp((double)cs.m - (double)m) : 0.0);
+      if (lane == 0) S.sw[w] = sw;
     }
     __syncthreads();
     // group-local inclusive prefixes: wave w over bins 64 w .. 64 w + 63
     {
       const int bb = w * WAVE + lane;
-      const uint32_t ci = wave_incl_scan_u32(S.hist[bb]);
-      const uint64_t mi2 = wave_incl_scan_u64(S.hmass[bb]);
+      const uint64_t ci = wave_incl_scan_u64(S.hist[bb]);
       S.hist[bb] = ci;
-      S.hmass[bb] = mi2;
-      if (lane == WAVE - 1) {
-        S.gc[w] = ci;
-        S.gm[w] = mi2;
-      }
+      if (lane == WAVE - 1) S.gt[w] = ci;
     }
+    double S_all = 0.0;
+#pragma unroll
+    for (int q = 0; q < GW; ++q) S_all += S.sw[q];
     __syncthreads();
     // lane g: inclusive prefix of the group totals
-    const uint64_t gcl = lane < GW ? (uint64_t)S.gc[lane] : 0ull;
-    const uint64_t gcinc = wave_incl_scan_u64(gcl);
-    const uint64_t gminc = wave_incl_scan_u64(lane < GW ? S.gm[lane] : 0ull);
-    const uint64_t n_all = rl_u64(gcinc, GW - 1), m_all = rl_u64(gminc, GW - 1);
+    const uint64_t gl = lane < GW ? S.gt[lane] : 0ull;
+    const uint64_t ginc = wave_incl_scan_u64(gl);
+    const uint64_t tot = rl_u64(ginc, GW - 1);
+    const uint64_t n_all = wcount(tot), m_all = wmass(tot);
     if (n_all == 0ull) return false;
     // every candidate with its mass into bin order: bin b starts at the cumulative count
     // of the bins before it (the group's exclusive prefix from lane g, plus the bins
-    // before b in the group)
+    // before b in the group); a slot without a candidate writes past the row's entries
     {
-      const int gce = (int)(gcinc - gcl);
+      const int gce = (int)wcount(ginc - gl);
+      // every read first (the empty asm statements keep them ahead of their uses), then
+      // every write
+      int at[GNE];
+      uint32_t hb[GNE];
+      int gb[GNE];
 #pragma unroll
       for (int q = 0; q < GNE; ++q) {
         const int bq = bn[q] < 0 ? 0 : bn[q];
-        const int before = __shfl(gce, bq / WAVE) + ((bq & (WAVE - 1)) ? (int)S.hist[bq - 1] : 0);
-        if (bn[q] >= 0) {
-          S.bkey[before + o[q]] = ckey(cd[q].l, cd[q].id);
-          S.bmass[before + o[q]] = cm[q];
-        }
+        hb[q] = (uint32_t)(S.hist[bq > 0 ? bq - 1 : 0] >> 32);
+        gb[q] = __shfl(gce, bq / WAVE);
+      }
+#pragma unroll
+      for (int q = 0; q < GNE; ++q) asm volatile("" : "+v"(hb[q]), "+v"(gb[q]));
+#pragma unroll
+      for (int q = 0; q < GNE; ++q) {
+        const int before = gb[q] + ((bn[q] & (WAVE - 1)) ? (int)(hb[q] >> (GCSH - 32)) : 0);
+        at[q] = bn[q] >= 0 ? before + (int)wcount(old[q]) : GCAND + lane;
+      }
+#pragma unroll
+      for (int q = 0; q < GNE; ++q) {
+        S.bkey[at[q]] = ckey(cd[q].l, cd[q].id);
+        S.bmass[at[q]] = cm[q];
       }
     }
     __syncthreads();
@@ -391,12 +410,12 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         excl = draft;
       }
       const int bb = bound == ~0ull ? GNB - 1 : gbin(m, key_l(bound), hscale);
-      const uint64_t ginc = mass ? gminc : gcinc;
       const int bz = gfind_bin(S, mass, ginc, thr, bb, xw, xb);
-      const uint64_t c0 = gcum(S, false, gcinc, bz - 1);
-      const int nzc = (int)(gcum(S, false, gcinc, bz) - c0);
+      const uint64_t w0 = gcum(S, ginc, bz - 1);
+      const uint64_t c0 = wcount(w0);
+      const int nzc = (int)(wcount(gcum(S, ginc, bz)) - c0);
       if (nzc > GZCAP) return false;
-      const uint64_t m0 = gcum(S, true, gminc, bz - 1) - (bz - 1 >= xb ? xw : 0ull);
+      const uint64_t m0 = wmass(w0) - (bz - 1 >= xb ? xw : 0ull);
       const GHit h = gresolve(S, nres++, (int)c0, nzc, mass, thr, bound, excl, c0, m0);
       if (step == 0) {
         if (h.key == ~0ull) return false;
@@ -414,7 +433,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
           uint64_t s = 0ull;
 #pragma unroll
           for (int q = 0; q < GW; ++q) s += S.u[q];
-          S0 = gcum(S, true, gminc, bz - 1) + s;
+          S0 = wmass(w0) + s;
         }
       } else if (step == 1) {
         if (h.key != ~0ull) {
