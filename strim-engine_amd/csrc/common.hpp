@@ -15,6 +15,33 @@
 
 namespace strim {
 
+// An LDS object named with its address space, for data handed to functions that are
+// not inlined: across such a call a plain pointer is generic, and the compiler then
+// reaches LDS with flat instructions (slower atomics, and every wait for them also waits
+// for the outstanding global loads). Cast to a plain pointer at the use; the compiler
+// still sees where it points.
+template <typename T>
+using lds_t = __attribute__((address_space(3))) T;
+// The same for global memory: a pointer re-typed with it at the top of a function that
+// is not inlined gives its loads the global instructions again.
+template <typename T>
+using glb_t = __attribute__((address_space(1))) T;
+
+// A copy of a workgroup-uniform value held in scalar registers. Functions that are not
+// inlined receive every argument in vector registers; re-reading the uniform ones with
+// readfirstlane at the entry frees those registers (the exact resolution runs in
+// 1024-thread workgroups, whose threads get at most 128 of them).
+template <typename T>
+__device__ __forceinline__ T uniform_copy(const T& v) {
+  static_assert(sizeof(T) % 4 == 0, "whole 32-bit words");
+  struct W { uint32_t w[sizeof(T) / 4]; };
+  W in = __builtin_bit_cast(W, v), out;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i)
+    out.w[i] = (uint32_t)__builtin_amdgcn_readfirstlane((int)in.w[i]);
+  return __builtin_bit_cast(T, out);
+}
+
 constexpr int CHUNK = 4096;    // tokens per workgroup
 constexpr int TPB = 512;       // threads per streaming workgroup (8 waves of 64)
 constexpr int EPT = 8;         // tokens per thread

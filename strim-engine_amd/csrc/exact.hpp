@@ -29,7 +29,7 @@ struct XState {
 
 // The tokens a select ranges over: allowed, passing min-p (lmp = log(min_p), -inf for
 // none), with order key in [lo, bound], other than `excl`. rS != 0: the weights are the
-// general-q residual max(0, p - q) scaled by the kept mass rS (see x_wt).
+// general-q residual max(0, p - q) scaled by the kept mass rS (see x_wt_q).
 struct XUni {
   float m;
   double lmp;
@@ -76,8 +76,12 @@ __device__ __forceinline__ bool x_in(const XUni& u, float l, int id) {
   const uint64_t k = ckey(l, id);
   return k >= u.lo && k <= u.bound;
 }
+// Fixed-point weight of a token, round(2^43 * exp(l - m)), from the float exp of the
+// float difference: within 2^-23 relative of the exact weight (far inside the 1e-6
+// decision tolerance) and the same value in every pass, at a fraction of a double exp's
+// cost (one workgroup computes it for every token of the row, once per pass).
 __device__ __forceinline__ uint64_t x_weight(float l, float m) {
-  return (uint64_t)__double2ull_rn(exp((double)l - (double)m) * XFIX);
+  return (uint64_t)(expf(l - m) * 8796093022208.0f + 0.5f);
 }
 // Weight of a universe token: exp(l - m) in fixed point, or, for a residual universe,
 // max(0, W - round(q * rS)): the residual (p - q)^+ in units of the kept mass rS.
@@ -86,9 +90,6 @@ __device__ __forceinline__ uint64_t x_wt_q(const XUni& u, float l, double q) {
   if (u.rS == 0ull || q == 0.0) return W;
   const uint64_t qS = (uint64_t)__double2ull_rn(q * (double)u.rS);
   return W > qS ? W - qS : 0ull;
-}
-__device__ __forceinline__ uint64_t x_wt(const XArgs& a, const XUni& u, float l, int id) {
-  return x_wt_q(u, l, u.rS == 0ull ? 0.0 : xq_prob(a.q, id));
 }
 // q from a streamed draft value (-inf: not in the table)
 __device__ __forceinline__ double xq_of(const XQ& q, float v) {
@@ -117,22 +118,45 @@ __device__ __forceinline__ uint32_t x_first_fkey(uint32_t lo, uint32_t hi, F pre
 
 // One streaming pass over the row: fn(i0, l, qv) for every thread and window, with qv
 // the draft values v of a general-q row's tokens (-inf outside the table; all -inf for
-// other rows). Aligned rows without penalties keep XPD windows of loads in flight; the
-// others load each window when they reach it (the history counts are rebuilt per
-// window).
-constexpr int XPD = 4;
-template <int NT, bool BF16, bool Q, typename F>
-__device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, const RowParams& p, F&& fn) {
+// other rows). Aligned rows keep xpd() windows of loads in flight; rows with penalties
+// hold the history ids in registers (when they fit) and rebuild each window's counts in
+// LDS while the next windows' loads are in flight. Unaligned rows load each window when
+// they reach it.
+// windows of loads in flight: 1024-thread workgroups have half the registers per thread
+template <int NT>
+constexpr int xpd() { return NT >= 1024 ? 2 : 4; }
+template <int NT, bool BF16, bool Q, bool PEN, typename F>
+__device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, int b, int j,
+                                            const RowParams& p, uint32_t* s_cnt, F&& fn) {
+  constexpr int XPD = xpd<NT>();
   constexpr int WIN = NT * EPT;
   const int t = threadIdx.x;
+  int hid[hpt<NT>()];
+  int hl = 0;
+  if constexpr (PEN) {
+    hist_load<NT>(a, b, hid);
+    hl = hist_len(a, b);
+    // the history ids arrive before the window loads are issued: inside the window loop
+    // a load from before it would make every window wait for all of its loads
+    __builtin_amdgcn_s_waitcnt(0);
+  }
   const int64_t base = (int64_t)r * a.row_stride;
   const int nwin = (a.V + WIN - 1) / WIN;
   const uint8_t* mrow = a.mask ? (const uint8_t*)(a.mask + (int64_t)r * a.mask_stride)
                                : (const uint8_t*)a.logits;
+  // the streamed arrays as global pointers (this runs inside an out-of-line call)
+  const glb_t<const uint8_t>* lg = (const glb_t<const uint8_t>*)a.logits;
+  const glb_t<const uint8_t>* mg = (const glb_t<const uint8_t>*)mrow;
+  const glb_t<const uint32_t>* qdb = (const glb_t<const uint32_t>*)a.q.dbits;
+  const glb_t<const float>* qvq = (const glb_t<const float>*)a.q.vq;
+  // (clang vector types: the HIP vector classes cannot be assigned from a global
+  // reference)
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   struct Slot {
-    uint4 x0, x1;
+    u32x4 x0, x1;
     uint32_t mb, qb;
-    float4 q0, q1;
+    f32x4 q0, q1;
   };
   Slot sl[XPD];
   // every load of a window from a clamped index, no branch between them; a segment that
@@ -141,16 +165,16 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, const RowPara
     const int i0 = w * WIN + t * EPT;
     const int ii = i0 + EPT <= a.V ? i0 : 0;
     if constexpr (BF16) {
-      sd.x0 = *(const uint4*)((const uint16_t*)a.logits + base + ii);
+      sd.x0 = *(const glb_t<const u32x4>*)(lg + 2 * (base + ii));
     } else {
-      sd.x0 = *(const uint4*)((const float*)a.logits + base + ii);
-      sd.x1 = *(const uint4*)((const float*)a.logits + base + ii + 4);
+      sd.x0 = *(const glb_t<const u32x4>*)(lg + 4 * (base + ii));
+      sd.x1 = *(const glb_t<const u32x4>*)(lg + 4 * (base + ii + 4));
     }
-    sd.mb = mrow[a.mask ? (ii >> 3) : 0];
+    sd.mb = mg[a.mask ? (ii >> 3) : 0];
     if constexpr (Q) {
-      sd.qb = a.q.dbits[ii >> 5];
-      sd.q0 = *(const float4*)(a.q.vq + ii);
-      sd.q1 = *(const float4*)(a.q.vq + ii + 4);
+      sd.qb = qdb[ii >> 5];
+      sd.q0 = *(const glb_t<const f32x4>*)(qvq + ii);
+      sd.q1 = *(const glb_t<const f32x4>*)(qvq + ii + 4);
     }
   };
 #pragma unroll
@@ -160,6 +184,8 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, const RowPara
     for (int d = 0; d < XPD; ++d) {
       if (w + d < nwin) {
         const int i0 = (w + d) * WIN + t * EPT;
+        // this window's history counts (uniform: every thread takes the barriers)
+        if constexpr (PEN) hist_count<NT, WIN>(a, b, j, (w + d) * WIN, hid, hl, s_cnt);
         const Slot& sd = sl[d];
         float x[EPT];
         if constexpr (BF16) {
@@ -174,6 +200,19 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, const RowPara
                                   sd.x1.x, sd.x1.y, sd.x1.z, sd.x1.w};
 #pragma unroll
           for (int e = 0; e < EPT; ++e) x[e] = __uint_as_float(wv[e]);
+        }
+        if constexpr (PEN) {
+          // the penalties as process_tokens applies them, one rounding per step
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) {
+            const uint32_t c = s_cnt[t * EPT + e];
+            if (c > 0u) {
+              float v = x[e];
+              v = v > 0.0f ? v / p.rep : v * p.rep;
+              v = v - p.freq * (float)c;
+              x[e] = v - p.pres;
+            }
+          }
         }
         const uint32_t bits = a.mask ? ((uint32_t)sd.mb & 0xFFu) : 0xFFu;
         float l[EPT], qv[EPT];
@@ -205,8 +244,17 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, const RowPara
       const int id = iP + e;
       const bool ok = own && id < a.V && ((bits >> e) & 1u);
       const int ic = ok ? id : 0;
-      const float x = BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[base + ic])
-                           : ((const float*)a.logits)[base + ic];
+      float x = BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[base + ic])
+                     : ((const float*)a.logits)[base + ic];
+      if constexpr (PEN) {
+        // the last window's counts are still in s_cnt (it holds the tail)
+        const uint32_t c = s_cnt[(iP % WIN) + e];
+        if (c > 0u) {
+          x = x > 0.0f ? x / p.rep : x * p.rep;
+          x = x - p.freq * (float)c;
+          x = x - p.pres;
+        }
+      }
       l[e] = ok ? (p.greedy ? x : x / p.T) : -INFINITY;
       qv[e] = -INFINITY;
       if constexpr (Q) {
@@ -216,16 +264,21 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, const RowPara
     fn(iP, l, qv);
   }
 }
-template <int NT, typename F>
+// HQ: the caller may resolve general-q verify rows (the draft distribution's code is
+// compiled only then).
+template <int NT, bool HQ, typename F>
 __device__ __forceinline__ void x_pass(const XArgs& a, int r, int b, int j, const RowParams& p,
                                        uint32_t* s_cnt, F&& fn) {
-  if (a.vec_ok && !p.pen) {
+  const bool hq = HQ && a.has_q;
+  if (a.vec_ok && !(hq && p.pen)) {
     if (a.dtype == STRIM_DTYPE_BF16) {
-      if (a.has_q) x_pass_pipe<NT, true, true>(a, r, p, fn);
-      else x_pass_pipe<NT, true, false>(a, r, p, fn);
+      if (hq) x_pass_pipe<NT, true, true, false>(a, r, b, j, p, s_cnt, fn);
+      else if (p.pen) x_pass_pipe<NT, true, false, true>(a, r, b, j, p, s_cnt, fn);
+      else x_pass_pipe<NT, true, false, false>(a, r, b, j, p, s_cnt, fn);
     } else {
-      if (a.has_q) x_pass_pipe<NT, false, true>(a, r, p, fn);
-      else x_pass_pipe<NT, false, false>(a, r, p, fn);
+      if (hq) x_pass_pipe<NT, false, true, false>(a, r, b, j, p, s_cnt, fn);
+      else if (p.pen) x_pass_pipe<NT, false, false, true>(a, r, b, j, p, s_cnt, fn);
+      else x_pass_pipe<NT, false, false, false>(a, r, b, j, p, s_cnt, fn);
     }
     return;
   }
@@ -241,7 +294,7 @@ __device__ __forceinline__ void x_pass(const XArgs& a, int r, int b, int j, cons
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       qv[e] = -INFINITY;
-      if (a.has_q && i0 + e < a.V) {
+      if (hq && i0 + e < a.V) {
         const int id = i0 + e;
         if ((a.q.dbits[id >> 5] >> (id & 31)) & 1u) qv[e] = a.q.vq[id];
       }
@@ -266,7 +319,7 @@ __device__ __forceinline__ int x_digit(const XLevel& lv, float l, int id, float 
 
 // Count and fixed-point mass per digit of the universe's tokens inside the level.
 // Each thread accumulates runs of equal digits and flushes a run with one LDS atomic.
-template <int NT>
+template <int NT, bool HQ>
 __device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, const RowParams& p, const XUni& u,
                        const XLevel& lv, uint32_t* s_cnt, uint32_t* s_hc, uint64_t* s_hm) {
   for (int i = threadIdx.x; i < XB; i += NT) {
@@ -277,7 +330,7 @@ __device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, cons
   int cur = -1;
   uint32_t ac = 0u;
   uint64_t am = 0ull;
-  x_pass<NT>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT], const float (&qv)[EPT]) {
+  x_pass<NT, HQ>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT], const float (&qv)[EPT]) {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       if (!x_in(u, l[e], i0 + e)) continue;
@@ -293,7 +346,7 @@ __device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, cons
         am = 0ull;
       }
       ac += 1u;
-      am += x_wt_q(u, l[e], u.rS == 0ull ? 0.0 : xq_of(a.q, qv[e]));
+      am += x_wt_q(u, l[e], (HQ && u.rS != 0ull) ? xq_of(a.q, qv[e]) : 0.0);
     }
   });
   if (cur >= 0) {
@@ -305,14 +358,14 @@ __device__ __forceinline__ void x_hist(const XArgs& a, int r, int b, int j, cons
 
 // Gathers the order keys of the universe's tokens inside the level's digit `dg` (all of
 // them for mode 2) into s_col; returns their number (<= XCOL by construction).
-template <int NT>
+template <int NT, bool HQ>
 __device__ __forceinline__ int x_collect(const XArgs& a, int r, int b, int j, const RowParams& p, const XUni& u,
                          const XLevel& lv, int dg, uint32_t* s_cnt, uint64_t* s_col,
-                         XState& s_x) {
+                         lds_t<XState>& s_x) {
   const int lane = threadIdx.x & (WAVE - 1);
   if (threadIdx.x == 0) s_x.ncol = 0u;
   __syncthreads();
-  x_pass<NT>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT], const float (&)[EPT]) {
+  x_pass<NT, HQ>(a, r, b, j, p, s_cnt, [&](int i0, const float (&l)[EPT], const float (&)[EPT]) {
     uint32_t sel = 0u;
     int c = 0;
 #pragma unroll
@@ -325,7 +378,7 @@ __device__ __forceinline__ int x_collect(const XArgs& a, int r, int b, int j, co
     const int ex = wave_excl_count(c, &tot);
     if (tot > 0) {
       uint32_t base = 0u;
-      if (lane == 0) base = atomicAdd(&s_x.ncol, (uint32_t)tot);
+      if (lane == 0) base = atomicAdd((uint32_t*)&s_x.ncol, (uint32_t)tot);
       base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
       uint32_t pos = base + (uint32_t)ex;
 #pragma unroll
@@ -348,41 +401,66 @@ __device__ __forceinline__ void x_sort(uint64_t* s_col, int n) {
   else bitonic_sort_lds<NT>(s_col, n);
 }
 
+// The LDS arrays of the exact resolution (address-space-typed: see lds_t).
 struct XScratch {
-  uint64_t* key;    // XB u64 histogram masses, then the gathered bucket
-  uint32_t* hc;     // XB u32 histogram counts
-  uint32_t* cnt;    // NT * EPT u32 history counts of a window
-  uint64_t* u2;     // 2 * NT / WAVE
-  double* dred;
-  uint64_t* ured;
-  int* ired;
+  lds_t<uint64_t>* key_;  // XB u64 histogram masses, then the gathered bucket
+  lds_t<uint32_t>* hc_;   // XB u32 histogram counts
+  lds_t<uint32_t>* cnt_;  // NT * EPT u32 history counts of a window
+  lds_t<uint64_t>* u2_;   // 2 * NT / WAVE
+  lds_t<double>* dred_;
+  lds_t<uint64_t>* ured_;
+  lds_t<int>* ired_;
+  __device__ __forceinline__ uint64_t* key() const { return (uint64_t*)key_; }
+  __device__ __forceinline__ uint32_t* hc() const { return (uint32_t*)hc_; }
+  __device__ __forceinline__ uint32_t* cnt() const { return (uint32_t*)cnt_; }
+  __device__ __forceinline__ uint64_t* u2() const { return (uint64_t*)u2_; }
+  __device__ __forceinline__ double* dred() const { return (double*)dred_; }
+  __device__ __forceinline__ uint64_t* ured() const { return (uint64_t*)ured_; }
+  __device__ __forceinline__ int* ired() const { return (int*)ired_; }
 };
+// An XScratch over a caller's LDS arrays.
+__device__ __forceinline__ XScratch xscratch(uint64_t* key, uint32_t* hc, uint32_t* cnt,
+                                             uint64_t* u2, double* dred, uint64_t* ured,
+                                             int* ired) {
+  return XScratch{(lds_t<uint64_t>*)key, (lds_t<uint32_t>*)hc, (lds_t<uint32_t>*)cnt,
+                  (lds_t<uint64_t>*)u2, (lds_t<double>*)dred, (lds_t<uint64_t>*)ured,
+                  (lds_t<int>*)ired};
+}
 
 // Weighted select: the last universe token x in the order whose universe mass before it
 // (by_mass) or count before it is <= T, where T = floor(coef * total mass) of the
 // universe, or T = cst when coef < 0. Result in s_x (found = 0 for an empty universe).
-template <int NT>
-__device__ __noinline__ void x_select(const XArgs& a, int r, int b, int j, const RowParams p,
-                                      const XUni u, bool by_mass, double coef, uint64_t cst,
-                                      const XScratch xs, XState& s_x) {
+template <int NT, bool HQ>
+__device__ __noinline__ void x_select(const XArgs& a_in, int r, int b, int j,
+                                      const RowParams p_in, const XUni u_in, bool by_mass,
+                                      double coef, uint64_t cst, const XScratch xs_in,
+                                      lds_t<XState>& s_x) {
+  // the uniform arguments in scalar registers (see uniform_copy)
+  const XArgs a = uniform_copy(a_in);
+  const RowParams p = uniform_copy(p_in);
+  const XUni u = uniform_copy(u_in);
+  const XScratch xs = uniform_copy(xs_in);
+  r = __builtin_amdgcn_readfirstlane(r);
+  b = __builtin_amdgcn_readfirstlane(b);
+  j = __builtin_amdgcn_readfirstlane(j);
   constexpr int XQ = XB / NT;  // bins (and bucket positions) per thread
   const int t = threadIdx.x;
   XLevel lv{0, 0, 0ull, 0ull};
   uint64_t below_m = 0ull, below_c = 0ull, T = 0ull;
   int dsel = -1;
   for (;;) {
-    x_hist<NT>(a, r, b, j, p, u, lv, xs.cnt, xs.hc, xs.key);
+    x_hist<NT, HQ>(a, r, b, j, p, u, lv, xs.cnt(), xs.hc(), xs.key());
     uint32_t c4[XQ];
     uint64_t m4[XQ], lc = 0ull, lm = 0ull;
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {
-      c4[q] = xs.hc[XQ * t + q];
-      m4[q] = xs.key[XQ * t + q];
+      c4[q] = xs.hc()[XQ * t + q];
+      m4[q] = xs.key()[XQ * t + q];
       lc += c4[q];
       lm += m4[q];
     }
     uint64_t exc, exm, totc, totm;
-    block_excl_scan2_u64<NT>(lc, lm, xs.u2, exc, exm, totc, totm);
+    block_excl_scan2_u64<NT>(lc, lm, xs.u2(), exc, exm, totc, totm);
     if (lv.mode == 0) {
       T = coef < 0.0 ? cst : (uint64_t)floor(coef * (double)totm);
       if (t == 0) {
@@ -405,7 +483,7 @@ __device__ __noinline__ void x_select(const XArgs& a, int r, int b, int j, const
       fc += c4[q];
       fm += m4[q];
     }
-    dsel = -block_min<NT>(-best, xs.ired);
+    dsel = -block_min<NT>(-best, xs.ired());
     if (dsel < 0) {
       if (t == 0) s_x.found = 0;
       __syncthreads();
@@ -444,21 +522,23 @@ __device__ __noinline__ void x_select(const XArgs& a, int r, int b, int j, const
     lv = nx;
   }
   // resolve the bucket exactly
-  const int n = x_collect<NT>(a, r, b, j, p, u, lv, dsel, xs.cnt, xs.key, s_x);
-  x_sort<NT>(xs.key, n);
+  const int n = x_collect<NT, HQ>(a, r, b, j, p, u, lv, dsel, xs.cnt(), xs.key(), s_x);
+  x_sort<NT>(xs.key(), n);
   uint64_t w4[XQ], lm = 0ull;
 #pragma unroll
   for (int q = 0; q < XQ; ++q) {
     const int pos = XQ * t + q;
     w4[q] = 0ull;
     if (pos < n) {
-      const uint64_t key = xs.key[pos];
-      w4[q] = x_wt(a, u, fkey_desc_inv((uint32_t)(key >> 32)), (int)(uint32_t)key);
+      const uint64_t key = xs.key()[pos];
+      const int id = (int)(uint32_t)key;
+      w4[q] = x_wt_q(u, fkey_desc_inv((uint32_t)(key >> 32)),
+                     (HQ && u.rS != 0ull) ? xq_prob(a.q, id) : 0.0);
       lm += w4[q];
     }
   }
   uint64_t ex0, exm, tot0, totm;
-  block_excl_scan2_u64<NT>(0ull, lm, xs.u2, ex0, exm, tot0, totm);
+  block_excl_scan2_u64<NT>(0ull, lm, xs.u2(), ex0, exm, tot0, totm);
   int best = -1;
   uint64_t bm = 0ull, bw = 0ull;
   uint64_t fm = below_m + exm;
@@ -474,10 +554,10 @@ __device__ __noinline__ void x_select(const XArgs& a, int r, int b, int j, const
       fm += w4[q];
     }
   }
-  const int psel = -block_min<NT>(-best, xs.ired);
+  const int psel = -block_min<NT>(-best, xs.ired());
   if (t == 0) s_x.found = psel >= 0 ? 1 : 0;
   if (psel >= 0 && best == psel) {
-    s_x.key = xs.key[psel];
+    s_x.key = xs.key()[psel];
     s_x.key_w = bw;
     s_x.below_m = bm;
     s_x.below_c = (uint32_t)(below_c + (uint64_t)psel);
@@ -492,9 +572,9 @@ struct XOut {
 };
 
 // The whole decision chain of one row from streaming passes (see above).
-template <int NT>
+template <int NT, bool HQ>
 __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const RowParams p, float m, int arg,
-                          int draft, bool vdr, float l_draft, const XScratch xs, XState& s_x) {
+                          int draft, bool vdr, float l_draft, const XScratch xs, lds_t<XState>& s_x) {
   const int V = a.V;
   const bool topk = p.top_k > 0 && p.top_k < V;
   const bool topp = p.top_p < 1.0f;
@@ -504,13 +584,13 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
   const bool cand_sorted = no_lse ? topp : (topk || topp);
   XUni u{m, p.min_p > 0.0f ? p.lmp : -INFINITY, 0ull, ~0ull, -1, 0ull};
   // general-q verify rows draw from the residual (p - q)^+ over the whole kept set
-  const bool resid = vdr && a.has_q;
+  const bool resid = HQ && vdr && a.has_q;
   uint64_t S = 0ull;
   bool haveS = false;
   uint32_t nkeep = 0u;
   if (topk) {
     const uint64_t K1 = (uint64_t)(p.top_k - 1);
-    x_select<NT>(a, r, b, j, p, u, false, -1.0, K1, xs, s_x);
+    x_select<NT, HQ>(a, r, b, j, p, u, false, -1.0, K1, xs, s_x);
     if (!s_x.found) return XOut{STRIM_EEMPTY, -1, 0, 0.0, 0ull};
     if (keep_ties) {
       u.bound = (s_x.key & 0xFFFFFFFF00000000ull) | 0xFFFFFFFFull;
@@ -523,7 +603,7 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
   }
   if (topp) {
     const double P = (double)p.top_p;
-    x_select<NT>(a, r, b, j, p, u, true, P, 0ull, xs, s_x);
+    x_select<NT, HQ>(a, r, b, j, p, u, true, P, 0ull, xs, s_x);
     if (!s_x.found) return XOut{STRIM_EEMPTY, -1, 0, 0.0, 0ull};
     u.bound = s_x.key;
     S = s_x.below_m + s_x.key_w;
@@ -540,8 +620,8 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
   ud.excl = vdr && !resid ? draft : -1;
   if (resid && !haveS) {
     const XLevel all{2, 0, 0ull, 0ull};
-    x_hist<NT>(a, r, b, j, p, u, all, xs.cnt, xs.hc, xs.key);
-    S = xs.key[0];
+    x_hist<NT, HQ>(a, r, b, j, p, u, all, xs.cnt(), xs.hc(), xs.key());
+    S = xs.key()[0];
     haveS = true;
     __syncthreads();
   }
@@ -550,11 +630,11 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
     const double uu = (double)row_uniform(a, r, p, 0);
     if (resid) {
       ud.rS = S;
-      x_select<NT>(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
+      x_select<NT, HQ>(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
       // an all-zero residual draws the first kept token
       token = (s_x.found && s_x.tot_m > 0ull) ? (int)(uint32_t)s_x.key : arg;
     } else {
-      x_select<NT>(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
+      x_select<NT, HQ>(a, r, b, j, p, ud, true, uu, 0ull, xs, s_x);
       S = s_x.tot_m + W_d;
       // an empty residual (only the draft kept) draws the first kept token
       token = s_x.found ? (int)(uint32_t)s_x.key : arg;
@@ -562,8 +642,8 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
   } else {
     if (!haveS) {
       const XLevel all{2, 0, 0ull, 0ull};
-      x_hist<NT>(a, r, b, j, p, u, all, xs.cnt, xs.hc, xs.key);
-      S = xs.key[0];
+      x_hist<NT, HQ>(a, r, b, j, p, u, all, xs.cnt(), xs.hc(), xs.key());
+      S = xs.key()[0];
       __syncthreads();
     }
     const double lse = log((double)S / XFIX);
@@ -598,14 +678,14 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
       XUni ub = ud;
       uint32_t below = 0u;
       while (below < nkeep) {
-        x_select<NT>(a, r, b, j, p, ub, false, -1.0, (uint64_t)(XCOL - 1), xs, s_x);
+        x_select<NT, HQ>(a, r, b, j, p, ub, false, -1.0, (uint64_t)(XCOL - 1), xs, s_x);
         if (!s_x.found) break;
         XUni uc = ub;
         uc.bound = s_x.key;
-        const int n = x_collect<NT>(a, r, b, j, p, uc, all, 0, xs.cnt, xs.key, s_x);
-        x_sort<NT>(xs.key, n);
+        const int n = x_collect<NT, HQ>(a, r, b, j, p, uc, all, 0, xs.cnt(), xs.key(), s_x);
+        x_sort<NT>(xs.key(), n);
         for (int pos = threadIdx.x; pos < n; pos += NT) {
-          const uint64_t key = xs.key[pos];
+          const uint64_t key = xs.key()[pos];
           take(fkey_desc_inv((uint32_t)(key >> 32)), (int)(uint32_t)key,
                (int64_t)below + pos, key, resid ? xq_prob(a.q, (int)(uint32_t)key) : 0.0);
         }
@@ -615,7 +695,7 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
         ub.lo = uc.bound + 1ull;
       }
     } else {
-      x_pass<NT>(a, r, b, j, p, xs.cnt, [&](int i0, const float (&l)[EPT], const float (&qv)[EPT]) {
+      x_pass<NT, HQ>(a, r, b, j, p, xs.cnt(), [&](int i0, const float (&l)[EPT], const float (&qv)[EPT]) {
 #pragma unroll
         for (int e = 0; e < EPT; ++e)
           if (x_in(ud, l[e], i0 + e))
@@ -623,7 +703,7 @@ __device__ __noinline__ XOut exact_row(const XArgs a, int r, int b, int j, const
                  resid ? xq_of(a.q, qv[e]) : 0.0);
       });
     }
-    block_argmax_score<NT>(bsc, btk, bid, xs.dred, xs.ured, xs.ired, &s_x.token);
+    block_argmax_score<NT>(bsc, btk, bid, xs.dred(), xs.ured(), xs.ired(), (int*)&s_x.token);
     token = s_x.token >= 0 ? s_x.token : arg;
   }
   int acc = 0;

@@ -73,14 +73,7 @@ __device__ __forceinline__ int dbin(float m, float l, float scale) {
 __device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int j,
                                             const RowParams& p, float m, int arg, int draft,
                                             bool vdr, float l_draft, FinalShared& S) {
-  XScratch xs;
-  xs.key = S.key;
-  xs.hc = S.xhc;
-  xs.cnt = S.xcnt;
-  xs.u2 = S.xu2;
-  xs.dred = S.d;
-  xs.ured = S.u;
-  xs.ired = S.i;
+  const XScratch xs = xscratch(S.key, S.xhc, S.xcnt, S.xu2, S.d, S.u, S.i);
   XArgs xa;
   xa.logits = a.logits;
   xa.row_stride = a.row_stride;
@@ -100,7 +93,8 @@ __device__ __forceinline__ void finalize_exact(const Args& a, int r, int b, int 
   xa.noise_stride = a.noise_stride;
   xa.has_q = 0;  // general-q rows are decided by k_final
   __syncthreads();
-  const XOut xo = exact_row<FTPB>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
+  const XOut xo = exact_row<FTPB, false>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs,
+                                  *(lds_t<XState>*)&S.x);
   finish_row(a, r, xo.status, xo.token, xo.accept, xo.sig, m, xo.last_key, PH_DONE);
 }
 

@@ -39,6 +39,7 @@ namespace strim {
 constexpr int GT = 1024;            // threads of a k_gfinal workgroup
 constexpr int GW = GT / WAVE;       // its waves; wave w owns the histogram bins of group w
 constexpr int GNE = 8;              // candidate slots per thread: W * GCAP <= GT * GNE
+constexpr int GNE2 = 3;             // second-tier slots per thread: W * GCAP2 <= GT * GNE2
 constexpr int GCAND = GT * GNE;     // candidates of a row held in bin order
 constexpr int GNB = GW * WAVE;      // histogram bins of d = m - l (64 per group)
 constexpr int GZCAP = GT;           // keys of one bin a decision resolves (one per thread)
@@ -69,7 +70,8 @@ struct GFinalShared {
                               // inclusive prefix
   uint64_t gt[GW];            // per group: its total
   uint32_t rcnt[GT];          // per chunk: its candidates
-  float v[GW], g[GW];
+  uint32_t rcnt2[GT];         // per chunk: its second-tier candidates
+  float v[GW], g[GW], g2[GW];
   int i[GW], f[GW];
   double sw[GW];              // per wave: its chunks' mass, relative to the row maximum
   double d[GW];
@@ -185,6 +187,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   // slot of the row (no branch between the loads: a missing optional input reads the
   // row's own state and is ignored; slots past a region's count are dropped later)
   const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (t < W ? t : 0)];
+  static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
   RowState* rsp = &a.s.rs[r];
   const bool gum = a.noise && a.noise_mode != STRIM_NOISE_ICDF;
   const float* nz = a.noise ? a.noise + (int64_t)r * a.noise_stride : (const float*)rsp;
@@ -195,6 +198,10 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const float ld_raw = rsp->l_draft;
   const int ne = W * GCAP;  // candidate slots of the row
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
+  // slots 0 .. GNE - 1: the first tier (entry e = q GT + t is region e / GCAP, offset
+  // e % GCAP); slots GNE .. GNE + GNE2 - 1: the second tier, loaded only when a decision
+  // falls at or below the first tier's bound (entry e is region e / GCAP2, offset GCAP +
+  // e % GCAP2)
   Cand cd[GNE];
 #pragma unroll
   for (int q = 0; q < GNE; ++q) {
@@ -210,26 +217,32 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const bool own = t < W;
   int ff = own ? (cs.flags | (cs.n > 0 ? 4 : 0)) : 0;
   float mv = own ? cs.m : -INFINITY, gv = own ? cs.g : -INFINITY;
+  float gv2 = own ? cs.g2 : -INFINITY;
   int mi = own ? cs.arg : -1;
   S.rcnt[t] = own ? cs.ncand : 0u;
+  S.rcnt2[t] = own ? cs.ncand2 : 0u;
   wave_argmax(mv, mi);
   ff = wave_or_i(ff);
   gv = wave_max_f(gv);
+  gv2 = wave_max_f(gv2);
   if (lane == 0) {
     S.v[w] = mv;
     S.i[w] = mi;
     S.f[w] = ff;
     S.g[w] = gv;
+    S.g2[w] = gv2;
   }
   S.hist[t] = 0ull;
   if (t < 2) S.tag[t] = -1;
   __syncthreads();
   // lane q holds wave q's results
   float m = lane < GW ? S.v[lane] : -INFINITY, G = lane < GW ? S.g[lane] : -INFINITY;
+  float G2 = lane < GW ? S.g2[lane] : -INFINITY;
   int arg = lane < GW ? S.i[lane] : -1, flags = lane < GW ? S.f[lane] : 0;
   wave_argmax(m, arg);
   flags = wave_or_i(flags);
   G = wave_max_f(G);
+  G2 = wave_max_f(G2);
   auto finish = [&](int status, int token, int accept, double sig, uint64_t last_key) {
     if (t != 0) return;
     rsp->status = status;
@@ -263,42 +276,61 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   }
 
   // ---- steps 2 and 3: the decision from the candidates ---------------------------
-  // (a lambda so that every "not above G" exit leads to the one exact-resolution call;
-  // its conditions are uniform over the workgroup)
-  auto decide = [&]() -> bool {
+  // Round 0 uses the first tier and the bound G, round 1 (when a decision of round 0
+  // fell at or below G) both tiers and the bound G2. The verdict: 0 decided, 1 a
+  // decision lies at or below the round's bound, 2 the candidates cannot decide the row
+  // (both lead to the exact resolution when no round is left). Every condition is uniform
+  // over the workgroup.
+  // (one instantiation per round: the first round's code and registers carry nothing
+  // of the second tier)
+  enum { DECIDED = 0, BELOW = 1, OTHER = 2 };
+  const int ne2 = W * GCAP2;  // second-tier slots of the row
+  auto decide = [&](auto round_c, const Cand (&cd2)[GNE2]) -> int {
+    constexpr int round = decltype(round_c)::value;
+    constexpr int NS = round == 0 ? GNE : GNE + GNE2;  // slots of this round
+    auto cand = [&](int q) -> const Cand& { return q < GNE ? cd[q] : cd2[q - GNE]; };
     const bool topk = p.top_k > 0 && p.top_k < V;
     const bool topp = p.top_p < 1.0f;
     const bool minp = p.min_p > 0.0f;
     const bool icdf = a.noise_mode == STRIM_NOISE_ICDF;
     // rank-indexed noise needs every kept token's rank
-    if ((p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp && !icdf) return false;
-    if (ne > GCAND) return false;
-    const bool all_in = !(G > -INFINITY);  // every allowed token is a candidate
-    // min-p keeps a set that lies above G only if G itself fails it
-    if (minp && !all_in && ((double)G - (double)m) >= p.lmp) return false;
-    const float span = all_in ? 64.0f : fminf(fmaxf(m - G, 1.0f / 64.0f), 64.0f);
+    if ((p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp && !icdf) return OTHER;
+    if (ne > GCAND) return OTHER;
+    const float Gr = round == 0 ? G : G2;
+    const bool all_in = !(Gr > -INFINITY);  // every allowed token is a candidate
+    // min-p keeps a set that lies above the bound only if the bound itself fails it
+    if (minp && !all_in && ((double)Gr - (double)m) >= p.lmp) return BELOW;
+    const float span = all_in ? 64.0f : fminf(fmaxf(m - Gr, 1.0f / 64.0f), 64.0f);
     const float hscale = (float)GNB / span;
-    // which of this thread's slots hold a candidate: entry e = q GT + t lies in region
-    // q (GT / GCAP) + (t >> 7), at offset t & 127
+    // which of this thread's slots hold a candidate: first-tier entry e = q GT + t lies
+    // in region q (GT / GCAP) + (t >> 7) at offset t & 127, second-tier entry e = q GT + t
+    // in region q (GT / GCAP2) + (t >> 6) at offset t & 63
     uint32_t vmask = 0u;
     {
-      uint32_t rc[GNE];
+      uint32_t rc[NS];
 #pragma unroll
       for (int q = 0; q < GNE; ++q) rc[q] = S.rcnt[min(q * (GT / GCAP) + (t >> 7), GT - 1)];
 #pragma unroll
+      for (int q = GNE; q < NS; ++q)
+        rc[q] = S.rcnt2[min((q - GNE) * (GT / GCAP2) + (t >> 6), GT - 1)];
+#pragma unroll
       for (int q = 0; q < GNE; ++q)
         vmask |= (((q * GT + t < ne) & ((uint32_t)(t & (GCAP - 1)) < rc[q])) ? 1u : 0u) << q;
+#pragma unroll
+      for (int q = GNE; q < NS; ++q)
+        vmask |= ((((q - GNE) * GT + t < ne2) & ((uint32_t)(t & (GCAP2 - 1)) < rc[q])) ? 1u : 0u)
+                 << q;
     }
-    // bin every candidate above G (passing min-p); the atomic's old count is its place in
+    // bin every candidate above the bound (passing min-p); the atomic's old count is its place in
     // the bin. A lane without a candidate leaves old[q] unset and never reads it; the
     // empty asm statements after the loop keep the compiler from reading any result
     // before every atomic is issued (it would otherwise wait for each in turn).
-    uint64_t old[GNE], cm[GNE];
-    int bn[GNE];
+    uint64_t old[NS], cm[NS];
+    int bn[NS];
 #pragma unroll
-    for (int q = 0; q < GNE; ++q) {
-      const float l = cd[q].l;
-      const bool k = ((vmask >> q) & 1u) && l > G && l > -INFINITY &&
+    for (int q = 0; q < NS; ++q) {
+      const float l = cand(q).l;
+      const bool k = ((vmask >> q) & 1u) && l > Gr && l > -INFINITY &&
                      (!minp || ((double)l - (double)m) >= p.lmp);
       bn[q] = k ? gbin(m, l, hscale) : -1;
       if (k) {
@@ -307,9 +339,9 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       }
     }
 #pragma unroll
-    for (int q = 0; q < GNE; ++q) asm volatile("" : "+v"(old[q]));
+    for (int q = 0; q < NS; ++q) asm volatile("" : "+v"(old[q]));
     // the whole row's mass relative to m, from the chunk sums (used while the kept set
-    // reaches below G), while the atomics complete
+    // reaches below the bound), while the atomics complete
     {
       const double sw = wave_sum((own && cs.n > 0) ? cs.S * exp((double)cs.m - (double)m) : 0.0);
       if (lane == 0) S.sw[w] = sw;
@@ -331,7 +363,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     const uint64_t ginc = wave_incl_scan_u64(gl);
     const uint64_t tot = rl_u64(ginc, GW - 1);
     const uint64_t n_all = wcount(tot), m_all = wmass(tot);
-    if (n_all == 0ull) return false;
+    if (n_all == 0ull) return BELOW;
     // every candidate with its mass into bin order: bin b starts at the cumulative count
     // of the bins before it (the group's exclusive prefix from lane g, plus the bins
     // before b in the group); a slot without a candidate writes past the row's entries
@@ -339,25 +371,25 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       const int gce = (int)wcount(ginc - gl);
       // every read first (the empty asm statements keep them ahead of their uses), then
       // every write
-      int at[GNE];
-      uint32_t hb[GNE];
-      int gb[GNE];
+      int at[NS];
+      uint32_t hb[NS];
+      int gb[NS];
 #pragma unroll
-      for (int q = 0; q < GNE; ++q) {
+      for (int q = 0; q < NS; ++q) {
         const int bq = bn[q] < 0 ? 0 : bn[q];
         hb[q] = (uint32_t)(S.hist[bq > 0 ? bq - 1 : 0] >> 32);
         gb[q] = __shfl(gce, bq / WAVE);
       }
 #pragma unroll
-      for (int q = 0; q < GNE; ++q) asm volatile("" : "+v"(hb[q]), "+v"(gb[q]));
+      for (int q = 0; q < NS; ++q) asm volatile("" : "+v"(hb[q]), "+v"(gb[q]));
 #pragma unroll
-      for (int q = 0; q < GNE; ++q) {
+      for (int q = 0; q < NS; ++q) {
         const int before = gb[q] + ((bn[q] & (WAVE - 1)) ? (int)(hb[q] >> (GCSH - 32)) : 0);
         at[q] = bn[q] >= 0 ? before + (int)wcount(old[q]) : GCAND + lane;
       }
 #pragma unroll
-      for (int q = 0; q < GNE; ++q) {
-        S.bkey[at[q]] = ckey(cd[q].l, cd[q].id);
+      for (int q = 0; q < NS; ++q) {
+        S.bkey[at[q]] = ckey(cand(q).l, cand(q).id);
         S.bmass[at[q]] = cm[q];
       }
     }
@@ -379,7 +411,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       if (step == 0) {
         if (!topk) continue;
         if (n_all < (uint64_t)p.top_k) {
-          if (!all_in) return false;  // the k-th token lies at or below G
+          if (!all_in) return BELOW;  // the k-th token lies at or below the bound
           continue;                   // every allowed token is kept
         }
         mass = false;
@@ -395,11 +427,11 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         thr = (double)p.top_p * (double)S0;
         bound = bound0;
       } else {
-        if (!icdf && !known1) return false;
+        if (!icdf && !known1) return BELOW;
         // the draft of a verify row: kept? its mass, and its bin when a candidate
         if (vdr && l_draft > -INFINITY && ckey(l_draft, draft) <= bound1) {
           wd = gmass(l_draft, m);
-          if (l_draft > G && (!minp || ((double)l_draft - (double)m) >= p.lmp)) {
+          if (l_draft > Gr && (!minp || ((double)l_draft - (double)m) >= p.lmp)) {
             xb = gbin(m, l_draft, hscale);
             xw = wd;
           }
@@ -414,11 +446,11 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       const uint64_t w0 = gcum(S, ginc, bz - 1);
       const uint64_t c0 = wcount(w0);
       const int nzc = (int)(wcount(gcum(S, ginc, bz)) - c0);
-      if (nzc > GZCAP) return false;
+      if (nzc > GZCAP) return OTHER;
       const uint64_t m0 = wmass(w0) - (bz - 1 >= xb ? xw : 0ull);
       const GHit h = gresolve(S, nres++, (int)c0, nzc, mass, thr, bound, excl, c0, m0);
       if (step == 0) {
-        if (h.key == ~0ull) return false;
+        if (h.key == ~0ull) return OTHER;
         known0 = true;
         if (!(p.flags & STRIM_FLAG_TOPK_KEEP_TIES)) {
           bound0 = h.key;
@@ -441,11 +473,11 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
           S1 = h.mass_before + h.mass;
           known1 = true;
         } else if (!known0) {
-          return false;  // the cut lies at or below G
+          return BELOW;  // the cut lies at or below the bound
         }
       } else {
         if (h.key != ~0ull) token = (int)(uint32_t)h.key;
-        else if (!known1) return false;  // the draw lies at or below G
+        else if (!known1) return BELOW;  // the draw lies at or below the bound
         else token = arg;                // only the draft kept: the first kept
       }
     }
@@ -475,19 +507,33 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     }
     const int acc = vdr && ((double)u_acc < (double)wd / (double)S1) ? 1 : 0;
     finish(STRIM_OK, token, acc, (double)S1 / GFIX, bound1);
-    return true;
+    return DECIDED;
   };
-  if (decide()) return;
+  // the second round needs room for both tiers and a lower bound than the first
+  const bool deepen_ok = W * (GCAP + GCAP2) <= GCAND && ne2 <= GT * GNE2 && G2 < G;
+  {
+    const Cand none[GNE2] = {};
+    const int verdict = decide(std::integral_constant<int, 0>{}, none);
+    if (verdict == DECIDED) return;
+    if (verdict == BELOW && deepen_ok) {
+      // the second tier (its loads are the only wait of this step), and the histogram
+      // and result slots cleared for the second round
+      Cand cd2[GNE2];
+#pragma unroll
+      for (int q = 0; q < GNE2; ++q) {
+        const int e = q * GT + t;
+        cd2[q] = slots[e < ne2 ? (int64_t)(e >> 6) * SLOT + GCAP + (e & (GCAP2 - 1)) : 0];
+      }
+      __syncthreads();  // every read of the first round's histogram is done
+      S.hist[t] = 0ull;
+      if (t < 2) S.tag[t] = -1;
+      __syncthreads();
+      if (decide(std::integral_constant<int, 1>{}, cd2) == DECIDED) return;
+    }
+  }
 
   // ---- a decision at or below G: the exact streaming resolution --------------------
-  XScratch xs;
-  xs.key = S.xkey;
-  xs.hc = S.xhc;
-  xs.cnt = S.xcnt;
-  xs.u2 = S.xu2;
-  xs.dred = S.d;
-  xs.ured = S.u;
-  xs.ired = S.i;
+  const XScratch xs = xscratch(S.xkey, S.xhc, S.xcnt, S.xu2, S.d, S.u, S.i);
   XArgs xa;
   xa.logits = a.logits;
   xa.row_stride = a.row_stride;
@@ -507,7 +553,8 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   xa.noise_stride = a.noise_stride;
   xa.has_q = 0;
   __syncthreads();
-  const XOut xo = exact_row<GT>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, S.x);
+  const XOut xo =
+      exact_row<GT, false>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, *(lds_t<XState>*)&S.x);
   finish(xo.status, xo.token, xo.accept, xo.sig, xo.last_key);
 }
 

@@ -32,6 +32,7 @@ constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
 constexpr int FCAP = 8192;       // candidate keys k_finalize holds in LDS
 constexpr int FCAP_FAST = 4096;  // of which fast rows use at most this many
 constexpr int GCAP = 128;        // candidates a general row's chunk collects (at most)
+constexpr int GCAP2 = 64;        // and its second tier, after them in the slot region
 constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
 constexpr float CB_SCALE = 2.0f;
 constexpr int KLOC = 256;        // largest top-k served by local candidates
@@ -59,7 +60,10 @@ struct ChunkStat {
   double S;        // sum exp(l - m) over the chunk (general rows)
   int32_t arg;     // first id reaching m
   uint32_t ncand;  // candidates in the chunk's slot region (> SLOT: overflow)
-  uint32_t pad_[3];
+  float g2;        // general rows: the largest l left out of both candidate tiers (-inf
+                   // when every allowed token is in one)
+  uint32_t ncand2; // general rows: second-tier candidates (at GCAP .. GCAP + GCAP2 - 1)
+  uint32_t pad_;
 };
 static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
 

@@ -32,14 +32,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   const int arg = rsp->token;
   const int draft = a.drafts[(int64_t)b * a.k + j];
   // ---- exact streaming resolution ---------------------------------------------------
-  XScratch xs;
-  xs.key = s_key;
-  xs.hc = (uint32_t*)(s_key + XB);
-  xs.cnt = s_cnt;
-  xs.u2 = s_u2;
-  xs.dred = s_dred;
-  xs.ured = s_ured;
-  xs.ired = s_ired;
+  const XScratch xs = xscratch(s_key, (uint32_t*)(s_key + XB), s_cnt, s_u2, s_dred, s_ured, s_ired);
   XArgs xa;
   xa.logits = a.logits;
   xa.row_stride = a.row_stride;
@@ -65,7 +58,8 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   xa.q.vq = a.s.vq + (size_t)qr * (size_t)a.s.wmax * CHUNK;
   xa.q.mq = qs.mq;
   xa.q.Z = qs.Z;
-  const XOut xo = exact_row<FIN_T>(xa, r, b, j, p, m, arg, draft, true, rsp->l_draft, xs, s_x);
+  const XOut xo = exact_row<FIN_T, true>(xa, r, b, j, p, m, arg, draft, true, rsp->l_draft, xs,
+                                   *(lds_t<XState>*)&s_x);
   if (threadIdx.x == 0) {
     rsp->status = xo.status;
     rsp->token = xo.token;

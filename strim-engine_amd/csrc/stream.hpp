@@ -33,7 +33,7 @@ struct StreamShared {
   uint32_t lad[2 * WAVE];
   float v[SMAXW];
   int i[SMAXW], n[SMAXW], f[SMAXW];
-  uint32_t off[SMAXW];
+  uint32_t off[SMAXW], off2[SMAXW];
   double d[SMAXW];
   float tf[4 * SMAXW];
   int ti[2 * SMAXW];
@@ -304,8 +304,8 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   const float m_w = (p.greedy || !(vm > -INFINITY)) ? vm : vm / p.T;
   if (m_w == INFINITY) f_w = 1;
   if (!(m_w > -INFINITY)) n_w = 0;
-  ChunkStat cs{m_w, n_w, f_w, -INFINITY, 0.0, -1, 0u, {}};
-  uint32_t cs_ncand = 0u;
+  ChunkStat cs{m_w, n_w, f_w, -INFINITY, 0.0, -1, 0u, -INFINITY, 0u, 0u};
+  uint32_t cs_ncand = 0u, cs_ncand2 = 0u;
   const bool live = n_w > 0 && !f_w;
 
   if (fast && live) {
@@ -432,19 +432,26 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       // chunk's slot region in wave order. cs.g is the largest l left out (-inf when every
       // allowed token is a candidate): every token of the chunk with l > cs.g is a
       // candidate, so k_gfinal can decide the row from the candidates alone when its
-      // decisions fall above the largest cs.g of the row. (The coarse histogram is
+      // decisions fall above the largest cs.g of the row. A second tier, the tokens of the
+      // following bins while they number at most GCAP2, goes to the region's entries from
+      // GCAP on, with cs.g2 the largest l left out of both tiers: k_gfinal reads it only
+      // when a decision falls at or below the row's largest cs.g. (The coarse histogram is
       // complete: the barriers of the sums above follow its atomics.)
       uint32_t hsum = 0u;
 #pragma unroll
       for (int q = 0; q < NW; ++q) hsum += S.hc[q][lane];
       const uint32_t hcum = wave_incl_scan_u32(hsum);
       const int bstar = __popcll(__ballot(hcum <= (uint32_t)GCAP)) - 1;  // -1: no bin fits
-      uint32_t sel[SSEG];
-      float umax = -INFINITY;
-      int mycnt = 0;
+      const uint32_t cum1 =
+          bstar >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)hcum, bstar) : 0u;
+      const int bstar2 = __popcll(__ballot(hcum <= cum1 + (uint32_t)GCAP2)) - 1;
+      uint32_t sel[SSEG], sel2[SSEG];
+      float umax = -INFINITY, umax2 = -INFINITY;
+      int mycnt = 0, mycnt2 = 0;
 #pragma unroll
       for (int s = 0; s < SSEG; ++s) {
         sel[s] = 0u;
+        sel2[s] = 0u;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
           const float le = l[s][e];
@@ -452,41 +459,58 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
           const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
           const bool live_e = le > -INFINITY;
           const bool take = live_e && bb <= bstar;
+          const bool take2 = live_e && !take && bb <= bstar2;
           sel[s] |= (take ? 1u : 0u) << e;
+          sel2[s] |= (take2 ? 1u : 0u) << e;
           mycnt += take ? 1 : 0;
+          mycnt2 += take2 ? 1 : 0;
           if (live_e && !take) umax = fmaxf(umax, le);
+          if (live_e && !take && !take2) umax2 = fmaxf(umax2, le);
         }
       }
-      int wtot;
-      const int wex =
-          wave_excl_count_bits<(SSEG == 1 ? 4 : SSEG == 2 ? 5 : SSEG == 4 ? 6 : 7)>(mycnt, &wtot);
+      constexpr int CB = SSEG == 1 ? 4 : SSEG == 2 ? 5 : SSEG == 4 ? 6 : 7;
+      int wtot, wtot2;
+      const int wex = wave_excl_count_bits<CB>(mycnt, &wtot);
+      const int wex2 = wave_excl_count_bits<CB>(mycnt2, &wtot2);
       umax = wave_max_f(umax);
+      umax2 = wave_max_f(umax2);
       if (lane == 0) {
         S.off[w] = (uint32_t)wtot;
+        S.off2[w] = (uint32_t)wtot2;
         S.tf[w] = umax;
+        S.tf[SMAXW + w] = umax2;
       }
       __syncthreads();
-      uint32_t before = 0u, tot = 0u;
-      float um = -INFINITY;
+      uint32_t before = 0u, tot = 0u, before2 = 0u, tot2 = 0u;
+      float um = -INFINITY, um2 = -INFINITY;
 #pragma unroll
       for (int q = 0; q < NW; ++q) {
         before += q < w ? S.off[q] : 0u;
         tot += S.off[q];
+        before2 += q < w ? S.off2[q] : 0u;
+        tot2 += S.off2[q];
         um = fmaxf(um, S.tf[q]);
+        um2 = fmaxf(um2, S.tf[SMAXW + q]);
       }
-      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT + before;
-      int pos = wex;
+      Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
+      int pos = (int)before + wex, pos2 = GCAP + (int)before2 + wex2;
 #pragma unroll
       for (int s = 0; s < SSEG; ++s) {
-        uint32_t msk = sel[s];
+        // one loop over both tiers' tokens (a token is in at most one)
+        uint32_t msk = sel[s] | sel2[s];
         while (msk) {
           const int e = __builtin_ctz(msk);
           msk &= msk - 1u;
-          dst[pos++] = Cand{pick8(l[s], e), i0[s] + e};
+          const bool t1 = (sel[s] >> e) & 1u;
+          dst[t1 ? pos : pos2] = Cand{pick8(l[s], e), i0[s] + e};
+          pos += t1 ? 1 : 0;
+          pos2 += t1 ? 0 : 1;
         }
       }
       cs_ncand = tot;
       cs.g = um;
+      cs_ncand2 = tot2;
+      cs.g2 = um2;
     } else {
       const uint64_t key = mix64(p.seed, p.position);
       float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
@@ -533,6 +557,8 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     *(float4*)csp = make_float4(cs.m, __int_as_float(cs.n), __int_as_float(cs.flags), cs.g);
     csp->S = cs.S;
     csp->ncand = cs_ncand;
+    csp->g2 = cs.g2;
+    csp->ncand2 = cs_ncand2;
   }
 }
 

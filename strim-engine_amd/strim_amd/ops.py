@@ -206,6 +206,39 @@ class Context:
                 "row_accept": None if racc is None else racc[:, :k], "row_token": rtok}
 
 
+    def bind_verify(self, target_logits: torch.Tensor, draft_tokens: torch.Tensor, params,
+                    draft_logits: torch.Tensor | None = None,
+                    draft_to_full: torch.Tensor | None = None,
+                    noise_mode: int = N.NOISE_GUMBEL, noise: torch.Tensor | None = None,
+                    stream=None) -> "BoundCall":
+        """strim_verify with every argument converted and the outputs allocated once:
+        calling the result launches the verify again on the same buffers (for HIP-graph
+        capture). Its out_ids / out_status are the accepted counts and the tokens."""
+        B, k1, V = target_logits.shape
+        k = k1 - 1
+        dev = target_logits.device
+        p = host_params(params)
+        if p.size != B:
+            raise ValueError(f"need {B} param rows, got {p.size}")
+        _check_cuda(target_logits, draft_tokens, draft_logits, draft_to_full, noise)
+        Vd = 0 if draft_logits is None else draft_logits.shape[-1]
+        if draft_logits is not None and (tuple(draft_logits.shape) != (B, k, Vd)
+                                         or not draft_logits.is_contiguous()
+                                         or draft_logits.dtype != target_logits.dtype):
+            raise ValueError(f"draft_logits must be contiguous [{B}, {k}, Vd] of the target dtype")
+        acc = torch.empty(B, dtype=torch.int32, device=dev)
+        tok = torch.empty(B, dtype=torch.int32, device=dev)
+        st = torch.empty(B, dtype=torch.int32, device=dev)
+        args = [self._h, None, _ptr(target_logits), _dtype_code(target_logits), B, k, V,
+                _ptr(draft_logits), Vd, _ptr(draft_to_full), _ptr(draft_tokens), _pp(p), None, 0,
+                None, None, 0, noise_mode, _ptr(noise), _ptr(acc), _ptr(tok), None, None,
+                _ptr(st)]
+        keep = (target_logits, draft_tokens, p, draft_logits, draft_to_full, noise, acc, tok, st)
+        call = BoundCall(N.lib().strim_verify, args, keep, acc, tok, stream, "strim_verify")
+        call.status = st
+        return call
+
+
 def mask_logits(logits: torch.Tensor, mask_words: torch.Tensor | None, stream=None):
     """maskLogits (TokenMask.swift:15-17): float32 logits with disallowed tokens at -inf."""
     if logits.dim() == 1:
@@ -259,11 +292,12 @@ class BoundCall:
     It launches on the given stream, or on the current stream at call time (so a graph
     capture records it)."""
 
-    def __init__(self, fn, args, keep, out_ids, out_status, stream=None):
+    def __init__(self, fn, args, keep, out_ids, out_status, stream=None, name="strim_sample"):
         self._fn = fn
         self._args = args
         self._keep = keep
         self._stream = stream
+        self._name = name
         self.out_ids = out_ids
         self.out_status = out_status
 
@@ -271,4 +305,4 @@ class BoundCall:
         self._args[1] = _stream(self._stream)
         rc = self._fn(*self._args)
         if rc != N.OK:
-            raise N.StrimError(rc, "strim_sample")
+            raise N.StrimError(rc, self._name)

@@ -258,3 +258,39 @@ def json_string_dfa():
         nt[2, c] = 1
     flags = np.array([2, 2, 2, 1], dtype=np.uint8)
     return nt, flags
+
+
+def json_object_dfa():
+    """The object {"name":"<string>","age":<integer>} without whitespace: the literal
+    {"name":" (states 0..8), the string (9; 10 after a backslash), the literal ,"age":
+    after the string's closing quote (11..18), the first digit (18), more digits (19),
+    the closing brace after a lone 0 (21) and the end (20, accepting). 22 states, so a
+    mask walks from the caches rather than from an LDS copy of the table.
+    Returns (next_table, flags, in_string_state)."""
+    lit1, lit2 = b'{"name":"', b',"age":'
+    S = len(lit1)            # inside the string
+    E = S + 1                # after a backslash
+    L2 = E + 1               # after the closing quote: expects lit2
+    D0 = L2 + len(lit2)      # the first digit
+    D = D0 + 1               # more digits
+    F = D + 1                # done (accepting)
+    Z = F + 1                # after a lone 0: only the brace
+    nt = np.full((Z + 1, 256), -1, dtype=np.int32)
+    for i, c in enumerate(lit1):
+        nt[i, c] = i + 1 if i + 1 < len(lit1) else S
+    nt[S, 0x20:] = S
+    nt[S, ord('"')] = L2
+    nt[S, ord("\\")] = E
+    for c in b'"\\/bfnrtu':
+        nt[E, c] = S
+    for i, c in enumerate(lit2):
+        nt[L2 + i, c] = L2 + i + 1
+    for c in b"123456789":
+        nt[D0, c] = D
+    nt[D0, ord("0")] = Z
+    nt[D, ord("0"):ord("9") + 1] = D
+    nt[D, ord("}")] = F
+    nt[Z, ord("}")] = F
+    flags = np.full(Z + 1, 2, dtype=np.uint8)
+    flags[F] = 1
+    return nt, flags, S
