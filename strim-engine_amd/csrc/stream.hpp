@@ -25,11 +25,12 @@ constexpr int stpb() { return CHUNK / (EPT * SSEG); }
 
 // LDS of one k_stream workgroup (the history table only in the penalties variants, so
 // the narrow workgroups of large launches fit many to a CU).
+constexpr int HCQ = 4;  // copies of the coarse histogram per wave (one per 16 lanes)
 template <bool PEN>
 struct StreamShared {
   uint32_t cnt[PEN ? CHUNK : 4];  // history counts of the chunk's tokens (16 KB)
-  uint32_t hc[SMAXW][NCB];  // general rows: per-wave coarse counts (one copy per wave
-                            // spreads the atomics' contention)
+  uint32_t hc[SMAXW][NCB][HCQ];  // general rows: coarse counts, one copy per quarter
+                                 // wave (spreads the atomics' contention)
   uint32_t lad[2 * WAVE];
   float v[SMAXW];
   int i[SMAXW], n[SMAXW], f[SMAXW];
@@ -202,9 +203,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   if (fast && topk)
     for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
   if (p.cls == CLS_GENERAL)
-    for (int q = t; q < NW * NCB; q += STPB) {
-      S.hc[q / NCB][q % NCB] = 0u;
-    }
+    for (int q = t; q < NW * NCB; q += STPB) ((uint4*)&S.hc[0][0][0])[q] = make_uint4(0u, 0u, 0u, 0u);
   if (pen) hist_count<STPB, CHUNK>(a, b, j, c0, hid, hl, S.cnt);
 
   // ---- penalties and mask, before temperature ("v space") ------------------------
@@ -393,53 +392,89 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     }
     cs_ncand = tot <= SLOT ? (uint32_t)tot : 0xFFFFFFFFu;
   } else if (p.cls == CLS_GENERAL && live && !(a.dlog && a.verify && j < a.k)) {
-    // processed logits; chunk sum exp(l - m_w) and a coarse histogram of counts of
-    // m_w - l (which bins the chunk's candidates come from). General-q draft rows skip
-    // this: their draw makes its own passes (qres_kernels.hip, exact.hpp).
-    float (&l)[SSEG][EPT] = v;  // v is not needed after this
-#pragma unroll
-    for (int s = 0; s < SSEG; ++s)
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) l[s][e] = v[s][e] > -INFINITY ? v[s][e] / p.T : -INFINITY;
-    // unfiltered Gumbel rows are decided from the chunks' two best tokens and the sum;
-    // only the other general rows need the histogram
+    // Chunk mass sum exp(l - m_w) and a coarse histogram of counts of m_w - l (which bins
+    // the chunk's candidates come from). The bins are taken in v space, dv CB_SCALE / T
+    // with dv = vm - v: they only have to be one consistent assignment of the tokens, as
+    // the certificate below is taken over exact l. The mass needs l to its float rounding
+    // (a term's relative error is that of its exponent, which is |l| times the rounding),
+    // so l is formed as v / T by one FMA correction of v * RN(1/T), correctly rounded
+    // but for rare last-bit cases that move a term by an ulp of l; the exponential is
+    // 2^((l - m_w) log2(e)), a sum of positive terms good to a few 1e-7 relative. The
+    // exact quotient v / T is formed only for the candidates written and the largest
+    // left-out value. General-q draft rows skip this: their draw makes its own passes
+    // (qres_kernels.hip, exact.hpp). Unfiltered Gumbel rows are decided from the chunks'
+    // two best tokens and the sum; only the other general rows need the histogram.
     const bool gum_nf = a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V);
+    const float yT = 1.0f / p.T;
+    // the FMA quotient needs 1/T and its products far from the float range's ends
+    const bool fq = p.T > 0x1p-100f && p.T < 0x1p+100f;
+    const float kb = CB_SCALE * yT;
+    const int hq = lane >> 4;
     double ssum = 0.0;
     int na = 0;
+    int bin[SSEG][EPT];
 #pragma unroll
-    for (int s = 0; s < SSEG; ++s)
+    for (int s = 0; s < SSEG; ++s) {
+      float es = 0.0f, eh = 0.0f;  // two float partial sums of four terms, each <= 1
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
-        if (!(l[s][e] > -INFINITY)) continue;
-        ++na;
-        const float d = m_w - l[s][e];
-        ssum += (double)expf(-d);
-        if (gum_nf) continue;
-        const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
-        atomicAdd(&S.hc[w][bb], 1u);
+        const float ve = v[s][e];
+        float le;
+        if (fq) {
+          const float q0 = ve * yT;
+          le = __builtin_fmaf(__builtin_fmaf(-p.T, q0, ve), yT, q0);
+        } else {
+          le = ve / p.T;
+        }
+        // a NaN (from -inf, or l overflowing to -inf) gives the floor: a zero term
+        const float ex = __builtin_amdgcn_exp2f(fmaxf((le - m_w) * 1.44269504f, -200.0f));
+        if (e < EPT / 2) es += ex; else eh += ex;
+        na += ve > -INFINITY ? 1 : 0;
+        const float db = (vm - ve) * kb;  // +inf for tokens not allowed
+        bin[s][e] = db < (float)(NCB - 1) ? (int)db : NCB - 1;
       }
-    cs.S = block_sum_f64<STPB>(ssum, S.d);
+      ssum += (double)es + (double)eh;
+    }
+    if (!gum_nf) {
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          if (v[s][e] > -INFINITY) atomicAdd(&S.hc[w][bin[s][e]][hq], 1u);
+    }
+    // the sums of the waves, one barrier (the histogram's atomics are complete after it)
+    ssum = wave_sum(ssum);
     na = wave_sum(na);
-    if (lane == 0) S.n[w] = na;
+    if (lane == 0) {
+      S.d[w] = ssum;
+      S.n[w] = na;
+    }
     __syncthreads();
+    cs.S = 0.0;
     cs.n = 0;
 #pragma unroll
-    for (int q = 0; q < NW; ++q) cs.n += S.n[q];
+    for (int q = 0; q < NW; ++q) {
+      cs.S += S.d[q];
+      cs.n += S.n[q];
+    }
     // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
     if (!gum_nf) {
-      // The chunk's candidates: the tokens of its first coarse bins (d = m_w - l below a
-      // bin edge), as many bins as keep them within GCAP, written as (l, id) to the
-      // chunk's slot region in wave order. cs.g is the largest l left out (-inf when every
-      // allowed token is a candidate): every token of the chunk with l > cs.g is a
-      // candidate, so k_gfinal can decide the row from the candidates alone when its
-      // decisions fall above the largest cs.g of the row. A second tier, the tokens of the
-      // following bins while they number at most GCAP2, goes to the region's entries from
-      // GCAP on, with cs.g2 the largest l left out of both tiers: k_gfinal reads it only
-      // when a decision falls at or below the row's largest cs.g. (The coarse histogram is
-      // complete: the barriers of the sums above follow its atomics.)
+      // The chunk's candidates: the tokens of its first coarse bins, as many bins as keep
+      // them within GCAP, written as (l, id) to the chunk's slot region in wave order.
+      // cs.g is the largest l left out (-inf when every allowed token is a candidate):
+      // every token of the chunk with l > cs.g is a candidate, so k_gfinal can decide the
+      // row from the candidates alone when its decisions fall above the largest cs.g of
+      // the row. A second tier, the tokens of the following bins while they number at
+      // most GCAP2, goes to the region's entries from GCAP on, with cs.g2 the largest l
+      // left out of both tiers: k_gfinal reads it only when a decision falls at or below
+      // the row's largest cs.g. The largest left-out l is found as the largest left-out v
+      // divided by T: rounded division by T > 0 is monotone.
       uint32_t hsum = 0u;
 #pragma unroll
-      for (int q = 0; q < NW; ++q) hsum += S.hc[q][lane];
+      for (int q = 0; q < NW; ++q) {
+        const uint4 h4 = *(const uint4*)&S.hc[q][lane][0];
+        hsum += h4.x + h4.y + h4.z + h4.w;
+      }
       const uint32_t hcum = wave_incl_scan_u32(hsum);
       const int bstar = __popcll(__ballot(hcum <= (uint32_t)GCAP)) - 1;  // -1: no bin fits
       const uint32_t cum1 =
@@ -454,18 +489,17 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         sel2[s] = 0u;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-          const float le = l[s][e];
-          const float d = m_w - le;
-          const int bb = d < 32.0f ? (int)(d * CB_SCALE) : NCB - 1;
-          const bool live_e = le > -INFINITY;
+          const float ve = v[s][e];
+          const int bb = bin[s][e];
+          const bool live_e = ve > -INFINITY;
           const bool take = live_e && bb <= bstar;
           const bool take2 = live_e && !take && bb <= bstar2;
           sel[s] |= (take ? 1u : 0u) << e;
           sel2[s] |= (take2 ? 1u : 0u) << e;
           mycnt += take ? 1 : 0;
           mycnt2 += take2 ? 1 : 0;
-          if (live_e && !take) umax = fmaxf(umax, le);
-          if (live_e && !take && !take2) umax2 = fmaxf(umax2, le);
+          umax = fmaxf(umax, take ? -INFINITY : ve);
+          umax2 = fmaxf(umax2, take || take2 ? -INFINITY : ve);
         }
       }
       constexpr int CB = SSEG == 1 ? 4 : SSEG == 2 ? 5 : SSEG == 4 ? 6 : 7;
@@ -502,16 +536,21 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
           const int e = __builtin_ctz(msk);
           msk &= msk - 1u;
           const bool t1 = (sel[s] >> e) & 1u;
-          dst[t1 ? pos : pos2] = Cand{pick8(l[s], e), i0[s] + e};
+          dst[t1 ? pos : pos2] = Cand{pick8(v[s], e) / p.T, i0[s] + e};
           pos += t1 ? 1 : 0;
           pos2 += t1 ? 0 : 1;
         }
       }
       cs_ncand = tot;
-      cs.g = um;
+      cs.g = um > -INFINITY ? um / p.T : -INFINITY;
       cs_ncand2 = tot2;
-      cs.g2 = um2;
+      cs.g2 = um2 > -INFINITY ? um2 / p.T : -INFINITY;
     } else {
+      float (&l)[SSEG][EPT] = v;  // v is not needed after this
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) l[s][e] = v[s][e] > -INFINITY ? v[s][e] / p.T : -INFINITY;
       const uint64_t key = mix64(p.seed, p.position);
       float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
       int id0 = -1, id1 = -1;
