@@ -198,6 +198,21 @@ int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, in
                        int32_t Vd, int64_t row_stride, const int32_t* draft_to_full,
                        int32_t* out);
 
+/* Producer of the logits (the step before the path): the decode step's final RMSNorm
+ * and dense lm_head linear (QwenModel.swift:202-212; store.rmsNorm and store.linear,
+ * Weights.swift:244-255,270-273), written as the bf16 logits strim_sample and
+ * strim_verify read. hidden: bf16 [B][hidden_stride]; norm_weight: bf16 [K], or NULL when
+ * hidden is already normalised; xn: bf16 [B][K] workspace for the normalised rows (unused
+ * when norm_weight is NULL); lm_head: bf16 [V][lm_head_stride]; out_logits: bf16
+ * [B][out_stride]. xn[b][k] = bf16(w[k] * bf16(x[b][k] / sqrt(mean_k x^2 + eps))) (squares
+ * summed in double), logits[b][v] = bf16(sum_k xn[b][k] lm_head[v][k]) accumulated in
+ * float32 on MFMA. B in [1, 64]; K a positive multiple of 256; hidden, xn, lm_head and
+ * their row strides 16-byte aligned. Sizes or alignment out of range: STRIM_EINVAL. */
+int strim_head_logits(void* stream, const void* hidden, int64_t hidden_stride, int32_t B,
+                      int32_t K, const void* norm_weight, float eps, void* xn,
+                      const void* lm_head, int64_t lm_head_stride, int32_t V, void* out_logits,
+                      int64_t out_stride);
+
 /* ---- per-kernel timing -------------------------------------------------------------
  * Counterpart of the reference's fenced per-region GPU timer OpTimer
  * (Sources/StrimCore/OpTimer.swift:1-60). While profiling is on, every kernel a call

@@ -33,6 +33,7 @@ UNITS = [
     ("sample_kernels.hip", []),
     ("qres_kernels.hip", []),
     ("aux_kernels.hip", []),
+    ("head_kernels.hip", []),
     ("grammar_kernels.hip", []),
     ("capi.hip", []),
 ]

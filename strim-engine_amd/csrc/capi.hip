@@ -14,6 +14,9 @@
 namespace strim {
 hipError_t launch_finalize(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_gfinal(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
+hipError_t launch_head(const void* hidden, int64_t hidden_stride, int B, int K,
+                       const void* norm_w, float eps, void* xn, const void* W, int64_t w_stride,
+                       int V, void* out, int64_t out_stride, bool vo, hipStream_t st);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
@@ -620,6 +623,24 @@ int strim_mask_logits(void* stream, const void* logits, int32_t dtype, int32_t R
   hipLaunchKernelGGL(k_mask_logits, grid, dim3(256), 0, (hipStream_t)stream, logits, dtype, V,
                      row_stride, mask_words, mask_stride, out);
   return launch_status();
+}
+
+int strim_head_logits(void* stream, const void* hidden, int64_t hidden_stride, int32_t B,
+                      int32_t K, const void* norm_weight, float eps, void* xn,
+                      const void* lm_head, int64_t lm_head_stride, int32_t V, void* out_logits,
+                      int64_t out_stride) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if (!hidden || !lm_head || !out_logits || B < 1 || B > 64 || K <= 0 || K % 256 != 0 ||
+      V <= 0 || hidden_stride < K || lm_head_stride < K || out_stride < V ||
+      !(eps >= 0.0f) || !al16(hidden) || hidden_stride % 8 != 0 || !al16(lm_head) ||
+      lm_head_stride % 8 != 0)
+    return STRIM_EINVAL;
+  if (norm_weight && (!xn || !al16(xn) || !al16(norm_weight))) return STRIM_EINVAL;
+  const bool vo = ((uintptr_t)out_logits & 7u) == 0 && out_stride % 4 == 0;
+  const hipError_t e = launch_head(hidden, hidden_stride, B, K, norm_weight, eps, xn, lm_head,
+                                   lm_head_stride, V, out_logits, out_stride, vo,
+                                   (hipStream_t)stream);
+  return e == hipSuccess ? STRIM_OK : STRIM_EHIP;
 }
 
 int strim_draft_argmax(void* stream, const void* draft_logits, int32_t dtype, int32_t R,

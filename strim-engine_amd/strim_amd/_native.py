@@ -33,6 +33,7 @@ EXPORTS = (
     "strim_sample_noalloc",
     "strim_verify",
     "strim_mask_logits",
+    "strim_head_logits",
     "strim_draft_argmax",
     "strim_profile_begin",
     "strim_profile_end",
@@ -127,6 +128,9 @@ def lib() -> ctypes.CDLL:
                                    I32, I32, P, P, P, P, P, P]
         L.strim_mask_logits.restype = ctypes.c_int
         L.strim_mask_logits.argtypes = [P, P, I32, I32, I32, I64, P, I64, P]
+        L.strim_head_logits.restype = ctypes.c_int
+        L.strim_head_logits.argtypes = [P, P, I64, I32, I32, P, ctypes.c_float, P, P, I64, I32,
+                                        P, I64]
         L.strim_draft_argmax.restype = ctypes.c_int
         L.strim_draft_argmax.argtypes = [P, P, I32, I32, I32, I64, P, P]
         L.strim_profile_begin.restype = ctypes.c_int

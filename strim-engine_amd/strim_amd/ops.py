@@ -254,6 +254,34 @@ def mask_logits(logits: torch.Tensor, mask_words: torch.Tensor | None, stream=No
     return out
 
 
+def head_logits(hidden: torch.Tensor, lm_head: torch.Tensor,
+                norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                out: torch.Tensor | None = None, xn: torch.Tensor | None = None, stream=None):
+    """The producer of the logits: final RMSNorm and dense lm_head of the decode step
+    (QwenModel.swift:202-212; Weights.swift:244-255,270-273) on the GPU. hidden bf16 [B, K],
+    lm_head bf16 [V, K], norm_weight bf16 [K] (None: hidden is already normalised).
+    Returns bf16 logits [B, V] (or fills `out`), the layout sample/verify take."""
+    if hidden.dim() == 1:
+        hidden = hidden.unsqueeze(0)
+    for t in (hidden, lm_head, norm_weight, out, xn):
+        _check_cuda(t)
+        if t is not None and t.dtype != torch.bfloat16:
+            raise TypeError("head_logits takes bf16 tensors")
+    B, K = hidden.shape
+    V = lm_head.shape[0]
+    if lm_head.shape[1] != K:
+        raise ValueError(f"lm_head is [{lm_head.shape[0]}, {lm_head.shape[1]}], hidden K={K}")
+    if out is None:
+        out = torch.empty(B, V, dtype=torch.bfloat16, device=hidden.device)
+    if norm_weight is not None and xn is None:
+        xn = torch.empty(B, K, dtype=torch.bfloat16, device=hidden.device)
+    N.check(N.lib().strim_head_logits(_stream(stream), _ptr(hidden), _row_stride(hidden), B, K,
+                                      _ptr(norm_weight), float(eps), _ptr(xn), _ptr(lm_head),
+                                      _row_stride(lm_head), V, _ptr(out), _row_stride(out)),
+            "strim_head_logits")
+    return out
+
+
 def draft_argmax(draft_logits: torch.Tensor, draft_to_full: torch.Tensor | None = None,
                  stream=None):
     """MTP.nextTokenIndex (MTP.swift:104-111): table[argmax(draft logits)] per row."""
