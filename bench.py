@@ -23,7 +23,8 @@ Timing:
 Beside it: cfg3 (masks + top-p), cfg2 (heterogeneous rows with penalties and min-p), the
 B=64 stress configuration (rows/s, roofline), the general-q verify (cfg4) and the
 reference's one-hot verify (both graph-timed), a wide-nucleus row on the exact
-resolution, grammar-mask production, and the CPU oracle (a C port of the reference
+resolution, grammar-mask production, the logits producer (final RMSNorm + lm_head
+GEMV) alone and followed by the n1 chain, and the CPU oracle (a C port of the reference
 sampler) single-threaded and on every host core.
 
 Prints ONE JSON line on stdout; diagnostics go to stderr.
@@ -290,6 +291,51 @@ STREAM_CASES = {"k_stream<1, true, true, true, 1>": "n1", "k_stream<1, true, tru
                 "k_stream<1, true, false, true, 4>": "cfg5", "k_stream<1, true, false, true, 1>": "cfg3",
                 "k_stream<1, true, false, false, 1>": "cfg4"}
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_bench_workloads.md"
+
+
+def head_bench(torch, ops, dev, ctx, args, w1, m1, hl, B=8, K=5120):
+    """The producer of the logits (final RMSNorm + dense bf16 lm_head, K=5120 hidden,
+    V=151,936) on its own and followed by the n1 chain: graph-timed like the headline.
+    The 1.56 GB weight matrix is read once per call, so it streams from HBM."""
+    from strim_amd import workloads as W
+    V = W.V_DEFAULT
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    x = (2.0 * torch.randn(B, K, device=dev, generator=g)).to(torch.bfloat16)
+    nw = (1.0 + 0.1 * torch.randn(K, device=dev, generator=g)).to(torch.bfloat16)
+    wt = (0.05 * torch.randn(V, K, device=dev, generator=g)).to(torch.bfloat16)
+    xn = torch.empty(B, K, dtype=torch.bfloat16, device=dev)
+    lg = torch.empty(B, V, dtype=torch.bfloat16, device=dev)
+    head = lambda: ops.head_logits(x, wt, nw, out=lg, xn=xn)
+    n = 20
+    steps = max(200, args.steps // 4)
+    ush, kh, _ = graph_median(torch, [head] * n, steps, n)
+    hs = torch.from_numpy(w1["history"]).to(dev)
+    ns = torch.from_numpy(w1["noise"]).to(dev)
+    samp = ctx.bind_sample(lg, w1["params"], mask=m1, history=hs, history_len=hl, noise=ns)
+    def step():
+        head()
+        samp()
+    usc, kc, _ = graph_median(torch, [step] * n, steps, n)
+    st = samp.out_status.cpu().numpy()
+    assert (st == 0).all(), f"head chain status {st}"
+    byt = V * K * 2 + B * V * 2 + B * K * 2 * 3 + K * 2
+    flops = 2.0 * B * V * K
+    log(f"[bench] head B={B} K={K} V={V}: {ush:.1f} us/call; head + n1 chain {usc:.1f} us/step")
+    del wt
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"final RMSNorm + dense bf16 lm_head: hidden [{B},{K}] x lm_head [{V},{K}] "
+                    "-> bf16 logits (k_head_norm + k_head_gemv, MFMA 16x16x32 bf16)",
+        "us_per_call": round(ush, 2), "steps": kh,
+        "roofline": {"bound": "hbm", "achieved": round(byt / (ush * 1e-6) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(byt / (ush * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "bytes_per_call": int(byt), "kernel": "k_head_norm + k_head_gemv"},
+        "mfma_tflops": round(flops / (ush * 1e-6) / 1e12, 2),
+        "then_n1_chain_us_per_step": round(usc, 2),
+        "sampler_share_us": round(usc - ush, 2),
+    }
 
 
 def measured_traffic():
@@ -727,6 +773,7 @@ def main():
             "us_per_step": round(usw, 3), "steps": kw,
             "kernel_us": {k: round(v[0], 3) for k, v in ktw.items()}}
         del xw, hw, nw, callsw
+        result["head"] = head_bench(torch, ops, dev, ctx, args, w1, m1, hl)
         result["grammar_masks"] = grammar_mask_bench(torch, dev, args)
     ctx.close()
 
