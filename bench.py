@@ -387,6 +387,8 @@ def summarize(d):
             if k in ("k_qprep", "k_qcombine"):  # run before their call's k_stream
                 pending.setdefault(k, []).append(us)
                 continue
+            if k.startswith("k_head"):
+                case = "head"
             if k.startswith("k_stream"):
                 case = STREAM_CASES.get(k, k)
                 for kk, v in pending.items():
@@ -420,10 +422,12 @@ def summarize(d):
                 v = float(r["Counter_Value"])
                 if k.startswith("k_stream"):
                     case = STREAM_CASES.get(k, k)
+                if k.startswith("k_head"):
+                    case = "head"
                 if "copyBuffer" in k and int(r["Grid_Size"]) >= 131072:
                     scale[cn] = 256 * 1024 / v  # KiB moved / KiB counted
                 if "strim::" in r["Kernel_Name"]:
-                    kk = "k_stream" if k.startswith("k_stream") else k
+                    kk = k.split("<")[0] if k.startswith(("k_stream", "k_head")) else k
                     per.setdefault((kk, case, cn), []).append(v)
     print("\n## HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)\n")
     print(f"Calibration: a 256 MiB device copy reads FETCH_SIZE x {scale.get('FETCH_SIZE', 0):.3f} "
@@ -443,6 +447,25 @@ def summarize(d):
     print("\nMachine-readable (bench.py reads these lines):\n")
     for ln in lines:
         print(f"    {ln}")
+    # any other counter pass (d/<name>/*counter_collection.csv): per-kernel averages
+    for sub in sorted(p for p in d.iterdir() if p.is_dir() and p.name not in
+                      ("trace", "fetch", "write")):
+        vals = {}
+        for f in glob.glob(str(sub / "*counter_collection.csv")):
+            for r in csv.DictReader(open(f)):
+                if "strim::" in r["Kernel_Name"]:
+                    key = (_kname(r["Kernel_Name"]), r["Counter_Name"])
+                    vals.setdefault(key, []).append(float(r["Counter_Value"]))
+        if not vals:
+            continue
+        names = sorted({c for _, c in vals})
+        print(f"\n## Counters per dispatch ({sub.name}: rocprofv3 --pmc {' '.join(names)})\n")
+        print("| kernel | dispatches | " + " | ".join(names) + " |")
+        print("|---|---|" + "---|" * len(names))
+        for k in sorted({k for k, _ in vals}):
+            n = len(vals.get((k, names[0]), []))
+            cells = [f"{sum(v) / len(v):.4g}" if (v := vals.get((k, c))) else "" for c in names]
+            print(f"| {k} | {n} | " + " | ".join(cells) + " |")
 
 
 def pmc_pass(torch, ops, W, dev, steps, pool_mb):
@@ -484,12 +507,22 @@ def pmc_pass(torch, ops, W, dev, steps, pool_mb):
     run([ctx.bind_verify(ts4[i], dr4[i], p4, draft_logits=ds4[i], draft_to_full=tab4,
                          noise_mode=1) for i in range(n4)])
     del ts4, ds4, dr4
+    # the logits producer (B=8, K=5120, V=151,936): a few calls over the 1.56 GB weights
+    K = 5120
+    x = torch.randn(B, K, device=dev).to(torch.bfloat16)
+    nw = torch.ones(K, device=dev).to(torch.bfloat16)
+    wt = (0.05 * torch.randn(V, K, device=dev)).to(torch.bfloat16)
+    for _ in range(3):
+        ops.head_logits(x, wt, nw)
+    torch.cuda.synchronize()
+    del wt
     src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
     ctx.close()
-    print(f"pmc pass: {steps} steps each of n1, cfg3, cfg2, cfg5 and cfg4, one 256 MiB copy",
+    print(f"pmc pass: {steps} steps each of n1, cfg3, cfg2, cfg5 and cfg4, 3 logits-producer "
+          "calls, one 256 MiB copy",
           flush=True)
 
 
