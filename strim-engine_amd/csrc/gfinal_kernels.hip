@@ -6,8 +6,14 @@
 // slot region as (l, id)), so with G the largest cs.g of the row every token with l > G
 // is a candidate: the order, the masses and the cumulative sums of the row above G are
 // known exactly. When every decision of the row (the k-th token, the top-p cut, the draw)
-// lies above G, one workgroup takes them from the candidates alone; otherwise the row is
-// resolved by the exact streaming resolution (exact.hpp) in the same workgroup.
+// lies above G, one workgroup takes them from the candidates alone. Otherwise the row
+// deepens once: k_stream also keeps a second tier of up to GCAP2 tokens per chunk below
+// the first, with its own bound cs.g2, and the decisions run again over both tiers above
+// G2 = max cs.g2. A row that still falls short (a nucleus wider than both tiers, a flat
+// row) is resolved by the exact streaming resolution (exact.hpp) in the same workgroup.
+// The first tier is kept small (GCAP = 32 per chunk decides the common rows: a nucleus up
+// to a few hundred tokens) because every candidate of a round costs LDS atomics and
+// stores on the one CU the row runs on.
 //
 // One 1024-thread workgroup per row; each thread holds up to GNE candidates in registers:
 //   1. the chunk statistics and every candidate slot are loaded together (the slots of
@@ -38,16 +44,19 @@ namespace strim {
 
 constexpr int GT = 1024;            // threads of a k_gfinal workgroup
 constexpr int GW = GT / WAVE;       // its waves; wave w owns the histogram bins of group w
-constexpr int GNE = 8;              // candidate slots per thread: W * GCAP <= GT * GNE
-constexpr int GNE2 = 3;             // second-tier slots per thread: W * GCAP2 <= GT * GNE2
-constexpr int GCAND = GT * GNE;     // candidates of a row held in bin order
+constexpr int GNE = 2;              // candidate slots per thread: W * GCAP <= GT * GNE
+constexpr int GNE2 = 6;             // second-tier slots per thread: W * GCAP2 <= GT * GNE2
+constexpr int GCAND = 8192;         // candidates of a row held in bin order (both tiers)
 constexpr int GNB = GW * WAVE;      // histogram bins of d = m - l (64 per group)
 constexpr int GZCAP = GT;           // keys of one bin a decision resolves (one per thread)
 constexpr double GFIX = 34359738368.0;  // 2^35: the fixed-point unit of mass
 constexpr int GCSH = 49;                // a bin word: count << GCSH | mass
 constexpr uint64_t GMMASK = (1ull << GCSH) - 1ull;
-static_assert(GCAP == 128, "candidate slot of an entry: e >> 7, e & 127");
-static_assert(GT % GCAP == 0, "whole regions per pass of the workgroup");
+constexpr int GSH = __builtin_ctz(GCAP), GSH2 = __builtin_ctz(GCAP2);  // region of entry e: e >> GSH
+static_assert((1 << GSH) == GCAP && (1 << GSH2) == GCAP2, "tier sizes are powers of two");
+static_assert(GT % GCAP == 0 && GT % GCAP2 == 0, "whole regions per pass of the workgroup");
+static_assert(GT * GNE >= 64 * GCAP, "the first tier of 64 chunks fits the slots");
+static_assert(GT * (GNE + GNE2) <= GCAND, "a second round fits the bin-order arrays");
 static_assert(GNB == GT, "one bin per thread to clear");
 
 // LDS of one k_gfinal workgroup.
@@ -206,7 +215,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
 #pragma unroll
   for (int q = 0; q < GNE; ++q) {
     const int e = q * GT + t;
-    cd[q] = slots[e < ne ? (int64_t)(e >> 7) * SLOT + (e & (GCAP - 1)) : 0];
+    cd[q] = slots[e < ne ? (int64_t)(e >> GSH) * SLOT + (e & (GCAP - 1)) : 0];
   }
   const RowParams p = load_params(a, b, j);
   if (!gfinal_row(a.p[b], V, a.noise_mode, a.dlog != nullptr && vdr)) return;
@@ -295,7 +304,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     const bool icdf = a.noise_mode == STRIM_NOISE_ICDF;
     // rank-indexed noise needs every kept token's rank
     if ((p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp && !icdf) return OTHER;
-    if (ne > GCAND) return OTHER;
+    if (ne > GT * GNE) return OTHER;
     const float Gr = round == 0 ? G : G2;
     const bool all_in = !(Gr > -INFINITY);  // every allowed token is a candidate
     // min-p keeps a set that lies above the bound only if the bound itself fails it
@@ -303,16 +312,16 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     const float span = all_in ? 64.0f : fminf(fmaxf(m - Gr, 1.0f / 64.0f), 64.0f);
     const float hscale = (float)GNB / span;
     // which of this thread's slots hold a candidate: first-tier entry e = q GT + t lies
-    // in region q (GT / GCAP) + (t >> 7) at offset t & 127, second-tier entry e = q GT + t
-    // in region q (GT / GCAP2) + (t >> 6) at offset t & 63
+    // in region e / GCAP at offset e % GCAP, second-tier entry e = q GT + t in region
+    // e / GCAP2 at offset GCAP + e % GCAP2
     uint32_t vmask = 0u;
     {
       uint32_t rc[NS];
 #pragma unroll
-      for (int q = 0; q < GNE; ++q) rc[q] = S.rcnt[min(q * (GT / GCAP) + (t >> 7), GT - 1)];
+      for (int q = 0; q < GNE; ++q) rc[q] = S.rcnt[min(q * (GT / GCAP) + (t >> GSH), GT - 1)];
 #pragma unroll
       for (int q = GNE; q < NS; ++q)
-        rc[q] = S.rcnt2[min((q - GNE) * (GT / GCAP2) + (t >> 6), GT - 1)];
+        rc[q] = S.rcnt2[min((q - GNE) * (GT / GCAP2) + (t >> GSH2), GT - 1)];
 #pragma unroll
       for (int q = 0; q < GNE; ++q)
         vmask |= (((q * GT + t < ne) & ((uint32_t)(t & (GCAP - 1)) < rc[q])) ? 1u : 0u) << q;
@@ -522,7 +531,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
 #pragma unroll
       for (int q = 0; q < GNE2; ++q) {
         const int e = q * GT + t;
-        cd2[q] = slots[e < ne2 ? (int64_t)(e >> 6) * SLOT + GCAP + (e & (GCAP2 - 1)) : 0];
+        cd2[q] = slots[e < ne2 ? (int64_t)(e >> GSH2) * SLOT + GCAP + (e & (GCAP2 - 1)) : 0];
       }
       __syncthreads();  // every read of the first round's histogram is done
       S.hist[t] = 0ull;

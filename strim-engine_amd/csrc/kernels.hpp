@@ -31,8 +31,8 @@ constexpr int FTPB = 256;        // threads of a k_finalize workgroup (one row)
 constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
 constexpr int FCAP = 8192;       // candidate keys k_finalize holds in LDS
 constexpr int FCAP_FAST = 4096;  // of which fast rows use at most this many
-constexpr int GCAP = 128;        // candidates a general row's chunk collects (at most)
-constexpr int GCAP2 = 64;        // and its second tier, after them in the slot region
+constexpr int GCAP = 32;         // candidates a general row's chunk collects (at most)
+constexpr int GCAP2 = 128;       // and its second tier, after them in the slot region
 constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
 constexpr float CB_SCALE = 2.0f;
 constexpr int KLOC = 256;        // largest top-k served by local candidates
