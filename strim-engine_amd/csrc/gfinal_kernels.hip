@@ -15,7 +15,9 @@
 // to a few hundred tokens) because every candidate of a round costs LDS atomics and
 // stores on the one CU the row runs on.
 //
-// One 1024-thread workgroup per row; each thread holds up to GNE candidates in registers:
+// One 512-thread workgroup per row (eight waves: 1,024 threads measured 1.4 us slower on
+// its merges and barriers, 256 slower on its per-thread loops); each thread holds up to
+// GNE candidates in registers:
 //   1. the chunk statistics and every candidate slot are loaded together (the slots of
 //      a region past its count are read and dropped, so nothing waits for the counts);
 //      the waves' maxima, flags, bounds and chunk mass sums are merged with one barrier;
@@ -42,10 +44,10 @@
 
 namespace strim {
 
-constexpr int GT = 1024;            // threads of a k_gfinal workgroup
+constexpr int GT = 512;             // threads of a k_gfinal workgroup
 constexpr int GW = GT / WAVE;       // its waves; wave w owns the histogram bins of group w
-constexpr int GNE = 2;              // candidate slots per thread: W * GCAP <= GT * GNE
-constexpr int GNE2 = 6;             // second-tier slots per thread: W * GCAP2 <= GT * GNE2
+constexpr int GNE = 4;              // candidate slots per thread: W * GCAP <= GT * GNE
+constexpr int GNE2 = 12;            // second-tier slots per thread: W * GCAP2 <= GT * GNE2
 constexpr int GCAND = 8192;         // candidates of a row held in bin order (both tiers)
 constexpr int GNB = GW * WAVE;      // histogram bins of d = m - l (64 per group)
 constexpr int GZCAP = GT;           // keys of one bin a decision resolves (one per thread)
