@@ -384,7 +384,7 @@ def summarize(d):
                 continue
             k = _kname(r["Kernel_Name"])
             us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-            if k in ("k_qprep", "k_qcombine"):  # run before their call's k_stream
+            if k == "k_qprep":  # runs before its call's k_stream
                 pending.setdefault(k, []).append(us)
                 continue
             if k.startswith("k_head"):
@@ -404,7 +404,7 @@ def summarize(d):
             acc.setdefault((kk, case), []).append(us)
         acc = {key: v for key, v in acc.items() if v}
         print("\nThe same trace per workload (a kernel belongs to the k_stream variant it "
-              "follows; k_qprep and k_qcombine to the one after them; k_gmask to the grammar-mask timings, "
+              "follows; k_qprep to the one after it; k_gmask to the grammar-mask timings, "
               "cache off, then cache on):\n")
         print("| kernel | workload | calls | avg us | median us |\n|---|---|---|---|---|")
         for (k, c), v in sorted(acc.items(), key=lambda t: (str(t[0][1]), t[0][0])):

@@ -21,7 +21,6 @@ __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
 __global__ void k_qprep(Args a);
-__global__ void k_qcombine(Args a);
 __global__ void k_qsum(Args a);
 __global__ void k_qhist(Args a);
 __global__ void k_qpick(Args a);
@@ -57,10 +56,9 @@ namespace {
 constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Byte offsets of the scratch buffers of R rows of up to max_vocab tokens, each 256-byte
-// aligned. The general-q verify buffers (dbits .. qflag) are sized only when `verify`.
+// aligned. The general-q verify buffers (dbits .. qpp) are sized only when `verify`.
 struct ScratchLayout {
-  size_t cstat, slot, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp,
-      qflag, bytes;
+  size_t cstat, slot, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp, bytes;
 };
 constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) {
   const size_t wmax = (max_vocab + CHUNK - 1) / CHUNK;
@@ -82,7 +80,6 @@ constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) 
   L.qhm = off; off = align_up(off + RQ * wmax * QNB * sizeof(unsigned long long), 256);
   L.qst = off; off = align_up(off + RV * sizeof(QStat), 256);
   L.qpp = off; off = align_up(off + RQ * QSPLIT * sizeof(QPart), 256);
-  L.qflag = off; off = align_up(off + (verify ? sizeof(int32_t) : 0), 256);
   L.bytes = off;
   return L;
 }
@@ -105,7 +102,6 @@ Scratch scratch_at(char* base, const ScratchLayout& L, size_t max_vocab, bool ve
     s.qhm = (unsigned long long*)(base + L.qhm);
     s.qst = (QStat*)(base + L.qst);
     s.qpp = (QPart*)(base + L.qpp);
-    s.qflag = (int32_t*)(base + L.qflag);
   }
   s.wmax = (int32_t)((max_vocab + CHUNK - 1) / CHUNK);
   return s;
@@ -201,7 +197,14 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
     else need_fin = true;
   }
   if (gq) need_fin = true;
-  const bool need_final = gq;  // k_final decides the general-q verify rows
+  // k_final decides the general-q draft rows left to the exact resolution: the filtered
+  // ones, and (icdf draws) those whose residual bin overflows
+  bool need_final = gq && a.noise_mode == STRIM_NOISE_ICDF;
+  if (gq)
+    for (int i = 0; i < nb; ++i) {
+      const strim_sampling_params& q = a.p[i];
+      if ((q.top_k > 0 && q.top_k < a.V) || q.top_p < 1.0f || q.min_p > 0.0f) need_final = true;
+    }
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
   hipError_t e = hipSuccess;
   auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };
@@ -406,7 +409,7 @@ int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t 
     return STRIM_OK;
   });
   if (rc != STRIM_OK) {
-    if (ctx->base) (void)hipFree(ctx->base);
+    if (ctx->base) (void)on_device(device, [&]() -> int { return (int)hipFree(ctx->base); });
     delete ctx;
     return rc;
   }
@@ -532,14 +535,15 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       }
       hipError_t e = hipSuccess;
       if (a.dlog) {
-        // draft distributions (QSPLIT workgroups per draft row, merged by k_qcombine)
-        // and, with the first group, the draft-vocab bitmap (one thread per table entry)
+        // draft distributions (QSPLIT workgroups per draft row; each draft row's
+        // k_finalize workgroup merges its slices) and, with the first group, the
+        // draft-vocab bitmap (one thread per table entry). (On a second stream beside
+        // k_stream, joined by an event before k_finalize, a graph step took 4.6 us longer:
+        // the cross-queue dependencies cost more than the overlap saves.)
         const int nwb = g0 == 0 ? (int)((Vd + QPT - 1) / QPT) : 0;
         timed(ctx, KID_QPREP, [&](hipEvent_t e0, hipEvent_t e1) {
           e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k * QSPLIT + nwb)),
-                          dim3(QPT), a, st, e0, nullptr);
-          if (e == hipSuccess)
-            e = launch_args((const void*)k_qcombine, dim3(1), dim3(MAXP), a, st, nullptr, e1);
+                          dim3(QPT), a, st, e0, e1);
         });
         if (e != hipSuccess) return STRIM_EHIP;
       }

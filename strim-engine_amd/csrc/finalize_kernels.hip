@@ -243,9 +243,27 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     return done;
   }
   if (vdr && a.dlog) {
-    // general-q draft row: the draft must be in a valid table; the residual draw and the
-    // p / q accept run on k_final's exact streaming resolution
-    if (*a.s.qflag == 0 || a.s.qst[b * a.k + j].td < 0) {
+    // general-q draft row: the draft distribution from k_qprep's slices (its maximum, the
+    // draft's table index, fp64 Z = sum exp(v - mq)), published for the residual draw;
+    // the draft must be in a valid table (the first draft row's slices checked it)
+    const int qr = b * a.k + j;
+    const QPart* pp = a.s.qpp + (size_t)qr * QSPLIT;
+    float mq = -INFINITY;
+    int td = -1, bad = 0;
+#pragma unroll
+    for (int q = 0; q < QSPLIT; ++q) {
+      mq = fmaxf(mq, pp[q].m);
+      td = max(td, pp[q].td);
+      bad |= a.s.qpp[q].bad;
+    }
+    if (t == 0) {
+      double z = 0.0;
+#pragma unroll
+      for (int q = 0; q < QSPLIT; ++q)
+        if (pp[q].m > -INFINITY) z += pp[q].z * exp((double)pp[q].m - (double)mq);
+      a.s.qst[qr] = QStat{mq, td, z};
+    }
+    if (bad || td < 0) {
       finish_row(a, r, STRIM_EINVAL, -1, 0, 0.0, m, 0ull, PH_DONE);
       return done;
     }

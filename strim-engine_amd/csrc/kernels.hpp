@@ -7,8 +7,8 @@
 //   k_finalize (one workgroup per row) decides greedy, fast and unfiltered Gumbel rows,
 //   k_gfinal   (one workgroup per row) the general rows (each runs only when some row of
 //                               the call needs it).
-// A general-q verify adds k_qprep / k_qcombine before them and the residual draw
-// (qres_kernels.hip) and k_final after them. Rows whose candidates overflow are decided
+// A general-q verify adds k_qprep before them and the residual draw (qres_kernels.hip)
+// after them, and k_final when a draft row can need the exact resolution. Rows whose candidates overflow are decided
 // by the exact streaming resolution (exact.hpp) inside the deciding workgroup.
 // Workgroups never wait for or fence against each other: every partial result is a
 // plain store into a per-(row, chunk) slot that the next kernel reads.
@@ -129,8 +129,7 @@ struct Scratch {
   uint32_t* qhc;                  // [MAXP][wmax][QNB] QRES rows: residual counts per bin
   unsigned long long* qhm;        // [MAXP][wmax][QNB] QRES rows: residual masses per bin
   QStat* qst;                     // [rows] per draft row (b * k + j)
-  QPart* qpp;                     // [MAXP][QSPLIT] k_qprep slices, merged by k_qcombine
-  int32_t* qflag;                 // [1] 1 when the draft table is valid
+  QPart* qpp;                     // [MAXP][QSPLIT] k_qprep slices, merged by k_finalize
   int32_t wmax;
 };
 

@@ -1,6 +1,6 @@
 // sample_kernels.hip — k_final (the exact resolution of general-q verify rows), the
 // validation output (k_probs), the verify combine and the general-q preparation
-// (k_qprep, k_qcombine).
+// (k_qprep).
 #include "exact.hpp"
 
 namespace strim {
@@ -170,7 +170,7 @@ __device__ __forceinline__ int table_lower_bound(const int32_t* tab, int n, int 
 // the table index of the row's draft token if the slice holds it, and v stored at each
 // table id of the row's dense array (the draft distribution of SpecSampling's general-q
 // extension); row 0's slices also check that the table is strictly ascending inside
-// [0, V). k_qcombine merges the slices. Blocks after them: one thread per table entry
+// [0, V). Each draft row's k_finalize workgroup merges the row's slices. Blocks after them: one thread per table entry
 // builds the membership bitmap: the first entry of each 32-id word writes the word's
 // bits and zeroes the empty words before it (the last entry also those after it), so
 // every word is written once.
@@ -270,34 +270,6 @@ __global__ __launch_bounds__(QPT) void k_qprep(Args a) {
   for (int z = max(pw + 1, 0); z < w; ++z) a.s.dbits[z] = 0u;
   if (i == Vd - 1)
     for (int z = w + 1; z < words; ++z) a.s.dbits[z] = 0u;
-}
-
-// k_qcombine: one thread per draft row merges its QSPLIT slices into the row's QStat
-// (maximum, Z rescaled to it, the draft's index) and row 0's table check into qflag.
-__global__ void k_qcombine(Args a) {
-  const int t = threadIdx.x;
-  const int nq = a.B * a.k;
-  if (t >= nq) return;
-  const QPart* pp = a.s.qpp + (size_t)t * QSPLIT;
-  const float T = a.p[t / a.k].temperature;
-  float m = -INFINITY;
-  int td = -1, bad = 0;
-  for (int s = 0; s < QSPLIT; ++s) {
-    m = fmaxf(m, pp[s].m);
-    td = max(td, pp[s].td);
-    bad |= pp[s].bad;
-  }
-  double z = 0.0;
-  for (int s = 0; s < QSPLIT; ++s)
-    if (pp[s].m > -INFINITY) z += pp[s].z * exp((double)pp[s].m - (double)m);
-  QStat q{-INFINITY, -1, 0.0};
-  if (T > 0.0f) {
-    q.mq = m;
-    q.td = td;
-    q.Z = z;
-  }
-  a.s.qst[t] = q;
-  if (t == 0) *a.s.qflag = bad ? 0 : 1;
 }
 
 }  // namespace strim
