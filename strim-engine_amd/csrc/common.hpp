@@ -115,10 +115,14 @@ __device__ __forceinline__ double gumbel64(float u) {
   float uu = u > 1e-30f ? u : 1e-30f;
   return -log(-log((double)uu));
 }
-// fp32 proxy of the same transform, used only to shortlist chunk winners.
+// fp32 proxy of the same transform, used only to shortlist chunk winners: two hardware
+// base-2 logarithms, -ln(-ln u) = -ln2 (log2(-log2 u) + log2(ln2)). Over every value u01
+// produces (k 2^-24) and the 1e-30 floor its absolute error against the fp64 transform is
+// at most 1.98e-6 (at most 1.6e-7 (1 + |g|)), that of a logf-based version 1.68e-6.
 __device__ __forceinline__ float gumbel32(float u) {
-  float uu = u > 1e-30f ? u : 1e-30f;
-  return -logf(-logf(uu));
+  const float uu = u > 1e-30f ? u : 1e-30f;
+  const float a = -__builtin_amdgcn_logf(uu);  // -log2(u) > 0
+  return -0.69314718f * (__builtin_amdgcn_logf(a) - 0.52876637f);
 }
 
 // ---- wave64 primitives on DPP ---------------------------------------------------------

@@ -546,11 +546,23 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       cs_ncand2 = tot2;
       cs.g2 = um2 > -INFINITY ? um2 / p.T : -INFINITY;
     } else {
-      float (&l)[SSEG][EPT] = v;  // v is not needed after this
+      // the fp32 proxy scores take l to its float rounding (the FMA-corrected quotient);
+      // the two tokens the chunk keeps are divided exactly when they are written
+      float l[SSEG][EPT];
 #pragma unroll
       for (int s = 0; s < SSEG; ++s)
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) l[s][e] = v[s][e] > -INFINITY ? v[s][e] / p.T : -INFINITY;
+        for (int e = 0; e < EPT; ++e) {
+          const float ve = v[s][e];
+          float le;
+          if (fq) {
+            const float q0 = ve * yT;
+            le = __builtin_fmaf(__builtin_fmaf(-p.T, q0, ve), yT, q0);
+          } else {
+            le = ve / p.T;
+          }
+          l[s][e] = ve > -INFINITY ? le : -INFINITY;
+        }
       const uint64_t key = mix64(p.seed, p.position);
       float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
       int id0 = -1, id1 = -1;
@@ -579,16 +591,20 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
           const int id = i0[s] + e;
           if (sc > s0) {
             s1 = s0; l1 = l0; id1 = id0;
-            s0 = sc; l0 = l[s][e]; id0 = id;
+            s0 = sc; l0 = v[s][e]; id0 = id;
           } else if (sc > s1) {
-            s1 = sc; l1 = l[s][e]; id1 = id;
+            s1 = sc; l1 = v[s][e]; id1 = id;
           }
         }
       }
+      // (l0, l1 carry the tokens' v until here)
       block_top2<STPB>(s0, l0, id0, s1, l1, id1, S.tf, S.ti);
       if (t == 0) {
         ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
-        pt.l0 = l0; pt.id0 = id0; pt.l1 = l1; pt.id1 = id1;
+        pt.l0 = id0 >= 0 ? l0 / p.T : -INFINITY;
+        pt.id0 = id0;
+        pt.l1 = id1 >= 0 ? l1 / p.T : -INFINITY;
+        pt.id1 = id1;
       }
     }
   }
