@@ -363,8 +363,8 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   // table (whose score is the p-score), a lower bound lb of the wave's best. Only tokens
   // with ub >= the wave's largest lb can be the best; they alone are scored exactly in
   // fp64, with the same arithmetic and tie rule as every token was before. The margin
-  // covers the fp32 rounding of l - m - lse and of the two logarithms (well below 1e-4
-  // at these magnitudes).
+  // covers the fp32 rounding of l - m - lse and the proxy transform's error (at most
+  // 2e-6; well below 1e-4 in all at these magnitudes).
   const float mf = m, lsef = (float)lse;
   float ub[EPT];
   float lbw = -INFINITY;
@@ -373,7 +373,7 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
     ub[e] = -INFINITY;
     if (!(l[e] > -INFINITY)) continue;
     const float bf = no_lse ? l[e] : (l[e] - mf) - lsef;
-    const float sf = bf - logf(-logf(fmaxf(u[e], 1e-30f)));
+    const float sf = bf + gumbel32(u[e]);
     const float mg = 1e-3f + 1e-5f * fabsf(sf);
     ub[e] = sf + mg;
     if (!((qbits >> e) & 1u)) lbw = fmaxf(lbw, sf - mg);
