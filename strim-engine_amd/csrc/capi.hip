@@ -21,7 +21,6 @@ __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
 __global__ void k_qprep(Args a);
-__global__ void k_qsum(Args a);
 __global__ void k_qhist(Args a);
 __global__ void k_qpick(Args a);
 __global__ void k_qcollect(Args a);
@@ -222,14 +221,13 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
     // the residual draw of unfiltered general-q rows (rows in other phases return)
     const dim3 grid_r((unsigned)a.R);
     timed(ctx, KID_QRES, [&](hipEvent_t e0, hipEvent_t e1) {
-      keep(launch_args((const void*)k_qsum, grid_rc, dim3(TPB), a, st, e0, nullptr));
       if (a.noise_mode == STRIM_NOISE_ICDF) {
-        keep(launch_args((const void*)k_qhist, grid_rc, dim3(TPB), a, st, nullptr, nullptr));
+        keep(launch_args((const void*)k_qhist, grid_rc, dim3(TPB), a, st, e0, nullptr));
         keep(launch_args((const void*)k_qpick, grid_r, dim3(QNB), a, st, nullptr, nullptr));
         keep(launch_args((const void*)k_qcollect, grid_rc, dim3(TPB), a, st, nullptr, nullptr));
         keep(launch_args((const void*)k_qfinal, grid_r, dim3(FIN_T), a, st, nullptr, e1));
       } else {
-        keep(launch_args((const void*)k_qgumbel, grid_rc, dim3(TPB), a, st, nullptr, nullptr));
+        keep(launch_args((const void*)k_qgumbel, grid_rc, dim3(TPB), a, st, e0, nullptr));
         keep(launch_args((const void*)k_qgpick, grid_r, dim3(WAVE), a, st, nullptr, e1));
       }
     });

@@ -270,6 +270,13 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     // unfiltered rows: the grid-wide residual draw (qres_kernels.hip); the others: k_final's
     // exact resolution (the row's first maximum is kept as the fallback token)
     const bool unfiltered = !(p.top_k > 0 && p.top_k < V) && !(p.top_p < 1.0f) && !(p.min_p > 0.0f);
+    if (unfiltered && own) {
+      // the residual draw's plain mass per chunk, round(2^43 sum exp(l - m)), from
+      // k_stream's chunk sums (fp64 over float terms: within a few 1e-7 of the sum of
+      // the per-token fixed-point weights)
+      const double wc = cs.n > 0 ? cs.S * exp((double)cs.m - (double)m) : 0.0;
+      a.s.qpart[(size_t)qr * a.s.wmax + t] = (unsigned long long)__double2ull_rn(wc * XFIX);
+    }
     finish_row(a, r, STRIM_OK, arg, 0, 0.0, m, 0ull, unfiltered ? PH_QRES : PH_EXACT);
     return done;
   }

@@ -6,8 +6,8 @@
 // 2^43 per unit of exp(l - m), so every sum is exact and independent of order): the
 // drawn token is the last one whose residual mass before it is <= T = floor(u R), R the
 // row's residual mass. The exact resolution makes these passes with one workgroup per
-// row; here each pass runs on a (chunks, rows) grid:
-//   k_qsum      per chunk: plain mass W = round(exp(l - m) 2^43) summed      -> S
+// row; here each pass runs on a (chunks, rows) grid. The row's plain mass S (2^43 units
+// of exp(l - m)) comes from k_stream's fp64 chunk sums, placed per chunk by k_finalize:
 //   k_qhist     per chunk: residual weights (they need S), counts and masses in QNB
 //               coarse bins of d = m - l (1/4 nat; monotone along the order)
 //   k_qpick     per row: R, T, the last non-empty bin whose mass before it is <= T
@@ -16,7 +16,7 @@
 // A bin with more than CAP tokens leaves the row to k_final's exact resolution.
 //
 // With Gumbel noise the draw is the argmax over the row of log(p - q) + g (log p where
-// q = 0, tokens with p <= q excluded), ties to the smaller id: after k_qsum,
+// q = 0, tokens with p <= q excluded), ties to the smaller id:
 //   k_qgumbel   per chunk: the chunk's best (score, id)
 //   k_qgpick    per row: the best over the chunks, the p(d) / q(d) accept.
 #include "exact.hpp"
@@ -70,26 +70,6 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* scratch)
   for (int q = 0; q < NT / WAVE; ++q) s += scratch[q];
   __syncthreads();
   return s;
-}
-
-__global__ __launch_bounds__(TPB) void k_qsum(Args a) {
-  __shared__ uint32_t s_cnt[CHUNK];
-  __shared__ uint64_t s_red[TPB / WAVE];
-  int r, c;
-  map_block(r, c);
-  int b, j;
-  row_bj(a, r, b, j);
-  if (a.s.rs[r].phase != PH_QRES) return;
-  const RowParams p = load_params(a, b, j);
-  const float m = a.s.rs[r].m;
-  float l[EPT];
-  q_tokens(a, r, b, j, p, c, s_cnt, l);
-  uint64_t w = 0ull;
-#pragma unroll
-  for (int e = 0; e < EPT; ++e)
-    if (l[e] > -INFINITY) w += x_weight(l[e], m);
-  w = block_sum_u64<TPB>(w, s_red);
-  if (threadIdx.x == 0) a.s.qpart[(size_t)(b * a.k + j) * a.s.wmax + c] = w;
 }
 
 __global__ __launch_bounds__(TPB) void k_qhist(Args a) {

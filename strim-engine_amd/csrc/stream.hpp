@@ -391,7 +391,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       }
     }
     cs_ncand = tot <= SLOT ? (uint32_t)tot : 0xFFFFFFFFu;
-  } else if (p.cls == CLS_GENERAL && live && !(a.dlog && a.verify && j < a.k)) {
+  } else if (p.cls == CLS_GENERAL && live) {
     // Chunk mass sum exp(l - m_w) and a coarse histogram of counts of m_w - l (which bins
     // the chunk's candidates come from). The bins are taken in v space, dv CB_SCALE / T
     // with dv = vm - v: they only have to be one consistent assignment of the tokens, as
@@ -401,10 +401,12 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     // but for rare last-bit cases that move a term by an ulp of l; the exponential is
     // 2^((l - m_w) log2(e)), a sum of positive terms good to a few 1e-7 relative. The
     // exact quotient v / T is formed only for the candidates written and the largest
-    // left-out value. General-q draft rows skip this: their draw makes its own passes
-    // (qres_kernels.hip, exact.hpp). Unfiltered Gumbel rows are decided from the chunks'
-    // two best tokens and the sum; only the other general rows need the histogram.
-    const bool gum_nf = a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V);
+    // left-out value. General-q draft rows keep the sum alone (the residual draw takes the
+    // row's mass from the chunks' sums and makes its own passes, qres_kernels.hip), and
+    // unfiltered Gumbel rows are decided from the chunks' two best tokens and the sum;
+    // only the other general rows need the histogram.
+    const bool qdraft = a.dlog && a.verify && j < a.k;
+    const bool gum_nf = !qdraft && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V);
     const float yT = 1.0f / p.T;
     // the FMA quotient needs 1/T and its products far from the float range's ends
     const bool fq = p.T > 0x1p-100f && p.T < 0x1p+100f;
@@ -435,7 +437,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       }
       ssum += (double)es + (double)eh;
     }
-    if (!gum_nf) {
+    if (!gum_nf && !qdraft) {
 #pragma unroll
       for (int s = 0; s < SSEG; ++s)
 #pragma unroll
@@ -458,7 +460,9 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       cs.n += S.n[q];
     }
     // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
-    if (!gum_nf) {
+    if (qdraft) {
+      // the sum alone
+    } else if (!gum_nf) {
       // The chunk's candidates: the tokens of its first coarse bins, as many bins as keep
       // them within GCAP, written as (l, id) to the chunk's slot region in wave order.
       // cs.g is the largest l left out (-inf when every allowed token is a candidate):
