@@ -26,7 +26,8 @@ __global__ void k_qpick(Args a);
 __global__ void k_qcollect(Args a);
 __global__ void k_qfinal(Args a);
 __global__ void k_qgumbel(Args a);
-__global__ void k_qgpick(Args a);
+hipError_t launch_qgpick(const Args& a, bool combine, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1);
 __global__ void k_mask_logits(const void* logits, int dtype, int V, int64_t row_stride,
                               const uint32_t* mask, int64_t mask_stride, float* out);
 __global__ void k_draft_argmax(const void* logits, int dtype, int Vd, int64_t row_stride,
@@ -182,7 +183,9 @@ bool nofilter(const strim_sampling_params& p, int32_t V) {
 // and unfiltered Gumbel rows (and the marking of general-q draft rows) and k_gfinal for
 // the general rows, each launched only when some row of the group needs it; general-q
 // verify groups add the residual draw and k_final.
-int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
+int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs,
+              bool* combined = nullptr) {
+  if (combined) *combined = false;
   bool need_fin = false, need_gfin = false, any_pen = false;
   const bool gq = a.verify && a.dlog != nullptr && a.k > 0;  // general-q draft rows
   for (int i = 0; i < nb; ++i) {
@@ -228,7 +231,10 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs) {
         keep(launch_args((const void*)k_qfinal, grid_r, dim3(FIN_T), a, st, nullptr, e1));
       } else {
         keep(launch_args((const void*)k_qgumbel, grid_rc, dim3(TPB), a, st, e0, nullptr));
-        keep(launch_args((const void*)k_qgpick, grid_r, dim3(WAVE), a, st, nullptr, e1));
+        // with nothing after it, k_qgpick also runs the verify combine
+        const bool comb = combined != nullptr && !need_final && !probs;
+        keep(launch_qgpick(a, comb, st, nullptr, e1));
+        if (comb) *combined = true;
       }
     });
   }
@@ -545,12 +551,14 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
         });
         if (e != hipSuccess) return STRIM_EHIP;
       }
-      int rc = run_group(ctx, st, a, nb, false);
+      bool combined = false;
+      int rc = run_group(ctx, st, a, nb, false, &combined);
       if (rc != STRIM_OK) return rc;
-      timed(ctx, KID_COMBINE, [&](hipEvent_t e0, hipEvent_t e1) {
-        e = launch_args((const void*)k_verify_combine, dim3((unsigned)((nb + 63) / 64)), dim3(64),
-                        a, st, e0, e1);
-      });
+      if (!combined)
+        timed(ctx, KID_COMBINE, [&](hipEvent_t e0, hipEvent_t e1) {
+          e = launch_args((const void*)k_verify_combine, dim3((unsigned)((nb + 63) / 64)),
+                          dim3(64), a, st, e0, e1);
+        });
       rc = e != hipSuccess ? STRIM_EHIP : launch_status();
       if (rc != STRIM_OK) return rc;
     }

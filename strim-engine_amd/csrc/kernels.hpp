@@ -214,6 +214,52 @@ __host__ __device__ inline bool gfinal_row(const strim_sampling_params& p, int32
   return !(noise_mode == STRIM_NOISE_GUMBEL && nofilter);
 }
 
+// A row's outcome as the verify combine reads it.
+struct RowOut {
+  int32_t status, accept, token;
+};
+// SpecSampling.verify's accept chain over sequence b's k + 1 rows (one thread): the
+// leading accepted drafts, the token at the first rejection (or the bonus row's), and the
+// per-row outputs; row(j) gives row j's outcome.
+template <typename F>
+__device__ __forceinline__ void verify_combine_one(const Args& a, int b, F row) {
+  const int k = a.k;
+  int status = STRIM_OK, n = 0, token = -1;
+  bool alive = true;
+  // SpecSampling.verify consumes only the rows its accept chain reaches, 0 .. n
+  // (SpecSampling.swift:101-105): a row error counts for the sequence only when the chain
+  // reaches that row; later rows report theirs in the per-row outputs alone
+  for (int j = 0; j <= k; ++j) {
+    const RowOut rs = row(j);
+    if (rs.status != STRIM_OK) {
+      if (alive) {
+        status = rs.status;
+        alive = false;
+      }
+      if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = 0;
+      if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = -1;
+      continue;
+    }
+    const int acc = j < k ? rs.accept : 0;
+    if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = acc;
+    if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = rs.token;
+    if (alive) {
+      if (j < k && acc) ++n;
+      else {
+        alive = false;
+        token = rs.token;
+      }
+    }
+  }
+  if (status != STRIM_OK) {
+    n = 0;
+    token = -1;
+  }
+  a.out_accepted[b] = n;
+  a.out_token[b] = token;
+  if (a.out_status) a.out_status[b] = status;
+}
+
 __device__ __forceinline__ void row_bj(const Args& a, int r, int& b, int& j) {
   if (a.verify) {
     b = r / (a.k + 1);

@@ -18,7 +18,8 @@
 // With Gumbel noise the draw is the argmax over the row of log(p - q) + g (log p where
 // q = 0, tokens with p <= q excluded), ties to the smaller id:
 //   k_qgumbel   per chunk: the chunk's best (score, id)
-//   k_qgpick    per row: the best over the chunks, the p(d) / q(d) accept.
+//   k_qgpick    per sequence: each row's best over the chunks and the p(d) / q(d)
+//               accept, then the sequence's accept chain when nothing follows.
 #include "exact.hpp"
 
 namespace strim {
@@ -392,44 +393,72 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   }
 }
 
-// One row per wave.
-__global__ __launch_bounds__(WAVE) void k_qgpick(Args a) {
-  const int r = blockIdx.x;
-  int b, j;
-  row_bj(a, r, b, j);
-  RowState* rs = &a.s.rs[r];
-  if (rs->phase != PH_QRES) return;
-  const int t = threadIdx.x, qr = b * a.k + j;
-  const RowParams p = load_params(a, b, j);
-  uint64_t sp = 0ull;
-  double bsc = -INFINITY;
-  int bid = -1;
-  for (int c = t; c < a.W; c += WAVE) {
-    sp += a.s.qpart[(size_t)qr * a.s.wmax + c];
-    const size_t o = ((size_t)qr * a.s.wmax + c) * QNB;
-    q_take(bsc, bid, __longlong_as_double((long long)a.s.qhm[o]), (int)a.s.qhc[o]);
+// One workgroup per sequence: wave w picks draft rows j = w, w + QGP_W, ... (those in
+// phase QRES); with COMBINE (no later kernel decides rows of the call) the sequence's
+// accept chain follows in the same workgroup, reading the picked rows from LDS.
+constexpr int QGP_W = 4;
+template <bool COMBINE>
+__global__ __launch_bounds__(QGP_W * WAVE) void k_qgpick(Args a) {
+  __shared__ RowOut s_out[MAXP];
+  __shared__ int s_mine[MAXP];
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  for (int j = w; j < a.k; j += QGP_W) {
+    const int r = b * (a.k + 1) + j;
+    RowState* rs = &a.s.rs[r];
+    const bool mine = rs->phase == PH_QRES;
+    if (lane == 0) s_mine[j] = mine ? 1 : 0;
+    if (!mine) continue;
+    const int qr = b * a.k + j;
+    const RowParams p = load_params(a, b, j);
+    uint64_t sp = 0ull;
+    double bsc = -INFINITY;
+    int bid = -1;
+    for (int c = lane; c < a.W; c += WAVE) {
+      sp += a.s.qpart[(size_t)qr * a.s.wmax + c];
+      const size_t o = ((size_t)qr * a.s.wmax + c) * QNB;
+      q_take(bsc, bid, __longlong_as_double((long long)a.s.qhm[o]), (int)a.s.qhc[o]);
+    }
+    const uint64_t S = wave_sum_u64(sp);
+    q_wave_best(bsc, bid);
+    const float m = rs->m;
+    const int draft = a.drafts[(int64_t)b * a.k + j];
+    const float l_draft = rs->l_draft;
+    const XQ q = q_of_row(a, qr);
+    const double sig = (double)S / XFIX;
+    const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
+    double ratio = w_d / sig;
+    const double qd = xq_prob(q, draft);
+    ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
+    const float ua = row_uniform(a, r, p, (int64_t)a.V);
+    const int acc = ((double)ua < ratio) ? 1 : 0;
+    if (lane == 0) {
+      const int token = bid >= 0 ? bid : rs->token;  // the row's first maximum when nothing scores
+      rs->status = STRIM_OK;
+      rs->token = token;
+      rs->accept = acc;
+      rs->sum_kept = sig;
+      rs->last_key = ~0ull;
+      rs->phase = PH_DONE;
+      s_out[j] = RowOut{STRIM_OK, acc, token};
+    }
   }
-  const uint64_t S = wave_sum_u64(sp);
-  q_wave_best(bsc, bid);
-  const float m = rs->m;
-  const int draft = a.drafts[(int64_t)b * a.k + j];
-  const float l_draft = rs->l_draft;
-  const XQ q = q_of_row(a, qr);
-  const double sig = (double)S / XFIX;
-  const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
-  double ratio = w_d / sig;
-  const double qd = xq_prob(q, draft);
-  ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
-  const float ua = row_uniform(a, r, p, (int64_t)a.V);
-  const int acc = ((double)ua < ratio) ? 1 : 0;
-  if (t == 0) {
-    rs->status = STRIM_OK;
-    rs->token = bid >= 0 ? bid : rs->token;  // the row's first maximum when nothing scores
-    rs->accept = acc;
-    rs->sum_kept = sig;
-    rs->last_key = ~0ull;
-    rs->phase = PH_DONE;
+  if constexpr (COMBINE) {
+    __syncthreads();
+    if (t == 0)
+      verify_combine_one(a, b, [&](int j) {
+        if (j < a.k && s_mine[j]) return s_out[j];
+        const RowState& rs = a.s.rs[(int64_t)b * (a.k + 1) + j];
+        return RowOut{rs.status, rs.accept, rs.token};
+      });
   }
+}
+
+hipError_t launch_qgpick(const Args& a, bool combine, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1) {
+  return combine ? launch_args((const void*)k_qgpick<true>, dim3((unsigned)a.B),
+                               dim3(QGP_W * WAVE), a, st, e0, e1)
+                 : launch_args((const void*)k_qgpick<false>, dim3((unsigned)a.B),
+                               dim3(QGP_W * WAVE), a, st, e0, e1);
 }
 
 }  // namespace strim

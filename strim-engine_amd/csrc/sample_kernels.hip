@@ -113,41 +113,10 @@ __global__ __launch_bounds__(TPB) void k_probs(Args a) {
 __global__ void k_verify_combine(Args a) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= a.B) return;
-  const int k = a.k;
-  int status = STRIM_OK, n = 0, token = -1;
-  bool alive = true;
-  // SpecSampling.verify consumes only the rows its accept chain reaches, 0 .. n
-  // (SpecSampling.swift:101-105): a row error counts for the sequence only when the chain
-  // reaches that row; later rows report theirs in the per-row outputs alone
-  for (int j = 0; j <= k; ++j) {
-    const RowState& rs = a.s.rs[(int64_t)b * (k + 1) + j];
-    if (rs.status != STRIM_OK) {
-      if (alive) {
-        status = rs.status;
-        alive = false;
-      }
-      if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = 0;
-      if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = -1;
-      continue;
-    }
-    const int acc = j < k ? rs.accept : 0;
-    if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = acc;
-    if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = rs.token;
-    if (alive) {
-      if (j < k && acc) ++n;
-      else {
-        alive = false;
-        token = rs.token;
-      }
-    }
-  }
-  if (status != STRIM_OK) {
-    n = 0;
-    token = -1;
-  }
-  a.out_accepted[b] = n;
-  a.out_token[b] = token;
-  if (a.out_status) a.out_status[b] = status;
+  verify_combine_one(a, b, [&](int j) {
+    const RowState& rs = a.s.rs[(int64_t)b * (a.k + 1) + j];
+    return RowOut{rs.status, rs.accept, rs.token};
+  });
 }
 
 // ---------------------------------------------------------------------------------
