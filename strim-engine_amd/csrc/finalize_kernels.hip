@@ -293,6 +293,11 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   }
 
   // ---- unfiltered Gumbel rows: the chunks' two best tokens ------------------------
+  // (and a chunk's near ties of its second best, as its candidates; flag 8: a chunk had
+  // more near ties than its candidate region holds, the exact resolution decides)
+  if (p.cls == CLS_GENERAL && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, V) &&
+      (flags & 8))
+    return ExactReq{1, m, arg, draft, l_draft};
   if (p.cls == CLS_GENERAL && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, V)) {
     const double wc = (t < W && cs.n > 0) ? cs.S * exp((double)cs.m - (double)m) : 0.0;
     const double sig = block_sum_f64<FTPB>(wc, S.d);
@@ -300,21 +305,22 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     double bsc = -INFINITY;
     uint64_t btk = ~0ull;
     int bid = -1;
+    auto take = [&](int id, float l) {
+      if (id < 0 || id == excl_id) return;
+      const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
+                              : philox_uniform(pkey, (uint64_t)id);
+      const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
+      const double sc = base + gumbel64(u);
+      if (bid < 0 || sc > bsc || (sc == bsc && (uint64_t)id < btk)) {
+        bsc = sc; btk = (uint64_t)id; bid = id;
+      }
+    };
     if (t < W) {
       const ChunkPart pt = a.s.part[(int64_t)r * a.s.wmax + t];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int id = h == 0 ? pt.id0 : pt.id1;
-        const float l = h == 0 ? pt.l0 : pt.l1;
-        if (id < 0 || id == excl_id) continue;
-        const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
-                                : philox_uniform(pkey, (uint64_t)id);
-        const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
-        const double sc = base + gumbel64(u);
-        if (bid < 0 || sc > bsc || (sc == bsc && (uint64_t)id < btk)) {
-          bsc = sc; btk = (uint64_t)id; bid = id;
-        }
-      }
+      take(pt.id0, pt.l0);
+      take(pt.id1, pt.l1);
+      const Cand* near = a.s.slot + ((int64_t)r * a.s.wmax + t) * SLOT;
+      for (uint32_t e = 0; e < cs.ncand; ++e) take(near[e].id, near[e].l);
     }
     block_argmax_score<FTPB>(bsc, btk, bid, S.d, S.u, S.i, &S.misc[3]);
     int token = S.misc[3];

@@ -158,8 +158,10 @@ __device__ __forceinline__ void top2_merge(float& s0, float& l0, int& i0, float&
 // score, the smallest id among equal scores; the runner-up is the best of every lane's
 // remaining candidate (the winner lane's second, the others' first). Ids are unique, so
 // the winner lane is.
+// With `s2` (each lane's third score on entry) the wave's third-best score is returned in
+// it: the best of what every lane has left once the two winners are taken.
 __device__ __forceinline__ void wave_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
-                                          int& i1) {
+                                          int& i1, float* s2 = nullptr) {
   const int lane = threadIdx.x & (WAVE - 1);
   auto best = [&](float sc, float lv, int id, float& bs, float& bl, int& bi) -> int {
     const bool ok = id >= 0;
@@ -180,39 +182,47 @@ __device__ __forceinline__ void wave_top2(float& s0, float& l0, int& i0, float& 
   int bi0, bi1;
   const int wl = best(s0, l0, i0, bs0, bl0, bi0);
   const bool mine = lane == wl;
-  best(mine ? s1 : s0, mine ? l1 : l0, mine ? i1 : i0, bs1, bl1, bi1);
+  const int wl1 = best(mine ? s1 : s0, mine ? l1 : l0, mine ? i1 : i0, bs1, bl1, bi1);
+  if (s2) {
+    // left on each lane: the winner of both its third, a winner of one its second
+    const float rem = mine ? (lane == wl1 ? *s2 : (i1 >= 0 ? s1 : -INFINITY))
+                           : (lane == wl1 ? (i1 >= 0 ? s1 : -INFINITY) : (i0 >= 0 ? s0 : -INFINITY));
+    *s2 = wave_max_f(rem);
+  }
   s0 = bs0; l0 = bl0; i0 = bi0;
   s1 = bs1; l1 = bl1; i1 = bi1;
 }
 
-// Block top-2 (result in thread 0): each wave's two best, then wave 0 over the waves'
-// pairs. sf: [4 * NT / WAVE] floats, si: [2 * NT / WAVE] ints of LDS.
+// Block top-2 (result in every thread): each wave's two best, then every wave over the
+// waves' pairs; s2 (each thread's third score on entry) ends as the block's third-best
+// score. sf: [5 * NT / WAVE] floats, si: [2 * NT / WAVE] ints of LDS.
 template <int NT>
 __device__ __forceinline__ void block_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
-                                           int& i1, float* sf, int* si) {
+                                           int& i1, float& s2, float* sf, int* si) {
   static_assert(NT / WAVE <= WAVE, "one lane per wave");
+  constexpr int NWV = NT / WAVE;
   const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-  wave_top2(s0, l0, i0, s1, l1, i1);
+  wave_top2(s0, l0, i0, s1, l1, i1, &s2);
   if (lane == 0) {
     sf[4 * w + 0] = s0; sf[4 * w + 1] = l0; sf[4 * w + 2] = s1; sf[4 * w + 3] = l1;
+    sf[4 * NWV + w] = s2;
     si[2 * w + 0] = i0; si[2 * w + 1] = i1;
   }
   __syncthreads();
-  if (w == 0) {
-    const bool own = lane < NT / WAVE;
-    const int q = own ? lane : 0;
-    s0 = sf[4 * q]; l0 = sf[4 * q + 1]; s1 = sf[4 * q + 2]; l1 = sf[4 * q + 3];
-    i0 = own ? si[2 * q] : -1;
-    i1 = own ? si[2 * q + 1] : -1;
-    wave_top2(s0, l0, i0, s1, l1, i1);
-  }
+  const bool own = lane < NWV;
+  const int q = own ? lane : 0;
+  s0 = sf[4 * q]; l0 = sf[4 * q + 1]; s1 = sf[4 * q + 2]; l1 = sf[4 * q + 3];
+  s2 = own ? sf[4 * NWV + q] : -INFINITY;
+  i0 = own ? si[2 * q] : -1;
+  i1 = own ? si[2 * q + 1] : -1;
+  wave_top2(s0, l0, i0, s1, l1, i1, &s2);
 }
 
 // Block argmax over (score desc, tie key asc); the winner's id lands in *out_id (-1 when
 // no thread holds a candidate).
 template <int NT>
-__device__ void block_argmax_score(double sc, uint64_t tk, int id, double* s_sc, uint64_t* s_tk,
-                                   int* s_id, int* out_id) {
+__device__ __forceinline__ void block_argmax_score(double sc, uint64_t tk, int id, double* s_sc,
+                                                   uint64_t* s_tk, int* s_id, int* out_id) {
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   auto take = [](double& a, uint64_t& ak, int& ai, double b, uint64_t bk, int bi) {
     if (bi >= 0 && (ai < 0 || b > a || (b == a && bk < ak))) { a = b; ak = bk; ai = bi; }

@@ -36,7 +36,7 @@ struct StreamShared {
   int i[SMAXW], n[SMAXW], f[SMAXW];
   uint32_t off[SMAXW], off2[SMAXW];
   double d[SMAXW];
-  float tf[4 * SMAXW];
+  float tf[5 * SMAXW];
   int ti[2 * SMAXW];
 };
 
@@ -551,29 +551,20 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       cs.g2 = um2 > -INFINITY ? um2 / p.T : -INFINITY;
     } else {
       // the fp32 proxy scores take l to its float rounding (the FMA-corrected quotient);
-      // the two tokens the chunk keeps are divided exactly when they are written
-      float l[SSEG][EPT];
-#pragma unroll
-      for (int s = 0; s < SSEG; ++s)
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-          const float ve = v[s][e];
-          float le;
-          if (fq) {
-            const float q0 = ve * yT;
-            le = __builtin_fmaf(__builtin_fmaf(-p.T, q0, ve), yT, q0);
-          } else {
-            le = ve / p.T;
-          }
-          l[s][e] = ve > -INFINITY ? le : -INFINITY;
+      // the tokens the chunk keeps are divided exactly when they are written
+      auto lq = [&](float ve) -> float {
+        float le;
+        if (fq) {
+          const float q0 = ve * yT;
+          le = __builtin_fmaf(__builtin_fmaf(-p.T, q0, ve), yT, q0);
+        } else {
+          le = ve / p.T;
         }
+        return ve > -INFINITY ? le : -INFINITY;
+      };
       const uint64_t key = mix64(p.seed, p.position);
-      float s0 = -INFINITY, s1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-      int id0 = -1, id1 = -1;
-#pragma unroll
-      for (int s = 0; s < SSEG; ++s) {
-        // the segment's 8 uniforms: two Philox blocks (a segment starts on a multiple of 8)
-        float u[EPT];
+      // the segment's 8 uniforms: two Philox blocks (a segment starts on a multiple of 8)
+      auto uniforms = [&](int s, float* u) {
         if (a.noise) {
 #pragma unroll
           for (int e = 0; e < EPT; ++e) {
@@ -588,11 +579,24 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
             u[4 * hb + 2] = u01(wb.z); u[4 * hb + 3] = u01(wb.w);
           }
         }
+      };
+      auto proxy = [&](float ve, float u) -> float {
+        const float le = lq(ve);
+        return le > -INFINITY ? le + gumbel32(u) : -INFINITY;
+      };
+      // each thread keeps its two best tokens (score, v, id) and its third best score
+      float s0 = -INFINITY, s1 = -INFINITY, s2 = -INFINITY, l0 = 0.f, l1 = 0.f;
+      int id0 = -1, id1 = -1;
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) {
+        float u[EPT];
+        uniforms(s, u);
         // ids rise along the thread's tokens: a strict compare keeps the first of ties
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-          const float sc = l[s][e] > -INFINITY ? l[s][e] + gumbel32(u[e]) : -INFINITY;
+          const float sc = proxy(v[s][e], u[e]);
           const int id = i0[s] + e;
+          s2 = __builtin_amdgcn_fmed3f(sc, s1, s2);  // the third: med3 while s1 >= s2
           if (sc > s0) {
             s1 = s0; l1 = l0; id1 = id0;
             s0 = sc; l0 = v[s][e]; id0 = id;
@@ -601,8 +605,34 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
           }
         }
       }
-      // (l0, l1 carry the tokens' v until here)
-      block_top2<STPB>(s0, l0, id0, s1, l1, id1, S.tf, S.ti);
+      const float ms0 = s0, ms1 = s1, mv0 = l0, mv1 = l1, ms2 = s2;
+      const int mi0 = id0, mi1 = id1;
+      // (l0, l1 carry the tokens' v until here; every thread gets the chunk's result)
+      block_top2<STPB>(s0, l0, id0, s1, l1, id1, s2, S.tf, S.ti);
+      // The fp64 decision rescores the tokens the chunk keeps; a token left out can win
+      // only if its proxy score is within twice the proxy's error of a kept one. The error
+      // is at most 2e-6 for the transform plus the float roundings of l (one ulp at worst)
+      // and of l + g, below 1e-5 + 5e-7 |s| in all. So when the chunk's third score comes
+      // within 2e-5 + 1e-6 |s1| of the second, the threads' kept tokens whose scores reach
+      // that bound are kept as well, as the chunk's candidates (slot entries 0 ..); a
+      // thread whose third score reaches it (a near tie it did not keep) sends the row to
+      // the exact resolution (STRIM flag 8).
+      const float thr = s1 - (2e-5f + 1e-6f * fabsf(s1));
+      if (id1 >= 0 && s2 >= thr) {
+        const bool n0 = mi0 >= 0 && ms0 >= thr && mi0 != id0 && mi0 != id1;
+        const bool n1 = mi1 >= 0 && ms1 >= thr && mi1 != id0 && mi1 != id1;
+        const int over = block_or<STPB>(ms2 >= thr ? 1 : 0, (int*)S.off);
+        uint32_t ntot;
+        const uint32_t pos = block_excl_scan_u32<STPB>((n0 ? 1u : 0u) + (n1 ? 1u : 0u), S.off, &ntot);
+        Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
+        if (!over && n0 && pos < (uint32_t)SLOT) dst[pos] = Cand{mv0 / p.T, mi0};
+        const uint32_t p1 = pos + (n0 ? 1u : 0u);
+        if (!over && n1 && p1 < (uint32_t)SLOT) dst[p1] = Cand{mv1 / p.T, mi1};
+        if (t == 0) {
+          if (over || ntot > (uint32_t)SLOT) cs.flags |= 8;
+          cs_ncand = (over || ntot > (uint32_t)SLOT) ? 0u : ntot;
+        }
+      }
       if (t == 0) {
         ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
         pt.l0 = id0 >= 0 ? l0 / p.T : -INFINITY;

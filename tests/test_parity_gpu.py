@@ -513,3 +513,64 @@ def test_gpu_verify_marginal(ctx, t, k, pp):
         stat, crit = _chi2(np.bincount(e, minlength=V).astype(np.float64), P)
         assert stat < crit
         assert abs(np.concatenate(accs).mean() - P[d]) < 0.015
+
+
+@pytest.mark.parametrize("const_noise", [True, False])
+def test_gumbel_unfiltered_ties_across_waves(ctx, const_noise):
+    # Unfiltered Gumbel rows (no top-k / top-p / min-p) with quantised logits whose maximum
+    # is held by ids in several waves and chunks. With one injected uniform for every
+    # token the proxy scores tie exactly across lanes, waves and chunks, so the chunks'
+    # two-best shortlist cannot be certain and the rows take the exact resolution (ties
+    # to the smallest id); with random uniforms the shortlist decides. strim_sample and
+    # strim_verify (the draft among the tied ids) against the oracle.
+    rng = np.random.default_rng(71 if const_noise else 72)
+    B, V, k = 4, 20000, 2
+    x = (np.round(rng.normal(0.0, 1.0, size=(B, V)) * 2.0) / 2.0).astype(np.float32)
+    tied = np.array([5, 700, 1100, 4095, 4100, 9000, 13313, 19999])
+    x[:, tied] = 6.0
+    p = O.make_params(B, seed=rng.integers(0, 2**63, size=B, dtype=np.uint64), position=3)
+    if const_noise:
+        noise = np.full((B, V + 1), 0.5, np.float32)
+    else:
+        noise = rng.random((B, V + 1), dtype=np.float32)
+    say(f"gumbel ties sample const={const_noise}")
+    ids, _, _ = check_sample(ctx, x, p, "f32", noise_mode=O.NOISE_GUMBEL, noise=noise,
+                             probs=False, label="gumbel-ties")
+    if const_noise:
+        assert (ids == tied[0]).all(), ids
+    xt = np.repeat(x[:, None, :], k + 1, axis=1)
+    drafts = np.stack([tied[[0, 3]], tied[[2, 1]], tied[[7, 0]], [3, tied[4]]]).astype(np.int32)
+    nv = np.repeat(noise[:, None, :], k + 1, axis=1).copy()
+    say(f"gumbel ties verify const={const_noise}")
+    check_verify(ctx, xt, k, drafts, p, "f32", noise_mode=O.NOISE_GUMBEL, noise=nv,
+                 label="gumbel-ties-verify")
+
+
+def test_gumbel_unfiltered_near_ties(ctx):
+    # Tokens of one chunk whose Gumbel scores differ by less than the fp32 proxy's error:
+    # equal logits and adjacent uniforms (u ~ 0.9 + k 2^-24, scores ~6e-7 apart), so the
+    # chunk's proxy order may differ from the fp64 one and every near tie must reach the
+    # fp64 decision. Row 1 holds a whole chunk of equal logits under one uniform: more near
+    # ties than a chunk keeps, decided by the exact resolution. Sample and verify (drafts
+    # among the near ties) against the oracle.
+    rng = np.random.default_rng(73)
+    B, V, k = 3, 20000, 2
+    x = (np.round(rng.normal(0.0, 1.0, size=(B, V)) * 2.0) / 2.0).astype(np.float32)
+    noise = (rng.random((B, V + 1), dtype=np.float32) * np.float32(0.5)).astype(np.float32)
+    near = np.array([9, 130, 2000, 4090, 8200, 8201, 12000])
+    x[:, near] = 7.0
+    steps = rng.permutation(len(near))
+    for r in range(B):
+        noise[r, near] = (np.float32(0.9) + steps.astype(np.float32) * np.float32(2.0 ** -24))
+    x[1, 4096:8192] = 7.0
+    noise[1, 4096:8192] = np.float32(0.75)
+    p = O.make_params(B, seed=rng.integers(0, 2**63, size=B, dtype=np.uint64), position=5)
+    say("gumbel near ties sample")
+    check_sample(ctx, x, p, "f32", noise_mode=O.NOISE_GUMBEL, noise=noise, probs=False,
+                 label="gumbel-near")
+    xt = np.repeat(x[:, None, :], k + 1, axis=1)
+    drafts = np.stack([near[[3, 2]], near[[4, 5]], [4100, near[1]]]).astype(np.int32)
+    nv = np.repeat(noise[:, None, :], k + 1, axis=1).copy()
+    say("gumbel near ties verify")
+    check_verify(ctx, xt, k, drafts, p, "f32", noise_mode=O.NOISE_GUMBEL, noise=nv,
+                 label="gumbel-near-verify")
