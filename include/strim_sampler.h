@@ -69,7 +69,12 @@ extern "C" {
  *          STRIM_FLAG_NOISE_BY_RANK), element V is the accept uniform.
  * noise == NULL: uniforms come from Philox4x32-10 keyed by
  *          SplitMix64(seed, position) (SpecSampling.mix, SpecSampling.swift:29-34), counter
- *          = element index / 4. ICDF uses elements 0 (draw) and 1 (accept).          */
+ *          = element index / 4. ICDF uses elements 0 (draw) and 1 (accept).
+ * Injected uniforms must lie in [0, 1) (what the Philox stream produces: k 2^-24). The
+ * library does not check them. Below 1e-30 they are taken as 1e-30; exactly 1 gives a
+ * Gumbel score of +inf; above 1, or NaN, gives a NaN score, and such a token is never
+ * drawn (its score loses every comparison), where a scalar loop over the tokens may
+ * keep a NaN score it met first.                                                     */
 #define STRIM_NOISE_ICDF 0
 #define STRIM_NOISE_GUMBEL 1
 
