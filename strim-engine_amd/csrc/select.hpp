@@ -193,31 +193,6 @@ __device__ __forceinline__ void wave_top2(float& s0, float& l0, int& i0, float& 
   s1 = bs1; l1 = bl1; i1 = bi1;
 }
 
-// Block top-2 (result in every thread): each wave's two best, then every wave over the
-// waves' pairs; s2 (each thread's third score on entry) ends as the block's third-best
-// score. sf: [5 * NT / WAVE] floats, si: [2 * NT / WAVE] ints of LDS.
-template <int NT>
-__device__ __forceinline__ void block_top2(float& s0, float& l0, int& i0, float& s1, float& l1,
-                                           int& i1, float& s2, float* sf, int* si) {
-  static_assert(NT / WAVE <= WAVE, "one lane per wave");
-  constexpr int NWV = NT / WAVE;
-  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-  wave_top2(s0, l0, i0, s1, l1, i1, &s2);
-  if (lane == 0) {
-    sf[4 * w + 0] = s0; sf[4 * w + 1] = l0; sf[4 * w + 2] = s1; sf[4 * w + 3] = l1;
-    sf[4 * NWV + w] = s2;
-    si[2 * w + 0] = i0; si[2 * w + 1] = i1;
-  }
-  __syncthreads();
-  const bool own = lane < NWV;
-  const int q = own ? lane : 0;
-  s0 = sf[4 * q]; l0 = sf[4 * q + 1]; s1 = sf[4 * q + 2]; l1 = sf[4 * q + 3];
-  s2 = own ? sf[4 * NWV + q] : -INFINITY;
-  i0 = own ? si[2 * q] : -1;
-  i1 = own ? si[2 * q + 1] : -1;
-  wave_top2(s0, l0, i0, s1, l1, i1, &s2);
-}
-
 // Block argmax over (score desc, tie key asc); the winner's id lands in *out_id (-1 when
 // no thread holds a candidate).
 template <int NT>

@@ -38,6 +38,8 @@ struct StreamShared {
   double d[SMAXW];
   float tf[5 * SMAXW];
   int ti[2 * SMAXW];
+  float wov[SMAXW];  // unfiltered Gumbel rows: a near-tie wave's largest own third score
+  int near_n;        // unfiltered Gumbel rows: near-tie candidates written
 };
 
 // ---------------------------------------------------------------------------------
@@ -262,6 +264,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     }
   }
   if (c == 0 && t == 0) a.s.ncand[r] = 0u;
+  if (t == 0) S.near_n = 0;  // (read after the barriers below)
 
   // ---- wave maxima ----------------------------------------------------------------
   const float wmv = wave_max_f(vmax);
@@ -584,7 +587,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         const float le = lq(ve);
         return le > -INFINITY ? le + gumbel32(u) : -INFINITY;
       };
-      // each thread keeps its two best tokens (score, v, id) and its third best score
+      // each thread keeps its two best tokens (score, v, id)
       float s0 = -INFINITY, s1 = -INFINITY, s2 = -INFINITY, l0 = 0.f, l1 = 0.f;
       int id0 = -1, id1 = -1;
 #pragma unroll
@@ -596,7 +599,6 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         for (int e = 0; e < EPT; ++e) {
           const float sc = proxy(v[s][e], u[e]);
           const int id = i0[s] + e;
-          s2 = __builtin_amdgcn_fmed3f(sc, s1, s2);  // the third: med3 while s1 >= s2
           if (sc > s0) {
             s1 = s0; l1 = l0; id1 = id0;
             s0 = sc; l0 = v[s][e]; id0 = id;
@@ -605,35 +607,87 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
           }
         }
       }
-      const float ms0 = s0, ms1 = s1, mv0 = l0, mv1 = l1, ms2 = s2;
-      const int mi0 = id0, mi1 = id1;
-      // (l0, l1 carry the tokens' v until here; every thread gets the chunk's result)
-      block_top2<STPB>(s0, l0, id0, s1, l1, id1, s2, S.tf, S.ti);
       // The fp64 decision rescores the tokens the chunk keeps; a token left out can win
       // only if its proxy score is within twice the proxy's error of a kept one. The error
       // is at most 2e-6 for the transform plus the float roundings of l (one ulp at worst)
-      // and of l + g, below 1e-5 + 5e-7 |s| in all. So when the chunk's third score comes
-      // within 2e-5 + 1e-6 |s1| of the second, the threads' kept tokens whose scores reach
-      // that bound are kept as well, as the chunk's candidates (slot entries 0 ..); a
-      // thread whose third score reaches it (a near tie it did not keep) sends the row to
-      // the exact resolution (STRIM flag 8).
-      const float thr = s1 - (2e-5f + 1e-6f * fabsf(s1));
-      if (id1 >= 0 && s2 >= thr) {
-        const bool n0 = mi0 >= 0 && ms0 >= thr && mi0 != id0 && mi0 != id1;
-        const bool n1 = mi1 >= 0 && ms1 >= thr && mi1 != id0 && mi1 != id1;
-        const int over = block_or<STPB>(ms2 >= thr ? 1 : 0, (int*)S.off);
-        uint32_t ntot;
-        const uint32_t pos = block_excl_scan_u32<STPB>((n0 ? 1u : 0u) + (n1 ? 1u : 0u), S.off, &ntot);
-        Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
-        if (!over && n0 && pos < (uint32_t)SLOT) dst[pos] = Cand{mv0 / p.T, mi0};
-        const uint32_t p1 = pos + (n0 ? 1u : 0u);
-        if (!over && n1 && p1 < (uint32_t)SLOT) dst[p1] = Cand{mv1 / p.T, mi1};
-        if (t == 0) {
-          if (over || ntot > (uint32_t)SLOT) cs.flags |= 8;
-          cs_ncand = (over || ntot > (uint32_t)SLOT) ? 0u : ntot;
+      // and of l + g, below 1e-5 + 5e-7 |s| in all; tol(s) = 2e-5 + 1e-6 |s| is twice it.
+      // Every token other than the chunk's two best whose score reaches s1 - tol(s1) (s1:
+      // the chunk's second score) is kept as well, as one of the chunk's candidates (slot
+      // entries 0 ..). Since the chunk's s1 is at least its wave's second score w1, such a
+      // token reaches w1 - tol(w1) too: each wave whose third comes that close collects
+      // its lanes' kept tokens above that bound (before the barrier, so nothing of a lane
+      // stays live across it), and thread 0 adds the waves' own pairs. A lane's third
+      // (a token it did not keep) reaching the chunk's bound sends the row to the exact
+      // resolution (STRIM flag 8).
+      auto tol = [](float x) { return 2e-5f + 1e-6f * fabsf(x); };
+      float w0 = s0, wl0 = l0, w1 = s1, wl1 = l1, w2 = s2;
+      int wi0 = id0, wi1 = id1;
+      wave_top2(w0, wl0, wi0, w1, wl1, wi1, &w2);
+      float wov = -INFINITY;
+      const float wthr = w1 - tol(w1);
+      if (wi1 >= 0 && w2 >= wthr) {
+        const bool n0 = id0 >= 0 && s0 >= wthr && id0 != wi0 && id0 != wi1;
+        const bool n1 = id1 >= 0 && s1 >= wthr && id1 != wi0 && id1 != wi1;
+        float t3 = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < SSEG; ++s) {
+          float u[EPT];
+          uniforms(s, u);
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) {
+            const int id = i0[s] + e;
+            if (id != id0 && id != id1) t3 = fmaxf(t3, proxy(v[s][e], u[e]));
+          }
         }
+        wov = wave_max_f(t3);
+        const uint64_t b0 = __ballot(n0), b1 = __ballot(n1);
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&S.near_n, __popcll(b0) + __popcll(b1));
+        base = __builtin_amdgcn_readfirstlane(base);
+        Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
+        const int p0 = base + lanes_below(b0), p1 = base + __popcll(b0) + lanes_below(b1);
+        if (n0 && p0 < SLOT) dst[p0] = Cand{l0 / p.T, id0};
+        if (n1 && p1 < SLOT) dst[p1] = Cand{l1 / p.T, id1};
+      }
+      // the block's two best and third: wave 0 over the waves' pairs
+      constexpr int NWV = STPB / WAVE;
+      if (lane == 0) {
+        S.tf[4 * w + 0] = w0; S.tf[4 * w + 1] = wl0; S.tf[4 * w + 2] = w1; S.tf[4 * w + 3] = wl1;
+        S.tf[4 * NWV + w] = w2;
+        S.ti[2 * w + 0] = wi0; S.ti[2 * w + 1] = wi1;
+        S.wov[w] = wov;
+      }
+      __syncthreads();
+      if (w == 0) {
+        const bool own = lane < NWV;
+        const int q = own ? lane : 0;
+        s0 = S.tf[4 * q]; l0 = S.tf[4 * q + 1]; s1 = S.tf[4 * q + 2]; l1 = S.tf[4 * q + 3];
+        s2 = own ? S.tf[4 * NWV + q] : -INFINITY;
+        id0 = own ? S.ti[2 * q] : -1;
+        id1 = own ? S.ti[2 * q + 1] : -1;
+        wave_top2(s0, l0, id0, s1, l1, id1, &s2);
       }
       if (t == 0) {
+        const float thr = s1 - tol(s1);
+        if (id1 >= 0 && s2 >= thr) {
+          Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
+          int n = S.near_n;
+          bool over = false;
+#pragma unroll 1
+          for (int q = 0; q < NWV; ++q) {
+            over = over || S.wov[q] >= thr;
+            for (int h = 0; h < 2; ++h) {
+              const float sc = S.tf[4 * q + 2 * h];
+              const int id = S.ti[2 * q + h];
+              if (id >= 0 && sc >= thr && id != id0 && id != id1) {
+                if (n < SLOT) dst[n] = Cand{S.tf[4 * q + 2 * h + 1] / p.T, id};
+                ++n;
+              }
+            }
+          }
+          if (over || n > SLOT) cs.flags |= 8;
+          cs_ncand = (over || n > SLOT) ? 0u : (uint32_t)n;
+        }
         ChunkPart& pt = a.s.part[(int64_t)r * a.s.wmax + c];
         pt.l0 = id0 >= 0 ? l0 / p.T : -INFINITY;
         pt.id0 = id0;
