@@ -286,10 +286,13 @@ def cpu_baseline_grammar(seconds: float):
             "sample": f"trie walk of the in-string state, {n} rows in {el:.1f}s"}
 
 
-# k_stream instantiation -> workload (dtype, aligned, penalties, mask, segments per thread)
-STREAM_CASES = {"k_stream<1, true, true, true, 1>": "n1", "k_stream<1, true, true, false, 1>": "cfg2",
-                "k_stream<1, true, false, true, 4>": "cfg5", "k_stream<1, true, false, true, 1>": "cfg3",
-                "k_stream<1, true, false, false, 1>": "cfg4"}
+# k_stream instantiation -> workload
+# (dtype, aligned, history counts, mask, segments per thread, general rows)
+STREAM_CASES = {"k_stream<1, true, 2, true, 1, true>": "n1",
+                "k_stream<1, true, 2, false, 1, false>": "cfg2",
+                "k_stream<1, true, 2, true, 4, false>": "cfg5",
+                "k_stream<1, true, 0, true, 1, true>": "cfg3",
+                "k_stream<1, true, 0, false, 1, true>": "cfg4"}
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_bench_workloads.md"
 
 
@@ -416,12 +419,18 @@ def summarize(d):
         sub = "fetch" if cn == "FETCH_SIZE" else "write"
         for f in glob.glob(str(d / sub / "*counter_collection.csv")):
             rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Dispatch_Id"]))
-            case = None
+            case, pend = None, []
             for r in rows:
                 k = _kname(r["Kernel_Name"])
                 v = float(r["Counter_Value"])
+                if k == "k_qprep":  # runs before its call's k_stream
+                    pend.append((k, v))
+                    continue
                 if k.startswith("k_stream"):
                     case = STREAM_CASES.get(k, k)
+                    for kk, vv in pend:
+                        per.setdefault((kk, case, cn), []).append(vv)
+                    pend = []
                 if k.startswith("k_head"):
                     case = "head"
                 if "copyBuffer" in k and int(r["Grid_Size"]) >= 131072:
@@ -733,8 +742,8 @@ def main():
         log(f"[bench] cfg5 graph {us5:.2f} us/step; kernels (us): "
             + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt5.items()))
         result["b64"] = {
-            "workload": "cfg5: B=64 bf16, 2048-token history, 5% masks, T 0.8, top-k 40, "
-                        "top-p 0.95, min-p 0.02, Philox per row",
+            "workload": "cfg5: B=64 bf16, 2048-token history (presence 0.5, frequency 0.3), "
+                        "5% masks, T 0.8, top-k 40, top-p 0.95, min-p 0.02, Philox per row",
             "us_per_step": round(us5, 3),
             "rows_per_s": round(B5 / (us5 * 1e-6), 1),
             "steps": k5,

@@ -26,7 +26,7 @@ OUT = PKG / "strim_amd" / "libstrim_sampler.so"
 # (source, extra defines): k_stream variants per (dtype, penalties, segments) triple
 UNITS = [
     ("stream_kernels.hip", [f"-DSTRIM_DT={dt}", f"-DSTRIM_PEN={pen}", f"-DSTRIM_SSEG={sseg}"])
-    for dt in (1, 0) for pen in (1, 0) for sseg in (1, 4)
+    for dt in (1, 0) for pen in (2, 1, 0) for sseg in (1, 4)
 ] + [
     ("finalize_kernels.hip", []),
     ("gfinal_kernels.hip", []),

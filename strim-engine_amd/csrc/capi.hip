@@ -163,15 +163,18 @@ constexpr int LARGE_ROWS = 32;
 
 hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen, hipEvent_t e0,
                          hipEvent_t e1) {
-  const bool pen = any_pen || a.vec_ok == 0;
+  // history counts: none, 16-bit when no count can reach 65,536 (the history length plus
+  // the draft prefix bound every count), else 32-bit; unaligned calls take the 32-bit
+  // object, whose unaligned variant checks penalties and mask per row
+  const int pen = a.vec_ok == 0 ? 1 : !any_pen ? 0 : (int64_t)a.H + a.k < 65536 ? 2 : 1;
   const bool big = a.R >= LARGE_ROWS;
 #define STRIM_GROUP(DT, PEN, SSEG) launch_stream_group<DT, PEN, SSEG>(a, grid, st, e0, e1)
-  if (a.dtype == STRIM_DTYPE_BF16) {
-    if (pen) return big ? STRIM_GROUP(STRIM_DTYPE_BF16, true, 4) : STRIM_GROUP(STRIM_DTYPE_BF16, true, 1);
-    return big ? STRIM_GROUP(STRIM_DTYPE_BF16, false, 4) : STRIM_GROUP(STRIM_DTYPE_BF16, false, 1);
-  }
-  if (pen) return big ? STRIM_GROUP(STRIM_DTYPE_F32, true, 4) : STRIM_GROUP(STRIM_DTYPE_F32, true, 1);
-  return big ? STRIM_GROUP(STRIM_DTYPE_F32, false, 4) : STRIM_GROUP(STRIM_DTYPE_F32, false, 1);
+#define STRIM_SEGS(DT, PEN) (big ? STRIM_GROUP(DT, PEN, 4) : STRIM_GROUP(DT, PEN, 1))
+#define STRIM_PENS(DT) \
+  (pen == 2 ? STRIM_SEGS(DT, 2) : pen == 1 ? STRIM_SEGS(DT, 1) : STRIM_SEGS(DT, 0))
+  return a.dtype == STRIM_DTYPE_BF16 ? STRIM_PENS(STRIM_DTYPE_BF16) : STRIM_PENS(STRIM_DTYPE_F32);
+#undef STRIM_PENS
+#undef STRIM_SEGS
 #undef STRIM_GROUP
 }
 
@@ -207,6 +210,13 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs,
       const strim_sampling_params& q = a.p[i];
       if ((q.top_k > 0 && q.top_k < a.V) || q.top_p < 1.0f || q.min_p > 0.0f) need_final = true;
     }
+  // rows per XCD when every chunk reads a history and no general row's cost depends on
+  // its mask density (measured: -25 % of k_stream's HBM bytes at cfg2 at equal time;
+  // general rows of unequal density 0.75 us slower when each XCD holds whole rows)
+  a.xmap = any_pen && !need_gfin && !gq ? 1 : 0;
+  a.gen = 0;
+  for (int i = 0; i < nb; ++i)
+    if (row_class(a.p[i], a.V) == CLS_GENERAL) a.gen = 1;
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
   hipError_t e = hipSuccess;
   auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };

@@ -142,6 +142,9 @@ struct Args {
   int32_t R, V, W;   // rows in this group, vocab, chunks per row
   int32_t B, k;      // batch rows in this group and draft length (k = 0: sample)
   int32_t verify;
+  int32_t xmap;           // k_stream and the residual-draw kernels: rows kept per XCD
+  int32_t gen;            // some row of the launch is general (row_class): the host picks
+                          // the k_stream variant with the general rows' code
   const uint32_t* mask;
   int64_t mask_stride;
   const int32_t* hist;
@@ -270,11 +273,29 @@ __device__ __forceinline__ void row_bj(const Args& a, int r, int& b, int& j) {
   }
 }
 
-// Workgroup -> (row, chunk): streaming kernels run on a (chunks, rows) grid, so the row
-// and its params are known from blockIdx without reading any kernel argument first.
-__device__ __forceinline__ void map_block(int& r, int& c) {
-  r = blockIdx.y;
-  c = blockIdx.x;
+// Workgroup -> (row, chunk) on a (W chunks, R rows) grid. The dispatcher hands the
+// workgroups of a launch to the 8 XCDs round robin in linear order, and each XCD has an
+// L2 of its own. With a.xmap the map gives XCD x one contiguous run of the row-major
+// (row, chunk) order, so the chunks of a row share one L2 and what every chunk of a row
+// reads (its history ids) comes from HBM once per row instead of once per XCD; without
+// it the chunks of a row spread over every XCD, which balances rows of unequal cost (a
+// dense-mask general row) better. Both are bijections for every grid, whatever the
+// dispatch order.
+constexpr uint32_t NXCD = 8;
+template <typename A>
+__device__ __forceinline__ void map_block(const A& a, int& r, int& c) {
+  if (!a.xmap) {
+    r = blockIdx.y;
+    c = blockIdx.x;
+    return;
+  }
+  const uint32_t W = (uint32_t)a.W;
+  const uint32_t n = W * (uint32_t)a.R;
+  const uint32_t L = blockIdx.x + blockIdx.y * W;
+  const uint32_t x = L % NXCD, q = n / NXCD, rem = n % NXCD;
+  const uint32_t m = x * q + (x < rem ? x : rem) + L / NXCD;
+  r = (int)(m / W);
+  c = (int)(m - (uint32_t)r * W);
 }
 
 __device__ __forceinline__ RowParams load_params(const Args& a, int b, int j) {
@@ -475,33 +496,47 @@ __device__ __forceinline__ int hist_len(const A& a, int b) {
   const int raw = a.hist_len[b];
   return raw < 0 ? 0 : (raw > a.H ? a.H : raw);
 }
-template <int NT, int SPAN, typename A>
+// NARROW: 16-bit counts, two to a word (token o in the low half of word o / 2 when o is
+// even), for callers that know no count reaches 65,536 (history length plus draft prefix
+// below it); otherwise one 32-bit count per token.
+template <int NT, int SPAN, typename A, bool NARROW = false>
 __device__ __forceinline__ void hist_count(const A& a, int b, int j, int c0,
                                            const int (&ids)[hpt<NT>()], int hl, uint32_t* s_cnt) {
   constexpr int HPT = hpt<NT>();
   const int t = threadIdx.x;
+  auto add = [&](uint32_t o) {
+    if constexpr (NARROW) atomicAdd(&s_cnt[o >> 1], 1u << ((o & 1u) << 4));
+    else atomicAdd(&s_cnt[o], 1u);
+  };
   uint4* s4 = (uint4*)s_cnt;
-  for (int i = t; i < SPAN / 4; i += NT) s4[i] = make_uint4(0u, 0u, 0u, 0u);
+  for (int i = t; i < (NARROW ? SPAN / 8 : SPAN / 4); i += NT) s4[i] = make_uint4(0u, 0u, 0u, 0u);
   __syncthreads();
   const uint32_t uc0 = (uint32_t)c0;
+  // ids inside [c0, c0 + lim) count: lim stops at the row end, and a negative id wraps
+  // to a large offset
+  const int rem = a.V - c0;
+  const uint32_t lim = rem <= 0 ? 0u : (uint32_t)(rem < SPAN ? rem : SPAN);
 #pragma unroll
   for (int q = 0; q < HPT; ++q) {
+    // a group of four ids per thread lies wholly past the history length for the whole
+    // workgroup (hl is the row's): skipped by a scalar branch
+    if (4 * (q >> 2) * NT >= hl) continue;
     const int i = 4 * ((q >> 2) * NT + t) + (q & 3);
     const uint32_t o = (uint32_t)ids[q] - uc0;
-    if (i < hl && o < (uint32_t)SPAN && ids[q] >= 0 && ids[q] < a.V) atomicAdd(&s_cnt[o], 1u);
+    if (i < hl && o < lim) add(o);
   }
   if (hl > HPT * NT) {
     const int32_t* h = a.hist + (int64_t)b * a.H;
     for (int i = HPT * NT + t; i < hl; i += NT) {
       const int id = h[i];
       const uint32_t o = (uint32_t)id - uc0;
-      if (o < (uint32_t)SPAN && id >= 0 && id < a.V) atomicAdd(&s_cnt[o], 1u);
+      if (o < (uint32_t)SPAN && id >= 0 && id < a.V) add(o);
     }
   }
   if (a.verify && t < j) {
     const int id = a.drafts[(int64_t)b * a.k + t];
     const uint32_t o = (uint32_t)id - uc0;
-    if (o < (uint32_t)SPAN && id >= 0 && id < a.V) atomicAdd(&s_cnt[o], 1u);
+    if (o < (uint32_t)SPAN && id >= 0 && id < a.V) add(o);
   }
   __syncthreads();
 }

@@ -79,7 +79,7 @@ __global__ __launch_bounds__(TPB) void k_qhist(Args a) {
   __shared__ uint32_t s_hc[QNB];
   __shared__ uint64_t s_hm[QNB];
   int r, c;
-  map_block(r, c);
+  map_block(a, r, c);
   int b, j;
   row_bj(a, r, b, j);
   if (a.s.rs[r].phase != PH_QRES) return;
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(QNB) void k_qpick(Args a) {
 __global__ __launch_bounds__(TPB) void k_qcollect(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
   int r, c;
-  map_block(r, c);
+  map_block(a, r, c);
   int b, j;
   row_bj(a, r, b, j);
   const RowState* rs = &a.s.rs[r];
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   __shared__ double s_sc[TPB / WAVE];
   __shared__ int s_id[TPB / WAVE];
   int r, c;
-  map_block(r, c);
+  map_block(a, r, c);
   int b, j;
   row_bj(a, r, b, j);
   if (a.s.rs[r].phase != PH_QRES) return;

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
 __global__ __launch_bounds__(TPB) void k_probs(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
   int r, c;
-  map_block(r, c);
+  map_block(a, r, c);
   int b, j;
   row_bj(a, r, b, j);
   const RowParams p = load_params(a, b, j);

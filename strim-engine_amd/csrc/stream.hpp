@@ -23,14 +23,17 @@ namespace strim {
 template <int SSEG>
 constexpr int stpb() { return CHUNK / (EPT * SSEG); }
 
-// LDS of one k_stream workgroup (the history table only in the penalties variants, so
-// the narrow workgroups of large launches fit many to a CU).
+// LDS of one k_stream workgroup of NW waves (the history table only in the penalties
+// variants and the coarse histograms only in the variants with general rows, so the
+// narrow workgroups of large launches fit many to a CU).
 constexpr int HCQ = 4;  // copies of the coarse histogram per wave (one per 16 lanes)
-template <bool PEN>
+template <int PEN, int NW, bool GEN>
 struct StreamShared {
-  uint32_t cnt[PEN ? CHUNK : 4];  // history counts of the chunk's tokens (16 KB)
-  uint32_t hc[SMAXW][NCB][HCQ];  // general rows: coarse counts, one copy per quarter
-                                 // wave (spreads the atomics' contention)
+  // history counts of the chunk's tokens: 32 bits each (16 KB), or 16 bits (8 KB) when
+  // the host knows no count reaches 65,536
+  uint32_t cnt[PEN == 1 ? CHUNK : PEN == 2 ? CHUNK / 2 : 4];
+  uint32_t hc[GEN ? NW : 1][NCB][HCQ];  // general rows: coarse counts, one copy per
+                                        // quarter wave (spreads the atomics' contention)
   uint32_t lad[2 * WAVE];
   float v[SMAXW];
   int i[SMAXW], n[SMAXW], f[SMAXW];
@@ -139,25 +142,28 @@ __device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)
 }
 
 // DT: logits dtype; VEC: rows are 16-byte aligned; PEN: some row of the launch has
-// penalties; MASK: allow-bits are given. The host picks the instantiation, so each
-// launch runs straight-line per-token code.
+// penalties (1: 32-bit history counts, 2: 16-bit counts, for histories shorter than
+// 65,536 ids with the draft prefix); MASK: allow-bits are given; GEN: some row of the
+// launch is general (without it the general rows' code is left out, which at SSEG = 4
+// halves the registers: 60 against 115 VGPRs, no SGPR spills). The host picks the
+// instantiation, so each launch runs straight-line per-token code.
 //
 // Wave w owns the 1024 tokens [c0 + 1024 w, +1024) of the chunk; lane l holds the two
 // 8-token segments at +8 l and +512 + 8 l, so each wave-wide load is 1 KB contiguous
 // and the first maximum of the chunk lies in the lowest wave that holds the maximum.
 // The chunk statistics are written without a closing barrier (see ChunkStat).
-template <int DT, bool VEC, bool PEN, bool MASK, int SSEG>
+template <int DT, bool VEC, int PEN, bool MASK, int SSEG, bool GEN>
 __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   constexpr int STPB = stpb<SSEG>();       // threads
   constexpr int NW = STPB / WAVE;          // waves
-  __shared__ StreamShared<PEN> S;
+  __shared__ StreamShared<PEN, NW, GEN> S;
   // the launch fields used before the first global load, read together: a field first
   // read inside a branch would be its own scalar-load round trip
   asm volatile("" ::"s"(a.logits), "s"(a.row_stride), "s"(a.V), "s"(a.verify), "s"(a.k),
                "s"(a.hist), "s"(a.H), "s"(a.hist_len), "s"(a.mask), "s"(a.mask_stride),
-               "s"(a.s.cstat), "s"(a.s.wmax));
+               "s"(a.s.cstat), "s"(a.s.wmax), "s"(a.W), "s"(a.R), "s"(a.xmap));
   int r, c;
-  map_block(r, c);
+  map_block(a, r, c);
   int b, j;
   row_bj(a, r, b, j);
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
@@ -168,7 +174,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   // history ids first: the counts are built while the logits are still in flight (the
   // ids are requested before the row's parameters are known, so no load waits for them)
   int hid[hpt<STPB>()];
-  if constexpr (PEN) hist_load<STPB>(a, b, hid);
+  if constexpr (PEN != 0) hist_load<STPB>(a, b, hid);
   int i0[SSEG];
 #pragma unroll
   for (int s = 0; s < SSEG; ++s)
@@ -192,8 +198,8 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   // the row's parameters only now: a scalar-load wait for them before this point would
   // also hold back the loads above
   const RowParams p = load_params(a, b, j);
-  const bool pen = PEN && p.pen;
-  const int hl = PEN ? hist_len(a, b) : 0;
+  const bool pen = PEN != 0 && p.pen;
+  const int hl = PEN != 0 ? hist_len(a, b) : 0;
   if constexpr (MASK) {
     if (!a.mask) {
 #pragma unroll
@@ -204,40 +210,69 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   const bool topk = p.top_k > 0 && p.top_k < a.V;
   if (fast && topk)
     for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
-  if (p.cls == CLS_GENERAL)
+  if (GEN && p.cls == CLS_GENERAL)
     for (int q = t; q < NW * NCB; q += STPB) ((uint4*)&S.hc[0][0][0])[q] = make_uint4(0u, 0u, 0u, 0u);
-  if (pen) hist_count<STPB, CHUNK>(a, b, j, c0, hid, hl, S.cnt);
+  if (pen) hist_count<STPB, CHUNK, Args, PEN == 2>(a, b, j, c0, hid, hl, S.cnt);
 
   // ---- penalties and mask, before temperature ("v space") ------------------------
   // Dividing by T > 0 is monotone, so maxima and candidate bounds are found on v; only
   // the chunk maximum and (in k_finalize) the candidates are divided. Tokens past the
   // row end load as -inf (not allowed).
-  float vmax = -INFINITY;
+  // The uniform tests (penalties at all, a repetition penalty of 1) are taken once, each
+  // case a straight-line pass over the tokens: tested inside the unrolled token loop they
+  // cost scalar branches and moves per token.
+  auto seg_counts = [&](int s, uint32_t (&cnt)[EPT]) {
+    if constexpr (PEN == 2) {
+      const uint4 c4 = *(const uint4*)(S.cnt + ((i0[s] - c0) >> 1));
+      const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
-  for (int s = 0; s < SSEG; ++s) {
-    uint32_t cnt[EPT];
-    if (pen) {
+      for (int e = 0; e < EPT; ++e) cnt[e] = (cw[e >> 1] >> ((e & 1) << 4)) & 0xFFFFu;
+    } else {
       const uint4 c4a = *(const uint4*)(S.cnt + (i0[s] - c0));
       const uint4 c4b = *(const uint4*)(S.cnt + (i0[s] - c0) + 4);
       cnt[0] = c4a.x; cnt[1] = c4a.y; cnt[2] = c4a.z; cnt[3] = c4a.w;
       cnt[4] = c4b.x; cnt[5] = c4b.y; cnt[6] = c4b.z; cnt[7] = c4b.w;
     }
+  };
+  if constexpr (PEN != 0) {
+    if (pen && p.rep == 1.0f) {
+      // a repetition penalty of 1 is exact identity (x / 1 = x * 1 = x): branch-free
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) {
+        uint32_t cnt[EPT];
+        seg_counts(s, cnt);
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          float yp = v[s][e] - p.freq * (float)cnt[e];
+          yp = yp - p.pres;
+          v[s][e] = cnt[e] > 0u ? yp : v[s][e];
+        }
+      }
+    } else if (pen) {
+      // otherwise only tokens in the history divide
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s) {
+        uint32_t cnt[EPT];
+        seg_counts(s, cnt);
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          float y = v[s][e];
+          if (cnt[e] > 0u) {
+            y = y > 0.0f ? y / p.rep : y * p.rep;
+            y = y - p.freq * (float)cnt[e];
+            y = y - p.pres;
+          }
+          v[s][e] = y;
+        }
+      }
+    }
+  }
+  float vmax = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < SSEG; ++s) {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       float y = v[s][e];
-      if (pen) {
-        // a repetition penalty of 1 is exact identity (x / 1 = x * 1 = x), so the
-        // common case is branch-free; otherwise only tokens in the history divide
-        if (p.rep == 1.0f) {
-          float yp = y - p.freq * (float)cnt[e];
-          yp = yp - p.pres;
-          y = cnt[e] > 0u ? yp : y;
-        } else if (cnt[e] > 0u) {
-          y = y > 0.0f ? y / p.rep : y * p.rep;
-          y = y - p.freq * (float)cnt[e];
-          y = y - p.pres;
-        }
-      }
       if constexpr (MASK) {
         // all ones where the token is allowed: y or -inf by a bit merge, no compare
         const uint32_t keep = (uint32_t)((int32_t)(bits[s] << (31 - e)) >> 31);
@@ -394,7 +429,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       }
     }
     cs_ncand = tot <= SLOT ? (uint32_t)tot : 0xFFFFFFFFu;
-  } else if (p.cls == CLS_GENERAL && live) {
+  } else if (GEN && p.cls == CLS_GENERAL && live) {
     // Chunk mass sum exp(l - m_w) and a coarse histogram of counts of m_w - l (which bins
     // the chunk's candidates come from). The bins are taken in v space, dv CB_SCALE / T
     // with dv = vm - v: they only have to be one consistent assignment of the tokens, as
@@ -708,7 +743,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
 // Launches the k_stream variant of one (dtype, penalties, segments) triple that matches
 // the call's alignment and mask. Defined in stream_kernels.hip, one object per triple;
 // unaligned calls always take the penalties object.
-template <int DT, bool PEN, int SSEG>
+template <int DT, int PEN, int SSEG>
 hipError_t launch_stream_group(const Args& a, dim3 grid, hipStream_t st, hipEvent_t e0,
                                hipEvent_t e1);
 

@@ -198,7 +198,9 @@ def cfg5(seed=5, B=64, V=V_DEFAULT, H=2048):
     x = bf16_round(x)
     hist = rng.integers(0, V, size=(B, H), dtype=np.int32)
     allowed = rng.random((B, V)) < 0.05
+    # the 2,048-token history penalises as in cfg2 (presence 0.5, frequency 0.3)
     params = params_array(B, temperature=0.8, top_k=40, top_p=0.95, min_p=0.02,
+                          presence_penalty=0.5, frequency_penalty=0.3,
                           seed=rng.integers(0, 2**63, size=B, dtype=np.uint64), position=0)
     return dict(x=x, dtype="bf16", params=params, history=hist,
                 history_len=np.full(B, H, np.int32), mask=pack_mask(allowed), allowed=allowed,

@@ -85,6 +85,55 @@ def test_sweep_large_batch(ctx, V):
                          label=f"large V={V} it={it} mode={mode}")
 
 
+@pytest.mark.parametrize("H", [300, 4096, 8192, 9000])
+def test_large_batch_long_histories(ctx, H):
+    # Launches of 32 rows or more group each row's history by chunk first (up to 8,192
+    # ids); a longer history scans per chunk. Zipf-skewed ids put hundreds of ids in one
+    # chunk's group; ids out of range and lengths below H are dropped.
+    rng = np.random.default_rng(4000 + H)
+    B, V = 36, 20000
+    x = rng.normal(0, 2.0, size=(B, V)).astype(np.float32)
+    perm = rng.permutation(V)
+    hist = W.zipf_ids(rng, B * H, V, perm).reshape(B, H).astype(np.int32)
+    hist[:, ::97] = rng.integers(-3, 0, size=hist[:, ::97].shape)
+    hist[:, 1::89] = V + rng.integers(0, 3, size=hist[:, 1::89].shape)
+    hl = rng.integers(0, H + 1, size=B).astype(np.int32)
+    hl[:4] = H
+    p = O.make_params(B, temperature=rng.choice([0.7, 1.0], size=B),
+                      top_k=rng.choice([0, 40], size=B), top_p=rng.choice([1.0, 0.9], size=B),
+                      min_p=rng.choice([0.0, 0.02], size=B),
+                      repetition_penalty=rng.choice([1.0, 1.1], size=B),
+                      presence_penalty=0.5, frequency_penalty=0.3,
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64), position=3)
+    allowed = rng.random((B, V)) < 0.3
+    allowed[:, perm[:50]] = True
+    for dt in ("bf16", "f32"):
+        for mask in (None, W.pack_mask(allowed)):
+            say(f"large-batch history H={H} dtype={dt} mask={mask is not None}")
+            check_sample(ctx, x, p, dt, mask, hist, hl, O.NOISE_ICDF, None,
+                         label=f"long history H={H} {dt}")
+
+
+def test_verify_large_batch_history(ctx):
+    # 10 sequences x (k + 1) = 40 rows: the grouped history plus each row's draft prefix
+    rng = np.random.default_rng(77)
+    B, k, V, H = 10, 3, 9001, 2048
+    tgt = rng.normal(0, 2.0, size=(B, k + 1, V)).astype(np.float32)
+    drafts = tgt[:, :k, :].argmax(-1).astype(np.int32)
+    drafts[::3, 1] = rng.integers(0, V, size=drafts[::3, 1].shape)
+    perm = rng.permutation(V)
+    hist = W.zipf_ids(rng, B * H, V, perm).reshape(B, H).astype(np.int32)
+    hist[:, :8] = drafts[:, :1]  # the drafts are in the history too
+    p = O.make_params(B, temperature=rng.choice([0.0, 0.7, 1.0], size=B),
+                      top_k=rng.choice([0, 20], size=B), top_p=rng.choice([1.0, 0.9], size=B),
+                      repetition_penalty=1.2, presence_penalty=0.4, frequency_penalty=0.1,
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64), position=5)
+    for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+        say(f"verify large batch history mode={mode}")
+        check_verify(ctx, tgt, k, drafts, p, "bf16", None, hist, None, mode,
+                     label="verify large batch history")
+
+
 # ------------------------------------------------------------- configs ----
 def test_cfg1_fp32_chain_and_greedy(ctx):
     w = W.cfg1()
