@@ -533,6 +533,8 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
         a.dlog = (const char*)draft_logits + (size_t)g0 * k * Vd * dtype_size(dtype);
         a.dtable = draft_to_full;
         a.Vd = Vd;
+        // without per-row tokens only the first rejection's residual is needed
+        a.qskip = noise_mode == STRIM_NOISE_GUMBEL && out_row_token == nullptr ? 1 : 0;
       }
       a.noise_mode = noise_mode;
       a.noise = noise ? noise + (size_t)g0 * (k + 1) * nstride : nullptr;

@@ -256,8 +256,8 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
       td = max(td, pp[q].td);
       bad |= a.s.qpp[q].bad;
     }
+    double z = 0.0;
     if (t == 0) {
-      double z = 0.0;
 #pragma unroll
       for (int q = 0; q < QSPLIT; ++q)
         if (pp[q].m > -INFINITY) z += pp[q].z * exp((double)pp[q].m - (double)mq);
@@ -270,12 +270,43 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     // unfiltered rows: the grid-wide residual draw (qres_kernels.hip); the others: k_final's
     // exact resolution (the row's first maximum is kept as the fallback token)
     const bool unfiltered = !(p.top_k > 0 && p.top_k < V) && !(p.top_p < 1.0f) && !(p.min_p > 0.0f);
+    uint64_t wq = 0ull;
     if (unfiltered && own) {
       // the residual draw's plain mass per chunk, round(2^43 sum exp(l - m)), from
       // k_stream's chunk sums (fp64 over float terms: within a few 1e-7 of the sum of
       // the per-token fixed-point weights)
       const double wc = cs.n > 0 ? cs.S * exp((double)cs.m - (double)m) : 0.0;
-      a.s.qpart[(size_t)qr * a.s.wmax + t] = (unsigned long long)__double2ull_rn(wc * XFIX);
+      wq = (unsigned long long)__double2ull_rn(wc * XFIX);
+      a.s.qpart[(size_t)qr * a.s.wmax + t] = wq;
+    }
+    if (unfiltered && a.qskip) {
+      // Only (accepted, token) is asked for: the accept test runs here, on the same
+      // numbers as k_qgpick's (the row mass is the integer sum of the chunk masses above),
+      // so the residual draw runs only for a sequence's first rejected row.
+      const uint64_t sw = wave_sum_u64(wq);
+      if (lane == 0) S.u[w] = sw;
+      __syncthreads();
+      if (t == 0) {
+        uint64_t Sq = 0ull;
+#pragma unroll
+        for (int q = 0; q < FTPB / WAVE; ++q) Sq += S.u[q];
+        const double sig = (double)Sq / XFIX;
+        const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
+        double ratio = w_d / sig;
+        const bool in_tab = (a.s.dbits[draft >> 5] >> (draft & 31)) & 1u;
+        const double qd =
+            in_tab ? exp((double)a.s.vq[(size_t)qr * (size_t)a.s.wmax * CHUNK + draft] -
+                         (double)mq) / z
+                   : 0.0;
+        ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
+        const float ua =
+            a.noise ? pf.n1
+                    : philox_uniform(mix64(p.seed, p.position),
+                                     a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
+        const int acc = ((double)ua < ratio) ? 1 : 0;
+        finish_row(a, r, STRIM_OK, acc ? draft : arg, acc, sig, m, 0ull, acc ? PH_DONE : PH_QRES);
+      }
+      return done;
     }
     finish_row(a, r, STRIM_OK, arg, 0, 0.0, m, 0ull, unfiltered ? PH_QRES : PH_EXACT);
     return done;

@@ -145,6 +145,8 @@ struct Args {
   int32_t xmap;           // k_stream and the residual-draw kernels: rows kept per XCD
   int32_t gen;            // some row of the launch is general (row_class): the host picks
                           // the k_stream variant with the general rows' code
+  int32_t qskip;          // general-q verify without per-row tokens: k_finalize takes the
+                          // accept test, the residual draw serves first rejections only
   const uint32_t* mask;
   int64_t mask_stride;
   const int32_t* hist;

@@ -31,6 +31,19 @@ __device__ __forceinline__ int q_bin(float l, float m) {
 }
 
 // The draft distribution of draft row qr = b * k + j (k_qprep).
+// With a.qskip (only (accepted, token) asked for), k_finalize has taken every draft
+// row's accept test, and a row in phase QRES needs its residual draw only when every
+// earlier row of its sequence was accepted (the first rejection); the draws of later
+// rows are not read.
+__device__ __forceinline__ bool q_needed(const Args& a, int b, int j) {
+  if (!a.qskip) return true;
+  for (int q = 0; q < j; ++q) {
+    const RowState& rs = a.s.rs[(int64_t)b * (a.k + 1) + q];
+    if (rs.status != STRIM_OK || !rs.accept) return false;
+  }
+  return true;
+}
+
 __device__ __forceinline__ XQ q_of_row(const Args& a, int qr) {
   const QStat qs = a.s.qst[qr];
   XQ q;
@@ -310,7 +323,7 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   map_block(a, r, c);
   int b, j;
   row_bj(a, r, b, j);
-  if (a.s.rs[r].phase != PH_QRES) return;
+  if (a.s.rs[r].phase != PH_QRES || !q_needed(a, b, j)) return;
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE, qr = b * a.k + j;
   const RowParams p = load_params(a, b, j);
   const float m = a.s.rs[r].m;
@@ -405,7 +418,7 @@ __global__ __launch_bounds__(QGP_W * WAVE) void k_qgpick(Args a) {
   for (int j = w; j < a.k; j += QGP_W) {
     const int r = b * (a.k + 1) + j;
     RowState* rs = &a.s.rs[r];
-    const bool mine = rs->phase == PH_QRES;
+    const bool mine = rs->phase == PH_QRES && q_needed(a, b, j);
     if (lane == 0) s_mine[j] = mine ? 1 : 0;
     if (!mine) continue;
     const int qr = b * a.k + j;

@@ -77,25 +77,26 @@ def check_sample(ctx, x, params, dtype="bf16", mask=None, history=None, history_
 
 def run_verify(ctx, target, k, drafts, params, dtype="bf16", mask=None, history=None,
                history_len=None, noise_mode=O.NOISE_ICDF, noise=None, draft_logits=None,
-               table=None):
+               table=None, row_outputs=True):
     B = target.shape[0]
     out = ctx.verify(dev_logits(target.reshape(B, k + 1, -1), dtype),
                      dev(np.asarray(drafts, np.int32).reshape(B, k)), params,
                      draft_logits=None if draft_logits is None else dev_logits(draft_logits, dtype),
                      draft_to_full=dev(table, np.int32), mask=dev(mask),
                      history=dev(history, np.int32), history_len=dev(history_len, np.int32),
-                     noise_mode=noise_mode, noise=dev(noise, np.float32))
+                     noise_mode=noise_mode, noise=dev(noise, np.float32),
+                     row_outputs=row_outputs)
     torch.cuda.synchronize()
     return {k_: (None if v is None else v.cpu().numpy()) for k_, v in out.items()}
 
 
 def check_verify(ctx, target, k, drafts, params, dtype="bf16", mask=None, history=None,
                  history_len=None, noise_mode=O.NOISE_ICDF, noise=None, draft_logits=None,
-                 table=None, label=""):
+                 table=None, label="", row_outputs=True):
     th = host_logits(target, dtype)
     dlh = None if draft_logits is None else host_logits(draft_logits, dtype)
     g = run_verify(ctx, th, k, drafts, params, dtype, mask, history, history_len, noise_mode,
-                   noise, dlh, table)
+                   noise, dlh, table, row_outputs)
     ref = O.verify(th, k, np.asarray(drafts, np.int32).reshape(th.shape[0], k), params,
                    draft_logits=dlh, draft_to_full=table, mask=mask, history=history,
                    history_len=history_len, noise_mode=noise_mode, noise=noise)

@@ -423,10 +423,14 @@ def test_verify_error_after_rejection(ctx):
 def test_verify_general_q_cfg4(ctx, mode):
     # configuration 4: target [4,4,V] bf16, draft logits [4,3,32768] over an ascending
     # injective table, drafts sampled from q, T 0.7, Philox uniforms per position
+    # Without per-row outputs only (accepted, token) is computed: k_finalize takes the
+    # accept tests and the residual draw serves each sequence's first rejection alone.
     w = W.cfg4()
-    say(f"verify general-q cfg4 mode={mode}")
-    check_verify(ctx, w["target"], w["k"], w["drafts"], w["params"], "bf16", noise_mode=mode,
-                 draft_logits=w["draft_logits"], table=w["table"], label=f"cfg4 mode={mode}")
+    for rows in (True, False):
+        say(f"verify general-q cfg4 mode={mode} row_outputs={rows}")
+        check_verify(ctx, w["target"], w["k"], w["drafts"], w["params"], "bf16", noise_mode=mode,
+                     draft_logits=w["draft_logits"], table=w["table"],
+                     label=f"cfg4 mode={mode} rows={rows}", row_outputs=rows)
 
 
 @pytest.mark.parametrize("k", [1, 3])
@@ -458,10 +462,11 @@ def test_verify_general_q_random(ctx, k):
         hist = rng.integers(0, V, size=(B, 8)).astype(np.int32) if it == 2 else None
         if hist is not None:
             p["presence_penalty"] = 0.4
-        for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
-            say(f"verify general-q k={k} it={it} B={B} V={V} Vd={Vd} mode={mode}")
+        for mode, rows in ((O.NOISE_ICDF, True), (O.NOISE_GUMBEL, True), (O.NOISE_GUMBEL, False)):
+            say(f"verify general-q k={k} it={it} B={B} V={V} Vd={Vd} mode={mode} rows={rows}")
             check_verify(ctx, tgt, k, drafts, p, "bf16", mask, hist, None, mode,
-                         draft_logits=dl, table=table, label=f"general-q k={k} it={it}")
+                         draft_logits=dl, table=table, label=f"general-q k={k} it={it}",
+                         row_outputs=rows)
 
 
 def test_verify_general_q_table_errors(ctx):
