@@ -180,7 +180,10 @@ int strim_sample_noalloc(void* stream, const void* logits, int32_t dtype, int32_
  *   out_accepted  [B] leading accepted drafts n; out_token [B] the token decided at row n
  *                 (residual at the first rejection, bonus sample after k accepts).
  *   out_row_accept [B][k] / out_row_token [B][k+1] or NULL: per-row outcomes
- *                 (SpecSampling.rowOutcome). out_status [B] or NULL.
+ *                 (SpecSampling.rowOutcome). out_status [B] or NULL. With general-q
+ *                 drafts and Gumbel noise, out_row_token NULL lets the call draw the
+ *                 residual of each sequence's first rejected row only (the rows the
+ *                 result depends on); out_row_accept is filled for every row either way.
  * T <= 0 rows use the greedy rule: accept while argmax == draft (SpecStream.swift:269-273). */
 int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_t dtype,
                  int32_t B, int32_t k, int32_t V, const void* draft_logits, int32_t Vd,
