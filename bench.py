@@ -770,8 +770,9 @@ def main():
         st4 = torch.stack([c.status for c in calls4]).cpu().numpy()
         assert (st4 == 0).all(), f"verify status {st4}"
         kt4 = kernel_times(torch, ctx, calls4, 192, window=32)
-        # k_stream's share: the target rows (the draft logits and the table are k_qprep's)
-        bytes4 = B4 * (K4 + 1) * (V * 2 + 48 + 8)
+        # k_stream's launch: the target rows, and (its extra workgroups) the draft logits,
+        # the table and the draft values written at the table ids
+        bytes4 = B4 * (K4 + 1) * (V * 2 + 48 + 8) + B4 * K4 * VD4 * (2 + 4) + VD4 * 4
         log(f"[bench] cfg4 graph {us4:.2f} us/step; kernels (us): "
             + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt4.items()))
         result["cfg4"] = {

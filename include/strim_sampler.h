@@ -230,8 +230,9 @@ int strim_head_logits(void* stream, const void* hidden, int64_t hidden_stride, i
  * off. Profiling allocates its events in strim_profile_begin, never in the calls it
  * times. Do not profile calls that are being captured into a graph. */
 #define STRIM_KERNEL_COUNT 8 /* stream, finalize, gfinal, final, probs, verify_combine,
-                                qprep, qres (the five launches of the residual draw of
-                                unfiltered general-q rows, timed together) */
+                                qprep (no launches: the draft distributions run in the
+                                stream launch), qres (the launches of the residual draw
+                                of unfiltered general-q rows, timed together) */
 int strim_profile_begin(strim_ctx* ctx, int32_t max_launches);
 int strim_profile_end(strim_ctx* ctx, double* total_ms /* [STRIM_KERNEL_COUNT] */,
                       int64_t* launches /* [STRIM_KERNEL_COUNT] */);

@@ -20,7 +20,6 @@ hipError_t launch_head(const void* hidden, int64_t hidden_stride, int B, int K,
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
-__global__ void k_qprep(Args a);
 __global__ void k_qhist(Args a);
 __global__ void k_qpick(Args a);
 __global__ void k_qcollect(Args a);
@@ -160,6 +159,7 @@ void timed(strim_ctx* ctx, int kind, F launch) {
 // the chip and instructions per token decide. (Eight segments in one-wave workgroups
 // measured slower at B=64: 11.1 against 9.9 us.)
 constexpr int LARGE_ROWS = 32;
+int stream_threads(int rows) { return rows >= LARGE_ROWS ? stpb<4>() : stpb<1>(); }
 
 hipError_t launch_stream(const Args& a, dim3 grid, hipStream_t st, bool any_pen, hipEvent_t e0,
                          hipEvent_t e1) {
@@ -218,10 +218,12 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs,
   for (int i = 0; i < nb; ++i)
     if (row_class(a.p[i], a.V) == CLS_GENERAL) a.gen = 1;
   const dim3 grid_rc((unsigned)a.W, (unsigned)a.R);
+  // (general-q verify: the draft distributions' workgroups in extra grid rows)
+  const dim3 grid_st((unsigned)a.W, (unsigned)(a.R + (a.nqprep + a.W - 1) / a.W));
   hipError_t e = hipSuccess;
   auto keep = [&e](hipError_t x) { if (e == hipSuccess) e = x; };
   timed(ctx, KID_STREAM,
-        [&](hipEvent_t e0, hipEvent_t e1) { keep(launch_stream(a, grid_rc, st, any_pen, e0, e1)); });
+        [&](hipEvent_t e0, hipEvent_t e1) { keep(launch_stream(a, grid_st, st, any_pen, e0, e1)); });
   if (need_fin)
     timed(ctx, KID_FINALIZE, [&](hipEvent_t e0, hipEvent_t e1) {
       keep(launch_finalize(a, st, e0, e1));
@@ -553,15 +555,12 @@ int strim_verify(strim_ctx* ctx, void* stream, const void* target_logits, int32_
       if (a.dlog) {
         // draft distributions (QSPLIT workgroups per draft row; each draft row's
         // k_finalize workgroup merges its slices) and, with the first group, the
-        // draft-vocab bitmap (one thread per table entry). (On a second stream beside
-        // k_stream, joined by an event before k_finalize, a graph step took 4.6 us longer:
-        // the cross-queue dependencies cost more than the overlap saves.)
-        const int nwb = g0 == 0 ? (int)((Vd + QPT - 1) / QPT) : 0;
-        timed(ctx, KID_QPREP, [&](hipEvent_t e0, hipEvent_t e1) {
-          e = launch_args((const void*)k_qprep, dim3((unsigned)(nb * k * QSPLIT + nwb)),
-                          dim3(QPT), a, st, e0, e1);
-        });
-        if (e != hipSuccess) return STRIM_EHIP;
+        // draft-vocab bitmap (one thread per table entry), as extra workgroups of the
+        // k_stream launch (measured: a launch of their own before k_stream cost 9.7 us
+        // per step; on a second stream beside k_stream, joined by an event, 4.6 us more)
+        const int nt = stream_threads(rows);
+        const int nwb = g0 == 0 ? (int)((Vd + nt - 1) / nt) : 0;
+        a.nqprep = nb * k * QSPLIT + nwb;
       }
       bool combined = false;
       int rc = run_group(ctx, st, a, nb, false, &combined);

@@ -256,12 +256,13 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
       td = max(td, pp[q].td);
       bad |= a.s.qpp[q].bad;
     }
+    // Z = sum over the slices of z exp(m - mq): one slice per lane of wave 0
     double z = 0.0;
-    if (t == 0) {
-#pragma unroll
-      for (int q = 0; q < QSPLIT; ++q)
-        if (pp[q].m > -INFINITY) z += pp[q].z * exp((double)pp[q].m - (double)mq);
-      a.s.qst[qr] = QStat{mq, td, z};
+    if (w == 0) {
+      const QPart& pq = pp[lane < QSPLIT ? lane : 0];
+      z = wave_sum(lane < QSPLIT && pq.m > -INFINITY ? pq.z * exp((double)pq.m - (double)mq)
+                                                     : 0.0);
+      if (t == 0) a.s.qst[qr] = QStat{mq, td, z};
     }
     if (bad || td < 0) {
       finish_row(a, r, STRIM_EINVAL, -1, 0, 0.0, m, 0ull, PH_DONE);

@@ -103,7 +103,7 @@ struct QStat {
 };
 
 // k_qprep's partial result over one of the QSPLIT slices of a draft row's table.
-constexpr int QSPLIT = 8;
+constexpr int QSPLIT = 16;
 struct QPart {
   float m;      // slice maximum of v (-inf if empty)
   int32_t td;   // table index of the draft in the slice, -1 if absent
@@ -147,6 +147,8 @@ struct Args {
                           // the k_stream variant with the general rows' code
   int32_t qskip;          // general-q verify without per-row tokens: k_finalize takes the
                           // accept test, the residual draw serves first rejections only
+  int32_t nqprep;         // general-q verify: k_qprep blocks carried by the k_stream launch
+                          // (its grid rows past R)
   const uint32_t* mask;
   int64_t mask_stride;
   const int32_t* hist;

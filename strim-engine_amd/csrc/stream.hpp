@@ -15,7 +15,7 @@
 // segments) triple, each object holding that triple's launcher.
 #pragma once
 
-#include "select.hpp"
+#include "qprep.hpp"
 
 namespace strim {
 
@@ -161,7 +161,15 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   // read inside a branch would be its own scalar-load round trip
   asm volatile("" ::"s"(a.logits), "s"(a.row_stride), "s"(a.V), "s"(a.verify), "s"(a.k),
                "s"(a.hist), "s"(a.H), "s"(a.hist_len), "s"(a.mask), "s"(a.mask_stride),
-               "s"(a.s.cstat), "s"(a.s.wmax), "s"(a.W), "s"(a.R), "s"(a.xmap));
+               "s"(a.s.cstat), "s"(a.s.wmax), "s"(a.W), "s"(a.R), "s"(a.xmap),
+               "s"(a.nqprep));
+  // general-q verify: the workgroups past row R carry the draft distributions' work
+  // (qprep.hpp), independent of the chunks'
+  if (blockIdx.y >= (unsigned)a.R) {
+    const int blk = (int)((blockIdx.y - (unsigned)a.R) * gridDim.x + blockIdx.x);
+    if (blk < a.nqprep) qprep_block<STPB>(a, blk);
+    return;
+  }
   int r, c;
   map_block(a, r, c);
   int b, j;
