@@ -407,7 +407,7 @@ def summarize(d):
             acc.setdefault((kk, case), []).append(us)
         acc = {key: v for key, v in acc.items() if v}
         print("\nThe same trace per workload (a kernel belongs to the k_stream variant it "
-              "follows; k_qprep to the one after it; k_gmask to the grammar-mask timings, "
+              "follows; k_gmask to the grammar-mask timings, "
               "cache off, then cache on):\n")
         print("| kernel | workload | calls | avg us | median us |\n|---|---|---|---|---|")
         for (k, c), v in sorted(acc.items(), key=lambda t: (str(t[0][1]), t[0][0])):
