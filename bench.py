@@ -71,6 +71,63 @@ def make_pool_cfg2(torch, dev, n_sets, B, V, H, seed=2):
     return xs, hs, ns
 
 
+def make_masks_cfg3(torch, x, hist=None, presence=0.5, frequency=0.3, T=0.8, P=0.9,
+                    gen=None):
+    """cfg3's allow masks for one pool set, built from that set's own logits (the
+    workloads.py layout on the device): rows 0-3 clustered runs of 64 at densities
+    0.01 / 1 / 10 / 30 %, rows 4-5 scattered at 0.01 / 1 %, row B-2 allows exactly one
+    token, row B-1 masks the whole top-p nucleus of its own penalised logits at (T, P)
+    and allows 30 % of the other tokens at random. `hist` gives the penalty histories
+    (presence / frequency as the chain applies them); None for a chain without them.
+    Returns packed int32 words [B, ceil(V/32)]."""
+    from strim_amd.ops import pack_mask
+
+    B, V = x.shape
+    dev = x.device
+    dens = [0.0001, 0.01, 0.10, 0.30]
+    allowed = torch.zeros(B, V, dtype=torch.bool, device=dev)
+    for r in range(B):
+        d = dens[r % 4]
+        n = max(1, int(round(d * V)))
+        if (r // 4) % 2 == 0:  # clustered: seeded contiguous runs of 64
+            run = 64
+            starts = torch.randperm(V // run, device=dev, generator=gen)[: max(1, n // run)] * run
+            idx = (starts[:, None] + torch.arange(run, device=dev)[None, :]).reshape(-1)
+            allowed[r, idx] = True
+        else:  # scattered
+            allowed[r, torch.randperm(V, device=dev, generator=gen)[:n]] = True
+    # one row allows exactly one token
+    allowed[B - 2] = False
+    allowed[B - 2, int(torch.randint(0, V, (1,), device=dev, generator=gen))] = True
+    # one row's top-p nucleus (of its penalised logits at T, P) lies in masked tokens
+    r = B - 1
+    v = x[r].float()
+    if hist is not None:
+        c = torch.bincount(hist[r].long().clamp(0, V - 1), minlength=V)[:V].float()
+        hit = c > 0
+        v = torch.where(hit, (v - frequency * c) - presence, v)
+    l = (v / T).double()
+    order = torch.argsort(l, descending=True, stable=True)
+    w = torch.exp(l[order] - l[order[0]])
+    cum = torch.cumsum(w, 0) / w.sum()
+    cut = int(torch.searchsorted(cum, torch.tensor([P], dtype=cum.dtype, device=dev))) + 1
+    allowed[r] = torch.rand(V, device=dev, generator=gen) < 0.3
+    allowed[r, order[:cut]] = False
+    return pack_mask(allowed).contiguous()
+
+
+def make_pool_n1(torch, dev, n_sets, B, V, H, seed=6, penalties=True):
+    """The n1 (penalties=True) or cfg3 (False) pool: cfg2-shaped logits, histories and
+    uniforms, each set with its own cfg3 masks made from its own penalised logits, so
+    every set has an active one-token row and a row whose nucleus is masked."""
+    xs, hs, ns = make_pool_cfg2(torch, dev, n_sets, B, V, H, seed=seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1000)
+    ms = [make_masks_cfg3(torch, xs[i], hs[i] if penalties else None, gen=g)
+          for i in range(n_sets)]
+    return xs, hs, ns, ms
+
+
 def make_pool_cfg5(torch, dev, n_sets, B, V, H, seed=5):
     """cfg5-shaped inputs: 70 % rows N(0, 2^2), 30 % rows with one +20 logit; uniform
     2,048-token histories; 5 %-density allow masks."""
@@ -490,14 +547,17 @@ def pmc_pass(torch, ops, W, dev, steps, pool_mb):
             calls[i % len(calls)]()
         torch.cuda.synchronize()
 
-    n2 = int(np.ceil(pool_mb * 2**20 / (B * V * 2 + B * H * 4)))
-    xs, hs, ns = make_pool_cfg2(torch, dev, n2, B, V, H, seed=6)
+    n2 = int(np.ceil(pool_mb * 2**20 / (B * V * 2 + B * H * 4 + B * ((V + 31) // 32) * 4)))
     w1, w3 = W.n1(), W.cfg3()
-    m1 = torch.from_numpy(w1["mask"].view(np.int32)).to(dev)
-    m3 = torch.from_numpy(w3["mask"].view(np.int32)).to(dev)
-    run([ctx.bind_sample(xs[i], w1["params"], mask=m1, history=hs[i], history_len=hl,
+    # the same pools as the timed lines: every set carries masks made from its own logits
+    xs, hs, ns, ms = make_pool_n1(torch, dev, n2, B, V, H, seed=6)
+    run([ctx.bind_sample(xs[i], w1["params"], mask=ms[i], history=hs[i], history_len=hl,
                          noise=ns[i]) for i in range(n2)])
-    run([ctx.bind_sample(xs[i], w3["params"], mask=m3, noise=ns[i]) for i in range(n2)])
+    del xs, hs, ns, ms
+    xs, hs, ns, ms = make_pool_n1(torch, dev, n2, B, V, 1, seed=3, penalties=False)
+    run([ctx.bind_sample(xs[i], w3["params"], mask=ms[i], noise=ns[i]) for i in range(n2)])
+    del xs, hs, ns, ms
+    xs, hs, ns = make_pool_cfg2(torch, dev, n2, B, V, H, seed=2)
     run([ctx.bind_sample(xs[i], W.cfg2()["params"], history=hs[i], history_len=hl,
                          noise=ns[i]) for i in range(n2)])
     del xs, hs, ns
@@ -625,13 +685,14 @@ def main():
 
     # ---- headline: the north-star chain (penalties + grammar masks + top-p) ----------
     w1 = W.n1()
-    per_set = B * V * 2 + B * H * 4 + B * 8
+    per_set = B * V * 2 + B * ((V + 31) // 32) * 4 + B * H * 4 + B * 8
     n_sets = int(np.ceil(args.pool_mb * 2**20 / per_set))
     log(f"[bench] n1 pool: {n_sets} sets x {per_set / 2**20:.2f} MiB")
-    xs, hs, ns = make_pool_cfg2(torch, dev, n_sets, B, V, H, seed=6)
-    m1 = torch.from_numpy(w1["mask"].view(np.int32)).to(dev)
+    # every set has its own masks, made from its own penalised logits: the one-token row
+    # and the masked-nucleus row are active in every step
+    xs, hs, ns, ms = make_pool_n1(torch, dev, n_sets, B, V, H, seed=6)
     hl = torch.full((B,), H, dtype=torch.int32, device=dev)
-    calls = [ctx.bind_sample(xs[i], w1["params"], mask=m1, history=hs[i], history_len=hl,
+    calls = [ctx.bind_sample(xs[i], w1["params"], mask=ms[i], history=hs[i], history_len=hl,
                              noise=ns[i]) for i in range(n_sets)]
     for i in range(args.warmup):
         calls[i % n_sets]()
@@ -648,7 +709,8 @@ def main():
     bytes1 = W.algorithmic_bytes(B, V, 2, mask=True, H=H, noise_floats=2)
     log(f"[bench] n1 graph {us1:.2f} us/step median of {len(per1)} replays (eager {eg1:.2f}); "
         "kernels (us): " + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt1.items()))
-    del xs, hs, ns, calls
+    m1 = ms[0]  # kept for the logits-producer line
+    del xs, hs, ns, ms, calls
     torch.cuda.empty_cache()
 
     result = {
@@ -664,12 +726,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 logits; f32 processing, f64 decisions",
-        "data": f"synthetic (seeded N(0,2.5^2)+Zipf bias logits, Zipf histories, the n1 "
-                f"grammar masks), rotating {n_sets}-set pool > 512 MB",
+        "data": f"synthetic (seeded N(0,2.5^2)+Zipf bias logits, Zipf histories, cfg3 "
+                f"grammar masks made per set from its own penalised logits), rotating "
+                f"{n_sets}-set pool > 512 MB",
         "config": {"workload": "n1 north-star chain: B=8 V=151936 bf16, presence 0.5 + "
                                "frequency 0.3 over a 4096-id history, packed grammar masks "
                                "(0.01-30% density, clustered and scattered, a one-token row, "
-                               "a masked-nucleus row), T 0.8, top-p 0.9, icdf draw",
+                               "a row whose top-p nucleus is masked; every pool set's masks "
+                               "made from its own logits), T 0.8, top-p 0.9, icdf draw",
                    "B": B, "V": V, "history": H,
                    "timing": f"hip-graph replay, median of {len(per1)} replays "
                              f"({k1} steps timed, at least {MIN_TIMED_STEPS})"},
@@ -682,10 +746,9 @@ def main():
     if not args.no_extra:
         # ---- cfg3: masks + top-p, no penalties ----------------------------------------
         w3 = W.cfg3()
-        n3 = int(np.ceil(args.pool_mb * 2**20 / (B * V * 2)))
-        xs3, _, ns3 = make_pool_cfg2(torch, dev, n3, B, V, 1, seed=3)
-        m3 = torch.from_numpy(w3["mask"].view(np.int32)).to(dev)
-        calls3 = [ctx.bind_sample(xs3[i], w3["params"], mask=m3, noise=ns3[i])
+        n3 = int(np.ceil(args.pool_mb * 2**20 / (B * V * 2 + B * ((V + 31) // 32) * 4)))
+        xs3, _, ns3, ms3 = make_pool_n1(torch, dev, n3, B, V, 1, seed=3, penalties=False)
+        calls3 = [ctx.bind_sample(xs3[i], w3["params"], mask=ms3[i], noise=ns3[i])
                   for i in range(n3)]
         us3, k3, per3 = graph_median(torch, calls3, args.steps, 20)
         kt3 = kernel_times(torch, ctx, calls3, 480)
@@ -693,13 +756,13 @@ def main():
             + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt3.items()))
         result["cfg3"] = {
             "workload": "cfg3: B=8 bf16 + packed allow masks (0.01-30% density, clustered and "
-                        "scattered, a one-token row, a row whose nucleus is masked), T 0.8, "
-                        "top-p 0.9, icdf",
+                        "scattered, a one-token row, a row whose nucleus is masked; every "
+                        "pool set's masks made from its own logits), T 0.8, top-p 0.9, icdf",
             "us_per_step": round(us3, 3), "steps": k3,
             "roofline": roofline(W.algorithmic_bytes(B, V, 2, mask=True, noise_floats=2),
                                  kt3["k_stream"][0], traffic.get(("k_stream", "cfg3"))),
             "kernel_us": {k: round(v[0], 3) for k, v in kt3.items()}}
-        del xs3, ns3, calls3
+        del xs3, ns3, ms3, calls3
         # ---- cfg2: heterogeneous rows, penalties, min-p -------------------------------
         w2 = W.cfg2()
         n2 = int(np.ceil(args.pool_mb * 2**20 / per_set))
@@ -770,16 +833,18 @@ def main():
         st4 = torch.stack([c.status for c in calls4]).cpu().numpy()
         assert (st4 == 0).all(), f"verify status {st4}"
         kt4 = kernel_times(torch, ctx, calls4, 192, window=32)
-        # k_stream's launch: the target rows, and (its extra workgroups) the draft logits,
-        # the table and the draft values written at the table ids
-        bytes4 = B4 * (K4 + 1) * (V * 2 + 48 + 8) + B4 * K4 * VD4 * (2 + 4) + VD4 * 4
+        # the step's algorithmic bytes: target rows, draft logits, the index table, and per
+        # sequence its params, drafts and outputs (the k_stream launch reads all of the
+        # inputs: its extra workgroups take the draft logits and the table)
+        bytes4 = (B4 * (K4 + 1) * V * 2 + B4 * K4 * VD4 * 2 + VD4 * 4
+                  + B4 * (48 + 4 * K4 + 8))
         log(f"[bench] cfg4 graph {us4:.2f} us/step; kernels (us): "
             + ", ".join(f"{k}={v[0]:.2f}" for k, v in kt4.items()))
         result["cfg4"] = {
             "workload": "cfg4: general-q verify B=4 k=3 V=151936 bf16, draft logits "
                         "[4,3,32768] bf16 + ascending table, T 0.7, Philox Gumbel",
             "us_per_step": round(us4, 3), "steps": k4,
-            "roofline": roofline(bytes4, kt4["k_stream"][0]),
+            "roofline": roofline(bytes4, kt4["k_stream"][0], traffic.get(("k_stream", "cfg4"))),
             "kernel_us": {k: round(v[0], 3) for k, v in kt4.items()}}
         # ---- the reference's verify: one-hot drafts, Gumbel noise (graph) -----------------
         calls4o = [ctx.bind_verify(ts4[i], dr4[i], p4, noise_mode=1) for i in range(n4)]
@@ -797,25 +862,36 @@ def main():
             "kernel_us": {k: round(v[0], 3) for k, v in kt4o.items()}}
         del ts4, ds4, dr4, calls4, calls4o
         torch.cuda.empty_cache()
-        # ---- a wide nucleus below the candidates: the exact resolution -------------------
-        # (the n1 configuration's own logits: its masked-nucleus row's top-p cut lies below
-        # the chunks' candidates, so k_gfinal resolves that row by streaming passes)
-        xw = torch.from_numpy(W.bf16_bits(w1["x"]).view(np.int16)).view(torch.bfloat16).to(dev)
-        hw = torch.from_numpy(w1["history"]).to(dev)
-        nw = torch.from_numpy(w1["noise"]).to(dev)
-        callsw = [ctx.bind_sample(xw, w1["params"], mask=m1, history=hw, history_len=hl,
-                                  noise=nw)]
-        usw, kw, _ = graph_median(torch, callsw, min(args.steps, MIN_TIMED_STEPS), 20)
-        ktw = kernel_times(torch, ctx, callsw, 96)
-        log(f"[bench] wide-nucleus n1 inputs graph {usw:.2f} us/step; kernels (us): "
+        # ---- wide nuclei: rows whose kept set is wider than the chunks' candidates ----
+        # B=8 rows of N(0,1) logits at T 1.0: seven with top-p 0.95 (a nucleus of tens of
+        # thousands of tokens) and one unfiltered (its icdf draw ranges over the whole
+        # vocabulary); a rotating pool, so the logits stream from HBM
+        nwd = int(np.ceil(args.pool_mb * 2**20 / (B * V * 2)))
+        gw = torch.Generator(device=dev)
+        gw.manual_seed(21)
+        xws = [torch.randn(B, V, device=dev, generator=gw).to(torch.bfloat16).contiguous()
+               for _ in range(nwd)]
+        nws = [torch.rand(B, 2, device=dev, generator=gw) for _ in range(nwd)]
+        pw = W.params_array(B, temperature=1.0, top_p=[0.95] * (B - 1) + [1.0],
+                            seed=np.arange(B, dtype=np.uint64) + 90, position=17)
+        callsw = [ctx.bind_sample(xws[i], pw, noise=nws[i]) for i in range(nwd)]
+        for c in callsw[:2]:
+            c()
+        torch.cuda.synchronize()
+        usw, kw, _ = graph_median(torch, callsw, min(args.steps, MIN_TIMED_STEPS), 2)
+        stw = torch.stack([c.out_status for c in callsw]).cpu().numpy()
+        assert (stw == 0).all(), f"wide-nucleus status {stw}"
+        ktw = kernel_times(torch, ctx, callsw, 96, window=16)
+        log(f"[bench] wide nuclei graph {usw:.2f} us/step; kernels (us): "
             + ", ".join(f"{k}={v[0]:.2f}" for k, v in ktw.items()))
         result["wide_nucleus"] = {
-            "workload": "the n1 chain on its own seeded inputs (one set, cache-resident): its "
-                        "masked-nucleus row keeps more tokens than the chunks' candidates "
-                        "cover, so that row takes the exact streaming resolution",
+            "workload": "B=8 V=151936 bf16 N(0,1) logits, T 1.0: 7 rows top-p 0.95 (nuclei of "
+                        "tens of thousands of tokens) and 1 unfiltered row, icdf draw; "
+                        f"rotating {nwd}-set pool > 512 MB",
             "us_per_step": round(usw, 3), "steps": kw,
             "kernel_us": {k: round(v[0], 3) for k, v in ktw.items()}}
-        del xw, hw, nw, callsw
+        del xws, nws, callsw
+        torch.cuda.empty_cache()
         result["head"] = head_bench(torch, ops, dev, ctx, args, w1, m1, hl)
         result["grammar_masks"] = grammar_mask_bench(torch, dev, args)
     ctx.close()

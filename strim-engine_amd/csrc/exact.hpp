@@ -229,6 +229,9 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, int b, int j,
           }
         }
         fn(i0, l, qv);
+        // every wave has read this window's counts before the next window's hist_count
+        // clears them (its first step runs before its own barrier)
+        if constexpr (PEN) __syncthreads();
       }
       issue(sl[d], w + d + XPD);
     }

@@ -172,6 +172,8 @@ struct Args {
   strim_sampling_params p[MAXP];  // per batch row of the group
   double lmp[MAXP];               // log(min_p) per batch row (host libm), -inf when off
 };
+// The block is passed by value: it must fit the 4 KB kernel-argument segment.
+static_assert(sizeof(Args) <= 4096, "Args exceeds the 4 KB kernel-argument limit");
 
 // Launches kernel `fn(Args)` on st. Given a start/stop event pair, the events take the
 // dispatch's own begin and end timestamps (hipExtLaunchKernel), so their elapsed time is

@@ -663,7 +663,11 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       // (a token it did not keep) reaching the chunk's bound sends the row to the exact
       // resolution (STRIM flag 8).
       auto tol = [](float x) { return 2e-5f + 1e-6f * fabsf(x); };
-      float w0 = s0, wl0 = l0, w1 = s1, wl1 = l1, w2 = s2;
+      // A lane's third is not tracked in the token loop: its second score stands in as
+      // the bound. When one lane holds both of the wave's winners, that bound opens the
+      // near-tie gate and the lanes' exact thirds are recomputed below, so w2 is always
+      // at least the best score the wave leaves out.
+      float w0 = s0, wl0 = l0, w1 = s1, wl1 = l1, w2 = s1;
       int wi0 = id0, wi1 = id1;
       wave_top2(w0, wl0, wi0, w1, wl1, wi1, &w2);
       float wov = -INFINITY;

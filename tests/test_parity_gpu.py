@@ -87,9 +87,11 @@ def test_sweep_large_batch(ctx, V):
 
 @pytest.mark.parametrize("H", [300, 4096, 8192, 9000])
 def test_large_batch_long_histories(ctx, H):
-    # Launches of 32 rows or more group each row's history by chunk first (up to 8,192
-    # ids); a longer history scans per chunk. Zipf-skewed ids put hundreds of ids in one
-    # chunk's group; ids out of range and lengths below H are dropped.
+    # Launches of 32 rows or more run four 8-token segments per thread. Every chunk's
+    # workgroup counts the row's history ids that fall inside it: the first 4,096 ids from
+    # registers loaded before the logits, a longer history's rest read in a loop.
+    # Zipf-skewed ids put hundreds of ids in one chunk; ids out of range and lengths
+    # below H are dropped.
     rng = np.random.default_rng(4000 + H)
     B, V = 36, 20000
     x = rng.normal(0, 2.0, size=(B, V)).astype(np.float32)
@@ -628,3 +630,67 @@ def test_gumbel_unfiltered_near_ties(ctx):
     say("gumbel near ties verify")
     check_verify(ctx, xt, k, drafts, p, "f32", noise_mode=O.NOISE_GUMBEL, noise=nv,
                  label="gumbel-near-verify")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_exact_resolution_penalised_aligned(ctx, dtype):
+    # Aligned rows with penalties whose nucleus is wider than both candidate tiers, so the
+    # exact streaming resolution decides them. Its windows rebuild the history counts in
+    # LDS one after another; the history ids carry a +6 logit that their penalty takes off
+    # again, so a window that lost a count would move most of the row's mass.
+    rng = np.random.default_rng(75)
+    B, V, H = 8, W.V_DEFAULT, 4096
+    x = rng.normal(0, 0.3, size=(B, V)).astype(np.float32)
+    hist = np.stack([rng.choice(V, size=H, replace=False) for _ in range(B)]).astype(np.int32)
+    hist[:, H // 2:] = hist[:, : H // 2]  # every id twice
+    for r in range(B):
+        x[r, hist[r]] += 6.0
+    p = O.make_params(B, temperature=np.float32(1.0),
+                      top_p=np.array([0.95, 0.9, 0.99, 0.8, 0.95, 0.97, 0.85, 0.9], np.float32),
+                      frequency_penalty=np.float32(2.0), presence_penalty=np.float32(2.0),
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                      position=np.arange(B, dtype=np.uint64))
+    for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+        say(f"exact penalised aligned dtype={dtype} mode={mode}")
+        check_sample(ctx, x, p, dtype, None, hist, None, mode, None, probs=False,
+                     label="exact-pen")
+    k = 2
+    xt = np.repeat(x[:, None, :], k + 1, axis=1)
+    drafts = hist[:, :k].copy()
+    say(f"exact penalised aligned verify dtype={dtype}")
+    check_verify(ctx, xt, k, drafts, p, dtype, None, hist, None, O.NOISE_ICDF, None,
+                 label="exact-pen-verify")
+
+
+def _gumbel_u(g):
+    # the uniform whose Gumbel transform -log(-log u) is g
+    return np.float32(np.exp(-np.exp(-np.float64(g))))
+
+
+def test_gumbel_three_near_ties_one_lane(ctx):
+    # Unfiltered Gumbel rows whose three best scores lie in one 8-token segment (one lane)
+    # within a few 1e-6 of each other, and every other score far below: the lane holds
+    # both of its wave's winners and the third near tie, which must still reach the fp64
+    # decision. Sample, and verify with a rejected draft (the residual decides).
+    rng = np.random.default_rng(76)
+    B, V, k = 32, W.V_DEFAULT, 1
+    x = np.full((B, V), -12.0, np.float32)
+    noise = rng.random((B, V + 1), dtype=np.float32)
+    for r in range(B):
+        seg = 8 * int(rng.integers(0, V // 8))
+        pos = seg + rng.choice(8, size=3, replace=False)
+        x[r, pos] = 30.0
+        gaps = np.array([0.0, 1.5e-6, 3.0e-6])[rng.permutation(3)]
+        for q in range(3):
+            noise[r, pos[q]] = _gumbel_u(0.4 + gaps[q])
+    p = O.make_params(B, temperature=np.float32(1.0), position=7,
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64))
+    say("gumbel three near ties in one lane: sample")
+    check_sample(ctx, x, p, "f32", noise_mode=O.NOISE_GUMBEL, noise=noise, probs=False,
+                 label="gumbel-3near")
+    xt = np.repeat(x[:, None, :], k + 1, axis=1)
+    drafts = np.zeros((B, k), np.int32)
+    nv = np.repeat(noise[:, None, :], k + 1, axis=1).copy()
+    say("gumbel three near ties in one lane: verify")
+    check_verify(ctx, xt, k, drafts, p, "f32", noise_mode=O.NOISE_GUMBEL, noise=nv,
+                 label="gumbel-3near-verify")
