@@ -57,7 +57,7 @@ constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // Byte offsets of the scratch buffers of R rows of up to max_vocab tokens, each 256-byte
 // aligned. The general-q verify buffers (dbits .. qpp) are sized only when `verify`.
 struct ScratchLayout {
-  size_t cstat, slot, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp, bytes;
+  size_t cstat, slot, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp, lat, bytes;
 };
 constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) {
   const size_t wmax = (max_vocab + CHUNK - 1) / CHUNK;
@@ -79,6 +79,7 @@ constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) 
   L.qhm = off; off = align_up(off + RQ * wmax * QNB * sizeof(unsigned long long), 256);
   L.qst = off; off = align_up(off + RV * sizeof(QStat), 256);
   L.qpp = off; off = align_up(off + RQ * QSPLIT * sizeof(QPart), 256);
+  L.lat = off; off = align_up(off + R * wmax * NBW * sizeof(unsigned long long), 256);
   L.bytes = off;
   return L;
 }
@@ -93,6 +94,7 @@ Scratch scratch_at(char* base, const ScratchLayout& L, size_t max_vocab, bool ve
   s.rs = (RowState*)(base + L.rs);
   s.cand = (Cand*)(base + L.cand);
   s.ncand = (uint32_t*)(base + L.nc);
+  s.lat = (unsigned long long*)(base + L.lat);
   if (verify) {
     s.dbits = (uint32_t*)(base + L.dbits);
     s.vq = (float*)(base + L.vq);

@@ -1,191 +1,447 @@
-// gfinal_kernels.hip — k_gfinal: the general rows, decided from the chunks' candidates.
+// gfinal_kernels.hip — k_gfinal: the general rows, decided from the chunks' lattice
+// histograms and candidates.
 //
 // A general row (top-p alone, a top-k above KLOC, a min-p below MINP_FAST, no filter with
-// icdf noise) cannot bound its candidates by a chunk's own maximum. k_stream keeps every
-// token with l > cs.g of its chunk as a candidate (at most GCAP per chunk, in the chunk's
-// slot region as (l, id)), so with G the largest cs.g of the row every token with l > G
-// is a candidate: the order, the masses and the cumulative sums of the row above G are
-// known exactly. When every decision of the row (the k-th token, the top-p cut, the draw)
-// lies above G, one workgroup takes them from the candidates alone. Otherwise the row
-// deepens once: k_stream also keeps a second tier of up to GCAP2 tokens per chunk below
-// the first, with its own bound cs.g2, and the decisions run again over both tiers above
-// G2 = max cs.g2. A row that still falls short (a nucleus wider than both tiers, a flat
-// row) is resolved by the exact streaming resolution (exact.hpp) in the same workgroup.
-// The first tier is kept small (GCAP = 32 per chunk decides the common rows: a nucleus up
-// to a few hundred tokens) because every candidate of a round costs LDS atomics and
-// stores on the one CU the row runs on.
+// icdf noise) cannot bound its candidates by a chunk's own maximum. k_stream bins every
+// general row's tokens on one absolute lattice of l, A(l) = floor(l * LBS): a chunk keeps
+// the counts and masses of the NBW bins below its top bin A(m_c) (its window) and writes
+// its window tokens in bin order, as many whole bins as fit LCAP slots (nfull bins). Since
+// every chunk bins the same way, row bin rb = A(m) - A(l) below the row's maximum m
+// collects chunk c's bin rb - d_c, d_c = A(m) - A(m_c): the chunks' histograms add up to
+// the row's, and every decision of the row (the k-th token, the min-p bound, the top-p
+// cut, the icdf draw) is found in two steps:
+//   1. the row bin where the cumulative count or mass crosses the decision's threshold;
+//   2. the bin's tokens (its zone), gathered from the chunks' slot regions (each chunk's
+//      part of the bin is a contiguous run there) and resolved exactly in (l desc, id asc)
+//      order, each token's mass taken from its own l.
+// A zone in a bin that some chunk could not write whole is collected by one streaming
+// pass of this workgroup over the row. A decision below a chunk's window (the lattice
+// cannot place it), rank-indexed noise and rows whose lattice words were not written take
+// the exact streaming resolution (exact.hpp).
 //
-// One 512-thread workgroup per row (eight waves: 1,024 threads measured 1.4 us slower on
-// its merges and barriers, 256 slower on its per-thread loops); each thread holds up to
-// GNE candidates in registers:
-//   1. the chunk statistics and every candidate slot are loaded together (the slots of
-//      a region past its count are read and dropped, so nothing waits for the counts);
-//      the waves' maxima, flags, bounds and chunk mass sums are merged with one barrier;
-//   2. the candidates above G are binned by d = m - l into GNB bins. A bin is one 64-bit
-//      word, count << 49 | mass, so each candidate costs one LDS atomic (they run about
-//      one lane per cycle, so their number sets this step's time), and the atomic's old
-//      count is the candidate's place in its bin. Masses are fixed point,
-//      round(2^35 * expf(l - m)): integer sums make every cumulative mass independent of
-//      summation order, 8192 unit masses stay below 2^48, and the per-token error (the
-//      float exp's 2^-23 relative plus 2^-36 absolute) keeps any cumulative mass within
-//      5e-7 relative of the exact one, inside the 1e-6 decision tolerance. Each wave turns
-//      its 64 bins into inclusive prefixes (a bin's cumulative count or mass is its
-//      group's prefix plus the totals of the groups before it), and every candidate is
-//      stored with its mass in bin order;
-//   3. the decisions run in order (the k-th token, the top-p cut, the icdf draw) through
-//      one loop, so their shared code is fetched once: each finds the bin where its
-//      threshold is crossed from the prefixes, and each key of that bin counts the bin's
-//      keys before it in order; the key whose interval contains the threshold is the
-//      decision (one barrier per decision). A Gumbel draw scores every kept candidate.
-// The kernel's time is latency (dependent steps, barriers and the first fetch of its
-// code), so the code is kept short: loops that run once per decision are not repeated
-// per decision.
+// Masses are fixed point, 2^40 per unit of exp(l - m) (RFIX): integer sums make every
+// cumulative mass independent of summation order. A chunk's bin masses (2^37 per unit of
+// exp(l - m_c), from float exponentials) are scaled by exp(m_c - m) once per (chunk, bin);
+// a zone token's mass is expf(l - m) 2^40. Both are within a few 1e-7 relative of the
+// exact mass, inside the 1e-6 decision tolerance.
+//
+// One 512-thread workgroup per row. Its time is latency (one global round trip for the
+// chunk statistics and lattice words, then one per zone), so the loads that do not depend
+// on the row's parameters are issued first, and every wave keeps the row's cumulative
+// histogram in its own registers (a decision's bin search needs no barrier).
 #include "exact.hpp"
 
 namespace strim {
 
-constexpr int GT = 512;             // threads of a k_gfinal workgroup
-constexpr int GW = GT / WAVE;       // its waves; wave w owns the histogram bins of group w
-constexpr int GNE = 4;              // candidate slots per thread: W * GCAP <= GT * GNE
-constexpr int GNE2 = 12;            // second-tier slots per thread: W * GCAP2 <= GT * GNE2
-constexpr int GCAND = 8192;         // candidates of a row held in bin order (both tiers)
-constexpr int GNB = GW * WAVE;      // histogram bins of d = m - l (64 per group)
-constexpr int GZCAP = GT;           // keys of one bin a decision resolves (one per thread)
-constexpr double GFIX = 34359738368.0;  // 2^35: the fixed-point unit of mass
-constexpr int GCSH = 49;                // a bin word: count << GCSH | mass
-constexpr uint64_t GMMASK = (1ull << GCSH) - 1ull;
-constexpr int GSH = __builtin_ctz(GCAP), GSH2 = __builtin_ctz(GCAP2);  // region of entry e: e >> GSH
-static_assert((1 << GSH) == GCAP && (1 << GSH2) == GCAP2, "tier sizes are powers of two");
-static_assert(GT % GCAP == 0 && GT % GCAP2 == 0, "whole regions per pass of the workgroup");
-static_assert(GT * GNE >= 64 * GCAP, "the first tier of 64 chunks fits the slots");
-static_assert(GT * (GNE + GNE2) <= GCAND, "a second round fits the bin-order arrays");
-static_assert(GNB == GT, "one bin per thread to clear");
+constexpr int GT = 512;                          // threads of a k_gfinal workgroup
+constexpr int GW = GT / WAVE;                    // its waves
+constexpr int LPL = NBW / WAVE;                  // row bins per lane (bins LPL lane + q)
+constexpr float RFIXF = 1099511627776.0f;        // 2^40: fixed-point unit of row mass
+constexpr double RFIX = 1099511627776.0;
+constexpr int ZCAP = 4096;                       // keys of one zone
+constexpr int ZQ = ZCAP / GT;                    // zone positions per thread (sorted zones)
+constexpr int PF = 160;                          // candidates of each chunk prefetched
+// The lattice words and the prefetched candidates are loaded straight into LDS, 1 KB per
+// wave instruction (16 bytes per lane): KW and KP instructions per wave.
+constexpr int LWB = LWMAX * NBW * 8, PFB = LWMAX * PF * 8;  // their bytes
+constexpr int KW = (LWB / 1024 + GW - 1) / GW, KP = (PFB / 1024 + GW - 1) / GW;
+static_assert(LWB % 1024 == 0 && PFB % 1024 == 0, "whole 1 KB blocks");
+static_assert(PF <= LCAP && PF % 2 == 0, "prefetch layout");
+constexpr int NOBIN = 1 << 20;                   // "no bin": beyond every window
+static_assert(NBW % WAVE == 0 && LWMAX % GW == 0 && LWMAX <= WAVE, "lattice layout");
+static_assert(LCAP <= SLOT && LCAP < 65536, "the candidates fit a chunk's slot region");
 
-// LDS of one k_gfinal workgroup.
-struct GFinalShared {
-  union {
-    struct {                  // the decision from the candidates
-      uint64_t bkey[GCAND + WAVE];   // the candidates above G in bin order (64 KB; the
-                                     // last WAVE entries take the writes of empty slots)
-      uint64_t bmass[GCAND + WAVE];  // their fixed-point masses
-    };
-    struct {                  // the exact streaming resolution (rows decided at or below G)
-      uint64_t xkey[XB > XCOL ? XB : XCOL];
-      uint32_t xhc[XB];
-      uint32_t xcnt[GT * EPT];
-      uint64_t xu2[2 * GT / WAVE];
-      XState x;
-    };
-  };
-  uint64_t hist[GNB];         // per bin count << GCSH | mass, then the group-local
-                              // inclusive prefix
-  uint64_t gt[GW];            // per group: its total
-  uint32_t rcnt[GT];          // per chunk: its candidates
-  uint32_t rcnt2[GT];         // per chunk: its second-tier candidates
-  float v[GW], g[GW], g2[GW];
+// LDS of one k_gfinal workgroup: the two large areas the lattice words and candidates are
+// loaded into (objects of their own: the loads into them are then known not to touch the
+// small state, so reading the chunk statistics does not wait for them), and the rest.
+union GBig {
+  uint64_t E[LWMAX * NBW];        // the chunks' lattice words (until they are merged)
+  struct {                        // a zone: its keys and their masses
+    uint64_t zkey[ZCAP];
+    uint64_t zmass[ZCAP];
+  } z;
+  struct {                        // the exact streaming resolution
+    uint64_t xkey[XB > XCOL ? XB : XCOL];
+    uint32_t xhc[XB];
+    uint32_t xcnt[GT * EPT];
+    uint64_t xu2[2 * GT / WAVE];
+    XState x;
+  } x;
+};
+union GPf {
+  Cand pfb[LWMAX * PF];           // each chunk's first PF candidates (prefetched)
+  uint32_t ccnt[GT * EPT];        // a collect pass: history counts of one window (the
+};                                // prefetched candidates are dropped by then)
+// A step of the decision loop, as the leader wave posts it to the workgroup.
+enum { GOP_PICK = 0, GOP_SUM = 1, GOP_SKIP = 2, GOP_BOUND = 3, GOP_FAIL = 4 };
+struct GCmd {
+  int op;           // GOP_*: pick a key, sum the zone's masses up to a bound, skip the
+                    // step, only set the bound, or leave the row to the exact resolution
+  int load;         // the zone to load first: 0 none (in LDS), 1 from the chunks' parts
+                    // (zpo / zpc / zpz), 2 by a collect pass
+  int bz, also;     // the step's bin; the bin loaded beside it (-1: none)
+  int n0, n1;       // the loaded bins' key counts
+  int by_mass, excl;
+  double thr;
+  uint64_t bnd, c0, m0, bmp;
+};
+struct GFinalShared {  uint16_t pc[LWMAX][NBW];        // per chunk: inclusive count prefix of its window bins
+  uint32_t rc[NBW];               // row bins: counts
+  unsigned long long rm[NBW];     // row bins: masses (RFIX per unit of exp(l - m))
+  float mch[LWMAX];               // per chunk: its maximum
+  int nbch[LWMAX], nfch[LWMAX];   // per chunk: window bins written, bins written whole
+  int ncnt[LWMAX];                // per chunk: allowed tokens
+  int dch[LWMAX];                 // per chunk: its top bin's distance below the row's
+  double sch[LWMAX];              // per chunk: its mass sum relative to the row maximum
+  int zoff[LWMAX + 1];            // the Gumbel walk: exclusive offsets of the chunks' parts
+  float v[GW];
   int i[GW], f[GW];
-  double sw[GW];              // per wave: its chunks' mass, relative to the row maximum
   double d[GW];
-  uint64_t u[GW];
-  int misc[8];
-  uint64_t res[2][4];         // a decision: key, count before, mass before, mass (two slots,
-  int32_t tag[2];             // alternating; tag = the decision's number when it holds one)
+  uint64_t u[GW], u2[2 * GW];
+  int ii[GW];
+  int misc[8];                    // 0 rowfull, 1 rowwin, 2 collect count, 3 some tail
+  uint64_t res[2][4];             // a pick: key, count before, mass before, mass (two
+  int32_t tag[2];                 // slots, alternating; tag = the pick's number)
+  int zpo[2][LWMAX], zpc[2][LWMAX], zpz[2][LWMAX];  // a zone's parts per chunk: first
+                                                    // slot, count, place in the zone
+  GCmd cmd;                       // the decision loop's current step
+  uint32_t prk[GT];               // a pick: each zone key's rank and the mass before it
+  unsigned long long pmb[GT];
 };
 
-// Fixed-point mass of a token: round(2^35 * exp(l - m)), from the float exp of the
-// float difference (l <= m).
-__device__ __forceinline__ uint64_t gmass(float l, float m) {
-  return (uint64_t)(expf(l - m) * 34359738368.0f + 0.5f);
-}
-__device__ __forceinline__ int gbin(float m, float l, float hscale) {
-  return (int)fminf((m - l) * hscale, (float)(GNB - 1));
-}
 __device__ __forceinline__ float key_l(uint64_t k) { return fkey_desc_inv((uint32_t)(k >> 32)); }
-
-// Cumulative bin word (count << GCSH | mass) of bins 0 .. b, from the group-local
-// prefixes and `ginc`, lane g's inclusive prefix of the group totals (b is wave-uniform).
-__device__ __forceinline__ uint64_t gcum(const GFinalShared& S, uint64_t ginc, int b) {
-  if (b < 0) return 0ull;
-  const int g = b / WAVE;
-  const uint64_t before = g > 0 ? rl_u64(ginc, g - 1) : 0ull;
-  return before + S.hist[b];
+// Fixed-point mass of a token relative to the row maximum m (l <= m).
+__device__ __forceinline__ uint64_t rmass(float l, float m) {
+  return (uint64_t)(expf(l - m) * RFIXF);
 }
-__device__ __forceinline__ uint64_t wcount(uint64_t x) { return x >> GCSH; }
-__device__ __forceinline__ uint64_t wmass(uint64_t x) { return x & GMMASK; }
-
-// The first bin whose cumulative count or mass, less excl_w from bin excl_b on, exceeds
-// thr, among the bins before bb; bb when none does (every wave computes the same bin).
-__device__ __forceinline__ int gfind_bin(const GFinalShared& S, bool mass, uint64_t ginc,
-                                         double thr, int bb, uint64_t excl_w, int excl_b) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  auto val = [&](uint64_t x, bool ex) -> uint64_t {
-    return mass ? wmass(x) - (ex ? excl_w : 0ull) : wcount(x);
-  };
-  // the first group whose cumulative total (with the exclusion) exceeds thr
-  const uint64_t gv = val(ginc, excl_b <= WAVE * lane + WAVE - 1);
-  const uint64_t gh = __ballot(lane < GW && (double)gv > thr);
-  if (gh == 0ull) return bb;
-  const int g = (int)__ffsll((long long)gh) - 1;
-  if (g * WAVE >= bb) return bb;
-  // within the group: one bin per lane
-  const int b = g * WAVE + lane;
-  const uint64_t before = g > 0 ? rl_u64(ginc, g - 1) : 0ull;
-  const uint64_t bv = val(before + S.hist[b], b >= excl_b);
-  const uint64_t bh = __ballot((double)bv > thr);
-  const int bz = bh ? g * WAVE + (int)__ffsll((long long)bh) - 1 : bb;
-  return bz < bb ? bz : bb;
+// Row bin of l: A(m) - A(l) (arow = A(m)); NOBIN past the row's window or for -inf.
+__device__ __forceinline__ int row_bin(float arow, float l) {
+  if (!(l > -INFINITY)) return NOBIN;
+  const float d = arow - floorf(l * (float)LBS);
+  return d < (float)NBW ? (int)d : NOBIN;
 }
 
-// A decision: the key (~0: none), the count and mass of the keys before it in the row's
+// A pick: the key (~0: none), the count and mass of the keys before it in the row's
 // order, and its own mass.
 struct GHit {
   uint64_t key, cnt_before, mass_before, mass;
 };
 
-// Decision number n over the zone bkey/bmass[z0, z0 + nz) (one bin in bin order; every
-// thread, nz <= GT): the first zone key in key order, key <= bound and id != excl, whose
-// inclusive cumulative count (mass == false) or mass exceeds thr, starting from cnt0 /
-// mass0 before the zone. Thread t owns zone key t and counts the zone keys before it; the
-// unique key whose interval contains thr writes its result with tag n to slot n & 1 (a
-// slot is rewritten two decisions later, after every thread has read it). One barrier.
-__device__ __forceinline__ GHit gresolve(GFinalShared& S, int n, int z0, int nz, bool mass,
-                                         double thr, uint64_t bound, int excl, uint64_t cnt0,
-                                         uint64_t mass0) {
+// The row's cumulative histogram in a wave's registers: lane l holds bins LPL l + q.
+struct RowCum {
+  uint32_t c[LPL];
+  uint64_t m[LPL];
+  __device__ __forceinline__ uint32_t cq(int q) const { return q == 0 ? c[0] : (q == 1 ? c[1] : c[2]); }
+  __device__ __forceinline__ uint64_t mq(int q) const { return q == 0 ? m[0] : (q == 1 ? m[1] : m[2]); }
+  // inclusive cumulative count / mass of bin b (wave-uniform; b < 0: 0, b past the row's
+  // window: the window's total)
+  __device__ __forceinline__ uint64_t cnt(int b) const {
+    if (b < 0) return 0ull;
+    if (b >= NBW) b = NBW - 1;
+    return (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)cq(b % LPL), b / LPL);
+  }
+  __device__ __forceinline__ uint64_t mass(int b) const {
+    if (b < 0) return 0ull;
+    if (b >= NBW) b = NBW - 1;
+    return rl_u64(mq(b % LPL), b / LPL);
+  }
+  // the first bin b < limit whose cumulative value (the mass less excl_w from bin excl_b
+  // on) exceeds thr; limit when none does
+  __device__ __forceinline__ int find(bool by_mass, double thr, int limit, uint64_t excl_w,
+                                      int excl_b) const {
+    const int lane = threadIdx.x & (WAVE - 1);
+    int first = NOBIN;
+#pragma unroll
+    for (int q = LPL - 1; q >= 0; --q) {
+      const int b = LPL * lane + q;
+      const uint64_t val = by_mass ? m[q] - (b >= excl_b ? excl_w : 0ull) : (uint64_t)c[q];
+      if (b < limit && (double)val > thr) first = b;
+    }
+    first = wave_min_i(first);
+    return first < limit ? first : limit;
+  }
+};
+static_assert(LPL == 3, "RowCum holds three bins per lane");
+
+// Pick number np over the zone zkey/zmass[z0, z0 + n) (unsorted, n <= GT): the first key in
+// key order, key <= bound and id != excl, whose inclusive cumulative count (by_mass false:
+// every key counts) or mass exceeds thr, from cnt0 / mass0 before the zone. Every thread
+// compares one key with every R-th key of the zone (R = GT / n), so each key's rank and
+// the mass before it are summed from R partial counts; the unique key whose interval
+// contains thr writes its result to slot np & 1 (a slot is rewritten two picks later,
+// after every thread has read it). Three barriers.
+__device__ __forceinline__ GHit pick_rank(GFinalShared& S, GBig& G, int np, int z0, int n, bool by_mass,
+                                          double thr, uint64_t bound, int excl, uint64_t cnt0,
+                                          uint64_t mass0) {
   const int t = threadIdx.x;
-  const int slot = n & 1;
-  if (t < nz) {
-    const uint64_t k = S.bkey[z0 + t];
-    const uint64_t km = S.bmass[z0 + t];
-    const bool in = k <= bound && (int)(uint32_t)k != excl;
+  const int slot = np & 1;
+  if (t < n) {
+    S.prk[t] = 0u;
+    S.pmb[t] = 0ull;
+  }
+  __syncthreads();
+  const int R = n > 0 ? GT / n : 1;
+  const int i = t / R, sg = t - i * R;
+  if (i < n) {
+    const uint64_t* zk = G.z.zkey + z0;
+    const uint64_t* zm = G.z.zmass + z0;
+    const uint64_t k = zk[i];
     uint32_t rank = 0u;
     uint64_t mb = 0ull;
-    for (int jj = 0; jj < nz; ++jj) {
-      const uint64_t kj = S.bkey[z0 + jj];
-      const uint64_t mj = S.bmass[z0 + jj];
+    int jj = sg;
+    for (; jj + 3 * R < n; jj += 4 * R) {
+      uint64_t kj[4], mj[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kj[u] = zk[jj + u * R];
+        mj[u] = zm[jj + u * R];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool lt = kj[u] < k;
+        rank += lt ? 1u : 0u;
+        mb += (lt && kj[u] <= bound && (int)(uint32_t)kj[u] != excl) ? mj[u] : 0ull;
+      }
+    }
+    for (; jj < n; jj += R) {
+      const uint64_t kj = zk[jj];
       const bool lt = kj < k;
       rank += lt ? 1u : 0u;
-      mb += (lt && kj <= bound && (int)(uint32_t)kj != excl) ? mj : 0ull;
+      mb += (lt && kj <= bound && (int)(uint32_t)kj != excl) ? zm[jj] : 0ull;
     }
-    // count mode counts every key (no bound, no exclusion)
-    const uint64_t before = mass ? mass0 + mb : cnt0 + rank;
-    const uint64_t own = mass ? (in ? km : 0ull) : 1ull;
+    if (rank) atomicAdd(&S.prk[i], rank);
+    if (mb) atomicAdd(&S.pmb[i], (unsigned long long)mb);
+  }
+  __syncthreads();
+  if (t < n) {
+    const uint64_t k = G.z.zkey[z0 + t];
+    const uint64_t km = G.z.zmass[z0 + t];
+    const bool in = k <= bound && (int)(uint32_t)k != excl;
+    const uint32_t rank = S.prk[t];
+    const uint64_t mb = S.pmb[t];
+    const uint64_t before = by_mass ? mass0 + mb : cnt0 + rank;
+    const uint64_t own = by_mass ? (in ? km : 0ull) : 1ull;
     if (own > 0ull && (double)before <= thr && (double)(before + own) > thr) {
       S.res[slot][0] = k;
       S.res[slot][1] = cnt0 + rank;
       S.res[slot][2] = mass0 + mb;
       S.res[slot][3] = km;
-      S.tag[slot] = n;
+      S.tag[slot] = np;
     }
   }
   __syncthreads();
-  if (S.tag[slot] != n) return GHit{~0ull, 0ull, 0ull, 0ull};
+  if (S.tag[slot] != np) return GHit{~0ull, 0ull, 0ull, 0ull};
   return GHit{S.res[slot][0], S.res[slot][1], S.res[slot][2], S.res[slot][3]};
+}
+
+// The same pick over a zone of more than GT keys: the keys are sorted in place (their
+// masses rewritten in the new order), each thread takes ZQ consecutive positions, and a
+// block scan gives every position its count and mass before it.
+__device__ __forceinline__ GHit pick_sorted(GFinalShared& S, GBig& G, int np, int n, bool by_mass, double thr,
+                                            uint64_t bound, int excl, uint64_t cnt0,
+                                            uint64_t mass0, float m) {
+  const int t = threadIdx.x;
+  const int slot = np & 1;
+  bitonic_sort_lds<GT>(G.z.zkey, n);
+  uint64_t km[ZQ], lm = 0ull;
+  bool in[ZQ];
+#pragma unroll
+  for (int q = 0; q < ZQ; ++q) {
+    const int pos = ZQ * t + q;
+    km[q] = 0ull;
+    in[q] = false;
+    if (pos < n) {
+      const uint64_t k = G.z.zkey[pos];
+      km[q] = rmass(key_l(k), m);
+      G.z.zmass[pos] = km[q];
+      in[q] = k <= bound && (int)(uint32_t)k != excl;
+      lm += in[q] ? km[q] : 0ull;
+    }
+  }
+  uint64_t exc, exm, totc, totm;
+  block_excl_scan2_u64<GT>(0ull, lm, S.u2, exc, exm, totc, totm);
+  int best = -1;
+  uint64_t bm = 0ull;
+  uint64_t fm = mass0 + exm;
+#pragma unroll
+  for (int q = 0; q < ZQ; ++q) {
+    const int pos = ZQ * t + q;
+    if (pos < n) {
+      const uint64_t before = by_mass ? fm : cnt0 + (uint64_t)pos;
+      const uint64_t own = by_mass ? (in[q] ? km[q] : 0ull) : 1ull;
+      if (own > 0ull && (double)before <= thr && (double)(before + own) > thr) {
+        best = pos;
+        bm = fm;
+      }
+      fm += in[q] ? km[q] : 0ull;
+    }
+  }
+  const int psel = -block_min<GT>(-best, S.ii);
+  if (psel >= 0 && best == psel) {
+    S.res[slot][0] = G.z.zkey[psel];
+    S.res[slot][1] = cnt0 + (uint64_t)psel;
+    S.res[slot][2] = bm;
+    S.res[slot][3] = G.z.zmass[psel];
+    S.tag[slot] = np;
+  }
+  __syncthreads();
+  if (S.tag[slot] != np) return GHit{~0ull, 0ull, 0ull, 0ull};
+  return GHit{S.res[slot][0], S.res[slot][1], S.res[slot][2], S.res[slot][3]};
+}
+
+// Sum of the masses of the zone's keys <= bound, zone zkey/zmass[z0, z0 + n) (every
+// thread; two barriers).
+__device__ __forceinline__ uint64_t zone_mass_upto(GFinalShared& S, GBig& G, int z0, int n,
+                                                  uint64_t bound) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  uint64_t s = 0ull;
+  for (int i = t; i < n; i += GT) s += G.z.zkey[z0 + i] <= bound ? G.z.zmass[z0 + i] : 0ull;
+  s = wave_sum_u64(s);
+  if (lane == 0) S.u[w] = s;
+  __syncthreads();
+  uint64_t tot = 0ull;
+#pragma unroll
+  for (int q = 0; q < GW; ++q) tot += S.u[q];
+  __syncthreads();
+  return tot;
+}
+
+// Out-of-line forms of the rare paths (their code stays out of the common path's
+// instruction stream; the LDS arrives as an address-space-typed pointer, and only the
+// launch fields they read are passed: a reference to the argument block would copy it
+// to private memory).
+__device__ __noinline__ GHit pick_sorted_ool(lds_t<GFinalShared>* Sl, lds_t<GBig>* Gl, int np,
+                                             int n, bool by_mass, double thr, uint64_t bound,
+                                             int excl, uint64_t cnt0, uint64_t mass0, float m) {
+  GFinalShared& S = *(GFinalShared*)Sl;
+  GBig& G = *(GBig*)Gl;
+  return pick_sorted(S, G, np, n, by_mass, thr, bound, excl, cnt0, mass0, m);
+}
+// The last key passing min-p, (double)l - (double)m >= lmp: the first fkey (descending l)
+// that fails, less one.
+__device__ __noinline__ uint32_t minp_last_fkey(float m, double lmp) {
+  return x_first_fkey(fkey_desc(m), fkey_desc(-INFINITY), [&](float l) {
+           return !((double)l - (double)m >= lmp);
+         }) - 1u;
+}
+// Gumbel over every kept candidate of a row (key <= bound, not the draft): the chunks'
+// candidate entries of bins up to the bound's bin bb, scored in fp64. Returns the token
+// (-1: none kept but the draft).
+__device__ __noinline__ int gumbel_kept(lds_t<GFinalShared>* Sl, const Cand* base,
+                                        const float* noise, int W, int bb, uint64_t bound,
+                                        int draft, const RowParams p, float m, uint64_t S1,
+                                        bool cand_sorted) {
+  GFinalShared& S = *(GFinalShared*)Sl;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  if (w == 0) {
+    // lane c: chunk c's entries up to its part of the bound's bin
+    int lim = 0;
+    if (lane < W) {
+      const int lb = bb - S.dch[lane];
+      if (lb >= 0 && S.nbch[lane] > 0) lim = S.pc[lane][lb < S.nbch[lane] ? lb : S.nbch[lane] - 1];
+    }
+    const int zof = (int)wave_incl_scan_u32((uint32_t)lim) - lim;
+    if (lane < W) S.zoff[lane] = zof;
+    if (lane == W - 1) S.zoff[W] = zof + lim;
+  }
+  __syncthreads();
+  const int N = S.zoff[W];
+  const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
+  const double lse = log((double)S1 / RFIX);
+  const uint64_t pkey = mix64(p.seed, p.position);
+  double bsc = -INFINITY;
+  uint64_t btk = ~0ull;
+  int bid = -1;
+  for (int i = t; i < N; i += GT) {
+    // the chunk holding entry i: the last c with zoff[c] <= i
+    int lo = 0, hi = W - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (S.zoff[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    const Cand x = base[(int64_t)lo * SLOT + (i - S.zoff[lo])];
+    const uint64_t k = ckey(x.l, x.id);
+    if (k > bound || x.id == draft) continue;
+    const float u = noise ? noise[x.id] : philox_uniform(pkey, (uint64_t)x.id);
+    const double bs = no_lse ? (double)x.l : ((double)x.l - (double)m) - lse;
+    const double sc = bs + gumbel64(u);
+    const uint64_t tk = cand_sorted ? k : (uint64_t)x.id;
+    if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) {
+      bsc = sc;
+      btk = tk;
+      bid = x.id;
+    }
+  }
+  block_argmax_score<GT>(bsc, btk, bid, S.d, S.u, S.ii, &S.misc[4]);
+  return S.misc[4];
+}
+
+// The LDS a collect pass writes (address-space-typed: see lds_t).
+struct ZoneLds {
+  lds_t<uint64_t>* key;
+  lds_t<uint64_t>* mass;
+  lds_t<uint32_t>* cnt;  // GT * EPT history counts of one window
+  lds_t<int>* n;
+};
+// Collect pass: every token of the row whose lattice bin A(l) is `at`, by one streaming
+// pass of the workgroup over the row's logits (the chain recomputed per window), into
+// key / mass. Returns their number, -1 past ZCAP. Out of line: the common path of
+// k_gfinal keeps none of the pass's registers.
+__device__ __noinline__ int collect_zone(const XArgs a_in, int r, int b, int j,
+                                         const RowParams p_in, float at, float m,
+                                         const ZoneLds z_in) {
+  const XArgs a = uniform_copy(a_in);
+  const RowParams p = uniform_copy(p_in);
+  const ZoneLds z = uniform_copy(z_in);
+  r = __builtin_amdgcn_readfirstlane(r);
+  b = __builtin_amdgcn_readfirstlane(b);
+  j = __builtin_amdgcn_readfirstlane(j);
+  // (readfirstlane takes an int: floats go through their bits)
+  at = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(at)));
+  m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
+  const int lane = threadIdx.x & (WAVE - 1);
+  if (threadIdx.x == 0) *z.n = 0;
+  __syncthreads();
+  x_pass<GT, false>(a, r, b, j, p, (uint32_t*)z.cnt,
+                    [&](int i0, const float (&l)[EPT], const float (&)[EPT]) {
+    uint32_t sel = 0u;
+    int c = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (l[e] > -INFINITY && floorf(l[e] * (float)LBS) == at) {
+        sel |= 1u << e;
+        ++c;
+      }
+    int tot;
+    const int ex = wave_excl_count(c, &tot);
+    if (tot > 0) {
+      int base = 0;
+      if (lane == 0) base = atomicAdd((int*)z.n, tot);
+      base = __builtin_amdgcn_readfirstlane(base);
+      int pos = base + ex;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        if ((sel >> e) & 1u) {
+          if (pos < ZCAP) {
+            z.key[pos] = ckey(l[e], i0 + e);
+            z.mass[pos] = rmass(l[e], m);
+          }
+          ++pos;
+        }
+    }
+  });
+  __syncthreads();
+  const int n = *z.n;
+  return n <= ZCAP ? n : -1;
 }
 
 __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   __shared__ GFinalShared S;
+  __shared__ GBig G;
+  __shared__ GPf P;
   // the launch fields of the first loads, read together (see k_stream)
-  asm volatile("" ::"s"(a.s.cstat), "s"(a.s.wmax), "s"(a.s.rs), "s"(a.s.slot), "s"(a.W),
+  asm volatile("" ::"s"(a.s.cstat), "s"(a.s.wmax), "s"(a.s.rs), "s"(a.s.lat), "s"(a.W),
                "s"(a.V), "s"(a.noise), "s"(a.noise_stride), "s"(a.noise_mode), "s"(a.verify),
                "s"(a.k), "s"(a.drafts));
   const int r = blockIdx.x;
@@ -193,12 +449,11 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   row_bj(a, r, b, j);
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int V = a.V, W = a.W;
-  // ---- step 1: every load that does not depend on the row's parameters ------------
-  // the chunk statistics (one chunk per thread), the noise, the draft and every candidate
-  // slot of the row (no branch between the loads: a missing optional input reads the
-  // row's own state and is ignored; slots past a region's count are dropped later)
+  // ---- every load that does not depend on the row's parameters ------------------
+  // the chunk statistics (one chunk per thread), the noise, the draft and the chunks'
+  // lattice words (no branch between the loads: a missing optional input reads the row's
+  // own state and is ignored; words past a chunk's written bins are dropped later)
   const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (t < W ? t : 0)];
-  static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
   RowState* rsp = &a.s.rs[r];
   const bool gum = a.noise && a.noise_mode != STRIM_NOISE_ICDF;
   const float* nz = a.noise ? a.noise + (int64_t)r * a.noise_stride : (const float*)rsp;
@@ -207,53 +462,78 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const int32_t* dp = vdr ? a.drafts + (int64_t)b * a.k + j : (const int32_t*)rsp;
   const int d_raw = *dp;
   const float ld_raw = rsp->l_draft;
-  const int ne = W * GCAP;  // candidate slots of the row
+  // the chunks' lattice words (E[c NBW + lb]) and each chunk's first PF candidates
+  // (pfb[c PF + place]; places past what a chunk wrote are stale and never used),
+  // straight into LDS: wave w issues blocks w, w + GW, ... of 1 KB (16 bytes per lane).
+  // The count per wave is fixed (blocks past the row's repeat its last block: the same
+  // bytes to the same place), so the statistics' loads are waited for by count alone.
+  const int nlw = W <= LWMAX ? W * NBW : 0;
+  const unsigned long long* lwp = a.s.lat + (int64_t)r * a.s.wmax * NBW;
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
-  // slots 0 .. GNE - 1: the first tier (entry e = q GT + t is region e / GCAP, offset
-  // e % GCAP); slots GNE .. GNE + GNE2 - 1: the second tier, loaded only when a decision
-  // falls at or below the first tier's bound (entry e is region e / GCAP2, offset GCAP +
-  // e % GCAP2)
-  Cand cd[GNE];
+  {
+    const int wl = W <= LWMAX ? W : 1;
+    const int nwb = (wl * NBW * 8 + 1023) / 1024, npb = (wl * PF * 8 + 1023) / 1024;
 #pragma unroll
-  for (int q = 0; q < GNE; ++q) {
-    const int e = q * GT + t;
-    cd[q] = slots[e < ne ? (int64_t)(e >> GSH) * SLOT + (e & (GCAP - 1)) : 0];
+    for (int q = 0; q < KW; ++q) {
+      const int blk = min(w + GW * q, nwb - 1);
+      const int e = blk * 128 + 2 * lane;  // its words e, e + 1
+      const int ec = e < wl * NBW ? e : 0;
+      __builtin_amdgcn_global_load_lds((const void*)(lwp + ec),
+                                       (lds_t<void>*)((char*)G.E + blk * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < KP; ++q) {
+      const int blk = min(w + GW * q, npb - 1);
+      const int e = blk * 128 + 2 * lane;  // its candidates e, e + 1 (PF even)
+      const int c = e / PF, pl = e - c * PF;
+      const Cand* src = c < wl ? slots + (int64_t)c * SLOT + pl : slots;
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (lds_t<void>*)((char*)P.pfb + blk * 1024), 16, 0, 0);
+    }
   }
   const RowParams p = load_params(a, b, j);
-  if (!gfinal_row(a.p[b], V, a.noise_mode, a.dlog != nullptr && vdr)) return;
+  if (!gfinal_row(a.p[b], V, a.noise_mode, a.dlog != nullptr && vdr)) {
+    __builtin_amdgcn_s_waitcnt(0);  // (no LDS write may land after the workgroup ends)
+    return;
+  }
   const int draft = vdr ? d_raw : -1;
   const float l_draft = vdr ? ld_raw : -INFINITY;
 
   // ---- the chunk statistics: per wave, then every wave merges the waves' results --
   const bool own = t < W;
   int ff = own ? (cs.flags | (cs.n > 0 ? 4 : 0)) : 0;
-  float mv = own ? cs.m : -INFINITY, gv = own ? cs.g : -INFINITY;
-  float gv2 = own ? cs.g2 : -INFINITY;
+  if (own && cs.n > 0 && cs.ncand2 == LNONE) ff |= 8;  // a chunk without lattice words
+  float mv = own ? cs.m : -INFINITY;
   int mi = own ? cs.arg : -1;
-  S.rcnt[t] = own ? cs.ncand : 0u;
-  S.rcnt2[t] = own ? cs.ncand2 : 0u;
+  if (own && t < LWMAX) {
+    S.mch[t] = cs.n > 0 ? cs.m : -INFINITY;
+    S.nbch[t] = cs.n > 0 ? (int)cs.ncand2 : 0;
+    S.nfch[t] = cs.n > 0 ? (int)cs.ncand : 0;
+    S.ncnt[t] = cs.n;
+  }
   wave_argmax(mv, mi);
   ff = wave_or_i(ff);
-  gv = wave_max_f(gv);
-  gv2 = wave_max_f(gv2);
   if (lane == 0) {
     S.v[w] = mv;
     S.i[w] = mi;
     S.f[w] = ff;
-    S.g[w] = gv;
-    S.g2[w] = gv2;
   }
-  S.hist[t] = 0ull;
+  if (t < NBW) {
+    S.rc[t] = 0u;
+    S.rm[t] = 0ull;
+  }
   if (t < 2) S.tag[t] = -1;
+  if (t == 0) {
+    S.misc[0] = NBW;
+    S.misc[1] = NBW;
+    S.misc[3] = 0;
+  }
   __syncthreads();
   // lane q holds wave q's results
-  float m = lane < GW ? S.v[lane] : -INFINITY, G = lane < GW ? S.g[lane] : -INFINITY;
-  float G2 = lane < GW ? S.g2[lane] : -INFINITY;
+  float m = lane < GW ? S.v[lane] : -INFINITY;
   int arg = lane < GW ? S.i[lane] : -1, flags = lane < GW ? S.f[lane] : 0;
   wave_argmax(m, arg);
   flags = wave_or_i(flags);
-  G = wave_max_f(G);
-  G2 = wave_max_f(G2);
   auto finish = [&](int status, int token, int accept, double sig, uint64_t last_key) {
     if (t != 0) return;
     rsp->status = status;
@@ -273,6 +553,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   if (status == STRIM_OK && (flags & 1)) status = STRIM_ENONFINITE;
   if (status == STRIM_OK && !(flags & 4)) status = STRIM_EEMPTY;
   if (status != STRIM_OK) {
+    __builtin_amdgcn_s_waitcnt(0);  // (no LDS write may land after the workgroup ends)
     finish(status, -1, 0, 0.0, 0ull);
     return;
   }
@@ -285,266 +566,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     u_draw = philox_uniform(pkey, 0);
     u_acc = philox_uniform(pkey, a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
   }
-
-  // ---- steps 2 and 3: the decision from the candidates ---------------------------
-  // Round 0 uses the first tier and the bound G, round 1 (when a decision of round 0
-  // fell at or below G) both tiers and the bound G2. The verdict: 0 decided, 1 a
-  // decision lies at or below the round's bound, 2 the candidates cannot decide the row
-  // (both lead to the exact resolution when no round is left). Every condition is uniform
-  // over the workgroup.
-  // (one instantiation per round: the first round's code and registers carry nothing
-  // of the second tier)
-  enum { DECIDED = 0, BELOW = 1, OTHER = 2 };
-  const int ne2 = W * GCAP2;  // second-tier slots of the row
-  auto decide = [&](auto round_c, const Cand (&cd2)[GNE2]) -> int {
-    constexpr int round = decltype(round_c)::value;
-    constexpr int NS = round == 0 ? GNE : GNE + GNE2;  // slots of this round
-    auto cand = [&](int q) -> const Cand& { return q < GNE ? cd[q] : cd2[q - GNE]; };
-    const bool topk = p.top_k > 0 && p.top_k < V;
-    const bool topp = p.top_p < 1.0f;
-    const bool minp = p.min_p > 0.0f;
-    const bool icdf = a.noise_mode == STRIM_NOISE_ICDF;
-    // rank-indexed noise needs every kept token's rank
-    if ((p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp && !icdf) return OTHER;
-    if (ne > GT * GNE) return OTHER;
-    const float Gr = round == 0 ? G : G2;
-    const bool all_in = !(Gr > -INFINITY);  // every allowed token is a candidate
-    // min-p keeps a set that lies above the bound only if the bound itself fails it
-    if (minp && !all_in && ((double)Gr - (double)m) >= p.lmp) return BELOW;
-    const float span = all_in ? 64.0f : fminf(fmaxf(m - Gr, 1.0f / 64.0f), 64.0f);
-    const float hscale = (float)GNB / span;
-    // which of this thread's slots hold a candidate: first-tier entry e = q GT + t lies
-    // in region e / GCAP at offset e % GCAP, second-tier entry e = q GT + t in region
-    // e / GCAP2 at offset GCAP + e % GCAP2
-    uint32_t vmask = 0u;
-    {
-      uint32_t rc[NS];
-#pragma unroll
-      for (int q = 0; q < GNE; ++q) rc[q] = S.rcnt[min(q * (GT / GCAP) + (t >> GSH), GT - 1)];
-#pragma unroll
-      for (int q = GNE; q < NS; ++q)
-        rc[q] = S.rcnt2[min((q - GNE) * (GT / GCAP2) + (t >> GSH2), GT - 1)];
-#pragma unroll
-      for (int q = 0; q < GNE; ++q)
-        vmask |= (((q * GT + t < ne) & ((uint32_t)(t & (GCAP - 1)) < rc[q])) ? 1u : 0u) << q;
-#pragma unroll
-      for (int q = GNE; q < NS; ++q)
-        vmask |= ((((q - GNE) * GT + t < ne2) & ((uint32_t)(t & (GCAP2 - 1)) < rc[q])) ? 1u : 0u)
-                 << q;
-    }
-    // bin every candidate above the bound (passing min-p); the atomic's old count is its place in
-    // the bin. A lane without a candidate leaves old[q] unset and never reads it; the
-    // empty asm statements after the loop keep the compiler from reading any result
-    // before every atomic is issued (it would otherwise wait for each in turn).
-    uint64_t old[NS], cm[NS];
-    int bn[NS];
-#pragma unroll
-    for (int q = 0; q < NS; ++q) {
-      const float l = cand(q).l;
-      const bool k = ((vmask >> q) & 1u) && l > Gr && l > -INFINITY &&
-                     (!minp || ((double)l - (double)m) >= p.lmp);
-      bn[q] = k ? gbin(m, l, hscale) : -1;
-      if (k) {
-        cm[q] = gmass(l, m);
-        old[q] = atomicAdd(&S.hist[bn[q]], (unsigned long long)((1ull << GCSH) | cm[q]));
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < NS; ++q) asm volatile("" : "+v"(old[q]));
-    // the whole row's mass relative to m, from the chunk sums (used while the kept set
-    // reaches below the bound), while the atomics complete
-    {
-      const double sw = wave_sum((own && cs.n > 0) ? cs.S * exp((double)cs.m - (double)m) : 0.0);
-      if (lane == 0) S.sw[w] = sw;
-    }
-    __syncthreads();
-    // group-local inclusive prefixes: wave w over bins 64 w .. 64 w + 63
-    {
-      const int bb = w * WAVE + lane;
-      const uint64_t ci = wave_incl_scan_u64(S.hist[bb]);
-      S.hist[bb] = ci;
-      if (lane == WAVE - 1) S.gt[w] = ci;
-    }
-    double S_all = 0.0;
-#pragma unroll
-    for (int q = 0; q < GW; ++q) S_all += S.sw[q];
-    __syncthreads();
-    // lane g: inclusive prefix of the group totals
-    const uint64_t gl = lane < GW ? S.gt[lane] : 0ull;
-    const uint64_t ginc = wave_incl_scan_u64(gl);
-    const uint64_t tot = rl_u64(ginc, GW - 1);
-    const uint64_t n_all = wcount(tot), m_all = wmass(tot);
-    if (n_all == 0ull) return BELOW;
-    // every candidate with its mass into bin order: bin b starts at the cumulative count
-    // of the bins before it (the group's exclusive prefix from lane g, plus the bins
-    // before b in the group); a slot without a candidate writes past the row's entries
-    {
-      const int gce = (int)wcount(ginc - gl);
-      // every read first (the empty asm statements keep them ahead of their uses), then
-      // every write
-      int at[NS];
-      uint32_t hb[NS];
-      int gb[NS];
-#pragma unroll
-      for (int q = 0; q < NS; ++q) {
-        const int bq = bn[q] < 0 ? 0 : bn[q];
-        hb[q] = (uint32_t)(S.hist[bq > 0 ? bq - 1 : 0] >> 32);
-        gb[q] = __shfl(gce, bq / WAVE);
-      }
-#pragma unroll
-      for (int q = 0; q < NS; ++q) asm volatile("" : "+v"(hb[q]), "+v"(gb[q]));
-#pragma unroll
-      for (int q = 0; q < NS; ++q) {
-        const int before = gb[q] + ((bn[q] & (WAVE - 1)) ? (int)(hb[q] >> (GCSH - 32)) : 0);
-        at[q] = bn[q] >= 0 ? before + (int)wcount(old[q]) : GCAND + lane;
-      }
-#pragma unroll
-      for (int q = 0; q < NS; ++q) {
-        S.bkey[at[q]] = ckey(cand(q).l, cand(q).id);
-        S.bmass[at[q]] = cm[q];
-      }
-    }
-    __syncthreads();
-
-    // ---- the decisions, in order: 0 the k-th token (count), 1 the top-p cut (mass), 2
-    // the icdf draw (mass, without the draft) -----------------------------------------
-    bool known0 = all_in || minp;  // every token of the set is a candidate
-    uint64_t bound0 = ~0ull, S0 = known0 ? m_all : (uint64_t)__double2ull_rn(S_all * GFIX);
-    uint64_t bound1 = ~0ull, S1 = S0, wd = 0ull;
-    bool known1 = known0;
-    int token = -1;
-    int nres = 0;  // decisions resolved so far (consecutive ones alternate result slots)
-    for (int step = 0; step < 3; ++step) {
-      bool mass = true;
-      double thr;
-      uint64_t bound, xw = 0ull;
-      int excl = -1, xb = GNB;
-      if (step == 0) {
-        if (!topk) continue;
-        if (n_all < (uint64_t)p.top_k) {
-          if (!all_in) return BELOW;  // the k-th token lies at or below the bound
-          continue;                   // every allowed token is kept
-        }
-        mass = false;
-        thr = (double)(p.top_k - 1);
-        bound = ~0ull;
-      } else if (step == 1) {
-        bound1 = bound0;
-        S1 = S0;
-        known1 = known0;
-        if (!topp) continue;
-        // the last kept token is the first whose inclusive mass exceeds P S0 (a token is
-        // dropped iff the mass before it exceeds P, SpecSampling.swift:62-66)
-        thr = (double)p.top_p * (double)S0;
-        bound = bound0;
-      } else {
-        if (!icdf && !known1) return BELOW;
-        // the draft of a verify row: kept? its mass, and its bin when a candidate
-        if (vdr && l_draft > -INFINITY && ckey(l_draft, draft) <= bound1) {
-          wd = gmass(l_draft, m);
-          if (l_draft > Gr && (!minp || ((double)l_draft - (double)m) >= p.lmp)) {
-            xb = gbin(m, l_draft, hscale);
-            xw = wd;
-          }
-        }
-        if (!icdf) break;
-        thr = (double)u_draw * (double)(S1 - wd);
-        bound = bound1;
-        excl = draft;
-      }
-      const int bb = bound == ~0ull ? GNB - 1 : gbin(m, key_l(bound), hscale);
-      const int bz = gfind_bin(S, mass, ginc, thr, bb, xw, xb);
-      const uint64_t w0 = gcum(S, ginc, bz - 1);
-      const uint64_t c0 = wcount(w0);
-      const int nzc = (int)(wcount(gcum(S, ginc, bz)) - c0);
-      if (nzc > GZCAP) return OTHER;
-      const uint64_t m0 = wmass(w0) - (bz - 1 >= xb ? xw : 0ull);
-      const GHit h = gresolve(S, nres++, (int)c0, nzc, mass, thr, bound, excl, c0, m0);
-      if (step == 0) {
-        if (h.key == ~0ull) return OTHER;
-        known0 = true;
-        if (!(p.flags & STRIM_FLAG_TOPK_KEEP_TIES)) {
-          bound0 = h.key;
-          S0 = h.mass_before + h.mass;
-        } else {
-          // the keys tied with the k-th one are kept too (same value, same bin)
-          bound0 = h.key | 0xFFFFFFFFull;
-          uint64_t loc = (t < nzc && S.bkey[c0 + t] <= bound0) ? S.bmass[c0 + t] : 0ull;
-          loc = wave_sum_u64(loc);
-          if (lane == 0) S.u[w] = loc;
-          __syncthreads();
-          uint64_t s = 0ull;
-#pragma unroll
-          for (int q = 0; q < GW; ++q) s += S.u[q];
-          S0 = wmass(w0) + s;
-        }
-      } else if (step == 1) {
-        if (h.key != ~0ull) {
-          bound1 = h.key;
-          S1 = h.mass_before + h.mass;
-          known1 = true;
-        } else if (!known0) {
-          return BELOW;  // the cut lies at or below the bound
-        }
-      } else {
-        if (h.key != ~0ull) token = (int)(uint32_t)h.key;
-        else if (!known1) return BELOW;  // the draw lies at or below the bound
-        else token = arg;                // only the draft kept: the first kept
-      }
-    }
-    if (!icdf) {
-      // ---- Gumbel: every kept candidate (key <= bound1, not the draft) ----------------
-      const bool no_lse = (p.flags & STRIM_FLAG_SCORE_NO_LSE) != 0;
-      const bool cand_sorted = no_lse ? topp : (topk || topp);
-      const double lse = log((double)S1 / GFIX);
-      double bsc = -INFINITY;
-      uint64_t btk = ~0ull;
-      int bid = -1;
-      for (int i = t; i < (int)n_all; i += GT) {
-        const uint64_t k = S.bkey[i];
-        const int id = (int)(uint32_t)k;
-        if (k > bound1 || id == draft) continue;
-        const float l = key_l(k);
-        const float u = a.noise ? a.noise[(int64_t)r * a.noise_stride + id]
-                                : philox_uniform(pkey, (uint64_t)id);
-        const double base = no_lse ? (double)l : ((double)l - (double)m) - lse;
-        const double sc = base + gumbel64(u);
-        const uint64_t tk = cand_sorted ? k : (uint64_t)id;
-        if (bid < 0 || sc > bsc || (sc == bsc && tk < btk)) { bsc = sc; btk = tk; bid = id; }
-      }
-      block_argmax_score<GT>(bsc, btk, bid, S.d, S.u, S.i, &S.misc[3]);
-      token = S.misc[3];
-      if (token < 0) token = arg;  // only the draft kept
-    }
-    const int acc = vdr && ((double)u_acc < (double)wd / (double)S1) ? 1 : 0;
-    finish(STRIM_OK, token, acc, (double)S1 / GFIX, bound1);
-    return DECIDED;
-  };
-  // the second round needs room for both tiers and a lower bound than the first
-  const bool deepen_ok = W * (GCAP + GCAP2) <= GCAND && ne2 <= GT * GNE2 && G2 < G;
-  {
-    const Cand none[GNE2] = {};
-    const int verdict = decide(std::integral_constant<int, 0>{}, none);
-    if (verdict == DECIDED) return;
-    if (verdict == BELOW && deepen_ok) {
-      // the second tier (its loads are the only wait of this step), and the histogram
-      // and result slots cleared for the second round
-      Cand cd2[GNE2];
-#pragma unroll
-      for (int q = 0; q < GNE2; ++q) {
-        const int e = q * GT + t;
-        cd2[q] = slots[e < ne2 ? (int64_t)(e >> GSH2) * SLOT + GCAP + (e & (GCAP2 - 1)) : 0];
-      }
-      __syncthreads();  // every read of the first round's histogram is done
-      S.hist[t] = 0ull;
-      if (t < 2) S.tag[t] = -1;
-      __syncthreads();
-      if (decide(std::integral_constant<int, 1>{}, cd2) == DECIDED) return;
-    }
-  }
-
-  // ---- a decision at or below G: the exact streaming resolution --------------------
-  const XScratch xs = xscratch(S.xkey, S.xhc, S.xcnt, S.xu2, S.d, S.u, S.i);
+  // the streaming passes' view of the launch (collect passes and the exact resolution)
   XArgs xa;
   xa.logits = a.logits;
   xa.row_stride = a.row_stride;
@@ -563,9 +585,567 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   xa.noise = a.noise;
   xa.noise_stride = a.noise_stride;
   xa.has_q = 0;
+
+  // ---- the row's lattice ---------------------------------------------------------
+  const float arow = floorf(m * (float)LBS);
+  const bool lat = W <= LWMAX && !(flags & 8) && fabsf(arow) < 0x1p+23f;
+  auto decide = [&]() -> bool {
+    // per chunk (the thread of chunk t): its distance below the row's top bin, its mass
+    // sum relative to the row maximum, how far down its bins are whole; the chunks'
+    // lattice words staged in LDS with their count prefixes (for the gathers)
+    if (own) {
+      if (cs.n > 0) {
+        const int d = (int)(arow - floorf(cs.m * (float)LBS));
+        const int nb = (int)cs.ncand2, nf = (int)cs.ncand;
+        S.dch[t] = d;
+        S.sch[t] = cs.S * exp((double)cs.m - (double)m);
+        if (nb == 0) {  // (no window words: nothing of the chunk is known)
+          atomicMin(&S.misc[1], d);
+          S.misc[3] = 1;
+        }
+        if (nf < nb && d + nf < NBW) atomicMin(&S.misc[0], d + nf);
+        if (d + nb > NBW) S.misc[3] = 1;  // its window reaches past the row's
+      } else {
+        S.dch[t] = NOBIN;
+        S.sch[t] = 0.0;
+      }
+    }
+    // the LDS loads have landed (every wave waits for its own, then the barrier)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // every row bin: the counts and masses of its chunks' bins (waves 0-2 over the even
+    // chunks, 3-5 over the odd ones, one row bin per lane: the chunk is uniform over the
+    // wave; a lattice bin's masses share their unit, so they add as integers); each
+    // chunk's inclusive count prefixes for the gathers; tokens below a chunk's window
+    if (w < 6) {
+      const int g = w / 3, bq = (w - 3 * g) * WAVE + lane;
+      const int dreg = lane < W ? S.dch[lane] : NOBIN;
+      const int nbreg = lane < W ? S.nbch[lane] : 0;
+      uint32_t cs_ = 0u;
+      uint64_t ms_ = 0ull;
+      for (int c = g; c < W; c += 2) {
+        const int d = __builtin_amdgcn_readlane(dreg, c);
+        const int nb = __builtin_amdgcn_readlane(nbreg, c);
+        const int lb = bq - d;
+        if (lb >= 0 && lb < nb) {
+          const uint64_t wv = G.E[c * NBW + lb];
+          const uint32_t prev = lb > 0 ? (uint32_t)(G.E[c * NBW + lb - 1] >> LCSH) : 0u;
+          const uint32_t incl = (uint32_t)(wv >> LCSH);
+          S.pc[c][lb] = (uint16_t)incl;
+          cs_ += incl - prev;
+          ms_ += wv & LMMASK;
+        }
+      }
+      if (cs_) {
+        atomicAdd(&S.rc[bq], cs_);
+        atomicAdd(&S.rm[bq], (unsigned long long)ms_);
+      }
+    }
+    if (own && cs.n > 0 && cs.ncand2 > 0u && cs.ncand2 != LNONE &&
+        cs.n > (int)(uint32_t)(G.E[t * NBW + cs.ncand2 - 1] >> LCSH))
+      S.misc[3] = 1;
+    __syncthreads();
+    // The leader wave (wave 0) keeps the row's cumulative histogram in its registers,
+    // scaled from each bin's lattice unit to RFIX per unit of exp(l - m): scale(b) =
+    // 8 exp(arow / LBS - m) 2^(-b log2(e) / LBS). Every wave takes the totals and limits.
+    RowCum rcum;
+    if (w == 0) {
+      const float base = 8.0f * expf(arow * (1.0f / (float)LBS) - m);
+      uint32_t lc = 0u;
+      uint64_t lm = 0ull;
+#pragma unroll
+      for (int q = 0; q < LPL; ++q) {
+        const int bq = LPL * lane + q;
+        rcum.c[q] = S.rc[bq];
+        const float sc = base * __builtin_amdgcn_exp2f(-(float)bq * (1.44269504f / (float)LBS));
+        rcum.m[q] = (uint64_t)__double2ull_rn((double)S.rm[bq] * (double)sc);
+        lc += rcum.c[q];
+        lm += rcum.m[q];
+      }
+      uint32_t bc = wave_incl_scan_u32(lc) - lc;
+      uint64_t bm = wave_incl_scan_u64(lm) - lm;
+#pragma unroll
+      for (int q = 0; q < LPL; ++q) {
+        bc += rcum.c[q];
+        bm += rcum.m[q];
+        rcum.c[q] = bc;
+        rcum.m[q] = bm;
+      }
+    }
+    const int rowwin = S.misc[1] < NBW ? S.misc[1] : NBW;
+    const int rowfull = S.misc[0] < rowwin ? S.misc[0] : rowwin;
+    const bool anytail = S.misc[3] != 0;
+    const int n_all = wave_sum(lane < W ? S.ncnt[lane] : 0);
+    const double S_all = wave_sum(lane < W ? S.sch[lane] : 0.0);
+    const uint64_t S0 = (uint64_t)__double2ull_rn(S_all * RFIX);
+
+    const bool topk = p.top_k > 0 && p.top_k < V;
+    const bool topp = p.top_p < 1.0f;
+    const bool minp = p.min_p > 0.0f;
+    const bool icdf = a.noise_mode == STRIM_NOISE_ICDF;
+    // rank-indexed noise needs every kept token's rank
+    if ((p.flags & STRIM_FLAG_NOISE_BY_RANK) && topp && !icdf) return false;
+
+    // ---- the leader alone ------------------------------------------------------------
+    // A row whose zones are small (the common case) is decided by wave 0 alone, with no
+    // workgroup barrier: it lays out each zone from the prefetched candidates (lane c
+    // copies chunk c's part) and ranks the zone's keys within the wave, one key a lane (a
+    // wave's serial scan costs four cycles an instruction, so wider zones go to the eight
+    // waves). A zone that needs a chunk's slot region or a collect pass, or holds more
+    // than SOLO keys, and Gumbel
+    // draws, go to the cooperative loop below (every wave; it starts over). Both follow
+    // the same decision rules.
+    constexpr int SOLO = WAVE;
+    bool pfok = true;  // the prefetched candidates are in LDS
+    auto solo = [&]() -> int {  // 0 decided, 1 cooperative, 2 exact resolution
+      if (!icdf) return 1;
+      int zb0 = -1, zb1 = -1, zn0 = 0, zn1 = 0;
+      // bins {bz, also} into the zone (bz at 0, also after it): 0 loaded, else a verdict
+      auto load = [&](int bz, int also) -> int {
+        if (bz >= rowwin) return 2;
+        if (bz >= rowfull) return 1;
+        const uint64_t cr = rcum.cnt(bz) - rcum.cnt(bz - 1);
+        if (cr > (uint64_t)SOLO) return 1;
+        const bool two = also >= 0 && also != bz && also < rowfull &&
+                         cr + rcum.cnt(also) - rcum.cnt(also - 1) <= (uint64_t)SOLO;
+        const int bins[2] = {bz, two ? also : -1};
+        int off[2], cnt[2], zoo[2], n[2];
+        bool ok = pfok;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          off[hh] = 0;
+          cnt[hh] = 0;
+          if (lane < W && bins[hh] >= 0) {
+            const int lb = bins[hh] - S.dch[lane];
+            if (lb >= 0 && lb < S.nbch[lane]) {
+              off[hh] = lb > 0 ? (int)S.pc[lane][lb - 1] : 0;
+              cnt[hh] = (int)S.pc[lane][lb] - off[hh];
+            }
+          }
+          zoo[hh] = (int)wave_incl_scan_u32((uint32_t)cnt[hh]) - cnt[hh];
+          n[hh] = __builtin_amdgcn_readlane(zoo[hh] + cnt[hh], WAVE - 1);
+          ok = ok && off[hh] + cnt[hh] <= PF;
+        }
+        if (__ballot(!ok) != 0ull) return 1;
+        zoo[1] += n[0];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          for (int i = 0; i < cnt[hh]; ++i) {
+            const Cand x = P.pfb[lane * PF + off[hh] + i];
+            G.z.zkey[zoo[hh] + i] = ckey(x.l, x.id);
+            G.z.zmass[zoo[hh] + i] = rmass(x.l, m);
+          }
+        // (one wave's LDS operations complete in order: its later reads see these)
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+        zb0 = bz;
+        zn0 = n[0];
+        zb1 = bins[1];
+        zn1 = n[1];
+        return 0;
+      };
+      // the zone of bin bz: its place and size (z0 < 0: not loaded)
+      auto where = [&](int bz, int& z0, int& n) {
+        z0 = -1;
+        n = 0;
+        if (bz == zb0) { z0 = 0; n = zn0; }
+        else if (bz == zb1) { z0 = zn0; n = zn1; }
+      };
+      // pick_rank within the wave: lane l holds key z0 + l
+      auto wpick = [&](int z0, int n, bool by_mass, double thr, uint64_t bnd, int excl,
+                       uint64_t c0, uint64_t m0) -> GHit {
+        const bool mine = lane < n;
+        const uint64_t k = mine ? G.z.zkey[z0 + lane] : ~0ull;
+        const uint64_t km = mine ? G.z.zmass[z0 + lane] : 0ull;
+        const bool in = mine && k <= bnd && (int)(uint32_t)k != excl;
+        const uint64_t kin = in ? km : 0ull;  // its mass where it is kept
+        uint32_t rk = 0u;
+        uint64_t mb = 0ull;
+        for (int jj = 0; jj < n; ++jj) {
+          const bool lt = rl_u64(k, jj) < k;
+          rk += lt ? 1u : 0u;
+          mb += lt ? rl_u64(kin, jj) : 0ull;
+        }
+        const uint64_t before = by_mass ? m0 + mb : c0 + rk;
+        const uint64_t own = by_mass ? kin : 1ull;
+        const bool hit = mine && own > 0ull && (double)before <= thr && (double)(before + own) > thr;
+        const uint64_t bal = __ballot(hit);
+        if (bal == 0ull) return GHit{~0ull, 0ull, 0ull, 0ull};
+        const int hl = (int)__ffsll((long long)bal) - 1;
+        return GHit{rl_u64(k, hl), c0 + (uint32_t)__builtin_amdgcn_readlane((int)rk, hl),
+                    m0 + rl_u64(mb, hl), rl_u64(km, hl)};
+      };
+      // the zone's masses of keys <= bnd
+      auto wsum = [&](int z0, int n, uint64_t bnd) -> uint64_t {
+        uint64_t sm = 0ull;
+        for (int i = lane; i < n; i += WAVE) sm += G.z.zkey[z0 + i] <= bnd ? G.z.zmass[z0 + i] : 0ull;
+        return wave_sum_u64(sm);
+      };
+      uint64_t bound = ~0ull, Sk = S0;
+      int bbin = NOBIN;
+      int z0, n, v;
+      // top-k: the k-th key in order (every key counts)
+      if (topk && n_all >= p.top_k) {
+        const double thr = (double)(p.top_k - 1);
+        const int bz = rcum.find(false, thr, rowwin, 0ull, NOBIN);
+        if (bz >= rowwin) return 2;
+        if ((v = load(bz, -1)) != 0) return v;
+        const GHit g = wpick(0, zn0, false, thr, ~0ull, -1, rcum.cnt(bz - 1), rcum.mass(bz - 1));
+        if (g.key == ~0ull) return 2;
+        if (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) {
+          bound = g.key | 0xFFFFFFFFull;
+          Sk = rcum.mass(bz - 1) + wsum(0, zn0, bound);
+        } else {
+          bound = g.key;
+          Sk = g.mass_before + g.mass;
+        }
+        bbin = bz;
+      }
+      // min-p: every key whose l passes, (double)l - (double)m >= log(min_p)
+      if (minp) {
+        const uint32_t flast = minp_last_fkey(m, p.lmp);
+        const uint64_t bmp = ((uint64_t)flast << 32) | 0xFFFFFFFFull;
+        if (bmp < bound) {
+          const int bz = row_bin(arow, fkey_desc_inv(flast));
+          bound = bmp;
+          if (bz >= rowwin) {
+            if (anytail) return 2;
+          } else {
+            where(bz, z0, n);
+            if (z0 < 0) {
+              if ((v = load(bz, -1)) != 0) return v;
+              z0 = 0;
+              n = zn0;
+            }
+            Sk = rcum.mass(bz - 1) + wsum(z0, n, bound);
+            bbin = bz;
+          }
+        }
+      }
+      // top-p (SpecSampling.swift:62-66)
+      uint64_t bound1 = bound, S1 = Sk;
+      int bb1 = bbin;
+      if (topp) {
+        const double thr = (double)p.top_p * (double)Sk;
+        const int lim = bbin < rowwin ? bbin : rowwin;
+        int bz = rcum.find(true, thr, lim, 0ull, NOBIN);
+        if (bz >= lim) {
+          if (bbin >= rowwin) return 2;
+          bz = bbin;
+        }
+        where(bz, z0, n);
+        if (z0 < 0) {
+          int also = -1;
+          if (!vdr) {
+            const int blo = rcum.find(true, (double)u_draw * (double)rcum.mass(bz - 1), bz + 1, 0ull, NOBIN);
+            const int bhi = rcum.find(true, (double)u_draw * (double)rcum.mass(bz), bz + 1, 0ull, NOBIN);
+            if (blo == bhi && blo <= bz) also = blo;
+          }
+          if ((v = load(bz, also)) != 0) return v;
+          z0 = 0;
+          n = zn0;
+        }
+        const GHit g = wpick(z0, n, true, thr, bound, -1, rcum.cnt(bz - 1), rcum.mass(bz - 1));
+        if (g.key != ~0ull) {
+          bound1 = g.key;
+          S1 = g.mass_before + g.mass;
+          bb1 = bz;
+        } else if (bz != bbin) {
+          return 2;
+        }
+      }
+      // the draft of a verify row: kept? its mass and bin
+      uint64_t wd = 0ull;
+      int xb = NOBIN;
+      if (vdr && l_draft > -INFINITY && ckey(l_draft, draft) <= bound1) {
+        wd = rmass(l_draft, m);
+        xb = row_bin(arow, l_draft);
+      }
+      // the icdf draw over the kept keys without the draft
+      int token;
+      if (S1 <= wd) {
+        token = arg;  // only the draft kept: the first kept token
+      } else {
+        const double thr = (double)u_draw * (double)(S1 - wd);
+        const int lim = bb1 < rowwin ? bb1 : rowwin;
+        int bz = rcum.find(true, thr, lim, wd, xb);
+        if (bz >= lim) {
+          if (bb1 >= rowwin) return 2;
+          bz = bb1;
+        }
+        where(bz, z0, n);
+        if (z0 < 0) {
+          if ((v = load(bz, -1)) != 0) return v;
+          z0 = 0;
+          n = zn0;
+        }
+        const uint64_t m0 = rcum.mass(bz - 1) - (bz - 1 >= xb ? wd : 0ull);
+        const GHit g = wpick(z0, n, true, thr, bound1, draft, rcum.cnt(bz - 1), m0);
+        if (g.key == ~0ull) return 2;
+        token = (int)(uint32_t)g.key;
+      }
+      const int acc = vdr && ((double)u_acc < (double)wd / (double)S1) ? 1 : 0;
+      finish(STRIM_OK, token, acc, (double)S1 / RFIX, bound1);
+      return 0;
+    };
+    if (w == 0) {
+      const int verdict = solo();
+      if (lane == 0) S.misc[5] = verdict;
+    }
+    __syncthreads();
+    if (S.misc[5] == 0) return true;
+    if (S.misc[5] == 2) return false;
+
+    // The zone in LDS: up to two bins, zb[h] at [zo[h], zo[h] + zn[h]). A chunk's part of a
+    // bin comes from its prefetched candidates when it lies among them, else from its slot
+    // region; a bin some chunk could not write whole is collected by a streaming pass.
+    int zb[2] = {-1, -1}, zo[2] = {0, 0}, zn[2] = {0, 0}, npick = 0;
+    lds_t<GFinalShared>* Sl = (lds_t<GFinalShared>*)&S;
+    lds_t<GBig>* Gl = (lds_t<GBig>*)&G;
+
+    // The decisions, in order, through one loop (its code is fetched once):
+    //   0 top-k: the k-th key in order (every key counts);
+    //   1 min-p: the kept mass of the keys whose l passes, (double)l - (double)m >= lmp;
+    //   2 top-p: the last kept token is the first whose inclusive mass exceeds P Sk (a
+    //     token is dropped iff the mass before it exceeds P, SpecSampling.swift:62-66);
+    //   3 the icdf draw over the kept keys without the draft.
+    // The leader finds each step's bin and lays out its zone; every wave then loads the
+    // zone and takes part in the pick, and keeps the same state (all of it uniform).
+    // The kept set before top-p: keys <= bound, mass Sk, the bound's bin bbin (NOBIN:
+    // none inside the window); after it: bound1, S1, bb1.
+    uint64_t bound = ~0ull, Sk = S0, bound1 = ~0ull, S1 = S0, wd = 0ull;
+    int bbin = NOBIN, bb1 = NOBIN, xb = NOBIN, token = -1;
+    for (int step = 0; step < 4; ++step) {
+      if (step == 0 && !topk) continue;
+      if (step == 1 && !minp) continue;
+      if (step == 2) {
+        bound1 = bound;
+        S1 = Sk;
+        bb1 = bbin;
+        if (!topp) continue;
+      }
+      if (step == 3) {
+        // the draft of a verify row: kept? its mass and bin
+        if (vdr && l_draft > -INFINITY && ckey(l_draft, draft) <= bound1) {
+          wd = rmass(l_draft, m);
+          xb = row_bin(arow, l_draft);
+        }
+        if (!icdf) break;
+        if (S1 <= wd) {
+          token = arg;  // only the draft kept: the first kept token
+          break;
+        }
+      }
+      // ---- the leader: this step's bin and zone -------------------------------------
+      if (w == 0) {
+        GCmd cmd;
+        cmd.op = GOP_PICK;
+        cmd.load = 0;
+        cmd.also = -1;
+        cmd.by_mass = 1;
+        cmd.excl = -1;
+        cmd.thr = 0.0;
+        cmd.bnd = ~0ull;
+        cmd.bmp = ~0ull;
+        int bz = -1, bfall = NOBIN;
+        uint64_t xw = 0ull;
+        int xbn = NOBIN;
+        if (step == 0) {
+          if (n_all < p.top_k) cmd.op = GOP_SKIP;  // every allowed token is kept
+          cmd.by_mass = 0;
+          cmd.thr = (double)(p.top_k - 1);
+        } else if (step == 1) {
+          const uint32_t flast = minp_last_fkey(m, p.lmp);
+          cmd.bmp = ((uint64_t)flast << 32) | 0xFFFFFFFFull;
+          cmd.op = GOP_SUM;
+          if (cmd.bmp >= bound) {
+            cmd.op = GOP_SKIP;
+          } else {
+            bz = row_bin(arow, fkey_desc_inv(flast));
+            // below the window: with no token below some chunk's window every allowed
+            // token passes (the bound alone is set), else the lattice cannot tell
+            if (bz >= rowwin) cmd.op = anytail ? GOP_FAIL : GOP_BOUND;
+          }
+        } else if (step == 2) {
+          cmd.thr = (double)p.top_p * (double)Sk;
+          cmd.bnd = bound;
+          bfall = bbin;  // the cut lies in the bound's bin when no bin above it crosses
+        } else {
+          cmd.thr = (double)u_draw * (double)(S1 - wd);
+          cmd.bnd = bound1;
+          cmd.excl = draft;
+          xw = wd;
+          xbn = xb;
+          bfall = bb1;
+        }
+        if (cmd.op == GOP_PICK || cmd.op == GOP_SUM) {
+          if (bz < 0) {
+            const int lim = bfall < rowwin ? bfall : rowwin;
+            bz = rcum.find(cmd.by_mass, cmd.thr, lim, xw, xbn);
+            if (bz >= lim) bz = bfall < rowwin ? bfall : NOBIN;
+            // top-p of a sample row: the icdf draw's bin, when it can be told now, is
+            // loaded with the cut's (the kept mass lies between the masses before and
+            // through the cut's bin, so the draw's threshold lies between u times each)
+            if (bz < NOBIN && step == 2 && icdf && !vdr) {
+              const int blo = rcum.find(true, (double)u_draw * (double)rcum.mass(bz - 1), bz + 1, 0ull, NOBIN);
+              const int bhi = rcum.find(true, (double)u_draw * (double)rcum.mass(bz), bz + 1, 0ull, NOBIN);
+              if (blo == bhi && blo <= bz) cmd.also = blo;
+            }
+          }
+          if (bz >= rowwin) {
+            cmd.op = GOP_FAIL;
+          } else if (zb[0] != bz && zb[1] != bz) {
+            if (bz >= rowfull) {
+              cmd.load = 2;
+              cmd.also = -1;
+            } else {
+              const uint64_t cr = rcum.cnt(bz) - rcum.cnt(bz - 1);
+              const int also = cmd.also;
+              const bool two = also >= 0 && also != bz && also < rowfull &&
+                               cr + rcum.cnt(also) - rcum.cnt(also - 1) <= (uint64_t)GT;
+              cmd.also = two ? also : -1;
+              if (cr > (uint64_t)ZCAP) cmd.op = GOP_FAIL;
+              // lane c: chunk c's parts of the bins and their places in the zone
+              const int bins[2] = {bz, cmd.also};
+              int n[2];
+#pragma unroll
+              for (int hh = 0; hh < 2; ++hh) {
+                int cnt = 0, off = 0;
+                if (lane < W && bins[hh] >= 0) {
+                  const int lb = bins[hh] - S.dch[lane];
+                  if (lb >= 0 && lb < S.nbch[lane]) {
+                    off = lb > 0 ? (int)S.pc[lane][lb - 1] : 0;
+                    cnt = (int)S.pc[lane][lb] - off;
+                  }
+                }
+                const int zo_ = (int)wave_incl_scan_u32((uint32_t)cnt) - cnt;
+                n[hh] = __builtin_amdgcn_readlane(zo_ + cnt, WAVE - 1);
+                if (lane < W) {
+                  S.zpo[hh][lane] = off;
+                  S.zpc[hh][lane] = cnt;
+                  S.zpz[hh][lane] = zo_ + (hh ? n[0] : 0);
+                }
+              }
+              cmd.load = 1;
+              cmd.n0 = n[0];
+              cmd.n1 = n[1];
+            }
+          }
+          cmd.c0 = rcum.cnt(bz - 1);
+          cmd.m0 = rcum.mass(bz - 1) - (bz - 1 >= xbn ? xw : 0ull);
+        }
+        cmd.bz = bz;
+        if (lane == 0) S.cmd = cmd;
+      }
+      __syncthreads();
+      const GCmd cmd = S.cmd;
+      if (cmd.op == GOP_FAIL) return false;
+      if (cmd.op == GOP_SKIP) continue;
+      if (cmd.op == GOP_BOUND) {
+        bound = cmd.bmp;
+        continue;
+      }
+      const int bz = cmd.bz;
+      // ---- every wave: the zone ------------------------------------------------------
+      if (cmd.load == 1) {
+        // wave w copies the parts of chunks w, w + GW, ...: from the prefetched
+        // candidates where they lie among them, else from the chunk's slot region
+        for (int cq = w; cq < W; cq += GW) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int o = S.zpo[hh][cq], cn = S.zpc[hh][cq], z0 = S.zpz[hh][cq];
+            for (int i = lane; i < cn; i += WAVE) {
+              const int e = o + i;
+              const Cand x = (pfok && e < PF) ? P.pfb[cq * PF + e] : slots[(int64_t)cq * SLOT + e];
+              if (z0 + i < ZCAP) {
+                G.z.zkey[z0 + i] = ckey(x.l, x.id);
+                G.z.zmass[z0 + i] = rmass(x.l, m);
+              }
+            }
+          }
+        }
+        __syncthreads();
+        zb[0] = bz;
+        zo[0] = 0;
+        zn[0] = cmd.n0;
+        zb[1] = cmd.also;
+        zo[1] = cmd.n0;
+        zn[1] = cmd.n1;
+      } else if (cmd.load == 2) {
+        const int n = collect_zone(xa, r, b, j, p, arow - (float)bz, m,
+                                   ZoneLds{(lds_t<uint64_t>*)G.z.zkey, (lds_t<uint64_t>*)G.z.zmass,
+                                           (lds_t<uint32_t>*)P.ccnt, (lds_t<int>*)&S.misc[2]});
+        pfok = false;  // (the pass's history counts took the prefetched candidates' LDS)
+        if (n < 0) return false;
+        zb[0] = bz;
+        zo[0] = 0;
+        zn[0] = n;
+        zb[1] = -1;
+      }
+      const int h = zb[0] == bz ? 0 : 1;
+      if (cmd.op == GOP_SUM) {
+        // min-p: the kept mass is everything before the bound's bin and the zone's keys
+        // up to the bound
+        bound = cmd.bmp;
+        Sk = cmd.m0 + zone_mass_upto(S, G, zo[h], zn[h], bound);
+        bbin = bz;
+        continue;
+      }
+      // ---- the pick: the key whose cumulative interval contains thr ------------------
+      GHit g;
+      {
+        const int np = npick++;
+        if (zn[h] <= GT)
+          g = pick_rank(S, G, np, zo[h], zn[h], cmd.by_mass != 0, cmd.thr, cmd.bnd, cmd.excl,
+                        cmd.c0, cmd.m0);
+        else  // (a zone wider than the workgroup holds its bin alone, at offset 0: sorted)
+          g = pick_sorted_ool(Sl, Gl, np, zn[h], cmd.by_mass != 0, cmd.thr, cmd.bnd, cmd.excl,
+                              cmd.c0, cmd.m0, m);
+      }
+      if (step == 0) {
+        if (g.key == ~0ull) return false;
+        if (p.flags & STRIM_FLAG_TOPK_KEEP_TIES) {
+          // the keys tied with the k-th one are kept too (same value, same bin)
+          bound = g.key | 0xFFFFFFFFull;
+          Sk = cmd.m0 + zone_mass_upto(S, G, zo[h], zn[h], bound);
+        } else {
+          bound = g.key;
+          Sk = g.mass_before + g.mass;
+        }
+        bbin = bz;
+      } else if (step == 2) {
+        if (g.key != ~0ull) {
+          bound1 = g.key;
+          S1 = g.mass_before + g.mass;
+          bb1 = bz;
+        } else if (bz != bbin) {
+          return false;
+        }
+      } else {
+        if (g.key == ~0ull) return false;
+        token = (int)(uint32_t)g.key;
+      }
+    }
+    if (!icdf) {
+      // Gumbel: every kept candidate (key <= bound1, not the draft)
+      if (bb1 >= rowfull) return false;  // every kept token must be a candidate
+      const bool cand_sorted = (p.flags & STRIM_FLAG_SCORE_NO_LSE) ? topp : (topk || topp);
+      token = gumbel_kept(Sl, slots, a.noise ? a.noise + (int64_t)r * a.noise_stride : nullptr,
+                          W, bb1, bound1, draft, p, m, S1, cand_sorted);
+      if (token < 0) token = arg;  // only the draft kept
+    }
+    const int acc = vdr && ((double)u_acc < (double)wd / (double)S1) ? 1 : 0;
+    finish(STRIM_OK, token, acc, (double)S1 / RFIX, bound1);
+    return true;
+  };
+  if (lat && decide()) return;
+
+  // ---- the exact streaming resolution ----------------------------------------------
+  const XScratch xs = xscratch(G.x.xkey, G.x.xhc, G.x.xcnt, G.x.xu2, S.d, S.u, S.ii);
+  __builtin_amdgcn_s_waitcnt(0);  // (its LDS overlaps the lattice words' and candidates')
   __syncthreads();
   const XOut xo =
-      exact_row<GT, false>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, *(lds_t<XState>*)&S.x);
+      exact_row<GT, false>(xa, r, b, j, p, m, arg, draft, vdr, l_draft, xs, *(lds_t<XState>*)&G.x.x);
   finish(xo.status, xo.token, xo.accept, xo.sig, xo.last_key);
 }
 

@@ -31,10 +31,19 @@ constexpr int FTPB = 256;        // threads of a k_finalize workgroup (one row)
 constexpr int FCAND = 8192;      // candidates per row k_finalize gathers
 constexpr int FCAP = 8192;       // candidate keys k_finalize holds in LDS
 constexpr int FCAP_FAST = 4096;  // of which fast rows use at most this many
-constexpr int GCAP = 32;         // candidates a general row's chunk collects (at most)
-constexpr int GCAP2 = 128;       // and its second tier, after them in the slot region
-constexpr int NCB = 64;          // coarse bins per chunk: width 1/2 over d in [0, 32)
-constexpr float CB_SCALE = 2.0f;
+// General rows bin their tokens on an absolute lattice of l = v / T: bin A(l) =
+// floor(l * LBS), so every chunk of a row bins the same way and the chunks' histograms
+// add up to the row's. A chunk keeps the NBW bins below its top bin A(m_c) (its window,
+// 12 nats), counts and masses per bin, and writes its window tokens in bin order, as
+// many whole bins as fit LCAP entries of its slot region.
+constexpr int LBS = 16;          // lattice bins per nat (a power of two: l * LBS is exact)
+constexpr int NBW = 192;         // window bins of a chunk (and of a row, below its top)
+constexpr int LCAP = 256;        // candidates a general row's chunk writes in bin order
+constexpr int LWMAX = 40;        // chunks of a row k_gfinal's lattice path serves
+                                 // (V <= 163,840; wider rows take the exact resolution)
+constexpr int LCSH = 51;         // a lattice word: count << LCSH | mass (2^37 per unit of
+                                 // exp(l - A / LBS), A the bin's lattice index)
+constexpr uint64_t LMMASK = (1ull << LCSH) - 1ull;
 constexpr int KLOC = 256;        // largest top-k served by local candidates
 constexpr float MINP_FAST = 3.3546262e-4f;  // e^-8: min-p at or above bounds candidates
 
@@ -54,17 +63,17 @@ struct ChunkStat {
   int32_t n;       // allowed tokens (fast and greedy rows: 1 if any)
   int32_t flags;   // bit0: non-finite logit
   float g;         // fast top-k rows: at least k of the chunk's tokens have v >= g (v is
-                   // the value before temperature), -inf when not certified; general
-                   // rows: the largest l the chunk left out of its candidates (-inf
-                   // when every allowed token is a candidate)
+                   // the value before temperature), -inf when not certified
   double S;        // sum exp(l - m) over the chunk (general rows)
   int32_t arg;     // first id reaching m
-  uint32_t ncand;  // candidates in the chunk's slot region (> SLOT: overflow)
-  float g2;        // general rows: the largest l left out of both candidate tiers (-inf
-                   // when every allowed token is in one)
-  uint32_t ncand2; // general rows: second-tier candidates (at GCAP .. GCAP + GCAP2 - 1)
+  uint32_t ncand;  // fast rows: candidates in the chunk's slot region (> SLOT: overflow);
+                   // general rows: window bins whose tokens are all written (nfull)
+  float g2;        // (unused)
+  uint32_t ncand2; // general rows: window bins with lattice words written (nb: the last
+                   // non-empty bin + 1); LNONE when the lattice cannot hold the row
   uint32_t pad_;
 };
+constexpr uint32_t LNONE = 0xFFFFFFFFu;
 static_assert(sizeof(ChunkStat) == 48, "ChunkStat layout");
 
 // Unfiltered Gumbel rows: the chunk's two best tokens by the fp32 Gumbel proxy l + g.
@@ -130,6 +139,9 @@ struct Scratch {
   unsigned long long* qhm;        // [MAXP][wmax][QNB] QRES rows: residual masses per bin
   QStat* qst;                     // [rows] per draft row (b * k + j)
   QPart* qpp;                     // [MAXP][QSPLIT] k_qprep slices, merged by k_finalize
+  unsigned long long* lat;        // [rows][wmax][NBW] general rows: per window bin of the
+                                  // chunk, its inclusive count prefix << LCSH | its mass
+                                  // (2^37 per unit of exp(l - A / LBS), A the bin's index)
   int32_t wmax;
 };
 

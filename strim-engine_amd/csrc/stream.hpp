@@ -24,16 +24,17 @@ template <int SSEG>
 constexpr int stpb() { return CHUNK / (EPT * SSEG); }
 
 // LDS of one k_stream workgroup of NW waves (the history table only in the penalties
-// variants and the coarse histograms only in the variants with general rows, so the
+// variants and the lattice histogram only in the variants with general rows, so the
 // narrow workgroups of large launches fit many to a CU).
-constexpr int HCQ = 4;  // copies of the coarse histogram per wave (one per 16 lanes)
 template <int PEN, int NW, bool GEN>
 struct StreamShared {
   // history counts of the chunk's tokens: 32 bits each (16 KB), or 16 bits (8 KB) when
   // the host knows no count reaches 65,536
   uint32_t cnt[PEN == 1 ? CHUNK : PEN == 2 ? CHUNK / 2 : 4];
-  uint32_t hc[GEN ? NW : 1][NCB][HCQ];  // general rows: coarse counts, one copy per
-                                        // quarter wave (spreads the atomics' contention)
+  // general rows: the window's lattice bins (count << LCSH | mass), then each bin's
+  // exclusive count prefix (its first entry in the chunk's slot region)
+  unsigned long long lat[GEN ? NBW : 1];
+  uint32_t lpre[GEN ? NBW : 1];
   uint32_t lad[2 * WAVE];
   float v[SMAXW];
   int i[SMAXW], n[SMAXW], f[SMAXW];
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   if (fast && topk)
     for (int q = t; q < VRUNG; q += STPB) S.lad[q] = 0u;
   if (GEN && p.cls == CLS_GENERAL)
-    for (int q = t; q < NW * NCB; q += STPB) ((uint4*)&S.hc[0][0][0])[q] = make_uint4(0u, 0u, 0u, 0u);
+    for (int q = t; q < NBW; q += STPB) S.lat[q] = 0ull;
   if (pen) hist_count<STPB, CHUNK, Args, PEN == 2>(a, b, j, c0, hid, hl, S.cnt);
 
   // ---- penalties and mask, before temperature ("v space") ------------------------
@@ -438,29 +439,35 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
     }
     cs_ncand = tot <= SLOT ? (uint32_t)tot : 0xFFFFFFFFu;
   } else if (GEN && p.cls == CLS_GENERAL && live) {
-    // Chunk mass sum exp(l - m_w) and a coarse histogram of counts of m_w - l (which bins
-    // the chunk's candidates come from). The bins are taken in v space, dv CB_SCALE / T
-    // with dv = vm - v: they only have to be one consistent assignment of the tokens, as
-    // the certificate below is taken over exact l. The mass needs l to its float rounding
-    // (a term's relative error is that of its exponent, which is |l| times the rounding),
-    // so l is formed as v / T by one FMA correction of v * RN(1/T), correctly rounded
-    // but for rare last-bit cases that move a term by an ulp of l; the exponential is
-    // 2^((l - m_w) log2(e)), a sum of positive terms good to a few 1e-7 relative. The
-    // exact quotient v / T is formed only for the candidates written and the largest
-    // left-out value. General-q draft rows keep the sum alone (the residual draw takes the
-    // row's mass from the chunks' sums and makes its own passes, qres_kernels.hip), and
-    // unfiltered Gumbel rows are decided from the chunks' two best tokens and the sum;
-    // only the other general rows need the histogram.
+    // Chunk mass sum exp(l - m_w) and, for the rows k_gfinal decides, the chunk's lattice
+    // histogram and its window tokens in bin order. The mass needs l to its float
+    // rounding (a term's relative error is that of its exponent, which is |l| times the
+    // rounding), so l is formed as v / T by one FMA correction of v * RN(1/T), correctly
+    // rounded but for rare last-bit cases that move a term by an ulp of l; the
+    // exponential is 2^((l - m_w) log2(e)), a sum of positive terms good to a few 1e-7
+    // relative. A token's lattice bin A(l) = floor(l * LBS) needs the exact quotient (an
+    // ulp off at a bin edge would put it in the neighbouring bin, out of order), which is
+    // formed for the tokens near or inside the window only. General-q draft rows keep the
+    // sum alone (the residual draw takes the row's mass from the chunks' sums and makes
+    // its own passes, qres_kernels.hip), and unfiltered Gumbel rows are decided from the
+    // chunks' two best tokens and the sum.
     const bool qdraft = a.dlog && a.verify && j < a.k;
     const bool gum_nf = !qdraft && a.noise_mode == STRIM_NOISE_GUMBEL && row_nofilter(p, a.V);
     const float yT = 1.0f / p.T;
     // the FMA quotient needs 1/T and its products far from the float range's ends
     const bool fq = p.T > 0x1p-100f && p.T < 0x1p+100f;
-    const float kb = CB_SCALE * yT;
-    const int hq = lane >> 4;
+    // the window: lattice bins atop - NBW + 1 .. atop (every bin index an exact float)
+    const float atop = floorf(m_w * (float)LBS);
+    const bool latr = !qdraft && !gum_nf && fabsf(atop) < 0x1p+23f;
+    const float lwin = (atop - (float)(NBW - 1)) * (1.0f / (float)LBS);
+    // the FMA quotient is within an ulp of l: tokens whose quotient reaches this bound
+    // get the exact one
+    const float lwin_lo = lwin - (fabsf(lwin) * 1e-6f + 1e-30f);
     double ssum = 0.0;
     int na = 0;
-    int bin[SSEG][EPT];
+    // window tokens: lb = atop - A(l) in [0, NBW), -1 otherwise; the fixed-point mass word
+    int lbw[SSEG][EPT];
+    uint64_t wword[SSEG][EPT];
 #pragma unroll
     for (int s = 0; s < SSEG; ++s) {
       float es = 0.0f, eh = 0.0f;  // two float partial sums of four terms, each <= 1
@@ -478,17 +485,43 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
         const float ex = __builtin_amdgcn_exp2f(fmaxf((le - m_w) * 1.44269504f, -200.0f));
         if (e < EPT / 2) es += ex; else eh += ex;
         na += ve > -INFINITY ? 1 : 0;
-        const float db = (vm - ve) * kb;  // +inf for tokens not allowed
-        bin[s][e] = db < (float)(NCB - 1) ? (int)db : NCB - 1;
+        lbw[s][e] = -1;
+        wword[s][e] = 0ull;
+        if (latr && le >= lwin_lo && ve > -INFINITY) {
+          const float l = ve / p.T;  // exact
+          const float d = atop - floorf(l * (float)LBS);
+          if (d < (float)NBW) {
+            lbw[s][e] = (int)d;
+            v[s][e] = l;  // the value written with the candidate
+            // the term relative to its bin's base, exp(l - A(l) / LBS) in [1, e^(1/LBS)):
+            // every chunk's bin at A has the same unit, so the chunks' bins add as
+            // integers and are scaled to the row's maximum once per row bin
+            const float lbase = (atop - d) * (1.0f / (float)LBS);
+            const float ew = __builtin_amdgcn_exp2f((l - lbase) * 1.44269504f);
+            wword[s][e] = (1ull << LCSH) | (uint64_t)(ew * 0x1p37f);
+          }
+        }
       }
       ssum += (double)es + (double)eh;
     }
-    if (!gum_nf && !qdraft) {
+    // the window tokens into the histogram; the atomic's old count is the token's place
+    // in its bin (every atomic is issued before any result is read)
+    uint32_t lrank[SSEG][EPT];
+    if (latr) {
+      uint64_t old[SSEG][EPT];
 #pragma unroll
       for (int s = 0; s < SSEG; ++s)
 #pragma unroll
         for (int e = 0; e < EPT; ++e)
-          if (v[s][e] > -INFINITY) atomicAdd(&S.hc[w][bin[s][e]][hq], 1u);
+          if (lbw[s][e] >= 0) old[s][e] = atomicAdd(&S.lat[lbw[s][e]], (unsigned long long)wword[s][e]);
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) asm volatile("" : "+v"(old[s][e]));
+#pragma unroll
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) lrank[s][e] = (uint32_t)(old[s][e] >> LCSH);
     }
     // the sums of the waves, one barrier (the histogram's atomics are complete after it)
     ssum = wave_sum(ssum);
@@ -505,96 +538,61 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
       cs.S += S.d[q];
       cs.n += S.n[q];
     }
-    // unfiltered Gumbel rows: the chunk's two best tokens decide the draw directly
-    if (qdraft) {
-      // the sum alone
-    } else if (!gum_nf) {
-      // The chunk's candidates: the tokens of its first coarse bins, as many bins as keep
-      // them within GCAP, written as (l, id) to the chunk's slot region in wave order.
-      // cs.g is the largest l left out (-inf when every allowed token is a candidate):
-      // every token of the chunk with l > cs.g is a candidate, so k_gfinal can decide the
-      // row from the candidates alone when its decisions fall above the largest cs.g of
-      // the row. A second tier, the tokens of the following bins while they number at
-      // most GCAP2, goes to the region's entries from GCAP on, with cs.g2 the largest l
-      // left out of both tiers: k_gfinal reads it only when a decision falls at or below
-      // the row's largest cs.g. The largest left-out l is found as the largest left-out v
-      // divided by T: rounded division by T > 0 is monotone.
-      uint32_t hsum = 0u;
+    if (latr) {
+      // wave 0: the bins' exclusive count prefixes, the bins written whole (nfull: the
+      // bins whose inclusive prefix stays within LCAP) and the last non-empty bin; the
+      // lattice words (inclusive prefix << LCSH | mass) of bins 0 .. nb - 1 to scratch
+      constexpr int LPL = NBW / WAVE;  // bins per lane
+      static_assert(NBW % WAVE == 0, "whole bins per lane");
+      if (w == 0) {
+        uint64_t hw[LPL];
+        uint32_t hc[LPL], tot = 0u;
 #pragma unroll
-      for (int q = 0; q < NW; ++q) {
-        const uint4 h4 = *(const uint4*)&S.hc[q][lane][0];
-        hsum += h4.x + h4.y + h4.z + h4.w;
-      }
-      const uint32_t hcum = wave_incl_scan_u32(hsum);
-      const int bstar = __popcll(__ballot(hcum <= (uint32_t)GCAP)) - 1;  // -1: no bin fits
-      const uint32_t cum1 =
-          bstar >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)hcum, bstar) : 0u;
-      const int bstar2 = __popcll(__ballot(hcum <= cum1 + (uint32_t)GCAP2)) - 1;
-      uint32_t sel[SSEG], sel2[SSEG];
-      float umax = -INFINITY, umax2 = -INFINITY;
-      int mycnt = 0, mycnt2 = 0;
-#pragma unroll
-      for (int s = 0; s < SSEG; ++s) {
-        sel[s] = 0u;
-        sel2[s] = 0u;
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-          const float ve = v[s][e];
-          const int bb = bin[s][e];
-          const bool live_e = ve > -INFINITY;
-          const bool take = live_e && bb <= bstar;
-          const bool take2 = live_e && !take && bb <= bstar2;
-          sel[s] |= (take ? 1u : 0u) << e;
-          sel2[s] |= (take2 ? 1u : 0u) << e;
-          mycnt += take ? 1 : 0;
-          mycnt2 += take2 ? 1 : 0;
-          umax = fmaxf(umax, take ? -INFINITY : ve);
-          umax2 = fmaxf(umax2, take || take2 ? -INFINITY : ve);
+        for (int q = 0; q < LPL; ++q) {
+          hw[q] = S.lat[LPL * lane + q];
+          hc[q] = (uint32_t)(hw[q] >> LCSH);
+          tot += hc[q];
         }
-      }
-      constexpr int CB = SSEG == 1 ? 4 : SSEG == 2 ? 5 : SSEG == 4 ? 6 : 7;
-      int wtot, wtot2;
-      const int wex = wave_excl_count_bits<CB>(mycnt, &wtot);
-      const int wex2 = wave_excl_count_bits<CB>(mycnt2, &wtot2);
-      umax = wave_max_f(umax);
-      umax2 = wave_max_f(umax2);
-      if (lane == 0) {
-        S.off[w] = (uint32_t)wtot;
-        S.off2[w] = (uint32_t)wtot2;
-        S.tf[w] = umax;
-        S.tf[SMAXW + w] = umax2;
+        uint32_t run = wave_incl_scan_u32(tot) - tot;
+        int nfull = 0, nbl = 0;
+        unsigned long long* lw = a.s.lat + ((int64_t)r * a.s.wmax + c) * NBW;
+#pragma unroll
+        for (int q = 0; q < LPL; ++q) {
+          const int bq = LPL * lane + q;
+          S.lpre[bq] = run;
+          run += hc[q];
+          nfull += run <= (uint32_t)LCAP ? 1 : 0;
+          nbl = hc[q] > 0u ? bq + 1 : nbl;
+          hw[q] = ((uint64_t)run << LCSH) | (hw[q] & LMMASK);
+        }
+        nfull = wave_sum(nfull);
+        nbl = wave_max_i(nbl);
+#pragma unroll
+        for (int q = 0; q < LPL; ++q)
+          if (LPL * lane + q < nbl) lw[LPL * lane + q] = hw[q];
+        if (lane == 0) {
+          S.i[0] = nfull < nbl ? nfull : nbl;
+          S.i[1] = nbl;
+        }
       }
       __syncthreads();
-      uint32_t before = 0u, tot = 0u, before2 = 0u, tot2 = 0u;
-      float um = -INFINITY, um2 = -INFINITY;
-#pragma unroll
-      for (int q = 0; q < NW; ++q) {
-        before += q < w ? S.off[q] : 0u;
-        tot += S.off[q];
-        before2 += q < w ? S.off2[q] : 0u;
-        tot2 += S.off2[q];
-        um = fmaxf(um, S.tf[q]);
-        um2 = fmaxf(um2, S.tf[SMAXW + q]);
-      }
+      const int nfull = S.i[0];
+      // the window tokens of bins 0 .. nfull - 1 as (l, id), at their bin's prefix plus
+      // their place in it
       Cand* dst = a.s.slot + ((int64_t)r * a.s.wmax + c) * SLOT;
-      int pos = (int)before + wex, pos2 = GCAP + (int)before2 + wex2;
 #pragma unroll
-      for (int s = 0; s < SSEG; ++s) {
-        // one loop over both tiers' tokens (a token is in at most one)
-        uint32_t msk = sel[s] | sel2[s];
-        while (msk) {
-          const int e = __builtin_ctz(msk);
-          msk &= msk - 1u;
-          const bool t1 = (sel[s] >> e) & 1u;
-          dst[t1 ? pos : pos2] = Cand{pick8(v[s], e) / p.T, i0[s] + e};
-          pos += t1 ? 1 : 0;
-          pos2 += t1 ? 0 : 1;
-        }
-      }
-      cs_ncand = tot;
-      cs.g = um > -INFINITY ? um / p.T : -INFINITY;
-      cs_ncand2 = tot2;
-      cs.g2 = um2 > -INFINITY ? um2 / p.T : -INFINITY;
+      for (int s = 0; s < SSEG; ++s)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          if (lbw[s][e] >= 0 && lbw[s][e] < nfull)
+            dst[S.lpre[lbw[s][e]] + lrank[s][e]] = Cand{v[s][e], i0[s] + e};
+      cs_ncand = (uint32_t)nfull;
+      cs_ncand2 = (uint32_t)S.i[1];
+    } else if (!qdraft && !gum_nf) {
+      cs_ncand2 = LNONE;  // the lattice cannot hold the row: k_gfinal resolves it exactly
+    }
+    if (qdraft || !gum_nf) {
+      // the sum alone (qdraft), or the lattice above
     } else {
       // the fp32 proxy scores take l to its float rounding (the FMA-corrected quotient);
       // the tokens the chunk keeps are divided exactly when they are written
