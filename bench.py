@@ -274,8 +274,10 @@ def grammar_mask_bench(torch, dev, args):
     8 rows per launch in a string's in-string state, where nearly every token walks all
     its bytes, for a JSON-string DFA (4 states: the walk reads an LDS copy of the table)
     and a JSON-object DFA (22 states: the walk reads the table through the caches).
-    "produce" runs with the mask cache off (every launch walks the vocabulary), "cached"
-    with it on (every launch after the first copies the rows)."""
+    "produce" runs with the mask cache off (every launch walks the vocabulary once for the
+    8 equal keys and writes the words to the 8 rows), "cached" with it on (every launch
+    after the first copies the rows); "produce_distinct" walks 8 different states of the
+    JSON-object DFA per launch."""
     from strim_amd import workloads as W
     from strim_amd.grammar import DeviceGrammar
 
@@ -289,34 +291,46 @@ def grammar_mask_bench(torch, dev, args):
         out = {}
         for name, cache in (("produce", 0), ("cached", 4 if dfa == "json_string" else 32)):
             g = DeviceGrammar(toks, W.V_DEFAULT, eos=W.GRAMMAR_EOS, skip=skip,
-                              cache_states=cache)
+                              cache_slots=cache)
             g.set_dfa(nt, fl)
             out[name] = _grammar_launch_us(torch, g, keys, steps)
+            g.close()
+        if dfa == "json_object":
+            con = [i for i in range(nt.shape[0]) if fl[i] & 2][:GRAMMAR_ROWS]
+            kd = torch.tensor(con, dtype=torch.int32, device=dev)
+            g = DeviceGrammar(toks, W.V_DEFAULT, eos=W.GRAMMAR_EOS, skip=skip, cache_slots=0)
+            g.set_dfa(nt, fl)
+            out["produce_distinct"] = _grammar_launch_us(torch, g, kd, steps)
+            out["distinct_rows"] = len(con)
             g.close()
         res[dfa] = out
         log(f"[bench] grammar masks ({dfa}, {nt.shape[0]} states): produce "
             f"{out['produce']:.2f} us/launch, cached {out['cached']:.2f} us/launch "
-            f"({GRAMMAR_ROWS} rows)")
+            f"({GRAMMAR_ROWS} rows of one state)"
+            + (f"; {out['distinct_rows']} distinct states produced "
+               f"{out['produce_distinct']:.2f} us/launch" if "produce_distinct" in out else ""))
     words = (W.V_DEFAULT + 31) // 32
-    # algorithmic bytes per row: each token's 16-byte head and 8-byte meta, the words out
-    row_bytes = len(toks) * 24 + words * 4
+    # algorithmic bytes of a launch: each token's 16-byte head and 8-byte meta read once
+    # (the 8 equal keys are walked once), the words of every row written
+    launch_bytes = len(toks) * 24 + words * 4 * GRAMMAR_ROWS
     out = res["json_string"]
-    gbs = row_bytes * GRAMMAR_ROWS / (out["produce"] * 1e-6) / 1e9
+    gbs = launch_bytes / (out["produce"] * 1e-6) / 1e9
     oo = res["json_object"]
     return {"workload": f"strim_grammar_masks: {GRAMMAR_ROWS} rows x V=151936, 151665 byte "
                         "strings (mean 6.5 bytes), JSON-string DFA, in-string state",
             "produce_us_per_launch": round(out["produce"], 3),
             "cached_us_per_launch": round(out["cached"], 3),
-            "produce_us_per_row": round(out["produce"] / GRAMMAR_ROWS, 3),
             "roofline_produce": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0,
                                  "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
-                                 "row_bytes": row_bytes},
+                                 "launch_bytes": launch_bytes},
             "json_object_dfa": {
                 "workload": f"{GRAMMAR_ROWS} rows, 22-state JSON-object DFA "
                             "({\"name\":\"<string>\",\"age\":<integer>}), in-string state; "
                             "the table is walked through the caches",
                 "produce_us_per_launch": round(oo["produce"], 3),
-                "cached_us_per_launch": round(oo["cached"], 3)}}
+                "cached_us_per_launch": round(oo["cached"], 3),
+                "produce_distinct_us_per_launch": round(oo["produce_distinct"], 3),
+                "distinct_states": oo["distinct_rows"]}}
 
 
 def cpu_baseline_grammar(seconds: float):

@@ -14,8 +14,20 @@
  *               when the state consumes, plus the end-of-turn ids when it accepts;
  *   key == -1   free: every token below width allowed;
  *   key <= -2   forced: only token (-2 - key) allowed (the thinking-budget close id).
- * A state at or above the DFA's state count gives an all-zero row, which strim_sample
+ * A state at or above the table's state count gives an all-zero row, which strim_sample
  * reports as STRIM_EEMPTY.
+ *
+ * One table holds every program's states (state ids are global), so a batch whose
+ * requests follow different grammars takes its masks from one call. The table grows:
+ * strim_grammar_append_states adds states without touching the cached masks, and a
+ * transition may be left unknown (STRIM_DFA_UNKNOWN) until the host has interned its
+ * target, as the reference's lazily built DFA does (GrammarDFA.swift:36-58). A walk that
+ * meets an unknown transition records the (state, byte) pair; strim_grammar_pending hands
+ * the pairs to the host, which interns the targets and fills the entries with
+ * strim_grammar_set_next. A mask row whose walk met one is incomplete (it is not cached,
+ * and its bits for the tokens that met one are 0) and must be produced again after the
+ * pairs are filled; a key walk that meets one gives STRIM_GRAMMAR_UNRESOLVED, a key whose
+ * row is all zero.
  *
  * All calls are stream-ordered; keys, tokens and outputs are device memory. Calls on one
  * strim_grammar must not overlap (issue them on one stream): a mask call reads the cached
@@ -37,6 +49,9 @@ typedef struct strim_grammar strim_grammar;
 
 #define STRIM_DFA_ACCEPTING 1 /* flags bit: the state may end (GrammarDFA.accepting)     */
 #define STRIM_DFA_CONSUMING 2 /* flags bit: the state can take bytes (GrammarDFA.consuming) */
+#define STRIM_DFA_DEAD (-1)    /* table entry: the byte kills every stack                  */
+#define STRIM_DFA_UNKNOWN (-2) /* table entry: not interned yet (GrammarDFA.unknown)       */
+#define STRIM_GRAMMAR_UNRESOLVED 0x7FFFFFFF /* key after an unknown transition (zero row) */
 
 /* Uploads the vocabulary (replaces GrammarVocab.init, GrammarVocab.swift:16-51, and the
  * GrammarEngine construction, GrammarVocab.swift:116-130).
@@ -46,28 +61,62 @@ typedef struct strim_grammar strim_grammar;
  *               (control tokens); empty byte strings never appear either
  *   width       logits width, the mask's bit count (ids at or above width are dropped)
  *   eos, n_eos  host end-of-turn ids, allowed in an accepting state's mask
- *   cache_states  states whose mask rows are cached in HBM (width / 8 bytes each);
- *               states at or above it are produced on every call
- * The DFA is empty until strim_grammar_set_dfa. */
+ *   cache_slots mask rows kept in HBM (width / 8 bytes each: the cache's byte budget,
+ *               as the reference bounds its masks, GrammarVocab.swift:124,150-156, and
+ *               DeviceMasks.capacity, RequestConstraint.swift:12,35-43). Any state may
+ *               occupy a slot, block by block: state s maps to the two slots of set
+ *               s mod (cache_slots / 2) and replaces the one stored first (DeviceMasks'
+ *               insertion order), except a slot holding a state that the same call
+ *               reads. 0 or 1: no cache
+ * The table is empty until strim_grammar_set_dfa or strim_grammar_append_states. */
 int strim_grammar_create(strim_grammar** out, int32_t device, int32_t count,
                          const uint32_t* offsets, const uint8_t* bytes, const uint8_t* skip,
                          int32_t width, const int32_t* eos, int32_t n_eos,
-                         int32_t cache_states);
+                         int32_t cache_slots);
 int strim_grammar_destroy(strim_grammar* g);
 
-/* Installs a DFA (replaces the compiled GrammarDFA of GrammarRuntime.init,
- * GrammarVocab.swift:57-69, GrammarDFA.swift:13-58) and clears the mask cache.
- *   next   host [n_states][256]: the state after byte b, -1 = dead. Every entry must be
- *          materialised (the reference's lazily expanded -2 entries are rejected)
+/* Replaces the whole table with one DFA (the compiled GrammarDFA of GrammarRuntime.init,
+ * GrammarVocab.swift:57-69, GrammarDFA.swift:13-58) and clears the mask cache and the
+ * pending pairs.
+ *   next   host [n_states][256]: the state after byte b, STRIM_DFA_DEAD, or
+ *          STRIM_DFA_UNKNOWN
  *   flags  host [n_states]: STRIM_DFA_ACCEPTING | STRIM_DFA_CONSUMING
- * Returns STRIM_EINVAL for an entry outside [-1, n_states) or more than 2^23 states. */
+ * Returns STRIM_EINVAL for an entry outside [-2, n_states) or more than 2^23 states. */
 int strim_grammar_set_dfa(strim_grammar* g, void* stream, int32_t n_states,
                           const int32_t* next, const uint8_t* flags);
+
+/* Appends n_new states to the table (GrammarDFA.intern, GrammarDFA.swift:47-58, for one
+ * or several programs): they take ids first .. first + n_new - 1, with *first_out =
+ * first = the previous state count. Cached masks stay valid (a known entry never
+ * changes). next host [n_new][256] with entries in [-2, first + n_new) (global ids),
+ * flags host [n_new]. Returns STRIM_EINVAL for a bad entry, STRIM_ECAPACITY past 2^23
+ * states. Synchronises the stream. */
+int strim_grammar_append_states(strim_grammar* g, void* stream, int32_t n_new,
+                                const int32_t* next, const uint8_t* flags, int32_t* first_out);
+
+/* Fills unknown entries (GrammarDFA.next memoising a transition, GrammarDFA.swift:36-45):
+ * entry where[i] = state * 256 + byte becomes to[i] (a state id or STRIM_DFA_DEAD). Only
+ * an unknown entry may change; setting a known entry to another value fails with
+ * STRIM_EINVAL (cached masks depend on it) and sets nothing. where, to host [n].
+ * Synchronises the stream. */
+int strim_grammar_set_next(strim_grammar* g, void* stream, int32_t n, const int64_t* where,
+                           const int32_t* to);
+
+/* The unknown transitions that walks met since the last call: up to cap entries
+ * state * 256 + byte into out (host), *n_out = how many were recorded (each pair once;
+ * more than cap: call again after filling these). The pairs handed out are forgotten;
+ * a walk that meets one again records it again. Synchronises the stream. */
+int strim_grammar_pending(strim_grammar* g, void* stream, int64_t* out, int32_t cap,
+                          int32_t* n_out);
+
+/* Forgets the cached mask rows of states [first, first + n) (GrammarEngine.trim dropping
+ * a program's masks, GrammarVocab.swift:150-156); their slots are reused first. */
+int strim_grammar_drop_masks(strim_grammar* g, void* stream, int32_t first, int32_t n);
 
 /* Mask rows for n keys (replaces GrammarRuntime.mask, GrammarVocab.swift:75-102, and
  * DeviceMasks.allowed / only / all with their bool expansion,
  * RequestConstraint.swift:16-58): out[r][0 .. ceil(width / 32)) packed words, out_stride
- * words apart. keys device [n]. */
+ * words apart. keys device [n]. Rows with equal keys are produced once and copied. */
 int strim_grammar_masks(strim_grammar* g, void* stream, const int32_t* keys, int32_t n,
                         uint32_t* out, int64_t out_stride);
 

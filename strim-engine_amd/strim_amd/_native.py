@@ -41,6 +41,10 @@ EXPORTS = (
     "strim_grammar_create",
     "strim_grammar_destroy",
     "strim_grammar_set_dfa",
+    "strim_grammar_append_states",
+    "strim_grammar_set_next",
+    "strim_grammar_pending",
+    "strim_grammar_drop_masks",
     "strim_grammar_masks",
     "strim_grammar_advance",
     "strim_request_keys",
@@ -146,6 +150,14 @@ def lib() -> ctypes.CDLL:
         L.strim_grammar_destroy.argtypes = [P]
         L.strim_grammar_set_dfa.restype = ctypes.c_int
         L.strim_grammar_set_dfa.argtypes = [P, P, I32, P, P]
+        L.strim_grammar_append_states.restype = ctypes.c_int
+        L.strim_grammar_append_states.argtypes = [P, P, I32, P, P, ctypes.POINTER(ctypes.c_int32)]
+        L.strim_grammar_set_next.restype = ctypes.c_int
+        L.strim_grammar_set_next.argtypes = [P, P, I32, P, P]
+        L.strim_grammar_pending.restype = ctypes.c_int
+        L.strim_grammar_pending.argtypes = [P, P, P, I32, ctypes.POINTER(ctypes.c_int32)]
+        L.strim_grammar_drop_masks.restype = ctypes.c_int
+        L.strim_grammar_drop_masks.argtypes = [P, P, I32, I32]
         L.strim_grammar_masks.restype = ctypes.c_int
         L.strim_grammar_masks.argtypes = [P, P, P, I32, P, I64]
         L.strim_grammar_advance.restype = ctypes.c_int

@@ -12,6 +12,16 @@ Per-request constraint state (RequestConstraint.State with its budget and close 
 RequestConstraint.swift:62-109) is a device tensor of REQUEST_STATE rows: `request_keys`
 gives the next-token and verify-row keys (the thinking budget's forced close id included)
 and `request_advance` steps the states by the emitted tokens, both on the device.
+
+Several grammars share one device table (GrammarEngine's programs,
+GrammarVocab.swift:116-147): `add_program` registers a host DFA that interns its states
+lazily (the GrammarDFA interface: `start`, `next(s, b)`, `accepting(s)`,
+`consuming(s)`, GrammarDFA.swift:13-58). Its states enter the table as the device walks
+reach them: a walk that meets a transition not interned yet reports it, the host asks the
+program for the target and appends or fills the table, and the masks are produced again
+(`masks` and `request_keys` run that loop while programs are registered). At most
+`max_programs` programs keep cached masks; the least recently used one's masks are
+dropped (GrammarEngine.runtime and trim, GrammarVocab.swift:132-156).
 """
 from __future__ import annotations
 
@@ -25,6 +35,9 @@ from . import _native as N
 FREE = -1
 ACCEPTING = 1  # STRIM_DFA_ACCEPTING
 CONSUMING = 2  # STRIM_DFA_CONSUMING
+DEAD = -1  # STRIM_DFA_DEAD
+UNKNOWN = -2  # STRIM_DFA_UNKNOWN: a table entry not interned yet
+UNRESOLVED = 0x7FFFFFFF  # STRIM_GRAMMAR_UNRESOLVED: a key walk met an UNKNOWN entry
 
 
 # strim_request_state: {g, in_think, count, budget, close_id, violated}
@@ -72,16 +85,32 @@ def _stream(stream):
     return ctypes.c_void_p(s.cuda_stream)
 
 
+class _Program:
+    """A registered host DFA: its local states' global ids, and the inverse."""
+
+    def __init__(self, key, dfa):
+        self.key = key
+        self.dfa = dfa
+        self.glob = {}  # local state -> global id
+        self.ranges = []  # (first, n) of its appended global ids
+        self.last_used = 0
+        self.resident = True  # its masks may be cached
+
+
 class DeviceGrammar:
-    """Vocabulary + DFA + mask cache on one GPU.
+    """Vocabulary + DFA table + mask cache on one GPU.
 
     tokens: byte strings per id (GrammarEngine.tokenBytes); width: logits width; eos: the
     end-of-turn ids; skip: ids never in a grammar mask (control tokens);
-    cache_states: states whose masks stay cached in HBM (width / 8 bytes each).
+    cache_slots: mask rows kept in HBM (width / 8 bytes each), the cache's budget; the
+    default holds the reference's 32 MB mask budget at width 151,936
+    (GrammarVocab.swift:124).
     """
 
+    MAX_PROGRAMS = 16  # GrammarEngine.maxPrograms (GrammarVocab.swift:123)
+
     def __init__(self, tokens, width: int, eos=(), skip=None, device: int = 0,
-                 cache_states: int = 1024):
+                 cache_slots: int | None = None, max_programs: int = MAX_PROGRAMS):
         self.count = len(tokens)
         self.width = int(width)
         self.words = (self.width + 31) // 32
@@ -95,13 +124,19 @@ class DeviceGrammar:
         if sk is not None and sk.shape != (self.count,):
             raise ValueError("skip must have one entry per token")
         ev = np.ascontiguousarray(list(eos), dtype=np.int32)
+        if cache_slots is None:
+            cache_slots = max(2, (32 << 20) // (self.words * 4))
         h = ctypes.c_void_p()
         N.check(N.lib().strim_grammar_create(ctypes.byref(h), device, self.count,
                                              _np_ptr(offsets), _np_ptr(data), _np_ptr(sk),
-                                             self.width, _np_ptr(ev), len(ev), cache_states),
+                                             self.width, _np_ptr(ev), len(ev), cache_slots),
                 "strim_grammar_create")
         self._h = h
         self.n_states = 0
+        self.max_programs = int(max_programs)
+        self._programs = {}  # key -> _Program
+        self._owner = {}  # global id -> (program, local state)
+        self._tick = 0
 
     @property
     def handle(self):
@@ -120,20 +155,134 @@ class DeviceGrammar:
         except Exception:
             pass
 
-    def set_dfa(self, next_table, flags, stream=None) -> None:
-        """Installs a fully materialised DFA: next_table [S][256] (-1 dead), flags [S]."""
+    @staticmethod
+    def _table(next_table, flags):
         nt = np.ascontiguousarray(next_table, dtype=np.int32)
         fl = np.ascontiguousarray(flags, dtype=np.uint8)
         if nt.ndim != 2 or nt.shape[1] != 256 or fl.shape != (nt.shape[0],):
             raise ValueError("next_table must be [S][256] and flags [S]")
+        return nt, fl
+
+    def set_dfa(self, next_table, flags, stream=None) -> None:
+        """Replaces the table with one DFA: next_table [S][256] (DEAD, UNKNOWN or a
+        state), flags [S]. Registered programs are forgotten."""
+        nt, fl = self._table(next_table, flags)
         N.check(N.lib().strim_grammar_set_dfa(self.handle, _stream(stream), nt.shape[0],
                                               _np_ptr(nt), _np_ptr(fl)),
                 "strim_grammar_set_dfa")
         self.n_states = nt.shape[0]
+        self._programs.clear()
+        self._owner.clear()
+
+    def append_states(self, next_table, flags, stream=None) -> int:
+        """Appends states (entries are global ids, DEAD or UNKNOWN); returns the first
+        new id. Cached masks stay."""
+        nt, fl = self._table(next_table, flags)
+        first = ctypes.c_int32()
+        N.check(N.lib().strim_grammar_append_states(self.handle, _stream(stream), nt.shape[0],
+                                                    _np_ptr(nt), _np_ptr(fl),
+                                                    ctypes.byref(first)),
+                "strim_grammar_append_states")
+        self.n_states += nt.shape[0]
+        return int(first.value)
+
+    def set_next(self, where, to, stream=None) -> None:
+        """Fills UNKNOWN entries: entry where[i] (state * 256 + byte) becomes to[i]."""
+        w = np.ascontiguousarray(where, dtype=np.int64)
+        t = np.ascontiguousarray(to, dtype=np.int32)
+        if w.shape != t.shape or w.ndim != 1:
+            raise ValueError("where and to must be 1-D of one length")
+        N.check(N.lib().strim_grammar_set_next(self.handle, _stream(stream), w.size,
+                                               _np_ptr(w), _np_ptr(t)),
+                "strim_grammar_set_next")
+
+    def pending(self, cap: int = 1 << 16, stream=None) -> np.ndarray:
+        """The UNKNOWN entries (state * 256 + byte) walks met since the last call."""
+        out = np.empty(cap, dtype=np.int64)
+        n = ctypes.c_int32()
+        N.check(N.lib().strim_grammar_pending(self.handle, _stream(stream), _np_ptr(out), cap,
+                                              ctypes.byref(n)),
+                "strim_grammar_pending")
+        return out[:n.value].copy()
+
+    def drop_masks(self, first: int, n: int, stream=None) -> None:
+        """Forgets the cached masks of states [first, first + n)."""
+        N.check(N.lib().strim_grammar_drop_masks(self.handle, _stream(stream), int(first),
+                                                 int(n)),
+                "strim_grammar_drop_masks")
+
+    # ---- programs: lazily interned DFAs in the shared table ----------------------
+    def _intern(self, prog: _Program, locals_, stream=None):
+        """Appends the program's local states not in the table yet (rows all UNKNOWN)."""
+        new = [s for s in dict.fromkeys(locals_) if s not in prog.glob]
+        if not new:
+            return
+        fl = np.array([(ACCEPTING if prog.dfa.accepting(s) else 0)
+                       | (CONSUMING if prog.dfa.consuming(s) else 0) for s in new], np.uint8)
+        nt = np.full((len(new), 256), UNKNOWN, dtype=np.int32)
+        first = self.append_states(nt, fl, stream)
+        prog.ranges.append((first, len(new)))
+        for i, s in enumerate(new):
+            prog.glob[s] = first + i
+            self._owner[first + i] = (prog, s)
+
+    def add_program(self, key, dfa, stream=None) -> int:
+        """Registers (or touches) the program `key` served by the host DFA `dfa`;
+        returns the global id of its start state. Past max_programs programs, the least
+        recently used one's cached masks are dropped (its states stay resolvable)."""
+        self._tick += 1
+        prog = self._programs.get(key)
+        if prog is None:
+            prog = _Program(key, dfa)
+            self._programs[key] = prog
+            self._intern(prog, [dfa.start], stream)
+        prog.last_used = self._tick
+        prog.resident = True
+        resident = [p for p in self._programs.values() if p.resident]
+        if len(resident) > self.max_programs:
+            old = min(resident, key=lambda p: p.last_used)
+            for first, n in old.ranges:
+                self.drop_masks(first, n, stream)
+            old.resident = False
+        return prog.glob[prog.dfa.start]
+
+    def resolve(self, stream=None) -> int:
+        """Fills every UNKNOWN entry walks have met: the owning program's DFA gives each
+        target, interned if new. Returns how many entries were filled."""
+        done = 0
+        while True:
+            pend = self.pending(stream=stream)
+            if pend.size == 0:
+                return done
+            targets, new = [], {}
+            for e in pend.tolist():
+                gs, b = divmod(int(e), 256)
+                if gs not in self._owner:
+                    raise ValueError(f"state {gs} belongs to no registered program")
+                prog, ls = self._owner[gs]
+                t = prog.dfa.next(ls, b)
+                targets.append((prog, t))
+                if t >= 0:
+                    new.setdefault(id(prog), (prog, []))[1].append(t)
+            for prog, ts in new.values():
+                self._intern(prog, ts, stream)
+            to = [prog.glob[t] if t >= 0 else DEAD for prog, t in targets]
+            self.set_next(pend, to, stream)
+            done += pend.size
 
     def masks(self, keys: torch.Tensor, out: torch.Tensor | None = None,
-              stream=None) -> torch.Tensor:
-        """Mask words [n][words] (int32 view of the u32 words) for device keys [n]."""
+              stream=None, resolve: bool | None = None) -> torch.Tensor:
+        """Mask words [n][words] (int32 view of the u32 words) for device keys [n]. With
+        programs registered (or resolve=True) the walks' unknown entries are filled and
+        the masks produced again until none is met."""
+        if resolve is None:
+            resolve = bool(self._programs)
+        while True:
+            out = self._masks(keys, out, stream)
+            if not resolve or self.resolve(stream) == 0:
+                return out
+
+    def _masks(self, keys, out, stream):
         if keys.dtype != torch.int32 or not keys.is_cuda or keys.dim() != 1:
             raise ValueError("keys must be a 1-D int32 CUDA tensor")
         keys = keys.contiguous()
@@ -181,9 +330,19 @@ class DeviceGrammar:
         return states.shape[0]
 
     def request_keys(self, states: torch.Tensor, drafts: torch.Tensor | None = None,
-                     stream=None) -> torch.Tensor:
+                     stream=None, resolve: bool | None = None) -> torch.Tensor:
         """RequestConstraint.key / verifyMask on the device: keys [B][k + 1] of the next
-        row and of the rows after each draft (states unchanged)."""
+        row and of the rows after each draft (states unchanged). With programs registered
+        (or resolve=True), draft walks that meet unknown entries are resolved and the
+        keys computed again."""
+        if resolve is None:
+            resolve = bool(self._programs)
+        while True:
+            out = self._request_keys(states, drafts, stream)
+            if not resolve or self.resolve(stream) == 0:
+                return out
+
+    def _request_keys(self, states, drafts, stream):
         B = self._check_states(states)
         if drafts is not None and drafts.numel() > 0:
             drafts = drafts.reshape(B, -1).to(torch.int32).contiguous()

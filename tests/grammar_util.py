@@ -86,6 +86,26 @@ def random_dfa(rng, S: int, alphabet: int = 6, p_dead: float = 0.15):
     return nt, fl
 
 
+class LazyTable:
+    """The GrammarDFA interface (start, next, accepting, consuming; GrammarDFA.swift:13-58)
+    over a full [S][256] table, as a host program that the device table interns from
+    lazily; counts the transitions asked for."""
+
+    def __init__(self, nt, fl, start=0):
+        self.nt, self.fl, self.start = nt, fl, start
+        self.calls = 0
+
+    def next(self, s, b):
+        self.calls += 1
+        return int(self.nt[s, b])
+
+    def accepting(self, s):
+        return bool(self.fl[s] & ACC)
+
+    def consuming(self, s):
+        return bool(self.fl[s] & CON)
+
+
 def brute_mask(tokens, width, eos, skip, nt, fl, key):
     """Per-token statement of the mask: token i (below width, non-empty, not skipped) is
     allowed iff its bytes never step to dead from a consuming state; end-of-turn ids join
