@@ -87,7 +87,8 @@ class BatchPicker:
     """One call per decode step for the whole batch (see the module docstring).
 
     ctx: a `strim_amd.ops.Context`; grammar: a `strim_amd.grammar.DeviceGrammar` shared by
-    the constrained requests, or None. Constrained requests carry a device tensor of
+    the constrained requests (its one table holds every request's program, so a batch
+    under several grammars is one call), or None. Constrained requests carry a device tensor of
     per-request states (`grammar.REQUEST_STATE` rows, int32 [B, 6]): the thinking phase
     and budget, the grammar state and the violation flag of RequestConstraint
     (RequestConstraint.swift:62-109). Each call reads the rows' keys from the states and

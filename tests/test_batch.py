@@ -199,6 +199,62 @@ def test_gpu_batch_pick_equals_per_row_loop(oracle_mod, ctx):
 
 
 @pytest.mark.gpu
+def test_gpu_batch_two_programs_one_pick(oracle_mod, ctx):
+    # requests under two different grammars in one batch (GrammarEngine's programs,
+    # GrammarVocab.swift:116-147): one DeviceGrammar table holds both, interned lazily;
+    # every step is one BatchPicker call, and each row equals the reference's loop over
+    # the row's own program (its mask, then the draw), for six steps
+    import torch
+
+    import grammar_util as G
+    from strim_amd.batch import BatchPicker
+    from strim_amd.grammar import DeviceGrammar, request_states, states_from_device, \
+        states_to_device
+
+    O = oracle_mod
+    V = G.FAKE_VOCAB
+    width = len(V) + 8
+    progs = {"obj": G.object_int_dfa(), "lit": G.literal_dfa(b'{"name": "Paris"}')}
+    g = DeviceGrammar(V, width, eos=[G.FAKE_EOS], skip=G.FAKE_SKIP, cache_slots=8)
+    oracles, starts = {}, {}
+    for name, (nt, fl) in progs.items():
+        go = O.GrammarOracle(V, width, [G.FAKE_EOS], G.FAKE_SKIP)
+        go.set_dfa(nt, fl)
+        oracles[name] = go
+        starts[name] = g.add_program(name, G.LazyTable(nt, fl))
+    B = 8
+    which = ["obj", "lit", "obj", "lit", "lit", "obj", "obj", "lit"]
+    st = request_states(B, grammar_state=[starts[w] for w in which])
+    sd = states_to_device(st)
+    picker = BatchPicker(ctx, g)
+    rng = np.random.default_rng(23)
+    local = [0] * B  # each request's state in its program; -1 once it ended (end of turn:
+    # the engine stops advancing a finished request, RequestConstraint.swift:104)
+    for step in range(6):
+        T = rng.choice([0.0, 0.7, 1.0], size=B)
+        p = O.make_params(B, temperature=T, seed=np.arange(B, dtype=np.uint64) + 100 * step,
+                          position=step)
+        x = rng.normal(0, 2.0, size=(B, width)).astype(np.float32)
+        ids, status, keys = picker.pick(torch.from_numpy(x).cuda(), p, sd)
+        ids, status, keys = ids.cpu().numpy(), status.cpu().numpy(), keys.cpu().numpy()
+        for b in range(B):
+            if local[b] < 0:
+                continue
+            prog, ls = g._owner[int(keys[b])]
+            assert prog.key == which[b] and ls == local[b], (step, b)
+            m = oracles[which[b]].mask(ls)[None]
+            ref = O.sample(x[b:b + 1], p[b:b + 1], mask=m)
+            assert status[b] == 0 and ids[b] == ref["token"][0], (step, b)
+            nl = oracles[which[b]].advance(ls, V[ids[b]]) if ids[b] != G.FAKE_EOS else -1
+            local[b] = nl
+        got = states_from_device(sd)
+        for b in range(B):
+            if local[b] >= 0:
+                assert g._owner[int(got["g"][b])][1] == local[b], (step, b)
+    g.close()
+
+
+@pytest.mark.gpu
 def test_gpu_thinking_budget(oracle_mod, ctx):
     # GrammarTests.swift:356-371 through the device state machine
     import torch
