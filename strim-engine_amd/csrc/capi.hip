@@ -57,7 +57,7 @@ constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // Byte offsets of the scratch buffers of R rows of up to max_vocab tokens, each 256-byte
 // aligned. The general-q verify buffers (dbits .. qpp) are sized only when `verify`.
 struct ScratchLayout {
-  size_t cstat, slot, part, rs, cand, nc, dbits, vq, qpart, qhc, qhm, qst, qpp, lat, bytes;
+  size_t cstat, slot, part, rs, cand, nc, dbits, wrank, qpart, qhc, qhm, qst, qpp, lat, bytes;
 };
 constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) {
   const size_t wmax = (max_vocab + CHUNK - 1) / CHUNK;
@@ -73,7 +73,7 @@ constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) 
   L.cand = off; off = align_up(off + R * CAP * sizeof(Cand), 256);
   L.nc = off; off = align_up(off + R * sizeof(uint32_t), 256);
   L.dbits = off; off = align_up(off + (verify ? words : 0) * sizeof(uint32_t), 256);
-  L.vq = off; off = align_up(off + RQ * wmax * CHUNK * sizeof(float), 256);
+  L.wrank = off; off = align_up(off + (verify ? words : 0) * sizeof(uint32_t), 256);
   L.qpart = off; off = align_up(off + RQ * wmax * sizeof(unsigned long long), 256);
   L.qhc = off; off = align_up(off + RQ * wmax * QNB * sizeof(uint32_t), 256);
   L.qhm = off; off = align_up(off + RQ * wmax * QNB * sizeof(unsigned long long), 256);
@@ -97,7 +97,7 @@ Scratch scratch_at(char* base, const ScratchLayout& L, size_t max_vocab, bool ve
   s.lat = (unsigned long long*)(base + L.lat);
   if (verify) {
     s.dbits = (uint32_t*)(base + L.dbits);
-    s.vq = (float*)(base + L.vq);
+    s.wrank = (uint32_t*)(base + L.wrank);
     s.qpart = (unsigned long long*)(base + L.qpart);
     s.qhc = (uint32_t*)(base + L.qhc);
     s.qhm = (unsigned long long*)(base + L.qhm);
@@ -244,7 +244,8 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs,
         keep(launch_args((const void*)k_qcollect, grid_rc, dim3(TPB), a, st, nullptr, nullptr));
         keep(launch_args((const void*)k_qfinal, grid_r, dim3(FIN_T), a, st, nullptr, e1));
       } else {
-        keep(launch_args((const void*)k_qgumbel, grid_rc, dim3(TPB), a, st, e0, nullptr));
+        const dim3 grid_q = a.qskip ? dim3((unsigned)a.W, (unsigned)a.B) : grid_rc;
+        keep(launch_args((const void*)k_qgumbel, grid_q, dim3(TPB), a, st, e0, nullptr));
         // with nothing after it, k_qgpick also runs the verify combine
         const bool comb = combined != nullptr && !need_final && !probs;
         keep(launch_qgpick(a, comb, st, nullptr, e1));

@@ -39,19 +39,53 @@ struct XUni {
 };
 
 // The draft distribution q of a general-q verify row: softmax(draft logits / T) over the
-// draft vocabulary, whose ids are the table's (membership bitmap dbits; vq holds
-// v = draft_logit / T at each member id).
+// draft vocabulary, whose ids are the table's (membership bitmap dbits). A member id's
+// table index is its rank among the members, wrank[id / 32] plus the member bits below
+// it in its word (the table ascends), so v = draft_logit / T is read from the row's
+// draft logits at that index.
 struct XQ {
   const uint32_t* dbits;
-  const float* vq;
+  const uint32_t* wrank;
+  const void* dlog;  // the row's draft logits [Vd], of dtype dt
+  int32_t dt;
+  float T;
   float mq;
   double Z;
 };
+// v at member id, given its membership word and rank word
+__device__ __forceinline__ float xq_v(const XQ& q, int id, uint32_t bits, uint32_t rank) {
+  const int i = (int)rank + __popc(bits & ((1u << (id & 31)) - 1u));
+  const float x = q.dt == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)q.dlog)[i])
+                                           : ((const float*)q.dlog)[i];
+  return x / q.T;
+}
+// The q of draft row qr (b * k + j) of a general-q verify launch (q_base: without its
+// maximum and sum).
+__device__ __forceinline__ XQ q_base(const Args& a, int qr) {
+  XQ q;
+  q.dbits = a.s.dbits;
+  q.wrank = a.s.wrank;
+  q.dt = a.dtype;
+  q.dlog = a.dtype == STRIM_DTYPE_BF16
+               ? (const void*)((const uint16_t*)a.dlog + (size_t)qr * (size_t)a.Vd)
+               : (const void*)((const float*)a.dlog + (size_t)qr * (size_t)a.Vd);
+  q.T = a.p[qr / a.k].temperature;
+  q.mq = 0.0f;
+  q.Z = 1.0;
+  return q;
+}
+__device__ __forceinline__ XQ q_of_row(const Args& a, int qr) {
+  const QStat qs = a.s.qst[qr];
+  XQ q = q_base(a, qr);
+  q.mq = qs.mq;
+  q.Z = qs.Z;
+  return q;
+}
 // q(id): exp(v - mq) / Z, 0 outside the table.
 __device__ __forceinline__ double xq_prob(const XQ& q, int id) {
   const uint32_t bits = q.dbits[id >> 5];
   if (!((bits >> (id & 31)) & 1u)) return 0.0;
-  return exp((double)q.vq[id] - (double)q.mq) / q.Z;
+  return exp((double)xq_v(q, id, bits, q.wrank[id >> 5]) - (double)q.mq) / q.Z;
 }
 
 // The fields of Args the streaming passes read (the exact path is one out-of-line call,
@@ -148,15 +182,14 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, int b, int j,
   const glb_t<const uint8_t>* lg = (const glb_t<const uint8_t>*)a.logits;
   const glb_t<const uint8_t>* mg = (const glb_t<const uint8_t>*)mrow;
   const glb_t<const uint32_t>* qdb = (const glb_t<const uint32_t>*)a.q.dbits;
-  const glb_t<const float>* qvq = (const glb_t<const float>*)a.q.vq;
+  const glb_t<const uint32_t>* qrk = (const glb_t<const uint32_t>*)a.q.wrank;
   // (clang vector types: the HIP vector classes cannot be assigned from a global
   // reference)
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   struct Slot {
     u32x4 x0, x1;
-    uint32_t mb, qb;
-    f32x4 q0, q1;
+    uint32_t mb, qb, qr;
   };
   Slot sl[XPD];
   // every load of a window from a clamped index, no branch between them; a segment that
@@ -173,8 +206,7 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, int b, int j,
     sd.mb = mg[a.mask ? (ii >> 3) : 0];
     if constexpr (Q) {
       sd.qb = qdb[ii >> 5];
-      sd.q0 = *(const glb_t<const f32x4>*)(qvq + ii);
-      sd.q1 = *(const glb_t<const f32x4>*)(qvq + ii + 4);
+      sd.qr = qrk[ii >> 5];
     }
   };
 #pragma unroll
@@ -216,16 +248,16 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, int b, int j,
         }
         const uint32_t bits = a.mask ? ((uint32_t)sd.mb & 0xFFu) : 0xFFu;
         float l[EPT], qv[EPT];
-        const float qa[EPT] = {sd.q0.x, sd.q0.y, sd.q0.z, sd.q0.w,
-                               sd.q1.x, sd.q1.y, sd.q1.z, sd.q1.w};
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
           const bool ok = (i0 + EPT <= a.V) && ((bits >> e) & 1u);
           l[e] = ok ? (p.greedy ? x[e] : x[e] / p.T) : -INFINITY;
           qv[e] = -INFINITY;
           if constexpr (Q) {
+            // (the members' draft logits: a dependent read of the row's draft logits,
+            // which stay in the caches)
             const int id = i0 + e;
-            if ((sd.qb >> (id & 31)) & 1u) qv[e] = qa[e];
+            if (i0 + EPT <= a.V && ((sd.qb >> (id & 31)) & 1u)) qv[e] = xq_v(a.q, id, sd.qb, sd.qr);
           }
         }
         fn(i0, l, qv);
@@ -261,7 +293,8 @@ __device__ __forceinline__ void x_pass_pipe(const XArgs& a, int r, int b, int j,
       l[e] = ok ? (p.greedy ? x : x / p.T) : -INFINITY;
       qv[e] = -INFINITY;
       if constexpr (Q) {
-        if (ok && ((a.q.dbits[id >> 5] >> (id & 31)) & 1u)) qv[e] = a.q.vq[id];
+        if (ok && ((a.q.dbits[id >> 5] >> (id & 31)) & 1u))
+          qv[e] = xq_v(a.q, id, a.q.dbits[id >> 5], a.q.wrank[id >> 5]);
       }
     }
     fn(iP, l, qv);
@@ -299,7 +332,8 @@ __device__ __forceinline__ void x_pass(const XArgs& a, int r, int b, int j, cons
       qv[e] = -INFINITY;
       if (hq && i0 + e < a.V) {
         const int id = i0 + e;
-        if ((a.q.dbits[id >> 5] >> (id & 31)) & 1u) qv[e] = a.q.vq[id];
+        if ((a.q.dbits[id >> 5] >> (id & 31)) & 1u)
+          qv[e] = xq_v(a.q, id, a.q.dbits[id >> 5], a.q.wrank[id >> 5]);
       }
     }
     fn(i0, l, qv);

@@ -294,9 +294,10 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
         const double sig = (double)Sq / XFIX;
         const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
         double ratio = w_d / sig;
-        const bool in_tab = (a.s.dbits[draft >> 5] >> (draft & 31)) & 1u;
+        const uint32_t dw = a.s.dbits[draft >> 5];
+        const bool in_tab = (dw >> (draft & 31)) & 1u;
         const double qd =
-            in_tab ? exp((double)a.s.vq[(size_t)qr * (size_t)a.s.wmax * CHUNK + draft] -
+            in_tab ? exp((double)xq_v(q_base(a, qr), draft, dw, a.s.wrank[draft >> 5]) -
                          (double)mq) / z
                    : 0.0;
         ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);

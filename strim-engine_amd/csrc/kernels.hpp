@@ -132,8 +132,8 @@ struct Scratch {
   Cand* cand;                     // [rows][CAP] QRES rows: the tokens of the draw's bin
   uint32_t* ncand;                // [rows] their count
   uint32_t* dbits;                // [ceil(V/32)] general-q verify: draft-vocab membership
-  float* vq;                      // [MAXP][wmax * CHUNK] general-q verify, per draft row:
-                                  // draft logit / T at each table id (others not written)
+  uint32_t* wrank;                // [ceil(V/32)] table entries below id 32 w: a member id's
+                                  // table index is wrank[id / 32] + the member bits below it
   unsigned long long* qpart;      // [MAXP][wmax] QRES rows: plain mass per chunk
   uint32_t* qhc;                  // [MAXP][wmax][QNB] QRES rows: residual counts per bin
   unsigned long long* qhm;        // [MAXP][wmax][QNB] QRES rows: residual masses per bin

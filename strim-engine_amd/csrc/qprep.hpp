@@ -24,14 +24,15 @@ __device__ __forceinline__ int table_lower_bound(const int32_t* tab, int n, int 
 
 // NT-thread workgroups. Blocks [0, B*k*QSPLIT): slice sp of draft row qr (blk = qr *
 // QSPLIT + sp, 1/QSPLIT of the table each): the slice maximum of v = draft_logit / T
-// (fp32 division, as the target's temperature), the slice's sum of exp(v - max) in fp64,
-// the table index of the row's draft token if the slice holds it, and v stored at each
-// table id of the row's dense array (the draft distribution of SpecSampling's general-q
-// extension); row 0's slices also check that the table is strictly ascending inside
-// [0, V). Each draft row's k_finalize workgroup merges the row's slices. Blocks after them: one thread per table entry
-// builds the membership bitmap: the first entry of each 32-id word writes the word's
-// bits and zeroes the empty words before it (the last entry also those after it), so
-// every word is written once.
+// (fp32 division, as the target's temperature), the slice's sum of exp(v - max) in fp64
+// and the table index of the row's draft token if the slice holds it (the draft
+// distribution of SpecSampling's general-q extension; its readers take v at a member id
+// from the draft logits through the id's table index); row 0's slices also check that
+// the table is strictly ascending inside [0, V). Each draft row's k_finalize workgroup
+// merges the row's slices. Blocks after them: one thread per table entry builds the
+// membership bitmap and the rank words: the first entry of each 32-id word writes the
+// word's bits and its table index, and the same index with no bits into the empty words
+// before it (the last entry also Vd into those after it), so every word is written once.
 template <int NT>
 __device__ __forceinline__ void qprep_block(const Args& a, int blk) {
   __shared__ float s_m[NT / WAVE];
@@ -48,15 +49,13 @@ __device__ __forceinline__ void qprep_block(const Args& a, int blk) {
     const int d = a.drafts[(int64_t)b * a.k + j];
     const float T = a.p[b].temperature;
     const size_t base = (size_t)qr * (size_t)Vd;
-    float* vq = a.s.vq + (size_t)qr * (size_t)a.s.wmax * CHUNK;
     auto ld = [&](int i) -> float {
       return a.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.dlog)[base + i])
                                          : ((const float*)a.dlog)[base + i];
     };
-    // batches of QB entries per thread: every load of a batch is issued before its
-    // stores (a store could alias a later load, which would serialise the loop). One
-    // pass: the table check (row 0), the draft's table index, v = logit / T at each id
-    // and the maximum.
+    // batches of QB entries per thread, every load of a batch issued before any wait.
+    // One pass: the table check (row 0), the draft's table index and the maximum of
+    // v = logit / T.
     constexpr int QB = 4;
     const bool live = T > 0.0f;
     float mx = -INFINITY;
@@ -77,11 +76,7 @@ __device__ __forceinline__ void qprep_block(const Args& a, int blk) {
         if (i >= hi) continue;
         if (id[q] < 0 || id[q] >= a.V || (i + 1 < Vd && !(id[q] < idn[q]))) bad = 1;
         if (id[q] == d) td = i;
-        if (live) {
-          v[q] = v[q] / T;
-          mx = fmaxf(mx, v[q]);
-          if (id[q] >= 0 && id[q] < a.V) vq[id[q]] = v[q];
-        }
+        if (live) mx = fmaxf(mx, v[q] / T);
       }
     }
     if (qr == 0) bad = block_or<NT>(bad, s_bad);
@@ -125,9 +120,16 @@ __device__ __forceinline__ void qprep_block(const Args& a, int blk) {
     bits |= 1u << (ide & 31);
   }
   a.s.dbits[w] = bits;
-  for (int z = max(pw + 1, 0); z < w; ++z) a.s.dbits[z] = 0u;
+  a.s.wrank[w] = (uint32_t)i;
+  for (int z = max(pw + 1, 0); z < w; ++z) {
+    a.s.dbits[z] = 0u;
+    a.s.wrank[z] = (uint32_t)i;
+  }
   if (i == Vd - 1)
-    for (int z = w + 1; z < words; ++z) a.s.dbits[z] = 0u;
+    for (int z = w + 1; z < words; ++z) {
+      a.s.dbits[z] = 0u;
+      a.s.wrank[z] = (uint32_t)Vd;
+    }
 }
 
 }  // namespace strim

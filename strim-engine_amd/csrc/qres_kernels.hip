@@ -44,15 +44,6 @@ __device__ __forceinline__ bool q_needed(const Args& a, int b, int j) {
   return true;
 }
 
-__device__ __forceinline__ XQ q_of_row(const Args& a, int qr) {
-  const QStat qs = a.s.qst[qr];
-  XQ q;
-  q.dbits = a.s.dbits;
-  q.vq = a.s.vq + (size_t)qr * (size_t)a.s.wmax * CHUNK;
-  q.mq = qs.mq;
-  q.Z = qs.Z;
-  return q;
-}
 
 // Residual weight of a token of plain weight W: max(0, W - round(q S)) where q > 0
 // (x_wt's rule with the kept mass S).
@@ -314,17 +305,38 @@ __device__ __forceinline__ void q_wave_best(double& sc, int& id) {
   id = bi;
 }
 
+// Grid (W, R), or with a.qskip (W, B): workgroup (c, b) takes chunk c of sequence b's
+// first rejected draft row (the only residual draw read), found from the rows' accept
+// outcomes in one wave load (k <= 64).
 __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   __shared__ uint32_t s_cnt[CHUNK];
   __shared__ uint64_t s_red[TPB / WAVE];
   __shared__ double s_sc[TPB / WAVE];
   __shared__ int s_id[TPB / WAVE];
-  int r, c;
-  map_block(a, r, c);
-  int b, j;
-  row_bj(a, r, b, j);
-  if (a.s.rs[r].phase != PH_QRES || !q_needed(a, b, j)) return;
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE, qr = b * a.k + j;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  int r, c, b, j;
+  if (a.qskip) {
+    b = blockIdx.y;
+    c = blockIdx.x;
+    const int k1 = a.k + 1;
+    bool rej = false;
+    int ph = -1;
+    if (lane < a.k) {
+      const RowState& rq = a.s.rs[(int64_t)b * k1 + lane];
+      rej = !(rq.status == STRIM_OK && rq.accept);
+      ph = rq.phase;
+    }
+    const uint64_t m_rej = __ballot(rej);
+    if (m_rej == 0ull) return;  // every draft accepted: no residual draw
+    j = (int)__ffsll((long long)m_rej) - 1;
+    if (__builtin_amdgcn_readlane(ph, j) != PH_QRES) return;
+    r = b * k1 + j;
+  } else {
+    map_block(a, r, c);
+    row_bj(a, r, b, j);
+    if (a.s.rs[r].phase != PH_QRES) return;
+  }
+  const int qr = b * a.k + j;
   const RowParams p = load_params(a, b, j);
   const float m = a.s.rs[r].m;
   const uint64_t sp = t < a.W ? a.s.qpart[(size_t)qr * a.s.wmax + t] : 0ull;
@@ -351,7 +363,8 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
       u[4 * hb + 2] = u01(wb.z); u[4 * hb + 3] = u01(wb.w);
     }
   }
-  const uint32_t qbits = q.dbits[(i0 < a.V ? i0 : 0) >> 5] >> (i0 & 31);
+  const uint32_t qword = q.dbits[(i0 < a.V ? i0 : 0) >> 5];
+  const uint32_t qbits = qword >> (i0 & 31);
   // fp32 screen: an upper bound ub of every token's score (log(p - q) <= log p, so a
   // table token's p-score bounds its residual score) and, from the tokens outside the
   // table (whose score is the p-score), a lower bound lb of the wave's best. Only tokens
@@ -381,7 +394,7 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
     const int id = i0 + e;
     double base = no_lse ? (double)l[e] : ((double)l[e] - (double)m) - lse;
     if ((qbits >> e) & 1u) {
-      const double qq = exp((double)q.vq[id] - (double)q.mq) / q.Z;
+      const double qq = exp((double)xq_v(q, id, qword, q.wrank[id >> 5]) - (double)q.mq) / q.Z;
       if (qq != 0.0) {
         // residual score: log(p - q), excluded where p <= q
         const double rr = exp(base) - qq;

@@ -54,10 +54,7 @@ __global__ __launch_bounds__(FIN_T) void k_final(Args a) {
   // the draft distribution q of the row (k_qprep)
   const int qr = b * a.k + j;
   const QStat qs = a.s.qst[qr];
-  xa.q.dbits = a.s.dbits;
-  xa.q.vq = a.s.vq + (size_t)qr * (size_t)a.s.wmax * CHUNK;
-  xa.q.mq = qs.mq;
-  xa.q.Z = qs.Z;
+  xa.q = q_of_row(a, qr);
   const XOut xo = exact_row<FIN_T, true>(xa, r, b, j, p, m, arg, draft, true, rsp->l_draft, xs,
                                    *(lds_t<XState>*)&s_x);
   if (threadIdx.x == 0) {
