@@ -393,9 +393,36 @@ def head_bench(torch, ops, dev, ctx, args, w1, m1, hl, B=8, K=5120):
     usc, kc, _ = graph_median(torch, [step] * n, steps, n)
     st = samp.out_status.cpu().numpy()
     assert (st == 0).all(), f"head chain status {st}"
+    # greedy rows: the producer then strim_sample at T = 0, against the pick fused into
+    # the producer's epilogue (strim_head_greedy), with and without the logits written
+    pg = W.params_array(B, temperature=0.0)
+    sg = ctx.bind_sample(lg, pg)
+    def step_g():
+        head()
+        sg()
+    usg, _, _ = graph_median(torch, [step_g] * n, steps, n)
+    gid = torch.empty(B, dtype=torch.int32, device=dev)
+    gst = torch.empty(B, dtype=torch.int32, device=dev)
+    fused = lambda: ops.head_greedy(ctx, x, wt, nw, out_logits=lg, xn=xn, ids=gid, status=gst)
+    fused_nl = lambda: ops.head_greedy(ctx, x, wt, nw, xn=xn, ids=gid, status=gst)
+    usf, _, _ = graph_median(torch, [fused] * n, steps, n)
+    usf_nl, _, _ = graph_median(torch, [fused_nl] * n, steps, n)
+    assert torch.equal(gid, sg.out_ids) and (gst == 0).all(), "fused greedy differs"
     byt = V * K * 2 + B * V * 2 + B * K * 2 * 3 + K * 2
     flops = 2.0 * B * V * K
-    log(f"[bench] head B={B} K={K} V={V}: {ush:.1f} us/call; head + n1 chain {usc:.1f} us/step")
+    log(f"[bench] head B={B} K={K} V={V}: {ush:.1f} us/call; head + n1 chain {usc:.1f} us/step; "
+        f"greedy: head + sample {usg:.1f}, fused {usf:.1f} (no logits written {usf_nl:.1f}) "
+        f"us/step")
+    # the producer at B = 64 (four 16-row batch tiles per MFMA step)
+    B64 = 64
+    x64 = (2.0 * torch.randn(B64, K, device=dev, generator=g)).to(torch.bfloat16)
+    xn64 = torch.empty(B64, K, dtype=torch.bfloat16, device=dev)
+    lg64 = torch.empty(B64, V, dtype=torch.bfloat16, device=dev)
+    head64 = lambda: ops.head_logits(x64, wt, nw, out=lg64, xn=xn64)
+    us64, _, _ = graph_median(torch, [head64] * n, steps, n)
+    byt64 = V * K * 2 + B64 * V * 2 + B64 * K * 2 * 3 + K * 2
+    log(f"[bench] head B={B64}: {us64:.1f} us/call, "
+        f"{byt64 / (us64 * 1e-6) / 1e9:.0f} GB/s, {2.0 * B64 * V * K / (us64 * 1e-6) / 1e12:.1f} TFLOP/s")
     del wt
     torch.cuda.empty_cache()
     return {
@@ -409,6 +436,17 @@ def head_bench(torch, ops, dev, ctx, args, w1, m1, hl, B=8, K=5120):
         "mfma_tflops": round(flops / (ush * 1e-6) / 1e12, 2),
         "then_n1_chain_us_per_step": round(usc, 2),
         "sampler_share_us": round(usc - ush, 2),
+        "greedy": {"head_then_sample_us_per_step": round(usg, 2),
+                   "fused_us_per_step": round(usf, 2),
+                   "fused_no_logits_us_per_step": round(usf_nl, 2),
+                   "workload": f"B={B} greedy rows (T=0, no penalties, mask or filters): "
+                               "strim_head_logits then strim_sample, against strim_head_greedy"},
+        "b64": {"us_per_call": round(us64, 2),
+                "roofline": {"bound": "hbm", "achieved": round(byt64 / (us64 * 1e-6) / 1e9, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(byt64 / (us64 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             "bytes_per_call": int(byt64)},
+                "mfma_tflops": round(2.0 * B64 * V * K / (us64 * 1e-6) / 1e12, 2)},
     }
 
 

@@ -221,6 +221,22 @@ int strim_head_logits(void* stream, const void* hidden, int64_t hidden_stride, i
                       const void* lm_head, int64_t lm_head_stride, int32_t V, void* out_logits,
                       int64_t out_stride);
 
+/* Hidden -> greedy token: the producer above (same operands and checks) with the pick
+ * fused into it, for rows the reference decides by argmax alone (T <= 0 with no
+ * penalties, no mask and no filters: Sampler.sample / SpecSampling's T -> 0 case,
+ * SpecSampling.swift:70-88). The GEMV's epilogue writes each 128-row vocabulary tile's
+ * first maximum per batch row (as bf16 logits, as strim_sample reads them) and one small
+ * launch merges them, so the logits are not read back; out_logits may be NULL (then they
+ * are not written at all). out_ids [B] = the first maximum's id, out_status [B] (or NULL)
+ * = STRIM_OK, STRIM_ENONFINITE (a NaN or +inf logit) or STRIM_EEMPTY (every logit -inf),
+ * with out_ids -1 on an error row: strim_sample's result for such a row. The tile maxima
+ * use ctx's scratch (B <= max_rows and V <= max_vocab, else STRIM_ECAPACITY); calls on
+ * one ctx run in stream order. */
+int strim_head_greedy(strim_ctx* ctx, void* stream, const void* hidden, int64_t hidden_stride,
+                      int32_t B, int32_t K, const void* norm_weight, float eps, void* xn,
+                      const void* lm_head, int64_t lm_head_stride, int32_t V, void* out_logits,
+                      int64_t out_stride, int32_t* out_ids, int32_t* out_status);
+
 /* ---- per-kernel timing -------------------------------------------------------------
  * Counterpart of the reference's fenced per-region GPU timer OpTimer
  * (Sources/StrimCore/OpTimer.swift:1-60). While profiling is on, every kernel a call

@@ -16,7 +16,8 @@ hipError_t launch_finalize(const Args& a, hipStream_t st, hipEvent_t e0, hipEven
 hipError_t launch_gfinal(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_head(const void* hidden, int64_t hidden_stride, int B, int K,
                        const void* norm_w, float eps, void* xn, const void* W, int64_t w_stride,
-                       int V, void* out, int64_t out_stride, bool vo, hipStream_t st);
+                       int V, void* out, int64_t out_stride, bool vo, hipStream_t st,
+                       uint2* tbest, int32_t* out_ids, int32_t* out_status);
 __global__ void k_final(Args a);
 __global__ void k_probs(Args a);
 __global__ void k_verify_combine(Args a);
@@ -651,21 +652,54 @@ int strim_mask_logits(void* stream, const void* logits, int32_t dtype, int32_t R
   return launch_status();
 }
 
+namespace {
+// the producer's operand checks (out_logits NULL is allowed where the caller says so)
+bool head_args_ok(const void* hidden, int64_t hidden_stride, int32_t B, int32_t K,
+                  const void* norm_weight, float eps, const void* xn, const void* lm_head,
+                  int64_t lm_head_stride, int32_t V, const void* out_logits, int64_t out_stride) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if (!hidden || !lm_head || B < 1 || B > 64 || K <= 0 || K % 256 != 0 || V <= 0 ||
+      hidden_stride < K || lm_head_stride < K || (out_logits && out_stride < V) ||
+      !(eps >= 0.0f) || !al16(hidden) || hidden_stride % 8 != 0 || !al16(lm_head) ||
+      lm_head_stride % 8 != 0)
+    return false;
+  if (norm_weight && (!xn || !al16(xn) || !al16(norm_weight))) return false;
+  return true;
+}
+}  // namespace
+
 int strim_head_logits(void* stream, const void* hidden, int64_t hidden_stride, int32_t B,
                       int32_t K, const void* norm_weight, float eps, void* xn,
                       const void* lm_head, int64_t lm_head_stride, int32_t V, void* out_logits,
                       int64_t out_stride) {
-  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  if (!hidden || !lm_head || !out_logits || B < 1 || B > 64 || K <= 0 || K % 256 != 0 ||
-      V <= 0 || hidden_stride < K || lm_head_stride < K || out_stride < V ||
-      !(eps >= 0.0f) || !al16(hidden) || hidden_stride % 8 != 0 || !al16(lm_head) ||
-      lm_head_stride % 8 != 0)
+  if (!out_logits || !head_args_ok(hidden, hidden_stride, B, K, norm_weight, eps, xn, lm_head,
+                                   lm_head_stride, V, out_logits, out_stride))
     return STRIM_EINVAL;
-  if (norm_weight && (!xn || !al16(xn) || !al16(norm_weight))) return STRIM_EINVAL;
   const bool vo = ((uintptr_t)out_logits & 7u) == 0 && out_stride % 4 == 0;
   const hipError_t e = launch_head(hidden, hidden_stride, B, K, norm_weight, eps, xn, lm_head,
                                    lm_head_stride, V, out_logits, out_stride, vo,
-                                   (hipStream_t)stream);
+                                   (hipStream_t)stream, nullptr, nullptr, nullptr);
+  return e == hipSuccess ? STRIM_OK : STRIM_EHIP;
+}
+
+int strim_head_greedy(strim_ctx* ctx, void* stream, const void* hidden, int64_t hidden_stride,
+                      int32_t B, int32_t K, const void* norm_weight, float eps, void* xn,
+                      const void* lm_head, int64_t lm_head_stride, int32_t V, void* out_logits,
+                      int64_t out_stride, int32_t* out_ids, int32_t* out_status) {
+  if (!ctx || !out_ids ||
+      !head_args_ok(hidden, hidden_stride, B, K, norm_weight, eps, xn, lm_head, lm_head_stride,
+                    V, out_logits, out_stride))
+    return STRIM_EINVAL;
+  if (B > ctx->max_rows || V > ctx->max_vocab) return STRIM_ECAPACITY;
+  // the tile maxima [B][ceil(V / 128)] go to the context's candidate slots (stream-ordered
+  // with every other call on the context; they need B * V / 16 bytes, the slots hold
+  // max_rows * max_vocab bytes)
+  static_assert(sizeof(Cand) * SLOT >= (CHUNK / 128) * sizeof(uint2), "tile maxima fit the slots");
+  uint2* tbest = (uint2*)ctx->s.slot;
+  const bool vo = out_logits && ((uintptr_t)out_logits & 7u) == 0 && out_stride % 4 == 0;
+  const hipError_t e = launch_head(hidden, hidden_stride, B, K, norm_weight, eps, xn, lm_head,
+                                   lm_head_stride, V, out_logits, out_stride, vo,
+                                   (hipStream_t)stream, tbest, out_ids, out_status);
   return e == hipSuccess ? STRIM_OK : STRIM_EHIP;
 }
 

@@ -9,6 +9,12 @@
 //   so the 1,187 workgroups of V = 151,936 each stream 1.3 MB of weights once, and the
 //   weight matrix is read exactly once per call whatever the batch. The batch is the
 //   MFMA's N side (16 rows per tile, up to four tiles), read from the L2-resident xn.
+//   For a greedy pick (strim_head_greedy) its epilogue also writes each batch row's first
+//   maximum over the workgroup's 128 logits (as bf16 values, as the sampler reads them),
+//   and the logits may be left unwritten.
+// k_head_pick: one workgroup per batch row merges the rows' tile maxima into the first
+//   maximum of the row: the greedy token, with the sampler's statuses (a NaN or +inf logit:
+//   STRIM_ENONFINITE; every logit -inf: STRIM_EEMPTY).
 //
 // MFMA operand layout (v_mfma_f32_16x16x32_bf16; checked on the device): lane l holds
 // A[l % 16][8 (l / 16) + i] and B[8 (l / 16) + i][l % 16] for i < 8, and C[4 (l / 16) + i]
@@ -82,11 +88,22 @@ __global__ __launch_bounds__(HN_T) void k_head_norm(const uint16_t* x, int64_t x
 // NT: 16-row batch tiles (B <= 16 NT). VO: 8-byte logit stores (rows 4-element aligned).
 // MT: 16-row vocabulary tiles per wave; NW: waves per workgroup; NTL: weights loaded
 // nontemporal (streamed once, kept out of the caches that hold xn).
-template <int NT, bool VO, int MT = HG_MT, int NW = HG_W, bool NTL = false>
+// The larger of two (value, id) pairs, the smaller id on equal values (NaN never taken).
+__device__ __forceinline__ void hb_take(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+// TB: write the tile maxima to tbest[n][blockIdx.x] = {value bits (NaN: the tile holds a
+// NaN or +inf), id}; out NULL: no logits stored.
+template <int NT, bool VO, bool TB = false, int MT = HG_MT, int NW = HG_W, bool NTL = false>
 __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int64_t xn_stride,
                                                           int B, int K, const uint16_t* W,
                                                           int64_t w_stride, int V,
-                                                          uint16_t* out, int64_t out_stride) {
+                                                          uint16_t* out, int64_t out_stride,
+                                                          uint2* tbest) {
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
   const int h = lane >> 4, r16 = lane & 15;
   const int v0 = blockIdx.x * (NW * MT * 16) + wv * (MT * 16);
@@ -152,16 +169,31 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
     __builtin_amdgcn_sched_barrier(0);
   }
   // lane l holds rows 4 h + i of each tile for batch row nt 16 + r16
+  float bv[NT];
+  int bi[NT];
+  bool bad[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
+    bv[nt] = -INFINITY;
+    bi[nt] = INT_MAX;
+    bad[nt] = false;
     const int n = nt * 16 + r16;
-    if (n >= B) continue;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int vb = v0 + mt * 16 + 4 * h;
       uint16_t o[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = head_bf16(acc[mt][nt][i]);
+      if constexpr (TB) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (vb + i < V) {
+            const float f = __uint_as_float((uint32_t)o[i] << 16);
+            bad[nt] = bad[nt] || !(f < INFINITY);  // NaN or +inf
+            hb_take(bv[nt], bi[nt], f, vb + i);
+          }
+      }
+      if (n >= B || out == nullptr) continue;
       uint16_t* dst = out + (int64_t)n * out_stride + vb;
       if (VO && vb + 3 < V) {
         *(uint2*)dst = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
@@ -173,11 +205,86 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
       }
     }
   }
+  if constexpr (TB) {
+    // the four lanes of a batch row (h = 0..3), then the workgroup's waves
+    __shared__ float s_v[NW][16 * NT];
+    __shared__ int s_i[NW][16 * NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int sh = 16; sh < WAVE; sh <<= 1) {
+        const float v2 = __shfl_xor(bv[nt], sh);
+        const int i2 = __shfl_xor(bi[nt], sh);
+        const bool b2 = __shfl_xor((int)bad[nt], sh) != 0;
+        hb_take(bv[nt], bi[nt], v2, i2);
+        bad[nt] = bad[nt] || b2;
+      }
+      if (h == 0) {
+        s_v[wv][nt * 16 + r16] = bad[nt] ? __uint_as_float(0x7FC00000u) : bv[nt];
+        s_i[wv][nt * 16 + r16] = bi[nt];
+      }
+    }
+    __syncthreads();
+    const int n = (int)threadIdx.x;
+    if (n < B && n < 16 * NT) {
+      float v = s_v[0][n];
+      int i = s_i[0][n];
+      bool nan = !(v == v);
+#pragma unroll
+      for (int q = 1; q < NW; ++q) {
+        nan = nan || !(s_v[q][n] == s_v[q][n]);
+        hb_take(v, i, s_v[q][n], s_i[q][n]);
+      }
+      tbest[(int64_t)n * gridDim.x + blockIdx.x] =
+          make_uint2(__float_as_uint(nan ? __uint_as_float(0x7FC00000u) : v), (uint32_t)i);
+    }
+  }
+}
+
+constexpr int HP_T = 256;  // k_head_pick threads
+
+__global__ __launch_bounds__(HP_T) void k_head_pick(const uint2* tbest, int ntiles,
+                                                     int32_t* out_ids, int32_t* out_status) {
+  __shared__ float s_v[HP_T / WAVE];
+  __shared__ int s_i[HP_T / WAVE], s_bad[HP_T / WAVE];
+  const int n = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  float v = -INFINITY;
+  int i = INT_MAX;
+  bool bad = false;
+  for (int q = t; q < ntiles; q += HP_T) {
+    const uint2 r = tbest[(int64_t)n * ntiles + q];
+    const float f = __uint_as_float(r.x);
+    bad = bad || !(f == f);
+    hb_take(v, i, f, (int)r.y);
+  }
+#pragma unroll
+  for (int sh = 1; sh < WAVE; sh <<= 1) {
+    const float v2 = __shfl_xor(v, sh);
+    const int i2 = __shfl_xor(i, sh);
+    bad = bad || (__shfl_xor((int)bad, sh) != 0);
+    hb_take(v, i, v2, i2);
+  }
+  if (lane == 0) {
+    s_v[w] = v;
+    s_i[w] = i;
+    s_bad[w] = bad ? 1 : 0;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int q = 1; q < HP_T / WAVE; ++q) {
+      hb_take(v, i, s_v[q], s_i[q]);
+      bad = bad || s_bad[q];
+    }
+    const int st = bad ? STRIM_ENONFINITE : (v > -INFINITY ? STRIM_OK : STRIM_EEMPTY);
+    out_ids[n] = st == STRIM_OK ? i : -1;
+    if (out_status) out_status[n] = st;
+  }
 }
 
 hipError_t launch_head(const void* hidden, int64_t hidden_stride, int B, int K,
                        const void* norm_w, float eps, void* xn, const void* W, int64_t w_stride,
-                       int V, void* out, int64_t out_stride, bool vo, hipStream_t st) {
+                       int V, void* out, int64_t out_stride, bool vo, hipStream_t st,
+                       uint2* tbest, int32_t* out_ids, int32_t* out_status) {
   const uint16_t* src = (const uint16_t*)hidden;
   int64_t src_stride = hidden_stride;
   if (norm_w) {
@@ -190,12 +297,18 @@ hipError_t launch_head(const void* hidden, int64_t hidden_stride, int B, int K,
   const dim3 grid((unsigned)((V + rows - 1) / rows)), blk(HG_W * WAVE);
   const int nt = (B + 15) / 16;
 #define STRIM_HEAD_GEMV(NT_)                                                                  \
-  if (vo)                                                                                     \
+  if (tbest && vo)                                                                            \
+    hipLaunchKernelGGL((k_head_gemv<NT_, true, true>), grid, blk, 0, st, src, src_stride, B,  \
+                       K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, tbest); \
+  else if (tbest)                                                                             \
+    hipLaunchKernelGGL((k_head_gemv<NT_, false, true>), grid, blk, 0, st, src, src_stride, B, \
+                       K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, tbest); \
+  else if (vo)                                                                                \
     hipLaunchKernelGGL((k_head_gemv<NT_, true>), grid, blk, 0, st, src, src_stride, B, K,    \
-                       (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride);         \
+                       (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, nullptr); \
   else                                                                                        \
     hipLaunchKernelGGL((k_head_gemv<NT_, false>), grid, blk, 0, st, src, src_stride, B, K,   \
-                       (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride);
+                       (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, nullptr);
   if (nt == 1) {
     STRIM_HEAD_GEMV(1)
   } else if (nt == 2) {
@@ -204,6 +317,9 @@ hipError_t launch_head(const void* hidden, int64_t hidden_stride, int B, int K,
     STRIM_HEAD_GEMV(4)
   }
 #undef STRIM_HEAD_GEMV
+  if (tbest)
+    hipLaunchKernelGGL(k_head_pick, dim3((unsigned)B), dim3(HP_T), 0, st, tbest, (int)grid.x,
+                       out_ids, out_status);
   return hipGetLastError();
 }
 

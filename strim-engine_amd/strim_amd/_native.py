@@ -34,6 +34,7 @@ EXPORTS = (
     "strim_verify",
     "strim_mask_logits",
     "strim_head_logits",
+    "strim_head_greedy",
     "strim_draft_argmax",
     "strim_profile_begin",
     "strim_profile_end",
@@ -135,6 +136,9 @@ def lib() -> ctypes.CDLL:
         L.strim_head_logits.restype = ctypes.c_int
         L.strim_head_logits.argtypes = [P, P, I64, I32, I32, P, ctypes.c_float, P, P, I64, I32,
                                         P, I64]
+        L.strim_head_greedy.restype = ctypes.c_int
+        L.strim_head_greedy.argtypes = [P, P, P, I64, I32, I32, P, ctypes.c_float, P, P, I64,
+                                        I32, P, I64, P, P]
         L.strim_draft_argmax.restype = ctypes.c_int
         L.strim_draft_argmax.argtypes = [P, P, I32, I32, I32, I64, P, P]
         L.strim_profile_begin.restype = ctypes.c_int

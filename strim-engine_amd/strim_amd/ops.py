@@ -282,6 +282,41 @@ def head_logits(hidden: torch.Tensor, lm_head: torch.Tensor,
     return out
 
 
+def head_greedy(ctx: "Context", hidden: torch.Tensor, lm_head: torch.Tensor,
+                norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                out_logits: torch.Tensor | None = None, xn: torch.Tensor | None = None,
+                ids: torch.Tensor | None = None, status: torch.Tensor | None = None,
+                stream=None):
+    """Hidden -> greedy token with the pick fused into the producer (strim_head_greedy):
+    the first maximum of each row's bf16 logits, which strim_sample gives for a T <= 0 row
+    without penalties, mask or filters. out_logits None: the logits are not written.
+    Returns (ids, status) int32 [B]."""
+    if hidden.dim() == 1:
+        hidden = hidden.unsqueeze(0)
+    for t in (hidden, lm_head, norm_weight, out_logits, xn):
+        _check_cuda(t)
+        if t is not None and t.dtype != torch.bfloat16:
+            raise TypeError("head_greedy takes bf16 tensors")
+    B, K = hidden.shape
+    V = lm_head.shape[0]
+    if lm_head.shape[1] != K:
+        raise ValueError(f"lm_head is [{lm_head.shape[0]}, {lm_head.shape[1]}], hidden K={K}")
+    if norm_weight is not None and xn is None:
+        xn = torch.empty(B, K, dtype=torch.bfloat16, device=hidden.device)
+    if ids is None:
+        ids = torch.empty(B, dtype=torch.int32, device=hidden.device)
+    if status is None:
+        status = torch.empty(B, dtype=torch.int32, device=hidden.device)
+    N.check(N.lib().strim_head_greedy(ctx.handle, _stream(stream), _ptr(hidden),
+                                      _row_stride(hidden), B, K, _ptr(norm_weight), float(eps),
+                                      _ptr(xn), _ptr(lm_head), _row_stride(lm_head), V,
+                                      _ptr(out_logits),
+                                      _row_stride(out_logits) if out_logits is not None else 0,
+                                      _ptr(ids), _ptr(status)),
+            "strim_head_greedy")
+    return ids, status
+
+
 def draft_argmax(draft_logits: torch.Tensor, draft_to_full: torch.Tensor | None = None,
                  stream=None):
     """MTP.nextTokenIndex (MTP.swift:104-111): table[argmax(draft logits)] per row."""

@@ -116,3 +116,54 @@ def test_head_then_sample_matches_oracle(ctx):
     noise = rng.random((B, 2)).astype(np.float32)
     check_sample(ctx, lx, params, "bf16", mask=O.pack_mask(allowed), history=hist,
                  history_len=np.full(B, Hn, np.int32), noise=noise, label="head chain")
+
+
+@pytest.mark.parametrize("B,K,V", [(1, 256, 1000), (8, 512, 4133), (17, 256, 777),
+                                   (64, 256, 2049), (8, 1024, 151936)])
+def test_head_greedy_equals_greedy_sample(ctx, B, K, V):
+    # the fused pick (strim_head_greedy) against strim_sample at T = 0 (no penalties, mask
+    # or filters) on the very logits the producer wrote, and against the numpy first
+    # maximum of those logits; then with the logits left unwritten. Quantised weights make
+    # exact ties across workgroup tiles, so the first-index rule is exercised.
+    rng = np.random.default_rng(B * 7 + V)
+    x = H.bf16_round(rng.normal(0, 1.0, (B, K)).astype(np.float32))
+    g = H.bf16_round(rng.normal(1.0, 0.1, K).astype(np.float32))
+    W = H.bf16_round((rng.integers(-3, 4, (V, K)) * 0.03125).astype(np.float32))
+    W[V - 1] = W[min(V - 1, 5)]  # the same row at both ends of the vocabulary
+    xd, gd, Wd = bf16_dev(x), bf16_dev(g), bf16_dev(W)
+    lg = torch.empty(B, V, dtype=torch.bfloat16, device="cuda")
+    ids, st = ops.head_greedy(ctx, xd, Wd, gd, out_logits=lg)
+    torch.cuda.synchronize()
+    lx = to_np(lg)
+    assert (st.cpu().numpy() == 0).all()
+    np.testing.assert_array_equal(ids.cpu().numpy(), np.argmax(lx, axis=1))
+    sid, sst, _ = ctx.sample(lg, O.make_params(B, temperature=0.0))
+    np.testing.assert_array_equal(ids.cpu().numpy(), sid.cpu().numpy())
+    ids2, st2 = ops.head_greedy(ctx, xd, Wd, gd)  # logits not written
+    np.testing.assert_array_equal(ids2.cpu().numpy(), ids.cpu().numpy())
+
+
+def test_head_greedy_statuses(ctx):
+    # a NaN or +inf logit gives STRIM_ENONFINITE and every logit -inf STRIM_EEMPTY, as
+    # strim_sample reports them for a greedy row (ids -1)
+    B, K, V = 4, 256, 700
+    rng = np.random.default_rng(3)
+    x = H.bf16_round(rng.normal(0, 1.0, (B, K)).astype(np.float32))
+    W = H.bf16_round(rng.normal(0, 0.05, (V, K)).astype(np.float32))
+    x[1, 0] = np.nan                         # row 1: every logit NaN
+    x[2] = 0.0
+    x[2, 0] = np.inf                         # row 2: +inf or NaN logits
+    W[:, 0] = np.where(np.arange(V) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    x[3] = 0.0
+    x[3, 0] = -np.inf
+    W3 = W.copy()
+    W3[:, 0] = 1.0                           # row 3: every logit -inf
+    lg = torch.empty(B, V, dtype=torch.bfloat16, device="cuda")
+    Wd = bf16_dev(W3)
+    ids, st = ops.head_greedy(ctx, bf16_dev(x), Wd, out_logits=lg)
+    sid, sst, _ = ctx.sample(lg, O.make_params(B, temperature=0.0))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(st.cpu().numpy(), sst.cpu().numpy())
+    np.testing.assert_array_equal(ids.cpu().numpy(), sid.cpu().numpy())
+    assert st.cpu().numpy()[0] == 0 and (st.cpu().numpy()[1:3] == O.STRIM_ENONFINITE).all()
+    assert st.cpu().numpy()[3] == O.STRIM_EEMPTY
