@@ -39,7 +39,8 @@ constexpr int LPL = NBW / WAVE;                  // row bins per lane (bins LPL 
 constexpr float RFIXF = 1099511627776.0f;        // 2^40: fixed-point unit of row mass
 constexpr double RFIX = 1099511627776.0;
 constexpr int ZCAP = 4096;                       // keys of one zone
-constexpr int ZQ = ZCAP / GT;                    // zone positions per thread (sorted zones)
+constexpr int ZQ = ZCAP / GT;                    // zone positions per thread (radix picks)
+constexpr int RADIX_MIN = 256;  // wider zones are picked by radix select, not all pairs
 constexpr int PF = 160;                          // candidates of each chunk prefetched
 // The lattice words and the prefetched candidates are loaded straight into LDS, 1 KB per
 // wave instruction (16 bytes per lane): KW and KP instructions per wave.
@@ -234,56 +235,118 @@ __device__ __forceinline__ GHit pick_rank(GFinalShared& S, GBig& G, int np, int 
   return GHit{S.res[slot][0], S.res[slot][1], S.res[slot][2], S.res[slot][3]};
 }
 
-// The same pick over a zone of more than GT keys: the keys are sorted in place (their
-// masses rewritten in the new order), each thread takes ZQ consecutive positions, and a
-// block scan gives every position its count and mass before it.
-__device__ __forceinline__ GHit pick_sorted(GFinalShared& S, GBig& G, int np, int n, bool by_mass, double thr,
-                                            uint64_t bound, int excl, uint64_t cnt0,
-                                            uint64_t mass0, float m) {
-  const int t = threadIdx.x;
+// The same pick over a zone of up to ZCAP keys at z0 (unsorted), for zones too wide for
+// pick_rank's all-pairs count (more than RADIX_MIN keys):
+// an MSD radix select over the keys' compact form (fkey << 20 | id, in the keys' order:
+// ids are below 2^20), up to 8 bits a pass from the highest bit where the zone's keys
+// differ. A pass histograms the candidates' digits (their count, and the kept mass: keys
+// <= bound, id != excl), and wave 0 finds the digit d whose interval of cumulative weight
+// (count, or kept mass), from cnt0 / mass0 and the weight below the candidates, holds thr:
+// (double)before(d) <= thr < (double)(before(d) + weight(d)), as pick_rank's rule for one
+// key. The candidates narrow to d until every bit is fixed: about five passes of three
+// barriers for the keys of one lattice bin.
+__device__ __forceinline__ GHit pick_sorted(GFinalShared& S, GBig& G, int np, int z0, int n,
+                                            bool by_mass, double thr, uint64_t bound, int excl,
+                                            uint64_t cnt0, uint64_t mass0) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
   const int slot = np & 1;
-  bitonic_sort_lds<GT>(G.z.zkey, n);
-  uint64_t km[ZQ], lm = 0ull;
+  auto compact = [](uint64_t k) { return ((k >> 32) << 20) | (k & 0xFFFFFull); };
+  uint64_t ck[ZQ], km[ZQ];
   bool in[ZQ];
+  const uint64_t ref = compact(G.z.zkey[z0]);
+  uint64_t diff = 0ull;
 #pragma unroll
   for (int q = 0; q < ZQ; ++q) {
-    const int pos = ZQ * t + q;
-    km[q] = 0ull;
-    in[q] = false;
-    if (pos < n) {
-      const uint64_t k = G.z.zkey[pos];
-      km[q] = rmass(key_l(k), m);
-      G.z.zmass[pos] = km[q];
-      in[q] = k <= bound && (int)(uint32_t)k != excl;
-      lm += in[q] ? km[q] : 0ull;
-    }
+    const int pos = t + GT * q;
+    const bool pr = pos < n;
+    const uint64_t k = pr ? G.z.zkey[z0 + pos] : 0ull;
+    ck[q] = pr ? compact(k) : ~0ull;
+    km[q] = pr ? G.z.zmass[z0 + pos] : 0ull;
+    in[q] = pr && k <= bound && (int)(uint32_t)k != excl;
+    if (pr) diff |= ck[q] ^ ref;
   }
-  uint64_t exc, exm, totc, totm;
-  block_excl_scan2_u64<GT>(0ull, lm, S.u2, exc, exm, totc, totm);
-  int best = -1;
-  uint64_t bm = 0ull;
-  uint64_t fm = mass0 + exm;
+  diff = block_or_u64<GT>(diff, S.u);
+  int hb = diff ? 63 - __clzll((long long)diff) : -1;
+  uint64_t pmask = ~((2ull << (hb < 0 ? 0 : hb)) - 1ull);  // the bits every candidate shares
+  if (hb < 0) pmask = ~0ull;
+  uint64_t prefix = ref & pmask;
+  uint64_t bc = cnt0, bm = mass0;  // weights below the candidates
+  while (hb >= 0) {
+    const int shift = hb >= 7 ? hb - 7 : 0;
+    if (t < 256) {
+      S.prk[t] = 0u;
+      S.pmb[t] = 0ull;
+    }
+    __syncthreads();
 #pragma unroll
-  for (int q = 0; q < ZQ; ++q) {
-    const int pos = ZQ * t + q;
-    if (pos < n) {
-      const uint64_t before = by_mass ? fm : cnt0 + (uint64_t)pos;
-      const uint64_t own = by_mass ? (in[q] ? km[q] : 0ull) : 1ull;
-      if (own > 0ull && (double)before <= thr && (double)(before + own) > thr) {
-        best = pos;
-        bm = fm;
+    for (int q = 0; q < ZQ; ++q)
+      if ((ck[q] & pmask) == prefix) {
+        const int d = (int)((ck[q] >> shift) & 255ull);
+        atomicAdd(&S.prk[d], 1u);
+        if (in[q]) atomicAdd(&S.pmb[d], (unsigned long long)km[q]);
       }
-      fm += in[q] ? km[q] : 0ull;
+    __syncthreads();
+    if (w == 0) {
+      // lane l: digits 4 l .. 4 l + 3
+      uint32_t c[4];
+      uint64_t mm[4];
+      uint32_t lc = 0u;
+      uint64_t lm = 0ull;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = S.prk[4 * lane + i];
+        mm[i] = S.pmb[4 * lane + i];
+        lc += c[i];
+        lm += mm[i];
+      }
+      uint64_t Bc = bc + (uint64_t)(wave_incl_scan_u32(lc) - lc);
+      uint64_t Bm = bm + (wave_incl_scan_u64(lm) - lm);
+      int hit = -1;
+      uint64_t hc = 0ull, hm = 0ull;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint64_t before = by_mass ? Bm : Bc;
+        const uint64_t own = by_mass ? mm[i] : (uint64_t)c[i];
+        if (hit < 0 && own > 0ull && (double)before <= thr && (double)(before + own) > thr) {
+          hit = 4 * lane + i;
+          hc = Bc;
+          hm = Bm;
+        }
+        Bc += c[i];
+        Bm += mm[i];
+      }
+      const uint64_t bal = __ballot(hit >= 0);
+      if (lane == 0) S.ii[0] = -1;
+      if (bal != 0ull) {
+        const int hl = (int)__ffsll((long long)bal) - 1;
+        if (lane == hl) {
+          S.ii[0] = hit;
+          S.u2[0] = hc;
+          S.u2[1] = hm;
+        }
+      }
     }
+    __syncthreads();
+    const int d = S.ii[0];
+    if (d < 0) return GHit{~0ull, 0ull, 0ull, 0ull};  // (uniform) no key crosses
+    prefix |= (uint64_t)d << shift;
+    pmask |= 255ull << shift;
+    bc = S.u2[0];
+    bm = S.u2[1];
+    hb = shift - 1;
+    __syncthreads();  // (S.ii and S.u2 are rewritten by the next pass)
   }
-  const int psel = -block_min<GT>(-best, S.ii);
-  if (psel >= 0 && best == psel) {
-    S.res[slot][0] = G.z.zkey[psel];
-    S.res[slot][1] = cnt0 + (uint64_t)psel;
-    S.res[slot][2] = bm;
-    S.res[slot][3] = G.z.zmass[psel];
-    S.tag[slot] = np;
-  }
+  // the crossing key: the candidate whose compact key is the prefix
+#pragma unroll
+  for (int q = 0; q < ZQ; ++q)
+    if (ck[q] == prefix) {
+      const int pos = t + GT * q;
+      S.res[slot][0] = G.z.zkey[z0 + pos];
+      S.res[slot][1] = bc;
+      S.res[slot][2] = bm;
+      S.res[slot][3] = km[q];
+      S.tag[slot] = np;
+    }
   __syncthreads();
   if (S.tag[slot] != np) return GHit{~0ull, 0ull, 0ull, 0ull};
   return GHit{S.res[slot][0], S.res[slot][1], S.res[slot][2], S.res[slot][3]};
@@ -311,11 +374,12 @@ __device__ __forceinline__ uint64_t zone_mass_upto(GFinalShared& S, GBig& G, int
 // launch fields they read are passed: a reference to the argument block would copy it
 // to private memory).
 __device__ __noinline__ GHit pick_sorted_ool(lds_t<GFinalShared>* Sl, lds_t<GBig>* Gl, int np,
-                                             int n, bool by_mass, double thr, uint64_t bound,
-                                             int excl, uint64_t cnt0, uint64_t mass0, float m) {
+                                             int z0, int n, bool by_mass, double thr,
+                                             uint64_t bound, int excl, uint64_t cnt0,
+                                             uint64_t mass0) {
   GFinalShared& S = *(GFinalShared*)Sl;
   GBig& G = *(GBig*)Gl;
-  return pick_sorted(S, G, np, n, by_mass, thr, bound, excl, cnt0, mass0, m);
+  return pick_sorted(S, G, np, z0, n, by_mass, thr, bound, excl, cnt0, mass0);
 }
 // The last key passing min-p, (double)l - (double)m >= lmp: the first fkey (descending l)
 // that fails, less one.
@@ -377,6 +441,108 @@ __device__ __noinline__ int gumbel_kept(lds_t<GFinalShared>* Sl, const Cand* bas
   return S.misc[4];
 }
 
+// Streams row r's raw logits and allow-bits (a row without penalties) window by window,
+// GT * EPT tokens a window, with the loads of D windows issued before any of them is
+// consumed; fn(i0, x, bits) gets a thread's EPT values and their allow-bits (tokens past
+// the row end not allowed).
+template <bool BF16, int D, typename F>
+__device__ __forceinline__ void stream_nopen(const XArgs& a, int r, F&& fn) {
+  constexpr int WINT = GT * EPT;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int t = threadIdx.x;
+  const int64_t base = (int64_t)r * a.row_stride;
+  const glb_t<const uint8_t>* lg = (const glb_t<const uint8_t>*)a.logits;
+  const glb_t<const uint8_t>* mg =
+      a.mask ? (const glb_t<const uint8_t>*)(a.mask + (int64_t)r * a.mask_stride) : nullptr;
+  const int nwin = (a.V + WINT - 1) / WINT;
+  for (int w0 = 0; w0 < nwin; w0 += D) {
+    u32x4 x0[D], x1[D];
+    uint32_t mb[D];
+    // every load of the batch from a clamped index, no branch between them
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int i0 = (w0 + d) * WINT + t * EPT;
+      const int ii = i0 + EPT <= a.V ? i0 : 0;
+      if constexpr (BF16) {
+        x0[d] = *(const glb_t<const u32x4>*)(lg + 2 * (base + ii));
+      } else {
+        x0[d] = *(const glb_t<const u32x4>*)(lg + 4 * (base + ii));
+        x1[d] = *(const glb_t<const u32x4>*)(lg + 4 * (base + ii + 4));
+      }
+      mb[d] = mg ? (uint32_t)mg[ii >> 3] : 0xFFu;
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (w0 + d < nwin) {
+        const int i0 = (w0 + d) * WINT + t * EPT;
+        float x[EPT];
+        uint32_t bits = mb[d];
+        if (i0 + EPT <= a.V) {
+          if constexpr (BF16) {
+            const uint32_t wv[4] = {x0[d].x, x0[d].y, x0[d].z, x0[d].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              x[2 * e] = __uint_as_float(wv[e] << 16);
+              x[2 * e + 1] = __uint_as_float(wv[e] & 0xFFFF0000u);
+            }
+          } else {
+            const uint32_t wv[8] = {x0[d].x, x0[d].y, x0[d].z, x0[d].w,
+                                    x1[d].x, x1[d].y, x1[d].z, x1[d].w};
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) x[e] = __uint_as_float(wv[e]);
+          }
+        } else {
+          // the segment at the row end (or past it): element loads of the tokens inside
+          bits = (mg && i0 < a.V) ? (uint32_t)mg[i0 >> 3] : 0xFFu;
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) {
+            const int id = i0 + e < a.V ? i0 + e : 0;
+            x[e] = BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[base + id])
+                        : ((const float*)a.logits)[base + id];
+          }
+        }
+        if (i0 + EPT > a.V) bits &= i0 < a.V ? (1u << (a.V - i0)) - 1u : 0u;
+        fn(i0, x, bits & 0xFFu);
+      }
+    }
+  }
+}
+
+// The least float x with fl(x / T) >= A (T > 0; x / T rounded as the streaming passes
+// divide): x -> fl(x / T) is monotone. Stepped in ulps from A T (a few ulps from the
+// answer), or found by bisection over the floats in order where that does not settle.
+__device__ __forceinline__ float least_x_for(float T, float A) {
+  auto ord = [](float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  };
+  auto unord = [](uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+  };
+  const float x0 = A * T;
+  if (x0 > -INFINITY && x0 < INFINITY) {
+    uint32_t k = ord(x0);
+    if (unord(k) / T >= A) {
+      for (int it = 0; it < 16; ++it) {  // down while the float below still passes
+        if (!(unord(k - 1u) / T >= A)) return unord(k);
+        --k;
+      }
+    } else {
+      for (int it = 0; it < 16; ++it) {  // up to the first float that passes
+        ++k;
+        if (unord(k) / T >= A) return unord(k);
+      }
+    }
+  }
+  uint32_t lo = ord(-INFINITY), hi = ord(INFINITY);  // pred(hi) holds (A is finite)
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2u;
+    if (unord(mid) / T >= A) hi = mid;
+    else lo = mid + 1u;
+  }
+  return unord(lo);
+}
+
 // The LDS a collect pass writes (address-space-typed: see lds_t).
 struct ZoneLds {
   lds_t<uint64_t>* key;
@@ -403,16 +569,15 @@ __device__ __noinline__ int collect_zone(const XArgs a_in, int r, int b, int j,
   const int lane = threadIdx.x & (WAVE - 1);
   if (threadIdx.x == 0) *z.n = 0;
   __syncthreads();
-  x_pass<GT, false>(a, r, b, j, p, (uint32_t*)z.cnt,
-                    [&](int i0, const float (&l)[EPT], const float (&)[EPT]) {
-    uint32_t sel = 0u;
-    int c = 0;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e)
-      if (l[e] > -INFINITY && floorf(l[e] * (float)LBS) == at) {
-        sel |= 1u << e;
-        ++c;
-      }
+  // A(l) = at, l = x / T (x for a greedy row): at / LBS <= l < (at + 1) / LBS, both bounds
+  // exact floats; for a row without penalties the same test on x is xa <= x < xb
+  const float la = at * (1.0f / (float)LBS), lb = (at + 1.0f) * (1.0f / (float)LBS);
+  const float xa = p.greedy ? la : least_x_for(p.T, la);
+  const float xb = p.greedy ? lb : least_x_for(p.T, lb);
+  // appends the thread's selected tokens (bits of sel), l = lof(e): a lane loops over its
+  // own set bits only (a window selects few tokens, so most lanes none)
+  auto append = [&](int i0, uint32_t sel, auto&& lof) {
+    const int c = __popc(sel);
     int tot;
     const int ex = wave_excl_count(c, &tot);
     if (tot > 0) {
@@ -420,17 +585,40 @@ __device__ __noinline__ int collect_zone(const XArgs a_in, int r, int b, int j,
       if (lane == 0) base = atomicAdd((int*)z.n, tot);
       base = __builtin_amdgcn_readfirstlane(base);
       int pos = base + ex;
+      while (sel) {
+        const int e = __builtin_ctz(sel);
+        sel &= sel - 1u;
+        const float le = lof(e);
+        if (pos < ZCAP) {
+          z.key[pos] = ckey(le, i0 + e);
+          z.mass[pos] = rmass(le, m);
+        }
+        ++pos;
+      }
+    }
+  };
+  if (!p.pen && a.vec_ok) {
+    auto take_x = [&](int i0, const float (&x)[EPT], uint32_t bits) {
+      uint32_t sel = 0u;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) sel |= (((bits >> e) & 1u) && x[e] >= xa && x[e] < xb) ? 1u << e : 0u;
+      append(i0, sel, [&](int e) {
+        const float xe = pick8(x, e);
+        return p.greedy ? xe : xe / p.T;
+      });
+    };
+    if (a.dtype == STRIM_DTYPE_BF16) stream_nopen<true, 16>(a, r, take_x);
+    else stream_nopen<false, 8>(a, r, take_x);
+  } else {
+    x_pass<GT, false>(a, r, b, j, p, (uint32_t*)z.cnt,
+                      [&](int i0, const float (&l)[EPT], const float (&)[EPT]) {
+      uint32_t sel = 0u;
 #pragma unroll
       for (int e = 0; e < EPT; ++e)
-        if ((sel >> e) & 1u) {
-          if (pos < ZCAP) {
-            z.key[pos] = ckey(l[e], i0 + e);
-            z.mass[pos] = rmass(l[e], m);
-          }
-          ++pos;
-        }
-    }
-  });
+        sel |= (l[e] > -INFINITY && floorf(l[e] * (float)LBS) == at) ? 1u << e : 0u;
+      append(i0, sel, [&](int e) { return pick8(l, e); });
+    });
+  }
   __syncthreads();
   const int n = *z.n;
   return n <= ZCAP ? n : -1;
@@ -1095,12 +1283,12 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       GHit g;
       {
         const int np = npick++;
-        if (zn[h] <= GT)
+        if (zn[h] <= RADIX_MIN)
           g = pick_rank(S, G, np, zo[h], zn[h], cmd.by_mass != 0, cmd.thr, cmd.bnd, cmd.excl,
                         cmd.c0, cmd.m0);
-        else  // (a zone wider than the workgroup holds its bin alone, at offset 0: sorted)
-          g = pick_sorted_ool(Sl, Gl, np, zn[h], cmd.by_mass != 0, cmd.thr, cmd.bnd, cmd.excl,
-                              cmd.c0, cmd.m0, m);
+        else
+          g = pick_sorted_ool(Sl, Gl, np, zo[h], zn[h], cmd.by_mass != 0, cmd.thr, cmd.bnd,
+                              cmd.excl, cmd.c0, cmd.m0);
       }
       if (step == 0) {
         if (g.key == ~0ull) return false;

@@ -58,21 +58,6 @@ __device__ __forceinline__ int dv_rung(float dv) {
   const int r = (int)(__float_as_uint(dv) >> 20) - (int)VRUNG0;
   return r < 0 ? 0 : (r > VRUNG - 1 ? VRUNG - 1 : r);
 }
-// x[e] for a lane-varying e, by a three-level merge under bit masks of e. Integer
-// merges, not selects: a select between two elements of one array may be folded into
-// an indexed load, which would move the whole array to scratch memory.
-__device__ __forceinline__ uint32_t merge_bits(uint32_t lo, uint32_t hi, uint32_t m) {
-  return lo ^ ((lo ^ hi) & m);
-}
-__device__ __forceinline__ float pick8(const float (&x)[EPT], int e) {
-  const uint32_t m0 = 0u - ((uint32_t)e & 1u), m1 = 0u - (((uint32_t)e >> 1) & 1u);
-  const uint32_t m2 = 0u - (((uint32_t)e >> 2) & 1u);
-  uint32_t a[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    a[q] = merge_bits(__float_as_uint(x[2 * q]), __float_as_uint(x[2 * q + 1]), m0);
-  return __uint_as_float(merge_bits(merge_bits(a[0], a[1], m1), merge_bits(a[2], a[3], m1), m2));
-}
 // Smallest dv above rung r (r < VRUNG - 1).
 __device__ __forceinline__ float dv_rung_end(int r) {
   return __uint_as_float(((uint32_t)r + 1u + VRUNG0) << 20);
