@@ -528,10 +528,19 @@ def summarize(d):
         sub = "fetch" if cn == "FETCH_SIZE" else "write"
         for f in glob.glob(str(d / sub / "*counter_collection.csv")):
             rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Dispatch_Id"]))
-            case, pend = None, []
+            case, pend, gm = None, [], False
             for r in rows:
                 k = _kname(r["Kernel_Name"])
                 v = float(r["Counter_Value"])
+                # grammar masks: cache off first; a table install (k_gclear) after mask
+                # launches starts the cached ones
+                if k == "k_gclear":
+                    case = "grammar cached" if gm else "grammar produce"
+                    continue
+                if k == "k_gmask":
+                    gm = True
+                    if not str(case).startswith("grammar"):
+                        case = "grammar produce"
                 if k == "k_qprep":  # runs before its call's k_stream
                     pend.append((k, v))
                     continue
@@ -637,13 +646,29 @@ def pmc_pass(torch, ops, W, dev, steps, pool_mb):
         ops.head_logits(x, wt, nw)
     torch.cuda.synchronize()
     del wt
+    # grammar masks (the JSON-string DFA's in-string state, 8 rows of one state and 8 of
+    # distinct JSON-object states): with the mask cache off, then on
+    from strim_amd.grammar import DeviceGrammar
+    toks, skip = W.grammar_vocab()
+    nt_s, fl_s = W.json_string_dfa()
+    nt_o, fl_o, _ = W.json_object_dfa()
+    con = [i for i in range(nt_o.shape[0]) if fl_o[i] & 2][:GRAMMAR_ROWS]
+    for cache in (0, 4):
+        for nt, fl, keys in ((nt_s, fl_s, [1] * GRAMMAR_ROWS), (nt_o, fl_o, con)):
+            g = DeviceGrammar(toks, V, eos=W.GRAMMAR_EOS, skip=skip, cache_slots=cache)
+            g.set_dfa(nt, fl)
+            kd = torch.tensor(keys, dtype=torch.int32, device=dev)
+            for _ in range(steps):
+                g.masks(kd)
+            torch.cuda.synchronize()
+            g.close()
     src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
     ctx.close()
     print(f"pmc pass: {steps} steps each of n1, cfg3, cfg2, cfg5 and cfg4, 3 logits-producer "
-          "calls, one 256 MiB copy",
+          f"calls, {steps} grammar-mask launches per case, one 256 MiB copy",
           flush=True)
 
 
