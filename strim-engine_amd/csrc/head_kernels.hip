@@ -127,7 +127,7 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // two register buffers: the next step's loads are in flight while this step multiplies
   uint4 a[2][MT][4], bq[2][NT][4];
-  auto load = [&](int buf, int kb) {
+  auto loada = [&](int buf, int kb) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -136,6 +136,9 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
         const u32x4_t v = NTL ? __builtin_nontemporal_load(src) : *src;
         a[buf][mt][q] = make_uint4(v[0], v[1], v[2], v[3]);
       }
+  };
+  auto load = [&](int buf, int kb) {
+    loada(buf, kb);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -157,16 +160,89 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
   // scheduling barriers keep each buffer's loads issued before the other buffer's
   // multiplies: left alone, the compiler sinks the loads next to their use
   const int nsteps = K / HG_KS;
-  load(0, 0);
-  for (int s = 0; s < nsteps; s += 2) {
-    load(1, (s + 1) * HG_KS);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(0);
-    __builtin_amdgcn_sched_barrier(0);
-    load(0, min(s + 2, nsteps - 2) * HG_KS);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(1);
-    __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NT == 1) {
+    load(0, 0);
+    for (int s = 0; s < nsteps; s += 2) {
+      load(1, (s + 1) * HG_KS);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(0, min(s + 2, nsteps - 2) * HG_KS);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    // Several batch tiles: every wave needs the same 16 NT rows of xn at each step, so
+    // the workgroup stages them in LDS once (double-buffered, rows padded by 16 bytes so
+    // the 16 rows a wave reads fall in different banks) instead of each wave reading
+    // them from L2 (four times the bytes: that bound B = 64 at 2.7 TB/s). Thread t
+    // carries NT 16-byte pieces of the next step's slice while this step multiplies.
+    constexpr int XR = 16 * NT, XW = HG_KS + 8;  // rows, padded row length (bf16)
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[2][XR][XW];
+    uint4 xr[NT];
+    auto xload = [&](int kb) {
+#pragma unroll
+      for (int i = 0; i < NT; ++i) {
+        const int e = (int)threadIdx.x + NW * WAVE * i;  // piece e: row e / 16, column 8 (e % 16)
+        const int row = e >> 4, col = (e & 15) * 8;
+        const int n = min(row, B - 1);
+        xr[i] = *(const uint4*)(xn + (int64_t)n * xn_stride + kb + col);
+      }
+    };
+    auto xstore = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < NT; ++i) {
+        const int e = (int)threadIdx.x + NW * WAVE * i;
+        *(uint4*)&s_x[buf][e >> 4][(e & 15) * 8] = xr[i];
+      }
+    };
+    // the multiplies of one step from LDS buffer buf, the B operand read one K slice (q)
+    // at a time next to its MFMAs: NT registers of it live instead of 4 NT
+    auto mma_lds = [&](int buf, int abuf) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint4 bx[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          bx[nt] = *(const uint4*)&s_x[buf][nt * 16 + r16][32 * q + 8 * h];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, a[abuf][mt][q]), __builtin_bit_cast(bf16x8_t, bx[nt]),
+                acc[mt][nt], 0, 0, 0);
+      }
+    };
+    static_assert(NT * NW * WAVE * 8 == XR * HG_KS, "one step's slice: NT pieces a thread");
+    // The barrier waits for the LDS stores alone: __syncthreads' fence would also wait
+    // for the next step's weight loads, the prefetch this loop depends on. The slice's
+    // loads are issued before the weights', so its store waits for them only.
+    auto sync_lds = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    // Unrolled by two so each register buffer has a fixed index (the host checks that K
+    // is a multiple of two steps; the last prefetch reloads the last step, unused).
+    xload(0);
+    xstore(0);
+    loada(0, 0);
+    sync_lds();
+    for (int s = 0; s < nsteps; s += 2) {
+      xload((s + 1) * HG_KS);
+      loada(1, (s + 1) * HG_KS);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_lds(0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      xstore(1);
+      sync_lds();
+      const int s2 = min(s + 2, nsteps - 2) * HG_KS;
+      xload(s2);
+      loada(0, s2);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_lds(1, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      xstore(0);
+      sync_lds();
+    }
   }
   // lane l holds rows 4 h + i of each tile for batch row nt 16 + r16
   float bv[NT];
@@ -293,28 +369,33 @@ hipError_t launch_head(const void* hidden, int64_t hidden_stride, int B, int K,
     src = (const uint16_t*)xn;
     src_stride = K;
   }
-  constexpr int rows = HG_W * HG_MT * 16;  // vocabulary rows per workgroup
-  const dim3 grid((unsigned)((V + rows - 1) / rows)), blk(HG_W * WAVE);
+  // vocabulary rows per workgroup: 4 waves of HG_MT 16-row tiles (one tile a wave above
+  // B = 16 measured slower: 767 against 534 us at B = 64, the staged batch slice is then
+  // loaded for half as many weight rows)
   const int nt = (B + 15) / 16;
-#define STRIM_HEAD_GEMV(NT_)                                                                  \
-  if (tbest && vo)                                                                            \
-    hipLaunchKernelGGL((k_head_gemv<NT_, true, true>), grid, blk, 0, st, src, src_stride, B,  \
-                       K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, tbest); \
-  else if (tbest)                                                                             \
-    hipLaunchKernelGGL((k_head_gemv<NT_, false, true>), grid, blk, 0, st, src, src_stride, B, \
-                       K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, tbest); \
-  else if (vo)                                                                                \
-    hipLaunchKernelGGL((k_head_gemv<NT_, true>), grid, blk, 0, st, src, src_stride, B, K,    \
-                       (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, nullptr); \
-  else                                                                                        \
-    hipLaunchKernelGGL((k_head_gemv<NT_, false>), grid, blk, 0, st, src, src_stride, B, K,   \
-                       (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, nullptr);
+  const int rows = HG_W * HG_MT * 16;
+  const dim3 grid((unsigned)((V + rows - 1) / rows)), blk(HG_W * WAVE);
+#define STRIM_HEAD_GEMV(NT_, MT_)                                                                \
+  if (tbest && vo)                                                                               \
+    hipLaunchKernelGGL((k_head_gemv<NT_, true, true, MT_>), grid, blk, 0, st, src, src_stride, B, \
+                       K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, tbest);    \
+  else if (tbest)                                                                                \
+    hipLaunchKernelGGL((k_head_gemv<NT_, false, true, MT_>), grid, blk, 0, st, src, src_stride,   \
+                       B, K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride, tbest); \
+  else if (vo)                                                                                   \
+    hipLaunchKernelGGL((k_head_gemv<NT_, true, false, MT_>), grid, blk, 0, st, src, src_stride,   \
+                       B, K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride,         \
+                       nullptr);                                                                 \
+  else                                                                                           \
+    hipLaunchKernelGGL((k_head_gemv<NT_, false, false, MT_>), grid, blk, 0, st, src, src_stride,  \
+                       B, K, (const uint16_t*)W, w_stride, V, (uint16_t*)out, out_stride,         \
+                       nullptr);
   if (nt == 1) {
-    STRIM_HEAD_GEMV(1)
+    STRIM_HEAD_GEMV(1, HG_MT)
   } else if (nt == 2) {
-    STRIM_HEAD_GEMV(2)
+    STRIM_HEAD_GEMV(2, HG_MT)
   } else {
-    STRIM_HEAD_GEMV(4)
+    STRIM_HEAD_GEMV(4, HG_MT)
   }
 #undef STRIM_HEAD_GEMV
   if (tbest)
