@@ -877,13 +877,13 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     // ---- the leader alone ------------------------------------------------------------
     // A row whose zones are small (the common case) is decided by wave 0 alone, with no
     // workgroup barrier: it lays out each zone from the prefetched candidates (lane c
-    // copies chunk c's part) and ranks the zone's keys within the wave, one key a lane (a
-    // wave's serial scan costs four cycles an instruction, so wider zones go to the eight
-    // waves). A zone that needs a chunk's slot region or a collect pass, or holds more
-    // than SOLO keys, and Gumbel
-    // draws, go to the cooperative loop below (every wave; it starts over). Both follow
-    // the same decision rules.
-    constexpr int SOLO = WAVE;
+    // copies chunk c's part) and picks within the wave: up to 64 keys by a serial scan
+    // of ranks (one key a lane), up to SOLO by a radix select in the wave (a wave's
+    // serial scan costs four cycles an instruction). A zone that needs a chunk's slot
+    // region or a collect pass, or holds more than SOLO keys, and Gumbel draws, go to the
+    // cooperative loop below (every wave; it starts over). Both follow the same decision
+    // rules.
+    constexpr int SQ = 3, SOLO = SQ * WAVE;  // zone keys a lane holds, a zone's keys
     bool pfok = true;  // the prefetched candidates are in LDS
     auto solo = [&]() -> int {  // 0 decided, 1 cooperative, 2 exact resolution
       if (!icdf) return 1;
@@ -940,8 +940,101 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         else if (bz == zb1) { z0 = zn0; n = zn1; }
       };
       // pick_rank within the wave: lane l holds key z0 + l
+      // wider zones (65..SOLO keys, SQ a lane): pick_sorted's radix select within the wave.
+      // The wave's LDS operations complete in order, so its digit histogram (S.prk /
+      // S.pmb, idle while the leader decides alone) needs no barrier.
+      auto wradix = [&](int z0, int n, bool by_mass, double thr, uint64_t bnd, int excl,
+                        uint64_t c0, uint64_t m0) -> GHit {
+        auto compact = [](uint64_t k) { return ((k >> 32) << 20) | (k & 0xFFFFFull); };
+        uint64_t ck[SQ], km[SQ];
+        bool in[SQ];
+        uint64_t diff = 0ull;
+        const uint64_t ref = compact(G.z.zkey[z0]);
+#pragma unroll
+        for (int q = 0; q < SQ; ++q) {
+          const int i = lane + WAVE * q;
+          const bool pr = i < n;
+          const uint64_t k = pr ? G.z.zkey[z0 + i] : 0ull;
+          ck[q] = pr ? compact(k) : ~0ull;
+          km[q] = pr ? G.z.zmass[z0 + i] : 0ull;
+          in[q] = pr && k <= bnd && (int)(uint32_t)k != excl;
+          if (pr) diff |= ck[q] ^ ref;
+        }
+        diff = ((uint64_t)(uint32_t)wave_or_i((int)(uint32_t)(diff >> 32)) << 32) |
+               (uint32_t)wave_or_i((int)(uint32_t)diff);
+        int hb = diff ? 63 - __clzll((long long)diff) : -1;
+        uint64_t pmask = hb < 0 ? ~0ull : ~((2ull << hb) - 1ull);
+        uint64_t prefix = ref & pmask;
+        uint64_t bc = c0, bm = m0;
+        while (hb >= 0) {
+          const int shift = hb >= 7 ? hb - 7 : 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            S.prk[4 * lane + i] = 0u;
+            S.pmb[4 * lane + i] = 0ull;
+          }
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int q = 0; q < SQ; ++q)
+            if ((ck[q] & pmask) == prefix) {
+              const int d = (int)((ck[q] >> shift) & 255ull);
+              atomicAdd(&S.prk[d], 1u);
+              if (in[q]) atomicAdd(&S.pmb[d], (unsigned long long)km[q]);
+            }
+          __builtin_amdgcn_wave_barrier();
+          uint32_t c[4];
+          uint64_t mm[4];
+          uint32_t lc = 0u;
+          uint64_t lm = 0ull;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            c[i] = S.prk[4 * lane + i];
+            mm[i] = S.pmb[4 * lane + i];
+            lc += c[i];
+            lm += mm[i];
+          }
+          uint64_t Bc = bc + (uint64_t)(wave_incl_scan_u32(lc) - lc);
+          uint64_t Bm = bm + (wave_incl_scan_u64(lm) - lm);
+          int hit = -1;
+          uint64_t hc = 0ull, hm = 0ull;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint64_t before = by_mass ? Bm : Bc;
+            const uint64_t own = by_mass ? mm[i] : (uint64_t)c[i];
+            if (hit < 0 && own > 0ull && (double)before <= thr && (double)(before + own) > thr) {
+              hit = 4 * lane + i;
+              hc = Bc;
+              hm = Bm;
+            }
+            Bc += c[i];
+            Bm += mm[i];
+          }
+          const uint64_t bal = __ballot(hit >= 0);
+          if (bal == 0ull) return GHit{~0ull, 0ull, 0ull, 0ull};
+          const int hl = (int)__ffsll((long long)bal) - 1;
+          const int d = __builtin_amdgcn_readlane(hit, hl);
+          bc = rl_u64(hc, hl);
+          bm = rl_u64(hm, hl);
+          prefix |= (uint64_t)d << shift;
+          pmask |= 255ull << shift;
+          hb = shift - 1;
+          __builtin_amdgcn_wave_barrier();  // (this pass's reads before the next clear)
+        }
+        // the crossing key: its holder's key and mass
+        int hq = -1;
+#pragma unroll
+        for (int q = 0; q < SQ; ++q)
+          if (ck[q] == prefix) hq = q;
+        const uint64_t bal = __ballot(hq >= 0);
+        if (bal == 0ull) return GHit{~0ull, 0ull, 0ull, 0ull};
+        const int hl = (int)__ffsll((long long)bal) - 1;
+        const int q = __builtin_amdgcn_readlane(hq, hl);
+        const uint64_t key = G.z.zkey[z0 + hl + WAVE * q], kmass = G.z.zmass[z0 + hl + WAVE * q];
+        return GHit{key, bc, bm, kmass};
+      };
       auto wpick = [&](int z0, int n, bool by_mass, double thr, uint64_t bnd, int excl,
                        uint64_t c0, uint64_t m0) -> GHit {
+        if (n > WAVE) return wradix(z0, n, by_mass, thr, bnd, excl, c0, m0);
         const bool mine = lane < n;
         const uint64_t k = mine ? G.z.zkey[z0 + lane] : ~0ull;
         const uint64_t km = mine ? G.z.zmass[z0 + lane] : 0ull;
@@ -963,7 +1056,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         return GHit{rl_u64(k, hl), c0 + (uint32_t)__builtin_amdgcn_readlane((int)rk, hl),
                     m0 + rl_u64(mb, hl), rl_u64(km, hl)};
       };
-      // the zone's masses of keys <= bnd
+      // the zone's masses of keys <= bnd (n <= SOLO)
       auto wsum = [&](int z0, int n, uint64_t bnd) -> uint64_t {
         uint64_t sm = 0ull;
         for (int i = lane; i < n; i += WAVE) sm += G.z.zkey[z0 + i] <= bnd ? G.z.zmass[z0 + i] : 0ull;
