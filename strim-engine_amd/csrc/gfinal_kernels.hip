@@ -129,33 +129,43 @@ struct GHit {
 };
 
 // The row's cumulative histogram in a wave's registers: lane l holds bins LPL l + q.
+// Three named members, not an array: a runtime-indexed array would be placed in scratch
+// memory, a round trip to the cache for every read.
 struct RowCum {
-  uint32_t c[LPL];
-  uint64_t m[LPL];
-  __device__ __forceinline__ uint32_t cq(int q) const { return q == 0 ? c[0] : (q == 1 ? c[1] : c[2]); }
-  __device__ __forceinline__ uint64_t mq(int q) const { return q == 0 ? m[0] : (q == 1 ? m[1] : m[2]); }
+  uint32_t c0, c1, c2;
+  uint64_t m0, m1, m2;
+  __device__ __forceinline__ uint32_t& cq(int q) { return q == 0 ? c0 : (q == 1 ? c1 : c2); }
+  __device__ __forceinline__ uint64_t& mq(int q) { return q == 0 ? m0 : (q == 1 ? m1 : m2); }
   // inclusive cumulative count / mass of bin b (wave-uniform; b < 0: 0, b past the row's
-  // window: the window's total)
+  // window: the window's total): the three bins of lane b / LPL read, one kept
   __device__ __forceinline__ uint64_t cnt(int b) const {
     if (b < 0) return 0ull;
     if (b >= NBW) b = NBW - 1;
-    return (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)cq(b % LPL), b / LPL);
+    const int L = b / LPL, q = b - LPL * L;
+    const uint32_t v0 = (uint32_t)__builtin_amdgcn_readlane((int)c0, L);
+    const uint32_t v1 = (uint32_t)__builtin_amdgcn_readlane((int)c1, L);
+    const uint32_t v2 = (uint32_t)__builtin_amdgcn_readlane((int)c2, L);
+    return (uint64_t)(q == 0 ? v0 : (q == 1 ? v1 : v2));
   }
   __device__ __forceinline__ uint64_t mass(int b) const {
     if (b < 0) return 0ull;
     if (b >= NBW) b = NBW - 1;
-    return rl_u64(mq(b % LPL), b / LPL);
+    const int L = b / LPL, q = b - LPL * L;
+    const uint64_t v0 = rl_u64(m0, L), v1 = rl_u64(m1, L), v2 = rl_u64(m2, L);
+    return q == 0 ? v0 : (q == 1 ? v1 : v2);
   }
   // the first bin b < limit whose cumulative value (the mass less excl_w from bin excl_b
   // on) exceeds thr; limit when none does
   __device__ __forceinline__ int find(bool by_mass, double thr, int limit, uint64_t excl_w,
                                       int excl_b) const {
     const int lane = threadIdx.x & (WAVE - 1);
+    const uint32_t cc[LPL] = {c0, c1, c2};
+    const uint64_t mm[LPL] = {m0, m1, m2};
     int first = NOBIN;
 #pragma unroll
     for (int q = LPL - 1; q >= 0; --q) {
       const int b = LPL * lane + q;
-      const uint64_t val = by_mass ? m[q] - (b >= excl_b ? excl_w : 0ull) : (uint64_t)c[q];
+      const uint64_t val = by_mass ? mm[q] - (b >= excl_b ? excl_w : 0ull) : (uint64_t)cc[q];
       if (b < limit && (double)val > thr) first = b;
     }
     first = wave_min_i(first);
@@ -844,20 +854,20 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
 #pragma unroll
       for (int q = 0; q < LPL; ++q) {
         const int bq = LPL * lane + q;
-        rcum.c[q] = S.rc[bq];
+        rcum.cq(q) = S.rc[bq];
         const float sc = base * __builtin_amdgcn_exp2f(-(float)bq * (1.44269504f / (float)LBS));
-        rcum.m[q] = (uint64_t)__double2ull_rn((double)S.rm[bq] * (double)sc);
-        lc += rcum.c[q];
-        lm += rcum.m[q];
+        rcum.mq(q) = (uint64_t)__double2ull_rn((double)S.rm[bq] * (double)sc);
+        lc += rcum.cq(q);
+        lm += rcum.mq(q);
       }
       uint32_t bc = wave_incl_scan_u32(lc) - lc;
       uint64_t bm = wave_incl_scan_u64(lm) - lm;
 #pragma unroll
       for (int q = 0; q < LPL; ++q) {
-        bc += rcum.c[q];
-        bm += rcum.m[q];
-        rcum.c[q] = bc;
-        rcum.m[q] = bm;
+        bc += rcum.cq(q);
+        bm += rcum.mq(q);
+        rcum.cq(q) = bc;
+        rcum.mq(q) = bm;
       }
     }
     const int rowwin = S.misc[1] < NBW ? S.misc[1] : NBW;

@@ -180,21 +180,25 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
     // carries NT 16-byte pieces of the next step's slice while this step multiplies.
     constexpr int XR = 16 * NT, XW = HG_KS + 8;  // rows, padded row length (bf16)
     __shared__ __attribute__((aligned(16))) uint16_t s_x[2][XR][XW];
-    uint4 xr[NT];
-    auto xload = [&](int kb) {
+    struct Slice {
+      uint4 v[NT];
+    };
+    auto xload = [&](int kb) -> Slice {
+      Slice xr;
 #pragma unroll
       for (int i = 0; i < NT; ++i) {
         const int e = (int)threadIdx.x + NW * WAVE * i;  // piece e: row e / 16, column 8 (e % 16)
         const int row = e >> 4, col = (e & 15) * 8;
         const int n = min(row, B - 1);
-        xr[i] = *(const uint4*)(xn + (int64_t)n * xn_stride + kb + col);
+        xr.v[i] = *(const uint4*)(xn + (int64_t)n * xn_stride + kb + col);
       }
+      return xr;
     };
-    auto xstore = [&](int buf) {
+    auto xstore = [&](int buf, const Slice& xr) {
 #pragma unroll
       for (int i = 0; i < NT; ++i) {
         const int e = (int)threadIdx.x + NW * WAVE * i;
-        *(uint4*)&s_x[buf][e >> 4][(e & 15) * 8] = xr[i];
+        *(uint4*)&s_x[buf][e >> 4][(e & 15) * 8] = xr.v[i];
       }
     };
     // the multiplies of one step from LDS buffer buf, the B operand read one K slice (q)
@@ -222,25 +226,24 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
     auto sync_lds = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
     // Unrolled by two so each register buffer has a fixed index (the host checks that K
     // is a multiple of two steps; the last prefetch reloads the last step, unused).
-    xload(0);
-    xstore(0);
+    xstore(0, xload(0));
     loada(0, 0);
     sync_lds();
     for (int s = 0; s < nsteps; s += 2) {
-      xload((s + 1) * HG_KS);
+      const Slice x1 = xload((s + 1) * HG_KS);
       loada(1, (s + 1) * HG_KS);
       __builtin_amdgcn_sched_barrier(0);
       mma_lds(0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      xstore(1);
+      xstore(1, x1);
       sync_lds();
       const int s2 = min(s + 2, nsteps - 2) * HG_KS;
-      xload(s2);
+      const Slice x0 = xload(s2);
       loada(0, s2);
       __builtin_amdgcn_sched_barrier(0);
       mma_lds(1, 1);
       __builtin_amdgcn_sched_barrier(0);
-      xstore(0);
+      xstore(0, x0);
       sync_lds();
     }
   }
