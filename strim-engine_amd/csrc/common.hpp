@@ -53,6 +53,12 @@ constexpr int WAVE = 64;
 static_assert(CHUNK == TPB * EPT, "chunk geometry");
 
 // ---- scalar helpers --------------------------------------------------------------
+// The thread's wave in its workgroup, as a scalar: the compiler cannot tell that
+// threadIdx.x / WAVE is uniform over a wave, and would otherwise keep it (and every loop
+// bound or branch derived from it) in vector registers under exec masks.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)threadIdx.x / WAVE);
+}
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
@@ -275,7 +281,7 @@ __device__ __forceinline__ double wave_incl_scan(double v) {
 // `scratch` holds >= NT/64 doubles. Returns the exclusive prefix; *total gets the sum.
 template <int NT>
 __device__ __forceinline__ double block_excl_scan_f64(double v, double* scratch, double* total) {
-  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1), w = wave_id();
   const double inc = wave_incl_scan(v);
   if (lane == WAVE - 1) scratch[w] = inc;
   __syncthreads();
@@ -311,7 +317,7 @@ template <int NT>
 __device__ __forceinline__ void block_excl_scan2_u64(uint64_t v1, uint64_t v2, uint64_t* scratch,
                                                      uint64_t& ex1, uint64_t& ex2,
                                                      uint64_t& tot1, uint64_t& tot2) {
-  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1), w = wave_id();
   const uint64_t i1 = wave_incl_scan_u64(v1), i2 = wave_incl_scan_u64(v2);
   if (lane == WAVE - 1) {
     scratch[w] = i1;

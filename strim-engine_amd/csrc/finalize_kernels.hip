@@ -169,7 +169,7 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
                                                  const RowParams& p, const RowPre& pf,
                                                  FinalShared& S) {
   const ExactReq done{0, 0.0f, -1, -1, 0.0f};
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int V = a.V, W = a.W;
   const bool vdr = a.verify && j < a.k;  // a verify row with a draft
   const int draft = pf.draft;

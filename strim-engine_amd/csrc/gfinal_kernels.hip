@@ -86,7 +86,8 @@ struct GCmd {
   double thr;
   uint64_t bnd, c0, m0, bmp;
 };
-struct GFinalShared {  uint16_t pc[LWMAX][NBW];        // per chunk: inclusive count prefix of its window bins
+struct GFinalShared {
+  uint16_t pc[LWMAX][NBW];        // per chunk: inclusive count prefix of its window bins
   uint32_t rc[NBW];               // row bins: counts
   unsigned long long rm[NBW];     // row bins: masses (RFIX per unit of exp(l - m))
   float mch[LWMAX];               // per chunk: its maximum
@@ -139,6 +140,7 @@ struct RowCum {
   // inclusive cumulative count / mass of bin b (wave-uniform; b < 0: 0, b past the row's
   // window: the window's total): the three bins of lane b / LPL read, one kept
   __device__ __forceinline__ uint64_t cnt(int b) const {
+    b = uniform_copy(b);
     if (b < 0) return 0ull;
     if (b >= NBW) b = NBW - 1;
     const int L = b / LPL, q = b - LPL * L;
@@ -148,6 +150,7 @@ struct RowCum {
     return (uint64_t)(q == 0 ? v0 : (q == 1 ? v1 : v2));
   }
   __device__ __forceinline__ uint64_t mass(int b) const {
+    b = uniform_copy(b);
     if (b < 0) return 0ull;
     if (b >= NBW) b = NBW - 1;
     const int L = b / LPL, q = b - LPL * L;
@@ -169,7 +172,7 @@ struct RowCum {
       if (b < limit && (double)val > thr) first = b;
     }
     first = wave_min_i(first);
-    return first < limit ? first : limit;
+    return uniform_copy(first < limit ? first : limit);
   }
 };
 static_assert(LPL == 3, "RowCum holds three bins per lane");
@@ -258,7 +261,7 @@ __device__ __forceinline__ GHit pick_rank(GFinalShared& S, GBig& G, int np, int 
 __device__ __forceinline__ GHit pick_sorted(GFinalShared& S, GBig& G, int np, int z0, int n,
                                             bool by_mass, double thr, uint64_t bound, int excl,
                                             uint64_t cnt0, uint64_t mass0) {
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int slot = np & 1;
   auto compact = [](uint64_t k) { return ((k >> 32) << 20) | (k & 0xFFFFFull); };
   uint64_t ck[ZQ], km[ZQ];
@@ -366,7 +369,7 @@ __device__ __forceinline__ GHit pick_sorted(GFinalShared& S, GBig& G, int np, in
 // thread; two barriers).
 __device__ __forceinline__ uint64_t zone_mass_upto(GFinalShared& S, GBig& G, int z0, int n,
                                                   uint64_t bound) {
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   uint64_t s = 0ull;
   for (int i = t; i < n; i += GT) s += G.z.zkey[z0 + i] <= bound ? G.z.zmass[z0 + i] : 0ull;
   s = wave_sum_u64(s);
@@ -406,7 +409,7 @@ __device__ __noinline__ int gumbel_kept(lds_t<GFinalShared>* Sl, const Cand* bas
                                         int draft, const RowParams p, float m, uint64_t S1,
                                         bool cand_sorted) {
   GFinalShared& S = *(GFinalShared*)Sl;
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   if (w == 0) {
     // lane c: chunk c's entries up to its part of the bound's bin
     int lim = 0;
@@ -645,7 +648,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const int r = blockIdx.x;
   int b, j;
   row_bj(a, r, b, j);
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int V = a.V, W = a.W;
   // ---- every load that does not depend on the row's parameters ------------------
   // the chunk statistics (one chunk per thread), the noise, the draft and the chunks'
@@ -821,18 +824,34 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       const int nbreg = lane < W ? S.nbch[lane] : 0;
       uint32_t cs_ = 0u;
       uint64_t ms_ = 0ull;
-      for (int c = g; c < W; c += 2) {
-        const int d = __builtin_amdgcn_readlane(dreg, c);
-        const int nb = __builtin_amdgcn_readlane(nbreg, c);
-        const int lb = bq - d;
-        if (lb >= 0 && lb < nb) {
-          const uint64_t wv = G.E[c * NBW + lb];
-          const uint32_t prev = lb > 0 ? (uint32_t)(G.E[c * NBW + lb - 1] >> LCSH) : 0u;
-          const uint32_t incl = (uint32_t)(wv >> LCSH);
-          S.pc[c][lb] = (uint16_t)incl;
-          cs_ += incl - prev;
-          ms_ += wv & LMMASK;
+      // four chunks a step, their words read unconditionally (clamped places, results
+      // dropped) so the reads are issued together rather than one LDS round trip each
+      constexpr int CU = 4;
+      for (int c0 = g; c0 < W; c0 += 2 * CU) {
+        uint64_t wv[CU], pv[CU];
+        int lbs[CU];
+        bool ok[CU];
+#pragma unroll
+        for (int u = 0; u < CU; ++u) {
+          const int c = c0 + 2 * u, cc = c < W ? c : g;
+          const int d = __builtin_amdgcn_readlane(dreg, cc);
+          const int nb = __builtin_amdgcn_readlane(nbreg, cc);
+          const int lb = bq - d;
+          ok[u] = c < W && lb >= 0 && lb < nb;
+          lbs[u] = lb;
+          const int e = ok[u] ? c * NBW + lb : 0;
+          wv[u] = G.E[e];
+          pv[u] = G.E[e > 0 ? e - 1 : 0];
         }
+#pragma unroll
+        for (int u = 0; u < CU; ++u)
+          if (ok[u]) {
+            const uint32_t prev = lbs[u] > 0 ? (uint32_t)(pv[u] >> LCSH) : 0u;
+            const uint32_t incl = (uint32_t)(wv[u] >> LCSH);
+            S.pc[c0 + 2 * u][lbs[u]] = (uint16_t)incl;
+            cs_ += incl - prev;
+            ms_ += wv[u] & LMMASK;
+          }
       }
       if (cs_) {
         atomicAdd(&S.rc[bq], cs_);
@@ -870,9 +889,10 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         rcum.mq(q) = bm;
       }
     }
-    const int rowwin = S.misc[1] < NBW ? S.misc[1] : NBW;
-    const int rowfull = S.misc[0] < rowwin ? S.misc[0] : rowwin;
-    const bool anytail = S.misc[3] != 0;
+    // (LDS values the same in every lane, kept in scalar registers: see uniform_copy)
+    const int rowwin = uniform_copy(S.misc[1] < NBW ? S.misc[1] : NBW);
+    const int rowfull = uniform_copy(S.misc[0] < rowwin ? S.misc[0] : rowwin);
+    const bool anytail = uniform_copy(S.misc[3]) != 0;
     const int n_all = wave_sum(lane < W ? S.ncnt[lane] : 0);
     const double S_all = wave_sum(lane < W ? S.sch[lane] : 0.0);
     const uint64_t S0 = (uint64_t)__double2ull_rn(S_all * RFIX);
@@ -926,12 +946,20 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         }
         if (__ballot(!ok) != 0ull) return 1;
         zoo[1] += n[0];
+        // lane c copies chunk c's part, four candidates a step (their reads issued
+        // together; places past the part are clamped inside the chunk's prefetch)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
-          for (int i = 0; i < cnt[hh]; ++i) {
-            const Cand x = P.pfb[lane * PF + off[hh] + i];
-            G.z.zkey[zoo[hh] + i] = ckey(x.l, x.id);
-            G.z.zmass[zoo[hh] + i] = rmass(x.l, m);
+          for (int i0 = 0; i0 < cnt[hh]; i0 += 4) {
+            Cand x[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = P.pfb[lane * PF + min(off[hh] + i0 + u, PF - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (i0 + u < cnt[hh]) {
+                G.z.zkey[zoo[hh] + i0 + u] = ckey(x[u].l, x[u].id);
+                G.z.zmass[zoo[hh] + i0 + u] = rmass(x[u].l, m);
+              }
           }
         // (one wave's LDS operations complete in order: its later reads see these)
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -1044,19 +1072,37 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       };
       auto wpick = [&](int z0, int n, bool by_mass, double thr, uint64_t bnd, int excl,
                        uint64_t c0, uint64_t m0) -> GHit {
+        z0 = uniform_copy(z0);
+        n = uniform_copy(n);
         if (n > WAVE) return wradix(z0, n, by_mass, thr, bnd, excl, c0, m0);
         const bool mine = lane < n;
         const uint64_t k = mine ? G.z.zkey[z0 + lane] : ~0ull;
         const uint64_t km = mine ? G.z.zmass[z0 + lane] : 0ull;
         const bool in = mine && k <= bnd && (int)(uint32_t)k != excl;
         const uint64_t kin = in ? km : 0ull;  // its mass where it is kept
+        // every lane compares its key with each zone key, read from LDS as a broadcast
+        // eight at a time (S.pmb, idle while the leader decides alone, holds the kept
+        // masses; the wave's LDS operations complete in order)
+        if (mine) S.pmb[lane] = kin;
+        __builtin_amdgcn_wave_barrier();
         uint32_t rk = 0u;
         uint64_t mb = 0ull;
-        for (int jj = 0; jj < n; ++jj) {
-          const bool lt = rl_u64(k, jj) < k;
-          rk += lt ? 1u : 0u;
-          mb += lt ? rl_u64(kin, jj) : 0ull;
+        for (int j0 = 0; j0 < n; j0 += 8) {
+          uint64_t kj[8], mj[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int jj = min(j0 + u, n - 1);
+            kj[u] = G.z.zkey[z0 + jj];
+            mj[u] = S.pmb[jj];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const bool lt = j0 + u < n && kj[u] < k;
+            rk += lt ? 1u : 0u;
+            mb += lt ? mj[u] : 0ull;
+          }
         }
+        __builtin_amdgcn_wave_barrier();  // (the reads before a later pick's stores)
         const uint64_t before = by_mass ? m0 + mb : c0 + rk;
         const uint64_t own = by_mass ? kin : 1ull;
         const bool hit = mine && own > 0ull && (double)before <= thr && (double)(before + own) > thr;
@@ -1184,8 +1230,9 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
       if (lane == 0) S.misc[5] = verdict;
     }
     __syncthreads();
-    if (S.misc[5] == 0) return true;
-    if (S.misc[5] == 2) return false;
+    const int verdict = uniform_copy(S.misc[5]);
+    if (verdict == 0) return true;
+    if (verdict == 2) return false;
 
     // The zone in LDS: up to two bins, zb[h] at [zo[h], zo[h] + zn[h]). A chunk's part of a
     // bin comes from its prefetched candidates when it lies among them, else from its slot
@@ -1329,7 +1376,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         if (lane == 0) S.cmd = cmd;
       }
       __syncthreads();
-      const GCmd cmd = S.cmd;
+      const GCmd cmd = uniform_copy(S.cmd);
       if (cmd.op == GOP_FAIL) return false;
       if (cmd.op == GOP_SKIP) continue;
       if (cmd.op == GOP_BOUND) {

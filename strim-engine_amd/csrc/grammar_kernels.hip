@@ -172,7 +172,7 @@ __global__ __launch_bounds__(GM_T) void k_gmask(GView g, const int32_t* keys, in
   __shared__ int s_dup[GM_DUP];
   __shared__ int s_ndup, s_slot, s_mode;
   const int blk = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
-  const int lane = t & (WAVE - 1), w = t / WAVE;
+  const int lane = t & (WAVE - 1), w = wave_id();
   const int key = keys[r];
   const bool grammar = key >= 0 && key < g.n_states;
   const bool cache = grammar && g.nsets > 0;

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(NW* WAVE) void k_head_gemv(const uint16_t* xn, int6
                                                           int64_t w_stride, int V,
                                                           uint16_t* out, int64_t out_stride,
                                                           uint2* tbest) {
-  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1), wv = wave_id();
   const int h = lane >> 4, r16 = lane & 15;
   const int v0 = blockIdx.x * (NW * MT * 16) + wv * (MT * 16);
   // rows past V or B read a clamped row; their results are not stored
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(HP_T) void k_head_pick(const uint2* tbest, int ntil
                                                      int32_t* out_ids, int32_t* out_status) {
   __shared__ float s_v[HP_T / WAVE];
   __shared__ int s_i[HP_T / WAVE], s_bad[HP_T / WAVE];
-  const int n = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int n = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   float v = -INFINITY;
   int i = INT_MAX;
   bool bad = false;

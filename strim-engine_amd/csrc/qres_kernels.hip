@@ -313,7 +313,7 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   __shared__ uint64_t s_red[TPB / WAVE];
   __shared__ double s_sc[TPB / WAVE];
   __shared__ int s_id[TPB / WAVE];
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   int r, c, b, j;
   if (a.qskip) {
     b = blockIdx.y;
@@ -427,7 +427,7 @@ template <bool COMBINE>
 __global__ __launch_bounds__(QGP_W * WAVE) void k_qgpick(Args a) {
   __shared__ RowOut s_out[MAXP];
   __shared__ int s_mine[MAXP];
-  const int b = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   for (int j = w; j < a.k; j += QGP_W) {
     const int r = b * (a.k + 1) + j;
     RowState* rs = &a.s.rs[r];

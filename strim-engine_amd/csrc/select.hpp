@@ -58,7 +58,7 @@ __device__ __forceinline__ int wave_excl_count32(int c, int* total) {
 template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* scratch,
                                                         uint32_t* total) {
-  const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1), w = wave_id();
   const uint32_t inc = wave_incl_scan_u32(v);
   if (lane == WAVE - 1) scratch[w] = inc;
   __syncthreads();
@@ -198,7 +198,7 @@ __device__ __forceinline__ void wave_top2(float& s0, float& l0, int& i0, float& 
 template <int NT>
 __device__ __forceinline__ void block_argmax_score(double sc, uint64_t tk, int id, double* s_sc,
                                                    uint64_t* s_tk, int* s_id, int* out_id) {
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   auto take = [](double& a, uint64_t& ak, int& ai, double b, uint64_t bk, int bi) {
     if (bi >= 0 && (ai < 0 || b > a || (b == a && bk < ak))) { a = b; ak = bk; ai = bi; }
   };
@@ -607,7 +607,7 @@ __device__ inline void sort_keys(uint64_t (&kk)[FIN_Q], int n, uint64_t* s_key, 
     // as a sorted run; a key's rank is its rank in its run plus its lower bound in each
     // other run (keys are unique, so the ranks are a permutation of 0..n-1). Pads sort
     // after every key (a finite l has key bits below 0xFF800000 << 32).
-    const int w = t / WAVE, lane = t & (WAVE - 1);
+    const int w = wave_id(), lane = t & (WAVE - 1);
     const uint64_t k0 = t < n ? kk[0] : (0xFFFFFFFF00000000ull | (uint32_t)t);
     uint64_t* run = s_key + FIN_T;  // FIN_T sorted keys, 64 per run
     s_key[t] = k0;

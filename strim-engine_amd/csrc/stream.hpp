@@ -160,7 +160,7 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
   map_block(a, r, c);
   int b, j;
   row_bj(a, r, b, j);
-  const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int c0 = c * CHUNK;
   const bool full = VEC && c0 + CHUNK <= a.V;
   ChunkStat* csp = &a.s.cstat[(int64_t)r * a.s.wmax + c];
