@@ -25,9 +25,8 @@ __global__ void k_qhist(Args a);
 __global__ void k_qpick(Args a);
 __global__ void k_qcollect(Args a);
 __global__ void k_qfinal(Args a);
-__global__ void k_qgumbel(Args a);
-hipError_t launch_qgpick(const Args& a, bool combine, hipStream_t st, hipEvent_t e0,
-                         hipEvent_t e1);
+hipError_t launch_qgumbel(const Args& a, bool combine, dim3 grid, hipStream_t st, hipEvent_t e0,
+                          hipEvent_t e1);
 __global__ void k_mask_logits(const void* logits, int dtype, int V, int64_t row_stride,
                               const uint32_t* mask, int64_t mask_stride, float* out);
 __global__ void k_draft_argmax(const void* logits, int dtype, int Vd, int64_t row_stride,
@@ -56,9 +55,10 @@ namespace {
 constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Byte offsets of the scratch buffers of R rows of up to max_vocab tokens, each 256-byte
-// aligned. The general-q verify buffers (dbits .. qpp) are sized only when `verify`.
+// aligned. The general-q verify buffers (dbits .. qarr) are sized only when `verify`.
 struct ScratchLayout {
-  size_t cstat, slot, part, rs, cand, nc, dbits, wrank, qpart, qhc, qhm, qst, qpp, lat, bytes;
+  size_t cstat, slot, part, rs, cand, nc, dbits, wrank, qpart, qhc, qhm, qst, qpp, qarr, lat,
+      bytes;
 };
 constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) {
   const size_t wmax = (max_vocab + CHUNK - 1) / CHUNK;
@@ -80,6 +80,7 @@ constexpr ScratchLayout scratch_layout(size_t R, size_t max_vocab, bool verify) 
   L.qhm = off; off = align_up(off + RQ * wmax * QNB * sizeof(unsigned long long), 256);
   L.qst = off; off = align_up(off + RV * sizeof(QStat), 256);
   L.qpp = off; off = align_up(off + RQ * QSPLIT * sizeof(QPart), 256);
+  L.qarr = off; off = align_up(off + RQ * sizeof(uint32_t), 256);
   L.lat = off; off = align_up(off + R * wmax * NBW * sizeof(unsigned long long), 256);
   L.bytes = off;
   return L;
@@ -104,6 +105,7 @@ Scratch scratch_at(char* base, const ScratchLayout& L, size_t max_vocab, bool ve
     s.qhm = (unsigned long long*)(base + L.qhm);
     s.qst = (QStat*)(base + L.qst);
     s.qpp = (QPart*)(base + L.qpp);
+    s.qarr = (uint32_t*)(base + L.qarr);
   }
   s.wmax = (int32_t)((max_vocab + CHUNK - 1) / CHUNK);
   return s;
@@ -246,10 +248,10 @@ int run_group(strim_ctx* ctx, hipStream_t st, Args& a, int nb, bool probs,
         keep(launch_args((const void*)k_qfinal, grid_r, dim3(FIN_T), a, st, nullptr, e1));
       } else {
         const dim3 grid_q = a.qskip ? dim3((unsigned)a.W, (unsigned)a.B) : grid_rc;
-        keep(launch_args((const void*)k_qgumbel, grid_q, dim3(TPB), a, st, e0, nullptr));
-        // with nothing after it, k_qgpick also runs the verify combine
+        // the last workgroup of each sequence picks its rows; with nothing after it, it
+        // also runs the verify combine
         const bool comb = combined != nullptr && !need_final && !probs;
-        keep(launch_qgpick(a, comb, st, nullptr, e1));
+        keep(launch_qgumbel(a, comb, grid_q, st, e0, e1));
         if (comb) *combined = true;
       }
     });

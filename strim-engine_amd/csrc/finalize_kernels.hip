@@ -282,7 +282,7 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
     }
     if (unfiltered && a.qskip) {
       // Only (accepted, token) is asked for: the accept test runs here, on the same
-      // numbers as k_qgpick's (the row mass is the integer sum of the chunk masses above),
+      // numbers as the residual pick's (the row mass is the integer sum of the chunk masses above),
       // so the residual draw runs only for a sequence's first rejected row.
       const uint64_t sw = wave_sum_u64(wq);
       if (lane == 0) S.u[w] = sw;

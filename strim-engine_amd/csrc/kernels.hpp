@@ -139,6 +139,8 @@ struct Scratch {
   unsigned long long* qhm;        // [MAXP][wmax][QNB] QRES rows: residual masses per bin
   QStat* qst;                     // [rows] per draft row (b * k + j)
   QPart* qpp;                     // [MAXP][QSPLIT] k_qprep slices, merged by k_finalize
+  uint32_t* qarr;                 // [MAXP] per sequence: k_qgumbel workgroups arrived (zero
+                                  // between launches: the last arriver resets it)
   unsigned long long* lat;        // [rows][wmax][NBW] general rows: per window bin of the
                                   // chunk, its inclusive count prefix << LCSH | its mass
                                   // (2^37 per unit of exp(l - A / LBS), A the bin's index)
@@ -249,26 +251,35 @@ __device__ __forceinline__ void verify_combine_one(const Args& a, int b, F row) 
   bool alive = true;
   // SpecSampling.verify consumes only the rows its accept chain reaches, 0 .. n
   // (SpecSampling.swift:101-105): a row error counts for the sequence only when the chain
-  // reaches that row; later rows report theirs in the per-row outputs alone
-  for (int j = 0; j <= k; ++j) {
-    const RowOut rs = row(j);
-    if (rs.status != STRIM_OK) {
-      if (alive) {
-        status = rs.status;
-        alive = false;
+  // reaches that row; later rows report theirs in the per-row outputs alone. The rows are
+  // taken four at a time, their outcomes read together (places past k repeat row k).
+  for (int j0 = 0; j0 <= k; j0 += 4) {
+    RowOut o[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[u] = row(min(j0 + u, k));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u;
+      if (j > k) break;
+      const RowOut rs = o[u];
+      if (rs.status != STRIM_OK) {
+        if (alive) {
+          status = rs.status;
+          alive = false;
+        }
+        if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = 0;
+        if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = -1;
+        continue;
       }
-      if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = 0;
-      if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = -1;
-      continue;
-    }
-    const int acc = j < k ? rs.accept : 0;
-    if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = acc;
-    if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = rs.token;
-    if (alive) {
-      if (j < k && acc) ++n;
-      else {
-        alive = false;
-        token = rs.token;
+      const int acc = j < k ? rs.accept : 0;
+      if (a.out_row_accept && j < k) a.out_row_accept[(int64_t)b * k + j] = acc;
+      if (a.out_row_token) a.out_row_token[(int64_t)b * (k + 1) + j] = rs.token;
+      if (alive) {
+        if (j < k && acc) ++n;
+        else {
+          alive = false;
+          token = rs.token;
+        }
       }
     }
   }

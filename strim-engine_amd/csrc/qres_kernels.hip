@@ -17,8 +17,8 @@
 //
 // With Gumbel noise the draw is the argmax over the row of log(p - q) + g (log p where
 // q = 0, tokens with p <= q excluded), ties to the smaller id:
-//   k_qgumbel   per chunk: the chunk's best (score, id)
-//   k_qgpick    per sequence: each row's best over the chunks and the p(d) / q(d)
+//   k_qgumbel   per chunk: the chunk's best (score, id); the sequence's last workgroup
+//               to finish then takes each row's best over the chunks and the p(d) / q(d)
 //               accept, then the sequence's accept chain when nothing follows.
 #include "exact.hpp"
 
@@ -305,37 +305,90 @@ __device__ __forceinline__ void q_wave_best(double& sc, int& id) {
   id = bi;
 }
 
-// Grid (W, R), or with a.qskip (W, B): workgroup (c, b) takes chunk c of sequence b's
-// first rejected draft row (the only residual draw read), found from the rows' accept
-// outcomes in one wave load (k <= 64).
-__global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
-  __shared__ uint32_t s_cnt[CHUNK];
-  __shared__ uint64_t s_red[TPB / WAVE];
-  __shared__ double s_sc[TPB / WAVE];
-  __shared__ int s_id[TPB / WAVE];
+// The residual draws of sequence b and its accept chain, in the last k_qgumbel workgroup
+// of the sequence to finish: wave w takes draft rows j = w, w + NW, ... (those in phase
+// QRES) and reduces their chunks' results; with COMBINE (no later kernel decides rows of
+// the call) the sequence's accept chain follows, reading the picked rows from LDS.
+template <bool COMBINE, int NW>
+__device__ __forceinline__ void qg_pick(const Args& a, int b, RowOut* s_out, int* s_mine) {
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
-  int r, c, b, j;
-  if (a.qskip) {
-    b = blockIdx.y;
-    c = blockIdx.x;
-    const int k1 = a.k + 1;
-    bool rej = false;
-    int ph = -1;
-    if (lane < a.k) {
-      const RowState& rq = a.s.rs[(int64_t)b * k1 + lane];
-      rej = !(rq.status == STRIM_OK && rq.accept);
-      ph = rq.phase;
-    }
-    const uint64_t m_rej = __ballot(rej);
-    if (m_rej == 0ull) return;  // every draft accepted: no residual draw
-    j = (int)__ffsll((long long)m_rej) - 1;
-    if (__builtin_amdgcn_readlane(ph, j) != PH_QRES) return;
-    r = b * k1 + j;
-  } else {
-    map_block(a, r, c);
-    row_bj(a, r, b, j);
-    if (a.s.rs[r].phase != PH_QRES) return;
+  const int k1 = a.k + 1;
+  // every draft row's state in one load, one lane a row (k <= 64): with qskip only the
+  // first rejected row takes its draw (q_needed)
+  int st = STRIM_OK, ac = 1, ph = PH_DONE;
+  if (lane < a.k) {
+    const RowState& rq = a.s.rs[(int64_t)b * k1 + lane];
+    st = rq.status;
+    ac = rq.accept;
+    ph = rq.phase;
   }
+  const uint64_t m_rej = __ballot(!(st == STRIM_OK && ac));
+  const int first_rej = m_rej ? (int)__ffsll((long long)m_rej) - 1 : WAVE;
+  for (int j = w; j < a.k; j += NW) {
+    const int r = b * k1 + j;
+    RowState* rs = &a.s.rs[r];
+    const bool mine = __builtin_amdgcn_readlane(ph, j) == PH_QRES && (!a.qskip || j == first_rej);
+    if (lane == 0) s_mine[j] = mine ? 1 : 0;
+    if (!mine) continue;
+    const int qr = b * a.k + j;
+    uint64_t sp = 0ull;
+    double bsc = -INFINITY;
+    int bid = -1;
+    for (int c = lane; c < a.W; c += WAVE) {
+      if (!a.qskip) sp += a.s.qpart[(size_t)qr * a.s.wmax + c];
+      const size_t o = ((size_t)qr * a.s.wmax + c) * QNB;
+      q_take(bsc, bid, __longlong_as_double((long long)a.s.qhm[o]), (int)a.s.qhc[o]);
+    }
+    q_wave_best(bsc, bid);
+    int acc;
+    double sig;
+    if (a.qskip) {
+      // k_finalize took the accept test (a first rejection: not accepted) and kept the
+      // row's mass
+      acc = rs->accept;
+      sig = rs->sum_kept;
+    } else {
+      const RowParams p = load_params(a, b, j);
+      const uint64_t S = wave_sum_u64(sp);
+      const float m = rs->m;
+      const int draft = a.drafts[(int64_t)b * a.k + j];
+      const float l_draft = rs->l_draft;
+      const XQ q = q_of_row(a, qr);
+      sig = (double)S / XFIX;
+      const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
+      double ratio = w_d / sig;
+      const double qd = xq_prob(q, draft);
+      ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
+      const float ua = row_uniform(a, r, p, (int64_t)a.V);
+      acc = ((double)ua < ratio) ? 1 : 0;
+    }
+    if (lane == 0) {
+      const int token = bid >= 0 ? bid : rs->token;  // the row's first maximum when nothing scores
+      rs->status = STRIM_OK;
+      rs->token = token;
+      rs->accept = acc;
+      rs->sum_kept = sig;
+      rs->last_key = ~0ull;
+      rs->phase = PH_DONE;
+      s_out[j] = RowOut{STRIM_OK, acc, token};
+    }
+  }
+  if constexpr (COMBINE) {
+    __syncthreads();
+    if (t == 0)
+      verify_combine_one(a, b, [&](int j) {
+        if (j < a.k && s_mine[j]) return s_out[j];
+        const RowState& rs = a.s.rs[(int64_t)b * k1 + j];
+        return RowOut{rs.status, rs.accept, rs.token};
+      });
+  }
+}
+
+// One chunk of a residual draw: the chunk's best (score, id) of row r = (b, j).
+__device__ __forceinline__ void qg_chunk(const Args& a, int r, int b, int j, int c,
+                                         uint32_t* s_cnt, uint64_t* s_red, double* s_sc,
+                                         int* s_id) {
+  const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int qr = b * a.k + j;
   const RowParams p = load_params(a, b, j);
   const float m = a.s.rs[r].m;
@@ -419,72 +472,68 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   }
 }
 
-// One workgroup per sequence: wave w picks draft rows j = w, w + QGP_W, ... (those in
-// phase QRES); with COMBINE (no later kernel decides rows of the call) the sequence's
-// accept chain follows in the same workgroup, reading the picked rows from LDS.
-constexpr int QGP_W = 4;
+// Grid (W, R), or with a.qskip (W, B): workgroup (c, b) takes chunk c of sequence b's
+// first rejected draft row (the only residual draw read), found from the rows' accept
+// outcomes in one wave load (k <= 64). Every workgroup, with a chunk to score or not,
+// then counts itself in the sequence's arrival counter (after a device-scope fence that
+// publishes its result); the last of the sequence's workgroups to arrive resets the
+// counter and runs the sequence's pick (qg_pick), so no further launch waits for them.
 template <bool COMBINE>
-__global__ __launch_bounds__(QGP_W * WAVE) void k_qgpick(Args a) {
+__global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
+  __shared__ uint32_t s_cnt[CHUNK];
+  __shared__ uint64_t s_red[TPB / WAVE];
+  __shared__ double s_sc[TPB / WAVE];
+  __shared__ int s_id[TPB / WAVE];
   __shared__ RowOut s_out[MAXP];
   __shared__ int s_mine[MAXP];
-  const int b = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
-  for (int j = w; j < a.k; j += QGP_W) {
-    const int r = b * (a.k + 1) + j;
-    RowState* rs = &a.s.rs[r];
-    const bool mine = rs->phase == PH_QRES && q_needed(a, b, j);
-    if (lane == 0) s_mine[j] = mine ? 1 : 0;
-    if (!mine) continue;
-    const int qr = b * a.k + j;
-    const RowParams p = load_params(a, b, j);
-    uint64_t sp = 0ull;
-    double bsc = -INFINITY;
-    int bid = -1;
-    for (int c = lane; c < a.W; c += WAVE) {
-      sp += a.s.qpart[(size_t)qr * a.s.wmax + c];
-      const size_t o = ((size_t)qr * a.s.wmax + c) * QNB;
-      q_take(bsc, bid, __longlong_as_double((long long)a.s.qhm[o]), (int)a.s.qhc[o]);
+  __shared__ int s_last;
+  const int t = threadIdx.x, lane = t & (WAVE - 1);
+  int r = 0, c, b, j = 0;
+  bool work = true;  // (uniform over the workgroup)
+  if (a.qskip) {
+    b = blockIdx.y;
+    c = blockIdx.x;
+    const int k1 = a.k + 1;
+    bool rej = false;
+    int ph = -1;
+    if (lane < a.k) {
+      const RowState& rq = a.s.rs[(int64_t)b * k1 + lane];
+      rej = !(rq.status == STRIM_OK && rq.accept);
+      ph = rq.phase;
     }
-    const uint64_t S = wave_sum_u64(sp);
-    q_wave_best(bsc, bid);
-    const float m = rs->m;
-    const int draft = a.drafts[(int64_t)b * a.k + j];
-    const float l_draft = rs->l_draft;
-    const XQ q = q_of_row(a, qr);
-    const double sig = (double)S / XFIX;
-    const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
-    double ratio = w_d / sig;
-    const double qd = xq_prob(q, draft);
-    ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
-    const float ua = row_uniform(a, r, p, (int64_t)a.V);
-    const int acc = ((double)ua < ratio) ? 1 : 0;
-    if (lane == 0) {
-      const int token = bid >= 0 ? bid : rs->token;  // the row's first maximum when nothing scores
-      rs->status = STRIM_OK;
-      rs->token = token;
-      rs->accept = acc;
-      rs->sum_kept = sig;
-      rs->last_key = ~0ull;
-      rs->phase = PH_DONE;
-      s_out[j] = RowOut{STRIM_OK, acc, token};
+    const uint64_t m_rej = __ballot(rej);
+    if (m_rej == 0ull) {
+      work = false;  // every draft accepted: no residual draw
+    } else {
+      j = (int)__ffsll((long long)m_rej) - 1;
+      if (__builtin_amdgcn_readlane(ph, j) != PH_QRES) work = false;
+      r = b * k1 + j;
     }
+  } else {
+    map_block(a, r, c);
+    row_bj(a, r, b, j);
+    if (uniform_copy(a.s.rs[r].phase) != PH_QRES) work = false;
   }
-  if constexpr (COMBINE) {
-    __syncthreads();
-    if (t == 0)
-      verify_combine_one(a, b, [&](int j) {
-        if (j < a.k && s_mine[j]) return s_out[j];
-        const RowState& rs = a.s.rs[(int64_t)b * (a.k + 1) + j];
-        return RowOut{rs.status, rs.accept, rs.token};
-      });
+  if (work) qg_chunk(a, r, b, j, c, s_cnt, s_red, s_sc, s_id);
+  // arrival: every workgroup of the sequence (W of them, or W (k + 1) without qskip)
+  if (t == 0) {
+    __threadfence();  // (this workgroup's result is visible before its count)
+    const uint32_t expect = (uint32_t)(a.qskip ? a.W : a.W * (a.k + 1));
+    const uint32_t old = atomicAdd(&a.s.qarr[b], 1u);
+    const bool last = old + 1u == expect;
+    if (last) a.s.qarr[b] = 0u;  // every workgroup has counted: ready for the next launch
+    s_last = last ? 1 : 0;
   }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();  // (the other workgroups' results are read after their counts)
+  qg_pick<COMBINE, TPB / WAVE>(a, b, s_out, s_mine);
 }
 
-hipError_t launch_qgpick(const Args& a, bool combine, hipStream_t st, hipEvent_t e0,
-                         hipEvent_t e1) {
-  return combine ? launch_args((const void*)k_qgpick<true>, dim3((unsigned)a.B),
-                               dim3(QGP_W * WAVE), a, st, e0, e1)
-                 : launch_args((const void*)k_qgpick<false>, dim3((unsigned)a.B),
-                               dim3(QGP_W * WAVE), a, st, e0, e1);
+hipError_t launch_qgumbel(const Args& a, bool combine, dim3 grid, hipStream_t st, hipEvent_t e0,
+                          hipEvent_t e1) {
+  return combine ? launch_args((const void*)k_qgumbel<true>, grid, dim3(TPB), a, st, e0, e1)
+                 : launch_args((const void*)k_qgumbel<false>, grid, dim3(TPB), a, st, e0, e1);
 }
 
 }  // namespace strim
