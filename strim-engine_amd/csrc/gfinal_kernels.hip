@@ -454,70 +454,114 @@ __device__ __noinline__ int gumbel_kept(lds_t<GFinalShared>* Sl, const Cand* bas
   return S.misc[4];
 }
 
-// Streams row r's raw logits and allow-bits (a row without penalties) window by window,
-// GT * EPT tokens a window, with the loads of D windows issued before any of them is
-// consumed; fn(i0, x, bits) gets a thread's EPT values and their allow-bits (tokens past
-// the row end not allowed).
-template <bool BF16, int D, typename F>
-__device__ __forceinline__ void stream_nopen(const XArgs& a, int r, F&& fn) {
+// The LDS a collect pass writes (address-space-typed: see lds_t).
+struct ZoneLds {
+  lds_t<uint64_t>* key;
+  lds_t<uint64_t>* mass;
+  lds_t<uint32_t>* cnt;  // GT * EPT history counts of one window
+  lds_t<int>* n;
+};
+// The collect pass of a row without penalties: streams the row's raw logits and
+// allow-bits window by window, GT * EPT tokens a window, with the loads of D windows
+// issued (from clamped indices, no branch between them) before any is consumed; selects
+// the tokens with xa <= x < xb, reserves their places once per batch of D windows (one
+// LDS atomic a wave, not one a window) and writes each lane's selected tokens,
+// l = x / T (x for a greedy row). The window holding the row end goes through `tail`.
+template <bool BF16, int D, typename Tail>
+__device__ __forceinline__ void collect_nopen(const XArgs& a, int r, float xa, float xb,
+                                              bool greedy, float T, float m, const ZoneLds& z,
+                                              Tail&& tail) {
   constexpr int WINT = GT * EPT;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, lane = t & (WAVE - 1);
   const int64_t base = (int64_t)r * a.row_stride;
   const glb_t<const uint8_t>* lg = (const glb_t<const uint8_t>*)a.logits;
   const glb_t<const uint8_t>* mg =
       a.mask ? (const glb_t<const uint8_t>*)(a.mask + (int64_t)r * a.mask_stride) : nullptr;
   const int nwin = (a.V + WINT - 1) / WINT;
+  // raw value e of a thread's window (its words w0..w3, and w4..w7 for fp32)
+  auto raw = [&](const u32x4& v0, const u32x4& v1, int e) -> float {
+    if constexpr (BF16) {
+      const int q = e >> 1;
+      const uint32_t wv = q == 0 ? v0.x : (q == 1 ? v0.y : (q == 2 ? v0.z : v0.w));
+      return __uint_as_float((e & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
+    } else {
+      const int q = e & 3;
+      const u32x4 v = e < 4 ? v0 : v1;
+      return __uint_as_float(q == 0 ? v.x : (q == 1 ? v.y : (q == 2 ? v.z : v.w)));
+    }
+  };
   for (int w0 = 0; w0 < nwin; w0 += D) {
     u32x4 x0[D], x1[D];
     uint32_t mb[D];
-    // every load of the batch from a clamped index, no branch between them
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int i0 = (w0 + d) * WINT + t * EPT;
       const int ii = i0 + EPT <= a.V ? i0 : 0;
       if constexpr (BF16) {
         x0[d] = *(const glb_t<const u32x4>*)(lg + 2 * (base + ii));
+        x1[d] = x0[d];
       } else {
         x0[d] = *(const glb_t<const u32x4>*)(lg + 4 * (base + ii));
         x1[d] = *(const glb_t<const u32x4>*)(lg + 4 * (base + ii + 4));
       }
       mb[d] = mg ? (uint32_t)mg[ii >> 3] : 0xFFu;
     }
+    // the selection bits of every whole window of the batch
+    uint32_t sel[D];
+    uint32_t cnt = 0u;
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      if (w0 + d < nwin) {
-        const int i0 = (w0 + d) * WINT + t * EPT;
-        float x[EPT];
-        uint32_t bits = mb[d];
-        if (i0 + EPT <= a.V) {
-          if constexpr (BF16) {
-            const uint32_t wv[4] = {x0[d].x, x0[d].y, x0[d].z, x0[d].w};
+      sel[d] = 0u;
+      const int i0 = (w0 + d) * WINT + t * EPT;
+      if (w0 + d < nwin && (w0 + d + 1) * WINT <= a.V) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              x[2 * e] = __uint_as_float(wv[e] << 16);
-              x[2 * e + 1] = __uint_as_float(wv[e] & 0xFFFF0000u);
-            }
-          } else {
-            const uint32_t wv[8] = {x0[d].x, x0[d].y, x0[d].z, x0[d].w,
-                                    x1[d].x, x1[d].y, x1[d].z, x1[d].w};
-#pragma unroll
-            for (int e = 0; e < EPT; ++e) x[e] = __uint_as_float(wv[e]);
-          }
-        } else {
-          // the segment at the row end (or past it): element loads of the tokens inside
-          bits = (mg && i0 < a.V) ? (uint32_t)mg[i0 >> 3] : 0xFFu;
-#pragma unroll
-          for (int e = 0; e < EPT; ++e) {
-            const int id = i0 + e < a.V ? i0 + e : 0;
-            x[e] = BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[base + id])
-                        : ((const float*)a.logits)[base + id];
-          }
+        for (int e = 0; e < EPT; ++e) {
+          const float x = raw(x0[d], x1[d], e);
+          sel[d] |= (((mb[d] >> e) & 1u) && x >= xa && x < xb) ? 1u << e : 0u;
         }
-        if (i0 + EPT > a.V) bits &= i0 < a.V ? (1u << (a.V - i0)) - 1u : 0u;
-        fn(i0, x, bits & 0xFFu);
+        cnt += (uint32_t)__popc(sel[d]);
       }
+      (void)i0;
     }
+    // one reservation a wave for the batch; each lane stages its tokens there as
+    // (raw value bits, id) (a few instructions a token, in window order), then the
+    // wave's lanes share the staged tokens evenly for the keys and masses (a division
+    // and an exponential each), in place (the wave's LDS operations complete in order)
+    const uint32_t inc = wave_incl_scan_u32(cnt);
+    const int tot = __builtin_amdgcn_readlane((int)inc, WAVE - 1);
+    if (tot > 0) {
+      int b0 = 0;
+      if (lane == 0) b0 = atomicAdd((int*)z.n, tot);
+      b0 = __builtin_amdgcn_readfirstlane(b0);
+      int pos = b0 + (int)(inc - cnt);
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int i0 = (w0 + d) * WINT + t * EPT;
+        uint32_t sl = sel[d];
+        while (sl) {
+          const int e = __builtin_ctz(sl);
+          sl &= sl - 1u;
+          if (pos < ZCAP)
+            z.key[pos] = ((uint64_t)__float_as_uint(raw(x0[d], x1[d], e)) << 32) | (uint32_t)(i0 + e);
+          ++pos;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      const int end = min(b0 + tot, ZCAP);
+      for (int i = b0 + lane; i < end; i += WAVE) {
+        const uint64_t v = z.key[i];
+        const float xe = __uint_as_float((uint32_t)(v >> 32));
+        const float le = greedy ? xe : xe / T;
+        z.key[i] = ckey(le, (int)(uint32_t)v);
+        z.mass[i] = rmass(le, m);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    // a window holding the row end: element by element
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (w0 + d < nwin && (w0 + d + 1) * WINT > a.V) tail(w0 + d);
   }
 }
 
@@ -556,13 +600,6 @@ __device__ __forceinline__ float least_x_for(float T, float A) {
   return unord(lo);
 }
 
-// The LDS a collect pass writes (address-space-typed: see lds_t).
-struct ZoneLds {
-  lds_t<uint64_t>* key;
-  lds_t<uint64_t>* mass;
-  lds_t<uint32_t>* cnt;  // GT * EPT history counts of one window
-  lds_t<int>* n;
-};
 // Collect pass: every token of the row whose lattice bin A(l) is `at`, by one streaming
 // pass of the workgroup over the row's logits (the chain recomputed per window), into
 // key / mass. Returns their number, -1 past ZCAP. Out of line: the common path of
@@ -611,7 +648,19 @@ __device__ __noinline__ int collect_zone(const XArgs a_in, int r, int b, int j,
     }
   };
   if (!p.pen && a.vec_ok) {
-    auto take_x = [&](int i0, const float (&x)[EPT], uint32_t bits) {
+    // the window holding the row end, token by token
+    auto tail = [&](int wi) {
+      const int i0 = wi * GT * EPT + (int)threadIdx.x * EPT;
+      const int64_t base = (int64_t)r * a.row_stride;
+      uint32_t bits = (a.mask && i0 < a.V) ? (uint32_t)((const uint8_t*)(a.mask + (int64_t)r * a.mask_stride))[i0 >> 3] : 0xFFu;
+      bits &= i0 < a.V ? (i0 + EPT <= a.V ? 0xFFu : (1u << (a.V - i0)) - 1u) : 0u;
+      float x[EPT];
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int id = i0 + e < a.V ? i0 + e : 0;
+        x[e] = a.dtype == STRIM_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[base + id])
+                                           : ((const float*)a.logits)[base + id];
+      }
       uint32_t sel = 0u;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) sel |= (((bits >> e) & 1u) && x[e] >= xa && x[e] < xb) ? 1u << e : 0u;
@@ -620,8 +669,8 @@ __device__ __noinline__ int collect_zone(const XArgs a_in, int r, int b, int j,
         return p.greedy ? xe : xe / p.T;
       });
     };
-    if (a.dtype == STRIM_DTYPE_BF16) stream_nopen<true, 16>(a, r, take_x);
-    else stream_nopen<false, 8>(a, r, take_x);
+    if (a.dtype == STRIM_DTYPE_BF16) collect_nopen<true, 16>(a, r, xa, xb, p.greedy, p.T, m, z, tail);
+    else collect_nopen<false, 8>(a, r, xa, xb, p.greedy, p.T, m, z, tail);
   } else {
     x_pass<GT, false>(a, r, b, j, p, (uint32_t*)z.cnt,
                       [&](int i0, const float (&l)[EPT], const float (&)[EPT]) {
