@@ -346,8 +346,36 @@ __device__ __forceinline__ GHit pick_sorted(GFinalShared& S, GBig& G, int np, in
     pmask |= 255ull << shift;
     bc = S.u2[0];
     bm = S.u2[1];
-    hb = shift - 1;
-    __syncthreads();  // (S.ii and S.u2 are rewritten by the next pass)
+    // the bits that still differ among the keys under the prefix (set in some, clear in
+    // others): the next pass starts at the highest of them, and the bits above it that
+    // every such key shares (a float's low bits that bf16 values leave zero, say) join
+    // the prefix without a pass; none left ends the search
+    uint64_t vo = 0ull, va = 0ull;  // OR of the keys, OR of their complements
+#pragma unroll
+    for (int q = 0; q < ZQ; ++q)
+      if ((ck[q] & pmask) == prefix) {
+        vo |= ck[q];
+        va |= ~ck[q];
+      }
+    vo = wave_or_u64(vo);
+    va = wave_or_u64(va);
+    if (lane == 0) {
+      S.u[w] = vo;
+      S.u2[GW + w] = va;  // (S.u2[0..1] are read above, before the barrier)
+    }
+    __syncthreads();  // (also: S.ii and S.u2 are rewritten by the next pass)
+    vo = 0ull;
+    va = 0ull;
+#pragma unroll
+    for (int q = 0; q < GW; ++q) {
+      vo |= S.u[q];
+      va |= S.u2[GW + q];
+    }
+    const uint64_t vary = vo & va & ~pmask;
+    hb = vary ? 63 - __clzll((long long)vary) : -1;
+    const uint64_t above = hb >= 0 ? ~((2ull << hb) - 1ull) : ~0ull;
+    prefix |= ~va & above & ~pmask;  // (~va: the bits every key under the prefix sets)
+    pmask = above;
   }
   // the crossing key: the candidate whose compact key is the prefix
 #pragma unroll
@@ -1047,8 +1075,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
           in[q] = pr && k <= bnd && (int)(uint32_t)k != excl;
           if (pr) diff |= ck[q] ^ ref;
         }
-        diff = ((uint64_t)(uint32_t)wave_or_i((int)(uint32_t)(diff >> 32)) << 32) |
-               (uint32_t)wave_or_i((int)(uint32_t)diff);
+        diff = wave_or_u64(diff);
         int hb = diff ? 63 - __clzll((long long)diff) : -1;
         uint64_t pmask = hb < 0 ? ~0ull : ~((2ull << hb) - 1ull);
         uint64_t prefix = ref & pmask;
@@ -1104,7 +1131,21 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
           bm = rl_u64(hm, hl);
           prefix |= (uint64_t)d << shift;
           pmask |= 255ull << shift;
-          hb = shift - 1;
+          // the bits still differing among the keys under the prefix (as pick_sorted)
+          uint64_t vo = 0ull, va = 0ull;
+#pragma unroll
+          for (int q = 0; q < SQ; ++q)
+            if ((ck[q] & pmask) == prefix) {
+              vo |= ck[q];
+              va |= ~ck[q];
+            }
+          vo = wave_or_u64(vo);
+          va = wave_or_u64(va);
+          const uint64_t vary = vo & va & ~pmask;
+          hb = vary ? 63 - __clzll((long long)vary) : -1;
+          const uint64_t above = hb >= 0 ? ~((2ull << hb) - 1ull) : ~0ull;
+          prefix |= ~va & above & ~pmask;
+          pmask = above;
           __builtin_amdgcn_wave_barrier();  // (this pass's reads before the next clear)
         }
         // the crossing key: its holder's key and mass
