@@ -178,6 +178,12 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   if (a.noise && !p.greedy) {
     if (a.noise_mode == STRIM_NOISE_ICDF) u_draw = pf.n0;
     u_acc = pf.n1;
+  } else if (!a.noise) {
+    // the row's own uniforms, computed while the prefetched loads are in flight (they
+    // depend on the parameters alone)
+    const uint64_t pk = mix64(p.seed, p.position);
+    u_draw = philox_uniform(pk, 0);
+    u_acc = philox_uniform(pk, a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
   }
 
   // ---- phase 1: chunk statistics (W <= 256: one chunk per thread) -----------------
@@ -320,10 +326,6 @@ __device__ __forceinline__ ExactReq finalize_row(const Args& a, int r, int b, in
   const bool cand_sorted = no_lse ? topp : (topk || topp);
   const uint64_t pkey = mix64(p.seed, p.position);
   const int excl_id = vdr ? draft : -1;
-  if (!a.noise) {
-    u_draw = philox_uniform(pkey, 0);
-    u_acc = philox_uniform(pkey, a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
-  }
 
   // ---- unfiltered Gumbel rows: the chunks' two best tokens ------------------------
   // (and a chunk's near ties of its second best, as its candidates; flag 8: a chunk had

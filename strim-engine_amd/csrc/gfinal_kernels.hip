@@ -770,6 +770,14 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     }
   }
   const RowParams p = load_params(a, b, j);
+  // the row's own uniforms (rows without given noise), computed while the loads above
+  // are in flight: they depend on the parameters alone
+  float pu_draw = 0.0f, pu_acc = 0.0f;
+  if (!a.noise) {
+    const uint64_t pkey = mix64(p.seed, p.position);
+    pu_draw = philox_uniform(pkey, 0);
+    pu_acc = philox_uniform(pkey, a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
+  }
   if (!gfinal_row(a.p[b], V, a.noise_mode, a.dlog != nullptr && vdr)) {
     __builtin_amdgcn_s_waitcnt(0);  // (no LDS write may land after the workgroup ends)
     return;
@@ -835,14 +843,13 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     finish(status, -1, 0, 0.0, 0ull);
     return;
   }
-  const uint64_t pkey = mix64(p.seed, p.position);
   float u_draw = 0.0f, u_acc = 0.0f;
   if (a.noise) {
     if (a.noise_mode == STRIM_NOISE_ICDF) u_draw = n0;
     u_acc = n1;
   } else {
-    u_draw = philox_uniform(pkey, 0);
-    u_acc = philox_uniform(pkey, a.noise_mode == STRIM_NOISE_GUMBEL ? (uint64_t)V : 1u);
+    u_draw = pu_draw;
+    u_acc = pu_acc;
   }
   // the streaming passes' view of the launch (collect passes and the exact resolution)
   XArgs xa;
