@@ -310,74 +310,95 @@ __device__ __forceinline__ void q_wave_best(double& sc, int& id) {
 // QRES) and reduces their chunks' results; with COMBINE (no later kernel decides rows of
 // the call) the sequence's accept chain follows, reading the picked rows from LDS.
 template <bool COMBINE, int NW>
-__device__ __forceinline__ void qg_pick(const Args& a, int b, RowOut* s_out, int* s_mine) {
+__device__ __forceinline__ void qg_pick(const Args& a, int b, RowOut* s_out, int* s_mine,
+                                        const double* s_sig, bool pre, int jq) {
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int k1 = a.k + 1;
-  // every draft row's state in one load, one lane a row (k <= 64): with qskip only the
-  // first rejected row takes its draw (q_needed)
-  int st = STRIM_OK, ac = 1, ph = PH_DONE;
-  if (lane < a.k) {
-    const RowState& rq = a.s.rs[(int64_t)b * k1 + lane];
-    st = rq.status;
-    ac = rq.accept;
-    ph = rq.phase;
-  }
-  const uint64_t m_rej = __ballot(!(st == STRIM_OK && ac));
-  const int first_rej = m_rej ? (int)__ffsll((long long)m_rej) - 1 : WAVE;
-  for (int j = w; j < a.k; j += NW) {
-    const int r = b * k1 + j;
-    RowState* rs = &a.s.rs[r];
-    const bool mine = __builtin_amdgcn_readlane(ph, j) == PH_QRES && (!a.qskip || j == first_rej);
-    if (lane == 0) s_mine[j] = mine ? 1 : 0;
-    if (!mine) continue;
+  // the chunks' best of draft row j: its token (the row's first maximum when nothing
+  // scores), and the row's plain mass sum over the chunks when sp is asked for
+  auto best = [&](int j, uint64_t* sp_out) -> int {
     const int qr = b * a.k + j;
     uint64_t sp = 0ull;
     double bsc = -INFINITY;
     int bid = -1;
     for (int c = lane; c < a.W; c += WAVE) {
-      if (!a.qskip) sp += a.s.qpart[(size_t)qr * a.s.wmax + c];
+      if (sp_out) sp += a.s.qpart[(size_t)qr * a.s.wmax + c];
       const size_t o = ((size_t)qr * a.s.wmax + c) * QNB;
       q_take(bsc, bid, __longlong_as_double((long long)a.s.qhm[o]), (int)a.s.qhc[o]);
     }
     q_wave_best(bsc, bid);
-    int acc;
-    double sig;
-    if (a.qskip) {
-      // k_finalize took the accept test (a first rejection: not accepted) and kept the
-      // row's mass
-      acc = rs->accept;
-      sig = rs->sum_kept;
-    } else {
-      const RowParams p = load_params(a, b, j);
-      const uint64_t S = wave_sum_u64(sp);
-      const float m = rs->m;
-      const int draft = a.drafts[(int64_t)b * a.k + j];
-      const float l_draft = rs->l_draft;
-      const XQ q = q_of_row(a, qr);
-      sig = (double)S / XFIX;
-      const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
-      double ratio = w_d / sig;
-      const double qd = xq_prob(q, draft);
-      ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
-      const float ua = row_uniform(a, r, p, (int64_t)a.V);
-      acc = ((double)ua < ratio) ? 1 : 0;
+    if (sp_out) *sp_out = wave_sum_u64(sp);
+    return bid;
+  };
+  auto done = [&](int j, int token, int acc, double sig) {
+    RowState* rs = &a.s.rs[b * k1 + j];
+    rs->status = STRIM_OK;
+    rs->token = token;
+    rs->accept = acc;
+    rs->sum_kept = sig;
+    rs->last_key = ~0ull;
+    rs->phase = PH_DONE;
+    s_out[j] = RowOut{STRIM_OK, acc, token};
+  };
+  if (pre) {
+    // qskip: the routing loaded every row's outcome into s_out and each draft row's mass
+    // into s_sig; only row jq (the first rejection) draws, and k_finalize took its accept
+    // test (not accepted) and kept its mass
+    if (jq >= 0 && w == 0) {
+      const int bid = best(jq, nullptr);
+      if (lane == 0) done(jq, bid >= 0 ? bid : s_out[jq].token, 0, s_sig[jq]);
     }
-    if (lane == 0) {
-      const int token = bid >= 0 ? bid : rs->token;  // the row's first maximum when nothing scores
-      rs->status = STRIM_OK;
-      rs->token = token;
-      rs->accept = acc;
-      rs->sum_kept = sig;
-      rs->last_key = ~0ull;
-      rs->phase = PH_DONE;
-      s_out[j] = RowOut{STRIM_OK, acc, token};
+  } else {
+    // every draft row's state in one load, one lane a row (k <= 64): with qskip only the
+    // first rejected row takes its draw (q_needed)
+    int st = STRIM_OK, ac = 1, ph = PH_DONE;
+    if (lane < a.k) {
+      const RowState& rq = a.s.rs[(int64_t)b * k1 + lane];
+      st = rq.status;
+      ac = rq.accept;
+      ph = rq.phase;
+    }
+    const uint64_t m_rej = __ballot(!(st == STRIM_OK && ac));
+    const int first_rej = m_rej ? (int)__ffsll((long long)m_rej) - 1 : WAVE;
+    for (int j = w; j < a.k; j += NW) {
+      const int r = b * k1 + j;
+      RowState* rs = &a.s.rs[r];
+      const bool mine =
+          __builtin_amdgcn_readlane(ph, j) == PH_QRES && (!a.qskip || j == first_rej);
+      if (lane == 0) s_mine[j] = mine ? 1 : 0;
+      if (!mine) continue;
+      const int qr = b * a.k + j;
+      int acc;
+      double sig;
+      uint64_t S = 0ull;
+      const int bid = best(j, a.qskip ? nullptr : &S);
+      if (a.qskip) {
+        // k_finalize took the accept test (a first rejection: not accepted) and kept the
+        // row's mass
+        acc = rs->accept;
+        sig = rs->sum_kept;
+      } else {
+        const RowParams p = load_params(a, b, j);
+        const float m = rs->m;
+        const int draft = a.drafts[(int64_t)b * a.k + j];
+        const float l_draft = rs->l_draft;
+        const XQ q = q_of_row(a, qr);
+        sig = (double)S / XFIX;
+        const double w_d = l_draft > -INFINITY ? exp((double)l_draft - (double)m) : 0.0;
+        double ratio = w_d / sig;
+        const double qd = xq_prob(q, draft);
+        ratio = qd > 0.0 ? ratio / qd : (ratio > 0.0 ? INFINITY : 0.0);
+        const float ua = row_uniform(a, r, p, (int64_t)a.V);
+        acc = ((double)ua < ratio) ? 1 : 0;
+      }
+      if (lane == 0) done(j, bid >= 0 ? bid : rs->token, acc, sig);
     }
   }
   if constexpr (COMBINE) {
     __syncthreads();
     if (t == 0)
       verify_combine_one(a, b, [&](int j) {
-        if (j < a.k && s_mine[j]) return s_out[j];
+        if (pre || (j < a.k && s_mine[j])) return s_out[j];
         const RowState& rs = a.s.rs[(int64_t)b * k1 + j];
         return RowOut{rs.status, rs.accept, rs.token};
       });
@@ -486,20 +507,29 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   __shared__ int s_id[TPB / WAVE];
   __shared__ RowOut s_out[MAXP];
   __shared__ int s_mine[MAXP];
+  __shared__ double s_sig[MAXP];
   __shared__ int s_last;
   const int t = threadIdx.x, lane = t & (WAVE - 1);
   int r = 0, c, b, j = 0;
   bool work = true;  // (uniform over the workgroup)
+  const bool pre = a.qskip && a.k < WAVE;  // the rows' outcomes kept from the routing load
   if (a.qskip) {
     b = blockIdx.y;
     c = blockIdx.x;
     const int k1 = a.k + 1;
     bool rej = false;
     int ph = -1;
-    if (lane < a.k) {
+    if (lane <= a.k) {
       const RowState& rq = a.s.rs[(int64_t)b * k1 + lane];
-      rej = !(rq.status == STRIM_OK && rq.accept);
-      ph = rq.phase;
+      const int st = rq.status, ac = rq.accept, tk = rq.token;
+      if (lane < a.k) {
+        rej = !(st == STRIM_OK && ac);
+        ph = rq.phase;
+      }
+      if (pre && t < WAVE) {  // (wave 0; for the last arriver's pick)
+        s_out[lane] = RowOut{st, ac, tk};
+        if (lane < a.k) s_sig[lane] = rq.sum_kept;
+      }
     }
     const uint64_t m_rej = __ballot(rej);
     if (m_rej == 0ull) {
@@ -527,7 +557,7 @@ __global__ __launch_bounds__(TPB) void k_qgumbel(Args a) {
   __syncthreads();
   if (!s_last) return;
   __threadfence();  // (the other workgroups' results are read after their counts)
-  qg_pick<COMBINE, TPB / WAVE>(a, b, s_out, s_mine);
+  qg_pick<COMBINE, TPB / WAVE>(a, b, s_out, s_mine, s_sig, pre, pre && work ? j : -1);
 }
 
 hipError_t launch_qgumbel(const Args& a, bool combine, dim3 grid, hipStream_t st, hipEvent_t e0,
