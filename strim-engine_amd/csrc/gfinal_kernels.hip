@@ -1012,6 +1012,9 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     // cooperative loop below (every wave; it starts over). Both follow the same decision
     // rules.
     constexpr int SQ = 3, SOLO = SQ * WAVE;  // zone keys a lane holds, a zone's keys
+    // (a zone of at most 64 keys starts below 2 SOLO; its rank loop reads up to 7 places
+    // past its end)
+    static_assert(2 * SOLO + WAVE + 8 <= ZCAP && WAVE + 8 <= GT, "rank loop reads in bounds");
     bool pfok = true;  // the prefetched candidates are in LDS
     auto solo = [&]() -> int {  // 0 decided, 1 cooperative, 2 exact resolution
       if (!icdf) return 1;
@@ -1198,13 +1201,16 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         __builtin_amdgcn_wave_barrier();
         uint32_t rk = 0u;
         uint64_t mb = 0ull;
+        // (places past n read stale entries inside the zone buffer and S.pmb, dropped by
+        // the scalar test below: the reads take constant offsets from one base)
+        const lds_t<uint64_t>* zk = (const lds_t<uint64_t>*)G.z.zkey + z0;
+        const lds_t<unsigned long long>* zm = (const lds_t<unsigned long long>*)S.pmb;
         for (int j0 = 0; j0 < n; j0 += 8) {
           uint64_t kj[8], mj[8];
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            const int jj = min(j0 + u, n - 1);
-            kj[u] = G.z.zkey[z0 + jj];
-            mj[u] = S.pmb[jj];
+            kj[u] = zk[j0 + u];
+            mj[u] = zm[j0 + u];
           }
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
