@@ -1047,21 +1047,28 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         }
         if (__ballot(!ok) != 0ull) return 1;
         zoo[1] += n[0];
-        // lane c copies chunk c's part, four candidates a step (their reads issued
-        // together; places past the part are clamped inside the chunk's prefetch)
+        // each zone place's source in the prefetched candidates, c PF + its place in
+        // chunk c's part: lane c writes its part's (a few stores each), then every lane
+        // builds the keys and masses of places lane, lane + 64, ... (S.prk is idle here)
+        lds_t<uint32_t>* src = (lds_t<uint32_t>*)S.prk;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
-          for (int i0 = 0; i0 < cnt[hh]; i0 += 4) {
-            Cand x[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) x[u] = P.pfb[lane * PF + min(off[hh] + i0 + u, PF - 1)];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-              if (i0 + u < cnt[hh]) {
-                G.z.zkey[zoo[hh] + i0 + u] = ckey(x[u].l, x[u].id);
-                G.z.zmass[zoo[hh] + i0 + u] = rmass(x[u].l, m);
-              }
+          for (int i = 0; i < cnt[hh]; ++i) src[zoo[hh] + i] = (uint32_t)(lane * PF + off[hh] + i);
+        __builtin_amdgcn_wave_barrier();
+        const int ntot = n[0] + n[1];
+        for (int i0 = 0; i0 < ntot; i0 += 2 * WAVE) {
+          const int ia = i0 + lane, ib = i0 + WAVE + lane;
+          const Cand xa = P.pfb[src[ia < ntot ? ia : 0]];
+          const Cand xb = P.pfb[src[ib < ntot ? ib : 0]];
+          if (ia < ntot) {
+            G.z.zkey[ia] = ckey(xa.l, xa.id);
+            G.z.zmass[ia] = rmass(xa.l, m);
           }
+          if (ib < ntot) {
+            G.z.zkey[ib] = ckey(xb.l, xb.id);
+            G.z.zmass[ib] = rmass(xb.l, m);
+          }
+        }
         // (one wave's LDS operations complete in order: its later reads see these)
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_wave_barrier();
