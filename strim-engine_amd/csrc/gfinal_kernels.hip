@@ -956,9 +956,12 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         atomicAdd(&S.rm[bq], (unsigned long long)ms_);
       }
     }
-    if (own && cs.n > 0 && cs.ncand2 > 0u && cs.ncand2 != LNONE &&
-        cs.n > (int)(uint32_t)(G.E[t * NBW + cs.ncand2 - 1] >> LCSH))
-      S.misc[3] = 1;
+    if (w == 0) {
+      // tokens below a chunk's window (one store, not one a lane)
+      const bool below = own && cs.n > 0 && cs.ncand2 > 0u && cs.ncand2 != LNONE &&
+                         cs.n > (int)(uint32_t)(G.E[t * NBW + cs.ncand2 - 1] >> LCSH);
+      if (__ballot(below) != 0ull && lane == 0) S.misc[3] = 1;
+    }
     __syncthreads();
     // The leader wave (wave 0) keeps the row's cumulative histogram in its registers,
     // scaled from each bin's lattice unit to RFIX per unit of exp(l - m): scale(b) =
