@@ -912,49 +912,49 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     // the LDS loads have landed (every wave waits for its own, then the barrier)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // every row bin: the counts and masses of its chunks' bins (waves 0-2 over the even
-    // chunks, 3-5 over the odd ones, one row bin per lane: the chunk is uniform over the
-    // wave; a lattice bin's masses share their unit, so they add as integers); each
-    // chunk's inclusive count prefixes for the gathers; tokens below a chunk's window
-    if (w < 6) {
-      const int g = w / 3, bq = (w - 3 * g) * WAVE + lane;
+    // every row bin: the counts and masses of its chunks' bins. Wave w takes chunks w,
+    // w + 8, ... (at most LWMAX / 8), lane l row bins 3 l .. 3 l + 2 of each (a chunk's
+    // bins read with the one before them: four words for three bins, all requested
+    // before any is used); a lattice bin's masses share their unit, so they add as
+    // integers, and each row bin gets one LDS atomic per wave. Each chunk's inclusive
+    // count prefixes are kept for the gathers.
+    {
+      static_assert(LPL == 3 && LWMAX % GW == 0, "three row bins a lane, whole chunk rounds");
       const int dreg = lane < W ? S.dch[lane] : NOBIN;
       const int nbreg = lane < W ? S.nbch[lane] : 0;
-      uint32_t cs_ = 0u;
-      uint64_t ms_ = 0ull;
-      // four chunks a step, their words read unconditionally (clamped places, results
-      // dropped) so the reads are issued together rather than one LDS round trip each
-      constexpr int CU = 4;
-      for (int c0 = g; c0 < W; c0 += 2 * CU) {
-        uint64_t wv[CU], pv[CU];
-        int lbs[CU];
-        bool ok[CU];
+      uint32_t cq[LPL] = {0u, 0u, 0u};
+      uint64_t mq[LPL] = {0ull, 0ull, 0ull};
 #pragma unroll
-        for (int u = 0; u < CU; ++u) {
-          const int c = c0 + 2 * u, cc = c < W ? c : g;
-          const int d = __builtin_amdgcn_readlane(dreg, cc);
-          const int nb = __builtin_amdgcn_readlane(nbreg, cc);
-          const int lb = bq - d;
-          ok[u] = c < W && lb >= 0 && lb < nb;
-          lbs[u] = lb;
-          const int e = ok[u] ? c * NBW + lb : 0;
-          wv[u] = G.E[e];
-          pv[u] = G.E[e > 0 ? e - 1 : 0];
+      for (int k = 0; k < LWMAX / GW; ++k) {
+        const int c = w + GW * k;
+        if (c >= W) break;
+        const int d = __builtin_amdgcn_readlane(dreg, c);
+        const int nb = __builtin_amdgcn_readlane(nbreg, c);
+        const int lb0 = LPL * lane - d;  // the chunk's bin of row bin 3 l
+        uint64_t wv[LPL + 1];  // words of chunk bins lb0 - 1 .. lb0 + 2
+        bool in[LPL + 1];
+#pragma unroll
+        for (int q = 0; q <= LPL; ++q) {
+          const int lb = lb0 + q - 1;
+          in[q] = lb >= 0 && lb < nb;
+          wv[q] = G.E[in[q] ? c * NBW + lb : 0];
         }
 #pragma unroll
-        for (int u = 0; u < CU; ++u)
-          if (ok[u]) {
-            const uint32_t prev = lbs[u] > 0 ? (uint32_t)(pv[u] >> LCSH) : 0u;
-            const uint32_t incl = (uint32_t)(wv[u] >> LCSH);
-            S.pc[c0 + 2 * u][lbs[u]] = (uint16_t)incl;
-            cs_ += incl - prev;
-            ms_ += wv[u] & LMMASK;
+        for (int q = 0; q < LPL; ++q)
+          if (in[q + 1]) {
+            const uint32_t incl = (uint32_t)(wv[q + 1] >> LCSH);
+            const uint32_t prev = in[q] ? (uint32_t)(wv[q] >> LCSH) : 0u;
+            S.pc[c][lb0 + q] = (uint16_t)incl;
+            cq[q] += incl - prev;
+            mq[q] += wv[q + 1] & LMMASK;
           }
       }
-      if (cs_) {
-        atomicAdd(&S.rc[bq], cs_);
-        atomicAdd(&S.rm[bq], (unsigned long long)ms_);
-      }
+#pragma unroll
+      for (int q = 0; q < LPL; ++q)
+        if (cq[q]) {
+          atomicAdd(&S.rc[LPL * lane + q], cq[q]);
+          atomicAdd(&S.rm[LPL * lane + q], (unsigned long long)mq[q]);
+        }
     }
     if (w == 0) {
       // tokens below a chunk's window (one store, not one a lane)
