@@ -1007,13 +1007,13 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
 
     // ---- the leader alone ------------------------------------------------------------
     // A row whose zones are small (the common case) is decided by wave 0 alone, with no
-    // workgroup barrier: it lays out each zone from the prefetched candidates (lane c
-    // copies chunk c's part) and picks within the wave: up to 64 keys by a serial scan
-    // of ranks (one key a lane), up to SOLO by a radix select in the wave (a wave's
-    // serial scan costs four cycles an instruction). A zone that needs a chunk's slot
-    // region or a collect pass, or holds more than SOLO keys, and Gumbel draws, go to the
-    // cooperative loop below (every wave; it starts over). Both follow the same decision
-    // rules.
+    // workgroup barrier: it lays out each zone from the prefetched candidates (each
+    // place's source recorded by its chunk's lane, then the keys and masses built by all
+    // lanes) and picks within the wave: up to 64 keys by ranks (one key a lane, the zone
+    // read as LDS broadcasts), up to SOLO by a radix select in the wave. A zone that needs
+    // a chunk's slot region or a collect pass, or holds more than SOLO keys, and Gumbel
+    // draws, go to the cooperative loop below (every wave; it starts over). Both follow
+    // the same decision rules.
     constexpr int SQ = 3, SOLO = SQ * WAVE;  // zone keys a lane holds, a zone's keys
     // (a zone of at most 64 keys starts below 2 SOLO; its rank loop reads up to 7 places
     // past its end)
