@@ -88,8 +88,8 @@ extern "C" {
                                         instead of log-prob + g (SpecSampling)          */
 #define STRIM_FLAG_SAMPLER_COMPAT 7u /* all three: the non-MTP Sampler.sample          */
 
-/* One per row. Defaults (strim_default_params) reproduce the reference exactly:
- * extensions are no-ops. Chain order: penalties -> mask -> /T -> min-p -> top-k -> top-p
+/* One per row. With the extensions at their defaults (strim_default_params) a row
+ * reproduces the reference exactly: they are no-ops. Chain order: penalties -> mask -> /T -> min-p -> top-k -> top-p
  * -> draw. 48 bytes, naturally aligned. */
 typedef struct strim_sampling_params {
   float temperature;        /* <= 0: greedy argmax (GenParams.isGreedy, EngineAPI.swift:66) */
@@ -106,7 +106,9 @@ typedef struct strim_sampling_params {
 
 typedef struct strim_ctx strim_ctx;
 
-/* Fill *p with the reference defaults: T=1, top_k=0, top_p=1, extensions off. Host. */
+/* Fill *p with T=1, top_k=0, top_p=1 and every extension off (plain sampling of the
+ * reference's SamplingConfig with its topK / topP defaults, SpecSampling.swift:12; the
+ * engine's GenParams defaults to T=0, greedy, EngineAPI.swift:59). Host. */
 void strim_default_params(strim_sampling_params* p);
 
 /* Validate n HOST param structs the way the engine consumes GenParams: temperature

@@ -64,8 +64,8 @@ assert ROW_RESULT_DTYPE.itemsize == 40
 
 
 def make_params(n: int, **kw) -> np.ndarray:
-    """Param array of n rows with the reference defaults, overridden by kw (scalars or
-    per-row sequences)."""
+    """Param array of n rows of plain sampling (T=1, no top-k/top-p, extensions off),
+    overridden by kw (scalars or per-row sequences)."""
     p = np.zeros(n, dtype=PARAMS_DTYPE)
     p["temperature"] = 1.0
     p["top_k"] = 0

@@ -412,7 +412,7 @@ int strim_check_params(const strim_sampling_params* hp, int32_t n) {
 
 int strim_ctx_create(strim_ctx** out, int32_t device, int32_t max_rows, int32_t max_vocab) {
   // V <= 2^20 keeps a row within 256 chunks, the bound of the finalize's per-chunk
-  // LDS tables, and keeps a row's fixed-point mass sums (2^35 per unit of exp(l - m) in
+  // LDS tables, and keeps a row's fixed-point mass sums (2^40 per unit of exp(l - m) in
   // k_gfinal, 2^43 in the exact resolution and the residual draw: at most V * 2^43)
   // inside 64 bits
   if (!out || max_rows <= 0 || max_vocab <= 0 || max_rows > (1 << 20) ||

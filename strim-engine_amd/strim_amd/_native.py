@@ -90,8 +90,8 @@ assert PARAMS_DTYPE.itemsize == 48
 
 
 def params_array(n: int, **kw) -> np.ndarray:
-    """Host param rows with the reference defaults (T=1, no top-k/top-p, extensions
-    off), overridden by kw (scalar or per-row sequence)."""
+    """Host param rows of plain sampling (T=1, no top-k/top-p, extensions off, as
+    strim_default_params), overridden by kw (scalar or per-row sequence)."""
     p = np.zeros(n, dtype=PARAMS_DTYPE)
     p["temperature"] = 1.0
     p["top_p"] = 1.0

@@ -194,6 +194,62 @@ def test_n1_north_star_chain(ctx, mode, injected):
         assert w["allowed"][r, ids[r]]
 
 
+@pytest.mark.parametrize("seed", [7, 8, 9, 10, 11, 12])
+def test_n1_other_sets(ctx, seed):
+    # more n1 sets: each masked-nucleus row's top-p cut falls in a lattice bin of 50-180
+    # keys on two or three values of l, and its draw often in another crowded bin
+    w = W.n1(seed=seed)
+    say(f"n1 seed={seed}")
+    ids, st, ref = check_sample(ctx, w["x"], w["params"], "bf16", w["mask"], w["history"],
+                                w["history_len"], O.NOISE_ICDF, w["noise"], label="n1-sets")
+    assert (st == 0).all()
+
+
+def _grid_logits(rng, n, V):
+    # rows of N(0, s^2) rounded to a grid of 1/16 .. 1/128: every lattice bin near a
+    # decision holds tens to hundreds of keys on one to eight values of l
+    s = rng.choice([1.0, 1.5, 2.0], size=n)
+    q = rng.choice([16.0, 32.0, 64.0, 128.0], size=n)
+    x = rng.normal(0, 1, size=(n, V)) * s[:, None]
+    return (np.round(x * q[:, None]) / q[:, None]).astype(np.float32)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_crowded_bins_few_values(ctx, seed):
+    # top-k (a count decision), kept ties, min-p, top-p and the draw over zones whose keys
+    # share a few values of l
+    rng = np.random.default_rng(500 + seed)
+    B, V = 16, 60000
+    x = _grid_logits(rng, B, V)
+    p = O.make_params(B, temperature=rng.choice([0.7, 1.0, 1.3], size=B),
+                      top_k=rng.choice([0, 0, 300, 1000, 2500], size=B),
+                      top_p=rng.choice([1.0, 0.5, 0.8, 0.9, 0.95, 0.99], size=B),
+                      min_p=rng.choice([0.0, 0.0, 0.01, 0.05], size=B),
+                      flags=rng.choice([0, 0, 1], size=B),
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                      position=np.arange(B, dtype=np.uint64))
+    noise = rng.random((B, 2), dtype=np.float32)
+    say(f"crowded bins seed={seed}")
+    check_sample(ctx, x, p, "bf16", None, None, None, O.NOISE_ICDF, noise, label="crowded")
+    check_sample(ctx, x, p, "bf16", None, None, None, O.NOISE_ICDF, None, label="crowded-own")
+
+
+def test_crowded_bins_verify(ctx):
+    # verify rows over the same kind of zones: the draft is excluded from the residual draw
+    rng = np.random.default_rng(510)
+    B, k, V = 6, 3, 60000
+    x = _grid_logits(rng, B * (k + 1), V).reshape(B, k + 1, V)
+    drafts = np.empty((B, k), np.int32)
+    for b in range(B):
+        for j in range(k):  # drafts among each row's leading values
+            drafts[b, j] = int(rng.choice(np.argsort(-x[b, j], kind="stable")[:400]))
+    p = O.make_params(B, temperature=np.float32(1.0), top_p=rng.choice([0.8, 0.9, 0.95], size=B),
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64))
+    say("crowded bins verify")
+    check_verify(ctx, x, k, drafts, p, "bf16", None, None, None, O.NOISE_ICDF, None,
+                 label="crowded-verify")
+
+
 def test_cfg5_stress_batch(ctx):
     w = W.cfg5()
     say("cfg5")
