@@ -1022,6 +1022,10 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     auto solo = [&]() -> int {  // 0 decided, 1 cooperative, 2 exact resolution
       if (!icdf) return 1;
       int zb0 = -1, zb1 = -1, zn0 = 0, zn1 = 0;
+      // lane c's chunk: its top bin's distance below the row's and its window bins
+      // written, from its own statistics (the values decide() stores, without the reads)
+      const int dme = own && cs.n > 0 ? (int)(arow - floorf(cs.m * (float)LBS)) : NOBIN;
+      const int nbme = own && cs.n > 0 ? (int)cs.ncand2 : 0;
       // bins {bz, also} into the zone (bz at 0, also after it): 0 loaded, else a verdict
       auto load = [&](int bz, int also) -> int {
         if (bz >= rowwin) return 2;
@@ -1038,8 +1042,8 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
           off[hh] = 0;
           cnt[hh] = 0;
           if (lane < W && bins[hh] >= 0) {
-            const int lb = bins[hh] - S.dch[lane];
-            if (lb >= 0 && lb < S.nbch[lane]) {
+            const int lb = bins[hh] - dme;
+            if (lb >= 0 && lb < nbme) {
               off[hh] = lb > 0 ? (int)S.pc[lane][lb - 1] : 0;
               cnt[hh] = (int)S.pc[lane][lb] - off[hh];
             }
@@ -1048,7 +1052,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
           n[hh] = __builtin_amdgcn_readlane(zoo[hh] + cnt[hh], WAVE - 1);
           ok = ok && off[hh] + cnt[hh] <= PF;
         }
-        if (__ballot(!ok) != 0ull) return 1;
+        if (__ballot(!ok) != 0ull || n[0] + n[1] > SOLO) return 1;
         zoo[1] += n[0];
         // each zone place's source in the prefetched candidates, c PF + its place in
         // chunk c's part: lane c writes its part's (a few stores each), then every lane
@@ -1058,18 +1062,23 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
         for (int hh = 0; hh < 2; ++hh)
           for (int i = 0; i < cnt[hh]; ++i) src[zoo[hh] + i] = (uint32_t)(lane * PF + off[hh] + i);
         __builtin_amdgcn_wave_barrier();
+        // (at most SOLO places: every lane's SQ sources read first, then their candidates)
         const int ntot = n[0] + n[1];
-        for (int i0 = 0; i0 < ntot; i0 += 2 * WAVE) {
-          const int ia = i0 + lane, ib = i0 + WAVE + lane;
-          const Cand xa = P.pfb[src[ia < ntot ? ia : 0]];
-          const Cand xb = P.pfb[src[ib < ntot ? ib : 0]];
-          if (ia < ntot) {
-            G.z.zkey[ia] = ckey(xa.l, xa.id);
-            G.z.zmass[ia] = rmass(xa.l, m);
-          }
-          if (ib < ntot) {
-            G.z.zkey[ib] = ckey(xb.l, xb.id);
-            G.z.zmass[ib] = rmass(xb.l, m);
+        uint32_t si[SQ];
+#pragma unroll
+        for (int q = 0; q < SQ; ++q) {
+          const int i = lane + WAVE * q;
+          si[q] = src[i < ntot ? i : 0];
+        }
+        Cand xc[SQ];
+#pragma unroll
+        for (int q = 0; q < SQ; ++q) xc[q] = P.pfb[lane + WAVE * q < ntot ? si[q] : 0u];
+#pragma unroll
+        for (int q = 0; q < SQ; ++q) {
+          const int i = lane + WAVE * q;
+          if (i < ntot) {
+            G.z.zkey[i] = ckey(xc[q].l, xc[q].id);
+            G.z.zmass[i] = rmass(xc[q].l, m);
           }
         }
         // (one wave's LDS operations complete in order: its later reads see these)
