@@ -45,7 +45,8 @@ constexpr int PF = 160;                          // candidates of each chunk pre
 // The lattice words and the prefetched candidates are loaded straight into LDS, 1 KB per
 // wave instruction (16 bytes per lane): KW and KP instructions per wave.
 constexpr int LWB = LWMAX * NBW * 8, PFB = LWMAX * PF * 8;  // their bytes
-constexpr int KW = (LWB / 1024 + GW - 1) / GW, KP = (PFB / 1024 + GW - 1) / GW;
+constexpr int DW = GW - 1;  // the waves that issue them: all but wave 0
+constexpr int KW = (LWB / 1024 + DW - 1) / DW, KP = (PFB / 1024 + DW - 1) / DW;
 static_assert(LWB % 1024 == 0 && PFB % 1024 == 0, "whole 1 KB blocks");
 static_assert(PF <= LCAP && PF % 2 == 0, "prefetch layout");
 constexpr int NOBIN = 1 << 20;                   // "no bin": beyond every window
@@ -90,8 +91,7 @@ struct GFinalShared {
   uint16_t pc[LWMAX][NBW];        // per chunk: inclusive count prefix of its window bins
   uint32_t rc[NBW];               // row bins: counts
   unsigned long long rm[NBW];     // row bins: masses (RFIX per unit of exp(l - m))
-  float mch[LWMAX];               // per chunk: its maximum
-  int nbch[LWMAX], nfch[LWMAX];   // per chunk: window bins written, bins written whole
+  int nbch[LWMAX];                // per chunk: window bins written
   int ncnt[LWMAX];                // per chunk: allowed tokens
   int dch[LWMAX];                 // per chunk: its top bin's distance below the row's
   double sch[LWMAX];              // per chunk: its mass sum relative to the row maximum
@@ -731,7 +731,10 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   // the chunk statistics (one chunk per thread), the noise, the draft and the chunks'
   // lattice words (no branch between the loads: a missing optional input reads the row's
   // own state and is ignored; words past a chunk's written bins are dropped later)
-  const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (t < W ? t : 0)];
+  // (a row of at most 64 chunks: every wave loads all of them, lane c chunk c, and
+  // reduces them alone; wider rows: thread t chunk t)
+  const int ci = W <= WAVE ? lane : t;
+  const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (ci < W ? ci : 0)];
   RowState* rsp = &a.s.rs[r];
   const bool gum = a.noise && a.noise_mode != STRIM_NOISE_ICDF;
   const float* nz = a.noise ? a.noise + (int64_t)r * a.noise_stride : (const float*)rsp;
@@ -748,12 +751,12 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const int nlw = W <= LWMAX ? W * NBW : 0;
   const unsigned long long* lwp = a.s.lat + (int64_t)r * a.s.wmax * NBW;
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
-  {
+  if (w > 0) {
     const int wl = W <= LWMAX ? W : 1;
     const int nwb = (wl * NBW * 8 + 1023) / 1024, npb = (wl * PF * 8 + 1023) / 1024;
 #pragma unroll
     for (int q = 0; q < KW; ++q) {
-      const int blk = min(w + GW * q, nwb - 1);
+      const int blk = min(w - 1 + DW * q, nwb - 1);
       const int e = blk * 128 + 2 * lane;  // its words e, e + 1
       const int ec = e < wl * NBW ? e : 0;
       __builtin_amdgcn_global_load_lds((const void*)(lwp + ec),
@@ -761,7 +764,7 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     }
 #pragma unroll
     for (int q = 0; q < KP; ++q) {
-      const int blk = min(w + GW * q, npb - 1);
+      const int blk = min(w - 1 + DW * q, npb - 1);
       const int e = blk * 128 + 2 * lane;  // its candidates e, e + 1 (PF even)
       const int c = e / PF, pl = e - c * PF;
       const Cand* src = c < wl ? slots + (int64_t)c * SLOT + pl : slots;
@@ -785,41 +788,33 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const int draft = vdr ? d_raw : -1;
   const float l_draft = vdr ? ld_raw : -INFINITY;
 
-  // ---- the chunk statistics: per wave, then every wave merges the waves' results --
-  const bool own = t < W;
-  int ff = own ? (cs.flags | (cs.n > 0 ? 4 : 0)) : 0;
-  if (own && cs.n > 0 && cs.ncand2 == LNONE) ff |= 8;  // a chunk without lattice words
-  float mv = own ? cs.m : -INFINITY;
-  int mi = own ? cs.arg : -1;
-  if (own && t < LWMAX) {
-    S.mch[t] = cs.n > 0 ? cs.m : -INFINITY;
-    S.nbch[t] = cs.n > 0 ? (int)cs.ncand2 : 0;
-    S.nfch[t] = cs.n > 0 ? (int)cs.ncand : 0;
-    S.ncnt[t] = cs.n;
-  }
-  wave_argmax(mv, mi);
-  ff = wave_or_i(ff);
-  if (lane == 0) {
-    S.v[w] = mv;
-    S.i[w] = mi;
-    S.f[w] = ff;
-  }
-  if (t < NBW) {
-    S.rc[t] = 0u;
-    S.rm[t] = 0ull;
-  }
-  if (t < 2) S.tag[t] = -1;
-  if (t == 0) {
-    S.misc[0] = NBW;
-    S.misc[1] = NBW;
-    S.misc[3] = 0;
-  }
-  __syncthreads();
-  // lane q holds wave q's results
-  float m = lane < GW ? S.v[lane] : -INFINITY;
-  int arg = lane < GW ? S.i[lane] : -1, flags = lane < GW ? S.f[lane] : 0;
+  // ---- the chunk statistics ---------------------------------------------------------
+  // A row of at most 64 chunks is reduced by every wave alone, with no LDS: an LDS access
+  // after the loads into LDS above waits for all of them (the compiler cannot tell the
+  // areas apart), so the first one is left to the lattice code, which needs them.
+  // Wider rows merge the waves' results through LDS.
+  const bool own = t < W;     // thread t holds chunk t (wave 0's lanes, W <= 64)
+  const bool hold = ci < W;   // this lane holds chunk ci
+  int ff = hold ? (cs.flags | (cs.n > 0 ? 4 : 0)) : 0;
+  if (hold && cs.n > 0 && cs.ncand2 == LNONE) ff |= 8;  // a chunk without lattice words
+  float m = hold ? cs.m : -INFINITY;
+  int arg = hold ? cs.arg : -1;
   wave_argmax(m, arg);
-  flags = wave_or_i(flags);
+  int flags = wave_or_i(ff);
+  if (W > WAVE) {
+    if (lane == 0) {
+      S.v[w] = m;
+      S.i[w] = arg;
+      S.f[w] = flags;
+    }
+    __syncthreads();
+    // lane q holds wave q's results
+    m = lane < GW ? S.v[lane] : -INFINITY;
+    arg = lane < GW ? S.i[lane] : -1;
+    flags = lane < GW ? S.f[lane] : 0;
+    wave_argmax(m, arg);
+    flags = wave_or_i(flags);
+  }
   auto finish = [&](int status, int token, int accept, double sig, uint64_t last_key) {
     if (t != 0) return;
     rsp->status = status;
@@ -881,9 +876,16 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
     // (the chunks' threads are all in wave 0, W <= LWMAX: the row's limits are wave
     // reductions there, one store each; an LDS atomic from every lane to one word is
     // serialised lane by lane, about 2.5 us for 38 chunks)
+    if (t < NBW) {
+      S.rc[t] = 0u;
+      S.rm[t] = 0ull;
+    }
+    if (t < 2) S.tag[t] = -1;
     if (w == 0) {
       int lwin = NBW, lfull = NBW, tail = 0;
       if (own) {
+        S.nbch[t] = cs.n > 0 ? (int)cs.ncand2 : 0;
+        S.ncnt[t] = cs.n;
         if (cs.n > 0) {
           const int d = (int)(arow - floorf(cs.m * (float)LBS));
           const int nb = (int)cs.ncand2, nf = (int)cs.ncand;
