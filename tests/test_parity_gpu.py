@@ -85,6 +85,30 @@ def test_sweep_large_batch(ctx, V):
                          label=f"large V={V} it={it} mode={mode}")
 
 
+@pytest.mark.parametrize("V", [300007, 1 << 20])
+def test_vocab_past_64_chunks(V):
+    # rows of more than 64 chunks (up to the 2^20 maximum): the chunk statistics merge
+    # across waves, and general rows (beyond the lattice's 40 chunks) take the exact
+    # resolution
+    from strim_amd import ops
+    rng = np.random.default_rng(V % 1000)
+    B = 4
+    x = rng.normal(0, 2.0, size=(B, V)).astype(np.float32)
+    hist = rng.integers(0, V, size=(B, 500)).astype(np.int32)
+    p = O.make_params(B, temperature=[0.8, 1.0, 0.0, 0.7], top_k=[0, 50, 0, 0],
+                      top_p=[0.9, 1.0, 1.0, 0.95], min_p=[0.0, 0.0, 0.0, 0.05],
+                      presence_penalty=np.float32(0.4),
+                      seed=rng.integers(0, 2**63, size=B, dtype=np.uint64),
+                      position=np.arange(B, dtype=np.uint64))
+    c = ops.Context(0, max_rows=B, max_vocab=V)
+    try:
+        for mode in (O.NOISE_ICDF, O.NOISE_GUMBEL):
+            say(f"vocab {V} mode={mode}")
+            check_sample(c, x, p, "bf16", None, hist, None, mode, None, label=f"V={V}")
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("H", [300, 4096, 8192, 9000])
 def test_large_batch_long_histories(ctx, H):
     # Launches of 32 rows or more run four 8-token segments per thread. Every chunk's
