@@ -85,12 +85,12 @@ def test_sweep_large_batch(ctx, V):
                          label=f"large V={V} it={it} mode={mode}")
 
 
-@pytest.mark.parametrize("V", [300007, 1 << 20])
+@pytest.mark.parametrize("V", [163840, 163841, 262144, 300007, 1 << 20])
 def test_vocab_past_64_chunks(V):
-    # rows of more than 64 chunks (up to the 2^20 maximum): the chunk statistics merge
-    # across waves, and general rows (beyond the lattice's 40 chunks) take the exact
+    # rows at and past the lattice's 40 chunks (163,840 tokens) and past 64 chunks (up to
+    # the 2^20 maximum): up to 64 chunks every wave reduces the chunk statistics alone,
+    # past that they merge across waves; general rows past 40 chunks take the exact
     # resolution
-    from strim_amd import ops
     rng = np.random.default_rng(V % 1000)
     B = 4
     x = rng.normal(0, 2.0, size=(B, V)).astype(np.float32)
