@@ -728,11 +728,10 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int V = a.V, W = a.W;
   // ---- every load that does not depend on the row's parameters ------------------
-  // the chunk statistics (one chunk per thread), the noise, the draft and the chunks'
+  // the chunk statistics (a row of at most 64 chunks: every wave loads all of them, lane
+  // c chunk c; wider rows: thread t chunk t), the noise, the draft and the chunks'
   // lattice words (no branch between the loads: a missing optional input reads the row's
   // own state and is ignored; words past a chunk's written bins are dropped later)
-  // (a row of at most 64 chunks: every wave loads all of them, lane c chunk c, and
-  // reduces them alone; wider rows: thread t chunk t)
   const int ci = W <= WAVE ? lane : t;
   const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (ci < W ? ci : 0)];
   RowState* rsp = &a.s.rs[r];
@@ -745,10 +744,10 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   const float ld_raw = rsp->l_draft;
   // the chunks' lattice words (E[c NBW + lb]) and each chunk's first PF candidates
   // (pfb[c PF + place]; places past what a chunk wrote are stale and never used),
-  // straight into LDS: wave w issues blocks w, w + GW, ... of 1 KB (16 bytes per lane).
-  // The count per wave is fixed (blocks past the row's repeat its last block: the same
-  // bytes to the same place), so the statistics' loads are waited for by count alone.
-  const int nlw = W <= LWMAX ? W * NBW : 0;
+  // straight into LDS by waves 1-7: wave w issues blocks w - 1, w - 1 + DW, ... of 1 KB
+  // (16 bytes per lane; a fixed count per wave: blocks past the row's repeat its last
+  // block, the same bytes to the same place). Wave 0 issues none, so its waits cover its
+  // own loads alone while the others' land.
   const unsigned long long* lwp = a.s.lat + (int64_t)r * a.s.wmax * NBW;
   const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
   if (w > 0) {
