@@ -29,7 +29,10 @@ UNITS = [
     for dt in (1, 0) for pen in (2, 1, 0) for sseg in (1, 4)
 ] + [
     ("finalize_kernels.hip", []),
-    ("gfinal_kernels.hip", []),
+    # k_gfinal's five leading arguments (the chunk statistics', lattice words' and slots'
+    # addresses, the chunk stride and count) arrive preloaded in SGPRs, so its first load
+    # is issued before any wait for the argument block
+    ("gfinal_kernels.hip", ["-mllvm", "-amdgpu-kernarg-preload-count=5"]),
     ("sample_kernels.hip", []),
     ("qres_kernels.hip", []),
     ("aux_kernels.hip", []),

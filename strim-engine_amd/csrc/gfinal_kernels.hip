@@ -714,26 +714,33 @@ __device__ __noinline__ int collect_zone(const XArgs a_in, int r, int b, int j,
   return n <= ZCAP ? n : -1;
 }
 
-__global__ __launch_bounds__(GT) void k_gfinal(Args a) {
+// The leading arguments repeat fields of `a` (a.s.cstat, a.s.lat, a.s.slot, a.s.wmax,
+// a.W): built with kernel-argument preloading, they arrive in SGPRs, so the chunk
+// statistics' load is issued before any wait for the argument block.
+__global__ __launch_bounds__(GT) void k_gfinal(const ChunkStat* pre_cstat,
+                                                const unsigned long long* pre_lat,
+                                                const Cand* pre_slot, int pre_wmax, int pre_W,
+                                                Args a) {
   __shared__ GFinalShared S;
   __shared__ GBig G;
   __shared__ GPf P;
+  // the chunk statistics first, their address from the preloaded arguments alone (a row
+  // of at most 64 chunks: every wave loads all of them, lane c chunk c; wider rows:
+  // thread t chunk t)
+  const int ci = pre_W <= WAVE ? (int)(threadIdx.x & (WAVE - 1)) : (int)threadIdx.x;
+  const ChunkStat cs = pre_cstat[(int64_t)blockIdx.x * pre_wmax + (ci < pre_W ? ci : 0)];
   // the launch fields of the first loads, read together (see k_stream)
-  asm volatile("" ::"s"(a.s.cstat), "s"(a.s.wmax), "s"(a.s.rs), "s"(a.s.lat), "s"(a.W),
-               "s"(a.V), "s"(a.noise), "s"(a.noise_stride), "s"(a.noise_mode), "s"(a.verify),
-               "s"(a.k), "s"(a.drafts));
+  asm volatile("" ::"s"(a.s.rs), "s"(a.V), "s"(a.noise), "s"(a.noise_stride),
+               "s"(a.noise_mode), "s"(a.verify), "s"(a.k), "s"(a.drafts));
   const int r = blockIdx.x;
   int b, j;
   row_bj(a, r, b, j);
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
-  const int V = a.V, W = a.W;
+  const int V = a.V, W = pre_W;
   // ---- every load that does not depend on the row's parameters ------------------
-  // the chunk statistics (a row of at most 64 chunks: every wave loads all of them, lane
-  // c chunk c; wider rows: thread t chunk t), the noise, the draft and the chunks'
-  // lattice words (no branch between the loads: a missing optional input reads the row's
-  // own state and is ignored; words past a chunk's written bins are dropped later)
-  const int ci = W <= WAVE ? lane : t;
-  const ChunkStat cs = a.s.cstat[(int64_t)r * a.s.wmax + (ci < W ? ci : 0)];
+  // the chunk statistics (above), the noise, the draft and the chunks' lattice words (no
+  // branch between the loads: a missing optional input reads the row's own state and is
+  // ignored; words past a chunk's written bins are dropped later)
   RowState* rsp = &a.s.rs[r];
   const bool gum = a.noise && a.noise_mode != STRIM_NOISE_ICDF;
   const float* nz = a.noise ? a.noise + (int64_t)r * a.noise_stride : (const float*)rsp;
@@ -748,8 +755,8 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
   // (16 bytes per lane; a fixed count per wave: blocks past the row's repeat its last
   // block, the same bytes to the same place). Wave 0 issues none, so its waits cover its
   // own loads alone while the others' land.
-  const unsigned long long* lwp = a.s.lat + (int64_t)r * a.s.wmax * NBW;
-  const Cand* slots = a.s.slot + (int64_t)r * a.s.wmax * SLOT;
+  const unsigned long long* lwp = pre_lat + (int64_t)r * pre_wmax * NBW;
+  const Cand* slots = pre_slot + (int64_t)r * pre_wmax * SLOT;
   if (w > 0) {
     const int wl = W <= LWMAX ? W : 1;
     const int nwb = (wl * NBW * 8 + 1023) / 1024, npb = (wl * PF * 8 + 1023) / 1024;
@@ -1625,7 +1632,14 @@ __global__ __launch_bounds__(GT) void k_gfinal(Args a) {
 }
 
 hipError_t launch_gfinal(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-  return launch_args((const void*)k_gfinal, dim3((unsigned)a.R), dim3(GT), a, st, e0, e1);
+  const ChunkStat* c = a.s.cstat;
+  const unsigned long long* l = a.s.lat;
+  const Cand* sl = a.s.slot;
+  int wm = a.s.wmax, W = a.W;
+  void* args[] = {&c, &l, &sl, &wm, &W, const_cast<Args*>(&a)};
+  const dim3 grid((unsigned)a.R), block(GT);
+  if (e0 || e1) return hipExtLaunchKernel((const void*)k_gfinal, grid, block, args, 0, st, e0, e1, 0);
+  return hipLaunchKernel((const void*)k_gfinal, grid, block, args, 0, st);
 }
 
 }  // namespace strim
