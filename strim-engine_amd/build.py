@@ -24,8 +24,11 @@ CSRC = PKG / "csrc"
 OUT = PKG / "strim_amd" / "libstrim_sampler.so"
 
 # (source, extra defines): k_stream variants per (dtype, penalties, segments) triple
+# (k_stream's ten leading arguments, the fields its first loads need, arrive preloaded in
+# SGPRs, so those loads are issued before any wait for the argument block)
 UNITS = [
-    ("stream_kernels.hip", [f"-DSTRIM_DT={dt}", f"-DSTRIM_PEN={pen}", f"-DSTRIM_SSEG={sseg}"])
+    ("stream_kernels.hip", [f"-DSTRIM_DT={dt}", f"-DSTRIM_PEN={pen}", f"-DSTRIM_SSEG={sseg}",
+                            "-mllvm", "-amdgpu-kernarg-preload-count=10"])
     for dt in (1, 0) for pen in (2, 1, 0) for sseg in (1, 4)
 ] + [
     ("finalize_kernels.hip", []),

@@ -68,8 +68,28 @@ __device__ __forceinline__ float dv_rung_end(int r) {
 // around a load makes the compiler wait for the load at the join, which would serialise
 // the memory round trips. Aligned full chunks take 16-byte loads; otherwise each token
 // is loaded from a clamped index and out-of-row tokens become -inf.
-template <int DT, bool VEC, int SSEG>
-__device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)[SSEG], bool full,
+// The launch fields k_stream's first loads need, from its preloaded leading arguments
+// (the same values as the argument block's): with them in SGPRs at wave start, the
+// history, mask and logits loads are issued before any wait for the argument block.
+struct StreamPre {
+  const void* logits;
+  int64_t row_stride;
+  const int32_t* hist;
+  const uint32_t* mask;
+  int64_t mask_stride;
+  int H, V, W, R, xmap;
+};
+// their packed flags (host): xmap | verify << 1 | wide strides << 2 | k << 3 (strides past
+// 32 bits are read from the argument block)
+inline bool pre_wide(const Args& a) {
+  return a.row_stride > INT32_MAX || a.mask_stride > INT32_MAX;
+}
+inline int pre_bits(const Args& a) {
+  return a.xmap | (a.verify << 1) | (pre_wide(a) ? 4 : 0) | (a.k << 3);
+}
+
+template <int DT, bool VEC, int SSEG, typename A>
+__device__ __forceinline__ void load_chunk(const A& a, int r, const int (&i0)[SSEG], bool full,
                                            float (&x)[SSEG][EPT]) {
   const int64_t base = (int64_t)r * a.row_stride;
   if constexpr (DT == STRIM_DTYPE_BF16) {
@@ -138,37 +158,44 @@ __device__ __forceinline__ void load_chunk(const Args& a, int r, const int (&i0)
 // 8-token segments at +8 l and +512 + 8 l, so each wave-wide load is 1 KB contiguous
 // and the first maximum of the chunk lies in the lowest wave that holds the maximum.
 // The chunk statistics are written without a closing barrier (see ChunkStat).
+// The leading arguments repeat fields of `a` (StreamPre with 32-bit strides, and the flags
+// of pre_bits); built with kernel-argument preloading, the 13 dwords arrive in SGPRs.
 template <int DT, bool VEC, int PEN, bool MASK, int SSEG, bool GEN>
-__global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
+__global__ __launch_bounds__(stpb<SSEG>()) void k_stream(const void* pre_logits, int pre_rs,
+                                                         const int32_t* pre_hist,
+                                                         const uint32_t* pre_mask, int pre_ms,
+                                                         int pre_H, int pre_V, int pre_W,
+                                                         int pre_R, int pre_f, Args a) {
   constexpr int STPB = stpb<SSEG>();       // threads
   constexpr int NW = STPB / WAVE;          // waves
   __shared__ StreamShared<PEN, NW, GEN> S;
-  // the launch fields used before the first global load, read together: a field first
-  // read inside a branch would be its own scalar-load round trip
-  asm volatile("" ::"s"(a.logits), "s"(a.row_stride), "s"(a.V), "s"(a.verify), "s"(a.k),
-               "s"(a.hist), "s"(a.H), "s"(a.hist_len), "s"(a.mask), "s"(a.mask_stride),
-               "s"(a.s.cstat), "s"(a.s.wmax), "s"(a.W), "s"(a.R), "s"(a.xmap),
-               "s"(a.nqprep));
+  const bool wide = (pre_f & 4) != 0;
+  const StreamPre P{pre_logits, wide ? a.row_stride : (int64_t)pre_rs, pre_hist, pre_mask,
+                    wide ? a.mask_stride : (int64_t)pre_ms, pre_H, pre_V, pre_W, pre_R,
+                    pre_f & 1};
   // general-q verify: the workgroups past row R carry the draft distributions' work
   // (qprep.hpp), independent of the chunks'
-  if (blockIdx.y >= (unsigned)a.R) {
-    const int blk = (int)((blockIdx.y - (unsigned)a.R) * gridDim.x + blockIdx.x);
+  if (blockIdx.y >= (unsigned)P.R) {
+    const int blk = (int)((blockIdx.y - (unsigned)P.R) * gridDim.x + blockIdx.x);
     if (blk < a.nqprep) qprep_block<STPB>(a, blk);
     return;
   }
   int r, c;
-  map_block(a, r, c);
-  int b, j;
-  row_bj(a, r, b, j);
+  map_block(P, r, c);
+  int b = r, j = 0;  // (row_bj from the packed flags)
+  if (pre_f & 2) {
+    const int k1 = (pre_f >> 3) + 1;
+    b = r / k1;
+    j = r - b * k1;
+  }
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = wave_id();
   const int c0 = c * CHUNK;
-  const bool full = VEC && c0 + CHUNK <= a.V;
-  ChunkStat* csp = &a.s.cstat[(int64_t)r * a.s.wmax + c];
+  const bool full = VEC && c0 + CHUNK <= P.V;
 
   // history ids first: the counts are built while the logits are still in flight (the
   // ids are requested before the row's parameters are known, so no load waits for them)
   int hid[hpt<STPB>()];
-  if constexpr (PEN != 0) hist_load<STPB>(a, b, hid);
+  if constexpr (PEN != 0) hist_load<STPB>(P, b, hid);
   int i0[SSEG];
 #pragma unroll
   for (int s = 0; s < SSEG; ++s)
@@ -182,20 +209,24 @@ __global__ __launch_bounds__(stpb<SSEG>()) void k_stream(Args a) {
 #pragma unroll
   for (int s = 0; s < SSEG; ++s) bits[s] = 0xFFu;
   if constexpr (MASK) {
-    const uint8_t* mb = a.mask ? (const uint8_t*)(a.mask + (int64_t)r * a.mask_stride)
-                               : (const uint8_t*)a.logits;
+    const uint8_t* mb = P.mask ? (const uint8_t*)(P.mask + (int64_t)r * P.mask_stride)
+                               : (const uint8_t*)P.logits;
 #pragma unroll
-    for (int s = 0; s < SSEG; ++s) bits[s] = mb[a.mask && i0[s] < a.V ? (i0[s] >> 3) : 0];
+    for (int s = 0; s < SSEG; ++s) bits[s] = mb[P.mask && i0[s] < P.V ? (i0[s] >> 3) : 0];
   }
   float v[SSEG][EPT];
-  load_chunk<DT, VEC, SSEG>(a, r, i0, full, v);
+  load_chunk<DT, VEC, SSEG>(P, r, i0, full, v);
+  // the launch fields used next, read together: a field first read inside a branch would
+  // be its own scalar-load round trip
+  asm volatile("" ::"s"(a.verify), "s"(a.k), "s"(a.hist_len), "s"(a.s.cstat), "s"(a.s.wmax));
+  ChunkStat* csp = &a.s.cstat[(int64_t)r * a.s.wmax + c];
   // the row's parameters only now: a scalar-load wait for them before this point would
   // also hold back the loads above
   const RowParams p = load_params(a, b, j);
   const bool pen = PEN != 0 && p.pen;
   const int hl = PEN != 0 ? hist_len(a, b) : 0;
   if constexpr (MASK) {
-    if (!a.mask) {
+    if (!P.mask) {
 #pragma unroll
       for (int s = 0; s < SSEG; ++s) bits[s] = 0xFFu;
     }

@@ -10,12 +10,26 @@
 
 namespace strim {
 
+// One k_stream launch: the preloaded leading arguments, then the argument block.
+inline hipError_t launch_stream_args(const void* fn, dim3 grid, dim3 blk, const Args& a,
+                                     hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  const void* lg = a.logits;
+  int rs = pre_wide(a) ? 0 : (int)a.row_stride, ms = pre_wide(a) ? 0 : (int)a.mask_stride;
+  const int32_t* h = a.hist;
+  const uint32_t* mk = a.mask;
+  int H = a.H, V = a.V, W = a.W, R = a.R, f = pre_bits(a);
+  void* args[] = {&lg, &rs, &h, &mk, &ms, &H, &V, &W, &R, &f, const_cast<Args*>(&a)};
+  if (e0 || e1) return hipExtLaunchKernel(fn, grid, blk, args, 0, st, e0, e1, 0);
+  return hipLaunchKernel(fn, grid, blk, args, 0, st);
+}
+
 template <int DT, int PEN, int SSEG>
 hipError_t launch_stream_group(const Args& a, dim3 grid, hipStream_t st, hipEvent_t e0,
                                hipEvent_t e1) {
   const dim3 blk(stpb<SSEG>());
 #define STRIM_K(VEC, MASK, GEN) \
-  launch_args((const void*)k_stream<DT, VEC, PEN, MASK, SSEG, GEN>, grid, blk, a, st, e0, e1)
+  launch_stream_args((const void*)k_stream<DT, VEC, PEN, MASK, SSEG, GEN>, grid, blk, a, st, \
+                     e0, e1)
   if constexpr (PEN == 1) {
     // unaligned logits take the general variant (penalties and mask checked per row)
     if (a.vec_ok == 0) return a.gen ? STRIM_K(false, true, true) : STRIM_K(false, true, false);
