@@ -1638,8 +1638,9 @@ hipError_t launch_gfinal(const Args& a, hipStream_t st, hipEvent_t e0, hipEvent_
   int wm = a.s.wmax, W = a.W;
   void* args[] = {&c, &l, &sl, &wm, &W, const_cast<Args*>(&a)};
   const dim3 grid((unsigned)a.R), block(GT);
-  if (e0 || e1) return hipExtLaunchKernel((const void*)k_gfinal, grid, block, args, 0, st, e0, e1, 0);
-  return hipLaunchKernel((const void*)k_gfinal, grid, block, args, 0, st);
+  const void* k = (const void*)k_gfinal;
+  if (e0 || e1) return hipExtLaunchKernel(k, grid, block, args, 0, st, e0, e1, 0);
+  return hipLaunchKernel(k, grid, block, args, 0, st);
 }
 
 }  // namespace strim
